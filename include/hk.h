@@ -1,0 +1,238 @@
+/*
+ * hk.h — C ABI of libhk.so, the MI355X (gfx950) BF16 transformer kernel path.
+ *
+ * Every entry point here replaces one host entry point of the reference
+ * (shuqi2077/rust-ascend). Citations are path:line relative to the reference
+ * repository root. The ABI uses plain pointers, sizes and a contiguous tensor
+ * descriptor; it exposes no C++ or torch types, so a Rust `extern "C"` shim, a
+ * ctypes binding or a C program can call it directly.
+ *
+ * Conventions shared by every op (mirroring rust-ascend-driver/src/tensor/runtime/mod.rs:147-435):
+ *   - Tensors are contiguous, row-major, device-resident. The caller owns all
+ *     memory; no entry point frees caller memory. Outputs are written into
+ *     caller storage ("_into" style; the reference's allocating forms map to
+ *     hk_alloc + the op).
+ *   - Every shape/dtype/domain check runs before any device work; a failed check
+ *     returns HK_INVALID_ARGUMENT and touches nothing.
+ *   - Outputs must not overlap any input or each other ([ptr, ptr+bytes) ranges),
+ *     as rust-ascend-driver/src/tensor/deepgemm/mod.rs:99-100,117-119 require.
+ *   - By default each call synchronizes its stream before returning, as every
+ *     reference launch does (deepgemm/mod.rs:134-145). hk_set_async(ctx,1)
+ *     leaves work queued on the context's stream until hk_sync().
+ *   - A failed launch or synchronization poisons the context: later calls return
+ *     HK_POISONED (deepgemm/mod.rs:39,143; common_ir/mod.rs:75,120).
+ *   - There is no CPU fallback (deepgemm/mod.rs:1-3, README.md:44).
+ *   - The message of the last failure on the calling thread is hk_last_error().
+ */
+#ifndef HK_H
+#define HK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; reference: CannError, rust-ascend-driver/src/lib.rs:18-78. */
+typedef enum hk_status {
+    HK_OK = 0,
+    HK_INVALID_ARGUMENT = 1,   /* CannError::InvalidTensor */
+    HK_HIP_ERROR = 2,          /* CannError::Status (runtime call failed) */
+    HK_COMPLETION_ERROR = 3,   /* CannError::Completion (launch or sync failed) */
+    HK_POISONED = 4,           /* provider poisoned by an earlier completion failure */
+    HK_NOT_INITIALIZED = 5,    /* "runtime is not initialized" (runtime/matrix.rs:41) */
+    HK_LOAD_ERROR = 6,         /* CannError::Library / Symbol (no gfx950 device, no code object) */
+} hk_status;
+
+/* Element types; the codes are the reference's DType codes,
+ * rust-ascend-driver/src/tensor/layout.rs:5-17. */
+typedef enum hk_dtype {
+    HK_F32 = 0,
+    HK_F16 = 1,
+    HK_BF16 = 27,
+} hk_dtype;
+
+/* Reference: deepgemm::Transpose, rust-ascend-driver/src/tensor/deepgemm/plan.rs:7. */
+typedef enum hk_transpose { HK_NO = 0, HK_YES = 1 } hk_transpose;
+
+/* Reference: RotaryLayout, rust-ascend-compiler/src/ascend/rotary_programs.rs:5-6. */
+typedef enum hk_rotary_layout { HK_ROTARY_INTERLEAVED = 0, HK_ROTARY_SPLIT_HALF = 1 } hk_rotary_layout;
+
+#define HK_MAX_RANK 8
+
+/* Contiguous tensor; reference: TensorBuffer {handle, shape, strides, dtype}
+ * restricted to contiguous strides (runtime/mod.rs:907-925). */
+typedef struct hk_tensor {
+    void* data;
+    int32_t dtype;            /* hk_dtype */
+    int32_t rank;             /* 0..HK_MAX_RANK */
+    int64_t shape[HK_MAX_RANK];
+} hk_tensor;
+
+/* Launch and module counters; reference: KernelStats{modules_loaded, launches,
+ * synchronizations}, deepgemm/mod.rs:15-16,142 and common_ir/mod.rs:11-12,119. */
+typedef struct hk_stats {
+    uint64_t modules_loaded;
+    uint64_t launches;
+    uint64_t synchronizations;
+} hk_stats;
+
+/* Host-only result of a GEMM contract check; reference: GemmSpec,
+ * deepgemm/plan.rs:31-86. kind: 0 dense, 1 batched. */
+typedef struct hk_gemm_plan {
+    int32_t kind;
+    int32_t out_rank;
+    int64_t batch, m, n, k;
+    int64_t out_shape[3];
+    char key[32];             /* "bf16_<kind>_<ta><tb>_<out>", plan.rs:84-86 */
+} hk_gemm_plan;
+
+typedef struct hk_context hk_context;
+
+/* ---------------------------------------------------------------- runtime */
+
+/* Reference: AscendRuntime::initialize_exclusive, runtime/mod.rs:424-435 and
+ * Worker::start (runtime/worker.rs:34-90). Binds `device`, checks that it is a
+ * gfx950 part, and creates the context. Only one context per process; a second
+ * call returns HK_INVALID_ARGUMENT ("already initialized", mod.rs:427-433). */
+hk_status hk_init(int32_t device, hk_context** out);
+/* Releases the context (the reference keeps its worker for the process lifetime;
+ * this exists for tests). */
+hk_status hk_shutdown(hk_context* ctx);
+/* Use `stream` (a hipStream_t; NULL = the null stream) for later launches. */
+hk_status hk_set_stream(hk_context* ctx, void* stream);
+void* hk_get_stream(hk_context* ctx);
+/* 0 (default): synchronize after every op, like the reference. 1: leave queued. */
+hk_status hk_set_async(hk_context* ctx, int32_t async_mode);
+/* Reference: CannSession::synchronize / ComputeClient::flush. */
+hk_status hk_sync(hk_context* ctx);
+hk_status hk_get_stats(hk_context* ctx, hk_stats* out);
+/* Thread-local message of the last failure; reference: Display for CannError. */
+const char* hk_last_error(void);
+/* Number of the library's ABI (bumped on incompatible change). */
+int32_t hk_abi_version(void);
+
+/* Device memory; reference: ComputeStorage alloc/dealloc with 32-B alignment
+ * (runtime/mod.rs:486-517), create_from_slice / read_one. */
+hk_status hk_alloc(hk_context* ctx, size_t bytes, void** out);
+hk_status hk_free(hk_context* ctx, void* ptr);
+hk_status hk_upload(hk_context* ctx, void* dst, const void* src, size_t bytes);
+hk_status hk_download(hk_context* ctx, void* dst, const void* src, size_t bytes);
+
+/* ---------------------------------------------------------------- GEMM */
+
+/* Host-only contract check, no device access. Reference: GemmSpec::new,
+ * deepgemm/plan.rs:49-80: BF16 A/B, BF16 or F32 output, rank 2 or equal-batch
+ * rank 3 (batch 1..4096, no broadcast), M/N/K positive multiples of 16 and at
+ * most INT32_MAX. */
+hk_status hk_gemm_plan_check(const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb,
+                             int32_t out_dtype, hk_gemm_plan* plan);
+
+/* out = op(A) @ op(B), FP32 accumulation, BF16 (RNE) or F32 out.
+ * Reference: AscendRuntime::gemm_into, runtime/mod.rs:350-354 (matrix.rs:54-59);
+ * AscendRuntime::gemm (mod.rs:344-348) is hk_alloc + this call. */
+hk_status hk_gemm_into(hk_context* ctx, const hk_tensor* a, const hk_tensor* b,
+                       int32_t ta, int32_t tb, hk_tensor* out);
+
+/* Linear backward for Y = X W^T: dX = dY W (BF16), dW = dY^T X (F32).
+ * Reference: AscendRuntime::linear_nt_backward, runtime/mod.rs:357-362 (matrix.rs:60-74). */
+hk_status hk_linear_nt_backward(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
+                                const hk_tensor* dy, hk_tensor* dx, hk_tensor* dw);
+
+/* FP32-storage, BF16-compute GEMM: rounds A and B to BF16 into a_bf16/b_bf16
+ * (the saved snapshots), then out(F32) = op(A) @ op(B).
+ * Reference: AscendRuntime::gemm_bf16_fp32, runtime/mod.rs:388-392 (matrix.rs:84-93). */
+hk_status hk_gemm_bf16_fp32(hk_context* ctx, const hk_tensor* a, const hk_tensor* b,
+                            int32_t ta, int32_t tb, hk_tensor* out,
+                            hk_tensor* a_bf16, hk_tensor* b_bf16);
+/* FP32 gradients in the original physical layouts from saved BF16 A/B and F32 dY
+ * (rounded to BF16 on device). Reference: AscendRuntime::gemm_bf16_fp32_backward,
+ * runtime/mod.rs:395-399 (matrix.rs:95-121). */
+hk_status hk_gemm_bf16_fp32_backward(hk_context* ctx, const hk_tensor* a_bf16,
+                                     const hk_tensor* b_bf16, const hk_tensor* dy,
+                                     int32_t ta, int32_t tb, hk_tensor* da, hk_tensor* db);
+/* Y(F32) = bf16(X) bf16(W)^T with rank-2 F32 X/W. Reference:
+ * AscendRuntime::linear_bf16_fp32, runtime/mod.rs:364-370 (matrix.rs:129-133). */
+hk_status hk_linear_bf16_fp32(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
+                              hk_tensor* y, hk_tensor* x_bf16, hk_tensor* w_bf16);
+/* Reference: AscendRuntime::linear_bf16_fp32_backward, runtime/mod.rs:372-377. */
+hk_status hk_linear_bf16_fp32_backward(hk_context* ctx, const hk_tensor* x_bf16,
+                                       const hk_tensor* w_bf16, const hk_tensor* dy,
+                                       hk_tensor* dx, hk_tensor* dw);
+
+/* Elementwise F32 <-> BF16 conversion (RNE, NaN kept quiet, Inf kept).
+ * Reference: AscendRuntime::cast_into, runtime/mod.rs:276-279 (conversion.rs:21-62). */
+hk_status hk_cast_into(hk_context* ctx, const hk_tensor* in, hk_tensor* out);
+
+/* ---------------------------------------------------------------- RMSNorm */
+
+/* y = x * rstd * w, rstd = 1/sqrt(mean(x^2) + eps) per row of the last axis.
+ * x: F32 or BF16 [..., W]; w: F32 [W] (or x's dtype); y: x's dtype; rstd: F32 [rows].
+ * Any positive W; empty batches are allowed. eps must be finite and positive in F32.
+ * Reference: AscendRuntime::rms_norm, runtime/mod.rs:402-408 (normalization.rs:153-166,
+ * row_programs.rs:144-151) and, for BF16 x with F32 rstd, CannSession::rms_norm
+ * (tensor/ops.rs:347-385). */
+hk_status hk_rms_norm(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, double eps,
+                      hk_tensor* y, hk_tensor* rstd);
+/* dx (x's dtype) and dw (F32 [W], summed over all rows; zeros for an empty batch),
+ * from the saved rstd (eps is not recomputed).
+ * Reference: AscendRuntime::rms_norm_backward, runtime/mod.rs:410-415
+ * (normalization.rs:168-186, row_programs.rs:200-217) and CannSession::rms_norm_backward
+ * (tensor/backward.rs:127-148). */
+hk_status hk_rms_norm_backward(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
+                               const hk_tensor* dy, const hk_tensor* rstd,
+                               hk_tensor* dx, hk_tensor* dw);
+
+/* ---------------------------------------------------------------- RoPE */
+
+/* Full last-axis rotation with same-row F32 tables (table shape = input shape with
+ * the last axis halved). x/y: F32 or BF16. Reference: AscendRuntime::rotary,
+ * runtime/mod.rs:257-261 (runtime/rotary.rs:15-29, rotary_programs.rs:47-97). */
+hk_status hk_rotary(hk_context* ctx, const hk_tensor* x, const hk_tensor* cos_t,
+                    const hk_tensor* sin_t, int32_t layout, hk_tensor* y);
+/* Transpose Jacobian. Reference: AscendRuntime::rotary_backward, runtime/mod.rs:264-268. */
+hk_status hk_rotary_backward(hk_context* ctx, const hk_tensor* dy, const hk_tensor* cos_t,
+                             const hk_tensor* sin_t, int32_t layout, hk_tensor* dx);
+/* Rotate the first `width` values of the last axis; the tail is copied bit-exactly;
+ * table leading axes are 1 or equal to the input's, last axis width/2.
+ * Reference: AscendRuntime::rotary_prefix(_backward), runtime/mod.rs:214-221
+ * (rotary_programs.rs:7-23,101-156). */
+hk_status hk_rotary_prefix(hk_context* ctx, const hk_tensor* x, const hk_tensor* cos_t,
+                           const hk_tensor* sin_t, int32_t width, int32_t layout, hk_tensor* y);
+hk_status hk_rotary_prefix_backward(hk_context* ctx, const hk_tensor* dy, const hk_tensor* cos_t,
+                                    const hk_tensor* sin_t, int32_t width, int32_t layout,
+                                    hk_tensor* dx);
+
+/* ---------------------------------------------------------------- attention */
+
+/* Fused causal/non-causal grouped-query attention forward (FlashAttention-style,
+ * online softmax, nothing materialized).
+ *   q [B,Hq,M,D], k/v [B,Hkv,N,D] BF16; o [B,Hq,M,D] BF16; lse [B,Hq,M] F32
+ *   (natural-log logsumexp of the scaled, masked scores, saved for backward).
+ *   Hq % Hkv == 0 and query head h reads KV head h / (Hq/Hkv) (heads_programs.rs:5-60).
+ *   Causal: key j is excluded when key_start + j > query_start + i (mask_programs.rs:5-40).
+ *   D in {16, 32, 64, 128}; the value width equals D.
+ * Replaces the composed chain of src/nn/attention.rs:10-80 (causal_mask,
+ * repeat_kv_heads, BF16 GEMMs, softmax) with one kernel; GEMM operands are BF16
+ * and P is rounded to BF16 before P.V, as matmul_bf16_fp32 does. */
+hk_status hk_attention_forward(hk_context* ctx, const hk_tensor* q, const hk_tensor* k,
+                               const hk_tensor* v, float scale, int32_t causal,
+                               uint64_t query_start, uint64_t key_start,
+                               hk_tensor* o, hk_tensor* lse);
+/* Backward of hk_attention_forward from saved o and lse: dq [B,Hq,M,D],
+ * dk/dv [B,Hkv,N,D] (F32 or BF16). dK/dV sum over the query heads of each group in a
+ * fixed order (no atomics), the deterministic analogue of repeat_kv_heads_backward
+ * (runtime/heads.rs:29-51). dS is scaled then rounded to BF16, as the reference's
+ * MatmulBf16Fp32Backward chain does (examples/grouped_attention_tensor.rs:30-40). */
+hk_status hk_attention_backward(hk_context* ctx, const hk_tensor* q, const hk_tensor* k,
+                                const hk_tensor* v, const hk_tensor* o, const hk_tensor* lse,
+                                const hk_tensor* dout, float scale, int32_t causal,
+                                uint64_t query_start, uint64_t key_start,
+                                hk_tensor* dq, hk_tensor* dk, hk_tensor* dv);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HK_H */

@@ -1,0 +1,362 @@
+"""CPU oracle for the BF16 transformer kernel path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import this module, and only as the checker or as the timed CPU baseline. The
+product path (``libhk.so`` and the ``rust_ascend_hip`` package) never imports it.
+
+This is a numpy/ctypes front end over ``hk_oracle.c`` (a C restatement of the
+reference's host loops; every C function cites the reference file:line it follows),
+plus the BF16 helpers and the counter-based input generator that tests and bench
+share.
+
+How each oracle function is pinned (tests/test_oracle.py), so that a dropped term,
+a wrong sign or index, or a transposed operand fails at least one check:
+
+* ``bf16_round``: bit patterns of hand-picked values (ties to even, Inf/NaN, -0,
+  overflow to Inf) and agreement with torch's float32->bfloat16 conversion.
+* ``gemm_f64``/``gemm_f32``: numpy float64 matmul for all four transposes and
+  batches; the reference's integer-formula cases of
+  rust-ascend-kernels/src/tests.rs:89-103,124-129 (80x96x144 dense, 3x16x32x16
+  batched, exact BF16 inputs), examples/matrix_runtime.rs:50-77 and
+  rust-ascend-driver/examples/deepgemm_validate.rs:30-56, which are exact or
+  near-exact in f64; the linear-gradient finite-difference identity of
+  tools/ascend/tests/test_adapter.py:89-93.
+* ``rms_norm_f64``/``rms_norm_backward_f64``: torch float64 autograd of
+  x*rsqrt(mean(x^2)+eps)*w (the independent reference of
+  tools/ascend/tests/test_row_reference.py:65-78); the weight-contribution known
+  answer x=2, dy=3, rstd=[.5,.25,2] -> [3,1.5,12] (row_tests.rs:280-287); the
+  six-element vectors of examples/gradients.rs:20-37.
+* ``rms_norm_lanes_f32``/``rms_norm_backward_lanes_f32``: against the f64 oracle
+  (1e-5) and the constant-row invariant of test_row_reference.py:81-83.
+* ``rotary``/``rotary_f64``/``rotary_prefix``: torch float64 autograd (the backward
+  must be the forward's vector-Jacobian product), pair-norm preservation,
+  angle-zero identity, the prefix tail bit patterns (NaN/Inf/-0) of
+  rotary_programs.rs:224-260, and prefix-with-full-width == full rotation
+  (rotary_programs.rs:262-275).
+* ``attention_f64``: the closed forms of examples/attention_tensor.rs:22-66
+  (orthogonal Q/K -> uniform probabilities) and
+  examples/causal_attention_tensor.rs:31-55 (Q=K=0 causal -> running means), the
+  exact mask patterns of causal_attention_tensor.rs:23-30, and torch float64
+  autograd of softmax(scale*QK^T+mask)V at the reference's tolerance
+  (grouped_attention_tensor.rs:10, 2e-3+3e-3|b|) on the reference's five GQA cases.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+
+def build() -> str:
+    """Compile liboracle.so with oracle/Makefile (gcc, no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.or_bf16.argtypes = [ctypes.c_float]
+        L.or_bf16.restype = ctypes.c_float
+        L.or_round_bf16.argtypes = [_f32p, _f32p, _i64]
+        L.or_num_threads.restype = _int
+        L.or_set_num_threads.argtypes = [_int]
+        L.or_gemm_f64.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _int, _int, _f64p]
+        L.or_gemm_f64_sampled.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _int, _int, _i64p, _i64p, _i64, _f64p]
+        L.or_gemm_f32.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _int, _int, _f32p]
+        L.or_rms_norm_f64.argtypes = [_f32p, _f32p, _i64, _i64, ctypes.c_double, _f64p, _f64p]
+        L.or_rms_norm_backward_f64.argtypes = [_f32p, _f32p, _f32p, _f64p, _i64, _i64, _f64p, _f64p]
+        L.or_rms_norm_lanes_f32.argtypes = [_f32p, _f32p, _i64, _i64, ctypes.c_float, _f32p, _f32p]
+        L.or_rms_norm_lanes_f32.restype = _int
+        L.or_rms_norm_backward_lanes_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _f32p, _f32p]
+        L.or_rms_norm_backward_lanes_f32.restype = _int
+        L.or_column_sum_pairwise.argtypes = [_f32p, _i64, _i64, _f32p]
+        L.or_rotary.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _int, _int, _f32p]
+        L.or_rotary_f64.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _int, _int, _f64p]
+        L.or_rotary_prefix.argtypes = [_f32p, _i64p, _i64p, _int, _i64, _int, _int, _f32p, _f32p, _f32p]
+        L.or_rotary_prefix.restype = _int
+        _vp = ctypes.c_void_p
+        L.or_attention_f64.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                       ctypes.c_double, _int, ctypes.c_uint64, ctypes.c_uint64,
+                                       _vp, _vp, _vp, _vp, _vp]
+        L.or_causal_mask.argtypes = [_i64, _i64, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32p]
+        _lib = L
+    return _lib
+
+
+def set_threads(n: int) -> None:
+    lib().or_set_num_threads(int(n))
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())
+
+
+# ------------------------------------------------------------------ BF16 helpers
+
+def bf16_round(x) -> np.ndarray:
+    """float32 values rounded to the nearest BF16 (RNE), returned as float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().or_round_bf16(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def bf16_bits(x) -> np.ndarray:
+    """uint16 BF16 bit patterns of float32 values (RNE)."""
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_decode(bits) -> np.ndarray:
+    """float32 values of uint16 BF16 bit patterns."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+# ------------------------------------------------------------------ inputs
+
+_MASK = (1 << 64) - 1
+
+
+def _splitmix64(x: np.ndarray) -> np.ndarray:
+    x = (x + np.uint64(0x9E3779B97F4A7C15)) & np.uint64(_MASK)
+    z = x
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def normal(shape, seed: int, stream: int, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
+    """Counter-based N(mean, std^2) float32: SplitMix64 of (seed, stream, index), then
+    Box-Muller. Deterministic for a given (seed, stream), independent of the platform."""
+    n = int(np.prod(shape)) if len(shape) else 1
+    pairs = (n + 1) // 2
+    idx = np.arange(pairs, dtype=np.uint64)
+    base = np.uint64(((seed & 0xFFFFFFFF) << 32) ^ ((stream & 0xFFFF) << 48))
+    with np.errstate(over="ignore"):
+        u1 = _splitmix64(base + idx * np.uint64(2))
+        u2 = _splitmix64(base + idx * np.uint64(2) + np.uint64(1))
+    f1 = ((u1 >> np.uint64(11)).astype(np.float64) + 1.0) / float(1 << 53)
+    f2 = (u2 >> np.uint64(11)).astype(np.float64) / float(1 << 53)
+    r = np.sqrt(-2.0 * np.log(f1))
+    z = np.concatenate([r * np.cos(2 * np.pi * f2), r * np.sin(2 * np.pi * f2)])[:n]
+    return (z * std + mean).astype(np.float32).reshape(shape)
+
+
+# ------------------------------------------------------------------ GEMM
+
+def _c32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def gemm_f64(a, b, ta: bool, tb: bool) -> np.ndarray:
+    """op(A) @ op(B) in f64 over float32 inputs; rank 2 or rank 3 (batched)."""
+    a = _c32(a)
+    b = _c32(b)
+    batched = a.ndim == 3
+    if not batched:
+        a = a[None]
+        b = b[None]
+    g = a.shape[0]
+    m, k = (a.shape[2], a.shape[1]) if ta else (a.shape[1], a.shape[2])
+    n = b.shape[1] if tb else b.shape[2]
+    out = np.empty((g, m, n), dtype=np.float64)
+    lib().or_gemm_f64(a.reshape(-1), b.reshape(-1), g, m, n, k, int(ta), int(tb), out.reshape(-1))
+    return out if batched else out[0]
+
+
+def gemm_f32(a, b, ta: bool, tb: bool) -> np.ndarray:
+    a = _c32(a)
+    b = _c32(b)
+    batched = a.ndim == 3
+    if not batched:
+        a = a[None]
+        b = b[None]
+    g = a.shape[0]
+    m, k = (a.shape[2], a.shape[1]) if ta else (a.shape[1], a.shape[2])
+    n = b.shape[1] if tb else b.shape[2]
+    out = np.empty((g, m, n), dtype=np.float32)
+    lib().or_gemm_f32(a.reshape(-1), b.reshape(-1), g, m, n, k, int(ta), int(tb), out.reshape(-1))
+    return out if batched else out[0]
+
+
+def gemm_f64_sampled(a, b, ta: bool, tb: bool, rows, cols) -> np.ndarray:
+    a = _c32(a)
+    b = _c32(b)
+    m, k = (a.shape[1], a.shape[0]) if ta else (a.shape[0], a.shape[1])
+    n = b.shape[0] if tb else b.shape[1]
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    cols = np.ascontiguousarray(cols, dtype=np.int64)
+    out = np.empty(rows.shape[0], dtype=np.float64)
+    lib().or_gemm_f64_sampled(a.reshape(-1), b.reshape(-1), m, n, k, int(ta), int(tb), rows, cols, rows.shape[0], out)
+    return out
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+def rms_norm_f64(x, w, eps: float):
+    x = _c32(x)
+    width = x.shape[-1]
+    rows = x.size // width if width else 0
+    y = np.empty(x.shape, dtype=np.float64)
+    rstd = np.empty(x.shape[:-1], dtype=np.float64)
+    lib().or_rms_norm_f64(x.reshape(-1), _c32(w), rows, width, float(eps), y.reshape(-1), rstd.reshape(-1))
+    return y, rstd
+
+
+def rms_norm_backward_f64(x, w, dy, rstd):
+    x = _c32(x)
+    width = x.shape[-1]
+    rows = x.size // width if width else 0
+    dx = np.empty(x.shape, dtype=np.float64)
+    dw = np.empty(width, dtype=np.float64)
+    r = np.ascontiguousarray(rstd, dtype=np.float64).reshape(-1)
+    lib().or_rms_norm_backward_f64(x.reshape(-1), _c32(w), _c32(dy).reshape(-1), r, rows, width,
+                                   dx.reshape(-1), dw)
+    return dx, dw
+
+
+def rms_norm_lanes_f32(x, w, eps: float):
+    x = _c32(x)
+    width = x.shape[-1]
+    rows = x.size // width
+    y = np.empty(x.shape, dtype=np.float32)
+    rstd = np.empty(x.shape[:-1], dtype=np.float32)
+    rc = lib().or_rms_norm_lanes_f32(x.reshape(-1), _c32(w), rows, width, float(eps), y.reshape(-1), rstd.reshape(-1))
+    if rc != 0:
+        raise ValueError("row program order needs width % 32 == 0")
+    return y, rstd
+
+
+def rms_norm_backward_lanes_f32(x, w, dy, rstd):
+    x = _c32(x)
+    width = x.shape[-1]
+    rows = x.size // width
+    dx = np.empty(x.shape, dtype=np.float32)
+    dw = np.empty(width, dtype=np.float32)
+    rc = lib().or_rms_norm_backward_lanes_f32(x.reshape(-1), _c32(w), _c32(dy).reshape(-1),
+                                              _c32(rstd).reshape(-1), rows, width, dx.reshape(-1), dw)
+    if rc != 0:
+        raise ValueError("row program order needs width % 32 == 0")
+    return dx, dw
+
+
+def column_sum_pairwise(parts) -> np.ndarray:
+    parts = np.array(parts, dtype=np.float32, copy=True, order="C")
+    rows, width = parts.shape
+    out = np.empty(width, dtype=np.float32)
+    lib().or_column_sum_pairwise(parts.reshape(-1), rows, width, out)
+    return out
+
+
+# ------------------------------------------------------------------ RoPE
+
+def rotary(x, cos_t, sin_t, layout: int, backward: bool = False) -> np.ndarray:
+    x = _c32(x)
+    width = x.shape[-1]
+    rows = x.size // width if width else 0
+    y = np.empty_like(x)
+    lib().or_rotary(x.reshape(-1), _c32(cos_t).reshape(-1), _c32(sin_t).reshape(-1), rows, width,
+                    int(layout), int(backward), y.reshape(-1))
+    return y
+
+
+def rotary_f64(x, cos_t, sin_t, layout: int, backward: bool = False) -> np.ndarray:
+    x = _c32(x)
+    width = x.shape[-1]
+    rows = x.size // width if width else 0
+    y = np.empty(x.shape, dtype=np.float64)
+    lib().or_rotary_f64(x.reshape(-1), _c32(cos_t).reshape(-1), _c32(sin_t).reshape(-1), rows, width,
+                        int(layout), int(backward), y.reshape(-1))
+    return y
+
+
+def rotary_prefix(x, cos_t, sin_t, width: int, layout: int, backward: bool = False) -> np.ndarray:
+    x = _c32(x)
+    cos_t = _c32(cos_t)
+    sin_t = _c32(sin_t)
+    ins = np.array(x.shape, dtype=np.int64)
+    tabs = np.array(cos_t.shape, dtype=np.int64)
+    y = np.empty_like(x)
+    rc = lib().or_rotary_prefix(x.reshape(-1), ins, tabs, x.ndim, int(width), int(layout), int(backward),
+                                cos_t.reshape(-1), sin_t.reshape(-1), y.reshape(-1))
+    if rc != 0:
+        raise ValueError("invalid rotary prefix spec")
+    return y
+
+
+def rope_tables(positions, dim: int, theta: float):
+    """cos/sin tables [len(positions), dim/2]: angle = pos * theta^(-2i/dim), computed in
+    f64 and rounded to f32 (the reference has no frequency policy; the caller builds
+    the tables, rotary_programs.rs:1)."""
+    pos = np.asarray(positions, dtype=np.float64)[:, None]
+    inv = theta ** (-np.arange(0, dim, 2, dtype=np.float64) / dim)
+    ang = pos * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+# ------------------------------------------------------------------ attention
+
+def attention_f64(q, k, v, dy=None, scale=0.25, causal=False, query_start=0, key_start=0,
+                  mask=None, want_grads=True):
+    """Returns dict(out, lse[, dq, dk, dv]) in f64 for q [B,Hq,M,D], k/v [B,Hkv,N,D]."""
+    q = _c32(q)
+    k = _c32(k)
+    v = _c32(v)
+    B, H, M, D = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    out = np.empty((B, H, M, D), dtype=np.float64)
+    lse = np.empty((B, H, M), dtype=np.float64)
+    res = {"out": out, "lse": lse}
+    ptr = lambda a: None if a is None else a.ctypes.data
+    dq = dk = dv = None
+    dyc = None
+    if dy is not None:
+        dyc = _c32(dy)
+        if want_grads:
+            dq = np.empty_like(out)
+            dk = np.empty((B, Hkv, N, D), dtype=np.float64)
+            dv = np.empty_like(dk)
+            res.update(dq=dq, dk=dk, dv=dv)
+    maskc = None if mask is None else _c32(mask)
+    lib().or_attention_f64(ptr(q), ptr(k), ptr(v), ptr(dyc), ptr(maskc), B, H, Hkv, M, N, D,
+                           float(scale), int(bool(causal)), int(query_start), int(key_start),
+                           ptr(out), ptr(lse), ptr(dq), ptr(dk), ptr(dv))
+    return res
+
+
+def causal_mask(batch, queries, keys, query_start, key_start) -> np.ndarray:
+    out = np.empty((batch, queries, keys), dtype=np.float32)
+    lib().or_causal_mask(batch, queries, keys, int(query_start), int(key_start), out.reshape(-1))
+    return out
+
+
+# ------------------------------------------------------------------ comparison
+
+def rel_err(actual, expected) -> float:
+    """max_i |a-b| / (|b| + atol), atol = 1e-3 * rms(b). Infinite when a has a
+    non-finite value where b is finite."""
+    a = np.asarray(actual, dtype=np.float64).reshape(-1)
+    b = np.asarray(expected, dtype=np.float64).reshape(-1)
+    if a.size == 0:
+        return 0.0
+    if not np.all(np.isfinite(a[np.isfinite(b)])):
+        return float("inf")
+    rms = float(np.sqrt(np.mean(b * b)))
+    atol = 1e-3 * rms if rms > 0 else 1e-30
+    return float(np.max(np.abs(a - b) / (np.abs(b) + atol)))

@@ -1,0 +1,817 @@
+// hk_driver.cpp — the C ABI of libhk.so (declared in include/hk.h).
+//
+// Replaces the reference's AscendCL loader and launch layers
+// (rust-ascend-driver/src/{api,sys,lib}.rs, tensor/deepgemm/mod.rs, tensor/common_ir/mod.rs,
+// tensor/runtime/{mod,worker,matrix,normalization,rotary}.rs) with a HIP runtime driver:
+//   * one process-wide context (initialize_exclusive, runtime/mod.rs:424-435),
+//   * every shape/dtype/domain check before any device work (plan.rs:49-80,
+//     normalization.rs:12-48, rotary_programs.rs:7-23, attention.rs:81-104),
+//   * output/input overlap rejection (deepgemm/mod.rs:99-100,117-119),
+//   * launch, then stream synchronization unless async mode is on (deepgemm/mod.rs:134-145),
+//   * a sticky poison flag after a failed launch or synchronization (deepgemm/mod.rs:39,143),
+//   * launch/sync counters (deepgemm/mod.rs:15-16,142).
+// The gfx950 code object is linked into this library as a fat binary and registered by
+// the HIP runtime when the library loads; there is no JIT build step and no CPU fallback.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/hk.h"
+#include "hk_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+hk_status fail(hk_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+struct Ctx {
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t stream = nullptr;
+    bool async = false;
+    bool poisoned = false;
+    std::mutex mu;
+    hk_stats stats{};
+    void* workspace = nullptr;
+    size_t ws_bytes = 0;
+};
+
+std::mutex g_init_mu;
+Ctx* g_ctx = nullptr;
+
+int64_t dtype_size(int32_t dt) {
+    switch (dt) {
+        case HK_F32: return 4;
+        case HK_F16:
+        case HK_BF16: return 2;
+        default: return 0;
+    }
+}
+
+const char* dtype_name(int32_t dt) {
+    switch (dt) {
+        case HK_F32: return "F32";
+        case HK_F16: return "F16";
+        case HK_BF16: return "BF16";
+        default: return "?";
+    }
+}
+
+// Element count with overflow and sign checks; -1 on an invalid descriptor.
+int64_t numel(const hk_tensor* t) {
+    if (!t || t->rank < 0 || t->rank > HK_MAX_RANK) return -1;
+    int64_t n = 1;
+    for (int i = 0; i < t->rank; ++i) {
+        if (t->shape[i] < 0) return -1;
+        if (t->shape[i] != 0 && n > INT64_MAX / 4 / t->shape[i]) return -1;
+        n *= t->shape[i];
+    }
+    return n;
+}
+
+int64_t nbytes(const hk_tensor* t) { return numel(t) * dtype_size(t->dtype); }
+
+std::string shape_str(const hk_tensor* t) {
+    std::string s = "[";
+    for (int i = 0; i < t->rank; ++i) {
+        if (i) s += ",";
+        s += std::to_string(t->shape[i]);
+    }
+    return s + "]";
+}
+
+// Basic descriptor check: known dtype, valid rank/shape, non-null data unless empty.
+bool tensor_ok(const hk_tensor* t, const char* name) {
+    if (!t) {
+        fail(HK_INVALID_ARGUMENT, "%s: null tensor descriptor", name);
+        return false;
+    }
+    if (dtype_size(t->dtype) == 0) {
+        fail(HK_INVALID_ARGUMENT, "%s: unsupported dtype code %d", name, t->dtype);
+        return false;
+    }
+    const int64_t n = numel(t);
+    if (n < 0) {
+        fail(HK_INVALID_ARGUMENT, "%s: invalid rank or shape", name);
+        return false;
+    }
+    if (n > 0 && t->data == nullptr) {
+        fail(HK_INVALID_ARGUMENT, "%s: null data pointer for a non-empty tensor", name);
+        return false;
+    }
+    return true;
+}
+
+bool same_shape(const hk_tensor* a, const hk_tensor* b) {
+    if (a->rank != b->rank) return false;
+    for (int i = 0; i < a->rank; ++i)
+        if (a->shape[i] != b->shape[i]) return false;
+    return true;
+}
+
+bool overlaps(const hk_tensor* a, const hk_tensor* b) {
+    const int64_t na = nbytes(a), nb = nbytes(b);
+    if (na <= 0 || nb <= 0) return false;
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a->data), b0 = reinterpret_cast<uintptr_t>(b->data);
+    return a0 < b0 + static_cast<uintptr_t>(nb) && b0 < a0 + static_cast<uintptr_t>(na);
+}
+
+// Every output must be disjoint from every input and from the other outputs.
+bool disjoint(std::initializer_list<const hk_tensor*> outs, std::initializer_list<const hk_tensor*> ins) {
+    std::vector<const hk_tensor*> o(outs), in(ins);
+    for (size_t i = 0; i < o.size(); ++i) {
+        for (const hk_tensor* x : in)
+            if (overlaps(o[i], x)) {
+                fail(HK_INVALID_ARGUMENT, "output overlaps an input");
+                return false;
+            }
+        for (size_t j = i + 1; j < o.size(); ++j)
+            if (overlaps(o[i], o[j])) {
+                fail(HK_INVALID_ARGUMENT, "outputs overlap each other");
+                return false;
+            }
+    }
+    return true;
+}
+
+hk_tensor make_view(void* data, int32_t dtype, std::initializer_list<int64_t> shape) {
+    hk_tensor t{};
+    t.data = data;
+    t.dtype = dtype;
+    t.rank = static_cast<int32_t>(shape.size());
+    int i = 0;
+    for (int64_t d : shape) t.shape[i++] = d;
+    return t;
+}
+
+// Acquire the context for an op: initialized, not poisoned; holds its mutex.
+struct OpGuard {
+    Ctx* c;
+    std::unique_lock<std::mutex> lock;
+    hk_status st = HK_OK;
+    explicit OpGuard(hk_context* h) : c(reinterpret_cast<Ctx*>(h)) {
+        if (!c || c != g_ctx) {
+            st = fail(HK_NOT_INITIALIZED, "runtime is not initialized (call hk_init)");
+            return;
+        }
+        lock = std::unique_lock<std::mutex>(c->mu);
+        if (c->poisoned) st = fail(HK_POISONED, "context poisoned by an earlier completion failure");
+    }
+};
+
+// After enqueuing an op: check the launch, then synchronize unless async. A failure
+// poisons the context, as a failed launch/sync poisons the reference's provider.
+hk_status complete(Ctx* c, hipError_t launch, const char* op, int kernels) {
+    c->stats.launches += static_cast<uint64_t>(kernels);
+    hipError_t sync = hipSuccess;
+    if (launch == hipSuccess && !c->async) {
+        sync = hipStreamSynchronize(c->stream);
+        c->stats.synchronizations += 1;
+    }
+    if (launch != hipSuccess || sync != hipSuccess) {
+        c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "%s: launch status %d (%s), synchronization status %d (%s)", op,
+                    static_cast<int>(launch), hipGetErrorString(launch), static_cast<int>(sync),
+                    hipGetErrorString(sync));
+    }
+    return HK_OK;
+}
+
+hk_status ensure_workspace(Ctx* c, size_t bytes) {
+    if (bytes <= c->ws_bytes) return HK_OK;
+    if (c->workspace) {
+        // queued work may still read the old buffer
+        hipError_t e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            c->poisoned = true;
+            return fail(HK_COMPLETION_ERROR, "workspace resize: synchronization status %d", static_cast<int>(e));
+        }
+        (void)hipFree(c->workspace);
+        c->workspace = nullptr;
+        c->ws_bytes = 0;
+    }
+    size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    hipError_t e = hipMalloc(&c->workspace, want);
+    if (e != hipSuccess) {
+        c->workspace = nullptr;
+        return fail(HK_HIP_ERROR, "workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
+    }
+    c->ws_bytes = want;
+    return HK_OK;
+}
+
+// ------------------------------------------------------------------ GEMM contract
+
+struct GemmSpec {
+    int kind = 0;  // 0 dense, 1 batched
+    int64_t batch = 1, m = 0, n = 0, k = 0;
+    int32_t out_dtype = HK_BF16;
+};
+
+// Reference: GemmSpec::new + GemmSpec::checked, rust-ascend-driver/src/tensor/deepgemm/plan.rs:49-80.
+hk_status gemm_spec(const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb, int32_t out_dtype,
+                    GemmSpec* s) {
+    if (!tensor_ok(a, "A") || !tensor_ok(b, "B")) return HK_INVALID_ARGUMENT;
+    if ((ta != HK_NO && ta != HK_YES) || (tb != HK_NO && tb != HK_YES))
+        return fail(HK_INVALID_ARGUMENT, "transpose flags must be 0 (No) or 1 (Yes)");
+    const int r = a->rank;
+    if (!(r == 2 || r == 3) || b->rank != r) return fail(HK_INVALID_ARGUMENT, "GEMM requires matching rank 2 or rank 3");
+    if (r == 3 && a->shape[0] != b->shape[0]) return fail(HK_INVALID_ARGUMENT, "batch broadcasting is not supported");
+    const int64_t* a2 = a->shape + (r - 2);
+    const int64_t* b2 = b->shape + (r - 2);
+    const int64_t m = ta == HK_NO ? a2[0] : a2[1];
+    const int64_t k = ta == HK_NO ? a2[1] : a2[0];
+    const int64_t kb = tb == HK_NO ? b2[0] : b2[1];
+    const int64_t n = tb == HK_NO ? b2[1] : b2[0];
+    if (kb != k) return fail(HK_INVALID_ARGUMENT, "GEMM contraction mismatch (%lld vs %lld)", (long long)k, (long long)kb);
+    const int64_t groups = r == 3 ? a->shape[0] : 1;
+    if (a->dtype != HK_BF16 || b->dtype != HK_BF16 || !(out_dtype == HK_BF16 || out_dtype == HK_F32))
+        return fail(HK_INVALID_ARGUMENT, "GEMM accepts BF16 inputs and BF16/F32 output only (got %s, %s -> %s)",
+                    dtype_name(a->dtype), dtype_name(b->dtype), dtype_name(out_dtype));
+    for (int64_t x : {m, n, k})
+        if (x <= 0 || x % 16 != 0 || x > INT32_MAX)
+            return fail(HK_INVALID_ARGUMENT,
+                        "M/N/K must be positive multiples of 16 <= INT32_MAX; batches 1..=4096 (M=%lld N=%lld K=%lld)",
+                        (long long)m, (long long)n, (long long)k);
+    if (groups <= 0 || groups > 4096)
+        return fail(HK_INVALID_ARGUMENT, "M/N/K must be positive multiples of 16 <= INT32_MAX; batches 1..=4096");
+    const int64_t tiles = ((m + 63) / 64) * ((n + 63) / 64) * groups;
+    if (tiles > static_cast<int64_t>(INT32_MAX) - 32) return fail(HK_INVALID_ARGUMENT, "tile range overflows");
+    s->kind = r == 3 ? 1 : 0;
+    s->batch = groups;
+    s->m = m;
+    s->n = n;
+    s->k = k;
+    s->out_dtype = out_dtype;
+    return HK_OK;
+}
+
+bool out_matches(const GemmSpec& s, const hk_tensor* out) {
+    if (out->dtype != s.out_dtype) return false;
+    if (s.kind == 0) return out->rank == 2 && out->shape[0] == s.m && out->shape[1] == s.n;
+    return out->rank == 3 && out->shape[0] == s.batch && out->shape[1] == s.m && out->shape[2] == s.n;
+}
+
+hk_status run_gemm(Ctx* c, const GemmSpec& s, const void* a, const void* b, void* out, int ta, int tb,
+                   void* ws, hipError_t* err) {
+    *err = hk::gemm_bf16(a, b, out, s.out_dtype == HK_BF16, s.batch, s.m, s.n, s.k, ta, tb, ws, c->num_cus,
+                         c->stream);
+    return HK_OK;
+}
+
+// The reference's FP32-storage wrappers take F32 A/B; the GEMM runs on BF16 copies.
+hk_status mixed_spec(const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb, GemmSpec* s) {
+    if (!tensor_ok(a, "A") || !tensor_ok(b, "B")) return HK_INVALID_ARGUMENT;
+    if (a->dtype != HK_F32 || b->dtype != HK_F32)
+        return fail(HK_INVALID_ARGUMENT, "BF16-compute FP32 matmul requires FP32 inputs");
+    hk_tensor ab = *a, bb = *b;
+    ab.dtype = HK_BF16;
+    bb.dtype = HK_BF16;
+    return gemm_spec(&ab, &bb, ta, tb, HK_F32, s);
+}
+
+bool is_bf16_copy_of(const hk_tensor* snap, const hk_tensor* src) {
+    return snap && snap->dtype == HK_BF16 && same_shape(snap, src);
+}
+
+// ------------------------------------------------------------------ row layouts
+
+// rows x width of a contiguous tensor whose last axis is the row.
+bool row_layout(const hk_tensor* x, int64_t* rows, int64_t* width, const char* op) {
+    if (x->rank < 1) {
+        fail(HK_INVALID_ARGUMENT, "%s requires a last dimension", op);
+        return false;
+    }
+    *width = x->shape[x->rank - 1];
+    if (*width <= 0) {
+        fail(HK_INVALID_ARGUMENT, "%s width must be positive", op);
+        return false;
+    }
+    *rows = numel(x) / *width;
+    return true;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+
+extern "C" {
+
+const char* hk_last_error(void) { return g_last_error.c_str(); }
+
+int32_t hk_abi_version(void) { return 1; }
+
+hk_status hk_init(int32_t device, hk_context** out) {
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output handle");
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    if (g_ctx) return fail(HK_INVALID_ARGUMENT, "HIP runtime already initialized");
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail(HK_LOAD_ERROR, "no HIP device available (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= count) return fail(HK_INVALID_ARGUMENT, "device ordinal %d out of range 0..%d", device, count - 1);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    // Reference: NativeApi::check_soc requires the one supported SoC (deepgemm/native.rs:16-35).
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(HK_LOAD_ERROR, "device %d is %s; libhk.so carries gfx950 code only", device, prop.gcnArchName);
+    Ctx* c = new Ctx();
+    c->device = device;
+    c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    c->stats.modules_loaded = 1;  // the fat binary linked into this library
+    g_ctx = c;
+    *out = reinterpret_cast<hk_context*>(c);
+    return HK_OK;
+}
+
+hk_status hk_shutdown(hk_context* h) {
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    Ctx* c = reinterpret_cast<Ctx*>(h);
+    if (!c || c != g_ctx) return fail(HK_NOT_INITIALIZED, "runtime is not initialized");
+    {
+        std::lock_guard<std::mutex> g(c->mu);
+        if (c->workspace) {
+            if (hipStreamSynchronize(c->stream) == hipSuccess) (void)hipFree(c->workspace);
+            // after a failed synchronization the buffer is leaked, never freed under queued work
+        }
+    }
+    delete c;
+    g_ctx = nullptr;
+    return HK_OK;
+}
+
+hk_status hk_set_stream(hk_context* h, void* stream) {
+    OpGuard g(h);
+    if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
+    g.c->stream = static_cast<hipStream_t>(stream);
+    return HK_OK;
+}
+
+void* hk_get_stream(hk_context* h) {
+    Ctx* c = reinterpret_cast<Ctx*>(h);
+    return (c && c == g_ctx) ? static_cast<void*>(c->stream) : nullptr;
+}
+
+hk_status hk_set_async(hk_context* h, int32_t mode) {
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    g.c->async = mode != 0;
+    return HK_OK;
+}
+
+hk_status hk_sync(hk_context* h) {
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hipStreamSynchronize(g.c->stream);
+    g.c->stats.synchronizations += 1;
+    if (e != hipSuccess) {
+        g.c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "synchronization status %d (%s)", static_cast<int>(e), hipGetErrorString(e));
+    }
+    return HK_OK;
+}
+
+hk_status hk_get_stats(hk_context* h, hk_stats* out) {
+    OpGuard g(h);
+    if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null stats pointer");
+    *out = g.c->stats;
+    return HK_OK;
+}
+
+hk_status hk_alloc(hk_context* h, size_t bytes, void** out) {
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    if (bytes == 0) return HK_OK;
+    hipError_t e = hipMalloc(out, bytes);  // 256-byte aligned (the reference aligns to 32 B)
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return HK_OK;
+}
+
+hk_status hk_free(hk_context* h, void* p) {
+    OpGuard g(h);
+    if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
+    if (!p) return HK_OK;
+    if (g.c->poisoned) return fail(HK_POISONED, "poisoned context: memory is leaked rather than freed");
+    // queued work may still use the buffer (async mode)
+    hipError_t e = hipStreamSynchronize(g.c->stream);
+    if (e == hipSuccess) e = hipFree(p);
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "hipFree: %s", hipGetErrorString(e));
+    return HK_OK;
+}
+
+hk_status hk_upload(hk_context* h, void* dst, const void* src, size_t bytes) {
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (bytes == 0) return HK_OK;
+    if (!dst || !src) return fail(HK_INVALID_ARGUMENT, "null pointer");
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g.c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.c->stream);
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "upload: %s", hipGetErrorString(e));
+    return HK_OK;
+}
+
+hk_status hk_download(hk_context* h, void* dst, const void* src, size_t bytes) {
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (bytes == 0) return HK_OK;
+    if (!dst || !src) return fail(HK_INVALID_ARGUMENT, "null pointer");
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g.c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.c->stream);
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "download: %s", hipGetErrorString(e));
+    return HK_OK;
+}
+
+// ------------------------------------------------------------------ GEMM
+
+hk_status hk_gemm_plan_check(const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb, int32_t out_dtype,
+                             hk_gemm_plan* plan) {
+    GemmSpec s;
+    hk_status st = gemm_spec(a, b, ta, tb, out_dtype, &s);
+    if (st != HK_OK) return st;
+    if (plan) {
+        std::memset(plan, 0, sizeof *plan);
+        plan->kind = s.kind;
+        plan->batch = s.batch;
+        plan->m = s.m;
+        plan->n = s.n;
+        plan->k = s.k;
+        if (s.kind == 0) {
+            plan->out_rank = 2;
+            plan->out_shape[0] = s.m;
+            plan->out_shape[1] = s.n;
+        } else {
+            plan->out_rank = 3;
+            plan->out_shape[0] = s.batch;
+            plan->out_shape[1] = s.m;
+            plan->out_shape[2] = s.n;
+        }
+        std::snprintf(plan->key, sizeof plan->key, "bf16_%s_%c%c_%s", s.kind ? "batched" : "dense",
+                      ta ? 't' : 'n', tb ? 't' : 'n', out_dtype == HK_BF16 ? "bf16" : "f32");
+    }
+    return HK_OK;
+}
+
+hk_status hk_gemm_into(hk_context* h, const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb, hk_tensor* out) {
+    if (!tensor_ok(out, "out")) return HK_INVALID_ARGUMENT;
+    GemmSpec s;
+    hk_status st = gemm_spec(a, b, ta, tb, out->dtype, &s);
+    if (st != HK_OK) return st;
+    if (!out_matches(s, out)) return fail(HK_INVALID_ARGUMENT, "GEMM output layout mismatch: %s", shape_str(out).c_str());
+    if (!disjoint({out}, {a, b})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    st = ensure_workspace(g.c, hk::gemm_workspace_bytes(s.batch, s.m, s.n, s.k, ta, tb));
+    if (st != HK_OK) return st;
+    hipError_t e;
+    run_gemm(g.c, s, a->data, b->data, out->data, ta, tb, g.c->workspace, &e);
+    return complete(g.c, e, "gemm", 1);
+}
+
+hk_status hk_linear_nt_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                                hk_tensor* dx, hk_tensor* dw) {
+    // Reference: matrix.rs:60-74.
+    GemmSpec fwd, sdx, sdw;
+    hk_status st = gemm_spec(x, w, HK_NO, HK_YES, HK_BF16, &fwd);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(dy, "dY") || !tensor_ok(dx, "dX") || !tensor_ok(dw, "dW")) return HK_INVALID_ARGUMENT;
+    if (fwd.kind != 0 || !out_matches(fwd, dy))
+        return fail(HK_INVALID_ARGUMENT, "linear backward requires rank-2 BF16 dY matching X @ W^T");
+    if ((st = gemm_spec(dy, w, HK_NO, HK_NO, HK_BF16, &sdx)) != HK_OK) return st;
+    if ((st = gemm_spec(dy, x, HK_YES, HK_NO, HK_F32, &sdw)) != HK_OK) return st;
+    if (!out_matches(sdx, dx)) return fail(HK_INVALID_ARGUMENT, "dX must be BF16 shaped like X");
+    if (!out_matches(sdw, dw)) return fail(HK_INVALID_ARGUMENT, "dW must be F32 shaped like W");
+    if (!disjoint({dx, dw}, {x, w, dy})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    size_t ws = std::max(hk::gemm_workspace_bytes(1, sdx.m, sdx.n, sdx.k, HK_NO, HK_NO),
+                         hk::gemm_workspace_bytes(1, sdw.m, sdw.n, sdw.k, HK_YES, HK_NO));
+    if ((st = ensure_workspace(g.c, ws)) != HK_OK) return st;
+    hipError_t e;
+    run_gemm(g.c, sdx, dy->data, w->data, dx->data, HK_NO, HK_NO, g.c->workspace, &e);
+    if (e == hipSuccess) run_gemm(g.c, sdw, dy->data, x->data, dw->data, HK_YES, HK_NO, g.c->workspace, &e);
+    return complete(g.c, e, "linear_nt_backward", 2);
+}
+
+hk_status hk_gemm_bf16_fp32(hk_context* h, const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb,
+                            hk_tensor* out, hk_tensor* a_bf16, hk_tensor* b_bf16) {
+    // Reference: matrix.rs:84-93 (cast both inputs into independent snapshots, then GEMM).
+    GemmSpec s;
+    hk_status st = mixed_spec(a, b, ta, tb, &s);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(out, "out") || !tensor_ok(a_bf16, "A_bf16") || !tensor_ok(b_bf16, "B_bf16")) return HK_INVALID_ARGUMENT;
+    if (!out_matches(s, out)) return fail(HK_INVALID_ARGUMENT, "output must be F32 %s", shape_str(out).c_str());
+    if (!is_bf16_copy_of(a_bf16, a) || !is_bf16_copy_of(b_bf16, b))
+        return fail(HK_INVALID_ARGUMENT, "BF16 snapshots must match the inputs' shapes");
+    if (!disjoint({out, a_bf16, b_bf16}, {a, b})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, hk::gemm_workspace_bytes(s.batch, s.m, s.n, s.k, ta, tb))) != HK_OK) return st;
+    hipError_t e = hk::cast_apply(1, a->data, a_bf16->data, numel(a), g.c->stream);
+    if (e == hipSuccess) e = hk::cast_apply(1, b->data, b_bf16->data, numel(b), g.c->stream);
+    if (e == hipSuccess) run_gemm(g.c, s, a_bf16->data, b_bf16->data, out->data, ta, tb, g.c->workspace, &e);
+    return complete(g.c, e, "gemm_bf16_fp32", 3);
+}
+
+hk_status hk_gemm_bf16_fp32_backward(hk_context* h, const hk_tensor* a, const hk_tensor* b, const hk_tensor* dy,
+                                     int32_t ta, int32_t tb, hk_tensor* da, hk_tensor* db) {
+    // Reference: matrix.rs:95-121.
+    GemmSpec fwd;
+    hk_status st = gemm_spec(a, b, ta, tb, HK_F32, &fwd);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(dy, "dY") || !tensor_ok(da, "dA") || !tensor_ok(db, "dB")) return HK_INVALID_ARGUMENT;
+    if (!out_matches(fwd, dy))
+        return fail(HK_INVALID_ARGUMENT, "BF16-compute matmul backward requires saved BF16 inputs and matching FP32 dY");
+    if (da->dtype != HK_F32 || !same_shape(da, a) || db->dtype != HK_F32 || !same_shape(db, b))
+        return fail(HK_INVALID_ARGUMENT, "gradients must be F32 in the inputs' physical shapes");
+    if (!disjoint({da, db}, {a, b, dy})) return HK_INVALID_ARGUMENT;
+    // dY rounded to BF16 in the workspace head, GEMM workspace after it.
+    hk_tensor dyb = *dy;
+    dyb.dtype = HK_BF16;
+    const int opp_ta = ta == HK_NO ? HK_YES : HK_NO;
+    const int opp_tb = tb == HK_NO ? HK_YES : HK_NO;
+    // dX: ta == No -> dY . op'(B) ; else B . dY^T   (matrix.rs:104-105)
+    const hk_tensor *dx_a = ta == HK_NO ? &dyb : b, *dx_b = ta == HK_NO ? b : &dyb;
+    const int dx_ta = ta == HK_NO ? HK_NO : tb, dx_tb = ta == HK_NO ? opp_tb : HK_YES;
+    // dW: tb == No -> op'(A) . dY ; else dY^T . A   (matrix.rs:106-107)
+    const hk_tensor *dw_a = tb == HK_NO ? a : &dyb, *dw_b = tb == HK_NO ? &dyb : a;
+    const int dw_ta = tb == HK_NO ? opp_ta : HK_YES, dw_tb = tb == HK_NO ? HK_NO : ta;
+    GemmSpec sdx, sdw;
+    if ((st = gemm_spec(dx_a, dx_b, dx_ta, dx_tb, HK_F32, &sdx)) != HK_OK) return st;
+    if ((st = gemm_spec(dw_a, dw_b, dw_ta, dw_tb, HK_F32, &sdw)) != HK_OK) return st;
+    const size_t dy_bytes = (static_cast<size_t>(numel(dy)) * 2 + 255) & ~size_t(255);
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const size_t ws = dy_bytes + std::max(hk::gemm_workspace_bytes(sdx.batch, sdx.m, sdx.n, sdx.k, dx_ta, dx_tb),
+                                          hk::gemm_workspace_bytes(sdw.batch, sdw.m, sdw.n, sdw.k, dw_ta, dw_tb));
+    if ((st = ensure_workspace(g.c, ws)) != HK_OK) return st;
+    void* dyb_ptr = g.c->workspace;
+    void* gws = static_cast<char*>(g.c->workspace) + dy_bytes;
+    dyb.data = dyb_ptr;
+    hipError_t e = hk::cast_apply(1, dy->data, dyb_ptr, numel(dy), g.c->stream);
+    if (e == hipSuccess) run_gemm(g.c, sdx, dx_a->data, dx_b->data, da->data, dx_ta, dx_tb, gws, &e);
+    if (e == hipSuccess) run_gemm(g.c, sdw, dw_a->data, dw_b->data, db->data, dw_ta, dw_tb, gws, &e);
+    return complete(g.c, e, "gemm_bf16_fp32_backward", 3);
+}
+
+hk_status hk_linear_bf16_fp32(hk_context* h, const hk_tensor* x, const hk_tensor* w, hk_tensor* y,
+                              hk_tensor* x_bf16, hk_tensor* w_bf16) {
+    // Reference: matrix.rs:123-133 (rank-2 check, then gemm_bf16_fp32 NT).
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "W")) return HK_INVALID_ARGUMENT;
+    if (x->rank != 2 || w->rank != 2)
+        return fail(HK_INVALID_ARGUMENT, "BF16-compute FP32 linear requires rank-2 input and weight");
+    return hk_gemm_bf16_fp32(h, x, w, HK_NO, HK_YES, y, x_bf16, w_bf16);
+}
+
+hk_status hk_linear_bf16_fp32_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                                       hk_tensor* dx, hk_tensor* dw) {
+    // Reference: matrix.rs:134-145.
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "W")) return HK_INVALID_ARGUMENT;
+    if (x->rank != 2 || w->rank != 2)
+        return fail(HK_INVALID_ARGUMENT, "BF16-compute linear backward requires saved rank-2 inputs");
+    return hk_gemm_bf16_fp32_backward(h, x, w, dy, HK_NO, HK_YES, dx, dw);
+}
+
+hk_status hk_cast_into(hk_context* h, const hk_tensor* in, hk_tensor* out) {
+    // Reference: conversion.rs:21-62 (shape retained, distinct output storage).
+    if (!tensor_ok(in, "input") || !tensor_ok(out, "output")) return HK_INVALID_ARGUMENT;
+    if (!same_shape(in, out)) return fail(HK_INVALID_ARGUMENT, "cast output shape mismatch");
+    const bool f2b = in->dtype == HK_F32 && out->dtype == HK_BF16;
+    const bool b2f = in->dtype == HK_BF16 && out->dtype == HK_F32;
+    if (!f2b && !b2f) return fail(HK_INVALID_ARGUMENT, "cast supports F32 <-> BF16");
+    if (!disjoint({out}, {in})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::cast_apply(f2b ? 1 : 0, in->data, out->data, numel(in), g.c->stream);
+    return complete(g.c, e, "cast", 1);
+}
+
+// ------------------------------------------------------------------ RMSNorm
+
+hk_status hk_rms_norm(hk_context* h, const hk_tensor* x, const hk_tensor* w, double eps, hk_tensor* y,
+                      hk_tensor* rstd) {
+    // Reference: normalization.rs:153-166 (+ layout_for / epsilon_for, :12-48).
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "weight") || !tensor_ok(y, "Y") || !tensor_ok(rstd, "rstd"))
+        return HK_INVALID_ARGUMENT;
+    int64_t rows, width;
+    if (!row_layout(x, &rows, &width, "RMSNorm")) return HK_INVALID_ARGUMENT;
+    if (x->dtype != HK_F32 && x->dtype != HK_BF16) return fail(HK_INVALID_ARGUMENT, "RMSNorm input must be F32 or BF16");
+    const float e32 = static_cast<float>(eps);
+    if (!std::isfinite(eps) || !std::isfinite(e32) || !(e32 > 0.0f))
+        return fail(HK_INVALID_ARGUMENT, "RMSNorm epsilon must be positive and representable in FP32");
+    if (w->dtype != HK_F32 || w->rank != 1 || w->shape[0] != width)
+        return fail(HK_INVALID_ARGUMENT, "RMSNorm weight must be F32 [%lld]", (long long)width);
+    if (y->dtype != x->dtype || !same_shape(x, y)) return fail(HK_INVALID_ARGUMENT, "RMSNorm output must match the input");
+    if (rstd->dtype != HK_F32 || numel(rstd) != rows)
+        return fail(HK_INVALID_ARGUMENT, "rstd must be F32 with one value per row (%lld)", (long long)rows);
+    if (!disjoint({y, rstd}, {x, w})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::rms_norm_forward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), y->data,
+                                        static_cast<float*>(rstd->data), rows, width, e32, g.c->stream);
+    return complete(g.c, e, "rms_norm", rows ? 1 : 0);
+}
+
+hk_status hk_rms_norm_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                               const hk_tensor* rstd, hk_tensor* dx, hk_tensor* dw) {
+    // Reference: normalization.rs:168-186.
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "weight") || !tensor_ok(dy, "dY") || !tensor_ok(rstd, "rstd") ||
+        !tensor_ok(dx, "dX") || !tensor_ok(dw, "dW"))
+        return HK_INVALID_ARGUMENT;
+    int64_t rows, width;
+    if (!row_layout(x, &rows, &width, "RMSNorm")) return HK_INVALID_ARGUMENT;
+    if (x->dtype != HK_F32 && x->dtype != HK_BF16) return fail(HK_INVALID_ARGUMENT, "RMSNorm input must be F32 or BF16");
+    if (w->dtype != HK_F32 || w->rank != 1 || w->shape[0] != width)
+        return fail(HK_INVALID_ARGUMENT, "RMSNorm weight must be F32 [%lld]", (long long)width);
+    if (dy->dtype != x->dtype || !same_shape(dy, x)) return fail(HK_INVALID_ARGUMENT, "dY must match X");
+    if (dx->dtype != x->dtype || !same_shape(dx, x)) return fail(HK_INVALID_ARGUMENT, "dX must match X");
+    if (rstd->dtype != HK_F32 || numel(rstd) != rows) return fail(HK_INVALID_ARGUMENT, "rstd must be F32 [rows]");
+    if (dw->dtype != HK_F32 || numel(dw) != width) return fail(HK_INVALID_ARGUMENT, "dW must be F32 [width]");
+    if (!disjoint({dx, dw}, {x, w, dy, rstd})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hk_status st = ensure_workspace(g.c, hk::rms_backward_workspace_bytes(rows, width));
+    if (st != HK_OK) return st;
+    hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
+                                         static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
+                                         static_cast<float*>(g.c->workspace), rows, width, g.c->stream);
+    return complete(g.c, e, "rms_norm_backward", 2);
+}
+
+// ------------------------------------------------------------------ RoPE
+
+static hk_status rotary_common(hk_context* h, const hk_tensor* x, const hk_tensor* c, const hk_tensor* s,
+                               int64_t p, bool prefix, int32_t layout, bool backward, hk_tensor* y) {
+    if (!tensor_ok(x, "X") || !tensor_ok(c, "cos") || !tensor_ok(s, "sin") || !tensor_ok(y, "Y"))
+        return HK_INVALID_ARGUMENT;
+    if (layout != HK_ROTARY_INTERLEAVED && layout != HK_ROTARY_SPLIT_HALF)
+        return fail(HK_INVALID_ARGUMENT, "rotary layout must be 0 (Interleaved) or 1 (SplitHalf)");
+    if (x->dtype != HK_F32 && x->dtype != HK_BF16) return fail(HK_INVALID_ARGUMENT, "rotary input must be F32 or BF16");
+    if (c->dtype != HK_F32 || s->dtype != HK_F32) return fail(HK_INVALID_ARGUMENT, "rotary tables must be F32");
+    if (y->dtype != x->dtype || !same_shape(x, y)) return fail(HK_INVALID_ARGUMENT, "rotary output must match the input");
+    if (!same_shape(c, s)) return fail(HK_INVALID_ARGUMENT, "cos and sin tables must have one shape");
+    const int rank = x->rank;
+    hk::RopeMap map{};
+    if (rank < 1 || rank > 8) return fail(HK_INVALID_ARGUMENT, "rotary requires rank 1..8");
+    const int64_t width = x->shape[rank - 1];
+    if (!prefix) {
+        // Reference: runtime/rotary.rs:6-14 (table shape = input shape with the width halved).
+        p = width;
+        if (width <= 0 || width % 2 != 0)
+            return fail(HK_INVALID_ARGUMENT, "rotary requires a positive even width");
+        bool ok = c->rank == rank;
+        for (int i = 0; ok && i < rank - 1; ++i) ok = c->shape[i] == x->shape[i];
+        if (!ok || c->shape[rank - 1] != width / 2)
+            return fail(HK_INVALID_ARGUMENT, "rotary tables must have the input shape with the last axis halved");
+        map.same_row = 1;
+    } else {
+        // Reference: PrefixRotarySpec::elements, rotary_programs.rs:11-23.
+        if (c->rank != rank)
+            return fail(HK_INVALID_ARGUMENT, "rotary prefix requires equal input/table ranks within 1..8");
+        bool ok = p > 0 && p % 2 == 0 && p <= width && c->shape[rank - 1] == p / 2;
+        for (int i = 0; ok && i < rank - 1; ++i) ok = c->shape[i] == 1 || c->shape[i] == x->shape[i];
+        if (!ok)
+            return fail(HK_INVALID_ARGUMENT,
+                        "rotary prefix requires positive even P<=D, table last axis P/2 and singleton or matching leading axes");
+        map.same_row = 0;
+        map.nlead = rank - 1;
+        int64_t tstride = 1;  // in units of table rows
+        for (int a = rank - 2; a >= 0; --a) {
+            map.shape[a] = x->shape[a];
+            map.tstride[a] = c->shape[a] == 1 ? 0 : tstride;
+            tstride *= c->shape[a];
+        }
+    }
+    if (!disjoint({y}, {x, c, s})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t rows = width > 0 ? numel(x) / width : 0;
+    hipError_t e = hk::rope_apply(x->dtype == HK_BF16, x->data, static_cast<const float*>(c->data),
+                                  static_cast<const float*>(s->data), y->data, rows, width, p, layout,
+                                  backward ? 1 : 0, map, g.c->stream);
+    return complete(g.c, e, prefix ? "rotary_prefix" : "rotary", rows ? 1 : 0);
+}
+
+hk_status hk_rotary(hk_context* h, const hk_tensor* x, const hk_tensor* c, const hk_tensor* s, int32_t layout,
+                    hk_tensor* y) {
+    return rotary_common(h, x, c, s, 0, false, layout, false, y);
+}
+hk_status hk_rotary_backward(hk_context* h, const hk_tensor* dy, const hk_tensor* c, const hk_tensor* s,
+                             int32_t layout, hk_tensor* dx) {
+    return rotary_common(h, dy, c, s, 0, false, layout, true, dx);
+}
+hk_status hk_rotary_prefix(hk_context* h, const hk_tensor* x, const hk_tensor* c, const hk_tensor* s, int32_t width,
+                           int32_t layout, hk_tensor* y) {
+    return rotary_common(h, x, c, s, width, true, layout, false, y);
+}
+hk_status hk_rotary_prefix_backward(hk_context* h, const hk_tensor* dy, const hk_tensor* c, const hk_tensor* s,
+                                    int32_t width, int32_t layout, hk_tensor* dx) {
+    return rotary_common(h, dy, c, s, width, true, layout, true, dx);
+}
+
+// ------------------------------------------------------------------ attention
+
+static hk_status attention_shape(const hk_tensor* q, const hk_tensor* k, const hk_tensor* v, float scale,
+                                 int32_t causal, uint64_t qs, uint64_t ks, hk::AttnShape* sh) {
+    if (!tensor_ok(q, "Q") || !tensor_ok(k, "K") || !tensor_ok(v, "V")) return HK_INVALID_ARGUMENT;
+    if (q->rank != 4 || k->rank != 4 || v->rank != 4)
+        return fail(HK_INVALID_ARGUMENT, "attention requires rank-4 Q[B,Hq,M,D], K/V[B,Hkv,N,D]");
+    if (q->dtype != HK_BF16 || k->dtype != HK_BF16 || v->dtype != HK_BF16)
+        return fail(HK_INVALID_ARGUMENT, "fused attention requires BF16 Q/K/V");
+    const int64_t B = q->shape[0], H = q->shape[1], M = q->shape[2], D = q->shape[3];
+    const int64_t Hkv = k->shape[1], N = k->shape[2];
+    // Reference: validate_gqa / validate_dimensions, src/nn/attention.rs:81-104.
+    if (H <= 0 || Hkv <= 0 || H % Hkv != 0 || k->shape[0] != B || v->shape[0] != B || v->shape[1] != Hkv ||
+        k->shape[3] != D || v->shape[2] != N)
+        return fail(HK_INVALID_ARGUMENT,
+                    "GQA requires matching batches, positive divisible Q/KV heads and matching K/V lengths and Q/K widths");
+    if (v->shape[3] != D) return fail(HK_INVALID_ARGUMENT, "fused attention requires the value width to equal D");
+    if (B <= 0 || B * H > 4096 || M <= 0 || N <= 0 || M > INT32_MAX || N > INT32_MAX || !std::isfinite(scale))
+        return fail(HK_INVALID_ARGUMENT,
+                    "attention requires 1..4096 flattened batches, positive M/N within INT32_MAX and a finite scale");
+    if (!(D == 16 || D == 32 || D == 64 || D == 128))
+        return fail(HK_INVALID_ARGUMENT, "fused attention supports head dims 16, 32, 64 and 128 (got %lld)", (long long)D);
+    if (causal && (qs > UINT64_MAX - static_cast<uint64_t>(M - 1) || ks > UINT64_MAX - static_cast<uint64_t>(N - 1)))
+        return fail(HK_INVALID_ARGUMENT, "causal absolute position overflow");
+    sh->batch = B;
+    sh->heads = H;
+    sh->kv_heads = Hkv;
+    sh->m = M;
+    sh->n = N;
+    sh->d = D;
+    sh->scale = scale;
+    sh->causal = causal ? 1 : 0;
+    sh->query_start = causal ? qs : 0;
+    sh->key_start = causal ? ks : 0;
+    return HK_OK;
+}
+
+hk_status hk_attention_forward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v, float scale,
+                               int32_t causal, uint64_t qs, uint64_t ks, hk_tensor* o, hk_tensor* lse) {
+    hk::AttnShape sh;
+    hk_status st = attention_shape(q, k, v, scale, causal, qs, ks, &sh);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(o, "O") || !tensor_ok(lse, "lse")) return HK_INVALID_ARGUMENT;
+    if (o->dtype != HK_BF16 || !same_shape(o, q)) return fail(HK_INVALID_ARGUMENT, "O must be BF16 shaped like Q");
+    if (lse->dtype != HK_F32 || lse->rank != 3 || lse->shape[0] != sh.batch || lse->shape[1] != sh.heads ||
+        lse->shape[2] != sh.m)
+        return fail(HK_INVALID_ARGUMENT, "lse must be F32 [B,Hq,M]");
+    if (!disjoint({o, lse}, {q, k, v})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::attention_forward(sh, q->data, k->data, v->data, o->data, static_cast<float*>(lse->data),
+                                         g.c->stream);
+    return complete(g.c, e, "attention_forward", 1);
+}
+
+hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                const hk_tensor* o, const hk_tensor* lse, const hk_tensor* dout, float scale,
+                                int32_t causal, uint64_t qs, uint64_t ks, hk_tensor* dq, hk_tensor* dk,
+                                hk_tensor* dv) {
+    hk::AttnShape sh;
+    hk_status st = attention_shape(q, k, v, scale, causal, qs, ks, &sh);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(o, "O") || !tensor_ok(lse, "lse") || !tensor_ok(dout, "dO") || !tensor_ok(dq, "dQ") ||
+        !tensor_ok(dk, "dK") || !tensor_ok(dv, "dV"))
+        return HK_INVALID_ARGUMENT;
+    if (o->dtype != HK_BF16 || !same_shape(o, q) || dout->dtype != HK_BF16 || !same_shape(dout, q))
+        return fail(HK_INVALID_ARGUMENT, "O and dO must be BF16 shaped like Q");
+    if (lse->dtype != HK_F32 || lse->rank != 3 || lse->shape[0] != sh.batch || lse->shape[1] != sh.heads ||
+        lse->shape[2] != sh.m)
+        return fail(HK_INVALID_ARGUMENT, "lse must be F32 [B,Hq,M]");
+    if (!same_shape(dq, q) || !same_shape(dk, k) || !same_shape(dv, v))
+        return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must have the shapes of Q/K/V");
+    if ((dq->dtype != HK_F32 && dq->dtype != HK_BF16) || (dk->dtype != HK_F32 && dk->dtype != HK_BF16) ||
+        dv->dtype != dk->dtype)
+        return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must be F32 or BF16 (dK and dV alike)");
+    if (!disjoint({dq, dk, dv}, {q, k, v, o, lse, dout})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, hk::attention_bwd_workspace_bytes(sh))) != HK_OK) return st;
+    hipError_t e = hk::attention_backward(sh, q->data, k->data, v->data, o->data, static_cast<const float*>(lse->data),
+                                          dout->data, dq->data, dq->dtype == HK_BF16, dk->data, dv->data,
+                                          dk->dtype == HK_BF16, g.c->workspace, g.c->stream);
+    return complete(g.c, e, "attention_backward", 3);
+}
+
+}  // extern "C"

@@ -1,0 +1,257 @@
+// hk_gemm.hip — BF16 GEMM with FP32 accumulation for gfx950 (MI355X).
+//
+// Semantics (reference rust-ascend-kernels/src/kernel.rs:5-76, ascend.rs:22-68):
+//   C[g, i, j] = sum_k A'[g, i, k] * B'[g, k, j]  with FP32 accumulation,
+//   C stored as BF16 (round to nearest even) or F32. A' is A ([M,K]) or A^T (A stored
+//   [K,M]); B' is B ([K,N]) or B^T (B stored [N,K]). Batched operands are contiguous
+//   [G, ...] with strides M*K, N*K, M*N (ascend.rs:88-114).
+//
+// Design (MI355X-first, not a translation of the reference's 64x64 Ascend tiles):
+//   * Core kernel: both operands K-contiguous ("NT": A [M,K], B [N,K]). Operands that are
+//     MN-contiguous are first transposed into the workspace by an HBM-bound kernel.
+//   * Workgroup = 4 wavefronts (2x2) computing a BMxBN output tile (256x256 for large
+//     problems; 128 or 64 when a 256 grid would not fill the 256 CUs). Each wave owns a
+//     (BM/2)x(BN/2) block of 32x32 MFMA tiles, v_mfma_f32_32x32x16_bf16, accumulators in
+//     the AGPR half of the register file.
+//   * K loop in steps of BK = 64: A and B slices are prefetched from HBM into registers one
+//     step ahead, written to a double-buffered LDS tile (rows of 64 BF16 = 128 B, 16-byte
+//     chunks XOR-swizzled by row%8 so both the row-contiguous writes and the 32-row
+//     fragment reads are bank-conflict-free), one barrier per step.
+//   * MFMA operand order is swapped (B tile as the MFMA "A" operand) so each lane ends with
+//     4 consecutive output columns per register group: 8-byte BF16 / 16-byte F32 stores.
+//   * Tile order: blocks are remapped so each of the 8 XCDs (blockIdx % 8) receives a
+//     contiguous range of tiles, then grouped in 8-tile-row bands, so tiles that share A/B
+//     slices run on the same XCD's L2.
+#include "hk_common.hpp"
+#include "hk_kernels.hpp"
+
+namespace hk {
+
+namespace {
+
+constexpr int kBK = 64;
+constexpr int kThreads = 256;
+
+struct GemmArgs {
+    const uint16_t* a;  // [batch][m][k]
+    const uint16_t* b;  // [batch][n][k]
+    void* c;            // [batch][m][n]
+    int m, n, k;
+    int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
+
+template <int BM, int BN, bool OUT_BF16>
+__global__ void __launch_bounds__(kThreads)
+gemm_nt_kernel(GemmArgs p) {
+    constexpr int TI = BM / 64;          // 32x32 tiles per wave along M
+    constexpr int TJ = BN / 64;          // along N
+    constexpr int A_LOADS = BM * 8 / kThreads;  // 16-byte chunks per thread per K step
+    constexpr int B_LOADS = BN * 8 / kThreads;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * kBK];
+
+    // ---- tile coordinates: XCD-contiguous ranges, then 8-row grouped order
+    const int tiles = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+    constexpr int GROUP = 8;
+    const int per_group = GROUP * p.tiles_n;
+    const int first_m = (bid / per_group) * GROUP;
+    const int gsize = min(p.tiles_m - first_m, GROUP);
+    const int tm = first_m + (bid % per_group) % gsize;
+    const int tn = (bid % per_group) / gsize;
+    const int64_t g = blockIdx.z;
+
+    const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
+    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // ---- global -> register prefetch assignment
+    const int lcol = t & 7;   // 16-byte chunk within the 64-wide K slice
+    const int lrow = t >> 3;  // 0..31, plus 32*i
+    const uint16_t* a_src[A_LOADS];
+    const uint16_t* b_src[B_LOADS];
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+        int r = tm * BM + lrow + 32 * i;
+        r = r < p.m ? r : p.m - 1;  // rows past M read a valid row; their outputs are not stored
+        a_src[i] = A + static_cast<int64_t>(r) * p.k + lcol * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+        int r = tn * BN + lrow + 32 * i;
+        r = r < p.n ? r : p.n - 1;
+        b_src[i] = B + static_cast<int64_t>(r) * p.k + lcol * 8;
+    }
+    u32x4_t ra[A_LOADS], rb[B_LOADS];
+    auto load_global = [&](int kt) {
+        const int kk = kt * kBK + lcol * 8;
+        const bool in = kk < p.k;  // K % 16 == 0: a 16-byte chunk is wholly in or out
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i)
+            ra[i] = in ? *reinterpret_cast<const u32x4_t*>(a_src[i] + kt * kBK) : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i)
+            rb[i] = in ? *reinterpret_cast<const u32x4_t*>(b_src[i] + kt * kBK) : u32x4_t{0, 0, 0, 0};
+    };
+    auto store_lds = [&](int buf) {
+        uint16_t* la = lds[buf];
+        uint16_t* lb = lds[buf] + BM * kBK;
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i)
+            *reinterpret_cast<u32x4_t*>(la + swz(lrow + 32 * i, lcol)) = ra[i];
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i)
+            *reinterpret_cast<u32x4_t*>(lb + swz(lrow + 32 * i, lcol)) = rb[i];
+    };
+
+    f32x16_t acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const int nk = (p.k + kBK - 1) / kBK;
+    load_global(0);
+    store_lds(0);
+    if (nk > 1) load_global(1);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const uint16_t* la = lds[cur];
+        const uint16_t* lb = lds[cur] + BM * kBK;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            const int chunk = ks * 2 + lk;
+            bf16x8_t af[TI], bfr[TJ];
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+                af[i] = *reinterpret_cast<const bf16x8_t*>(la + swz(wm * (BM / 2) + i * 32 + lr, chunk));
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                bfr[j] = *reinterpret_cast<const bf16x8_t*>(lb + swz(wn * (BN / 2) + j * 32 + lr, chunk));
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            store_lds(cur ^ 1);
+            if (kt + 2 < nk) load_global(kt + 2);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: lane holds C[m = .. + lr][n = .. + 8*grp + 4*lk + 0..3]
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int m = tm * BM + wm * (BM / 2) + i * 32 + lr;
+        if (m >= p.m) continue;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int n = tn * BN + wn * (BN / 2) + j * 32 + grp * 8 + lk * 4;
+                if (n >= p.n) continue;
+                const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
+                if constexpr (OUT_BF16) {
+                    u32x2_t w = {pack_bf16x2(acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1]),
+                                 pack_bf16x2(acc[i][j][grp * 4 + 2], acc[i][j][grp * 4 + 3])};
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = w;
+                } else {
+                    f32x4_t w = {acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1], acc[i][j][grp * 4 + 2],
+                                 acc[i][j][grp * 4 + 3]};
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.c) + off) = w;
+                }
+            }
+        }
+    }
+}
+
+// out[g][c][r] = in[g][r][c] for BF16, 64x64 tiles through LDS (padded rows).
+__global__ void __launch_bounds__(256)
+transpose_bf16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t rows, int64_t cols) {
+    __shared__ uint16_t tile[64][66];
+    const int64_t g = blockIdx.z;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const uint16_t* src = in + g * rows * cols;
+    uint16_t* dst = out + g * rows * cols;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) tile[i][tx] = src[r * cols + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t c = c0 + i, r = r0 + tx;
+        if (r < rows && c < cols) dst[c * rows + r] = tile[tx][i];
+    }
+}
+
+template <int BM, int BN>
+void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
+    GemmArgs p = a;
+    p.tiles_m = (p.m + BM - 1) / BM;
+    p.tiles_n = (p.n + BN - 1) / BN;
+    const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), 1, static_cast<unsigned>(batch));
+    if (out_bf16)
+        hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, false>), grid, dim3(kThreads), 0, s, p);
+}
+
+size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k, int ta, int tb) {
+    size_t bytes = 0;
+    if (ta) bytes += round256(static_cast<size_t>(batch * m * k) * 2);
+    if (!tb) bytes += round256(static_cast<size_t>(batch * n * k) * 2);
+    return bytes;
+}
+
+hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_t batch, int64_t m, int64_t n,
+                     int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s) {
+    const uint16_t* ak = static_cast<const uint16_t*>(a);
+    const uint16_t* bk = static_cast<const uint16_t*>(b);
+    char* ws = static_cast<char*>(workspace);
+    if (ta) {  // A stored [K,M] -> [M,K]
+        uint16_t* t = reinterpret_cast<uint16_t*>(ws);
+        hipLaunchKernelGGL(transpose_bf16, dim3((unsigned)((m + 63) / 64), (unsigned)((k + 63) / 64), (unsigned)batch),
+                           dim3(256), 0, s, ak, t, k, m);
+        ak = t;
+        ws += round256(static_cast<size_t>(batch * m * k) * 2);
+    }
+    if (!tb) {  // B stored [K,N] -> [N,K]
+        uint16_t* t = reinterpret_cast<uint16_t*>(ws);
+        hipLaunchKernelGGL(transpose_bf16, dim3((unsigned)((n + 63) / 64), (unsigned)((k + 63) / 64), (unsigned)batch),
+                           dim3(256), 0, s, bk, t, k, n);
+        bk = t;
+    }
+    GemmArgs p{};
+    p.a = ak;
+    p.b = bk;
+    p.c = c;
+    p.m = static_cast<int>(m);
+    p.n = static_cast<int>(n);
+    p.k = static_cast<int>(k);
+    const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
+    const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128) * batch;
+    if (t256 >= num_cus) launch_nt<256, 256>(p, batch, out_bf16, s);
+    else if (t128 >= num_cus) launch_nt<128, 128>(p, batch, out_bf16, s);
+    else launch_nt<64, 64>(p, batch, out_bf16, s);
+    return hipGetLastError();
+}
+
+}  // namespace hk

@@ -1,0 +1,56 @@
+// hk_kernels.hpp — host-side launchers of the gfx950 kernels (internal to libhk.so).
+// Each launcher enqueues work on `s` and returns hipGetLastError(); shapes were
+// validated by the C-ABI layer (hk_driver.cpp) before any launcher is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hk {
+
+// ---- RMSNorm (hk_rmsnorm.hip)
+// Bytes of workspace the backward needs for its FP32 dw partial rows.
+size_t rms_backward_workspace_bytes(int64_t rows, int64_t width);
+hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void* y, float* rstd,
+                            int64_t rows, int64_t width, float eps, hipStream_t s);
+hipError_t rms_norm_backward(int dtype_bf16, const void* x, const float* w, const void* dy,
+                             const float* rstd, void* dx, float* dw, float* workspace, int64_t rows,
+                             int64_t width, hipStream_t s);
+
+// ---- RoPE and casts (hk_rope.hip)
+// Table row of input row r: sum over leading axes a of coord_a(r) * tstride[a]
+// (tstride 0 on broadcast axes); same_row means table row == input row.
+struct RopeMap {
+    int32_t same_row;
+    int32_t nlead;
+    int64_t shape[7];
+    int64_t tstride[7];
+};
+hipError_t rope_apply(int dtype_bf16, const void* x, const float* cos_t, const float* sin_t, void* y,
+                      int64_t rows, int64_t width, int64_t p, int layout, int backward,
+                      const RopeMap& map, hipStream_t s);
+hipError_t cast_apply(int to_bf16, const void* in, void* out, int64_t n, hipStream_t s);
+
+// ---- GEMM (hk_gemm.hip)
+// C[g] = op(A[g]) op(B[g]) for g < batch; A, B BF16; C BF16 or F32. ta/tb as in the
+// reference (0 = row-major [M,K] / [K,N]; 1 = [K,M] / [N,K]). Operands that are not
+// K-contiguous are first transposed into `workspace` (gemm_workspace_bytes).
+size_t gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k, int ta, int tb);
+hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_t batch, int64_t m,
+                     int64_t n, int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s);
+
+// ---- attention (hk_attention.hip)
+struct AttnShape {
+    int64_t batch, heads, kv_heads, m, n, d;
+    float scale;
+    int32_t causal;
+    uint64_t query_start, key_start;
+};
+size_t attention_bwd_workspace_bytes(const AttnShape& sh);
+hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o,
+                             float* lse, hipStream_t s);
+hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k, const void* v,
+                              const void* o, const float* lse, const void* dout, void* dq, int dq_bf16,
+                              void* dk, void* dv, int dkv_bf16, void* workspace, hipStream_t s);
+
+}  // namespace hk

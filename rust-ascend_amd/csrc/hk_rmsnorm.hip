@@ -1,0 +1,403 @@
+// hk_rmsnorm.hip — RMSNorm forward and backward for gfx950.
+//
+// Semantics (reference, paths relative to the shuqi2077/rust-ascend root):
+//   forward  rust-ascend-compiler/src/ascend/row_programs.rs:144-151
+//            rstd = 1/sqrt(sum(x^2)/W + eps); y = (x*rstd)*w
+//   backward row_programs.rs:208-217 (input) and :200-207 (weight contributions)
+//            g = dy*w; mean = sum(g*x)/W; dx = (g - x*(mean*rstd^2))*rstd
+//            dw[c] = sum_rows (x*rstd)*dy, the column sum of normalization.rs:95-114
+//
+// Layout: x/y/dy/dx are [rows, W] row-major in F32 or BF16; w is F32 [W]; rstd is F32
+// [rows]; dw is F32 [W]. HBM-bound: per row the forward moves W*(2 sizeof(T)) bytes
+// and the backward W*(3 sizeof(T)) bytes.
+//
+// Fast path (W % 8 == 0, W <= 4096): one wavefront owns one row at a time; lane l
+// owns the 8-element chunks l, l+64, l+128, ... (16-byte loads for BF16, fully
+// coalesced), so a row is MAXJ chunks per lane held in registers. Each wave keeps its
+// columns' w (and, in the backward, its dw partial sums) in registers across a
+// grid-stride loop over rows, so w is read once per wave, not once per row. Row sums
+// are butterfly reductions across the wave (no LDS, no barriers). The backward writes
+// one FP32 dw partial per workgroup (waves combined through LDS in wave order) and a
+// second kernel sums the partials in workgroup order: deterministic, no atomics.
+//
+// General path (any positive W): the same math with one element per lane-step and the
+// row re-read from cache for the second pass; dw comes from a column-parallel kernel.
+#include "hk_common.hpp"
+#include "hk_kernels.hpp"
+
+#include <initializer_list>
+
+namespace hk {
+
+namespace {
+
+constexpr int kRowsThreads = 256;  // 4 waves per workgroup (forward)
+constexpr int kBwdThreads = 512;   // 8 waves per workgroup (backward)
+
+template <typename T, int MAXJ>
+__global__ void __launch_bounds__(kRowsThreads)
+rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y,
+             float* __restrict__ rstd, int64_t rows, int width, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int waves_per_block = blockDim.x >> 6;
+    const int chunks = width >> 3;
+    float wr[MAXJ][8];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) load8(w + 8 * c, wr[j]);
+    }
+    const float inv_w = 1.0f / static_cast<float>(width);
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * waves_per_block) {
+        const T* xr = x + row * width;
+        float v[MAXJ][8];
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) load8(xr + 8 * c, v[j]);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+            }
+        }
+        ss = wave_sum(ss);
+        const float r = 1.0f / sqrtf(ss * inv_w + eps);
+        T* yr = y + row * width;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (v[j][e] * r) * wr[j][e];
+                store8(yr + 8 * c, o);
+            }
+        }
+        if (lane == 0) rstd[row] = r;
+    }
+}
+
+// Eight elements kept in their storage form between the two passes over a row
+// (4 VGPRs for BF16, 8 for F32) and widened to float on use.
+template <typename T> struct Raw8;
+template <> struct Raw8<uint16_t> {
+    u32x4_t w;
+    __device__ __forceinline__ void load(const uint16_t* p) { w = *reinterpret_cast<const u32x4_t*>(p); }
+    // Opaque to the optimizer: the widening below is recomputed after this point instead
+    // of being kept live (as 8 extra VGPRs per chunk) across the row reduction.
+    __device__ __forceinline__ void pin() { asm volatile("" : "+v"(w)); }
+    __device__ __forceinline__ void get(float (&v)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = bf16lo(w[i]);
+            v[2 * i + 1] = bf16hi(w[i]);
+        }
+    }
+};
+template <> struct Raw8<float> {
+    f32x4_t a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = *reinterpret_cast<const f32x4_t*>(p);
+        b = *reinterpret_cast<const f32x4_t*>(p + 4);
+    }
+    __device__ __forceinline__ void pin() {}
+    __device__ __forceinline__ void get(float (&v)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = a[i];
+            v[4 + i] = b[i];
+        }
+    }
+};
+
+template <typename T, int MAXJ>
+__global__ void __launch_bounds__(kBwdThreads)
+rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
+             const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ partial,
+             int64_t rows, int width) {
+    extern __shared__ float lds[];  // [width] weight, then [width] partial of the workgroup
+    float* w_lds = lds;
+    float* p_lds = lds + width;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int waves_per_block = blockDim.x >> 6;
+    const int chunks = width >> 3;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) w_lds[c] = w[c];
+    __syncthreads();
+    float acc[MAXJ][8];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+    const float inv_w = 1.0f / static_cast<float>(width);
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * waves_per_block) {
+        const T* xr = x + row * width;
+        const T* gr = dy + row * width;
+        Raw8<T> xs[MAXJ], gs[MAXJ];
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                xs[j].load(xr + 8 * c);
+                gs[j].load(gr + 8 * c);
+            }
+        }
+        const float r = rstd[row];
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                float xv[8], gv[8], wv[8];
+                xs[j].get(xv);
+                gs[j].get(gv);
+                load8(w_lds + 8 * c, wv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    dot += (gv[e] * wv[e]) * xv[e];
+                    acc[j][e] += (xv[e] * r) * gv[e];
+                }
+            }
+        }
+        dot = wave_sum(dot);
+        const float corr = (dot * inv_w) * (r * r);
+        T* dr = dx + row * width;
+#pragma unroll
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                float xv[8], gv[8], wv[8], o[8];
+                xs[j].pin();
+                gs[j].pin();
+                xs[j].get(xv);
+                gs[j].get(gv);
+                load8(w_lds + 8 * c, wv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (gv[e] * wv[e] - xv[e] * corr) * r;
+                store8(dr + 8 * c, o);
+            }
+        }
+    }
+    // Combine the waves' dw partial sums in wave order, then write the workgroup's.
+    for (int src = 0; src < waves_per_block; ++src) {
+        if (wave == src) {
+#pragma unroll
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = lane + 64 * j;
+                if (c < chunks) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        float* p = &p_lds[8 * c + e];
+                        *p = (src == 0) ? acc[j][e] : (*p + acc[j][e]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* out = partial + static_cast<int64_t>(blockIdx.x) * width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = p_lds[c];
+}
+
+// dw[c] = sum over p of partial[p][c], p ascending within each of 8 slices, then the
+// slices in order: fixed order for a given (parts, width).
+__global__ void __launch_bounds__(256)
+sum_partials(const float* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
+    __shared__ float red[8][33];
+    const int col = blockIdx.x * 32 + (threadIdx.x & 31);
+    const int slice = threadIdx.x >> 5;
+    float s = 0.0f;
+    if (col < width)
+        for (int p = slice; p < parts; p += 8) s += partial[static_cast<int64_t>(p) * width + col];
+    red[slice][threadIdx.x & 31] = s;
+    __syncthreads();
+    if (slice == 0 && col < width) {
+        float t = red[0][threadIdx.x];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) t += red[i][threadIdx.x];
+        dw[col] = t;
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kRowsThreads)
+rms_fwd_general(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y,
+                float* __restrict__ rstd, int64_t rows, int64_t width, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int waves_per_block = blockDim.x >> 6;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * waves_per_block) {
+        const T* xr = x + row * width;
+        float ss = 0.0f;
+        for (int64_t c = lane; c < width; c += 64) {
+            const float v = Elem<T>::load(xr, c);
+            ss += v * v;
+        }
+        ss = wave_sum(ss);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(width) + eps);
+        T* yr = y + row * width;
+        for (int64_t c = lane; c < width; c += 64) Elem<T>::store(yr, c, (Elem<T>::load(xr, c) * r) * w[c]);
+        if (lane == 0) rstd[row] = r;
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kRowsThreads)
+rms_bwd_dx_general(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
+                   const float* __restrict__ rstd, T* __restrict__ dx, int64_t rows, int64_t width) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int waves_per_block = blockDim.x >> 6;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * waves_per_block) {
+        const T* xr = x + row * width;
+        const T* gr = dy + row * width;
+        const float r = rstd[row];
+        float dot = 0.0f;
+        for (int64_t c = lane; c < width; c += 64)
+            dot += (Elem<T>::load(gr, c) * w[c]) * Elem<T>::load(xr, c);
+        dot = wave_sum(dot);
+        const float corr = (dot / static_cast<float>(width)) * (r * r);
+        T* dr = dx + row * width;
+        for (int64_t c = lane; c < width; c += 64)
+            Elem<T>::store(dr, c, (Elem<T>::load(gr, c) * w[c] - Elem<T>::load(xr, c) * corr) * r);
+    }
+}
+
+// partial[chunk][c] = sum over the chunk's rows of (x*rstd)*dy, rows ascending.
+template <typename T>
+__global__ void __launch_bounds__(256)
+rms_bwd_dw_general(const T* __restrict__ x, const T* __restrict__ dy, const float* __restrict__ rstd,
+                   float* __restrict__ partial, int64_t rows, int64_t width, int64_t rows_per_chunk) {
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t chunk = blockIdx.y;
+    if (col >= width) return;
+    const int64_t r0 = chunk * rows_per_chunk;
+    const int64_t r1 = (r0 + rows_per_chunk < rows) ? r0 + rows_per_chunk : rows;
+    float s = 0.0f;
+    for (int64_t r = r0; r < r1; ++r)
+        s += (Elem<T>::load(x, r * width + col) * rstd[r]) * Elem<T>::load(dy, r * width + col);
+    partial[chunk * width + col] = s;
+}
+
+__global__ void fill_zero_f32(float* p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+bool fast_rows(int64_t width, std::initializer_list<const void*> ptrs) {
+    if (width % 8 != 0 || width > 4096) return false;
+    for (const void* p : ptrs)
+        if (!aligned16(p)) return false;
+    return true;
+}
+
+int grid_for_rows(int64_t rows, int waves_per_block, int cap) {
+    int64_t g = (rows + waves_per_block - 1) / waves_per_block;
+    if (g > cap) g = cap;
+    return g < 1 ? 1 : static_cast<int>(g);
+}
+
+template <typename T, int MAXJ>
+void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_t rows, int width,
+                     float eps, hipStream_t s) {
+    const int grid = grid_for_rows(rows, kRowsThreads / 64, 2048);
+    hipLaunchKernelGGL((rms_fwd_fast<T, MAXJ>), dim3(grid), dim3(kRowsThreads), 0, s,
+                       static_cast<const T*>(x), w, static_cast<T*>(y), rstd, rows, width, eps);
+}
+
+template <typename T, int MAXJ>
+void launch_bwd_fast(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
+                     float* partial, int parts, int64_t rows, int width, hipStream_t s) {
+    hipLaunchKernelGGL((rms_bwd_fast<T, MAXJ>), dim3(parts), dim3(kBwdThreads),
+                       2 * static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x), w,
+                       static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
+}
+
+int parts_fast(int64_t rows) { return grid_for_rows(rows, kBwdThreads / 64, 512); }
+int parts_general(int64_t rows) {
+    int64_t parts = (rows + 63) / 64;  // at most 64 rows per column chunk
+    if (parts > 512) parts = 512;
+    return parts < 1 ? 1 : static_cast<int>(parts);
+}
+
+template <typename T>
+hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, int64_t rows,
+                         int64_t width, float eps, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (fast_rows(width, {x, w, y})) {
+        const int chunks_per_lane = static_cast<int>((width / 8 + 63) / 64);
+        if (chunks_per_lane <= 1) launch_fwd_fast<T, 1>(x, w, y, rstd, rows, (int)width, eps, s);
+        else if (chunks_per_lane <= 2) launch_fwd_fast<T, 2>(x, w, y, rstd, rows, (int)width, eps, s);
+        else if (chunks_per_lane <= 4) launch_fwd_fast<T, 4>(x, w, y, rstd, rows, (int)width, eps, s);
+        else launch_fwd_fast<T, 8>(x, w, y, rstd, rows, (int)width, eps, s);
+    } else {
+        const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
+        hipLaunchKernelGGL((rms_fwd_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
+                           static_cast<const T*>(x), w, static_cast<T*>(y), rstd, rows, width, eps);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
+                          float* dw, float* workspace, int64_t rows, int64_t width, hipStream_t s) {
+    if (rows == 0) {
+        hipLaunchKernelGGL(fill_zero_f32, dim3((width + 255) / 256), dim3(256), 0, s, dw, width);
+        return hipGetLastError();
+    }
+    if (fast_rows(width, {x, w, dy, dx})) {
+        const int parts = parts_fast(rows);
+        const int chunks_per_lane = static_cast<int>((width / 8 + 63) / 64);
+        if (chunks_per_lane <= 1) launch_bwd_fast<T, 1>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+        else if (chunks_per_lane <= 2) launch_bwd_fast<T, 2>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+        else if (chunks_per_lane <= 4) launch_bwd_fast<T, 4>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+        else launch_bwd_fast<T, 8>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+        hipLaunchKernelGGL(sum_partials, dim3((width + 31) / 32), dim3(256), 0, s, workspace, parts, (int)width, dw);
+    } else {
+        const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
+        hipLaunchKernelGGL((rms_bwd_dx_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
+                           static_cast<const T*>(x), w, static_cast<const T*>(dy), rstd, static_cast<T*>(dx),
+                           rows, width);
+        const int parts = parts_general(rows);
+        const int64_t per = (rows + parts - 1) / parts;
+        hipLaunchKernelGGL((rms_bwd_dw_general<T>), dim3((width + 255) / 256, parts), dim3(256), 0, s,
+                           static_cast<const T*>(x), static_cast<const T*>(dy), rstd, workspace, rows,
+                           width, per);
+        hipLaunchKernelGGL(sum_partials, dim3((width + 31) / 32), dim3(256), 0, s, workspace, parts, (int)width, dw);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t rms_backward_workspace_bytes(int64_t rows, int64_t width) {
+    const int parts = parts_fast(rows) > parts_general(rows) ? parts_fast(rows) : parts_general(rows);
+    return static_cast<size_t>(parts) * static_cast<size_t>(width) * sizeof(float);
+}
+
+hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void* y, float* rstd,
+                            int64_t rows, int64_t width, float eps, hipStream_t s) {
+    return dtype_bf16 ? rms_forward_t<uint16_t>(x, w, y, rstd, rows, width, eps, s)
+                      : rms_forward_t<float>(x, w, y, rstd, rows, width, eps, s);
+}
+
+hipError_t rms_norm_backward(int dtype_bf16, const void* x, const float* w, const void* dy,
+                             const float* rstd, void* dx, float* dw, float* workspace, int64_t rows,
+                             int64_t width, hipStream_t s) {
+    return dtype_bf16 ? rms_backward_t<uint16_t>(x, w, dy, rstd, dx, dw, workspace, rows, width, s)
+                      : rms_backward_t<float>(x, w, dy, rstd, dx, dw, workspace, rows, width, s);
+}
+
+}  // namespace hk

@@ -1,0 +1,228 @@
+// hk_rope.hip — table-driven rotary position encoding (RoPE) and F32<->BF16 casts.
+//
+// RoPE semantics (reference rust-ascend-compiler/src/ascend/rotary_programs.rs:47-156):
+// the pair (a, b) is (2p, 2p+1) for Interleaved or (p, p+P/2) for SplitHalf;
+//   forward   y_a = x_a*c - x_b*s,  y_b = x_b*c + x_a*s
+//   backward  y_a = x_a*c + x_b*s,  y_b = x_b*c - x_a*s   (the transpose Jacobian)
+// with c, s = cos/sin[table_row, p]. Columns >= P (prefix form) are copied bit-exactly.
+// Table rows broadcast singleton leading axes (rotary_programs.rs:125-139); the full
+// form uses same-row tables (table row = input row).
+//
+// Memory-bound: each thread owns V consecutive pairs of one row (V = 8: 16-byte BF16
+// loads/stores for both halves in SplitHalf, one 32-byte span for Interleaved) and
+// reads V cos and V sin values (F32).
+#include "hk_common.hpp"
+#include "hk_kernels.hpp"
+
+namespace hk {
+
+namespace {
+
+template <typename T, int V>
+__device__ __forceinline__ void load_v(const T* p, float (&v)[V]) {
+    if constexpr (V == 8) {
+        load8(p, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = Elem<T>::load(p, i);
+    }
+}
+template <typename T, int V>
+__device__ __forceinline__ void store_v(T* p, const float (&v)[V]) {
+    if constexpr (V == 8) {
+        store8(p, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) Elem<T>::store(p, i, v[i]);
+    }
+}
+
+__device__ __forceinline__ int64_t table_row(int64_t row, const RopeMap& map) {
+    if (map.same_row) return row;
+    int64_t rem = row, t = 0;
+    for (int a = map.nlead - 1; a >= 0; --a) {
+        const int64_t coord = rem % map.shape[a];
+        rem /= map.shape[a];
+        t += coord * map.tstride[a];
+    }
+    return t;
+}
+
+template <typename T, int V, int LAYOUT, bool BWD>
+__global__ void __launch_bounds__(256)
+rope_pairs(const T* __restrict__ x, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+           T* __restrict__ y, int64_t rows, int64_t width, int64_t half, RopeMap map) {
+    const int64_t per_row = half / V;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= rows * per_row) return;
+    const int64_t row = idx / per_row;
+    const int64_t p0 = (idx - row * per_row) * V;
+    const int64_t t = table_row(row, map) * half + p0;
+    float c[V], s[V], a[V], b[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        c[i] = cos_t[t + i];
+        s[i] = sin_t[t + i];
+    }
+    const T* xr = x + row * width;
+    T* yr = y + row * width;
+    if constexpr (LAYOUT == 1) {
+        load_v<T, V>(xr + p0, a);
+        load_v<T, V>(xr + half + p0, b);
+    } else {
+        float ab[2 * V];
+        if constexpr (V == 8) {
+            float lo[8], hi[8];
+            load8(xr + 2 * p0, lo);
+            load8(xr + 2 * p0 + 8, hi);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ab[i] = lo[i];
+                ab[8 + i] = hi[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2 * V; ++i) ab[i] = Elem<T>::load(xr, 2 * p0 + i);
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            a[i] = ab[2 * i];
+            b[i] = ab[2 * i + 1];
+        }
+    }
+    float ya[V], yb[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        // out = x*cos + sign*(paired*sin), sign = -1 on side a, +1 on side b (negated backward)
+        if constexpr (!BWD) {
+            ya[i] = a[i] * c[i] - b[i] * s[i];
+            yb[i] = b[i] * c[i] + a[i] * s[i];
+        } else {
+            ya[i] = a[i] * c[i] + b[i] * s[i];
+            yb[i] = b[i] * c[i] - a[i] * s[i];
+        }
+    }
+    if constexpr (LAYOUT == 1) {
+        store_v<T, V>(yr + p0, ya);
+        store_v<T, V>(yr + half + p0, yb);
+    } else {
+        if constexpr (V == 8) {
+            float lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo[2 * i] = ya[i];
+                lo[2 * i + 1] = yb[i];
+                hi[2 * i] = ya[4 + i];
+                hi[2 * i + 1] = yb[4 + i];
+            }
+            store8(yr + 2 * p0, lo);
+            store8(yr + 2 * p0 + 8, hi);
+        } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                Elem<T>::store(yr, 2 * (p0 + i), ya[i]);
+                Elem<T>::store(yr, 2 * (p0 + i) + 1, yb[i]);
+            }
+        }
+    }
+}
+
+// Columns [p, width) of every row, copied as raw bits.
+template <typename T>
+__global__ void __launch_bounds__(256)
+copy_tail(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int64_t width, int64_t p) {
+    const int64_t tail = width - p;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= rows * tail) return;
+    const int64_t row = idx / tail;
+    const int64_t col = p + (idx - row * tail);
+    y[row * width + col] = x[row * width + col];
+}
+
+template <typename T, int V, int LAYOUT>
+void launch_pairs(bool bwd, const void* x, const float* c, const float* s, void* y, int64_t rows,
+                  int64_t width, int64_t half, const RopeMap& map, hipStream_t st) {
+    const int64_t n = rows * (half / V);
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    if (bwd)
+        hipLaunchKernelGGL((rope_pairs<T, V, LAYOUT, true>), grid, dim3(256), 0, st, static_cast<const T*>(x), c,
+                           s, static_cast<T*>(y), rows, width, half, map);
+    else
+        hipLaunchKernelGGL((rope_pairs<T, V, LAYOUT, false>), grid, dim3(256), 0, st, static_cast<const T*>(x), c,
+                           s, static_cast<T*>(y), rows, width, half, map);
+}
+
+template <typename T>
+hipError_t rope_t(const void* x, const float* c, const float* s, void* y, int64_t rows, int64_t width,
+                  int64_t p, int layout, bool bwd, const RopeMap& map, hipStream_t st) {
+    const int64_t half = p / 2;
+    if (rows == 0) return hipSuccess;
+    // 8 pairs per thread when every row's pair spans are 16-byte aligned (the tables are
+    // F32 with 8*4 = 32-byte spans, aligned when half % 8 == 0).
+    const bool vec = (half % 8 == 0) && (width % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    if (layout == 0) {
+        if (vec) launch_pairs<T, 8, 0>(bwd, x, c, s, y, rows, width, half, map, st);
+        else launch_pairs<T, 1, 0>(bwd, x, c, s, y, rows, width, half, map, st);
+    } else {
+        if (vec) launch_pairs<T, 8, 1>(bwd, x, c, s, y, rows, width, half, map, st);
+        else launch_pairs<T, 1, 1>(bwd, x, c, s, y, rows, width, half, map, st);
+    }
+    if (p < width) {
+        const int64_t n = rows * (width - p);
+        hipLaunchKernelGGL((copy_tail<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+                           static_cast<const T*>(x), static_cast<T*>(y), rows, width, p);
+    }
+    return hipGetLastError();
+}
+
+// Each thread converts 8 consecutive elements; `vec` (16-byte aligned bases) selects
+// the vector loads/stores, otherwise element accesses.
+__global__ void __launch_bounds__(256)
+cast_f32_to_bf16(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n, int vec) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+    if (vec && i + 8 <= n) {
+        float v[8];
+        load8(in + i, v);
+        store8(out + i, v);
+    } else {
+        for (int64_t j = i; j < n && j < i + 8; ++j) out[j] = f32_to_bf16(in[j]);
+    }
+}
+
+__global__ void __launch_bounds__(256)
+cast_bf16_to_f32(const uint16_t* __restrict__ in, float* __restrict__ out, int64_t n, int vec) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+    if (vec && i + 8 <= n) {
+        float v[8];
+        load8(in + i, v);
+        store8(out + i, v);
+    } else {
+        for (int64_t j = i; j < n && j < i + 8; ++j) out[j] = bf16_to_f32(in[j]);
+    }
+}
+
+}  // namespace
+
+hipError_t rope_apply(int dtype_bf16, const void* x, const float* cos_t, const float* sin_t, void* y,
+                      int64_t rows, int64_t width, int64_t p, int layout, int backward,
+                      const RopeMap& map, hipStream_t s) {
+    return dtype_bf16 ? rope_t<uint16_t>(x, cos_t, sin_t, y, rows, width, p, layout, backward != 0, map, s)
+                      : rope_t<float>(x, cos_t, sin_t, y, rows, width, p, layout, backward != 0, map, s);
+}
+
+hipError_t cast_apply(int to_bf16, const void* in, void* out, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const int64_t threads = (n + 7) / 8;
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    const int vec = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+    if (to_bf16)
+        hipLaunchKernelGGL(cast_f32_to_bf16, grid, dim3(256), 0, s, static_cast<const float*>(in),
+                           static_cast<uint16_t*>(out), n, vec);
+    else
+        hipLaunchKernelGGL(cast_bf16_to_f32, grid, dim3(256), 0, s, static_cast<const uint16_t*>(in),
+                           static_cast<float*>(out), n, vec);
+    return hipGetLastError();
+}
+
+}  // namespace hk

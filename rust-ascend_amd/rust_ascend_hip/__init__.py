@@ -1,0 +1,7 @@
+"""rust_ascend_hip — MI355X (gfx950) BF16 transformer kernel path, the drop-in counterpart of
+rust-ascend's AscendRuntime / nn::* hot path, over libhk.so (include/hk.h)."""
+from ._lib import HkError, LIB_PATH, load
+from .runtime import HipRuntime, RotaryLayout, Transpose, gemm_plan
+from . import nn
+
+__all__ = ["HkError", "LIB_PATH", "load", "HipRuntime", "RotaryLayout", "Transpose", "gemm_plan", "nn"]

@@ -1,0 +1,153 @@
+"""Autograd entry points mirroring the reference's `rust_ascend::nn` functions on
+`Autodiff<Ascend>` (src/nn.rs, src/nn/{attention,rotary}.rs), with torch.autograd standing in
+for RUDA's autodiff graph. Saved state matches the reference's Backward nodes:
+
+* linear_bf16_fp32 / matmul_bf16_fp32 save the BF16 snapshots of both operands
+  (src/nn.rs:375-453), and their backward rounds dY to BF16 before the two GEMMs;
+* rms_norm saves (x, w, rstd) and the backward reuses rstd (src/nn.rs:203-232);
+* rotary/rotary_prefix save nothing but the fixed tables (src/nn/rotary.rs:32-105);
+* the fused attention saves (q, k, v, o, lse) instead of the materialized score,
+  mask and probability tensors of the composed reference (src/nn/attention.rs:10-80).
+"""
+from __future__ import annotations
+
+import torch
+
+from .runtime import HipRuntime, RotaryLayout, Transpose
+
+
+class _LinearBf16Fp32(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w):
+        y, xb, wb = HipRuntime.linear_bf16_fp32(x.contiguous(), w.contiguous())
+        ctx.save_for_backward(xb, wb)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        xb, wb = ctx.saved_tensors
+        dx, dw = HipRuntime.linear_bf16_fp32_backward(xb, wb, dy.contiguous().float())
+        return dx, dw
+
+
+def linear_bf16_fp32(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Y = bf16(X) bf16(W)^T with F32 storage. Reference: nn::linear_bf16_fp32 (src/nn.rs:80-88)."""
+    return _LinearBf16Fp32.apply(x, w)
+
+
+class _MatmulBf16Fp32(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, ta, tb):
+        out, ab, bb = HipRuntime.gemm_bf16_fp32(a.contiguous(), b.contiguous(), ta, tb)
+        ctx.save_for_backward(ab, bb)
+        ctx.ta, ctx.tb = ta, tb
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        ab, bb = ctx.saved_tensors
+        da, db = HipRuntime.gemm_bf16_fp32_backward(ab, bb, dy.contiguous().float(), ctx.ta, ctx.tb)
+        return da, db, None, None
+
+
+def matmul_bf16_fp32(a, b, ta=Transpose.No, tb=Transpose.No) -> torch.Tensor:
+    """op(A) op(B) with BF16 compute and F32 storage. Reference: nn::matmul_bf16_fp32 (src/nn.rs:70-78)."""
+    return _MatmulBf16Fp32.apply(a, b, Transpose(ta), Transpose(tb))
+
+
+class _LinearBf16(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return HipRuntime.gemm(x, w, Transpose.No, Transpose.Yes, torch.bfloat16)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx, dw = HipRuntime.linear_nt_backward(x, w, dy.contiguous().to(torch.bfloat16))
+        return dx, dw.to(w.dtype)
+
+
+def linear_bf16(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """BF16 Y = X W^T with F32 accumulation (DeepGemm dense NT); backward through
+    AscendRuntime::linear_nt_backward semantics (BF16 dX, F32 dW cast to W's dtype)."""
+    return _LinearBf16.apply(x.contiguous(), w.contiguous())
+
+
+class _RmsNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        y, rstd = HipRuntime.rms_norm(x, w, eps)
+        ctx.save_for_backward(x, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, rstd = ctx.saved_tensors
+        dx, dw = HipRuntime.rms_norm_backward(x, w, dy.contiguous().to(x.dtype), rstd)
+        return dx, dw, None
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """Reference: nn::rms_norm (src/nn.rs:165-174)."""
+    return _RmsNorm.apply(x.contiguous(), w.contiguous(), float(eps))
+
+
+class _Rotary(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, cos, sin, layout, width):
+        ctx.save_for_backward(cos, sin)
+        ctx.layout, ctx.width = layout, width
+        if width is None:
+            return HipRuntime.rotary(x, cos, sin, layout)
+        return HipRuntime.rotary_prefix(x, cos, sin, width, layout)
+
+    @staticmethod
+    def backward(ctx, dy):
+        cos, sin = ctx.saved_tensors
+        dy = dy.contiguous()
+        if ctx.width is None:
+            dx = HipRuntime.rotary_backward(dy, cos, sin, ctx.layout)
+        else:
+            dx = HipRuntime.rotary_prefix_backward(dy, cos, sin, ctx.width, ctx.layout)
+        return dx, None, None, None, None
+
+
+def rotary(x, cos, sin, layout=RotaryLayout.SplitHalf) -> torch.Tensor:
+    """Reference: nn::rotary (src/nn/rotary.rs:32-53)."""
+    return _Rotary.apply(x.contiguous(), cos.contiguous(), sin.contiguous(), RotaryLayout(layout), None)
+
+
+def rotary_prefix(x, cos, sin, width: int, layout=RotaryLayout.SplitHalf) -> torch.Tensor:
+    """Reference: nn::rotary_prefix (src/nn/rotary.rs:55-105)."""
+    return _Rotary.apply(x.contiguous(), cos.contiguous(), sin.contiguous(), RotaryLayout(layout), int(width))
+
+
+class _Attention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, scale, causal, query_start, key_start):
+        o, lse = HipRuntime.attention_forward(q, k, v, scale, causal, query_start, key_start)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.args = (scale, causal, query_start, key_start)
+        return o
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, o, lse = ctx.saved_tensors
+        scale, causal, qs, ks = ctx.args
+        dq, dk, dv = HipRuntime.attention_backward(q, k, v, o, lse, dy.contiguous().to(torch.bfloat16), scale,
+                                                   causal, qs, ks, grad_dtype=q.dtype)
+        return dq, dk, dv, None, None, None, None
+
+
+def grouped_query_attention_bf16(q, k, v, scale: float) -> torch.Tensor:
+    """Non-causal GQA, Q[B,Hq,M,D], K/V[B,Hkv,N,D]. Reference:
+    nn::grouped_query_attention_bf16_fp32 without a mask (src/nn/attention.rs:49-67)."""
+    return _Attention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale), False, 0, 0)
+
+
+def causal_grouped_query_attention_bf16(q, k, v, scale: float, query_start: int = 0, key_start: int = 0):
+    """Causal GQA with absolute query/key starts. Reference:
+    nn::causal_grouped_query_attention_bf16_fp32 (src/nn/attention.rs:68-80)."""
+    return _Attention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale), True, int(query_start),
+                            int(key_start))

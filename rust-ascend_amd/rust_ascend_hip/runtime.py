@@ -1,0 +1,267 @@
+"""HipRuntime: the MI355X counterpart of the reference's AscendRuntime static entry points
+(rust-ascend-driver/src/tensor/runtime/mod.rs:147-435), over the C ABI of libhk.so.
+
+Tensors are torch tensors on the GPU: torch provides device allocation and the current
+stream, libhk.so does every computation. Each method validates through the C ABI (which
+checks shapes before any device work), allocates outputs with torch (the reference's
+allocating forms), and raises HkError on failure. Methods keep the reference's names,
+argument meaning and return arity.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import threading
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F16, F32, HkError, check, tensor_desc
+
+
+class Transpose(enum.IntEnum):
+    """Reference: deepgemm::Transpose (rust-ascend-driver/src/tensor/deepgemm/plan.rs:7)."""
+    No = 0
+    Yes = 1
+
+
+class RotaryLayout(enum.IntEnum):
+    """Reference: RotaryLayout (rust-ascend-compiler/src/ascend/rotary_programs.rs:5-6)."""
+    Interleaved = 0
+    SplitHalf = 1
+
+
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+_TORCH = {v: k for k, v in _DTYPES.items()}
+
+_ctx = None
+_ctx_lock = threading.Lock()
+
+
+def _context():
+    """The process-wide context (initialize_exclusive, runtime/mod.rs:424-435), created on
+    first use on torch's current CUDA device."""
+    global _ctx
+    with _ctx_lock:
+        if _ctx is None:
+            lib = _lib.load()
+            if not torch.cuda.is_available():
+                raise HkError(_lib.LOAD_ERROR, "no GPU visible to torch; libhk.so has no CPU fallback")
+            h = ctypes.c_void_p()
+            check(lib.hk_init(torch.cuda.current_device(), ctypes.byref(h)))
+            _ctx = h
+        return _ctx
+
+
+def _call(name: str, *args) -> None:
+    lib = _lib.load()
+    ctx = _context()
+    check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    check(getattr(lib, name)(ctx, *args))
+
+
+def desc(t: torch.Tensor):
+    """hk_tensor descriptor of a contiguous GPU tensor."""
+    if not isinstance(t, torch.Tensor):
+        raise HkError(_lib.INVALID_ARGUMENT, f"expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype not in _DTYPES:
+        raise HkError(_lib.INVALID_ARGUMENT, f"unsupported dtype {t.dtype}")
+    if not t.is_contiguous():
+        raise HkError(_lib.INVALID_ARGUMENT, "native buffers must be contiguous")
+    if t.numel() and not t.is_cuda:
+        raise HkError(_lib.INVALID_ARGUMENT, "tensors must be on the GPU")
+    return ctypes.byref(tensor_desc(t.data_ptr() if t.numel() else 0, _DTYPES[t.dtype], t.shape))
+
+
+def _empty(shape, dtype, like: torch.Tensor) -> torch.Tensor:
+    return torch.empty(tuple(shape), dtype=dtype, device=like.device)
+
+
+def gemm_plan(a_shape, b_shape, ta, tb, out_dtype=torch.bfloat16, a_dtype=torch.bfloat16, b_dtype=torch.bfloat16):
+    """Host-only GEMM contract check (GemmSpec::new, plan.rs:49-80); needs no GPU.
+    Returns dict(kind, batch, m, n, k, out_shape, key) or raises HkError."""
+    lib = _lib.load()
+    ta_ = tensor_desc(0, _DTYPES[a_dtype], a_shape)
+    tb_ = tensor_desc(0, _DTYPES[b_dtype], b_shape)
+    # descriptors of non-empty tensors need a non-null pointer; the plan never dereferences it
+    ta_.data = 256
+    tb_.data = 256
+    plan = _lib.HkGemmPlan()
+    check(lib.hk_gemm_plan_check(ctypes.byref(ta_), ctypes.byref(tb_), int(ta), int(tb), _DTYPES[out_dtype],
+                                 ctypes.byref(plan)))
+    return {"kind": "dense" if plan.kind == 0 else "batched", "batch": plan.batch, "m": plan.m, "n": plan.n,
+            "k": plan.k, "out_shape": tuple(plan.out_shape[:plan.out_rank]), "key": plan.key.decode()}
+
+
+class HipRuntime:
+    """Static entry points mirroring AscendRuntime (runtime/mod.rs:147-435)."""
+
+    # ---------------------------------------------------------------- runtime
+
+    @staticmethod
+    def initialize_exclusive():
+        """Reference: AscendRuntime::initialize_exclusive (mod.rs:424-435)."""
+        _context()
+
+    @staticmethod
+    def set_async(enabled: bool) -> None:
+        """Benchmark mode: leave work queued instead of synchronizing after each op."""
+        lib = _lib.load()
+        check(lib.hk_set_async(_context(), 1 if enabled else 0))
+
+    @staticmethod
+    def synchronize() -> None:
+        lib = _lib.load()
+        ctx = _context()
+        check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        check(lib.hk_sync(ctx))
+
+    @staticmethod
+    def stats() -> dict:
+        lib = _lib.load()
+        s = _lib.HkStats()
+        check(lib.hk_get_stats(_context(), ctypes.byref(s)))
+        return {"modules_loaded": s.modules_loaded, "launches": s.launches, "synchronizations": s.synchronizations}
+
+    # ---------------------------------------------------------------- GEMM
+
+    @staticmethod
+    def gemm(a, b, ta=Transpose.No, tb=Transpose.No, dtype=torch.bfloat16):
+        """Reference: AscendRuntime::gemm (mod.rs:344-348)."""
+        plan = gemm_plan(a.shape, b.shape, ta, tb, dtype, a.dtype, b.dtype)
+        out = _empty(plan["out_shape"], dtype, a)
+        HipRuntime.gemm_into(a, b, ta, tb, out)
+        return out
+
+    @staticmethod
+    def gemm_into(a, b, ta, tb, out) -> None:
+        """Reference: AscendRuntime::gemm_into (mod.rs:350-354)."""
+        _call("hk_gemm_into", desc(a), desc(b), int(ta), int(tb), desc(out))
+
+    @staticmethod
+    def linear_nt_backward(x, w, dy):
+        """[BF16 dX, F32 dW] for Y = X W^T. Reference: AscendRuntime::linear_nt_backward (mod.rs:357-362)."""
+        dx = _empty(x.shape, torch.bfloat16, x)
+        dw = _empty(w.shape, torch.float32, x)
+        _call("hk_linear_nt_backward", desc(x), desc(w), desc(dy), desc(dx), desc(dw))
+        return dx, dw
+
+    @staticmethod
+    def gemm_bf16_fp32(a, b, ta=Transpose.No, tb=Transpose.No):
+        """[F32 out, saved BF16 A, saved BF16 B]. Reference: AscendRuntime::gemm_bf16_fp32 (mod.rs:388-392)."""
+        plan = gemm_plan(a.shape, b.shape, ta, tb, torch.float32)
+        out = _empty(plan["out_shape"], torch.float32, a)
+        ab = _empty(a.shape, torch.bfloat16, a)
+        bb = _empty(b.shape, torch.bfloat16, a)
+        _call("hk_gemm_bf16_fp32", desc(a), desc(b), int(ta), int(tb), desc(out), desc(ab), desc(bb))
+        return out, ab, bb
+
+    @staticmethod
+    def gemm_bf16_fp32_backward(a_bf16, b_bf16, grad, ta=Transpose.No, tb=Transpose.No):
+        """[F32 dA, F32 dB] in the physical input layouts. Reference: mod.rs:395-399."""
+        da = _empty(a_bf16.shape, torch.float32, a_bf16)
+        db = _empty(b_bf16.shape, torch.float32, a_bf16)
+        _call("hk_gemm_bf16_fp32_backward", desc(a_bf16), desc(b_bf16), desc(grad), int(ta), int(tb), desc(da),
+              desc(db))
+        return da, db
+
+    @staticmethod
+    def linear_bf16_fp32(x, w):
+        """[F32 Y, saved BF16 X, saved BF16 W]. Reference: AscendRuntime::linear_bf16_fp32 (mod.rs:364-370)."""
+        y = _empty((x.shape[0], w.shape[0]) if x.dim() == 2 and w.dim() == 2 else (0,), torch.float32, x)
+        xb = _empty(x.shape, torch.bfloat16, x)
+        wb = _empty(w.shape, torch.bfloat16, x)
+        _call("hk_linear_bf16_fp32", desc(x), desc(w), desc(y), desc(xb), desc(wb))
+        return y, xb, wb
+
+    @staticmethod
+    def linear_bf16_fp32_backward(x_bf16, w_bf16, grad):
+        """[F32 dX, F32 dW]. Reference: AscendRuntime::linear_bf16_fp32_backward (mod.rs:372-377)."""
+        dx = _empty(x_bf16.shape, torch.float32, x_bf16)
+        dw = _empty(w_bf16.shape, torch.float32, x_bf16)
+        _call("hk_linear_bf16_fp32_backward", desc(x_bf16), desc(w_bf16), desc(grad), desc(dx), desc(dw))
+        return dx, dw
+
+    @staticmethod
+    def cast(x, dtype):
+        """Reference: AscendRuntime::cast (mod.rs:271-274)."""
+        out = _empty(x.shape, dtype, x)
+        HipRuntime.cast_into(x, out)
+        return out
+
+    @staticmethod
+    def cast_into(x, out) -> None:
+        """Reference: AscendRuntime::cast_into (mod.rs:276-279)."""
+        _call("hk_cast_into", desc(x), desc(out))
+
+    # ---------------------------------------------------------------- RMSNorm
+
+    @staticmethod
+    def rms_norm(x, weight, epsilon: float):
+        """[Y, rstd]. Reference: AscendRuntime::rms_norm (mod.rs:402-408); rstd has one F32 per row."""
+        y = _empty(x.shape, x.dtype, x)
+        rows = x.numel() // x.shape[-1] if x.dim() and x.shape[-1] else 0
+        rstd = _empty((rows,), torch.float32, x)
+        _call("hk_rms_norm", desc(x), desc(weight), float(epsilon), desc(y), desc(rstd))
+        return y, rstd
+
+    @staticmethod
+    def rms_norm_backward(x, weight, grad, rstd):
+        """[dX, F32 dW]. Reference: AscendRuntime::rms_norm_backward (mod.rs:410-415)."""
+        dx = _empty(x.shape, x.dtype, x)
+        dw = _empty((x.shape[-1],), torch.float32, x)
+        _call("hk_rms_norm_backward", desc(x), desc(weight), desc(grad), desc(rstd), desc(dx), desc(dw))
+        return dx, dw
+
+    # ---------------------------------------------------------------- RoPE
+
+    @staticmethod
+    def rotary(x, cos, sin, layout=RotaryLayout.SplitHalf):
+        """Reference: AscendRuntime::rotary (mod.rs:257-261)."""
+        y = _empty(x.shape, x.dtype, x)
+        _call("hk_rotary", desc(x), desc(cos), desc(sin), int(layout), desc(y))
+        return y
+
+    @staticmethod
+    def rotary_backward(grad, cos, sin, layout=RotaryLayout.SplitHalf):
+        """Reference: AscendRuntime::rotary_backward (mod.rs:264-268)."""
+        dx = _empty(grad.shape, grad.dtype, grad)
+        _call("hk_rotary_backward", desc(grad), desc(cos), desc(sin), int(layout), desc(dx))
+        return dx
+
+    @staticmethod
+    def rotary_prefix(x, cos, sin, width: int, layout=RotaryLayout.SplitHalf):
+        """Reference: AscendRuntime::rotary_prefix (mod.rs:214-217)."""
+        y = _empty(x.shape, x.dtype, x)
+        _call("hk_rotary_prefix", desc(x), desc(cos), desc(sin), int(width), int(layout), desc(y))
+        return y
+
+    @staticmethod
+    def rotary_prefix_backward(grad, cos, sin, width: int, layout=RotaryLayout.SplitHalf):
+        """Reference: AscendRuntime::rotary_prefix_backward (mod.rs:218-221)."""
+        dx = _empty(grad.shape, grad.dtype, grad)
+        _call("hk_rotary_prefix_backward", desc(grad), desc(cos), desc(sin), int(width), int(layout), desc(dx))
+        return dx
+
+    # ---------------------------------------------------------------- attention
+
+    @staticmethod
+    def attention_forward(q, k, v, scale: float, causal: bool = True, query_start: int = 0, key_start: int = 0):
+        """Fused GQA attention forward: [O (BF16), lse (F32 [B,Hq,M])]. Replaces the composed
+        chain of src/nn/attention.rs:10-80."""
+        o = _empty(q.shape, torch.bfloat16, q)
+        lse = _empty(q.shape[:3], torch.float32, q)
+        _call("hk_attention_forward", desc(q), desc(k), desc(v), float(scale), int(bool(causal)), int(query_start),
+              int(key_start), desc(o), desc(lse))
+        return o, lse
+
+    @staticmethod
+    def attention_backward(q, k, v, o, lse, grad, scale: float, causal: bool = True, query_start: int = 0,
+                           key_start: int = 0, grad_dtype=torch.float32):
+        """[dQ, dK, dV] of the fused GQA attention (dK/dV summed over each KV group)."""
+        dq = _empty(q.shape, grad_dtype, q)
+        dk = _empty(k.shape, grad_dtype, q)
+        dv = _empty(v.shape, grad_dtype, q)
+        _call("hk_attention_backward", desc(q), desc(k), desc(v), desc(o), desc(lse), desc(grad), float(scale),
+              int(bool(causal)), int(query_start), int(key_start), desc(dq), desc(dk), desc(dv))
+        return dq, dk, dv

@@ -1,0 +1,47 @@
+"""Helpers shared by the GPU parity tests (imported by tests only)."""
+import numpy as np
+import torch
+
+import oracle
+
+DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
+
+
+def dev_f32(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV)
+
+
+def dev_bf16(a) -> torch.Tensor:
+    """BF16 device tensor holding the RNE rounding of `a` (exactly the oracle's bf16_round)."""
+    bits = oracle.bf16_bits(np.ascontiguousarray(a, dtype=np.float32))
+    return torch.from_numpy(bits.view(np.int16)).to(DEV).view(torch.bfloat16)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    """float32 numpy copy of a device tensor (BF16 widened exactly)."""
+    return t.detach().float().cpu().numpy()
+
+
+def randn_bf16(shape, seed: int, std: float = 1.0):
+    """Seeded BF16 N(0, std^2) tensor generated on the GPU, plus its exact float32 host copy."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    t = (torch.randn(shape, generator=g, device=DEV, dtype=torch.float32) * std).to(torch.bfloat16)
+    return t, host(t)
+
+
+def close(actual, expected, atol, rtol, name=""):
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    assert a.shape == b.shape, (name, a.shape, b.shape)
+    ok = np.abs(a - b) <= atol + rtol * np.abs(b)
+    ok &= np.isfinite(a) | ~np.isfinite(b)
+    if not ok.all():
+        i = np.argwhere(~ok)[0]
+        raise AssertionError(f"{name}: {int((~ok).sum())} mismatches; first at {tuple(i)}: {a[tuple(i)]} vs {b[tuple(i)]}")
+
+
+def rel_ok(actual, expected, tol, name=""):
+    e = oracle.rel_err(actual, expected)
+    assert e <= tol, f"{name}: max rel err {e:.3e} > {tol}"
+    return e

@@ -1,0 +1,154 @@
+"""CPU tests of the C ABI: the library loads, exports every symbol include/hk.h declares, and
+rejects invalid calls before any device work (the reference's host contract tests:
+deepgemm/plan.rs:89-109, runtime/normalization.rs:188-221, rotary_programs.rs:277-297,
+src/nn/attention.rs:105-133). No compute call is made here."""
+import ctypes
+import re
+
+import pytest
+
+import rust_ascend_hip as rh
+from rust_ascend_hip import _lib
+from rust_ascend_hip._lib import BF16, F16, F32, HkError, tensor_desc
+
+
+def declared_functions():
+    text = open(_lib.HEADER_PATH).read()
+    return sorted(set(re.findall(r"^\s*(?:hk_status|const char\*|int32_t|void\*)\s+(hk_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 29
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+    assert lib.hk_abi_version() == 1
+
+
+def fake(dtype, shape, ptr=1 << 20):
+    return ctypes.byref(tensor_desc(ptr, dtype, shape))
+
+
+def test_ops_without_context_report_not_initialized():
+    lib = _lib.load()
+    a, b = fake(BF16, (32, 48)), fake(BF16, (48, 64), ptr=1 << 30)
+    out = fake(BF16, (32, 64), ptr=1 << 31)
+    assert lib.hk_gemm_into(None, a, b, 0, 0, out) == _lib.NOT_INITIALIZED
+    assert "not initialized" in _lib.last_error()
+    assert lib.hk_sync(None) == _lib.NOT_INITIALIZED
+
+
+def test_init_without_gpu_is_a_load_error():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    assert lib.hk_init(0, ctypes.byref(h)) == _lib.LOAD_ERROR
+
+
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_four_transposes_share_the_logical_shape(ta, tb):
+    # plan.rs:93-99
+    a = (48, 32) if ta else (32, 48)
+    b = (64, 48) if tb else (48, 64)
+    p = rh.gemm_plan(a, b, ta, tb, out_dtype=__import__("torch").float32)
+    assert (p["m"], p["n"], p["k"]) == (32, 64, 48)
+    assert p["out_shape"] == (32, 64)
+    assert p["key"] == f"bf16_dense_{'nt'[ta]}{'nt'[tb]}_f32"
+
+
+def test_gemm_contract_rejections():
+    import torch
+    with pytest.raises(HkError):  # batch broadcast, plan.rs:100
+        rh.gemm_plan((2, 16, 16), (1, 16, 16), 0, 0)
+    for dims in [(0, 16), (17, 16), (16,), (1, 1, 16, 16)]:  # plan.rs:101-104
+        with pytest.raises(HkError):
+            rh.gemm_plan(dims, (16, 16), 0, 0)
+    with pytest.raises(HkError):
+        rh.gemm_plan((16, 16), (16, 16), 0, 0, a_dtype=torch.float16)
+    with pytest.raises(HkError):  # contraction mismatch
+        rh.gemm_plan((32, 48), (32, 64), 0, 0)
+    with pytest.raises(HkError):  # batches 1..=4096
+        rh.gemm_plan((4097, 16, 16), (4097, 16, 16), 0, 0)
+    p = rh.gemm_plan((3, 16, 32), (3, 32, 48), 0, 0)
+    assert p["kind"] == "batched" and p["out_shape"] == (3, 16, 48) and p["key"] == "bf16_batched_nn_bf16"
+    # training dimension mapping (plan.rs:107): dY[32,64] . W[64,48] -> X shape, dY^T X -> W shape
+    assert rh.gemm_plan((32, 64), (64, 48), 0, 0)["out_shape"] == (32, 48)
+    assert rh.gemm_plan((32, 64), (32, 48), 1, 0)["out_shape"] == (64, 48)
+
+
+def test_overlap_and_shape_checks_run_before_the_context():
+    lib = _lib.load()
+    a = fake(BF16, (32, 48), ptr=1 << 20)
+    b = fake(BF16, (48, 64), ptr=1 << 24)
+    # output overlapping A
+    assert lib.hk_gemm_into(None, a, b, 0, 0, fake(BF16, (32, 64), ptr=(1 << 20) + 64)) == _lib.INVALID_ARGUMENT
+    assert "overlap" in _lib.last_error()
+    # wrong output layout
+    assert lib.hk_gemm_into(None, a, b, 0, 0, fake(BF16, (64, 32), ptr=1 << 28)) == _lib.INVALID_ARGUMENT
+    assert lib.hk_gemm_into(None, a, b, 0, 0, fake(F16, (32, 64), ptr=1 << 28)) == _lib.INVALID_ARGUMENT
+
+
+def test_rms_norm_contract():
+    lib = _lib.load()
+    x = fake(F32, (3, 96), 1 << 20)
+    w = fake(F32, (96,), 1 << 24)
+    y = fake(F32, (3, 96), 1 << 26)
+    r = fake(F32, (3,), 1 << 28)
+    # normalization.rs:200, 217: epsilon must be positive and representable in FP32
+    for eps in (0.0, -1.0, float("nan"), float("inf"), 1e300, 1e-100):
+        assert lib.hk_rms_norm(None, x, w, eps, y, r) == _lib.INVALID_ARGUMENT, eps
+    assert lib.hk_rms_norm(None, x, w, 1e-5, y, r) == _lib.NOT_INITIALIZED
+    assert lib.hk_rms_norm(None, x, fake(F32, (95,), 1 << 24), 1e-5, y, r) == _lib.INVALID_ARGUMENT
+    assert lib.hk_rms_norm(None, x, w, 1e-5, fake(BF16, (3, 96), 1 << 26), r) == _lib.INVALID_ARGUMENT
+    assert lib.hk_rms_norm(None, x, w, 1e-5, y, fake(F32, (4,), 1 << 28)) == _lib.INVALID_ARGUMENT
+    assert lib.hk_rms_norm(None, fake(F32, (3, 0), 1 << 20), w, 1e-5, y, r) == _lib.INVALID_ARGUMENT
+    assert lib.hk_rms_norm(None, fake(F16, (3, 96), 1 << 20), w, 1e-5, y, r) == _lib.INVALID_ARGUMENT
+    # empty batch is valid (normalization.rs:194)
+    assert lib.hk_rms_norm(None, fake(F32, (0, 64), 0), fake(F32, (64,), 1 << 24), 1e-5,
+                           fake(F32, (0, 64), 0), fake(F32, (0,), 0)) == _lib.NOT_INITIALIZED
+
+
+def test_rotary_prefix_contract():
+    # rotary_programs.rs:277-283: invalid broadcast and widths are rejected
+    lib = _lib.load()
+    x = fake(F32, (2, 3, 5, 11), 1 << 20)
+    y = fake(F32, (2, 3, 5, 11), 1 << 26)
+
+    def call(table, p):
+        return lib.hk_rotary_prefix(None, x, fake(F32, table, 1 << 24), fake(F32, table, 1 << 25), p, 0, y)
+
+    assert call((1, 1, 5, 3), 6) == _lib.NOT_INITIALIZED
+    for table, p in [((5, 3), 6), ((1, 2, 5, 3), 6), ((1, 1, 5, 6), 6), ((1, 1, 5, 3), 0), ((1, 1, 5, 3), 5),
+                     ((1, 1, 5, 6), 12)]:
+        assert call(table, p) == _lib.INVALID_ARGUMENT, (table, p)
+    # full rotation requires same-row tables and an even width
+    assert lib.hk_rotary(None, fake(F32, (3, 6), 1 << 20), fake(F32, (3, 3), 1 << 24), fake(F32, (3, 3), 1 << 25),
+                         1, fake(F32, (3, 6), 1 << 26)) == _lib.NOT_INITIALIZED
+    assert lib.hk_rotary(None, fake(F32, (3, 7), 1 << 20), fake(F32, (3, 3), 1 << 24), fake(F32, (3, 3), 1 << 25),
+                         1, fake(F32, (3, 7), 1 << 26)) == _lib.INVALID_ARGUMENT
+    assert lib.hk_rotary(None, fake(F32, (3, 6), 1 << 20), fake(F32, (1, 3), 1 << 24), fake(F32, (1, 3), 1 << 25),
+                         1, fake(F32, (3, 6), 1 << 26)) == _lib.INVALID_ARGUMENT
+
+
+def test_attention_contract():
+    # src/nn/attention.rs:120-132: head ratios, batches and lengths
+    lib = _lib.load()
+
+    def call(q, k, v, d_out=None, causal=1, scale=0.25):
+        o = fake(BF16, q, 1 << 34)
+        lse = fake(F32, q[:3], 1 << 35)
+        return lib.hk_attention_forward(None, fake(BF16, q, 1 << 20), fake(BF16, k, 1 << 26), fake(BF16, v, 1 << 30),
+                                        scale, causal, 0, 0, o, lse)
+
+    for heads, kv in [(1, 1), (6, 6), (6, 3), (6, 1), (15, 3)]:
+        assert call((2, heads, 32, 64), (2, kv, 96, 64), (2, kv, 96, 64)) == _lib.NOT_INITIALIZED
+    for q, k, v in [((2, 5, 32, 64), (2, 3, 96, 64), (2, 3, 96, 64)), ((2, 6, 32, 64), (2, 3, 96, 64), (2, 2, 96, 64)),
+                    ((2, 6, 32, 64), (2, 3, 96, 64), (1, 3, 96, 64)), ((2, 6, 32, 64), (2, 3, 96, 64), (2, 3, 32, 64)),
+                    ((4096, 2, 32, 64), (4096, 1, 96, 64), (4096, 1, 96, 64)), ((2, 6, 32, 48), (2, 3, 96, 48), (2, 3, 96, 48))]:
+        assert call(q, k, v) == _lib.INVALID_ARGUMENT, (q, k, v)
+    assert call((2, 2, 32, 64), (2, 1, 96, 64), (2, 1, 96, 64), scale=float("nan")) == _lib.INVALID_ARGUMENT

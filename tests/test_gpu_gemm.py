@@ -1,0 +1,153 @@
+"""GPU parity: BF16 GEMM (all transposes, dense and batched, BF16/F32 out), the Linear backward
+and the FP32-storage wrappers, through the C ABI, against the golden vectors and the oracle.
+
+Tolerances: the reference acceptance check (deepgemm_validate.rs:16: 0.05 + 0.01|b|), bit
+exactness where the reference's integer-formula inputs make every partial sum exact in F32
+(rust-ascend-kernels/src/tests.rs:89-103), and max rel err <= 1e-2 vs the f64 oracle otherwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import DEV, close, dev_bf16, dev_f32, host, randn_bf16, rel_ok
+from rust_ascend_hip import HipRuntime, HkError, Transpose
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
+def test_gemm_deepgemm_validate_cases(golden, batch, ta, tb, out):
+    key = f"gemm_dv_b{batch}_{'tn'[ta]}{'tn'[tb]}"
+    a, b, want = golden[key + "_a"], golden[key + "_b"], golden[key + "_out"]
+    at, bt = dev_bf16(a), dev_bf16(b)
+    y = HipRuntime.gemm(at, bt, Transpose(ta), Transpose(tb), out)
+    close(host(y), want, 0.05, 0.01, "GEMM")
+    # gemm_into reuses the output storage (deepgemm_validate.rs:40-42)
+    y.zero_()
+    HipRuntime.gemm_into(at, bt, Transpose(ta), Transpose(tb), y)
+    close(host(y), want, 0.05, 0.01, "GEMM output reuse")
+
+
+@pytest.mark.parametrize("shape", ["1x80x96x144", "3x16x32x16"])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_exact_integer_cases(golden, shape, ta, tb):
+    key = f"gemm_vm_{shape}_{'nt'[ta]}{'nt'[tb]}"
+    a, b, want = golden[key + "_a"], golden[key + "_b"], golden[key + "_out"]
+    at, bt = dev_bf16(a), dev_bf16(b)
+    y32 = host(HipRuntime.gemm(at, bt, Transpose(ta), Transpose(tb), torch.float32))
+    np.testing.assert_array_equal(y32, want.astype(np.float32))  # every partial sum is exact in F32
+    y16 = host(HipRuntime.gemm(at, bt, Transpose(ta), Transpose(tb), torch.bfloat16))
+    np.testing.assert_array_equal(y16, oracle.bf16_round(want.astype(np.float32)))
+
+
+def test_linear_nt_backward_golden(golden):
+    x, w, dy = golden["linbwd_x"], golden["linbwd_w"], golden["linbwd_dy"]
+    dx, dw = HipRuntime.linear_nt_backward(dev_bf16(x), dev_bf16(w), dev_bf16(dy))
+    assert dx.dtype == torch.bfloat16 and dw.dtype == torch.float32
+    assert dx.shape == (32, 16) and dw.shape == (48, 16)
+    # matrix_runtime.rs:21-22 tolerances (5e-4 + 4e-3|b| BF16, 5e-4|b| F32)
+    close(host(dx), golden["linbwd_dx"], 5e-4, 4e-3, "dX")
+    close(host(dw), golden["linbwd_dw"], 5e-4, 5e-4, "dW")
+
+
+SHAPES = [(16, 16, 16), (48, 80, 144), (272, 528, 1040), (1024, 1024, 1024), (512, 1024, 1024), (2048, 4096, 512),
+          (4096, 4096, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0), (1, 1)])
+def test_gemm_random_vs_oracle(m, n, k, ta, tb):
+    if (m * n * k > 1 << 31) and (ta, tb) != (0, 1):
+        pytest.skip("large shapes run NT only (the others share the kernel after the transpose)")
+    a_t, a = randn_bf16((k, m) if ta else (m, k), seed=m + n + k, std=1 / np.sqrt(k))
+    b_t, b = randn_bf16((n, k) if tb else (k, n), seed=m * 3 + k, std=1.0)
+    for out in (torch.bfloat16, torch.float32):
+        y = host(HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), out))
+        if m * n * k <= 1 << 28:
+            want = oracle.gemm_f64(a, b, ta, tb)
+        else:
+            rows = np.arange(0, m, 7)[:512]
+            cols = np.arange(0, n, 5)[:512]
+            r, c = np.meshgrid(rows, cols, indexing="ij")
+            want = oracle.gemm_f64_sampled(a, b, ta, tb, r.ravel(), c.ravel())
+            y = y[r.ravel(), c.ravel()]
+        rel_ok(y, want, 1e-2 if out == torch.bfloat16 else 1e-4, f"GEMM {m}x{n}x{k} {ta}{tb} {out}")
+
+
+def test_gemm_batched_vs_oracle():
+    for ta, tb in [(0, 0), (0, 1), (1, 0), (1, 1)]:
+        a_t, a = randn_bf16((5, 96, 64) if ta else (5, 64, 96), seed=1)
+        b_t, b = randn_bf16((5, 112, 96) if tb else (5, 96, 112), seed=2)
+        y = host(HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), torch.float32))
+        rel_ok(y, oracle.gemm_f64(a, b, ta, tb), 1e-4, f"batched {ta}{tb}")
+
+
+@pytest.mark.parametrize("m,n,k", [(8192, 8192, 8192), (8192, 14336, 4096), (8192, 4096, 14336)])
+def test_gemm_c3_full_size_sampled(m, n, k):
+    """A, B ~N(0,1)/sqrt(K) BF16, NT (Linear weights [N,K]), BF16 out; sampled
+    parity on 4096 random (i, j) plus a full row and a full column."""
+    a_t, a = randn_bf16((m, k), seed=1, std=1 / np.sqrt(k))
+    b_t, b = randn_bf16((n, k), seed=2, std=1 / np.sqrt(k))
+    y_t = HipRuntime.gemm(a_t, b_t, Transpose.No, Transpose.Yes, torch.bfloat16)
+    rng = np.random.default_rng(0)
+    rows = np.concatenate([rng.integers(0, m, 4096), np.full(n, m // 3), np.arange(m)])
+    cols = np.concatenate([rng.integers(0, n, 4096), np.arange(n), np.full(m, n - 1)])
+    y = host(y_t[torch.from_numpy(rows).to(DEV), torch.from_numpy(cols).to(DEV)])
+    want = oracle.gemm_f64_sampled(a, b, 0, 1, rows, cols)
+    rel_ok(y, want, 1e-2, f"C3 {m}x{n}x{k}")
+
+
+def test_c1_linear_forward():
+    """X[512,1024] ~N(0,1), W[1024,1024] ~N(0,0.02), bias zeros, BF16 out."""
+    x = oracle.normal((512, 1024), 0, 1)
+    w = oracle.normal((1024, 1024), 0, 2, std=0.02)
+    y = host(HipRuntime.gemm(dev_bf16(x), dev_bf16(w), Transpose.No, Transpose.Yes, torch.bfloat16))
+    rel_ok(y, oracle.gemm_f64(oracle.bf16_round(x), oracle.bf16_round(w), 0, 1), 1e-2, "C1")
+
+
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_bf16_fp32_forward_backward(ta, tb):
+    m, n, k = 64, 48, 80
+    a = oracle.normal((k, m) if ta else (m, k), 5, 1)
+    b = oracle.normal((n, k) if tb else (k, n), 5, 2)
+    out, ab, bb = HipRuntime.gemm_bf16_fp32(dev_f32(a), dev_f32(b), Transpose(ta), Transpose(tb))
+    np.testing.assert_array_equal(host(ab), oracle.bf16_round(a))
+    np.testing.assert_array_equal(host(bb), oracle.bf16_round(b))
+    ar, br = oracle.bf16_round(a), oracle.bf16_round(b)
+    rel_ok(host(out), oracle.gemm_f64(ar, br, ta, tb), 1e-4, "fwd")
+    dy = oracle.normal((m, n), 5, 3)
+    da, db = HipRuntime.gemm_bf16_fp32_backward(ab, bb, dev_f32(dy), Transpose(ta), Transpose(tb))
+    assert da.shape == ab.shape and db.shape == bb.shape
+    dyr = oracle.bf16_round(dy)
+    op_a = ar.T if ta else ar
+    op_b = br.T if tb else br
+    want_da = dyr.astype(np.float64) @ op_b.T.astype(np.float64)  # d op(A)
+    want_db = op_a.T.astype(np.float64) @ dyr.astype(np.float64)  # d op(B)
+    rel_ok(host(da), want_da.T if ta else want_da, 1e-4, "dA")
+    rel_ok(host(db), want_db.T if tb else want_db, 1e-4, "dB")
+
+
+def test_linear_bf16_fp32_matches_gemm():
+    x = oracle.normal((32, 64), 6, 1)
+    w = oracle.normal((48, 64), 6, 2)
+    y, xb, wb = HipRuntime.linear_bf16_fp32(dev_f32(x), dev_f32(w))
+    rel_ok(host(y), oracle.gemm_f64(oracle.bf16_round(x), oracle.bf16_round(w), 0, 1), 1e-4, "linear")
+    dy = oracle.normal((32, 48), 6, 3)
+    dx, dw = HipRuntime.linear_bf16_fp32_backward(xb, wb, dev_f32(dy))
+    dyr = oracle.bf16_round(dy).astype(np.float64)
+    rel_ok(host(dx), dyr @ oracle.bf16_round(w), 1e-4, "dX")
+    rel_ok(host(dw), dyr.T @ oracle.bf16_round(x), 1e-4, "dW")
+
+
+def test_gemm_rejects_overlap_and_stays_healthy():
+    a_t, a = randn_bf16((64, 64), seed=3)
+    with pytest.raises(HkError):
+        HipRuntime.gemm_into(a_t, a_t, Transpose.No, Transpose.No, a_t)  # in-place output overlaps inputs
+    y = host(HipRuntime.gemm(a_t, a_t, Transpose.No, Transpose.No, torch.float32))
+    rel_ok(y, oracle.gemm_f64(a, a, 0, 0), 1e-4, "after rejection")

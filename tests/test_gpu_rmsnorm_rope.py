@@ -1,0 +1,169 @@
+"""GPU parity: RMSNorm forward/backward, RoPE (full and prefix) and F32<->BF16 casts through
+the C ABI, against the CPU oracle and the golden vectors.
+
+Tolerances: the reference's own (rms_norm_runtime.rs:20: 5e-4 + 5e-4|b| for F32 I/O;
+rotary_tensor.rs:8: 2e-5 + 1e-4|b|), and for BF16 I/O max rel err <= 1e-2 on BF16 outputs and
+<= 1e-4 on the F32 weight gradient, rel err = max |a-b| / (|b| + 1e-3 rms(b)).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import DEV, close, dev_bf16, dev_f32, host, randn_bf16, rel_ok
+from rust_ascend_hip import HipRuntime, HkError, RotaryLayout
+
+pytestmark = pytest.mark.gpu
+
+RMS_CASES = ["0x32", "1x32", "3x96", "7x256", "33x4096", "3x7", "2x4100"]
+
+
+@pytest.mark.parametrize("case", RMS_CASES)
+def test_rms_norm_f32_golden(golden, case):
+    g = {k[len("rms_" + case) + 1:]: v for k, v in golden.items() if k.startswith("rms_" + case + "_")}
+    x = dev_f32(g["x"])
+    w = dev_f32(g["w"])
+    y, rstd = HipRuntime.rms_norm(x, w, 1e-3)
+    dx, dw = HipRuntime.rms_norm_backward(x, w, dev_f32(g["dy"]), rstd)
+    assert y.shape == x.shape and rstd.shape == (x.shape[0],) and dw.shape == (x.shape[1],)
+    close(host(y), g["y"], 5e-4, 5e-4, "Y")
+    close(host(rstd), g["rstd"], 5e-4, 5e-4, "rstd")
+    close(host(dx), g["dx"], 5e-4, 5e-4, "dX")
+    close(host(dw), g["dw"], 5e-4, 5e-4, "dW")
+
+
+@pytest.mark.parametrize("rows,width", [(1, 4096), (37, 4096), (300, 1024), (5, 8), (9, 520), (4, 4100), (3, 8224),
+                                        (2, 1), (1000, 64)])
+def test_rms_norm_bf16_vs_oracle(rows, width):
+    x_t, x = randn_bf16((rows, width), seed=rows * 7 + width)
+    dy_t, dy = randn_bf16((rows, width), seed=rows * 7 + width + 1)
+    w = (1 + oracle.normal((width,), 0, 9, std=0.1)).astype(np.float32)
+    y, rstd = HipRuntime.rms_norm(x_t, dev_f32(w), 1e-6)
+    dx, dw = HipRuntime.rms_norm_backward(x_t, dev_f32(w), dy_t, rstd)
+    y_ref, r_ref = oracle.rms_norm_f64(x, w, 1e-6)
+    dx_ref, dw_ref = oracle.rms_norm_backward_f64(x, w, dy, r_ref)
+    rel_ok(host(y), y_ref, 1e-2, "Y")
+    rel_ok(host(rstd), r_ref, 1e-5, "rstd")
+    rel_ok(host(dx), dx_ref, 1e-2, "dX")
+    rel_ok(host(dw), dw_ref, 1e-4, "dW")
+
+
+def test_rms_norm_c2_full_size_and_determinism():
+    """x[16384,4096] bf16 ~N(0,1), w F32 ~1+N(0,0.1), eps 1e-6, dy bf16 ~N(0,1)."""
+    x_t, x = randn_bf16((16384, 4096), seed=0)
+    dy_t, dy = randn_bf16((16384, 4096), seed=1)
+    w = (1 + oracle.normal((4096,), 0, 2, std=0.1)).astype(np.float32)
+    w_t = dev_f32(w)
+    y, rstd = HipRuntime.rms_norm(x_t, w_t, 1e-6)
+    dx, dw = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd)
+    dx2, dw2 = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd)
+    assert torch.equal(dw, dw2) and torch.equal(dx, dx2), "backward must be deterministic"
+    y_ref, r_ref = oracle.rms_norm_f64(x, w, 1e-6)
+    dx_ref, dw_ref = oracle.rms_norm_backward_f64(x, w, dy, r_ref)
+    rel_ok(host(y), y_ref, 1e-2, "Y")
+    rel_ok(host(dx), dx_ref, 1e-2, "dX")
+    rel_ok(host(dw), dw_ref, 1e-4, "dW")
+
+
+def test_rms_norm_empty_batch_and_known_answer(golden):
+    w = dev_f32(np.ones(32, np.float32))
+    x = torch.empty((0, 32), device=DEV)
+    y, rstd = HipRuntime.rms_norm(x, w, 1e-5)
+    dx, dw = HipRuntime.rms_norm_backward(x, w, x.clone(), rstd)
+    assert y.shape == (0, 32) and torch.count_nonzero(dw) == 0
+    # row_tests.rs:280-287: x = 2, dy = 3, rstd = [.5,.25,2] -> per-row contributions 3, 1.5, 12
+    for r, want in zip(golden["rmskat_rstd"], golden["rmskat_contrib"]):
+        xt = torch.full((1, 32), 2.0, device=DEV)
+        _, dw = HipRuntime.rms_norm_backward(xt, w, torch.full((1, 32), 3.0, device=DEV),
+                                             torch.tensor([r], device=DEV, dtype=torch.float32))
+        assert torch.all(dw == float(want))
+
+
+def test_rms_norm_misaligned_view_uses_general_path():
+    base_t, base = randn_bf16((1, 4096 + 4), seed=5)
+    x_t = base_t[0, 4:].reshape(16, 256)  # 8-byte offset: not 16-byte aligned
+    assert x_t.data_ptr() % 16 != 0
+    w = np.ones(256, np.float32)
+    y, rstd = HipRuntime.rms_norm(x_t, dev_f32(w), 1e-6)
+    y_ref, _ = oracle.rms_norm_f64(base[0, 4:].reshape(16, 256), w, 1e-6)
+    rel_ok(host(y), y_ref, 1e-2, "Y")
+
+
+@pytest.mark.parametrize("case", ["0x6", "1x2", "3x6", "2x96"])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_rotary_f32_golden(golden, case, layout):
+    key = f"rope_{case}_l{layout}"
+    x, dy, c, s = (golden[key + s_] for s_ in ("_x", "_dy", "_cos", "_sin"))
+    y = HipRuntime.rotary(dev_f32(x), dev_f32(c), dev_f32(s), RotaryLayout(layout))
+    dx = HipRuntime.rotary_backward(dev_f32(dy), dev_f32(c), dev_f32(s), RotaryLayout(layout))
+    close(host(y), golden[key + "_y"], 2e-5, 1e-4, "rotary Y")
+    close(host(dx), golden[key + "_dx"], 2e-5, 1e-4, "rotary dX")
+
+
+@pytest.mark.parametrize("ci", range(5))
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("backward", [0, 1])
+def test_rotary_prefix_golden_tail_bits(golden, ci, layout, backward):
+    key = f"ropepre_{ci}_l{layout}_b{backward}"
+    x, c, s, want = golden[key + "_x"], golden[key + "_cos"], golden[key + "_sin"], golden[key + "_y"]
+    fn = HipRuntime.rotary_prefix_backward if backward else HipRuntime.rotary_prefix
+    y = host(fn(dev_f32(x), dev_f32(c), dev_f32(s), 6, RotaryLayout(layout)))
+    head = (slice(None),) * (x.ndim - 1) + (slice(0, 6),)
+    tail = (slice(None),) * (x.ndim - 1) + (slice(6, None),)
+    close(y[head], want[head], 3e-6, 3e-6, "prefix head")
+    np.testing.assert_array_equal(y[tail].view(np.uint32), x[tail].view(np.uint32))
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_rotary_c4_shape_bf16(layout):
+    """C4's RoPE: Q [4,32,4096,128] and K [4,8,4096,128] BF16 with [1,1,4096,64] tables, theta 5e5."""
+    cos, sin = oracle.rope_tables(np.arange(4096), 128, 5e5)
+    c_t, s_t = dev_f32(cos[None, None]), dev_f32(sin[None, None])
+    for shape, seed in (((4, 32, 4096, 128), 11), ((4, 8, 4096, 128), 12)):
+        x_t, x = randn_bf16(shape, seed)
+        y = HipRuntime.rotary_prefix(x_t, c_t, s_t, 128, RotaryLayout(layout))
+        want = oracle.rotary_prefix(x, cos[None, None], sin[None, None], 128, layout)
+        rel_ok(host(y), want, 1e-2, f"rope {shape}")
+        # transpose Jacobian undoes the rotation
+        back = HipRuntime.rotary_prefix_backward(y.float().contiguous(), c_t, s_t, 128, RotaryLayout(layout))
+        rel_ok(host(back), x, 1e-2, "rope round trip")
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("width", [2, 6, 64, 96, 128])
+def test_rotary_random_widths_vs_oracle(layout, width):
+    rows = 37
+    x = oracle.normal((rows, width), 3, width)
+    ang = oracle.normal((rows, width // 2), 4, width)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    for bw in (False, True):
+        fn = HipRuntime.rotary_backward if bw else HipRuntime.rotary
+        y = host(fn(dev_f32(x), dev_f32(c), dev_f32(s), RotaryLayout(layout)))
+        close(y, oracle.rotary(x, c, s, layout, bw), 1e-6, 1e-6, "rotary f32")
+        yb = host(fn(dev_bf16(x), dev_f32(c), dev_f32(s), RotaryLayout(layout)))
+        rel_ok(yb, oracle.rotary(oracle.bf16_round(x), c, s, layout, bw), 1e-2, "rotary bf16")
+
+
+def test_cast_round_trip_bits():
+    specials = np.array([0x80000000, 0x7FC01234, 0x7F800000, 0xFF800000, 0x00000001, 0x3F808000, 0x3F818000,
+                         0x7F7FFFFF], dtype=np.uint32).view(np.float32)
+    x = np.concatenate([specials, oracle.normal((100003,), 1, 1, std=50.0)]).astype(np.float32)
+    b = HipRuntime.cast(dev_f32(x), torch.bfloat16)
+    got = b.cpu().view(torch.int16).numpy().view(np.uint16)
+    want = oracle.bf16_bits(x)
+    finite = np.isfinite(x)
+    np.testing.assert_array_equal(got[finite], want[finite])
+    assert np.all(np.isnan(host(b)[np.isnan(x)]))
+    assert np.array_equal(np.isinf(host(b)), np.isinf(oracle.bf16_round(x)))
+    back = HipRuntime.cast(b, torch.float32)
+    np.testing.assert_array_equal(host(back)[finite], oracle.bf16_round(x)[finite])
+
+
+def test_invalid_call_raises_and_does_not_poison():
+    x = dev_f32(np.ones((4, 32), np.float32))
+    with pytest.raises(HkError):
+        HipRuntime.rms_norm(x, dev_f32(np.ones(31, np.float32)), 1e-5)
+    y, _ = HipRuntime.rms_norm(x, dev_f32(np.ones(32, np.float32)), 1e-5)
+    assert torch.allclose(y, torch.ones_like(y), atol=1e-4)
+    s = HipRuntime.stats()
+    assert s["launches"] > 0 and s["synchronizations"] > 0 and s["modules_loaded"] == 1

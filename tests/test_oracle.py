@@ -1,0 +1,289 @@
+"""Pins the CPU oracle (oracle/) against the golden vectors, closed forms and
+float64 autograd. CPU only. See oracle/oracle.py's header for what pins what."""
+import numpy as np
+import pytest
+import torch
+
+
+def close(actual, expected, atol, rtol):
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    bad = ~(np.abs(a - b) <= atol + rtol * np.abs(b))
+    assert not bad.any(), f"{bad.sum()} mismatches, first at {np.argwhere(bad)[0]}: {a[bad][0]} vs {b[bad][0]}"
+
+
+# ------------------------------------------------------------------ BF16
+
+def test_bf16_rounding_bit_patterns(oracle):
+    cases = {
+        1.0: 0x3F80, 1.00390625: 0x3F80,          # tie -> even (down)
+        1.01171875: 0x3F82,                        # tie -> even (up)
+        -0.0: 0x8000, 3.0e38: 0x7F62, 3.4e38: 0x7F80,  # finite; overflow to +Inf
+        float("inf"): 0x7F80, float("-inf"): 0xFF80,
+    }
+    for x, bits in cases.items():
+        assert int(oracle.bf16_bits(np.array([x], np.float32))[0]) == bits, x
+    nan = np.array([0x7FC01234], dtype=np.uint32).view(np.float32)
+    assert int(oracle.bf16_bits(nan)[0]) == 0x7FC0  # NaN keeps top bits, stays NaN
+
+
+def test_bf16_rounding_matches_torch(oracle):
+    x = oracle.normal((1 << 16,), seed=3, stream=1, std=100.0)
+    x[:64] = np.ldexp(np.float32(1.0) + np.arange(64, dtype=np.float32) / 256, -130)  # subnormals
+    want = torch.tensor(x).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(oracle.bf16_round(x), want)
+
+
+def test_normal_generator_is_deterministic_and_standard(oracle):
+    a = oracle.normal((4096, 64), seed=0, stream=5)
+    b = oracle.normal((4096, 64), seed=0, stream=5)
+    c = oracle.normal((4096, 64), seed=0, stream=6)
+    np.testing.assert_array_equal(a, b)
+    assert not np.array_equal(a, c)
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1) < 0.01
+
+
+# ------------------------------------------------------------------ GEMM
+
+@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_deepgemm_validate_cases(oracle, golden, batch, ta, tb):
+    key = f"gemm_dv_b{batch}_{'tn'[ta]}{'tn'[tb]}"
+    a, b, want = golden[key + "_a"], golden[key + "_b"], golden[key + "_out"]
+    close(oracle.gemm_f64(a, b, ta, tb), want, 1e-12, 0)
+    close(oracle.gemm_f32(a, b, ta, tb), want, 1e-4, 1e-5)
+
+
+@pytest.mark.parametrize("shape", ["1x80x96x144", "3x16x32x16"])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_kernel_vm_cases(oracle, golden, shape, ta, tb):
+    key = f"gemm_vm_{shape}_{'nt'[ta]}{'nt'[tb]}"
+    a, b, want = golden[key + "_a"], golden[key + "_b"], golden[key + "_out"]
+    close(oracle.gemm_f64(a, b, ta, tb), want, 1e-12, 0)
+    # rust-ascend-kernels/src/tests.rs:117 compares at 1e-4 absolute
+    close(oracle.gemm_f32(a, b, ta, tb), want, 1e-4, 0)
+
+
+def test_gemm_random_vs_numpy_and_transpose_identity(oracle):
+    a = oracle.normal((3, 40, 24), 1, 1)
+    b = oracle.normal((3, 24, 56), 1, 2)
+    want = np.einsum("gik,gkj->gij", a.astype(np.float64), b.astype(np.float64))
+    close(oracle.gemm_f64(a, b, 0, 0), want, 1e-10, 1e-12)
+    # (A B)^T = B^T A^T, through the transposed addressing
+    at = np.ascontiguousarray(a.transpose(0, 2, 1))
+    bt = np.ascontiguousarray(b.transpose(0, 2, 1))
+    close(oracle.gemm_f64(at, bt, 1, 1), want, 1e-10, 1e-12)
+    close(oracle.gemm_f64(bt, at, 0, 0).transpose(0, 2, 1), want, 1e-10, 1e-12)
+    rows = np.array([0, 5, 39, 17])
+    cols = np.array([0, 55, 3, 28])
+    close(oracle.gemm_f64_sampled(a[0], b[0], 0, 0, rows, cols), want[0][rows, cols], 1e-12, 0)
+    close(oracle.gemm_f64_sampled(at[0], b[0], 1, 0, rows, cols), want[0][rows, cols], 1e-12, 0)
+
+
+def test_linear_backward_gradient_identity(oracle, golden):
+    """dX = dY W and dW = dY^T X (matrix_runtime.rs:70-77) and the finite-difference
+    identity of tools/ascend/tests/test_adapter.py:89-93."""
+    x, w, dy = golden["linbwd_x"], golden["linbwd_w"], golden["linbwd_dy"]
+    dx = oracle.gemm_f64(dy, w, 0, 0)
+    dw = oracle.gemm_f64(dy, x, 1, 0)
+    close(dx, golden["linbwd_dx"], 1e-12, 0)
+    close(dw, golden["linbwd_dw"], 1e-12, 0)
+    y = oracle.gemm_f64(x, w, 0, 1)
+    for p, q in [(0, 0), (8, 3), (31, 15)]:
+        xx = x.astype(np.float64).copy()
+        xx[p, q] += 1.0  # linear: the difference is exact
+        yy = xx @ w.astype(np.float64).T
+        assert abs(np.sum((yy - y) * dy) - dx[p, q]) < 1e-9
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+@pytest.mark.parametrize("case", ["0x32", "1x32", "3x96", "7x256", "33x4096", "3x7", "2x4100"])
+def test_rms_norm_f64_vs_autograd(oracle, golden, case):
+    g = {k[len("rms_" + case) + 1:]: v for k, v in golden.items() if k.startswith("rms_" + case + "_")}
+    y, rstd = oracle.rms_norm_f64(g["x"], g["w"], 1e-3)
+    close(y, g["y"], 1e-12, 1e-12)
+    close(rstd, g["rstd"], 1e-12, 1e-12)
+    dx, dw = oracle.rms_norm_backward_f64(g["x"], g["w"], g["dy"], rstd)
+    close(dx, g["dx"], 1e-11, 1e-11)
+    close(dw, g["dw"], 1e-10, 1e-11)
+
+
+@pytest.mark.parametrize("case", ["1x32", "3x96", "7x256", "33x4096"])
+def test_rms_norm_lanes_f32_vs_autograd(oracle, golden, case):
+    g = {k[len("rms_" + case) + 1:]: v for k, v in golden.items() if k.startswith("rms_" + case + "_")}
+    y, rstd = oracle.rms_norm_lanes_f32(g["x"], g["w"], 1e-3)
+    close(y, g["y"], 2e-6, 1e-5)
+    close(rstd, g["rstd"], 0, 1e-6)
+    dx, dw = oracle.rms_norm_backward_lanes_f32(g["x"], g["w"], g["dy"], rstd)
+    close(dx, g["dx"], 2e-6, 1e-5)
+    close(dw, g["dw"], 5e-5, 1e-5)
+
+
+def test_rms_norm_gradients_rs_vectors(oracle, golden):
+    x, w, dy = golden["rmsgrad_x"], golden["rmsgrad_w"], golden["rmsgrad_dy"]
+    y, rstd = oracle.rms_norm_f64(x, w, 1e-5)
+    close(y, golden["rmsgrad_y"], 1e-12, 1e-12)
+    dx, dw = oracle.rms_norm_backward_f64(x, w, dy, rstd)
+    close(dx, golden["rmsgrad_dx"], 1e-12, 1e-12)
+    close(dw, golden["rmsgrad_dw"], 1e-12, 1e-12)
+
+
+def test_rms_weight_contribution_known_answer(oracle, golden):
+    """row_tests.rs:280-287: x = 2, dy = 3, rstd = [.5,.25,2] -> contributions [3,1.5,12].
+    With width 32 and w = 1, the contribution of row r to dw is (x*rstd)*dy per column,
+    so a one-row backward gives dw = 3, 1.5 and 12."""
+    for r, want in zip(golden["rmskat_rstd"], golden["rmskat_contrib"]):
+        x = np.full((1, 32), 2.0, np.float32)
+        dy = np.full((1, 32), 3.0, np.float32)
+        w = np.ones(32, np.float32)
+        _, dw = oracle.rms_norm_backward_lanes_f32(x, w, dy, np.array([r], np.float32))
+        np.testing.assert_array_equal(dw, np.full(32, want, np.float32))
+        _, dw64 = oracle.rms_norm_backward_f64(x, w, dy, np.array([r], np.float64))
+        np.testing.assert_array_equal(dw64, np.full(32, want))
+
+
+def test_rms_constant_row_and_pairwise_tree(oracle):
+    # test_row_reference.py:81-83: a constant 1000 row's mean is exactly 1000 -> y = w*sign
+    x = np.full((3, 4096), 1000.0, np.float32)
+    w = np.linspace(0.5, 1.5, 4096).astype(np.float32)
+    y, rstd = oracle.rms_norm_lanes_f32(x, w, 1e-6)
+    np.testing.assert_allclose(rstd, np.full(3, 1e-3), rtol=1e-6)
+    np.testing.assert_allclose(y, np.broadcast_to(w, (3, 4096)), rtol=1e-6)
+    # normalization.rs:95-114: odd rows are carried; rows == 0 gives zeros
+    for rows in (0, 1, 2, 3, 5, 7, 16, 33):
+        parts = np.arange(rows * 5, dtype=np.float32).reshape(rows, 5)
+        np.testing.assert_array_equal(oracle.column_sum_pairwise(parts), parts.sum(0) if rows else np.zeros(5))
+
+
+# ------------------------------------------------------------------ RoPE
+
+@pytest.mark.parametrize("case", ["0x6", "1x2", "3x6", "2x96"])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_rotary_vs_autograd(oracle, golden, case, layout):
+    key = f"rope_{case}_l{layout}"
+    x, dy, c, s = (golden[key + s_] for s_ in ("_x", "_dy", "_cos", "_sin"))
+    close(oracle.rotary_f64(x, c, s, layout), golden[key + "_y"], 1e-12, 1e-12)
+    close(oracle.rotary_f64(dy, c, s, layout, True), golden[key + "_dx"], 1e-12, 1e-12)
+    # device order in f32 (rotary_tensor.rs:8: 2e-5 + 1e-4|b|)
+    close(oracle.rotary(x, c, s, layout), golden[key + "_y"], 2e-6, 2e-6)
+    close(oracle.rotary(dy, c, s, layout, True), golden[key + "_dx"], 2e-6, 2e-6)
+
+
+def test_rotary_invariants(oracle):
+    x = oracle.normal((5, 64), 0, 1)
+    ang = oracle.normal((5, 32), 0, 2)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    for layout in (0, 1):
+        y = oracle.rotary_f64(x, c, s, layout)
+        # pair norms are preserved
+        if layout == 0:
+            na, nb = x[:, 0::2], x[:, 1::2]
+            ya, yb = y[:, 0::2], y[:, 1::2]
+        else:
+            na, nb, ya, yb = x[:, :32], x[:, 32:], y[:, :32], y[:, 32:]
+        np.testing.assert_allclose(ya ** 2 + yb ** 2, na.astype(np.float64) ** 2 + nb.astype(np.float64) ** 2, rtol=1e-5)
+        # backward undoes forward (rotation is orthogonal)
+        back = oracle.rotary_f64(y.astype(np.float32), c, s, layout, True)
+        np.testing.assert_allclose(back, x, atol=1e-5)
+        # angle 0 is the identity
+        np.testing.assert_array_equal(oracle.rotary(x, np.ones_like(c), np.zeros_like(s), layout), x)
+
+
+@pytest.mark.parametrize("ci", range(5))
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("backward", [0, 1])
+def test_rotary_prefix_golden(oracle, golden, ci, layout, backward):
+    key = f"ropepre_{ci}_l{layout}_b{backward}"
+    x, c, s, want = golden[key + "_x"], golden[key + "_cos"], golden[key + "_sin"], golden[key + "_y"]
+    y = oracle.rotary_prefix(x, c, s, 6, layout, bool(backward))
+    head = (slice(None),) * (x.ndim - 1) + (slice(0, 6),)
+    tail = (slice(None),) * (x.ndim - 1) + (slice(6, None),)
+    close(y[head], want[head], 3e-6, 3e-6)
+    np.testing.assert_array_equal(y[tail].view(np.uint32), x[tail].view(np.uint32))
+
+
+def test_rotary_prefix_full_width_equals_rotary(oracle):
+    x = (np.arange(18, dtype=np.float32) / 8).reshape(3, 6)
+    c = np.full((3, 3), 0.75, np.float32)
+    s = np.full((3, 3), 0.25, np.float32)
+    for layout in (0, 1):
+        for bw in (False, True):
+            np.testing.assert_array_equal(oracle.rotary_prefix(x, c, s, 6, layout, bw),
+                                          oracle.rotary(x, c, s, layout, bw))
+    for bad in (0, 5, 8):
+        with pytest.raises(ValueError):
+            oracle.rotary_prefix(x, c, s, bad, 0)
+
+
+# ------------------------------------------------------------------ attention
+
+@pytest.mark.parametrize("case", ["kv3_g1_n32_c0", "kv1_g3_n96_c0", "kv3_g2_n32_c0", "kv3_g5_n96_c0", "kv3_g3_n96_c1"])
+def test_attention_reference_cases_vs_autograd(oracle, golden, case):
+    g = {k[len("attn_" + case) + 1:]: v for k, v in golden.items() if k.startswith("attn_" + case + "_")}
+    causal = case.endswith("c1")
+    n = g["k"].shape[2]
+    m = g["q"].shape[2]
+    kw = dict(scale=0.25, causal=causal, query_start=(1 << 40) + n - m, key_start=1 << 40)
+    if not causal:
+        kw["mask"] = g["mask"]
+    r = oracle.attention_f64(g["q"], g["k"], g["v"], g["dy"], **kw)
+    tol = dict(atol=2e-3, rtol=3e-3)  # grouped_attention_tensor.rs:10
+    close(r["out"], g["out"], **tol)
+    close(r["lse"], g["lse"], 1e-9, 1e-12)  # no BF16 rounding enters the scores' lse
+    close(r["dq"], g["dq"], **tol)
+    close(r["dk"], g["dk"], **tol)
+    close(r["dv"], g["dv"], **tol)
+
+
+def test_attention_causal_equals_explicit_mask(oracle, golden):
+    g = {k[len("attn_kv3_g3_n96_c1") + 1:]: v for k, v in golden.items() if k.startswith("attn_kv3_g3_n96_c1_")}
+    a = oracle.attention_f64(g["q"], g["k"], g["v"], g["dy"], scale=0.25, causal=True,
+                             query_start=(1 << 40) + 64, key_start=1 << 40)
+    b = oracle.attention_f64(g["q"], g["k"], g["v"], g["dy"], scale=0.25, causal=False, mask=g["mask"])
+    for key in ("out", "lse", "dq", "dk", "dv"):
+        np.testing.assert_array_equal(a[key], b[key])
+
+
+@pytest.mark.parametrize("n", [32, 256])
+def test_attention_orthogonal_closed_form(oracle, golden, n):
+    key = f"attnkat_orth_n{n}"
+    q, k, v, dy = (golden[key + s][:, None] for s in ("_q", "_k", "_v", "_dy"))
+    r = oracle.attention_f64(q, k, v, dy, scale=0.25)
+    for name in ("out", "dq", "dk", "dv"):
+        close(r[name][:, 0], golden[key + "_" + name], 5e-4, 5e-4)
+
+
+@pytest.mark.parametrize("n", [32, 96])
+@pytest.mark.parametrize("cached", [0, 1])
+def test_attention_causal_closed_form(oracle, golden, n, cached):
+    key = f"attnkat_causal_n{n}_c{cached}"
+    v, dy, qs = golden[key + "_v"][:, None], golden[key + "_dy"][:, None], int(golden[key + "_qs"])
+    q = np.zeros((2, 1, 32, 16), np.float32)
+    k = np.zeros((2, 1, n, 16), np.float32)
+    r = oracle.attention_f64(q, k, v, dy, scale=0.25, causal=True, query_start=qs, key_start=0)
+    close(r["out"][:, 0], golden[key + "_out"], 5e-4, 5e-4)   # attention_tensor.rs close(): 5e-4+5e-4|b|
+    close(r["dv"][:, 0], golden[key + "_dv"], 5e-4, 5e-4)
+    assert np.all(r["dq"] == 0) and np.all(r["dk"] == 0)
+
+
+def test_causal_mask_bit_patterns(oracle, golden):
+    for ci in range(3):
+        b, qn, kn, qs, ks = (int(x) for x in golden[f"mask_{ci}_spec"])
+        np.testing.assert_array_equal(oracle.causal_mask(b, qn, kn, qs, ks).view(np.uint32),
+                                      golden[f"mask_{ci}"].view(np.uint32))
+
+
+def test_attention_fully_masked_rows_are_zero(oracle):
+    q = oracle.normal((1, 1, 4, 16), 0, 1)
+    k = oracle.normal((1, 1, 4, 16), 0, 2)
+    v = oracle.normal((1, 1, 4, 16), 0, 3)
+    dy = oracle.normal((1, 1, 4, 16), 0, 4)
+    # key_start 2 > query_start 0: rows 0 and 1 see no key
+    r = oracle.attention_f64(q, k, v, dy, causal=True, query_start=0, key_start=2)
+    assert np.all(r["out"][0, 0, :2] == 0) and np.all(np.isneginf(r["lse"][0, 0, :2]))
+    assert np.all(r["dq"][0, 0, :2] == 0)
+    assert np.all(np.isfinite(r["out"]))
