@@ -348,9 +348,9 @@ def causal_mask(batch, queries, keys, query_start, key_start) -> np.ndarray:
 
 # ------------------------------------------------------------------ comparison
 
-def rel_err(actual, expected) -> float:
-    """max_i |a-b| / (|b| + atol), atol = 1e-3 * rms(b). Infinite when a has a
-    non-finite value where b is finite."""
+def rel_err(actual, expected, atol_frac: float = 1e-3) -> float:
+    """max_i |a-b| / (|b| + atol), atol = atol_frac * rms(b) (1e-3 by default). Infinite when a
+    has a non-finite value where b is finite."""
     a = np.asarray(actual, dtype=np.float64).reshape(-1)
     b = np.asarray(expected, dtype=np.float64).reshape(-1)
     if a.size == 0:
@@ -358,5 +358,5 @@ def rel_err(actual, expected) -> float:
     if not np.all(np.isfinite(a[np.isfinite(b)])):
         return float("inf")
     rms = float(np.sqrt(np.mean(b * b)))
-    atol = 1e-3 * rms if rms > 0 else 1e-30
+    atol = atol_frac * rms if rms > 0 else 1e-30
     return float(np.max(np.abs(a - b) / (np.abs(b) + atol)))

@@ -208,22 +208,23 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
 }
 
 // dw[c] = sum over p of partial[p][c], p ascending within each of 8 slices, then the
-// slices in order: fixed order for a given (parts, width).
+// slices in order: fixed order for a given (parts, width). The (at most 512) partials are
+// added in double so this stage adds no rounding beyond the final conversion to F32.
 __global__ void __launch_bounds__(256)
 sum_partials(const float* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
-    __shared__ float red[8][33];
+    __shared__ double red[8][33];
     const int col = blockIdx.x * 32 + (threadIdx.x & 31);
     const int slice = threadIdx.x >> 5;
-    float s = 0.0f;
+    double s = 0.0;
     if (col < width)
-        for (int p = slice; p < parts; p += 8) s += partial[static_cast<int64_t>(p) * width + col];
+        for (int p = slice; p < parts; p += 8) s += static_cast<double>(partial[static_cast<int64_t>(p) * width + col]);
     red[slice][threadIdx.x & 31] = s;
     __syncthreads();
     if (slice == 0 && col < width) {
-        float t = red[0][threadIdx.x];
+        double t = red[0][threadIdx.x];
 #pragma unroll
         for (int i = 1; i < 8; ++i) t += red[i][threadIdx.x];
-        dw[col] = t;
+        dw[col] = static_cast<float>(t);
     }
 }
 

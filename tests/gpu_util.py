@@ -41,7 +41,24 @@ def close(actual, expected, atol, rtol, name=""):
         raise AssertionError(f"{name}: {int((~ok).sum())} mismatches; first at {tuple(i)}: {a[tuple(i)]} vs {b[tuple(i)]}")
 
 
-def rel_ok(actual, expected, tol, name=""):
-    e = oracle.rel_err(actual, expected)
+def rel_ok(actual, expected, tol, name="", atol_frac=1e-3):
+    e = oracle.rel_err(actual, expected, atol_frac)
     assert e <= tol, f"{name}: max rel err {e:.3e} > {tol}"
     return e
+
+
+# FP32 weight gradients are sums over R rows of FP32 products; each product carries a
+# rounding error of ~2^-24 of its magnitude, so any FP32 implementation (the reference's
+# pairwise tree included) sits ~2^-24*sqrt(R)*rms(term) from the exact sum: 1.5e-5 at
+# R = 16384, rms(dw) = 128. The dW check therefore uses atol = 1e-2*rms(dw) in the rel err
+# (an absolute floor of 1e-6*rms(dw) at tol 1e-4), and the plain relative error on every
+# element with |dw| >= 1e-2*rms(dw).
+DW_ATOL_FRAC = 1e-2
+
+
+def f32_close(actual, expected, name=""):
+    """The reference's F32 GEMM criterion, examples/matrix_runtime.rs:21-22: 5e-4 + 5e-4|b|,
+    with the absolute term scaled by rms(b) (the reference's values are O(1))."""
+    b = np.asarray(expected, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(b * b))) if b.size else 1.0
+    close(actual, expected, 5e-4 * rms, 5e-4, name)

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import DEV, close, dev_bf16, dev_f32, host, randn_bf16, rel_ok
+from gpu_util import DEV, close, dev_bf16, dev_f32, f32_close, host, randn_bf16, rel_ok
 from rust_ascend_hip import HipRuntime, HkError, Transpose
 
 pytestmark = pytest.mark.gpu
@@ -76,7 +76,10 @@ def test_gemm_random_vs_oracle(m, n, k, ta, tb):
             r, c = np.meshgrid(rows, cols, indexing="ij")
             want = oracle.gemm_f64_sampled(a, b, ta, tb, r.ravel(), c.ravel())
             y = y[r.ravel(), c.ravel()]
-        rel_ok(y, want, 1e-2 if out == torch.bfloat16 else 1e-4, f"GEMM {m}x{n}x{k} {ta}{tb} {out}")
+        if out == torch.bfloat16:
+            rel_ok(y, want, 1e-2, f"GEMM {m}x{n}x{k} {ta}{tb} bf16")
+        else:
+            f32_close(y, want, f"GEMM {m}x{n}x{k} {ta}{tb} f32")
 
 
 def test_gemm_batched_vs_oracle():
@@ -84,7 +87,7 @@ def test_gemm_batched_vs_oracle():
         a_t, a = randn_bf16((5, 96, 64) if ta else (5, 64, 96), seed=1)
         b_t, b = randn_bf16((5, 112, 96) if tb else (5, 96, 112), seed=2)
         y = host(HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), torch.float32))
-        rel_ok(y, oracle.gemm_f64(a, b, ta, tb), 1e-4, f"batched {ta}{tb}")
+        f32_close(y, oracle.gemm_f64(a, b, ta, tb), f"batched {ta}{tb}")
 
 
 @pytest.mark.parametrize("m,n,k", [(8192, 8192, 8192), (8192, 14336, 4096), (8192, 4096, 14336)])
@@ -120,7 +123,7 @@ def test_gemm_bf16_fp32_forward_backward(ta, tb):
     np.testing.assert_array_equal(host(ab), oracle.bf16_round(a))
     np.testing.assert_array_equal(host(bb), oracle.bf16_round(b))
     ar, br = oracle.bf16_round(a), oracle.bf16_round(b)
-    rel_ok(host(out), oracle.gemm_f64(ar, br, ta, tb), 1e-4, "fwd")
+    f32_close(host(out), oracle.gemm_f64(ar, br, ta, tb), "fwd")
     dy = oracle.normal((m, n), 5, 3)
     da, db = HipRuntime.gemm_bf16_fp32_backward(ab, bb, dev_f32(dy), Transpose(ta), Transpose(tb))
     assert da.shape == ab.shape and db.shape == bb.shape
@@ -129,20 +132,20 @@ def test_gemm_bf16_fp32_forward_backward(ta, tb):
     op_b = br.T if tb else br
     want_da = dyr.astype(np.float64) @ op_b.T.astype(np.float64)  # d op(A)
     want_db = op_a.T.astype(np.float64) @ dyr.astype(np.float64)  # d op(B)
-    rel_ok(host(da), want_da.T if ta else want_da, 1e-4, "dA")
-    rel_ok(host(db), want_db.T if tb else want_db, 1e-4, "dB")
+    f32_close(host(da), want_da.T if ta else want_da, "dA")
+    f32_close(host(db), want_db.T if tb else want_db, "dB")
 
 
 def test_linear_bf16_fp32_matches_gemm():
     x = oracle.normal((32, 64), 6, 1)
     w = oracle.normal((48, 64), 6, 2)
     y, xb, wb = HipRuntime.linear_bf16_fp32(dev_f32(x), dev_f32(w))
-    rel_ok(host(y), oracle.gemm_f64(oracle.bf16_round(x), oracle.bf16_round(w), 0, 1), 1e-4, "linear")
+    f32_close(host(y), oracle.gemm_f64(oracle.bf16_round(x), oracle.bf16_round(w), 0, 1), "linear")
     dy = oracle.normal((32, 48), 6, 3)
     dx, dw = HipRuntime.linear_bf16_fp32_backward(xb, wb, dev_f32(dy))
     dyr = oracle.bf16_round(dy).astype(np.float64)
-    rel_ok(host(dx), dyr @ oracle.bf16_round(w), 1e-4, "dX")
-    rel_ok(host(dw), dyr.T @ oracle.bf16_round(x), 1e-4, "dW")
+    f32_close(host(dx), dyr @ oracle.bf16_round(w), "dX")
+    f32_close(host(dw), dyr.T @ oracle.bf16_round(x), "dW")
 
 
 def test_gemm_rejects_overlap_and_stays_healthy():
@@ -150,4 +153,4 @@ def test_gemm_rejects_overlap_and_stays_healthy():
     with pytest.raises(HkError):
         HipRuntime.gemm_into(a_t, a_t, Transpose.No, Transpose.No, a_t)  # in-place output overlaps inputs
     y = host(HipRuntime.gemm(a_t, a_t, Transpose.No, Transpose.No, torch.float32))
-    rel_ok(y, oracle.gemm_f64(a, a, 0, 0), 1e-4, "after rejection")
+    f32_close(y, oracle.gemm_f64(a, a, 0, 0), "after rejection")
