@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X BF16 transformer kernel path (one GPU).
+
+Prints ONE JSON line. The headline workload is BASELINE config C2, RMSNorm forward+backward on
+x[16384,4096] BF16 / weight F32 / eps 1e-6 (configs[1]; configs[0] is the reference's small
+CPU-runnable Linear). A step is one forward plus one backward over that batch; `value` is
+algorithmic HBM bytes per step / wall time per step. The BF16 GEMM (C3), RoPE (C4's Q/K), the
+C1 Linear and, when built, fused attention (C4) are measured in the same run and reported
+under "secondary", each with its own roofline. Inputs are synthetic, seeded and resident in
+HBM before timing starts. Kernel durations come from HIP events recorded on the stream the
+kernels run on (torch's current stream, which libhk.so is bound to for every call).
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-secondary]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "rust-ascend_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "BF16 GEMM & attention TFLOP/s (% MI355X MFMA peak); RMSNorm HBM GB/s"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense BF16 MFMA
+C2_ROWS, C2_WIDTH = 16384, 4096
+# Algorithmic bytes (BF16 x/y/dy/dx, F32 w/rstd/dw):
+C2_FWD_BYTES = 2 * C2_ROWS * C2_WIDTH * 2 + C2_WIDTH * 4 + C2_ROWS * 4           # x, y, w, rstd = 268,517,376
+C2_BWD_BYTES = 3 * C2_ROWS * C2_WIDTH * 2 + 2 * C2_WIDTH * 4 + C2_ROWS * 4       # x, dy, dx, w, dw, rstd = 402,751,488
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-secondary", action="store_true", help="headline workload only")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    return p.parse_args()
+
+
+def event_ms(pairs):
+    import torch
+    torch.cuda.synchronize()
+    vals = [a.elapsed_time(b) for a, b in pairs]
+    return sum(vals) / len(vals)
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE and WRITE_SIZE, scaled by
+    the same counters on a copy of known size), kept in profiles/hbm_traffic.txt as
+    `<kernel> <bytes>` lines; None when not measured."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 2 and parts[0] == kernel:
+            return int(float(parts[1]))
+    return None
+
+
+def roofline(bound, algo, ms, kernel):
+    if bound == "hbm":
+        achieved = algo / (ms * 1e-3) / 1e9
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved = algo / (ms * 1e-3) / 1e12
+        peak, unit = BF16_PEAK_TFLOPS, "TFLOP/s"
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": read_traffic(kernel), "kernel": kernel,
+            "algorithmic_per_launch": algo, "avg_launch_ms": round(ms, 5)}
+
+
+def bench_c2(steps, warmup):
+    import torch
+    from rust_ascend_hip import HipRuntime
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    x = torch.randn((C2_ROWS, C2_WIDTH), generator=g, device="cuda").to(torch.bfloat16)
+    dy = torch.randn((C2_ROWS, C2_WIDTH), generator=g, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn((C2_WIDTH,), generator=g, device="cuda")).float()
+    y, rstd = HipRuntime.rms_norm(x, w, 1e-6)
+    dx, dw = HipRuntime.rms_norm_backward(x, w, dy, rstd)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+
+    def step(e=None):
+        if e: e[0].record()
+        HipRuntime.rms_norm(x, w, 1e-6)
+        if e: e[1].record()
+        HipRuntime.rms_norm_backward(x, w, dy, rstd)
+        if e: e[2].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    fwd_ms = event_ms([(e[0], e[1]) for e in ev])
+    bwd_ms = event_ms([(e[1], e[2]) for e in ev])
+    return wall_ms, fwd_ms, bwd_ms
+
+
+def cpu_baseline_c2(threads):
+    """The oracle's restatement of the reference's FP32 row programs (row_programs.rs:144-151,
+    200-217 plus the pairwise column sum of normalization.rs:95-114), timed on the host."""
+    import numpy as np
+    import oracle
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(0)
+    x = oracle.bf16_round(rng.standard_normal((C2_ROWS, C2_WIDTH), dtype=np.float32))
+    dy = oracle.bf16_round(rng.standard_normal((C2_ROWS, C2_WIDTH), dtype=np.float32))
+    w = (1 + 0.1 * rng.standard_normal(C2_WIDTH)).astype(np.float32)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        _, rstd = oracle.rms_norm_lanes_f32(x, w, 1e-6)
+        oracle.rms_norm_backward_lanes_f32(x, w, dy, rstd)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": round((C2_FWD_BYTES + C2_BWD_BYTES) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "seconds_per_step": round(t, 3),
+            "sample": "full C2 step (fwd+bwd, 16384x4096), FP32 row-program order on BF16-valued inputs, "
+                      "median of 3"}
+
+
+def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
+    import torch
+    from rust_ascend_hip import HipRuntime, Transpose
+    out = out or torch.bfloat16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(m + n + k)
+    a = (torch.randn((k, m) if ta else (m, k), generator=g, device="cuda") / k ** 0.5).to(torch.bfloat16)
+    b = (torch.randn((n, k) if tb else (k, n), generator=g, device="cuda") / k ** 0.5).to(torch.bfloat16)
+    c = torch.empty((m, n), device="cuda", dtype=out)
+    for _ in range(warmup):
+        HipRuntime.gemm_into(a, b, Transpose(ta), Transpose(tb), c)
+    pairs = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        HipRuntime.gemm_into(a, b, Transpose(ta), Transpose(tb), c)
+        e1.record()
+        pairs.append((e0, e1))
+    return event_ms(pairs)
+
+
+def bench_rope(iters=10):
+    import numpy as np
+    import torch
+    from rust_ascend_hip import HipRuntime, RotaryLayout
+    pos = np.arange(4096, dtype=np.float64)[:, None]
+    ang = pos * (5e5 ** (-np.arange(0, 128, 2) / 128))[None, :]
+    c = torch.from_numpy(np.cos(ang).astype(np.float32)).cuda()[None, None]
+    s = torch.from_numpy(np.sin(ang).astype(np.float32)).cuda()[None, None]
+    q = torch.randn((4, 32, 4096, 128), device="cuda").to(torch.bfloat16)
+    for _ in range(3):
+        HipRuntime.rotary_prefix(q, c, s, 128, RotaryLayout.SplitHalf)
+    pairs = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        HipRuntime.rotary_prefix(q, c, s, 128, RotaryLayout.SplitHalf)
+        e1.record()
+        pairs.append((e0, e1))
+    ms = event_ms(pairs)
+    algo = 2 * q.numel() * 2 + 2 * c.numel() * 4
+    return ms, algo
+
+
+def bench_attention(iters=5):
+    import torch
+    from rust_ascend_hip import HipRuntime
+    B, H, HKV, S, D = 4, 32, 8, 4096, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    q = torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((B, HKV, S, D), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((B, HKV, S, D), generator=g, device="cuda").to(torch.bfloat16)
+    do = torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16)
+    scale = D ** -0.5
+    o, lse = HipRuntime.attention_forward(q, k, v, scale, True)
+    HipRuntime.attention_backward(q, k, v, o, lse, do, scale, True, grad_dtype=torch.bfloat16)
+    fw, bw = [], []
+    for _ in range(iters):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        HipRuntime.attention_forward(q, k, v, scale, True)
+        e[1].record()
+        HipRuntime.attention_backward(q, k, v, o, lse, do, scale, True, grad_dtype=torch.bfloat16)
+        e[2].record()
+        fw.append((e[0], e[1]))
+        bw.append((e[1], e[2]))
+    fwd_flops = 2 * B * H * S * S * D  # causal-useful (FlashAttention convention): 4*B*H*S^2*D/2
+    return event_ms(fw), event_ms(bw), fwd_flops, 2.5 * fwd_flops
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from rust_ascend_hip import HipRuntime
+    torch.cuda.set_device(0)
+    HipRuntime.initialize_exclusive()
+    HipRuntime.set_async(True)
+
+    wall_ms, fwd_ms, bwd_ms = bench_c2(args.steps, args.warmup)
+    step_bytes = C2_FWD_BYTES + C2_BWD_BYTES
+    value = step_bytes / (wall_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 x and dy, F32 weight 1+N(0,0.1), resident in HBM)",
+        "config": {"workload": "C2 RMSNorm fwd+bwd: x[16384,4096] BF16, weight F32, eps 1e-6, dX BF16, dW F32",
+                   "rows": C2_ROWS, "width": C2_WIDTH, "bytes_per_step": step_bytes,
+                   "fwd_ms": round(fwd_ms, 5), "bwd_ms": round(bwd_ms, 5),
+                   "fwd_GBps": round(C2_FWD_BYTES / fwd_ms / 1e6, 1),
+                   "bwd_GBps": round(C2_BWD_BYTES / bwd_ms / 1e6, 1)},
+        "roofline": roofline("hbm", C2_BWD_BYTES, bwd_ms, "rms_bwd_fast"),
+    }
+    if not args.no_secondary:
+        sec = []
+        for (m, n, k, ta, tb, name) in [(8192, 8192, 8192, 0, 1, "C3 GEMM 8192^3 NT"),
+                                        (8192, 8192, 8192, 0, 0, "C3 GEMM 8192^3 NN"),
+                                        (8192, 14336, 4096, 0, 1, "C3 Llama 8192x4096->14336 NT"),
+                                        (8192, 4096, 14336, 0, 1, "C3 Llama 8192x14336->4096 NT"),
+                                        (4096, 4096, 4096, 0, 1, "C3 GEMM 4096^3 NT"),
+                                        (1024, 1024, 1024, 0, 1, "C3 GEMM 1024^3 NT"),
+                                        (512, 1024, 1024, 0, 1, "C1 Linear X[512,1024] W[1024,1024]^T")]:
+            ms = bench_gemm(m, n, k, ta, tb)
+            flops = 2 * m * n * k
+            sec.append({"workload": name, "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
+                        "ms": round(ms, 5), "roofline": roofline("mfma", flops, ms, "gemm_nt_kernel")})
+        ms, algo = bench_rope()
+        sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
+                    "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
+                    "roofline": roofline("hbm", algo, ms, "rope_pairs")})
+        try:
+            f_ms, b_ms, ff, bf = bench_attention()
+            sec.append({"workload": "C4 causal GQA attention fwd B4 S4096 Hq32 Hkv8 D128", "value": round(ff / f_ms / 1e9, 2),
+                        "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd")})
+            sec.append({"workload": "C4 causal GQA attention bwd B4 S4096 Hq32 Hkv8 D128", "value": round(bf / b_ms / 1e9, 2),
+                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd")})
+        except Exception as exc:  # reported, never silently replaced by another path
+            sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
+        line["secondary"] = sec
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+    if not args.no_cpu:
+        threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
+        line["cpu_baseline"] = cpu_baseline_c2(threads)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
