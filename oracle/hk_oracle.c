@@ -387,17 +387,24 @@ int or_rotary_prefix(const float* x, const int64_t* in_shape, const int64_t* tab
  * excluded). `mask` (optional, [B,Hq,M,N] additive) is used when causal == 0.
  * Rows whose keys are all excluded produce zeros and lse = -inf (the composed
  * reference produces NaN there; see the attention kernel's documentation).
- * Any of out/lse/dq/dk/dv may be NULL; dq/dk/dv require dy. Outputs are overwritten. */
+ * Any of out/lse/dq/dk/dv/mag may be NULL; dq/dk/dv require dy. Outputs are overwritten. */
 void or_attention_f64(const float* q, const float* k, const float* v, const float* dy,
                       const float* mask, int64_t batch, int64_t heads, int64_t kv_heads,
                       int64_t m, int64_t n, int64_t d, double scale, int causal,
                       uint64_t query_start, uint64_t key_start, double* out, double* lse,
-                      double* dq, double* dk, double* dv) {
+                      double* dq, double* dk, double* dv, double* mag) {
     int64_t group = heads / kv_heads;
     if (out) memset(out, 0, sizeof(double) * (size_t)(batch * heads * m * d));
     if (dq) memset(dq, 0, sizeof(double) * (size_t)(batch * heads * m * d));
     if (dk) memset(dk, 0, sizeof(double) * (size_t)(batch * kv_heads * n * d));
     if (dv) memset(dv, 0, sizeof(double) * (size_t)(batch * kv_heads * n * d));
+    /* mag (optional): the same sums over the absolute values of their terms, laid out as
+     * [out | dq | dk | dv]; sum |terms| bounds the effect of rounding any term. */
+    double* out_m = mag;
+    double* dq_m = mag ? mag + batch * heads * m * d : NULL;
+    double* dk_m = mag ? dq_m + batch * heads * m * d : NULL;
+    double* dv_m = mag ? dk_m + batch * kv_heads * n * d : NULL;
+    if (mag) memset(mag, 0, sizeof(double) * (size_t)(2 * batch * heads * m * d + 2 * batch * kv_heads * n * d));
     /* Parallel over (batch, kv head): the group's query heads run sequentially inside,
      * so dk/dv accumulate in a fixed order without races. */
 #pragma omp parallel for schedule(dynamic) collapse(2)
@@ -436,6 +443,8 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
                             double pb = (double)bf16r((float)p[j]);
                             if (pb == 0.0) continue;
                             for (int64_t c = 0; c < d; ++c) out[oi * d + c] += pb * (double)bf16r(vh[j * d + c]);
+                            if (out_m)
+                                for (int64_t c = 0; c < d; ++c) out_m[oi * d + c] += fabs(pb * (double)bf16r(vh[j * d + c]));
                         }
                     }
                     if (!dy) continue;
@@ -461,6 +470,17 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
                         if (dk) {
                             double* dkh = dk + ((b * kv_heads + kv) * n + j) * d;
                             for (int64_t c = 0; c < d; ++c) dkh[c] += dsb * (double)bf16r(qh[row * d + c]);
+                        }
+                        if (mag) {
+                            /* |dS| uses |p|*(|dp| + |dot|): the magnitude of the terms of dS itself */
+                            double dsm = scale * p[j] * (fabs(dp[j]) + fabs(dot));
+                            double* dvm = dv_m + ((b * kv_heads + kv) * n + j) * d;
+                            double* dkm = dk_m + ((b * kv_heads + kv) * n + j) * d;
+                            for (int64_t c = 0; c < d; ++c) {
+                                dvm[c] += fabs(pb * (double)bf16r(g[c]));
+                                dq_m[oi * d + c] += dsm * fabs((double)bf16r(kh[j * d + c]));
+                                dkm[c] += dsm * fabs((double)bf16r(qh[row * d + c]));
+                            }
                         }
                     }
                 }

@@ -93,7 +93,7 @@ def lib():
         _vp = ctypes.c_void_p
         L.or_attention_f64.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                        ctypes.c_double, _int, ctypes.c_uint64, ctypes.c_uint64,
-                                       _vp, _vp, _vp, _vp, _vp]
+                                       _vp, _vp, _vp, _vp, _vp, _vp]
         L.or_causal_mask.argtypes = [_i64, _i64, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32p]
         _lib = L
     return _lib
@@ -313,8 +313,10 @@ def rope_tables(positions, dim: int, theta: float):
 # ------------------------------------------------------------------ attention
 
 def attention_f64(q, k, v, dy=None, scale=0.25, causal=False, query_start=0, key_start=0,
-                  mask=None, want_grads=True):
-    """Returns dict(out, lse[, dq, dk, dv]) in f64 for q [B,Hq,M,D], k/v [B,Hkv,N,D]."""
+                  mask=None, want_grads=True, magnitudes=False):
+    """Returns dict(out, lse[, dq, dk, dv]) in f64 for q [B,Hq,M,D], k/v [B,Hkv,N,D]. With
+    magnitudes=True also out_mag/dq_mag/dk_mag/dv_mag: each output's sum over the absolute
+    values of its terms (the scale against which a rounding of any term is measured)."""
     q = _c32(q)
     k = _c32(k)
     v = _c32(v)
@@ -334,10 +336,32 @@ def attention_f64(q, k, v, dy=None, scale=0.25, causal=False, query_start=0, key
             dv = np.empty_like(dk)
             res.update(dq=dq, dk=dk, dv=dv)
     maskc = None if mask is None else _c32(mask)
+    mag = None
+    if magnitudes:
+        mag = np.empty(2 * B * H * M * D + 2 * B * Hkv * N * D, dtype=np.float64)
     lib().or_attention_f64(ptr(q), ptr(k), ptr(v), ptr(dyc), ptr(maskc), B, H, Hkv, M, N, D,
                            float(scale), int(bool(causal)), int(query_start), int(key_start),
-                           ptr(out), ptr(lse), ptr(dq), ptr(dk), ptr(dv))
+                           ptr(out), ptr(lse), ptr(dq), ptr(dk), ptr(dv), ptr(mag))
+    if magnitudes:
+        a, c = B * H * M * D, B * Hkv * N * D
+        res["out_mag"] = mag[:a].reshape(out.shape)
+        res["dq_mag"] = mag[a:2 * a].reshape(out.shape)
+        res["dk_mag"] = mag[2 * a:2 * a + c].reshape((B, Hkv, N, D))
+        res["dv_mag"] = mag[2 * a + c:].reshape((B, Hkv, N, D))
     return res
+
+
+def mag_err(actual, expected, magnitude) -> float:
+    """max_i |a-b| / magnitude_i, magnitude = the sum of |terms| of each output (attention)."""
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    mg = np.asarray(magnitude, dtype=np.float64)
+    if a.size == 0:
+        return 0.0
+    if not np.all(np.isfinite(a)):
+        return float("inf")
+    floor = 1e-6 * max(float(np.max(mg)), 1e-30)
+    return float(np.max(np.abs(a - b) / np.maximum(mg, floor)))
 
 
 def causal_mask(batch, queries, keys, query_start, key_start) -> np.ndarray:

@@ -1,13 +1,341 @@
-// hk_attention.hip — placeholder until the fused kernels land.
+// hk_attention.hip — fused causal / grouped-query attention (forward and backward) for gfx950.
+//
+// Semantics (reference src/nn/attention.rs:10-80, examples/grouped_attention_tensor.rs:14-44):
+//   S = scale * Q K^T (+ causal mask: key_start + j > query_start + i is excluded),
+//   P = softmax(S) per query row, O = P V, with query head h reading KV head h / (Hq/Hkv)
+//   (heads_programs.rs:5-60). GEMM operands are BF16 and accumulate in FP32; P is rounded to
+//   BF16 before P.V (matmul_bf16_fp32 rounds its inputs), softmax statistics are FP32.
+//   Backward: dV = P^T dO, dP = dO V^T, dS = P (dP - rowsum(dO o O)), dQ = scale dS K,
+//   dK = scale dS^T Q; dS is scaled and rounded to BF16 before its two GEMMs, as the
+//   reference's MatmulBf16Fp32Backward chain rounds it.
+//   Rows that see no key produce O = 0, lse = -inf and zero gradients (the composed reference
+//   would produce NaN from softmax over an all -inf row).
+//
+// Layout: Q/O/dO [B,Hq,M,D], K/V [B,Hkv,N,D] BF16 row-major; lse and the backward's row
+// statistics F32 [B,Hq,M]. Nothing of size M x N is ever materialized.
+//
+// Forward kernel (FlashAttention-2 style, MI355X-first):
+//   * one workgroup = 4 wavefronts = 128 query rows of one (batch, head); K/V tiles of 64 keys
+//     are double-buffered in LDS (rows XOR-swizzled in 16-byte chunks) and prefetched from HBM
+//     into registers one tile ahead;
+//   * each wave computes S^T = K Q^T (v_mfma_f32_32x32x16_bf16, Q held in registers as the B
+//     operand), so every lane owns ONE query column: the row max/sum need a single exchange
+//     with lane^32 instead of a 32-lane reduction;
+//   * the FP32 accumulators of S^T, converted to BF16, are directly the B operand of
+//     O^T = V^T P^T (the key order inside each MFMA k-group is matched on the V side);
+//     V^T comes straight from the row-major V tile through ds_read_b64_tr_b16 (the gfx950
+//     transposing LDS read), so V is never transposed in memory;
+//   * online softmax in base 2 (scale*log2(e) folded into one multiply, v_exp_f32);
+//   * causal: tiles past the diagonal are never loaded, waves skip tiles that are fully masked
+//     for their 32 rows, and blocks are issued heaviest-first within each (batch, head).
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
+
 namespace hk {
-size_t attention_bwd_workspace_bytes(const AttnShape&) { return 0; }
-hipError_t attention_forward(const AttnShape&, const void*, const void*, const void*, void*, float*, hipStream_t) {
-    return hipErrorNotSupported;
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kBlockM = 128;  // query rows per forward workgroup (4 waves x 32)
+constexpr int kBlockN = 64;   // keys per K/V tile
+constexpr int kThreads = 256;
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+// 16-byte chunk swizzle of a tile row: keeps the 32-row MFMA operand reads, the 4-row
+// transposing reads and the row-contiguous tile writes free of LDS bank conflicts.
+template <int D>
+__device__ __forceinline__ int tile_off(int row, int col) {  // element offset in a [rows][D] tile
+    constexpr int chunks = D / 8;
+    constexpr int mask = chunks - 1 < 7 ? chunks - 1 : 7;
+    const int f = (((row & 3) << 1) | ((row >> 2) & 1)) & mask;
+    return row * D + ((((col >> 3) ^ f)) << 3) + (col & 7);
 }
+
+// 16 bytes at (row, 8*chunk) of a swizzled tile.
+template <int D>
+__device__ __forceinline__ bf16x8_t tile_read16(const uint16_t* t, int row, int chunk) {
+    return *reinterpret_cast<const bf16x8_t*>(t + tile_off<D>(row, chunk * 8));
+}
+
+// MFMA 32x32x16 operand "rows i = this lane's l%32, k = 8 consecutive tile rows" read from a
+// row-major [k][i] tile: two transposing reads of 4 rows each. kbase0/kbase1 are the tile rows
+// of the two 4-row halves for this lane's k-group; ibase is the first of the 32 columns.
+template <int D>
+__device__ __forceinline__ bf16x8_t tile_read_tr(const uint16_t* t, int lane, int kbase0, int kbase1, int ibase) {
+    const int g = (lane >> 4) & 1;     // which 16 columns of the 32
+    const int i = lane & 15;           // lane within its 16-lane group
+    const int col = ibase + 16 * g + 4 * (i & 3);
+    const int r = i >> 2;
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16_t*)(t + tile_off<D>(kbase0 + r, col)));
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16_t*)(t + tile_off<D>(kbase1 + r, col)));
+    typedef short v8i16_t __attribute__((ext_vector_type(8)));
+    v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const f32x16_t& a, int base) {
+    u32x4_t w = {pack_bf16x2(a[base + 0], a[base + 1]), pack_bf16x2(a[base + 2], a[base + 3]),
+                 pack_bf16x2(a[base + 4], a[base + 5]), pack_bf16x2(a[base + 6], a[base + 7])};
+    return __builtin_bit_cast(bf16x8_t, w);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+struct FwdArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    uint16_t* o;
+    float* lse;
+    int64_t heads, kv_heads, m, n;
+    int64_t diag;  // key j is visible to query i iff j <= i + diag (causal only)
+    float scale_log2;
+    int causal;
+    int mblocks;
+};
+
+// Tile rows [row0, row0+64) of a [N, D] matrix -> registers (rows >= n clamp to n-1), laid
+// out in LDS as [64][DP] with DP = max(D, 32); columns >= D are zero.
+template <int D, int DP>
+struct TileLoader {
+    static constexpr int kChunks = DP / 8;                          // 16-byte chunks per LDS row
+    static constexpr int kPerThread = kBlockN * kChunks / kThreads;  // >= 1 since DP >= 32
+    u32x4_t r[kPerThread];
+    __device__ __forceinline__ void load(const uint16_t* base, int64_t row0, int64_t n, int t) {
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+            const int idx = t + i * kThreads;
+            const int row = idx / kChunks, chunk = idx % kChunks;
+            int64_t gr = row0 + row;
+            gr = gr < n ? gr : n - 1;
+            r[i] = (chunk * 8 < D) ? *reinterpret_cast<const u32x4_t*>(base + gr * D + chunk * 8) : u32x4_t{0, 0, 0, 0};
+        }
+    }
+    __device__ __forceinline__ void store(uint16_t* tile, int t) const {
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+            const int idx = t + i * kThreads;
+            const int row = idx / kChunks, chunk = idx % kChunks;
+            *reinterpret_cast<u32x4_t*>(tile + tile_off<DP>(row, chunk * 8)) = r[i];
+        }
+    }
+};
+
+// D is the head dim in memory; the kernel works on DP = max(D, 32) (zero-padded columns).
+template <int D>
+__global__ void __launch_bounds__(kThreads, 2)
+attn_fwd(FwdArgs a) {
+    constexpr int DP = D < 32 ? 32 : D;
+    constexpr int KS = DP / 16;  // MFMA k-steps over the head dim
+    constexpr int DT = DP / 32;  // 32-wide output tiles over the head dim
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBlockN * DP];  // [buf][K,V]
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lq = lane & 31, lg = lane >> 5;
+    const int bh = blockIdx.x / a.mblocks;
+    const int mb = a.mblocks - 1 - (blockIdx.x % a.mblocks);  // heaviest causal blocks first
+    const int64_t b = bh / a.heads, h = bh % a.heads;
+    const int64_t kvh = h / (a.heads / a.kv_heads);
+    const uint16_t* Q = a.q + (bh * a.m) * D;
+    const uint16_t* K = a.k + ((b * a.kv_heads + kvh) * a.n) * D;
+    const uint16_t* V = a.v + ((b * a.kv_heads + kvh) * a.n) * D;
+    const int64_t q0 = static_cast<int64_t>(mb) * kBlockM;
+    const int64_t q0w = q0 + wave * 32;
+    const int64_t my_q = q0w + lq;
+
+    // keys this workgroup needs: [0, kv_end)
+    int64_t kv_end = a.n;
+    if (a.causal) {
+        const int64_t last = q0 + kBlockM - 1 + a.diag;  // last visible key of the block's last row
+        kv_end = last + 1 < kv_end ? last + 1 : kv_end;
+    }
+    const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
+
+    // Q of this lane's query as the B operand: d = 16*s + 8*lg .. +7
+    bf16x8_t qf[KS];
+    {
+        const int64_t qr = my_q < a.m ? my_q : a.m - 1;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int d0 = 16 * s + 8 * lg;
+            qf[s] = d0 < D ? *reinterpret_cast<const bf16x8_t*>(Q + qr * D + d0)
+                           : __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
+        }
+    }
+
+    f32x16_t o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    TileLoader<D, DP> lk, lv;
+    if (ntiles > 0) {
+        lk.load(K, 0, a.n, t);
+        lv.load(V, 0, a.n, t);
+        lk.store(lds[0][0], t);
+        lv.store(lds[0][1], t);
+        if (ntiles > 1) {
+            lk.load(K, kBlockN, a.n, t);
+            lv.load(V, kBlockN, a.n, t);
+        }
+    }
+    __syncthreads();
+
+    for (int j = 0; j < ntiles; ++j) {
+        const int cur = j & 1;
+        const int64_t kv0 = static_cast<int64_t>(j) * kBlockN;
+        const uint16_t* Kt = lds[cur][0];
+        const uint16_t* Vt = lds[cur][1];
+        // this wave's rows see no key of this tile -> skip (still takes part in the barriers)
+        const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
+        if (!skip) {
+            f32x16_t s[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Kt, 32 * tt + lq, 2 * ks + lg),
+                                                                    qf[ks], s[tt], 0, 0, 0);
+            }
+            // scale, mask, tile max
+            const bool need_mask = (kv0 + kBlockN > a.n) || (a.causal && kv0 + kBlockN - 1 > q0w + a.diag);
+            float mt = -INFINITY;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    float x = s[tt][v] * a.scale_log2;
+                    if (need_mask) {
+                        const int64_t key = kv0 + 32 * tt + (v >> 2) * 8 + lg * 4 + (v & 3);
+                        const bool vis = key < a.n && (!a.causal || key <= my_q + a.diag);
+                        x = vis ? x : -INFINITY;
+                    }
+                    s[tt][v] = x;
+                    mt = fmaxf(mt, x);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = fast_exp2(m_run - m_use);
+            float ls = 0.0f;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float p = fast_exp2(s[tt][v] - m_use);
+                    s[tt][v] = p;
+                    ls += p;
+                }
+            l_run = l_run * alpha + ls;
+            m_run = m_new;
+#pragma unroll
+            for (int i = 0; i < DT; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
+            // O^T += V^T P^T over the tile's 64 keys (4 k-steps of 16)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8_t pb = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
+                const int kb0 = 16 * ks + 4 * lg;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Vt, lane, kb0, kb0 + 8, 32 * dt),
+                                                                    pb, o[dt], 0, 0, 0);
+            }
+        }
+        if (j + 1 < ntiles) {
+            lk.store(lds[cur ^ 1][0], t);
+            lv.store(lds[cur ^ 1][1], t);
+            if (j + 2 < ntiles) {
+                lk.load(K, kv0 + 2 * kBlockN, a.n, t);
+                lv.load(V, kv0 + 2 * kBlockN, a.n, t);
+            }
+        }
+        __syncthreads();
+    }
+
+    // epilogue: O[q][d] = O^T / l ; lse = (m + log2 l) ln 2
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (my_q < a.m) {
+        uint16_t* orow = a.o + (bh * a.m + my_q) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * dt + 8 * g + 4 * lg;
+                if (d >= D) continue;
+                u32x2_t w = {pack_bf16x2(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv),
+                             pack_bf16x2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
+                *reinterpret_cast<u32x2_t*>(orow + d) = w;
+            }
+        if (lg == 0)
+            a.lse[bh * a.m + my_q] = l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+    }
+}
+
+int64_t clamp_diag(const AttnShape& sh) {
+    // visible iff key_start + j <= query_start + i  <=>  j <= i + (query_start - key_start)
+    if (!sh.causal) return 0;
+    const uint64_t qs = sh.query_start, ks = sh.key_start;
+    if (qs >= ks) {
+        const uint64_t d = qs - ks;
+        return d > static_cast<uint64_t>(sh.n) ? sh.n : static_cast<int64_t>(d);
+    }
+    const uint64_t d = ks - qs;
+    const uint64_t cap = static_cast<uint64_t>(sh.m + sh.n + 1);
+    return -static_cast<int64_t>(d > cap ? cap : d);
+}
+
+template <int D>
+hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const void* v, void* o, float* lse,
+                      hipStream_t s) {
+    FwdArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.k = static_cast<const uint16_t*>(k);
+    a.v = static_cast<const uint16_t*>(v);
+    a.o = static_cast<uint16_t*>(o);
+    a.lse = lse;
+    a.heads = sh.heads;
+    a.kv_heads = sh.kv_heads;
+    a.m = sh.m;
+    a.n = sh.n;
+    a.diag = clamp_diag(sh);
+    a.scale_log2 = sh.scale * kLog2e;
+    a.causal = sh.causal;
+    a.mblocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
+    const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
+    hipLaunchKernelGGL((attn_fwd<D>), grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t attention_bwd_workspace_bytes(const AttnShape&) { return 0; }
+
+hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o, float* lse,
+                             hipStream_t s) {
+    switch (sh.d) {
+        case 16: return launch_fwd<16>(sh, q, k, v, o, lse, s);
+        case 32: return launch_fwd<32>(sh, q, k, v, o, lse, s);
+        case 64: return launch_fwd<64>(sh, q, k, v, o, lse, s);
+        case 128: return launch_fwd<128>(sh, q, k, v, o, lse, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t attention_backward(const AttnShape&, const void*, const void*, const void*, const void*, const float*,
                               const void*, void*, int, void*, void*, int, void*, hipStream_t) {
     return hipErrorNotSupported;
 }
+
 }  // namespace hk

@@ -1,0 +1,113 @@
+"""GPU parity of the fused causal/grouped-query attention through the C ABI, against the f64
+oracle (which restates examples/grouped_attention_tensor.rs:14-44 with the reference's BF16
+rounding points), the reference's closed forms and the golden vectors.
+
+Tolerances: the reference's GQA check (grouped_attention_tensor.rs:10: 2e-3 + 3e-3|b|) on its
+own cases, the closed-form checks' 5e-4 + 5e-4|b| (attention_tensor.rs), and max rel err
+<= 1e-2 on BF16 outputs elsewhere. The fused kernel takes the causal mask or no mask; the
+reference's arbitrary additive masks are not on the fused path, so its non-causal GQA cases
+run here without the mask (against the oracle evaluated the same way).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import DEV, close, dev_bf16, host, mag_ok, randn_bf16, rel_ok
+from rust_ascend_hip import HipRuntime, HkError
+
+pytestmark = pytest.mark.gpu
+
+GQA_CASES = ["kv3_g1_n32_c0", "kv1_g3_n96_c0", "kv3_g2_n32_c0", "kv3_g5_n96_c0", "kv3_g3_n96_c1"]
+
+
+def golden_case(golden, case):
+    return {k[len("attn_" + case) + 1:]: v for k, v in golden.items() if k.startswith("attn_" + case + "_")}
+
+
+@pytest.mark.parametrize("case", GQA_CASES)
+def test_forward_reference_gqa_cases(golden, case):
+    g = golden_case(golden, case)
+    causal = case.endswith("c1")
+    n, m = g["k"].shape[2], g["q"].shape[2]
+    qs, ks = ((1 << 40) + n - m, 1 << 40) if causal else (0, 0)
+    o, lse = HipRuntime.attention_forward(dev_bf16(g["q"]), dev_bf16(g["k"]), dev_bf16(g["v"]), 0.25, causal, qs, ks)
+    ref = oracle.attention_f64(g["q"], g["k"], g["v"], scale=0.25, causal=causal, query_start=qs, key_start=ks)
+    close(host(o), ref["out"], 2e-3, 3e-3, "O")
+    close(host(lse), ref["lse"], 1e-4, 1e-5, "lse")
+    if causal:  # the golden vectors of this case are the torch-f64 autograd ones with the causal mask
+        close(host(o), g["out"], 2e-3, 3e-3, "O vs golden")
+        close(host(lse), g["lse"], 1e-4, 1e-5, "lse vs golden")
+
+
+@pytest.mark.parametrize("n", [32, 256])
+def test_forward_orthogonal_closed_form(golden, n):
+    key = f"attnkat_orth_n{n}"
+    q, k, v = (golden[key + s][:, None] for s in ("_q", "_k", "_v"))
+    o, _ = HipRuntime.attention_forward(dev_bf16(q), dev_bf16(k), dev_bf16(v), 0.25, False)
+    close(host(o)[:, 0], golden[key + "_out"], 5e-4, 5e-4, "O")
+
+
+@pytest.mark.parametrize("n", [32, 96])
+@pytest.mark.parametrize("cached", [0, 1])
+def test_forward_causal_running_mean(golden, n, cached):
+    key = f"attnkat_causal_n{n}_c{cached}"
+    v, qs = golden[key + "_v"][:, None], int(golden[key + "_qs"])
+    q = np.zeros((2, 1, 32, 16), np.float32)
+    k = np.zeros((2, 1, n, 16), np.float32)
+    o, lse = HipRuntime.attention_forward(dev_bf16(q), dev_bf16(k), dev_bf16(v), 0.25, True, qs, 0)
+    close(host(o)[:, 0], golden[key + "_out"], 5e-4, 5e-4, "O")
+    active = np.minimum(qs + np.arange(32) + 1, n)
+    close(host(lse)[:, 0], np.broadcast_to(np.log(active), (2, 32)), 1e-5, 1e-5, "lse")
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("m,n", [(256, 256), (200, 328), (64, 1000), (130, 130)])
+def test_forward_random_vs_oracle(d, causal, m, n):
+    h, hkv = 4, 2
+    q_t, q = randn_bf16((2, h, m, d), seed=d + m)
+    k_t, k = randn_bf16((2, hkv, n, d), seed=d + n + 1)
+    v_t, v = randn_bf16((2, hkv, n, d), seed=d + n + 2)
+    qs = max(n - m, 0) if causal else 0  # bottom-right aligned when keys outnumber queries
+    o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, d ** -0.5, causal, qs, 0)
+    ref = oracle.attention_f64(q, k, v, scale=d ** -0.5, causal=causal, query_start=qs, key_start=0, magnitudes=True)
+    mag_ok(host(o), ref["out"], ref["out_mag"], 1e-2, "O")
+    close(host(lse), ref["lse"], 1e-3, 1e-4, "lse")
+
+
+def test_forward_fully_masked_rows_and_positions():
+    """key_start > query_start: the first rows see no key (O = 0, lse = -inf); the oracle agrees."""
+    q_t, q = randn_bf16((1, 2, 64, 64), seed=3)
+    k_t, k = randn_bf16((1, 1, 64, 64), seed=4)
+    v_t, v = randn_bf16((1, 1, 64, 64), seed=5)
+    o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, 0.125, True, 100, 110)
+    ref = oracle.attention_f64(q, k, v, scale=0.125, causal=True, query_start=100, key_start=110, magnitudes=True)
+    lse_h = host(lse)
+    assert np.all(np.isneginf(lse_h[:, :, :10])) and np.all(host(o)[:, :, :10] == 0)
+    mag_ok(host(o)[:, :, 10:], ref["out"][:, :, 10:], ref["out_mag"][:, :, 10:], 1e-2, "O")
+    close(lse_h[:, :, 10:], ref["lse"][:, :, 10:], 1e-3, 1e-4, "lse")
+    # huge absolute positions with no key visible at all
+    o2, lse2 = HipRuntime.attention_forward(q_t, k_t, v_t, 0.125, True, 5, (1 << 63) + 7)
+    assert torch.count_nonzero(o2) == 0 and torch.all(torch.isneginf(lse2))
+
+
+def test_forward_c4_full_size_sampled():
+    """B4, S4096, Hq32/Hkv8, D128, causal, scale 1/sqrt(128); parity on
+    batch 0 x KV group 0 (4 query heads) over all 4096 rows."""
+    B, H, HKV, S, D = 4, 32, 8, 4096, 128
+    q_t, _ = randn_bf16((B, H, S, D), seed=41)
+    k_t, _ = randn_bf16((B, HKV, S, D), seed=42)
+    v_t, _ = randn_bf16((B, HKV, S, D), seed=43)
+    o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, D ** -0.5, True)
+    ref = oracle.attention_f64(host(q_t[:1, :4]), host(k_t[:1, :1]), host(v_t[:1, :1]), scale=D ** -0.5,
+                               causal=True, magnitudes=True)
+    mag_ok(host(o[:1, :4]), ref["out"], ref["out_mag"], 1e-2, "O")
+    close(host(lse[:1, :4]), ref["lse"], 1e-3, 1e-4, "lse")
+
+
+def test_forward_rejects_bad_shapes():
+    q_t, _ = randn_bf16((1, 3, 64, 64), seed=1)
+    k_t, _ = randn_bf16((1, 2, 64, 64), seed=2)
+    with pytest.raises(HkError):
+        HipRuntime.attention_forward(q_t, k_t, k_t, 0.125, True)  # 3 % 2 != 0

@@ -287,3 +287,20 @@ def test_attention_fully_masked_rows_are_zero(oracle):
     assert np.all(r["out"][0, 0, :2] == 0) and np.all(np.isneginf(r["lse"][0, 0, :2]))
     assert np.all(r["dq"][0, 0, :2] == 0)
     assert np.all(np.isfinite(r["out"]))
+
+
+def test_attention_magnitudes_bound_the_outputs(oracle):
+    """Each magnitude is the sum of |terms|: >= |value| everywhere, == value when every term
+    is non-negative (V, dY >= 0 give O, dV >= 0), and it scales linearly with V."""
+    q = oracle.normal((1, 2, 40, 32), 0, 1)
+    k = oracle.normal((1, 1, 72, 32), 0, 2)
+    v = oracle.normal((1, 1, 72, 32), 0, 3)
+    dy = oracle.normal((1, 2, 40, 32), 0, 4)
+    r = oracle.attention_f64(q, k, v, dy, scale=0.2, causal=True, query_start=32, magnitudes=True)
+    for name in ("out", "dq", "dk", "dv"):  # the BF16-rounded terms may exceed theirs by 2^-8
+        assert np.all(r[name + "_mag"] * (1 + 2.0 ** -8) >= np.abs(r[name]) - 1e-12), name
+    rp = oracle.attention_f64(q, k, np.abs(v), np.abs(dy), scale=0.2, causal=True, query_start=32, magnitudes=True)
+    np.testing.assert_allclose(rp["out_mag"], rp["out"], rtol=1e-12)
+    np.testing.assert_allclose(rp["dv_mag"], rp["dv"], rtol=1e-12)
+    r2 = oracle.attention_f64(q, k, 2 * v, dy, scale=0.2, causal=True, query_start=32, magnitudes=True)
+    np.testing.assert_allclose(r2["out_mag"], 2 * r["out_mag"], rtol=1e-12)
