@@ -449,12 +449,17 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
                     }
                     if (!dy) continue;
                     const float* g = dy + oi * d;
-                    double dot = 0.0;
+                    double dot = 0.0, dot_mag = 0.0, dot_mag_o = 0.0;
                     for (int64_t j = 0; j < n; ++j) {
                         double acc = 0.0;
                         for (int64_t c = 0; c < d; ++c) acc += (double)bf16r(g[c]) * (double)bf16r(vh[j * d + c]);
                         dp[j] = acc;
                         dot += p[j] * acc;
+                        dot_mag += p[j] * fabs(acc);
+                    }
+                    if (mag && out) {
+                        for (int64_t c = 0; c < d; ++c) dot_mag_o += fabs((double)bf16r(g[c]) * out[oi * d + c]);
+                        if (dot_mag_o > dot_mag) dot_mag = dot_mag_o;
                     }
                     for (int64_t j = 0; j < n; ++j) {
                         double ds = p[j] * (dp[j] - dot);
@@ -472,8 +477,10 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
                             for (int64_t c = 0; c < d; ++c) dkh[c] += dsb * (double)bf16r(qh[row * d + c]);
                         }
                         if (mag) {
-                            /* |dS| uses |p|*(|dp| + |dot|): the magnitude of the terms of dS itself */
-                            double dsm = scale * p[j] * (fabs(dp[j]) + fabs(dot));
+                            /* |dS| term magnitude: p*(|dp| + |row term|), where the row term's own
+                             * magnitude is the larger of sum_j p_j |dp_j| (its form here) and
+                             * sum_d |dY_d O_d| (the form rowsum(dY o O) a fused kernel uses). */
+                            double dsm = scale * p[j] * (fabs(dp[j]) + dot_mag);
                             double* dvm = dv_m + ((b * kv_heads + kv) * n + j) * d;
                             double* dkm = dk_m + ((b * kv_heads + kv) * n + j) * d;
                             for (int64_t c = 0; c < d; ++c) {

@@ -318,9 +318,427 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------- backward
+//
+// Pre-pass: rowstat[bh, i] = sum_d dO[i, d] * O[i, d] (F32). With O = P V this equals
+// sum_j P_ij dP_ij, the softmax-backward row term of row_programs.rs:152-163.
+template <int D>
+__global__ void __launch_bounds__(256)
+attn_bwd_rowstat(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout, float* __restrict__ stat,
+                 int64_t rows) {
+    constexpr int kLanesPerRow = D / 8;  // each lane reads 8 elements
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t row = gid / kLanesPerRow;
+    const int part = static_cast<int>(gid % kLanesPerRow);
+    float s = 0.0f;
+    if (row < rows) {
+        float a[8], b[8];
+        load8(o + row * D + part * 8, a);
+        load8(dout + row * D + part * 8, b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += a[e] * b[e];
+    }
+#pragma unroll
+    for (int off = kLanesPerRow / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanesPerRow);
+    if (row < rows && part == 0) stat[row] = s;
+}
+
+struct BwdArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* dout;
+    const float* lse;
+    const float* stat;
+    void* dq;
+    void* dk;
+    void* dv;
+    int64_t heads, kv_heads, m, n;
+    int64_t diag;
+    float scale, scale_log2;
+    int causal;
+    int dq_bf16, dkv_bf16;
+    int blocks;  // key blocks (dK/dV kernel) or query blocks (dQ kernel) per head
+};
+
+// Rows [row0, row0+rows) of a [*, D] matrix -> LDS [rows][DP] through registers (rows past
+// `limit` clamp to limit-1; columns >= D are zero).
+template <int D, int DP, int ROWS>
+struct RowsLoader {
+    static constexpr int kChunks = DP / 8;
+    static constexpr int kPerThread = ROWS * kChunks / kThreads;
+    u32x4_t r[kPerThread];
+    __device__ __forceinline__ void load(const uint16_t* base, int64_t row0, int64_t limit, int t) {
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+            const int idx = t + i * kThreads;
+            const int row = idx / kChunks, chunk = idx % kChunks;
+            int64_t gr = row0 + row;
+            gr = gr < limit ? gr : limit - 1;
+            r[i] = (chunk * 8 < D) ? *reinterpret_cast<const u32x4_t*>(base + gr * D + chunk * 8) : u32x4_t{0, 0, 0, 0};
+        }
+    }
+    __device__ __forceinline__ void store(uint16_t* tile, int t) const {
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+            const int idx = t + i * kThreads;
+            const int row = idx / kChunks, chunk = idx % kChunks;
+            *reinterpret_cast<u32x4_t*>(tile + tile_off<DP>(row, chunk * 8)) = r[i];
+        }
+    }
+};
+
+// One lane's MFMA operand of 8 head-dim values of row `row` (d = 16*s + 8*lg .. +7).
+template <int D, int KS>
+__device__ __forceinline__ void load_row_operand(const uint16_t* base, int64_t row, int lg, bf16x8_t (&f)[KS]) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int d0 = 16 * s + 8 * lg;
+        f[s] = d0 < D ? *reinterpret_cast<const bf16x8_t*>(base + row * D + d0)
+                      : __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void store_row4(void* base, bool bf16_out, int64_t row, int d, const float (&v)[4]) {
+    if (d >= D) return;
+    if (bf16_out) {
+        u32x2_t w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(base) + row * D + d) = w;
+    } else {
+        f32x4_t w = {v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4_t*>(static_cast<float*>(base) + row * D + d) = w;
+    }
+}
+
+constexpr int kQStep = 64;    // queries per step of the dK/dV kernel
+constexpr int kKBlock = 128;  // keys per dK/dV workgroup (4 waves x 32)
+
+// dK and dV of 128 keys of one (batch, KV head): loop over the group's query heads (in head
+// order) and over 64-query steps, accumulating in registers; no atomics.
+//   S = Q K^T and dP = dO V^T are computed with the queries as rows and this wave's 32 keys
+//   as columns, so the accumulators (keys in lanes) are directly the B operands of
+//   dV^T += dO^T P and dK^T += Q^T dS, whose A operands (dO^T, Q^T) come from the row-major
+//   Q and dO tiles through transposing LDS reads.
+template <int D>
+__global__ void __launch_bounds__(kThreads, 1)
+attn_bwd_dkdv(BwdArgs a) {
+    constexpr int DP = D < 32 ? 32 : D;
+    constexpr int KS = DP / 16;
+    constexpr int DT = DP / 32;
+    __shared__ __attribute__((aligned(16))) uint16_t tiles[2][2][kQStep * DP];  // [buf][Q, dO]
+    __shared__ __attribute__((aligned(16))) float stats[2][2][kQStep];         // [buf][lse*log2e, rowstat]
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lq = lane & 31, lg = lane >> 5;
+    const int bkv = blockIdx.x / a.blocks;  // b * kv_heads + kvh
+    const int nb = blockIdx.x % a.blocks;
+    const int64_t b = bkv / a.kv_heads;
+    const int64_t group = a.heads / a.kv_heads;
+    const int64_t kvh = bkv % a.kv_heads;
+    const int64_t n0 = static_cast<int64_t>(nb) * kKBlock;
+    const int64_t n0w = n0 + wave * 32;
+    const int64_t my_key = n0w + lq;
+    const uint16_t* K = a.k + (static_cast<int64_t>(bkv) * a.n) * D;
+    const uint16_t* V = a.v + (static_cast<int64_t>(bkv) * a.n) * D;
+
+    bf16x8_t kf[KS], vf[KS];
+    {
+        const int64_t kr = my_key < a.n ? my_key : a.n - 1;
+        load_row_operand<D, KS>(K, kr, lg, kf);
+        load_row_operand<D, KS>(V, kr, lg, vf);
+    }
+    f32x16_t dk[DT], dv[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            dk[i][v] = 0.0f;
+            dv[i][v] = 0.0f;
+        }
+
+    // query steps that can see a key of this block: causal -> from the block's first key on
+    int64_t qfirst = 0;
+    if (a.causal) {
+        qfirst = n0 - a.diag;
+        qfirst = qfirst < 0 ? 0 : qfirst;
+    }
+    const int step0 = static_cast<int>(qfirst / kQStep);
+    const int nsteps_head = qfirst < a.m ? static_cast<int>((a.m + kQStep - 1) / kQStep) - step0 : 0;
+    const int total = nsteps_head * static_cast<int>(group);
+
+    RowsLoader<D, DP, kQStep> lq_ld, ldo;
+    float st_lse = 0.0f, st_stat = 0.0f;  // thread t < 64 prefetches row t's statistics
+    auto load_step = [&](int it) {
+        const int64_t h = kvh * group + it / nsteps_head;
+        const int64_t q0 = static_cast<int64_t>(step0 + it % nsteps_head) * kQStep;
+        const int64_t bh = b * a.heads + h;
+        lq_ld.load(a.q + bh * a.m * D, q0, a.m, t);
+        ldo.load(a.dout + bh * a.m * D, q0, a.m, t);
+        if (t < kQStep) {
+            const int64_t qi = q0 + t < a.m ? q0 + t : a.m - 1;
+            st_lse = a.lse[bh * a.m + qi] * kLog2e;
+            st_stat = a.stat[bh * a.m + qi];
+        }
+    };
+    auto store_step = [&](int buf) {
+        lq_ld.store(tiles[buf][0], t);
+        ldo.store(tiles[buf][1], t);
+        if (t < kQStep) {
+            stats[buf][0][t] = st_lse;
+            stats[buf][1][t] = st_stat;
+        }
+    };
+    if (total > 0) {
+        load_step(0);
+        store_step(0);
+        if (total > 1) load_step(1);
+    }
+    __syncthreads();
+
+    for (int it = 0; it < total; ++it) {
+        const int cur = it & 1;
+        const int64_t q0 = static_cast<int64_t>(step0 + it % nsteps_head) * kQStep;
+        const uint16_t* Qt = tiles[cur][0];
+        const uint16_t* Ot = tiles[cur][1];
+        const bool skip = a.causal && (n0w > q0 + kQStep - 1 + a.diag);
+        if (!skip) {
+            f32x16_t s[2], dp[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    s[qt][v] = 0.0f;
+                    dp[qt][v] = 0.0f;
+                }
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    s[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Qt, 32 * qt + lq, 2 * ks + lg),
+                                                                    kf[ks], s[qt], 0, 0, 0);
+                    dp[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Ot, 32 * qt + lq, 2 * ks + lg),
+                                                                     vf[ks], dp[qt], 0, 0, 0);
+                }
+            }
+            // P and dS; lane holds key my_key, queries q0 + 32*qt + 8*(v/4) + 4*lg + v%4
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int qi = 32 * qt + 8 * g4 + 4 * lg;
+                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&stats[cur][0][qi]);
+                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&stats[cur][1][qi]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int v = 4 * g4 + e;
+                        const int64_t query = q0 + qi + e;
+                        const bool vis = query < a.m && my_key < a.n && (!a.causal || my_key <= query + a.diag);
+                        const float p = vis ? fast_exp2(s[qt][v] * a.scale_log2 - l4[e]) : 0.0f;
+                        s[qt][v] = p;
+                        dp[qt][v] = a.scale * (p * (dp[qt][v] - d4[e]));
+                    }
+                }
+            // dV^T += dO^T P ; dK^T += Q^T dS  (k = 64 queries in 4 steps of 16)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8_t pb = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
+                const bf16x8_t sb = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
+                const int kb0 = 16 * ks + 4 * lg;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Ot, lane, kb0, kb0 + 8, 32 * dt),
+                                                                     pb, dv[dt], 0, 0, 0);
+                    dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Qt, lane, kb0, kb0 + 8, 32 * dt),
+                                                                     sb, dk[dt], 0, 0, 0);
+                }
+            }
+        }
+        if (it + 1 < total) {
+            store_step(cur ^ 1);
+            if (it + 2 < total) load_step(it + 2);
+        }
+        __syncthreads();
+    }
+
+    if (my_key < a.n) {
+        const int64_t row = static_cast<int64_t>(bkv) * a.n + my_key;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * dt + 8 * g4 + 4 * lg;
+                const float kv4[4] = {dk[dt][4 * g4], dk[dt][4 * g4 + 1], dk[dt][4 * g4 + 2], dk[dt][4 * g4 + 3]};
+                const float vv4[4] = {dv[dt][4 * g4], dv[dt][4 * g4 + 1], dv[dt][4 * g4 + 2], dv[dt][4 * g4 + 3]};
+                store_row4<D>(a.dk, a.dkv_bf16, row, d, kv4);
+                store_row4<D>(a.dv, a.dkv_bf16, row, d, vv4);
+            }
+    }
+}
+
+// dQ of 128 queries of one (batch, head), looping over 64-key tiles up to the diagonal:
+// S^T = K Q^T and dP^T = V dO^T with keys as rows (each lane owns one query, so the softmax
+// row statistics are per-lane scalars), dS^T is the B operand of dQ^T += K^T dS^T with K^T
+// read from the row-major K tile through transposing LDS reads.
+template <int D>
+__global__ void __launch_bounds__(kThreads, 1)
+attn_bwd_dq(BwdArgs a) {
+    constexpr int DP = D < 32 ? 32 : D;
+    constexpr int KS = DP / 16;
+    constexpr int DT = DP / 32;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBlockN * DP];  // [buf][K, V]
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lq = lane & 31, lg = lane >> 5;
+    const int bh = blockIdx.x / a.blocks;
+    const int mb = a.blocks - 1 - (blockIdx.x % a.blocks);
+    const int64_t b = bh / a.heads, h = bh % a.heads;
+    const int64_t kvh = h / (a.heads / a.kv_heads);
+    const uint16_t* K = a.k + ((b * a.kv_heads + kvh) * a.n) * D;
+    const uint16_t* V = a.v + ((b * a.kv_heads + kvh) * a.n) * D;
+    const int64_t q0 = static_cast<int64_t>(mb) * kBlockM;
+    const int64_t q0w = q0 + wave * 32;
+    const int64_t my_q = q0w + lq;
+    const int64_t qr = my_q < a.m ? my_q : a.m - 1;
+
+    bf16x8_t qf[KS], of[KS];
+    load_row_operand<D, KS>(a.q + static_cast<int64_t>(bh) * a.m * D, qr, lg, qf);
+    load_row_operand<D, KS>(a.dout + static_cast<int64_t>(bh) * a.m * D, qr, lg, of);
+    const float lse2 = a.lse[static_cast<int64_t>(bh) * a.m + qr] * kLog2e;
+    const float rstat = a.stat[static_cast<int64_t>(bh) * a.m + qr];
+
+    f32x16_t dq[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dq[i][v] = 0.0f;
+
+    int64_t kv_end = a.n;
+    if (a.causal) {
+        const int64_t last = q0 + kBlockM - 1 + a.diag;
+        kv_end = last + 1 < kv_end ? last + 1 : kv_end;
+    }
+    const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
+
+    TileLoader<D, DP> lk, lv;
+    if (ntiles > 0) {
+        lk.load(K, 0, a.n, t);
+        lv.load(V, 0, a.n, t);
+        lk.store(lds[0][0], t);
+        lv.store(lds[0][1], t);
+        if (ntiles > 1) {
+            lk.load(K, kBlockN, a.n, t);
+            lv.load(V, kBlockN, a.n, t);
+        }
+    }
+    __syncthreads();
+
+    for (int j = 0; j < ntiles; ++j) {
+        const int cur = j & 1;
+        const int64_t kv0 = static_cast<int64_t>(j) * kBlockN;
+        const uint16_t* Kt = lds[cur][0];
+        const uint16_t* Vt = lds[cur][1];
+        const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
+        if (!skip) {
+            f32x16_t s[2], dp[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    s[tt][v] = 0.0f;
+                    dp[tt][v] = 0.0f;
+                }
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Kt, 32 * tt + lq, 2 * ks + lg),
+                                                                    qf[ks], s[tt], 0, 0, 0);
+                    dp[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Vt, 32 * tt + lq, 2 * ks + lg),
+                                                                     of[ks], dp[tt], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t key = kv0 + 32 * tt + (v >> 2) * 8 + lg * 4 + (v & 3);
+                    const bool vis = my_q < a.m && key < a.n && (!a.causal || key <= my_q + a.diag);
+                    const float p = vis ? fast_exp2(s[tt][v] * a.scale_log2 - lse2) : 0.0f;
+                    dp[tt][v] = a.scale * (p * (dp[tt][v] - rstat));
+                }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8_t sb = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
+                const int kb0 = 16 * ks + 4 * lg;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+                    dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Kt, lane, kb0, kb0 + 8, 32 * dt),
+                                                                     sb, dq[dt], 0, 0, 0);
+            }
+        }
+        if (j + 1 < ntiles) {
+            lk.store(lds[cur ^ 1][0], t);
+            lv.store(lds[cur ^ 1][1], t);
+            if (j + 2 < ntiles) {
+                lk.load(K, kv0 + 2 * kBlockN, a.n, t);
+                lv.load(V, kv0 + 2 * kBlockN, a.n, t);
+            }
+        }
+        __syncthreads();
+    }
+
+    if (my_q < a.m) {
+        const int64_t row = static_cast<int64_t>(bh) * a.m + my_q;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float v4[4] = {dq[dt][4 * g4], dq[dt][4 * g4 + 1], dq[dt][4 * g4 + 2], dq[dt][4 * g4 + 3]};
+                store_row4<D>(a.dq, a.dq_bf16, row, 32 * dt + 8 * g4 + 4 * lg, v4);
+            }
+    }
+}
+
+template <int D>
+hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const void* v, const void* o,
+                      const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv, int dkv_bf16,
+                      float* stat, hipStream_t s) {
+    const int64_t rows = sh.batch * sh.heads * sh.m;
+    constexpr int lanes = D / 8;
+    const int64_t threads = rows * lanes;
+    hipLaunchKernelGGL((attn_bwd_rowstat<D>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), stat, rows);
+    BwdArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.k = static_cast<const uint16_t*>(k);
+    a.v = static_cast<const uint16_t*>(v);
+    a.dout = static_cast<const uint16_t*>(dout);
+    a.lse = lse;
+    a.stat = stat;
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    a.heads = sh.heads;
+    a.kv_heads = sh.kv_heads;
+    a.m = sh.m;
+    a.n = sh.n;
+    a.diag = clamp_diag(sh);
+    a.scale = sh.scale;
+    a.scale_log2 = sh.scale * kLog2e;
+    a.causal = sh.causal;
+    a.dq_bf16 = dq_bf16;
+    a.dkv_bf16 = dkv_bf16;
+    a.blocks = static_cast<int>((sh.n + kKBlock - 1) / kKBlock);
+    hipLaunchKernelGGL((attn_bwd_dkdv<D>), dim3(static_cast<unsigned>(sh.batch * sh.kv_heads * a.blocks)),
+                       dim3(kThreads), 0, s, a);
+    a.blocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
+    hipLaunchKernelGGL((attn_bwd_dq<D>), dim3(static_cast<unsigned>(sh.batch * sh.heads * a.blocks)), dim3(kThreads),
+                       0, s, a);
+    return hipGetLastError();
+}
+
 }  // namespace
 
-size_t attention_bwd_workspace_bytes(const AttnShape&) { return 0; }
+size_t attention_bwd_workspace_bytes(const AttnShape& sh) {
+    return static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float);
+}
 
 hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o, float* lse,
                              hipStream_t s) {
@@ -333,9 +751,17 @@ hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, 
     }
 }
 
-hipError_t attention_backward(const AttnShape&, const void*, const void*, const void*, const void*, const float*,
-                              const void*, void*, int, void*, void*, int, void*, hipStream_t) {
-    return hipErrorNotSupported;
+hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k, const void* v, const void* o,
+                              const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv,
+                              int dkv_bf16, void* workspace, hipStream_t s) {
+    float* stat = static_cast<float*>(workspace);
+    switch (sh.d) {
+        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
+        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
+        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
+        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace hk

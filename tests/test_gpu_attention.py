@@ -111,3 +111,96 @@ def test_forward_rejects_bad_shapes():
     k_t, _ = randn_bf16((1, 2, 64, 64), seed=2)
     with pytest.raises(HkError):
         HipRuntime.attention_forward(q_t, k_t, k_t, 0.125, True)  # 3 % 2 != 0
+
+
+# ---------------------------------------------------------------------------- backward
+
+def run_fwd_bwd(q_t, k_t, v_t, do_t, scale, causal, qs=0, ks=0, grad_dtype=torch.float32):
+    o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, scale, causal, qs, ks)
+    dq, dk, dv = HipRuntime.attention_backward(q_t, k_t, v_t, o, lse, do_t, scale, causal, qs, ks, grad_dtype=grad_dtype)
+    return o, lse, dq, dk, dv
+
+
+@pytest.mark.parametrize("case", GQA_CASES[1:])
+def test_backward_reference_gqa_cases(golden, case):
+    """The reference's GQA gradient cases (grouped_attention_tensor.rs:74-97, d = 16) at its
+    tolerance 2e-3 + 3e-3|b|, against the oracle (which keeps its BF16 rounding points)."""
+    g = golden_case(golden, case)
+    causal = case.endswith("c1")
+    n, m = g["k"].shape[2], g["q"].shape[2]
+    qs, ks = ((1 << 40) + n - m, 1 << 40) if causal else (0, 0)
+    _, _, dq, dk, dv = run_fwd_bwd(dev_bf16(g["q"]), dev_bf16(g["k"]), dev_bf16(g["v"]), dev_bf16(g["dy"]), 0.25,
+                                   causal, qs, ks)
+    ref = oracle.attention_f64(g["q"], g["k"], g["v"], g["dy"], scale=0.25, causal=causal, query_start=qs, key_start=ks)
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        close(host(got), ref[name], 2e-3, 3e-3, name)
+        if causal:  # torch-f64 autograd golden vectors of the reference's causal case
+            close(host(got), g[name], 2e-3, 3e-3, name + " vs golden")
+
+
+@pytest.mark.parametrize("n", [32, 256])
+def test_backward_orthogonal_closed_form(golden, n):
+    key = f"attnkat_orth_n{n}"
+    q, k, v, dy = (golden[key + s][:, None] for s in ("_q", "_k", "_v", "_dy"))
+    _, _, dq, dk, dv = run_fwd_bwd(dev_bf16(q), dev_bf16(k), dev_bf16(v), dev_bf16(dy), 0.25, False)
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        close(host(got)[:, 0], golden[key + "_" + name], 5e-4, 5e-4, name)
+
+
+@pytest.mark.parametrize("n", [32, 96])
+@pytest.mark.parametrize("cached", [0, 1])
+def test_backward_causal_closed_form(golden, n, cached):
+    key = f"attnkat_causal_n{n}_c{cached}"
+    v, dy, qs = golden[key + "_v"][:, None], golden[key + "_dy"][:, None], int(golden[key + "_qs"])
+    q = np.zeros((2, 1, 32, 16), np.float32)
+    k = np.zeros((2, 1, n, 16), np.float32)
+    _, _, dq, dk, dv = run_fwd_bwd(dev_bf16(q), dev_bf16(k), dev_bf16(v), dev_bf16(dy), 0.25, True, qs, 0)
+    close(host(dv)[:, 0], golden[key + "_dv"], 5e-4, 5e-4, "dV")
+    assert float(torch.max(torch.abs(dq))) < 1e-6 and float(torch.max(torch.abs(dk))) < 1e-6
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("m,n", [(256, 256), (200, 328), (64, 1000), (130, 130)])
+def test_backward_random_vs_oracle(d, causal, m, n):
+    h, hkv = 4, 2
+    q_t, q = randn_bf16((2, h, m, d), seed=d + m + 7)
+    k_t, k = randn_bf16((2, hkv, n, d), seed=d + n + 8)
+    v_t, v = randn_bf16((2, hkv, n, d), seed=d + n + 9)
+    do_t, do = randn_bf16((2, h, m, d), seed=d + m + 10)
+    qs = max(n - m, 0) if causal else 0
+    _, _, dq, dk, dv = run_fwd_bwd(q_t, k_t, v_t, do_t, d ** -0.5, causal, qs)
+    ref = oracle.attention_f64(q, k, v, do, scale=d ** -0.5, causal=causal, query_start=qs, magnitudes=True)
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        mag_ok(host(got), ref[name], ref[name + "_mag"], 1e-2, name)
+
+
+def test_backward_bf16_grads_and_determinism():
+    q_t, q = randn_bf16((1, 8, 192, 128), seed=51)
+    k_t, k = randn_bf16((1, 2, 192, 128), seed=52)
+    v_t, v = randn_bf16((1, 2, 192, 128), seed=53)
+    do_t, do = randn_bf16((1, 8, 192, 128), seed=54)
+    a = run_fwd_bwd(q_t, k_t, v_t, do_t, 128 ** -0.5, True, grad_dtype=torch.bfloat16)
+    b = run_fwd_bwd(q_t, k_t, v_t, do_t, 128 ** -0.5, True, grad_dtype=torch.bfloat16)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y), "attention must be deterministic"
+    ref = oracle.attention_f64(q, k, v, do, scale=128 ** -0.5, causal=True, magnitudes=True)
+    for name, got in zip(("dq", "dk", "dv"), a[2:]):
+        assert got.dtype == torch.bfloat16
+        mag_ok(host(got), ref[name], ref[name + "_mag"], 1e-2, name)
+
+
+def test_backward_c4_full_size_sampled():
+    """BASELINE config C4 backward: B4, S4096, Hq32/Hkv8, D128, causal; parity on batch 0 x KV
+    group 0 (the 4 query heads that share KV head 0) over all rows."""
+    B, H, HKV, S, D = 4, 32, 8, 4096, 128
+    q_t, _ = randn_bf16((B, H, S, D), seed=61)
+    k_t, _ = randn_bf16((B, HKV, S, D), seed=62)
+    v_t, _ = randn_bf16((B, HKV, S, D), seed=63)
+    do_t, _ = randn_bf16((B, H, S, D), seed=64)
+    _, _, dq, dk, dv = run_fwd_bwd(q_t, k_t, v_t, do_t, D ** -0.5, True)
+    ref = oracle.attention_f64(host(q_t[:1, :4]), host(k_t[:1, :1]), host(v_t[:1, :1]), host(do_t[:1, :4]),
+                               scale=D ** -0.5, causal=True, magnitudes=True)
+    mag_ok(host(dq[:1, :4]), ref["dq"], ref["dq_mag"], 1e-2, "dq")
+    mag_ok(host(dk[:1, :1]), ref["dk"], ref["dk_mag"], 1e-2, "dk")
+    mag_ok(host(dv[:1, :1]), ref["dv"], ref["dv_mag"], 1e-2, "dv")
