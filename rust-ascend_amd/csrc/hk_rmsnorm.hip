@@ -34,56 +34,6 @@ namespace {
 constexpr int kRowsThreads = 256;  // 4 waves per workgroup (forward)
 constexpr int kBwdThreads = 512;   // 8 waves per workgroup (backward)
 
-template <typename T, int MAXJ>
-__global__ void __launch_bounds__(kRowsThreads)
-rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y,
-             float* __restrict__ rstd, int64_t rows, int width, float eps) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int waves_per_block = blockDim.x >> 6;
-    const int chunks = width >> 3;
-    float wr[MAXJ][8];
-#pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c < chunks) load8(w + 8 * c, wr[j]);
-    }
-    const float inv_w = 1.0f / static_cast<float>(width);
-    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows;
-         row += static_cast<int64_t>(gridDim.x) * waves_per_block) {
-        const T* xr = x + row * width;
-        float v[MAXJ][8];
-#pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
-            if (c < chunks) load8(xr + 8 * c, v[j]);
-        }
-        float ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
-            if (c < chunks) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
-            }
-        }
-        ss = wave_sum(ss);
-        const float r = 1.0f / sqrtf(ss * inv_w + eps);
-        T* yr = y + row * width;
-#pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
-            if (c < chunks) {
-                float o[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = (v[j][e] * r) * wr[j][e];
-                store8(yr + 8 * c, o);
-            }
-        }
-        if (lane == 0) rstd[row] = r;
-    }
-}
-
 // Eight elements kept in their storage form between the two passes over a row
 // (4 VGPRs for BF16, 8 for F32) and widened to float on use.
 template <typename T> struct Raw8;
@@ -116,6 +66,55 @@ template <> struct Raw8<float> {
         }
     }
 };
+
+// One wavefront per row and one row per wavefront (no grid-stride loop): the row is held
+// in its storage form (32 VGPRs for a 4096-wide BF16 row), so the kernel runs at full
+// occupancy and every wave has its whole row of loads in flight at once; w is re-read per
+// row from L2 (16 KB, shared by every row).
+template <typename T, int MAXJ>
+__global__ void __launch_bounds__(kRowsThreads)
+rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y,
+             float* __restrict__ rstd, int64_t rows, int width, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int chunks = width >> 3;
+    const T* xr = x + row * width;
+    Raw8<T> xs[MAXJ];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) xs[j].load(xr + 8 * c);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+            float v[8];
+            xs[j].get(v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+        }
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss * (1.0f / static_cast<float>(width)) + eps);
+    T* yr = y + row * width;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+            float v[8], wv[8], o[8];
+            xs[j].pin();
+            xs[j].get(v);
+            load8(w + 8 * c, wv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (v[e] * r) * wv[e];
+            store8(yr + 8 * c, o);
+        }
+    }
+    if (lane == 0) rstd[row] = r;
+}
 
 template <typename T, int MAXJ>
 __global__ void __launch_bounds__(kBwdThreads)
@@ -207,23 +206,26 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
     for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = p_lds[c];
 }
 
-// dw[c] = sum over p of partial[p][c], p ascending within each of 8 slices, then the
-// slices in order: fixed order for a given (parts, width). The (at most 512) partials are
-// added in double so this stage adds no rounding beyond the final conversion to F32.
-__global__ void __launch_bounds__(256)
+// dw[c] = sum over p of partial[p][c]: a workgroup covers 64 columns with 16 slices of
+// partial rows (p = slice, slice+16, ... ascending), and the 16 slice sums are then added in
+// slice order: a fixed order for given (parts, width). Sums are kept in double, so this stage
+// adds no rounding beyond the final conversion to F32.
+__global__ void __launch_bounds__(1024)
 sum_partials(const float* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
-    __shared__ double red[8][33];
-    const int col = blockIdx.x * 32 + (threadIdx.x & 31);
-    const int slice = threadIdx.x >> 5;
+    __shared__ double red[16][64];
+    const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int slice = threadIdx.x >> 6;
     double s = 0.0;
-    if (col < width)
-        for (int p = slice; p < parts; p += 8) s += static_cast<double>(partial[static_cast<int64_t>(p) * width + col]);
-    red[slice][threadIdx.x & 31] = s;
+    if (col < width) {
+#pragma unroll 8
+        for (int p = slice; p < parts; p += 16) s += static_cast<double>(partial[static_cast<int64_t>(p) * width + col]);
+    }
+    red[slice][threadIdx.x & 63] = s;
     __syncthreads();
     if (slice == 0 && col < width) {
         double t = red[0][threadIdx.x];
 #pragma unroll
-        for (int i = 1; i < 8; ++i) t += red[i][threadIdx.x];
+        for (int i = 1; i < 16; ++i) t += red[i][threadIdx.x];
         dw[col] = static_cast<float>(t);
     }
 }
@@ -313,8 +315,8 @@ int grid_for_rows(int64_t rows, int waves_per_block, int cap) {
 template <typename T, int MAXJ>
 void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_t rows, int width,
                      float eps, hipStream_t s) {
-    const int grid = grid_for_rows(rows, kRowsThreads / 64, 2048);
-    hipLaunchKernelGGL((rms_fwd_fast<T, MAXJ>), dim3(grid), dim3(kRowsThreads), 0, s,
+    const int64_t grid = (rows + kRowsThreads / 64 - 1) / (kRowsThreads / 64);  // one row per wave
+    hipLaunchKernelGGL((rms_fwd_fast<T, MAXJ>), dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads), 0, s,
                        static_cast<const T*>(x), w, static_cast<T*>(y), rstd, rows, width, eps);
 }
 
@@ -365,7 +367,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
         else if (chunks_per_lane <= 2) launch_bwd_fast<T, 2>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
         else if (chunks_per_lane <= 4) launch_bwd_fast<T, 4>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
         else launch_bwd_fast<T, 8>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        hipLaunchKernelGGL(sum_partials, dim3((width + 31) / 32), dim3(256), 0, s, workspace, parts, (int)width, dw);
+        hipLaunchKernelGGL(sum_partials, dim3((width + 63) / 64), dim3(1024), 0, s, workspace, parts, (int)width, dw);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_bwd_dx_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
@@ -376,7 +378,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
         hipLaunchKernelGGL((rms_bwd_dw_general<T>), dim3((width + 255) / 256, parts), dim3(256), 0, s,
                            static_cast<const T*>(x), static_cast<const T*>(dy), rstd, workspace, rows,
                            width, per);
-        hipLaunchKernelGGL(sum_partials, dim3((width + 31) / 32), dim3(256), 0, s, workspace, parts, (int)width, dw);
+        hipLaunchKernelGGL(sum_partials, dim3((width + 63) / 64), dim3(1024), 0, s, workspace, parts, (int)width, dw);
     }
     return hipGetLastError();
 }
