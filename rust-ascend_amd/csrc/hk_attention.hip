@@ -40,6 +40,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kBlockM = 128;  // query rows per forward workgroup (4 waves x 32)
 constexpr int kBlockN = 64;   // keys per K/V tile
 constexpr int kThreads = 256;
+constexpr int kXcds = 8;     // accelerator complex dies; workgroups are dispatched round-robin over them
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
@@ -47,11 +48,15 @@ typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 // 16-byte chunk swizzle of a tile row: keeps the 32-row MFMA operand reads, the 4-row
 // transposing reads and the row-contiguous tile writes free of LDS bank conflicts.
 template <int D>
-__device__ __forceinline__ int tile_off(int row, int col) {  // element offset in a [rows][D] tile
+__device__ __forceinline__ int tile_swz(int row) {  // XOR applied to the 16-byte chunk index of a row
     constexpr int chunks = D / 8;
     constexpr int mask = chunks - 1 < 7 ? chunks - 1 : 7;
-    const int f = (((row & 3) << 1) | ((row >> 2) & 1)) & mask;
-    return row * D + ((((col >> 3) ^ f)) << 3) + (col & 7);
+    return (((row & 3) << 1) | ((row >> 2) & 1)) & mask;
+}
+
+template <int D>
+__device__ __forceinline__ int tile_off(int row, int col) {  // element offset in a [rows][D] tile
+    return row * D + ((((col >> 3) ^ tile_swz<D>(row))) << 3) + (col & 7);
 }
 
 // 16 bytes at (row, 8*chunk) of a swizzled tile.
@@ -85,6 +90,18 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const f32x16_t& a, int base) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Loop-invariant operands loaded from global memory before a tile loop are passed through an
+// empty asm: the one wait for their loads then happens here, before the loop. Otherwise the
+// compiler's wait-count insertion cannot prove them complete inside the loop, and because
+// loads complete in order, its wait for them also waits for the K/V prefetch loads issued one
+// iteration earlier, exposing a full HBM round trip per tile.
+template <int N>
+__device__ __forceinline__ void settle(bf16x8_t (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+__device__ __forceinline__ void settle(float& v) { asm volatile("" : "+v"(v)); }
 
 struct FwdArgs {
     const uint16_t* q;
@@ -126,7 +143,95 @@ struct TileLoader {
     }
 };
 
+// S^T = K Q^T for one 64-key tile and this wave's 32 queries (keys in rows, one query per lane).
+template <int DP, int KS>
+__device__ __forceinline__ void tile_scores(const uint16_t* Kt, const bf16x8_t (&qf)[KS], int lq, int lg,
+                                            f32x16_t (&s)[2]) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Kt, 32 * tt + lq, 2 * ks + lg), qf[ks],
+                                                            s[tt], 0, 0, 0);
+    }
+}
+
+// Online-softmax update of one tile's raw scores (masked, when MASK, to the keys visible to
+// this lane's query), then O^T += V^T P^T. c = |scale|*log2(e) > 0 (a negative scale is folded
+// into Q), so the scaled row max is c times the raw max and p = 2^(c*s - m) is one FMA + exp2.
+//
+// The running max m is allowed to lag the true max by up to kStaleMax (base-2 units): O, l and
+// m are only rescaled when some row of the wave sees its max grow by more than that, so most
+// tiles skip the 64-register rescale of O. Then p <= 2^kStaleMax, well inside BF16/F32 range,
+// and O / l and lse = m + log2(l) are the same quantities as with an exact running max.
+constexpr float kStaleMax = 8.0f;
+
+template <int DP, int DT>
+__device__ __forceinline__ void tile_update(f32x16_t (&s)[2], const uint16_t* Vt, int lane, float c, bool mask,
+                                            int64_t kv0, int64_t key_limit, float& m_run, float& l_run,
+                                            f32x16_t (&o)[DT]) {
+    const int lg = lane >> 5;
+    // key kv0 + 32*tt + 8*(v/4) + 4*lg + v%4 is visible iff it is <= key_limit, i.e. iff
+    // 32*tt + 8*(v/4) + v%4 <= rel (a compile-time constant against one register)
+    int64_t rel64 = key_limit - kv0 - 4 * lg;
+    rel64 = rel64 < -1 ? -1 : (rel64 > kBlockN ? kBlockN : rel64);
+    const int rel = static_cast<int>(rel64);
+    float mt = -INFINITY;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            float x = s[tt][v];
+            if (mask) {
+                x = 32 * tt + (v >> 2) * 8 + (v & 3) <= rel ? x : -INFINITY;
+                s[tt][v] = x;
+            }
+            mt = fmaxf(mt, x);
+        }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * c;
+    if (__any(mt > m_run + kStaleMax)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < DT; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
+    }
+    const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
+    float ls = 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float p = fast_exp2(__builtin_fmaf(s[tt][v], c, neg_m));
+            s[tt][v] = p;
+            ls += p;
+        }
+    l_run += ls;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8_t pb = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
+        const int kb0 = 16 * ks + 4 * lg;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Vt, lane, kb0, kb0 + 8, 32 * dt), pb, o[dt],
+                                                            0, 0, 0);
+    }
+}
+
 // D is the head dim in memory; the kernel works on DP = max(D, 32) (zero-padded columns).
+//
+// Tile pipeline: iteration j issues the scores of tile j+1 (from K_{j+1} in LDS) and then
+// runs the softmax and P.V of tile j (V_j in LDS), so the MFMAs of the next tile's scores are in
+// flight while the current tile's exponentials run. K therefore stays one tile ahead of V:
+// at the end of iteration j the registers prefetched one iteration earlier (K_{j+2}, V_{j+1})
+// are stored into the LDS buffers last read in iteration j-1, the loads of K_{j+3}, V_{j+2} are
+// issued, and one barrier closes the iteration. Tiles fully visible to every row of the
+// workgroup run without mask arithmetic; only the diagonal / ragged tail tiles are masked.
 template <int D>
 __global__ void __launch_bounds__(kThreads, 2)
 attn_fwd(FwdArgs a) {
@@ -137,24 +242,40 @@ attn_fwd(FwdArgs a) {
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int lq = lane & 31, lg = lane >> 5;
-    const int bh = blockIdx.x / a.mblocks;
-    const int mb = a.mblocks - 1 - (blockIdx.x % a.mblocks);  // heaviest causal blocks first
-    const int64_t b = bh / a.heads, h = bh % a.heads;
-    const int64_t kvh = h / (a.heads / a.kv_heads);
+    // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so that each XCD
+    // runs a contiguous range of the logical order (KV head group, query block heaviest first,
+    // query head in the group). The workgroups resident on one XCD then share one K/V head, which
+    // stays in that XCD's L2.
+    const int nwg = static_cast<int>(gridDim.x), xcd = static_cast<int>(blockIdx.x) % kXcds;
+    const int per_xcd = nwg / kXcds, extra = nwg % kXcds;
+    const int logical = xcd * per_xcd + (xcd < extra ? xcd : extra) + static_cast<int>(blockIdx.x) / kXcds;
+    const int group_heads = static_cast<int>(a.heads / a.kv_heads);
+    const int per_group = a.mblocks * group_heads;
+    const int grp = logical / per_group, in_grp = logical % per_group;
+    const int mb = a.mblocks - 1 - in_grp / group_heads;  // heaviest causal blocks first
+    const int64_t b = grp / a.kv_heads, kvh = grp % a.kv_heads;
+    const int64_t h = kvh * group_heads + in_grp % group_heads;
+    const int64_t bh = b * a.heads + h;
     const uint16_t* Q = a.q + (bh * a.m) * D;
     const uint16_t* K = a.k + ((b * a.kv_heads + kvh) * a.n) * D;
     const uint16_t* V = a.v + ((b * a.kv_heads + kvh) * a.n) * D;
     const int64_t q0 = static_cast<int64_t>(mb) * kBlockM;
-    const int64_t q0w = q0 + wave * 32;
-    const int64_t my_q = q0w + lq;
+    const int64_t my_q = q0 + wave * 32 + lq;
 
-    // keys this workgroup needs: [0, kv_end)
-    int64_t kv_end = a.n;
+    // keys this workgroup needs: [0, kv_end); tiles [0, nfull) are visible to all its rows
+    int64_t kv_end = a.n, full_end = a.n;
     if (a.causal) {
-        const int64_t last = q0 + kBlockM - 1 + a.diag;  // last visible key of the block's last row
+        const int64_t last = q0 + kBlockM - 1 + a.diag;  // last key visible to the block's last row
         kv_end = last + 1 < kv_end ? last + 1 : kv_end;
+        const int64_t first = q0 + a.diag + 1;            // keys [0, first) are visible to its first row
+        full_end = first < full_end ? first : full_end;
     }
     const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
+    int nfull = full_end > 0 ? static_cast<int>(full_end / kBlockN) : 0;
+    nfull = nfull < ntiles ? nfull : ntiles;
+    // the last key this lane's query may see (causal and bounds)
+    int64_t key_limit = a.n - 1;
+    if (a.causal) key_limit = my_q + a.diag < key_limit ? my_q + a.diag : key_limit;
 
     // Q of this lane's query as the B operand: d = 16*s + 8*lg .. +7
     bf16x8_t qf[KS];
@@ -167,6 +288,15 @@ attn_fwd(FwdArgs a) {
                            : __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
         }
     }
+    // c = |scale| log2(e); a negative scale flips the sign of Q instead
+    float c = a.scale_log2;
+    if (c < 0.0f) {
+        c = -c;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            qf[s] = __builtin_bit_cast(bf16x8_t, __builtin_bit_cast(u32x4_t, qf[s]) ^ 0x80008000u);
+    }
+    settle(qf);
 
     f32x16_t o[DT];
 #pragma unroll
@@ -188,69 +318,18 @@ attn_fwd(FwdArgs a) {
     }
     __syncthreads();
 
+    // Tile j is read from buffer j&1 while tile j+1 waits in registers (stored into the other
+    // buffer at the end of the iteration) and tile j+2 is being fetched.
+    const int64_t q0w = q0 + wave * 32;
     for (int j = 0; j < ntiles; ++j) {
         const int cur = j & 1;
         const int64_t kv0 = static_cast<int64_t>(j) * kBlockN;
-        const uint16_t* Kt = lds[cur][0];
-        const uint16_t* Vt = lds[cur][1];
         // this wave's rows see no key of this tile -> skip (still takes part in the barriers)
         const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
         if (!skip) {
             f32x16_t s[2];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Kt, 32 * tt + lq, 2 * ks + lg),
-                                                                    qf[ks], s[tt], 0, 0, 0);
-            }
-            // scale, mask, tile max
-            const bool need_mask = (kv0 + kBlockN > a.n) || (a.causal && kv0 + kBlockN - 1 > q0w + a.diag);
-            float mt = -INFINITY;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    float x = s[tt][v] * a.scale_log2;
-                    if (need_mask) {
-                        const int64_t key = kv0 + 32 * tt + (v >> 2) * 8 + lg * 4 + (v & 3);
-                        const bool vis = key < a.n && (!a.causal || key <= my_q + a.diag);
-                        x = vis ? x : -INFINITY;
-                    }
-                    s[tt][v] = x;
-                    mt = fmaxf(mt, x);
-                }
-            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-            const float m_new = fmaxf(m_run, mt);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = fast_exp2(m_run - m_use);
-            float ls = 0.0f;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float p = fast_exp2(s[tt][v] - m_use);
-                    s[tt][v] = p;
-                    ls += p;
-                }
-            l_run = l_run * alpha + ls;
-            m_run = m_new;
-#pragma unroll
-            for (int i = 0; i < DT; ++i)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) o[i][v] *= alpha;
-            // O^T += V^T P^T over the tile's 64 keys (4 k-steps of 16)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8_t pb = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
-                const int kb0 = 16 * ks + 4 * lg;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Vt, lane, kb0, kb0 + 8, 32 * dt),
-                                                                    pb, o[dt], 0, 0, 0);
-            }
+            tile_scores<DP, KS>(lds[cur][0], qf, lq, lg, s);
+            tile_update<DP, DT>(s, lds[cur][1], lane, c, j >= nfull, kv0, key_limit, m_run, l_run, o);
         }
         if (j + 1 < ntiles) {
             lk.store(lds[cur ^ 1][0], t);
@@ -448,6 +527,8 @@ attn_bwd_dkdv(BwdArgs a) {
         load_row_operand<D, KS>(K, kr, lg, kf);
         load_row_operand<D, KS>(V, kr, lg, vf);
     }
+    settle(kf);
+    settle(vf);
     f32x16_t dk[DT], dv[DT];
 #pragma unroll
     for (int i = 0; i < DT; ++i)
@@ -602,8 +683,12 @@ attn_bwd_dq(BwdArgs a) {
     bf16x8_t qf[KS], of[KS];
     load_row_operand<D, KS>(a.q + static_cast<int64_t>(bh) * a.m * D, qr, lg, qf);
     load_row_operand<D, KS>(a.dout + static_cast<int64_t>(bh) * a.m * D, qr, lg, of);
-    const float lse2 = a.lse[static_cast<int64_t>(bh) * a.m + qr] * kLog2e;
-    const float rstat = a.stat[static_cast<int64_t>(bh) * a.m + qr];
+    float lse2 = a.lse[static_cast<int64_t>(bh) * a.m + qr] * kLog2e;
+    float rstat = a.stat[static_cast<int64_t>(bh) * a.m + qr];
+    settle(qf);
+    settle(of);
+    settle(lse2);
+    settle(rstat);
 
     f32x16_t dq[DT];
 #pragma unroll
