@@ -103,6 +103,15 @@ __device__ __forceinline__ void settle(bf16x8_t (&v)[N]) {
 }
 __device__ __forceinline__ void settle(float& v) { asm volatile("" : "+v"(v)); }
 
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2. Renumbering
+// blockIdx so that each XCD runs one contiguous range of a logical order lets a kernel place
+// the workgroups that share operands on the same XCD.
+__device__ __forceinline__ int xcd_logical() {
+    const int nwg = static_cast<int>(gridDim.x), id = static_cast<int>(blockIdx.x);
+    const int xcd = id % kXcds, per_xcd = nwg / kXcds, extra = nwg % kXcds;
+    return xcd * per_xcd + (xcd < extra ? xcd : extra) + id / kXcds;
+}
+
 struct FwdArgs {
     const uint16_t* q;
     const uint16_t* k;
@@ -242,13 +251,9 @@ attn_fwd(FwdArgs a) {
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int lq = lane & 31, lg = lane >> 5;
-    // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so that each XCD
-    // runs a contiguous range of the logical order (KV head group, query block heaviest first,
-    // query head in the group). The workgroups resident on one XCD then share one K/V head, which
-    // stays in that XCD's L2.
-    const int nwg = static_cast<int>(gridDim.x), xcd = static_cast<int>(blockIdx.x) % kXcds;
-    const int per_xcd = nwg / kXcds, extra = nwg % kXcds;
-    const int logical = xcd * per_xcd + (xcd < extra ? xcd : extra) + static_cast<int>(blockIdx.x) / kXcds;
+    // logical order: KV head group, query block heaviest first, query head in the group -- the
+    // workgroups resident on one XCD share one K/V head, which stays in that XCD's L2
+    const int logical = xcd_logical();
     const int group_heads = static_cast<int>(a.heads / a.kv_heads);
     const int per_group = a.mblocks * group_heads;
     const int grp = logical / per_group, in_grp = logical % per_group;
@@ -510,8 +515,11 @@ attn_bwd_dkdv(BwdArgs a) {
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int lq = lane & 31, lg = lane >> 5;
-    const int bkv = blockIdx.x / a.blocks;  // b * kv_heads + kvh
-    const int nb = blockIdx.x % a.blocks;
+    // logical order: (batch, KV head), key block heaviest first -- the workgroups resident on
+    // one XCD read the same Q / dO heads
+    const int logical = xcd_logical();
+    const int bkv = logical / a.blocks;  // b * kv_heads + kvh
+    const int nb = logical % a.blocks;
     const int64_t b = bkv / a.kv_heads;
     const int64_t group = a.heads / a.kv_heads;
     const int64_t kvh = bkv % a.kv_heads;
@@ -669,10 +677,16 @@ attn_bwd_dq(BwdArgs a) {
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int lq = lane & 31, lg = lane >> 5;
-    const int bh = blockIdx.x / a.blocks;
-    const int mb = a.blocks - 1 - (blockIdx.x % a.blocks);
-    const int64_t b = bh / a.heads, h = bh % a.heads;
-    const int64_t kvh = h / (a.heads / a.kv_heads);
+    // same logical order as the forward kernel: KV head group, query block heaviest first,
+    // query head in the group
+    const int logical = xcd_logical();
+    const int group_heads = static_cast<int>(a.heads / a.kv_heads);
+    const int per_group = a.blocks * group_heads;
+    const int grp = logical / per_group, in_grp = logical % per_group;
+    const int mb = a.blocks - 1 - in_grp / group_heads;
+    const int64_t b = grp / a.kv_heads, kvh = grp % a.kv_heads;
+    const int64_t h = kvh * group_heads + in_grp % group_heads;
+    const int64_t bh = b * a.heads + h;
     const uint16_t* K = a.k + ((b * a.kv_heads + kvh) * a.n) * D;
     const uint16_t* V = a.v + ((b * a.kv_heads + kvh) * a.n) * D;
     const int64_t q0 = static_cast<int64_t>(mb) * kBlockM;
