@@ -157,14 +157,16 @@ template <int DP, int KS>
 __device__ __forceinline__ void tile_scores(const uint16_t* Kt, const bf16x8_t (&qf)[KS], int lq, int lg,
                                             f32x16_t (&s)[2]) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
+    // the two 32-key halves alternate so that consecutive MFMAs never depend on each other
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
             s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Kt, 32 * tt + lq, 2 * ks + lg), qf[ks],
                                                             s[tt], 0, 0, 0);
-    }
 }
 
 // Online-softmax update of one tile's raw scores (masked, when MASK, to the keys visible to
@@ -184,21 +186,22 @@ __device__ __forceinline__ void tile_update(f32x16_t (&s)[2], const uint16_t* Vt
     const int lg = lane >> 5;
     // key kv0 + 32*tt + 8*(v/4) + 4*lg + v%4 is visible iff it is <= key_limit, i.e. iff
     // 32*tt + 8*(v/4) + v%4 <= rel (a compile-time constant against one register)
-    int64_t rel64 = key_limit - kv0 - 4 * lg;
-    rel64 = rel64 < -1 ? -1 : (rel64 > kBlockN ? kBlockN : rel64);
-    const int rel = static_cast<int>(rel64);
+    if (mask) {
+        int64_t rel64 = key_limit - kv0 - 4 * lg;
+        rel64 = rel64 < -1 ? -1 : (rel64 > kBlockN ? kBlockN : rel64);
+        int rel = static_cast<int>(rel64);
+        asm volatile("" : "+v"(rel));  // keep the compares 32-bit
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                s[tt][v] = 32 * tt + (v >> 2) * 8 + (v & 3) <= rel ? s[tt][v] : -INFINITY;
+    }
     float mt = -INFINITY;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            float x = s[tt][v];
-            if (mask) {
-                x = 32 * tt + (v >> 2) * 8 + (v & 3) <= rel ? x : -INFINITY;
-                s[tt][v] = x;
-            }
-            mt = fmaxf(mt, x);
-        }
+        for (int v = 0; v < 16; ++v) mt = fmaxf(mt, s[tt][v]);
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * c;
     if (__any(mt > m_run + kStaleMax)) {
         const float m_new = fmaxf(m_run, mt);
