@@ -178,6 +178,260 @@ gemm_nt_kernel(GemmArgs p) {
     }
 }
 
+// Same GEMM for K % 32 == 0, with the operand slices moved by the global->LDS path
+// (buffer_load ... lds) instead of through registers:
+//   * K steps of 32 rotate through four LDS stages, so the loads of step kt+3 are in flight
+//     while step kt is multiplied (no staging registers, no ds_write instructions);
+//   * the stages are four separately declared arrays and the K loop is unrolled by four, so
+//     every access names its stage statically: the compiler can then tell the loads into one
+//     stage from the fragment reads of another and does not make the reads wait for them;
+//   * a stage row is 32 BF16 = 64 B = 4 chunks of 16 B; the chunk index is XORed with
+//     (row/2)%4, which spreads the 8 rows of a fragment read over all 32 banks. Each wave
+//     load instruction fills 1 KB of consecutive LDS (16 rows), so lane l fetches the global
+//     chunk the swizzle places at its position (row l/4, chunk (l%4) ^ ((l/4)/2 % 4));
+//   * each step is two 16-wide k slices ("phases"); a phase issues the next slice's fragment
+//     reads, then the current slice's MFMAs, and the compiler may not reorder across phases.
+constexpr int kSBK = 32;       // K per stage
+constexpr int kStages = 4;
+// Buffer resource word 3 for gfx9-family raw buffer loads (32-bit data format).
+constexpr int kBufferConfig = 0x00020000;
+
+__device__ __forceinline__ int swz32(int row, int chunk) {  // element offset in a [rows][32] stage
+    return row * kSBK + ((chunk ^ ((row >> 1) & 3)) << 3);
+}
+
+// This wave's MFMA operands for one 16-wide k slice of a stage.
+template <int BM, int BN>
+struct Frags {
+    bf16x8_t a[BM / 64];
+    bf16x8_t b[BN / 64];
+};
+
+template <int BM, int BN>
+__device__ __forceinline__ void read_frags(const uint16_t* stage, int ks, int wm, int wn, int lr, int lk,
+                                           Frags<BM, BN>& f) {
+    const int c = ks * 2 + lk;
+    const uint16_t* lb = stage + BM * kSBK;
+#pragma unroll
+    for (int i = 0; i < BM / 64; ++i)
+        f.a[i] = *reinterpret_cast<const bf16x8_t*>(stage + swz32(wm * (BM / 2) + i * 32 + lr, c));
+#pragma unroll
+    for (int j = 0; j < BN / 64; ++j)
+        f.b[j] = *reinterpret_cast<const bf16x8_t*>(lb + swz32(wn * (BN / 2) + j * 32 + lr, c));
+}
+
+// The empty asm pins the fragments to VGPRs (the accumulators fill the AGPR file; left to
+// itself the register allocator may park fragments there and spill accumulators).
+template <int BM, int BN>
+__device__ __forceinline__ void mma_frags(Frags<BM, BN>& f, f32x16_t (&acc)[BM / 64][BN / 64]) {
+#pragma unroll
+    for (int i = 0; i < BM / 64; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+    for (int j = 0; j < BN / 64; ++j) asm volatile("" : "+v"(f.b[j]));
+#pragma unroll
+    for (int i = 0; i < BM / 64; ++i)
+#pragma unroll
+        for (int j = 0; j < BN / 64; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over `bytes` bytes at `base` (wave-uniform).
+__device__ __forceinline__ i32x4_t buffer_resource(const void* base, int bytes) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    return i32x4_t{__builtin_amdgcn_readfirstlane(static_cast<int>(addr)),
+                   __builtin_amdgcn_readfirstlane(static_cast<int>(addr >> 32)),
+                   __builtin_amdgcn_readfirstlane(bytes), kBufferConfig};
+}
+
+__device__ __forceinline__ uint32_t lds_address(const uint16_t* p) {
+    const auto* l = (const __attribute__((address_space(3))) uint16_t*)(p);
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(l)));
+}
+
+// One wave instruction of the global->LDS path: 16 bytes per lane from rsrc + voff + soff
+// into LDS at lds + 16 * lane. Issued as inline assembly so that the compiler's wait-count
+// insertion does not track it: the kernel waits for these loads itself (stage_barrier), at
+// the distance the stage rotation allows, instead of before every later LDS read. M0 holds
+// the LDS address; nothing else in these kernels keeps a value in M0.
+__device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
+                 :
+                 : "v"(voff), "s"(lds), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
+
+// The compiler may not move instructions across this point.
+__device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// mma_frags with the P global->LDS instructions of one step spread between the MFMAs, so
+// the wave issues them while the matrix core is busy instead of stalling on a burst of
+// vector memory issue. load(d) issues instruction d.
+template <int BM, int BN, int P, class Load>
+__device__ __forceinline__ void mma_frags_loads(Frags<BM, BN>& f, f32x16_t (&acc)[BM / 64][BN / 64], Load&& load) {
+    constexpr int TI = BM / 64, TJ = BN / 64, NM = TI * TJ;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) asm volatile("" : "+v"(f.b[j]));
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+        const int i = mi / TJ, j = mi % TJ;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
+        // loads [mi*P/NM, (mi+1)*P/NM) follow MFMA mi
+#pragma unroll
+        for (int d = mi * P / NM; d < (mi + 1) * P / NM; ++d) {
+            phase_fence();
+            load(d);
+            phase_fence();
+        }
+    }
+}
+
+// Workgroup barrier after which the loads of the step before the last N outstanding ones
+// (per wave, in issue order) have landed in LDS and every LDS read issued before it has
+// completed. A plain barrier without the memory fence of __syncthreads, whose release
+// semantics would wait for every outstanding load, including the prefetches meant to stay in
+// flight. The empty asm statements keep the compiler from moving memory accesses across it.
+// gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int BM, int BN, bool OUT_BF16>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, const f32x16_t (&acc)[BM / 64][BN / 64], int tm,
+                                           int tn, int64_t g, int wm, int wn, int lr, int lk) {
+#pragma unroll
+    for (int i = 0; i < BM / 64; ++i) {
+        const int m = tm * BM + wm * (BM / 2) + i * 32 + lr;
+        if (m >= p.m) continue;
+#pragma unroll
+        for (int j = 0; j < BN / 64; ++j) {
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int n = tn * BN + wn * (BN / 2) + j * 32 + grp * 8 + lk * 4;
+                if (n >= p.n) continue;
+                const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
+                if constexpr (OUT_BF16) {
+                    u32x2_t w = {pack_bf16x2(acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1]),
+                                 pack_bf16x2(acc[i][j][grp * 4 + 2], acc[i][j][grp * 4 + 3])};
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = w;
+                } else {
+                    f32x4_t w = {acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1], acc[i][j][grp * 4 + 2],
+                                 acc[i][j][grp * 4 + 3]};
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.c) + off) = w;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, bool OUT_BF16>
+__global__ void __launch_bounds__(kThreads, (BM >= 256 ? 1 : 2))
+gemm_nt_dma_kernel(GemmArgs p) {
+    constexpr int TI = BM / 64;
+    constexpr int TJ = BN / 64;
+    constexpr int kStage = (BM + BN) * kSBK;        // elements per stage
+    constexpr int kPerWave = (BM + BN) / 16 / 4;    // 1 KB (16-row) load instructions per wave per step
+    __shared__ __attribute__((aligned(1024))) uint16_t stage0[kStage];
+    __shared__ __attribute__((aligned(1024))) uint16_t stage1[kStage];
+    __shared__ __attribute__((aligned(1024))) uint16_t stage2[kStage];
+    __shared__ __attribute__((aligned(1024))) uint16_t stage3[kStage];
+
+    const int tiles = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+    constexpr int GROUP = 8;
+    const int per_group = GROUP * p.tiles_n;
+    const int first_m = (bid / per_group) * GROUP;
+    const int gsize = min(p.tiles_m - first_m, GROUP);
+    const int tm = first_m + (bid % per_group) % gsize;
+    const int tn = (bid % per_group) / gsize;
+    const int64_t g = blockIdx.z;
+    const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
+    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // Loads go through buffer resources over this batch's A and B: one per-lane offset and a
+    // uniform offset per instruction. Rows past M (N) fall outside the resource and are not
+    // fetched; they only feed outputs that are not stored.
+    const i32x4_t ra = buffer_resource(A, p.m * p.k * 2);
+    const i32x4_t rb = buffer_resource(B, p.n * p.k * 2);
+    // instruction i of this wave fills stage rows 16*(wave + 4*i) .. +15
+    const int r_in = lane >> 2;
+    const int voff = ((16 * wave + r_in) * p.k + ((lane & 3) ^ ((r_in >> 1) & 3)) * 8) * 2;
+    auto fetch_one = [&](uint16_t* stage, int kt, int i) {
+        const uint32_t dst = lds_address(stage + (16 * wave + 64 * i) * kSBK);
+        if (i < BM / 64)
+            load_lds16(ra, dst, voff, ((tm * BM + 64 * i) * p.k + kt * kSBK) * 2);
+        else
+            load_lds16(rb, dst, voff, ((tn * BN + 64 * (i - BM / 64)) * p.k + kt * kSBK) * 2);
+    };
+    auto fetch = [&](uint16_t* stage, int kt) {
+#pragma unroll
+        for (int i = 0; i < kPerWave; ++i) fetch_one(stage, kt, i);
+    };
+
+    f32x16_t acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // Step kt multiplies stage X; its first fragments arrive in fa. Its first phase also
+    // issues the loads of step kt+3 into stage Z, freed by the barrier of step kt-1. Then the
+    // workgroup waits for step kt+1 to land in stage Y (the loads of steps kt+2 and kt+3 stay
+    // in flight) and meets at the barrier, and Y's first fragments are read while X's last
+    // MFMAs run. Every step issues its loads, so the wait counts are the same for all steps:
+    // past the last step the loads repeat step nk-1 into stages that are no longer read.
+    const int nk = p.k / kSBK;
+    const int last = nk - 1;
+    Frags<BM, BN> fa, fb;
+    auto step = [&](const uint16_t* X, const uint16_t* Y, uint16_t* Z, int kt) {
+        const int ahead = kt + 3 < nk ? kt + 3 : last;
+        phase_fence();
+        read_frags<BM, BN>(X, 1, wm, wn, lr, lk, fb);
+        mma_frags_loads<BM, BN, kPerWave>(fa, acc, [&](int d) { fetch_one(Z, ahead, d); });
+        phase_fence();
+        if (kt + 1 < nk) {
+            stage_barrier<2 * kPerWave>();
+            read_frags<BM, BN>(Y, 0, wm, wn, lr, lk, fa);
+        }
+        mma_frags<BM, BN>(fb, acc);
+    };
+
+    fetch(stage0, 0);
+    fetch(stage1, nk > 1 ? 1 : last);
+    fetch(stage2, nk > 2 ? 2 : last);
+    stage_barrier<2 * kPerWave>();
+    read_frags<BM, BN>(stage0, 0, wm, wn, lr, lk, fa);
+    int kt = 0;
+    do {  // nk >= 1: the accumulators never bypass the MFMAs on their way to the epilogue
+        step(stage0, stage1, stage3, kt);
+        if (kt + 1 < nk) step(stage1, stage2, stage0, kt + 1);
+        if (kt + 2 < nk) step(stage2, stage3, stage1, kt + 2);
+        if (kt + 3 < nk) step(stage3, stage0, stage2, kt + 3);
+        kt += 4;
+    } while (kt < nk);
+    // the trailing loads must land before the workgroup ends and its LDS is handed on
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    store_tile<BM, BN, OUT_BF16>(p, acc, tm, tn, g, wm, wn, lr, lk);
+}
+
 // out[g][c][r] = in[g][r][c] for BF16, 64x64 tiles through LDS (padded rows).
 __global__ void __launch_bounds__(256)
 transpose_bf16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t rows, int64_t cols) {
@@ -204,7 +458,14 @@ void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
     p.tiles_m = (p.m + BM - 1) / BM;
     p.tiles_n = (p.n + BN - 1) / BN;
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), 1, static_cast<unsigned>(batch));
-    if (out_bf16)
+    // the global->LDS kernel needs whole K steps and 32-bit byte offsets into A and B
+    const bool whole_steps = p.k % kSBK == 0 && p.k > 0 && static_cast<int64_t>(p.m) * p.k * 2 < (int64_t{1} << 31) &&
+                             static_cast<int64_t>(p.n) * p.k * 2 < (int64_t{1} << 31);
+    if (whole_steps && out_bf16)
+        hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
+    else if (whole_steps)
+        hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, false>), grid, dim3(kThreads), 0, s, p);
+    else if (out_bf16)
         hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
     else
         hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, false>), grid, dim3(kThreads), 0, s, p);
