@@ -186,9 +186,12 @@ gemm_nt_kernel(GemmArgs p) {
 //     every access names its stage statically: the compiler can then tell the loads into one
 //     stage from the fragment reads of another and does not make the reads wait for them;
 //   * a stage row is 32 BF16 = 64 B = 4 chunks of 16 B; the chunk index is XORed with
-//     (row/2)%4, which spreads the 8 rows of a fragment read over all 32 banks. Each wave
-//     load instruction fills 1 KB of consecutive LDS (16 rows), so lane l fetches the global
-//     chunk the swizzle places at its position (row l/4, chunk (l%4) ^ ((l/4)/2 % 4));
+//     (row/4)%4. gfx950's LDS serves a 16-byte read for 16 lanes per clock (64 banks), and
+//     a fragment read has 16 consecutive rows at the same chunk in those lanes: four rows share
+//     each 256-byte bank line, and the XOR moves the four to distinct chunks, so the 16 reads
+//     hit 16 distinct bank groups (measured: 2x the throughput of a (row/2)%4 swizzle). Each
+//     wave load instruction fills 1 KB of consecutive LDS (16 rows), so lane l fetches the
+//     global chunk the swizzle places at its position (row l/4, chunk (l%4) ^ ((l/16) % 4));
 //   * each step is two 16-wide k slices ("phases"); a phase issues the next slice's fragment
 //     reads, then the current slice's MFMAs, and the compiler may not reorder across phases.
 constexpr int kSBK = 32;       // K per stage
@@ -197,7 +200,7 @@ constexpr int kStages = 4;
 constexpr int kBufferConfig = 0x00020000;
 
 __device__ __forceinline__ int swz32(int row, int chunk) {  // element offset in a [rows][32] stage
-    return row * kSBK + ((chunk ^ ((row >> 1) & 3)) << 3);
+    return row * kSBK + ((chunk ^ ((row >> 2) & 3)) << 3);
 }
 
 // This wave's MFMA operands for one 16-wide k slice of a stage.
@@ -264,6 +267,49 @@ __device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds, int voff,
 
 // The compiler may not move instructions across this point.
 __device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Fragment r of a slice: r < TI is A fragment r, otherwise B fragment r - TI.
+template <int BM, int BN>
+__device__ __forceinline__ void read_frag(const uint16_t* stage, int ks, int r, int wm, int wn, int lr, int lk,
+                                          Frags<BM, BN>& f) {
+    constexpr int TI = BM / 64;
+    const int c = ks * 2 + lk;
+    if (r < TI)
+        f.a[r] = *reinterpret_cast<const bf16x8_t*>(stage + swz32(wm * (BM / 2) + r * 32 + lr, c));
+    else
+        f.b[r - TI] =
+            *reinterpret_cast<const bf16x8_t*>(stage + BM * kSBK + swz32(wn * (BN / 2) + (r - TI) * 32 + lr, c));
+}
+
+// One phase: the MFMAs of the current slice (fragments in cur) with, spread between them
+// in this order, the reads of the next slice's fragments (read(r), r < TI + TJ, one after
+// each of the first MFMAs, so they complete well before the next phase needs them) and P
+// global->LDS loads (load(d)). Spreading matters because issue is in order: a burst of LDS or
+// memory instructions that the memory pipelines accept slowly would hold back the MFMAs
+// behind it. The compiler may not reorder across the fences.
+template <int BM, int BN, int P, class Read, class Load>
+__device__ __forceinline__ void mma_phase(Frags<BM, BN>& cur, f32x16_t (&acc)[BM / 64][BN / 64], Read&& read,
+                                          Load&& load) {
+    constexpr int TI = BM / 64, TJ = BN / 64, NM = TI * TJ, NR = TI + TJ;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) asm volatile("" : "+v"(cur.a[i]));
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) asm volatile("" : "+v"(cur.b[j]));
+    phase_fence();
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+        const int i = mi / TJ, j = mi % TJ;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.b[j], cur.a[i], acc[i][j], 0, 0, 0);
+        phase_fence();
+        // reads: r in [mi*NR/NM', ...) over the first NM' = max(NM/2, 1) MFMAs
+        constexpr int NMR = NM / 2 > 0 ? NM / 2 : 1;
+#pragma unroll
+        for (int r = mi * NR / NMR; r < (mi + 1) * NR / NMR && r < NR; ++r) read(r);
+#pragma unroll
+        for (int d = mi * P / NM; d < (mi + 1) * P / NM; ++d) load(d);
+        phase_fence();
+    }
+}
 
 // mma_frags with the P global->LDS instructions of one step spread between the MFMAs, so
 // the wave issues them while the matrix core is busy instead of stalling on a burst of
@@ -370,7 +416,7 @@ gemm_nt_dma_kernel(GemmArgs p) {
     const i32x4_t rb = buffer_resource(B, p.n * p.k * 2);
     // instruction i of this wave fills stage rows 16*(wave + 4*i) .. +15
     const int r_in = lane >> 2;
-    const int voff = ((16 * wave + r_in) * p.k + ((lane & 3) ^ ((r_in >> 1) & 3)) * 8) * 2;
+    const int voff = ((16 * wave + r_in) * p.k + ((lane & 3) ^ ((r_in >> 2) & 3)) * 8) * 2;
     auto fetch_one = [&](uint16_t* stage, int kt, int i) {
         const uint32_t dst = lds_address(stage + (16 * wave + 64 * i) * kSBK);
         if (i < BM / 64)
@@ -391,26 +437,28 @@ gemm_nt_dma_kernel(GemmArgs p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    // Step kt multiplies stage X; its first fragments arrive in fa. Its first phase also
-    // issues the loads of step kt+3 into stage Z, freed by the barrier of step kt-1. Then the
-    // workgroup waits for step kt+1 to land in stage Y (the loads of steps kt+2 and kt+3 stay
-    // in flight) and meets at the barrier, and Y's first fragments are read while X's last
-    // MFMAs run. Every step issues its loads, so the wait counts are the same for all steps:
+    // Step kt multiplies stage X; its first fragments arrive in fa. Its two phases also issue
+    // the loads of step kt+3 into stage Z, freed by the barrier of step kt-1. Between them the
+    // workgroup waits for step kt+1 to land in stage Y (the loads of step kt+2 and the first
+    // half of step kt+3 stay in flight) and meets at the barrier, and Y's first fragments are
+    // read while X's last MFMAs run. Every step issues its loads, so the wait counts are the same for all steps:
     // past the last step the loads repeat step nk-1 into stages that are no longer read.
     const int nk = p.k / kSBK;
     const int last = nk - 1;
     Frags<BM, BN> fa, fb;
     auto step = [&](const uint16_t* X, const uint16_t* Y, uint16_t* Z, int kt) {
         const int ahead = kt + 3 < nk ? kt + 3 : last;
-        phase_fence();
-        read_frags<BM, BN>(X, 1, wm, wn, lr, lk, fb);
-        mma_frags_loads<BM, BN, kPerWave>(fa, acc, [&](int d) { fetch_one(Z, ahead, d); });
-        phase_fence();
-        if (kt + 1 < nk) {
-            stage_barrier<2 * kPerWave>();
-            read_frags<BM, BN>(Y, 0, wm, wn, lr, lk, fa);
-        }
-        mma_frags<BM, BN>(fb, acc);
+        // the loads of step kt+3 are split over both phases (stage Z stays free until step
+        // kt+3 reads it); at the barrier the second half is still in flight
+        constexpr int P0 = (kPerWave + 1) / 2, P1 = kPerWave - P0;
+        mma_phase<BM, BN, P0>(
+            fa, acc, [&](int r) { read_frag<BM, BN>(X, 1, r, wm, wn, lr, lk, fb); },
+            [&](int d) { fetch_one(Z, ahead, d); });
+        if (kt + 1 < nk) stage_barrier<kPerWave + P0>();
+        // after the last step these reads fetch fragments that are never used
+        mma_phase<BM, BN, P1>(
+            fb, acc, [&](int r) { read_frag<BM, BN>(Y, 0, r, wm, wn, lr, lk, fa); },
+            [&](int d) { fetch_one(Z, ahead, P0 + d); });
     };
 
     fetch(stage0, 0);
