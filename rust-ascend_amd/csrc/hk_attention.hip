@@ -45,13 +45,24 @@ constexpr int kXcds = 8;     // accelerator complex dies; workgroups are dispatc
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
-// 16-byte chunk swizzle of a tile row: keeps the 32-row MFMA operand reads, the 4-row
-// transposing reads and the row-contiguous tile writes free of LDS bank conflicts.
+// 16-byte chunk swizzle of a tile row (XOR applied to the chunk index). gfx950's LDS has 64
+// banks: one clock serves 16 lanes of a 16-byte read or 32 lanes of an 8-byte read, i.e. one
+// 256-byte bank line. The MFMA operand reads put 16 consecutive rows at the same chunk in those
+// 16 lanes, and the transposing reads put 4 consecutive rows (from a multiple of 4) x 4
+// consecutive chunks (from a multiple of 4) in 32 lanes; the XOR gives both patterns 16
+// distinct 16-byte bank groups. Row-contiguous tile writes stay conflict-free.
 template <int D>
-__device__ __forceinline__ int tile_swz(int row) {  // XOR applied to the 16-byte chunk index of a row
+__device__ __forceinline__ int tile_swz(int row) {
     constexpr int chunks = D / 8;
-    constexpr int mask = chunks - 1 < 7 ? chunks - 1 : 7;
-    return (((row & 3) << 1) | ((row >> 2) & 1)) & mask;
+    static_assert(chunks == 4 || chunks == 8 || chunks == 16, "tile widths of 32, 64 or 128 elements");
+    if constexpr (chunks == 16) {  // 256-byte rows: one row per bank line
+        return ((row & 3) << 2) | ((row >> 2) & 3);
+    } else if constexpr (chunks == 8) {  // 128-byte rows: two rows per bank line
+        const int u = row >> 1;
+        return ((u & 1) << 2) | ((u >> 1) & 3);
+    } else {  // 64-byte rows: four rows per bank line
+        return (row >> 2) & 3;
+    }
 }
 
 template <int D>
