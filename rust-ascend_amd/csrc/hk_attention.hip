@@ -138,15 +138,16 @@ struct FwdArgs {
 
 // Tile rows [row0, row0+64) of a [N, D] matrix -> registers (rows >= n clamp to n-1), laid
 // out in LDS as [64][DP] with DP = max(D, 32); columns >= D are zero.
-template <int D, int DP>
+template <int D, int DP, int THREADS = kThreads>
 struct TileLoader {
     static constexpr int kChunks = DP / 8;                          // 16-byte chunks per LDS row
-    static constexpr int kPerThread = kBlockN * kChunks / kThreads;  // >= 1 since DP >= 32
+    static constexpr int kPerThread = kBlockN * kChunks / THREADS;
+    static_assert(kPerThread >= 1 && kBlockN * kChunks % THREADS == 0, "tile must split over the threads");
     u32x4_t r[kPerThread];
     __device__ __forceinline__ void load(const uint16_t* base, int64_t row0, int64_t n, int t) {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
-            const int idx = t + i * kThreads;
+            const int idx = t + i * THREADS;
             const int row = idx / kChunks, chunk = idx % kChunks;
             int64_t gr = row0 + row;
             gr = gr < n ? gr : n - 1;
@@ -156,7 +157,7 @@ struct TileLoader {
     __device__ __forceinline__ void store(uint16_t* tile, int t) const {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
-            const int idx = t + i * kThreads;
+            const int idx = t + i * THREADS;
             const int row = idx / kChunks, chunk = idx % kChunks;
             *reinterpret_cast<u32x4_t*>(tile + tile_off<DP>(row, chunk * 8)) = r[i];
         }
@@ -190,10 +191,12 @@ __device__ __forceinline__ void tile_scores(const uint16_t* Kt, const bf16x8_t (
 // and O / l and lse = m + log2(l) are the same quantities as with an exact running max.
 constexpr float kStaleMax = 8.0f;
 
-template <int DP, int DT>
-__device__ __forceinline__ void tile_update(f32x16_t (&s)[2], const uint16_t* Vt, int lane, float c, bool mask,
-                                            int64_t kv0, int64_t key_limit, float& m_run, float& l_run,
-                                            f32x16_t (&o)[DT]) {
+// Softmax part: updates m, l (and rescales O when needed) and leaves P in BF16 as the B
+// operands of the four 16-key MFMA steps of P.V.
+template <int DT>
+__device__ __forceinline__ void tile_softmax(f32x16_t (&s)[2], int lane, float c, bool mask, int64_t kv0,
+                                             int64_t key_limit, float& m_run, float& l_run, f32x16_t (&o)[DT],
+                                             bf16x8_t (&pb)[4]) {
     const int lg = lane >> 5;
     // key kv0 + 32*tt + 8*(v/4) + 4*lg + v%4 is visible iff it is <= key_limit, i.e. iff
     // 32*tt + 8*(v/4) + v%4 <= rel (a compile-time constant against one register)
@@ -236,25 +239,36 @@ __device__ __forceinline__ void tile_update(f32x16_t (&s)[2], const uint16_t* Vt
         }
     l_run += ls;
 #pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pb[ks] = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
+}
+
+// O^T += V^T P^T over one 64-key tile (V^T through transposing reads of the row-major V tile).
+template <int DP, int DT>
+__device__ __forceinline__ void tile_pv(const bf16x8_t (&pb)[4], const uint16_t* Vt, int lane, f32x16_t (&o)[DT]) {
+    const int lg = lane >> 5;
+#pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8_t pb = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
         const int kb0 = 16 * ks + 4 * lg;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Vt, lane, kb0, kb0 + 8, 32 * dt), pb, o[dt],
-                                                            0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Vt, lane, kb0, kb0 + 8, 32 * dt), pb[ks],
+                                                            o[dt], 0, 0, 0);
     }
 }
 
+template <int DP, int DT>
+__device__ __forceinline__ void tile_update(f32x16_t (&s)[2], const uint16_t* Vt, int lane, float c, bool mask,
+                                            int64_t kv0, int64_t key_limit, float& m_run, float& l_run,
+                                            f32x16_t (&o)[DT]) {
+    bf16x8_t pb[4];
+    tile_softmax<DT>(s, lane, c, mask, kv0, key_limit, m_run, l_run, o, pb);
+    tile_pv<DP, DT>(pb, Vt, lane, o);
+}
+
 // D is the head dim in memory; the kernel works on DP = max(D, 32) (zero-padded columns).
-//
-// Tile pipeline: iteration j issues the scores of tile j+1 (from K_{j+1} in LDS) and then
-// runs the softmax and P.V of tile j (V_j in LDS), so the MFMAs of the next tile's scores are in
-// flight while the current tile's exponentials run. K therefore stays one tile ahead of V:
-// at the end of iteration j the registers prefetched one iteration earlier (K_{j+2}, V_{j+1})
-// are stored into the LDS buffers last read in iteration j-1, the loads of K_{j+3}, V_{j+2} are
-// issued, and one barrier closes the iteration. Tiles fully visible to every row of the
-// workgroup run without mask arithmetic; only the diagonal / ragged tail tiles are masked.
+// Used for D <= 32; wider heads use the ping-pong kernel below. Tile j is read from LDS buffer
+// j&1 while tile j+1 waits in registers and is stored into the other buffer at the end of the
+// iteration. Tiles fully visible to every row of the workgroup run without mask arithmetic.
 template <int D>
 __global__ void __launch_bounds__(kThreads, 2)
 attn_fwd(FwdArgs a) {
@@ -381,6 +395,288 @@ attn_fwd(FwdArgs a) {
     }
 }
 
+// Ping-pong forward kernel for D = 64 / 128: 8 wavefronts = 256 query rows per workgroup,
+// two waves per SIMD (waves w and w+4). Each wave alternates an MFMA phase (P.V of the previous
+// tile and S = K Q^T of the current one, 32 MFMAs) with a softmax phase (VALU and v_exp_f32),
+// and the second group of four waves runs one phase behind the first: at every barrier the two
+// waves on a SIMD swap roles, so the matrix core is fed by one while the other computes the
+// exponentials, instead of both waiting on their own softmax. The MFMA phase raises the wave's
+// issue priority so its next MFMA is issued as soon as the matrix core frees up.
+//
+// Half-step h (barrier-separated): tiles K_t and V_{t-1} (t = h/2) are in LDS; the group lagging
+// by g half-steps does its phase s = h - g: even s -> MFMA phase of tile s/2, odd s -> softmax
+// of tile (s-1)/2. K_{t+1} and V_t are fetched straight into LDS (into the buffers read two
+// half-steps earlier) from the even half-step on, and waited for before the barrier that ends
+// the odd one. The K/V tile is shared by all 8 waves: half the global->LDS traffic per query
+// of the 4-wave kernel.
+// The ping-pong kernel keeps its K and V tiles in padded rows instead of XOR-swizzled ones, so
+// that every operand read is one base register plus an immediate offset (the swizzle's
+// lane-dependent XOR would need a register per read pattern, and with Q, O, S and P resident
+// those spill). The pads are chosen for gfx950's 64 banks (256-byte bank line):
+//   K rows of D+8 elements: the 16 rows of an operand read (16 lanes, 16 bytes each) start
+//     16 bytes apart modulo 256 -> 16 distinct bank groups;
+//   V rows of D+32 elements: the 4 rows x 64 bytes of a transposing read (32 lanes, 8 bytes
+//     each) start 64 bytes apart modulo 256 -> 4 distinct bank groups.
+template <int D> constexpr int kKStride = D + 8;
+template <int D> constexpr int kVStride = D + 32;
+
+template <int STRIDE>
+__device__ __forceinline__ bf16x8_t pad_read16(const uint16_t* t, int row, int chunk) {
+    return *reinterpret_cast<const bf16x8_t*>(t + row * STRIDE + chunk * 8);
+}
+
+// Same operand as tile_read_tr, from a padded [64][STRIDE] tile.
+template <int STRIDE>
+__device__ __forceinline__ bf16x8_t pad_read_tr(const uint16_t* t, int lane, int kbase0, int kbase1, int ibase) {
+    const int g = (lane >> 4) & 1;
+    const int i = lane & 15;
+    const int col = ibase + 16 * g + 4 * (i & 3);
+    const int r = i >> 2;
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + (kbase0 + r) * STRIDE + col));
+    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + (kbase1 + r) * STRIDE + col));
+    typedef short v8i16_t __attribute__((ext_vector_type(8)));
+    v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// MFMA phase of the ping-pong kernel: up to 16 MFMAs of O^T += V^T P^T (tile j-1) followed by
+// 16 (D=128) or 8 (D=64) MFMAs of S^T = K Q^T (tile j), as one software pipeline: the LDS
+// operand of MFMA i + kAhead is read while MFMA i runs, through a ring of kAhead + 1 registers.
+// The fences keep the compiler from regrouping the reads in front of their MFMAs (which
+// serializes every MFMA behind a full LDS round trip); the empty asm makes the wait for each
+// operand land right before its MFMA.
+constexpr int kAhead = 4;
+
+template <int D, bool PV, bool QK>
+__device__ __forceinline__ void mfma_phase(const uint16_t* Vt, const uint16_t* Kt, const bf16x8_t (&pb)[4],
+                                           const bf16x8_t (&qf)[D / 16], int lane, int lq, int lg,
+                                           f32x16_t (&o)[D / 32], f32x16_t (&s)[2]) {
+    constexpr int DT = D / 32, KS = D / 16;
+    constexpr int NPV = PV ? 4 * DT : 0;  // P.V MFMAs: ks-major, dt-minor
+    constexpr int NQK = QK ? 2 * KS : 0;  // score MFMAs: ks-major, tt-minor
+    constexpr int N = NPV + NQK;
+    constexpr int R = kAhead + 1;
+    auto fetch = [&](int i) -> bf16x8_t {
+        if (i < NPV) {
+            const int ks = i / DT, dt = i % DT;
+            const int kb0 = 16 * ks + 4 * lg;
+            return pad_read_tr<kVStride<D>>(Vt, lane, kb0, kb0 + 8, 32 * dt);
+        }
+        const int q = i - NPV, ks = q >> 1, tt = q & 1;
+        return pad_read16<kKStride<D>>(Kt, 32 * tt + lq, 2 * ks + lg);
+    };
+    bf16x8_t ring[R];
+#pragma unroll
+    for (int i = 0; i < kAhead && i < N; ++i) ring[i % R] = fetch(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (i + kAhead < N) ring[(i + kAhead) % R] = fetch(i + kAhead);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8_t x = ring[i % R];
+        asm volatile("" : "+v"(x));
+        if (i < NPV) {
+            const int ks = i / DT, dt = i % DT;
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, pb[ks], o[dt], 0, 0, 0);
+        } else {
+            const int q = i - NPV, ks = q >> 1, tt = q & 1;
+            const f32x16_t zero = {};
+            s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, qf[ks], ks == 0 ? zero : s[tt], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = kPPWaves * 64;
+constexpr int kPPBlockM = kPPWaves * 32;
+
+// Rows [row0, row0 + 64) of one K or V head into a padded [64][STRIDE] LDS tile through the
+// global->LDS path (no staging registers, no LDS write instructions). The tile is a run of
+// 64 * STRIDE / 8 16-byte positions; wave instruction q fills positions 64q .. 64q+63, so lane
+// l fetches the chunk that belongs at position 64q + l (pad positions fetch a chunk of their
+// row again). Rows past n repeat row n-1 (finite values for the masked keys). The caller waits
+// (vmcnt) before the barrier that publishes the tile.
+template <int D, int STRIDE>
+struct PadTileDma {
+    static constexpr int kPerRow = STRIDE / 8;  // 16-byte positions per row, pad included
+    static constexpr int kInstr = kPerRow;      // 64 rows * kPerRow positions / 64 lanes
+    // row0 and n fit in 32 bits: the launcher keeps n * D * 2 below 2^31
+    __device__ __forceinline__ static void issue(i32x4_t rsrc, uint16_t* tile, int row0, int n, int wave,
+                                                 int lane) {
+        // recompute the lane's positions here rather than keep them in registers across the loop
+        asm volatile("" : "+v"(lane));
+#pragma unroll
+        for (int i = 0; i < (kInstr + kPPWaves - 1) / kPPWaves; ++i) {
+            const int q = wave + kPPWaves * i;
+            if (q < kInstr) {
+                const int pos = 64 * q + lane;
+                const int row = pos / kPerRow, c = pos % kPerRow;
+                const int chunk = c < D / 8 ? c : 0;
+                const int gr = min(row0 + row, n - 1);
+                load_lds16(rsrc, lds_address(tile + 8 * 64 * q), (gr * D + chunk * 8) * 2, 0);
+            }
+        }
+    }
+};
+
+template <int D>
+__global__ void __launch_bounds__(kPPThreads, 1)
+attn_fwd_pp(FwdArgs a) {
+    static_assert(D == 64 || D == 128, "ping-pong kernel is for D = 64 or 128");
+    constexpr int KS = D / 16;
+    constexpr int DT = D / 32;
+    __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kBlockN * kKStride<D>];
+    __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kBlockN * kVStride<D>];
+    using KDma = PadTileDma<D, kKStride<D>>;
+    using VDma = PadTileDma<D, kVStride<D>>;
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lq = lane & 31, lg = lane >> 5;
+    const int group = wave >> 2;  // 0: leads, 1: one half-step behind
+    // logical order: KV head group, query block heaviest first, query head in the group
+    const int logical = xcd_logical();
+    const int group_heads = static_cast<int>(a.heads / a.kv_heads);
+    const int per_group = a.mblocks * group_heads;
+    const int grp = logical / per_group, in_grp = logical % per_group;
+    const int mb = a.mblocks - 1 - in_grp / group_heads;
+    const int64_t b = grp / a.kv_heads, kvh = grp % a.kv_heads;
+    const int64_t h = kvh * group_heads + in_grp % group_heads;
+    const int64_t bh = b * a.heads + h;
+    const uint16_t* Q = a.q + (bh * a.m) * D;
+    const uint16_t* K = a.k + ((b * a.kv_heads + kvh) * a.n) * D;
+    const uint16_t* V = a.v + ((b * a.kv_heads + kvh) * a.n) * D;
+    const int64_t q0 = static_cast<int64_t>(mb) * kPPBlockM;
+    const int64_t q0w = q0 + wave * 32;
+    const int64_t my_q = q0w + lq;
+
+    // keys this workgroup needs: [0, kv_end); tiles [0, nfull) are visible to all its rows
+    int64_t kv_end = a.n, full_end = a.n;
+    if (a.causal) {
+        const int64_t last = q0 + kPPBlockM - 1 + a.diag;
+        kv_end = last + 1 < kv_end ? last + 1 : kv_end;
+        const int64_t first = q0 + a.diag + 1;
+        full_end = first < full_end ? first : full_end;
+    }
+    const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
+    int nfull = full_end > 0 ? static_cast<int>(full_end / kBlockN) : 0;
+    nfull = nfull < ntiles ? nfull : ntiles;
+    int64_t key_limit = a.n - 1;
+    if (a.causal) key_limit = my_q + a.diag < key_limit ? my_q + a.diag : key_limit;
+    // this wave's 32 rows see no key of tile j (it still takes part in every barrier)
+    auto skip = [&](int j) { return a.causal && static_cast<int64_t>(j) * kBlockN > q0w + 31 + a.diag; };
+
+    bf16x8_t qf[KS];
+    {
+        const int64_t qr = my_q < a.m ? my_q : a.m - 1;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const bf16x8_t*>(Q + qr * D + 16 * s + 8 * lg);
+    }
+    float c = a.scale_log2;
+    if (c < 0.0f) {
+        c = -c;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            qf[s] = __builtin_bit_cast(bf16x8_t, __builtin_bit_cast(u32x4_t, qf[s]) ^ 0x80008000u);
+    }
+    settle(qf);
+
+    f32x16_t o[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x16_t s[2];
+    bf16x8_t pb[4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
+
+    // byte offsets into one K/V head stay below 2^31 (checked by the launcher)
+    const i32x4_t rk = buffer_resource(K, static_cast<int>(a.n * D * 2));
+    const i32x4_t rv = buffer_resource(V, static_cast<int>(a.n * D * 2));
+    const int n32 = static_cast<int>(a.n);
+    if (ntiles > 0) KDma::issue(rk, kbuf[0], 0, n32, wave, lane);
+    // the first MFMA phase multiplies a zero P with V buffer 1: it must hold finite values
+    for (int i = t; i < kBlockN * kVStride<D> / 8; i += kPPThreads)
+        *reinterpret_cast<u32x4_t*>(vbuf[1] + 8 * i) = u32x4_t{0, 0, 0, 0};
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    // Half-step hs (0 .. 2*ntiles+1) ends with a barrier; K_{hs/2} and V_{hs/2-1} are in LDS
+    // during it. Every even half-step starts the loads of K_{t+1}, V_t (t = hs/2) into the
+    // buffers read two half-steps earlier; every odd one waits for them before its barrier.
+    // The leading group runs MFMA phase t at half-step 2t and softmax t at 2t+1; the lagging
+    // group runs them one half-step later. Each group's schedule is straight-line code (two
+    // copies of the loop), so the values that live across phases stay in their registers.
+    auto fetch = [&](int tl) {
+        if (tl + 1 < ntiles) KDma::issue(rk, kbuf[(tl + 1) & 1], (tl + 1) * kBlockN, n32, wave, lane);
+        if (tl < ntiles) VDma::issue(rv, vbuf[tl & 1], tl * kBlockN, n32, wave, lane);
+    };
+    auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j. Always the full phase: a P of zeros (no
+    // previous tile, or one this wave skips) adds nothing, and scores of a skipped or
+    // past-the-end tile are not used.
+    auto mfma = [&](int j) {
+        __builtin_amdgcn_s_setprio(1);
+        mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    auto softmax = [&](int j) {
+        if (!skip(j)) {
+            tile_softmax<DT>(s, lane, c, j >= nfull, static_cast<int64_t>(j) * kBlockN, key_limit, m_run, l_run, o,
+                             pb);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) pb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
+        }
+    };
+    if (group == 0) {
+        for (int j = 0; j <= ntiles; ++j) {
+            fetch(j);                   // half-step 2j
+            mfma(j);
+            __syncthreads();
+            if (j < ntiles) softmax(j);  // half-step 2j+1
+            landed();
+            __syncthreads();
+        }
+    } else {
+        fetch(0);  // half-step 0
+        __syncthreads();
+        for (int j = 0; j <= ntiles; ++j) {
+            mfma(j);  // half-step 2j+1
+            landed();
+            __syncthreads();
+            if (j < ntiles) {  // half-step 2j+2
+                fetch(j + 1);
+                softmax(j);
+                __syncthreads();
+            }
+        }
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (my_q < a.m) {
+        uint16_t* orow = a.o + (bh * a.m + my_q) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * dt + 8 * g + 4 * lg;
+                u32x2_t w = {pack_bf16x2(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv),
+                             pack_bf16x2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
+                *reinterpret_cast<u32x2_t*>(orow + d) = w;
+            }
+        if (lg == 0)
+            a.lse[bh * a.m + my_q] = l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+    }
+}
+
 int64_t clamp_diag(const AttnShape& sh) {
     // visible iff key_start + j <= query_start + i  <=>  j <= i + (query_start - key_start)
     if (!sh.causal) return 0;
@@ -410,9 +706,16 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
     a.diag = clamp_diag(sh);
     a.scale_log2 = sh.scale * kLog2e;
     a.causal = sh.causal;
-    a.mblocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
-    const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
-    hipLaunchKernelGGL((attn_fwd<D>), grid, dim3(kThreads), 0, s, a);
+    if constexpr (D >= 64) {
+        if (sh.n * D * 2 >= (int64_t{1} << 31)) return hipErrorInvalidValue;  // 32-bit buffer offsets
+        a.mblocks = static_cast<int>((sh.m + kPPBlockM - 1) / kPPBlockM);
+        const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
+        hipLaunchKernelGGL((attn_fwd_pp<D>), grid, dim3(kPPThreads), 0, s, a);
+    } else {
+        a.mblocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
+        const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
+        hipLaunchKernelGGL((attn_fwd<D>), grid, dim3(kThreads), 0, s, a);
+    }
     return hipGetLastError();
 }
 

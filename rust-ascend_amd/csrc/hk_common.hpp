@@ -93,4 +93,38 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// ---- global->LDS loads (buffer_load ... lds)
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource word 3 for gfx9-family raw buffer loads (32-bit data format).
+constexpr int kBufferConfig = 0x00020000;
+
+// Raw buffer resource over `bytes` bytes at `base` (wave-uniform).
+__device__ __forceinline__ i32x4_t buffer_resource(const void* base, int bytes) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(base);
+    return i32x4_t{__builtin_amdgcn_readfirstlane(static_cast<int>(addr)),
+                   __builtin_amdgcn_readfirstlane(static_cast<int>(addr >> 32)),
+                   __builtin_amdgcn_readfirstlane(bytes), kBufferConfig};
+}
+
+// LDS byte address of a __shared__ element (wave-uniform pointer).
+__device__ __forceinline__ uint32_t lds_address(const uint16_t* p) {
+    const auto* l = (const __attribute__((address_space(3))) uint16_t*)(p);
+    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(l)));
+}
+
+// One wave instruction of the global->LDS path: 16 bytes per lane from rsrc + voff + soff
+// into LDS at lds + 16 * lane. Issued as inline assembly so that the compiler's wait-count
+// insertion does not track it: a kernel using it waits for these loads itself (s_waitcnt
+// vmcnt before the barrier that publishes the tile), at the distance its buffering allows,
+// instead of before every later LDS read. M0 holds the LDS address; the kernels that use this
+// keep no other value in M0.
+__device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
+                 :
+                 : "v"(voff), "s"(lds), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
+
 }  // namespace hk

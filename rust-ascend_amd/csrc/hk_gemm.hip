@@ -196,9 +196,6 @@ gemm_nt_kernel(GemmArgs p) {
 //     reads, then the current slice's MFMAs, and the compiler may not reorder across phases.
 constexpr int kSBK = 32;       // K per stage
 constexpr int kStages = 4;
-// Buffer resource word 3 for gfx9-family raw buffer loads (32-bit data format).
-constexpr int kBufferConfig = 0x00020000;
-
 __device__ __forceinline__ int swz32(int row, int chunk) {  // element offset in a [rows][32] stage
     return row * kSBK + ((chunk ^ ((row >> 2) & 3)) << 3);
 }
@@ -236,33 +233,6 @@ __device__ __forceinline__ void mma_frags(Frags<BM, BN>& f, f32x16_t (&acc)[BM /
 #pragma unroll
         for (int j = 0; j < BN / 64; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
-}
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// Raw buffer resource over `bytes` bytes at `base` (wave-uniform).
-__device__ __forceinline__ i32x4_t buffer_resource(const void* base, int bytes) {
-    const uint64_t addr = reinterpret_cast<uint64_t>(base);
-    return i32x4_t{__builtin_amdgcn_readfirstlane(static_cast<int>(addr)),
-                   __builtin_amdgcn_readfirstlane(static_cast<int>(addr >> 32)),
-                   __builtin_amdgcn_readfirstlane(bytes), kBufferConfig};
-}
-
-__device__ __forceinline__ uint32_t lds_address(const uint16_t* p) {
-    const auto* l = (const __attribute__((address_space(3))) uint16_t*)(p);
-    return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(l)));
-}
-
-// One wave instruction of the global->LDS path: 16 bytes per lane from rsrc + voff + soff
-// into LDS at lds + 16 * lane. Issued as inline assembly so that the compiler's wait-count
-// insertion does not track it: the kernel waits for these loads itself (stage_barrier), at
-// the distance the stage rotation allows, instead of before every later LDS read. M0 holds
-// the LDS address; nothing else in these kernels keeps a value in M0.
-__device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds, int voff, int soff) {
-    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds"
-                 :
-                 : "v"(voff), "s"(lds), "s"(rsrc), "s"(soff)
-                 : "memory");
 }
 
 // The compiler may not move instructions across this point.
