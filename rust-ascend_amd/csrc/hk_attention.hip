@@ -445,12 +445,14 @@ __device__ __forceinline__ bf16x8_t pad_read_tr(const uint16_t* t, int lane, int
 // The fences keep the compiler from regrouping the reads in front of their MFMAs (which
 // serializes every MFMA behind a full LDS round trip); the empty asm makes the wait for each
 // operand land right before its MFMA.
-constexpr int kAhead = 4;
+constexpr int kAhead = 6;
 
-template <int D, bool PV, bool QK>
+// NL global->LDS loads (load(d), d < NL) are spread one per few MFMAs, so they trickle into the
+// memory pipeline while the matrix core is busy instead of stalling the wave as a burst.
+template <int D, bool PV, bool QK, int NL = 0, class Load = void (*)(int)>
 __device__ __forceinline__ void mfma_phase(const uint16_t* Vt, const uint16_t* Kt, const bf16x8_t (&pb)[4],
                                            const bf16x8_t (&qf)[D / 16], int lane, int lq, int lg,
-                                           f32x16_t (&o)[D / 32], f32x16_t (&s)[2]) {
+                                           f32x16_t (&o)[D / 32], f32x16_t (&s)[2], Load&& load = nullptr) {
     constexpr int DT = D / 32, KS = D / 16;
     constexpr int NPV = PV ? 4 * DT : 0;  // P.V MFMAs: ks-major, dt-minor
     constexpr int NQK = QK ? 2 * KS : 0;  // score MFMAs: ks-major, tt-minor
@@ -483,6 +485,11 @@ __device__ __forceinline__ void mfma_phase(const uint16_t* Vt, const uint16_t* K
             s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, qf[ks], ks == 0 ? zero : s[tt], 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NL > 0) {
+#pragma unroll
+            for (int d = i * NL / N; d < (i + 1) * NL / N; ++d) load(d);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 }
 
@@ -500,21 +507,32 @@ template <int D, int STRIDE>
 struct PadTileDma {
     static constexpr int kPerRow = STRIDE / 8;  // 16-byte positions per row, pad included
     static constexpr int kInstr = kPerRow;      // 64 rows * kPerRow positions / 64 lanes
-    // row0 and n fit in 32 bits: the launcher keeps n * D * 2 below 2^31
+    // Instruction q (< kInstr) of the tile. row0 and n fit in 32 bits: the launcher keeps
+    // n * D * 2 below 2^31.
+    __device__ __forceinline__ static void issue_one(i32x4_t rsrc, uint16_t* tile, int row0, int n, int q, int lane) {
+        // recompute the lane's position here rather than keep it in a register across the loop
+        asm volatile("" : "+v"(lane));
+        const int pos = 64 * q + lane;
+        const int row = pos / kPerRow, c = pos % kPerRow;
+        const int chunk = c < D / 8 ? c : 0;
+        const int gr = min(row0 + row, n - 1);
+        load_lds16(rsrc, lds_address(tile + 8 * 64 * q), (gr * D + chunk * 8) * 2, 0);
+    }
+    // Lane byte offset of instruction q within a tile whose rows are all below n: the load is
+    // then rsrc + lane_offset(q) + row0 * D * 2 (uniform), with nothing to compute per load.
+    __device__ __forceinline__ static int lane_offset(int q, int lane) {
+        const int pos = 64 * q + lane;
+        const int row = pos / kPerRow, c = pos % kPerRow;
+        const int chunk = c < D / 8 ? c : 0;
+        return (row * D + chunk * 8) * 2;
+    }
+    // The whole tile from the 8 waves of the workgroup.
     __device__ __forceinline__ static void issue(i32x4_t rsrc, uint16_t* tile, int row0, int n, int wave,
                                                  int lane) {
-        // recompute the lane's positions here rather than keep them in registers across the loop
-        asm volatile("" : "+v"(lane));
 #pragma unroll
         for (int i = 0; i < (kInstr + kPPWaves - 1) / kPPWaves; ++i) {
             const int q = wave + kPPWaves * i;
-            if (q < kInstr) {
-                const int pos = 64 * q + lane;
-                const int row = pos / kPerRow, c = pos % kPerRow;
-                const int chunk = c < D / 8 ? c : 0;
-                const int gr = min(row0 + row, n - 1);
-                load_lds16(rsrc, lds_address(tile + 8 * 64 * q), (gr * D + chunk * 8) * 2, 0);
-            }
+            if (q < kInstr) issue_one(rsrc, tile, row0, n, q, lane);
         }
     }
 };
@@ -608,24 +626,23 @@ attn_fwd_pp(FwdArgs a) {
     __syncthreads();
 
     // Half-step hs (0 .. 2*ntiles+1) ends with a barrier; K_{hs/2} and V_{hs/2-1} are in LDS
-    // during it. Every even half-step starts the loads of K_{t+1}, V_t (t = hs/2) into the
-    // buffers read two half-steps earlier; every odd one waits for them before its barrier.
-    // The leading group runs MFMA phase t at half-step 2t and softmax t at 2t+1; the lagging
-    // group runs them one half-step later. Each group's schedule is straight-line code (two
-    // copies of the loop), so the values that live across phases stay in their registers.
-    auto fetch = [&](int tl) {
-        if (tl + 1 < ntiles) KDma::issue(rk, kbuf[(tl + 1) & 1], (tl + 1) * kBlockN, n32, wave, lane);
-        if (tl < ntiles) VDma::issue(rv, vbuf[tl & 1], tl * kBlockN, n32, wave, lane);
-    };
+    // during it. The leading group runs MFMA phase t at half-step 2t and softmax t at 2t+1; the
+    // lagging group runs them one half-step later. Each group's schedule is straight-line code
+    // (two copies of the loop), so the values that live across phases stay in their registers.
+    // The leading group's MFMA phase t also issues the loads of K_{t+1} and V_t into the
+    // buffers read two half-steps earlier (its four waves share the tile's load instructions);
+    // every wave waits for its loads before the barrier that ends half-step 2t+1.
+    constexpr int kKInstr = KDma::kInstr, kVInstr = VDma::kInstr;
+    constexpr int kLoadsPerWave = (kKInstr + kVInstr + 3) / 4;
+    // lane offsets of this wave's load instructions (leading group only), for whole tiles
+    int loff[kLoadsPerWave];
+#pragma unroll
+    for (int d = 0; d < kLoadsPerWave; ++d) {
+        const int q = (wave & 3) + 4 * d;
+        loff[d] = q < kKInstr ? KDma::lane_offset(q, lane)
+                              : (q < kKInstr + kVInstr ? VDma::lane_offset(q - kKInstr, lane) : 0);
+    }
     auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
-    // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j. Always the full phase: a P of zeros (no
-    // previous tile, or one this wave skips) adds nothing, and scores of a skipped or
-    // past-the-end tile are not used.
-    auto mfma = [&](int j) {
-        __builtin_amdgcn_s_setprio(1);
-        mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
-        __builtin_amdgcn_s_setprio(0);
-    };
     auto softmax = [&](int j) {
         if (!skip(j)) {
             tile_softmax<DT>(s, lane, c, j >= nfull, static_cast<int64_t>(j) * kBlockN, key_limit, m_run, l_run, o,
@@ -635,24 +652,47 @@ attn_fwd_pp(FwdArgs a) {
             for (int ks = 0; ks < 4; ++ks) pb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
         }
     };
+    // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j. Always the full phase: a P of zeros (no
+    // previous tile, or one this wave skips) adds nothing, and scores of a skipped or
+    // past-the-end tile are not used.
     if (group == 0) {
         for (int j = 0; j <= ntiles; ++j) {
-            fetch(j);                   // half-step 2j
-            mfma(j);
+            const bool k_next = j + 1 < ntiles, v_cur = j < ntiles;
+            uint16_t* kdst = kbuf[(j + 1) & 1];
+            uint16_t* vdst = vbuf[j & 1];
+            // tiles that reach past n take the clamping path
+            const bool k_whole = (j + 2) * kBlockN <= n32, v_whole = (j + 1) * kBlockN <= n32;
+            auto load = [&](int d) {
+                const int q = wave + 4 * d;  // this wave's share of the tile's instructions
+                if (q < kKInstr) {
+                    if (k_next && k_whole)
+                        load_lds16(rk, lds_address(kdst + 8 * 64 * q), loff[d], (j + 1) * kBlockN * D * 2);
+                    else if (k_next)
+                        KDma::issue_one(rk, kdst, (j + 1) * kBlockN, n32, q, lane);
+                } else if (q < kKInstr + kVInstr) {
+                    const int qv = q - kKInstr;
+                    if (v_cur && v_whole)
+                        load_lds16(rv, lds_address(vdst + 8 * 64 * qv), loff[d], j * kBlockN * D * 2);
+                    else if (v_cur)
+                        VDma::issue_one(rv, vdst, j * kBlockN, n32, qv, lane);
+                }
+            };
+            __builtin_amdgcn_s_setprio(1);  // half-step 2j
+            mfma_phase<D, true, true, kLoadsPerWave>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s, load);
+            __builtin_amdgcn_s_setprio(0);
             __syncthreads();
             if (j < ntiles) softmax(j);  // half-step 2j+1
             landed();
             __syncthreads();
         }
     } else {
-        fetch(0);  // half-step 0
-        __syncthreads();
+        __syncthreads();  // half-step 0
         for (int j = 0; j <= ntiles; ++j) {
-            mfma(j);  // half-step 2j+1
-            landed();
+            __builtin_amdgcn_s_setprio(1);  // half-step 2j+1
+            mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
+            __builtin_amdgcn_s_setprio(0);
             __syncthreads();
             if (j < ntiles) {  // half-step 2j+2
-                fetch(j + 1);
                 softmax(j);
                 __syncthreads();
             }
