@@ -252,7 +252,7 @@ def main():
             ms = bench_gemm(m, n, k, ta, tb)
             flops = 2 * m * n * k
             sec.append({"workload": name, "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
-                        "ms": round(ms, 5), "roofline": roofline("mfma", flops, ms, "gemm_nt_kernel")})
+                        "ms": round(ms, 5), "roofline": roofline("mfma", flops, ms, "gemm_nt_dma_kernel")})
         ms, algo = bench_rope()
         sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
                     "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
@@ -260,9 +260,9 @@ def main():
         try:
             f_ms, b_ms, ff, bf = bench_attention()
             sec.append({"workload": "C4 causal GQA attention fwd B4 S4096 Hq32 Hkv8 D128", "value": round(ff / f_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd")})
+                        "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd_pp")})
             sec.append({"workload": "C4 causal GQA attention bwd B4 S4096 Hq32 Hkv8 D128", "value": round(bf / b_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd")})
+                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq")})
         except Exception as exc:  # reported, never silently replaced by another path
             sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
         line["secondary"] = sec
