@@ -68,24 +68,35 @@ template <> struct Raw8<float> {
 };
 
 // One wavefront per row and one row per wavefront (no grid-stride loop): the row is held
-// in its storage form (32 VGPRs for a 4096-wide BF16 row), so the kernel runs at full
-// occupancy and every wave has its whole row of loads in flight at once; w is re-read per
-// row from L2 (16 KB, shared by every row).
+// in its storage form (32 VGPRs for a 4096-wide BF16 row), so the kernel runs at high
+// occupancy and every wave has its whole row of loads in flight at once. The workgroup
+// stages w in LDS with loads issued together with the rows', so a row costs one memory
+// round trip, not two (x, then w after the reduction).
 template <typename T, int MAXJ>
 __global__ void __launch_bounds__(kRowsThreads)
 rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y,
              float* __restrict__ rstd, int64_t rows, int width, float eps) {
+    extern __shared__ float w_lds[];
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const bool active = row < rows;
     const int chunks = width >> 3;
     const T* xr = x + row * width;
     Raw8<T> xs[MAXJ];
+    if (active) {
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c < chunks) xs[j].load(xr + 8 * c);
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) xs[j].load(xr + 8 * c);
+        }
     }
+    for (int c = threadIdx.x; c < chunks; c += kRowsThreads) {
+        float wv[8];
+        load8(w + 8 * c, wv);
+        store8(w_lds + 8 * c, wv);
+    }
+    __syncthreads();
+    if (!active) return;
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
@@ -107,7 +118,7 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
             float v[8], wv[8], o[8];
             xs[j].pin();
             xs[j].get(v);
-            load8(w + 8 * c, wv);
+            load8(w_lds + 8 * c, wv);
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = (v[e] * r) * wv[e];
             store8(yr + 8 * c, o);
@@ -316,8 +327,9 @@ template <typename T, int MAXJ>
 void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_t rows, int width,
                      float eps, hipStream_t s) {
     const int64_t grid = (rows + kRowsThreads / 64 - 1) / (kRowsThreads / 64);  // one row per wave
-    hipLaunchKernelGGL((rms_fwd_fast<T, MAXJ>), dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads), 0, s,
-                       static_cast<const T*>(x), w, static_cast<T*>(y), rstd, rows, width, eps);
+    hipLaunchKernelGGL((rms_fwd_fast<T, MAXJ>), dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads),
+                       static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x), w,
+                       static_cast<T*>(y), rstd, rows, width, eps);
 }
 
 template <typename T, int MAXJ>
@@ -328,7 +340,9 @@ void launch_bwd_fast(const void* x, const float* w, const void* dy, const float*
                        static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
 }
 
-int parts_fast(int64_t rows) { return grid_for_rows(rows, kBwdThreads / 64, 512); }
+// One 8-wave workgroup per CU is resident (2 waves per SIMD at the fast kernel's register use):
+// a grid of exactly one round of workgroups, each wave walking rows/2048 rows.
+int parts_fast(int64_t rows) { return grid_for_rows(rows, kBwdThreads / 64, 256); }
 int parts_general(int64_t rows) {
     int64_t parts = (rows + 63) / 64;  // at most 64 rows per column chunk
     if (parts > 512) parts = 512;
