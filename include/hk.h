@@ -184,6 +184,20 @@ hk_status hk_rms_norm_backward(hk_context* ctx, const hk_tensor* x, const hk_ten
                                const hk_tensor* dy, const hk_tensor* rstd,
                                hk_tensor* dx, hk_tensor* dw);
 
+/* ---------------------------------------------------------------- softmax rows */
+
+/* Softmax (logarithmic = 0) or log-softmax (logarithmic = 1) over the last axis of a
+ * contiguous F32 tensor of any positive last-axis width; y has x's shape. Reference:
+ * AscendRuntime::softmax / log_softmax, runtime/mod.rs:322-330 (runtime/rows.rs:50-62,
+ * wide_rows.rs:162-210; arithmetic row_programs.rs:135-143). */
+hk_status hk_softmax(hk_context* ctx, const hk_tensor* x, int32_t logarithmic, hk_tensor* y);
+/* Backward from the saved output y: dx = y (dy - sum(y dy)) for softmax,
+ * dx = dy - exp(y) sum(dy) for log-softmax. Reference: AscendRuntime::softmax_backward /
+ * log_softmax_backward, runtime/mod.rs:332-341 (rows.rs:64-79, wide_rows.rs:212-232;
+ * row_programs.rs:152-163). */
+hk_status hk_softmax_backward(hk_context* ctx, const hk_tensor* y, const hk_tensor* dy, int32_t logarithmic,
+                              hk_tensor* dx);
+
 /* ---------------------------------------------------------------- RoPE */
 
 /* Full last-axis rotation with same-row F32 tables (table shape = input shape with

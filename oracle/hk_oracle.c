@@ -509,3 +509,38 @@ void or_causal_mask(int64_t batch, int64_t queries, int64_t keys, uint64_t query
                 out[(b * queries + i) * keys + j] =
                     (key_start + (uint64_t)j > query_start + (uint64_t)i) ? -INFINITY : 0.0f;
 }
+
+/* Row softmax / log-softmax in double over [rows, width] F32 input.
+ * Reference: the host check of rust-ascend-driver/examples/common_rows_validate.rs:55-58
+ * (m = max, exp(x - m), sum; y = e / sum or x - m - ln(sum)), i.e. the arithmetic of
+ * row_programs.rs:135-143. */
+void or_softmax_f64(const float* x, int64_t rows, int64_t width, int logarithmic, double* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* a = x + r * width;
+        double* o = out + r * width;
+        double m = -INFINITY;
+        for (int64_t j = 0; j < width; ++j) m = a[j] > m ? (double)a[j] : m;
+        double sum = 0.0;
+        for (int64_t j = 0; j < width; ++j) sum += exp((double)a[j] - m);
+        for (int64_t j = 0; j < width; ++j)
+            o[j] = logarithmic ? ((double)a[j] - m) - log(sum) : exp((double)a[j] - m) / sum;
+    }
+}
+
+/* Backward from the saved output y. Reference: common_rows_validate.rs:82-85
+ * (row_programs.rs:152-163): softmax dx = y (dy - sum(y dy)); log-softmax
+ * dx = dy - exp(y) sum(dy). */
+void or_softmax_backward_f64(const float* y, const float* dy, int64_t rows, int64_t width, int logarithmic,
+                             double* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* a = y + r * width;
+        const float* g = dy + r * width;
+        double* o = out + r * width;
+        double dot = 0.0;
+        for (int64_t j = 0; j < width; ++j) dot += logarithmic ? (double)g[j] : (double)a[j] * (double)g[j];
+        for (int64_t j = 0; j < width; ++j)
+            o[j] = logarithmic ? (double)g[j] - exp((double)a[j]) * dot : (double)a[j] * ((double)g[j] - dot);
+    }
+}

@@ -33,6 +33,11 @@ a wrong sign or index, or a transposed operand fails at least one check:
   angle-zero identity, the prefix tail bit patterns (NaN/Inf/-0) of
   rotary_programs.rs:224-260, and prefix-with-full-width == full rotation
   (rotary_programs.rs:262-275).
+* ``softmax_f64``/``softmax_backward_f64``: known answers (x = ln[1,2,3] -> [1,2,3]/6,
+  a constant row -> 1/W), rows summing to one / log-sum-exp of zero, invariance to a
+  per-row shift, and torch float64 autograd (the backward must be the forward's
+  vector-Jacobian product) on the reference's own inputs and shapes
+  (examples/common_rows_validate.rs:7-9,100).
 * ``attention_f64``: the closed forms of examples/attention_tensor.rs:22-66
   (orthogonal Q/K -> uniform probabilities) and
   examples/causal_attention_tensor.rs:31-55 (Q=K=0 causal -> running means), the
@@ -95,6 +100,8 @@ def lib():
                                        ctypes.c_double, _int, ctypes.c_uint64, ctypes.c_uint64,
                                        _vp, _vp, _vp, _vp, _vp, _vp]
         L.or_causal_mask.argtypes = [_i64, _i64, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32p]
+        L.or_softmax_f64.argtypes = [_f32p, _i64, _i64, _int, _f64p]
+        L.or_softmax_backward_f64.argtypes = [_f32p, _f32p, _i64, _i64, _int, _f64p]
         _lib = L
     return _lib
 
@@ -298,6 +305,24 @@ def rotary_prefix(x, cos_t, sin_t, width: int, layout: int, backward: bool = Fal
     if rc != 0:
         raise ValueError("invalid rotary prefix spec")
     return y
+
+
+def softmax_f64(x, logarithmic: bool = False) -> np.ndarray:
+    """Last-axis softmax / log-softmax in float64 (common_rows_validate.rs:55-58)."""
+    x = _c32(x)
+    width = x.shape[-1]
+    out = np.empty(x.shape, np.float64)
+    lib().or_softmax_f64(x, x.size // width if width else 0, width, int(logarithmic), out)
+    return out
+
+
+def softmax_backward_f64(y, dy, logarithmic: bool = False) -> np.ndarray:
+    """dX from the saved output (common_rows_validate.rs:82-85)."""
+    y, dy = _c32(y), _c32(dy)
+    width = y.shape[-1]
+    out = np.empty(y.shape, np.float64)
+    lib().or_softmax_backward_f64(y, dy, y.size // width if width else 0, width, int(logarithmic), out)
+    return out
 
 
 def rope_tables(positions, dim: int, theta: float):

@@ -608,6 +608,42 @@ hk_status hk_cast_into(hk_context* h, const hk_tensor* in, hk_tensor* out) {
 
 // ------------------------------------------------------------------ RMSNorm
 
+hk_status hk_softmax(hk_context* h, const hk_tensor* x, int32_t logarithmic, hk_tensor* y) {
+    // Reference: rows.rs:50-62 (layout_for / check_for: contiguous F32, positive width).
+    if (!tensor_ok(x, "X") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    int64_t rows, width;
+    if (!row_layout(x, &rows, &width, "softmax")) return HK_INVALID_ARGUMENT;
+    if (x->dtype != HK_F32) return fail(HK_INVALID_ARGUMENT, "softmax input must be F32");
+    if (y->dtype != HK_F32 || !same_shape(x, y)) return fail(HK_INVALID_ARGUMENT, "softmax output must match the input");
+    if (logarithmic != 0 && logarithmic != 1) return fail(HK_INVALID_ARGUMENT, "logarithmic must be 0 or 1");
+    if (rows > INT32_MAX) return fail(HK_INVALID_ARGUMENT, "softmax supports at most 2^31-1 rows");
+    if (!disjoint({y}, {x})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::softmax_forward(static_cast<const float*>(x->data), static_cast<float*>(y->data), rows, width,
+                                       logarithmic, g.c->stream);
+    return complete(g.c, e, logarithmic ? "log_softmax" : "softmax", rows ? 1 : 0);
+}
+
+hk_status hk_softmax_backward(hk_context* h, const hk_tensor* y, const hk_tensor* dy, int32_t logarithmic,
+                              hk_tensor* dx) {
+    // Reference: rows.rs:64-79.
+    if (!tensor_ok(y, "Y") || !tensor_ok(dy, "dY") || !tensor_ok(dx, "dX")) return HK_INVALID_ARGUMENT;
+    int64_t rows, width;
+    if (!row_layout(y, &rows, &width, "softmax backward")) return HK_INVALID_ARGUMENT;
+    if (y->dtype != HK_F32) return fail(HK_INVALID_ARGUMENT, "softmax backward input must be F32");
+    if (dy->dtype != HK_F32 || !same_shape(dy, y)) return fail(HK_INVALID_ARGUMENT, "dY must match Y");
+    if (dx->dtype != HK_F32 || !same_shape(dx, y)) return fail(HK_INVALID_ARGUMENT, "dX must match Y");
+    if (logarithmic != 0 && logarithmic != 1) return fail(HK_INVALID_ARGUMENT, "logarithmic must be 0 or 1");
+    if (rows > INT32_MAX) return fail(HK_INVALID_ARGUMENT, "softmax supports at most 2^31-1 rows");
+    if (!disjoint({dx}, {y, dy})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::softmax_backward(static_cast<const float*>(y->data), static_cast<const float*>(dy->data),
+                                        static_cast<float*>(dx->data), rows, width, logarithmic, g.c->stream);
+    return complete(g.c, e, logarithmic ? "log_softmax_backward" : "softmax_backward", rows ? 1 : 0);
+}
+
 hk_status hk_rms_norm(hk_context* h, const hk_tensor* x, const hk_tensor* w, double eps, hk_tensor* y,
                       hk_tensor* rstd) {
     // Reference: normalization.rs:153-166 (+ layout_for / epsilon_for, :12-48).

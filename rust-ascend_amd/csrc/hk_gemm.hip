@@ -194,8 +194,7 @@ gemm_nt_kernel(GemmArgs p) {
 //     global chunk the swizzle places at its position (row l/4, chunk (l%4) ^ ((l/16) % 4));
 //   * each step is two 16-wide k slices ("phases"); a phase issues the next slice's fragment
 //     reads, then the current slice's MFMAs, and the compiler may not reorder across phases.
-constexpr int kSBK = 32;       // K per stage
-constexpr int kStages = 4;
+constexpr int kSBK = 32;       // K per stage (four stages)
 __device__ __forceinline__ int swz32(int row, int chunk) {  // element offset in a [rows][32] stage
     return row * kSBK + ((chunk ^ ((row >> 2) & 3)) << 3);
 }

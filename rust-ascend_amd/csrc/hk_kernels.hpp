@@ -40,6 +40,11 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
                      int64_t n, int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s);
 
 // ---- attention (hk_attention.hip)
+// Row softmax / log-softmax over the last axis of contiguous F32 [rows, width] (hk_softmax.hip).
+hipError_t softmax_forward(const float* x, float* y, int64_t rows, int64_t width, int logarithmic, hipStream_t s);
+hipError_t softmax_backward(const float* y, const float* dy, float* dx, int64_t rows, int64_t width, int logarithmic,
+                            hipStream_t s);
+
 struct AttnShape {
     int64_t batch, heads, kv_heads, m, n, d;
     float scale;

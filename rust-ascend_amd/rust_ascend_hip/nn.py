@@ -93,6 +93,32 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return _RmsNorm.apply(x.contiguous(), w.contiguous(), float(eps))
 
 
+class _Softmax(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, logarithmic):
+        y = HipRuntime.log_softmax(x) if logarithmic else HipRuntime.softmax(x)
+        ctx.save_for_backward(y)  # the backward needs only the output
+        ctx.logarithmic = logarithmic
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (y,) = ctx.saved_tensors
+        dy = dy.contiguous().to(y.dtype)
+        dx = HipRuntime.log_softmax_backward(y, dy) if ctx.logarithmic else HipRuntime.softmax_backward(y, dy)
+        return dx, None
+
+
+def softmax(x: torch.Tensor) -> torch.Tensor:
+    """Last-axis softmax of an F32 tensor. Reference: nn::softmax / SoftmaxBackward (src/nn.rs:141-159, 234-278)."""
+    return _Softmax.apply(x.contiguous(), False)
+
+
+def log_softmax(x: torch.Tensor) -> torch.Tensor:
+    """Last-axis log-softmax of an F32 tensor (AscendRuntime::log_softmax, runtime/mod.rs:327-341)."""
+    return _Softmax.apply(x.contiguous(), True)
+
+
 class _Rotary(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, cos, sin, layout, width):

@@ -196,6 +196,38 @@ class HipRuntime:
 
     # ---------------------------------------------------------------- RMSNorm
 
+    # ---------------------------------------------------------------- softmax rows
+
+    @staticmethod
+    def softmax(x):
+        """Row softmax over the last axis (F32). Reference: AscendRuntime::softmax (mod.rs:322-325)."""
+        y = _empty(x.shape, x.dtype, x)
+        _call("hk_softmax", desc(x), 0, desc(y))
+        return y
+
+    @staticmethod
+    def log_softmax(x):
+        """Reference: AscendRuntime::log_softmax (mod.rs:327-330)."""
+        y = _empty(x.shape, x.dtype, x)
+        _call("hk_softmax", desc(x), 1, desc(y))
+        return y
+
+    @staticmethod
+    def softmax_backward(output, grad):
+        """dX from the saved softmax output. Reference: AscendRuntime::softmax_backward (mod.rs:332-335)."""
+        dx = _empty(output.shape, output.dtype, output)
+        _call("hk_softmax_backward", desc(output), desc(grad), 0, desc(dx))
+        return dx
+
+    @staticmethod
+    def log_softmax_backward(output, grad):
+        """Reference: AscendRuntime::log_softmax_backward (mod.rs:338-341)."""
+        dx = _empty(output.shape, output.dtype, output)
+        _call("hk_softmax_backward", desc(output), desc(grad), 1, desc(dx))
+        return dx
+
+    # ---------------------------------------------------------------- RMSNorm
+
     @staticmethod
     def rms_norm(x, weight, epsilon: float):
         """[Y, rstd]. Reference: AscendRuntime::rms_norm (mod.rs:402-408); rstd has one F32 per row."""

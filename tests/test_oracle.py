@@ -304,3 +304,57 @@ def test_attention_magnitudes_bound_the_outputs(oracle):
     np.testing.assert_allclose(rp["dv_mag"], rp["dv"], rtol=1e-12)
     r2 = oracle.attention_f64(q, k, 2 * v, dy, scale=0.2, causal=True, query_start=32, magnitudes=True)
     np.testing.assert_allclose(r2["out_mag"], 2 * r["out_mag"], rtol=1e-12)
+
+
+# ------------------------------------------------------------------ softmax rows
+
+def _reference_row_inputs(rows, width):
+    """The inputs of examples/common_rows_validate.rs:7-9."""
+    i = np.arange(rows * width)
+    x = ((i % 41).astype(np.float32) / np.float32(7.0) - np.float32(2.0)).reshape(rows, width)
+    dy = ((i % 13).astype(np.float32) / np.float32(9.0) - np.float32(0.5)).reshape(rows, width)
+    return x.astype(np.float32), dy.astype(np.float32)
+
+
+def test_softmax_known_answers(oracle):
+    x = np.log(np.array([[1.0, 2.0, 3.0], [5.0, 5.0, 5.0]], np.float64)).astype(np.float32)
+    y = oracle.softmax_f64(x)
+    close(y[0], [1 / 6, 2 / 6, 3 / 6], 1e-7, 1e-7)
+    close(y[1], [1 / 3] * 3, 1e-15, 0)
+    close(oracle.softmax_f64(np.zeros((2, 7), np.float32)), np.full((2, 7), 1 / 7), 1e-15, 0)
+    close(np.exp(oracle.softmax_f64(x, True)), y, 1e-15, 1e-12)
+
+
+@pytest.mark.parametrize("logarithmic", [False, True])
+def test_softmax_invariants(oracle, logarithmic):
+    x = oracle.normal((33, 257), seed=1, stream=40, std=3.0)
+    y = oracle.softmax_f64(x, logarithmic)
+    p = np.exp(y) if logarithmic else y
+    close(p.sum(-1), np.ones(33), 1e-12, 0)                       # rows sum to one
+    shifted = oracle.softmax_f64(x + np.float32(2.0), logarithmic)  # exact shift in float32 here
+    close(shifted, y, 1e-6, 1e-6)
+
+
+@pytest.mark.parametrize("rows,width", [(1, 32), (3, 96), (7, 256), (2, 33)])
+@pytest.mark.parametrize("logarithmic", [False, True])
+def test_softmax_vs_autograd_on_reference_inputs(oracle, rows, width, logarithmic):
+    x, dy = _reference_row_inputs(rows, width)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    fn = torch.log_softmax if logarithmic else torch.softmax
+    yt = fn(xt, dim=-1)
+    yt.backward(torch.tensor(dy, dtype=torch.float64))
+    y = oracle.softmax_f64(x, logarithmic)
+    close(y, yt.detach().numpy(), 1e-12, 1e-12)
+    # the backward takes the saved output, rounded to F32 as a device would store it
+    dx = oracle.softmax_backward_f64(y.astype(np.float32), dy, logarithmic)
+    close(dx, xt.grad.numpy(), 1e-6, 1e-6)
+
+
+def test_softmax_backward_catches_planted_mistakes(oracle):
+    """A sign or a dropped term in the backward breaks the vector-Jacobian identity."""
+    x, dy = _reference_row_inputs(3, 96)
+    y = oracle.softmax_f64(x).astype(np.float32)
+    good = oracle.softmax_backward_f64(y, dy)
+    assert abs(good.sum(-1)).max() < 1e-6             # softmax gradients sum to zero per row
+    wrong = y.astype(np.float64) * dy                  # dropped "- dot" term
+    assert abs(wrong.sum(-1)).max() > 1e-2
