@@ -198,6 +198,25 @@ hk_status hk_softmax(hk_context* ctx, const hk_tensor* x, int32_t logarithmic, h
 hk_status hk_softmax_backward(hk_context* ctx, const hk_tensor* y, const hk_tensor* dy, int32_t logarithmic,
                               hk_tensor* dx);
 
+/* ---------------------------------------------------------------- composed-attention shims */
+
+/* The fused attention entry points apply the mask and the KV-head mapping themselves; these
+ * three serve callers of the reference's composed attention. All F32, contiguous. */
+
+/* out [B, Q, K] F32: -inf where key_start + k > query_start + q, else +0. Q, K > 0; the
+ * absolute positions must not overflow u64 and B*Q*K must fit u32 (CausalMaskSpec::elements,
+ * mask_programs.rs:7-19). Reference: AscendRuntime::causal_mask, runtime/mod.rs:205-206
+ * (mask_programs.rs:20-40). */
+hk_status hk_causal_mask(hk_context* ctx, uint64_t query_start, uint64_t key_start, hk_tensor* out);
+/* x [B, Hkv, N, D] -> y [B, Hq, N, D] with kv_head = q_head / (Hq/Hkv); Hq % Hkv == 0 and both
+ * element counts fit u32 (RepeatKvSpec::elements, heads_programs.rs:5-18). Reference:
+ * AscendRuntime::repeat_kv_heads, runtime/mod.rs:208-209 (runtime/heads.rs:21-28). */
+hk_status hk_repeat_kv_heads(hk_context* ctx, const hk_tensor* x, hk_tensor* y);
+/* dy [B, Hq, N, D] -> dx [B, Hkv, N, D]: the replicas' sum, added in the reference's pairwise
+ * level order. Reference: AscendRuntime::repeat_kv_heads_backward, runtime/mod.rs:210-213
+ * (runtime/heads.rs:29-51). */
+hk_status hk_repeat_kv_heads_backward(hk_context* ctx, const hk_tensor* dy, hk_tensor* dx);
+
 /* ---------------------------------------------------------------- RoPE */
 
 /* Full last-axis rotation with same-row F32 tables (table shape = input shape with

@@ -544,3 +544,28 @@ void or_softmax_backward_f64(const float* y, const float* dy, int64_t rows, int6
             o[j] = logarithmic ? (double)g[j] - exp((double)a[j]) * dot : (double)a[j] * ((double)g[j] - dot);
     }
 }
+
+/* KV-head repetition backward in F32, in the reference's level order: each level adds the
+ * neighbouring groups (2i, 2i+1) of every row and carries an odd last group through, until one
+ * group is left. dy is [rows, groups, width] (rows = B*Hkv, groups = Hq/Hkv, width = N*D).
+ * Reference: rust-ascend-driver/src/tensor/runtime/heads.rs:29-51 with the pair/tail
+ * programs of heads_programs.rs:56-86. */
+void or_repeat_kv_backward(const float* dy, int64_t rows, int64_t groups, int64_t width, float* out) {
+    float* value = (float*)malloc((size_t)(rows * groups * width) * sizeof(float));
+    memcpy(value, dy, (size_t)(rows * groups * width) * sizeof(float));
+    while (groups > 1) {
+        const int64_t next_groups = (groups + 1) / 2;
+        float* next = (float*)malloc((size_t)(rows * next_groups * width) * sizeof(float));
+        for (int64_t r = 0; r < rows; ++r)
+            for (int64_t g = 0; g < next_groups; ++g)
+                for (int64_t c = 0; c < width; ++c) {
+                    const float* src = value + (r * groups + 2 * g) * width + c;
+                    next[(r * next_groups + g) * width + c] = 2 * g + 1 < groups ? src[0] + src[width] : src[0];
+                }
+        free(value);
+        value = next;
+        groups = next_groups;
+    }
+    memcpy(out, value, (size_t)(rows * width) * sizeof(float));
+    free(value);
+}

@@ -38,6 +38,10 @@ a wrong sign or index, or a transposed operand fails at least one check:
   per-row shift, and torch float64 autograd (the backward must be the forward's
   vector-Jacobian product) on the reference's own inputs and shapes
   (examples/common_rows_validate.rs:7-9,100).
+* ``repeat_kv``/``repeat_kv_backward``: the backward is the repeat's transpose (inner products
+  <repeat(x), dy> == <x, backward(dy)> in float64), equals the float64 group sum within
+  rounding, and follows the pairwise level order exactly on inputs where the order decides the
+  float32 result ([1e8, 1, -1e8, 1] sums to 0 pairwise, to 1 left to right).
 * ``attention_f64``: the closed forms of examples/attention_tensor.rs:22-66
   (orthogonal Q/K -> uniform probabilities) and
   examples/causal_attention_tensor.rs:31-55 (Q=K=0 causal -> running means), the
@@ -101,6 +105,7 @@ def lib():
                                        _vp, _vp, _vp, _vp, _vp, _vp]
         L.or_causal_mask.argtypes = [_i64, _i64, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32p]
         L.or_softmax_f64.argtypes = [_f32p, _i64, _i64, _int, _f64p]
+        L.or_repeat_kv_backward.argtypes = [_f32p, _i64, _i64, _i64, _f32p]
         L.or_softmax_backward_f64.argtypes = [_f32p, _f32p, _i64, _i64, _int, _f64p]
         _lib = L
     return _lib
@@ -322,6 +327,22 @@ def softmax_backward_f64(y, dy, logarithmic: bool = False) -> np.ndarray:
     width = y.shape[-1]
     out = np.empty(y.shape, np.float64)
     lib().or_softmax_backward_f64(y, dy, y.size // width if width else 0, width, int(logarithmic), out)
+    return out
+
+
+def repeat_kv(x, query_heads: int) -> np.ndarray:
+    """[B,Hkv,N,D] -> [B,Hq,N,D], kv_head = q_head // (Hq/Hkv) (heads_programs.rs:42-55)."""
+    x = np.asarray(x, np.float32)
+    return np.repeat(x, query_heads // x.shape[1], axis=1)
+
+
+def repeat_kv_backward(dy, kv_heads: int) -> np.ndarray:
+    """[B,Hq,N,D] -> [B,Hkv,N,D], the replicas summed in F32 in the reference's level order
+    (runtime/heads.rs:29-51)."""
+    dy = _c32(dy)
+    b, hq, n, d = dy.shape
+    out = np.empty((b, kv_heads, n, d), np.float32)
+    lib().or_repeat_kv_backward(dy, b * kv_heads, hq // kv_heads, n * d, out)
     return out
 
 

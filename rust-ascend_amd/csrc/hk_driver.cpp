@@ -644,6 +644,70 @@ hk_status hk_softmax_backward(hk_context* h, const hk_tensor* y, const hk_tensor
     return complete(g.c, e, logarithmic ? "log_softmax_backward" : "softmax_backward", rows ? 1 : 0);
 }
 
+hk_status hk_causal_mask(hk_context* h, uint64_t query_start, uint64_t key_start, hk_tensor* out) {
+    // Reference: CausalMaskSpec::elements (mask_programs.rs:7-19), mask.rs via runtime/mod.rs:205-206.
+    if (!tensor_ok(out, "mask")) return HK_INVALID_ARGUMENT;
+    if (out->dtype != HK_F32 || out->rank != 3) return fail(HK_INVALID_ARGUMENT, "causal mask output must be F32 [B,Q,K]");
+    const int64_t batch = out->shape[0], queries = out->shape[1], keys = out->shape[2];
+    if (queries <= 0 || keys <= 0) return fail(HK_INVALID_ARGUMENT, "causal mask requires positive query/key lengths");
+    if (query_start > UINT64_MAX - static_cast<uint64_t>(queries - 1) ||
+        key_start > UINT64_MAX - static_cast<uint64_t>(keys - 1))
+        return fail(HK_INVALID_ARGUMENT, "causal absolute position overflow");
+    if (batch < 0 || numel(out) > static_cast<int64_t>(UINT32_MAX))
+        return fail(HK_INVALID_ARGUMENT, "causal mask domain exceeds u32");
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::causal_mask(static_cast<float*>(out->data), batch, queries, keys, query_start, key_start,
+                                   g.c->stream);
+    return complete(g.c, e, "causal_mask", numel(out) ? 1 : 0);
+}
+
+namespace {
+// [B, H, N, D] F32 with both element counts within u32 (RepeatKvSpec::elements, heads_programs.rs:5-18).
+bool kv_shapes(const hk_tensor* kv, const hk_tensor* qh, const char* kv_name, const char* q_name) {
+    if (kv->dtype != HK_F32 || qh->dtype != HK_F32 || kv->rank != 4 || qh->rank != 4)
+        return fail(HK_INVALID_ARGUMENT, "KV repetition requires F32 [B,Hkv,N,D] %s and [B,Hq,N,D] %s", kv_name, q_name),
+               false;
+    if (kv->shape[0] != qh->shape[0] || kv->shape[2] != qh->shape[2] || kv->shape[3] != qh->shape[3])
+        return fail(HK_INVALID_ARGUMENT, "%s and %s must agree in B, N and D", kv_name, q_name), false;
+    if (kv->shape[1] <= 0 || qh->shape[1] <= 0 || qh->shape[1] % kv->shape[1] != 0)
+        return fail(HK_INVALID_ARGUMENT, "KV repetition requires positive heads and query_heads divisible by kv_heads"),
+               false;
+    if (numel(kv) > static_cast<int64_t>(UINT32_MAX) || numel(qh) > static_cast<int64_t>(UINT32_MAX))
+        return fail(HK_INVALID_ARGUMENT, "KV repetition complete domain exceeds u32"), false;
+    return true;
+}
+}  // namespace
+
+hk_status hk_repeat_kv_heads(hk_context* h, const hk_tensor* x, hk_tensor* y) {
+    // Reference: runtime/heads.rs:21-28.
+    if (!tensor_ok(x, "X") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    if (!kv_shapes(x, y, "X", "Y")) return HK_INVALID_ARGUMENT;
+    if (!disjoint({y}, {x})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::repeat_kv_heads(static_cast<const float*>(x->data), static_cast<float*>(y->data), x->shape[0],
+                                       x->shape[1], y->shape[1], x->shape[2] * x->shape[3], g.c->stream);
+    return complete(g.c, e, "repeat_kv_heads", numel(y) ? 1 : 0);
+}
+
+hk_status hk_repeat_kv_heads_backward(hk_context* h, const hk_tensor* dy, hk_tensor* dx) {
+    // Reference: runtime/heads.rs:29-51.
+    if (!tensor_ok(dy, "dY") || !tensor_ok(dx, "dX")) return HK_INVALID_ARGUMENT;
+    if (!kv_shapes(dx, dy, "dX", "dY")) return HK_INVALID_ARGUMENT;
+    if (!disjoint({dx}, {dy})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t plane = dx->shape[2] * dx->shape[3];
+    hk_status st = ensure_workspace(g.c, hk::repeat_kv_backward_workspace_bytes(dx->shape[0], dx->shape[1],
+                                                                                dy->shape[1], plane));
+    if (st != HK_OK) return st;
+    hipError_t e = hk::repeat_kv_heads_backward(static_cast<const float*>(dy->data), static_cast<float*>(dx->data),
+                                                dx->shape[0], dx->shape[1], dy->shape[1], plane, g.c->workspace,
+                                                g.c->stream);
+    return complete(g.c, e, "repeat_kv_heads_backward", numel(dx) ? 1 : 0);
+}
+
 hk_status hk_rms_norm(hk_context* h, const hk_tensor* x, const hk_tensor* w, double eps, hk_tensor* y,
                       hk_tensor* rstd) {
     // Reference: normalization.rs:153-166 (+ layout_for / epsilon_for, :12-48).

@@ -45,6 +45,15 @@ hipError_t softmax_forward(const float* x, float* y, int64_t rows, int64_t width
 hipError_t softmax_backward(const float* y, const float* dy, float* dx, int64_t rows, int64_t width, int logarithmic,
                             hipStream_t s);
 
+// Composed-attention compatibility kernels (hk_heads.hip); F32, contiguous.
+hipError_t causal_mask(float* out, int64_t batch, int64_t queries, int64_t keys, uint64_t query_start,
+                       uint64_t key_start, hipStream_t s);
+hipError_t repeat_kv_heads(const float* x, float* y, int64_t batch, int64_t kv_heads, int64_t query_heads,
+                           int64_t plane, hipStream_t s);
+size_t repeat_kv_backward_workspace_bytes(int64_t batch, int64_t kv_heads, int64_t query_heads, int64_t plane);
+hipError_t repeat_kv_heads_backward(const float* dy, float* dx, int64_t batch, int64_t kv_heads,
+                                    int64_t query_heads, int64_t plane, void* workspace, hipStream_t s);
+
 struct AttnShape {
     int64_t batch, heads, kv_heads, m, n, d;
     float scale;

@@ -81,6 +81,9 @@ SIGNATURES = {
     "hk_cast_into": [_CTX, _T, _T],
     "hk_softmax": [_CTX, _T, _i32, _T],
     "hk_softmax_backward": [_CTX, _T, _T, _i32, _T],
+    "hk_causal_mask": [_CTX, _u64, _u64, _T],
+    "hk_repeat_kv_heads": [_CTX, _T, _T],
+    "hk_repeat_kv_heads_backward": [_CTX, _T, _T],
     "hk_rms_norm": [_CTX, _T, _T, ctypes.c_double, _T, _T],
     "hk_rms_norm_backward": [_CTX, _T, _T, _T, _T, _T, _T],
     "hk_rotary": [_CTX, _T, _T, _T, _i32, _T],

@@ -194,6 +194,32 @@ class HipRuntime:
         """Reference: AscendRuntime::cast_into (mod.rs:276-279)."""
         _call("hk_cast_into", desc(x), desc(out))
 
+    # ---------------------------------------------------------------- composed-attention shims
+
+    @staticmethod
+    def causal_mask(batch: int, queries: int, keys: int, query_start: int = 0, key_start: int = 0, device=None):
+        """F32 [B,Q,K] additive mask. Reference: AscendRuntime::causal_mask (mod.rs:205-206)."""
+        out = torch.empty((batch, queries, keys), dtype=torch.float32, device=device or torch.device("cuda"))
+        _call("hk_causal_mask", int(query_start), int(key_start), desc(out))
+        return out
+
+    @staticmethod
+    def repeat_kv_heads(x, query_heads: int):
+        """[B,Hkv,N,D] -> [B,Hq,N,D]. Reference: AscendRuntime::repeat_kv_heads (mod.rs:208-209)."""
+        b, _, n, d = x.shape
+        y = _empty((b, int(query_heads), n, d), x.dtype, x)
+        _call("hk_repeat_kv_heads", desc(x), desc(y))
+        return y
+
+    @staticmethod
+    def repeat_kv_heads_backward(input_shape, query_heads: int, grad):
+        """dX [B,Hkv,N,D] from dY [B,Hq,N,D]. Reference: AscendRuntime::repeat_kv_heads_backward (mod.rs:210-213)."""
+        if int(grad.shape[1]) != int(query_heads):
+            raise ValueError("grad must have query_heads heads")
+        dx = _empty(tuple(input_shape), grad.dtype, grad)
+        _call("hk_repeat_kv_heads_backward", desc(grad), desc(dx))
+        return dx
+
     # ---------------------------------------------------------------- RMSNorm
 
     # ---------------------------------------------------------------- softmax rows

@@ -358,3 +358,53 @@ def test_softmax_backward_catches_planted_mistakes(oracle):
     assert abs(good.sum(-1)).max() < 1e-6             # softmax gradients sum to zero per row
     wrong = y.astype(np.float64) * dy                  # dropped "- dot" term
     assert abs(wrong.sum(-1)).max() > 1e-2
+
+
+# ------------------------------------------------------------------ KV-head repetition
+
+def _repeat_case(group):
+    # examples/grouped_attention_tensor.rs:51-53
+    batch, kv, n, d = 2, 3, 5, 7
+    heads = kv * group
+    x = (np.arange(batch * kv * n * d, dtype=np.float32) / 8 - 1).reshape(batch, kv, n, d)
+    dy = ((np.arange(batch * heads * n * d) % 11).astype(np.float32) / 8 - 0.25).reshape(batch, heads, n, d)
+    return x, dy, heads
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 5, 9])
+def test_repeat_kv_reference_cases(oracle, group):
+    x, dy, heads = _repeat_case(group)
+    y = oracle.repeat_kv(x, heads)
+    b, kv, n, d = x.shape
+    for h in range(heads):   # grouped_attention_tensor.rs:58-60: kv head = h / group
+        np.testing.assert_array_equal(y[:, h], x[:, h // group])
+    dx = oracle.repeat_kv_backward(dy, kv)
+    want = dy.astype(np.float64).reshape(b, kv, group, n, d).sum(axis=2)
+    close(dx, want, 5e-4, 5e-4)
+    # the backward is the transpose of the repeat: <repeat(x), dy> == <x, backward(dy)>
+    lhs = float(np.sum(y.astype(np.float64) * dy))
+    rhs = float(np.sum(x.astype(np.float64) * dx))
+    assert abs(lhs - rhs) <= 1e-6 * max(1.0, abs(lhs))
+
+
+def test_repeat_kv_backward_follows_the_pairwise_order(oracle):
+    # [1e8, 1, -1e8, 1]: pairwise (1e8+1) + (-1e8+1) == 0 in float32; left to right gives 1
+    dy = np.array([1e8, 1.0, -1e8, 1.0], np.float32).reshape(1, 4, 1, 1)
+    assert oracle.repeat_kv_backward(dy, 1).item() == 0.0
+    # five groups: ((g0+g1) + (g2+g3)) + g4, the odd group carried through two levels
+    dy = np.array([1.0, 1e8, -1e8, 1.0, 1.0], np.float32).reshape(1, 5, 1, 1)
+    assert oracle.repeat_kv_backward(dy, 1).item() == np.float32(np.float32(1e8) + np.float32(-1e8)) + 1.0
+    # a left-to-right sum (1 + 1e8) - 1e8 + 1 + 1 would give 2.0
+    assert oracle.repeat_kv_backward(dy, 1).item() == 1.0
+
+
+def test_repeat_kv_backward_catches_planted_mistakes(oracle):
+    x, dy, heads = _repeat_case(3)
+    dx = oracle.repeat_kv_backward(dy, 3)
+    want = dy.astype(np.float64).reshape(2, 3, 3, 5, 7).sum(axis=2)
+    wrong_map = dy.astype(np.float64).reshape(2, 3, 3, 5, 7).transpose(0, 2, 1, 3, 4).sum(axis=2)  # h % kv
+    dropped = dy.astype(np.float64).reshape(2, 3, 3, 5, 7)[:, :, :2].sum(axis=2)                  # tail lost
+    close(dx, want, 5e-4, 5e-4)
+    for bad in (wrong_map, dropped):
+        with pytest.raises(AssertionError):
+            close(bad, want, 5e-4, 5e-4)
