@@ -9,10 +9,12 @@
 // Design (MI355X-first, not a translation of the reference's 64x64 Ascend tiles):
 //   * Core kernel: both operands K-contiguous ("NT": A [M,K], B [N,K]). Operands that are
 //     MN-contiguous are first transposed into the workspace by an HBM-bound kernel.
-//   * Workgroup = 4 wavefronts (2x2) computing a BMxBN output tile (256x256 for large
-//     problems; 128 or 64 when a 256 grid would not fill the 256 CUs). Each wave owns a
-//     (BM/2)x(BN/2) block of 32x32 MFMA tiles, v_mfma_f32_32x32x16_bf16, accumulators in
-//     the AGPR half of the register file.
+//   * Large problems (at least one 256x256 tile per CU, K % 64 == 0): gemm_nt_pp_kernel, eight
+//     wavefronts in two groups that alternate between MFMA turns and memory turns.
+//   * Otherwise a workgroup of 4 wavefronts (2x2) computes a BMxBN output tile (256, 128 or 64
+//     when a larger grid would not fill the 256 CUs). Each wave owns a (BM/2)x(BN/2) block of
+//     32x32 MFMA tiles, v_mfma_f32_32x32x16_bf16, accumulators in the AGPR half of the
+//     register file.
 //   * K loop in steps of BK = 64: A and B slices are prefetched from HBM into registers one
 //     step ahead, written to a double-buffered LDS tile (rows of 64 BF16 = 128 B, 16-byte
 //     chunks XOR-swizzled by row%8 so both the row-contiguous writes and the 32-row
@@ -449,6 +451,203 @@ gemm_nt_dma_kernel(GemmArgs p) {
     store_tile<BM, BN, OUT_BF16>(p, acc, tm, tn, g, wm, wn, lr, lk);
 }
 
+// 256x256 output tiles with eight wavefronts in two groups of four that take turns ("ping-pong"):
+// the waves w and w+4 share a SIMD, and while one group issues MFMAs the other moves data (its
+// next operand fragments from LDS into registers, staged tile data from registers into LDS, and
+// the global loads of a later stage), so each SIMD's matrix core is fed by one wave while its
+// partner works the memory pipelines. A workgroup barrier separates the turns.
+//   * Group g (waves 4g..4g+3) computes rows 128g..128g+127 of the tile; wave q of the group
+//     columns 64q..64q+63: 4x2 MFMA tiles of 32x32, 128 accumulators per lane (AGPRs).
+//   * K advances in stages of 64 through two 64 KB LDS slots. A stage row is 64 BF16 = 128 B,
+//     so each global request is a whole 128-byte line (in this access pattern the L2 delivers
+//     26 TB/s to the CUs against 16 TB/s with 64-byte rows). The 16-byte chunks of a row are
+//     XORed with (row/2)%8, so a fragment read (16 consecutive rows at one chunk per 16-lane
+//     group) touches 16 distinct 16-byte bank groups of the 64-bank LDS.
+//   * A stage is consumed in four turns of 32 k (16 MFMAs per wave): group 0 reads the first
+//     half in turn 4s and multiplies it in 4s+1, reads the second half in 4s+2 and multiplies
+//     it in 4s+3; group 1 runs one turn behind. Stage s is read in turns 4s..4s+3 only.
+//   * Tile data travels global -> registers -> LDS: each wave owns eight 1 KB row blocks of a
+//     stage (32 staging registers per lane). In each of its two memory turns of stage s a wave
+//     writes half of its staged stage s+1 into the free slot and reloads those registers with
+//     stage s+2, so the loads are spread evenly over the turns (the vector memory path moves
+//     about 64 bytes per clock per CU, half of what a stage needs at the MFMA rate) and each
+//     has four turns to arrive.
+constexpr int kPPThreads = 512;
+constexpr int kPPTile = 256;
+constexpr int kPK = 64;  // K per stage
+
+__device__ __forceinline__ int swz64(int row, int chunk) {  // element offset in a [rows][64] stage
+    return row * kPK + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
+
+template <bool OUT_BF16>
+__global__ void __launch_bounds__(kPPThreads, 1)
+gemm_nt_pp_kernel(GemmArgs p) {
+    constexpr int kStage = 2 * kPPTile * kPK;  // A rows 0..255, then B rows 0..255
+    __shared__ __attribute__((aligned(1024))) uint16_t slot0[kStage];
+    __shared__ __attribute__((aligned(1024))) uint16_t slot1[kStage];
+
+    const int tiles = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+    constexpr int GROUP = 8;
+    const int per_group = GROUP * p.tiles_n;
+    const int first_m = (bid / per_group) * GROUP;
+    const int gsize = min(p.tiles_m - first_m, GROUP);
+    const int tm = first_m + (bid % per_group) % gsize;
+    const int tn = (bid % per_group) / gsize;
+    const int64_t g = blockIdx.z;
+    const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
+    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int group = wave >> 2, q = wave & 3;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // Rows past M (N) fall outside the buffer ranges and read as zero; they only feed outputs
+    // that are not stored.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, p.m * p.k * 2,
+                                                                        kBufferConfig);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, p.n * p.k * 2,
+                                                                        kBufferConfig);
+    // Block d (0..7) of this wave is the 8-row block wave + 8d of a stage: blocks 0..31 are A
+    // rows, 32..63 B rows, so blocks 0..3 come from A and 4..7 from B. Lane l owns row l/8,
+    // chunk position l%8 of the block, which holds the global chunk the swizzle puts there (the
+    // block's parity, that of the wave, sets bit 2 of the row's XOR).
+    const int r_in = lane >> 3;
+    const int src_chunk = (lane & 7) ^ ((4 * (wave & 1) + (r_in >> 1)) & 7);
+    const int voff = (r_in * p.k + src_chunk * 8) * 2;
+    u32x4_t stg[8];
+    auto gload = [&](int kt, int d) __attribute__((always_inline)) {
+        const int blk = wave + 8 * d;
+        if (d < 4)
+            stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     ra, voff, ((tm * kPPTile + 8 * blk) * p.k + kt * kPK) * 2, 0));
+        else
+            stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rb, voff, ((tn * kPPTile + 8 * (blk - 32)) * p.k + kt * kPK) * 2, 0));
+    };
+    const int wlane = wave * 8 * kPK + lane * 8;  // element offset of this lane's chunk in block d = 0
+    auto lwrite = [&](uint16_t* slot, int d) __attribute__((always_inline)) {
+        *reinterpret_cast<u32x4_t*>(slot + wlane + d * 64 * kPK) = stg[d];
+    };
+
+    // Fragments of one half stage (k slices 2h and 2h+1): A fragment i, B fragment j.
+    const int a_row = 128 * group + lr, b_row = kPPTile + 64 * q + lr;
+    bf16x8_t fa[2][4], fb[2][2];
+    auto read = [&](const uint16_t* slot, int h) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int c = 2 * (2 * h + t) + lk;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[t][i] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 32 * i, c));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fb[t][j] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 32 * j, c));
+        }
+    };
+
+    f32x16_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    // The accumulators live in the AGPR file, the fragments and staging data in VGPRs.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) asm volatile("" : "+a"(acc[i][j]));
+
+    auto compute = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(fa[t][i]));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(fb[t][j]));
+        }
+        phase_fence();
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t][j], fa[t][i], acc[i][j], 0, 0, 0);
+        phase_fence();
+    };
+
+    // Memory turn h of stage s (slot R; the other slot W is free from turn 4s on): staged
+    // blocks 4h..4h+3 of stage s+1 go to W, those registers are reloaded with stage s+2, and
+    // the fragments of half h of stage s are read. Near the end the loads repeat the last
+    // stage and the writes land in a slot that is no longer read: every turn issues the same
+    // loads, so the compiler's wait counts stay those of the steady state (a wave's loads of
+    // the other half, issued two turns later, may remain in flight).
+    const int nk = p.k / kPK;
+    auto memory_turn = [&](const uint16_t* R, uint16_t* W, int s, int h) __attribute__((always_inline)) {
+#pragma unroll
+        for (int d = 4 * h; d < 4 * h + 4; ++d) lwrite(W, d);
+        const int ahead = s + 2 < nk ? s + 2 : nk - 1;
+#pragma unroll
+        for (int d = 4 * h; d < 4 * h + 4; ++d) gload(ahead, d);
+        read(R, h);
+    };
+    auto stage = [&](const uint16_t* R, uint16_t* W, int s) __attribute__((always_inline)) {
+        stage_barrier<63>();
+        memory_turn(R, W, s, 0);
+        stage_barrier<63>();
+        compute();
+        stage_barrier<63>();
+        memory_turn(R, W, s, 1);
+        stage_barrier<63>();
+        compute();
+    };
+
+    // Prologue: stage 0 into slot 0, stage 1 into the staging registers.
+#pragma unroll
+    for (int d = 0; d < 8; ++d) gload(0, d);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) lwrite(slot0, d);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) gload(nk > 1 ? 1 : 0, d);
+    if (group == 1) stage_barrier<63>();  // turn 0: group 1 has nothing to multiply yet
+    int s = 0;
+    do {
+        stage(slot0, slot1, s);
+        if (s + 1 < nk) stage(slot1, slot0, s + 1);
+        s += 2;
+    } while (s < nk);
+    if (group == 0) stage_barrier<63>();  // the turn in which group 1 multiplies the last half stage
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = tm * kPPTile + 128 * group + 32 * i + lr;
+        if (m >= p.m) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int grp = 0; grp < 4; ++grp) {
+                const int n = tn * kPPTile + 64 * q + 32 * j + grp * 8 + lk * 4;
+                if (n >= p.n) continue;
+                const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
+                if constexpr (OUT_BF16) {
+                    u32x2_t w = {pack_bf16x2(acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1]),
+                                 pack_bf16x2(acc[i][j][grp * 4 + 2], acc[i][j][grp * 4 + 3])};
+                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = w;
+                } else {
+                    f32x4_t w = {acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1], acc[i][j][grp * 4 + 2],
+                                 acc[i][j][grp * 4 + 3]};
+                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.c) + off) = w;
+                }
+            }
+        }
+    }
+}
+
 // out[g][c][r] = in[g][r][c] for BF16, 64x64 tiles through LDS (padded rows).
 __global__ void __launch_bounds__(256)
 transpose_bf16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int64_t rows, int64_t cols) {
@@ -478,7 +677,10 @@ void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
     // the global->LDS kernel needs whole K steps and 32-bit byte offsets into A and B
     const bool whole_steps = p.k % kSBK == 0 && p.k > 0 && static_cast<int64_t>(p.m) * p.k * 2 < (int64_t{1} << 31) &&
                              static_cast<int64_t>(p.n) * p.k * 2 < (int64_t{1} << 31);
-    if (whole_steps && out_bf16)
+    if (whole_steps && p.k % kPK == 0 && BM == kPPTile && BN == kPPTile) {
+        if (out_bf16) hipLaunchKernelGGL((gemm_nt_pp_kernel<true>), grid, dim3(kPPThreads), 0, s, p);
+        else hipLaunchKernelGGL((gemm_nt_pp_kernel<false>), grid, dim3(kPPThreads), 0, s, p);
+    } else if (whole_steps && out_bf16)
         hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
     else if (whole_steps)
         hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, false>), grid, dim3(kThreads), 0, s, p);
