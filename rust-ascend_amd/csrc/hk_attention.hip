@@ -629,12 +629,15 @@ attn_fwd_pp(FwdArgs a) {
     // during it. The leading group runs MFMA phase t at half-step 2t and softmax t at 2t+1; the
     // lagging group runs them one half-step later. Each group's schedule is straight-line code
     // (two copies of the loop), so the values that live across phases stay in their registers.
-    // The leading group's MFMA phase t also issues the loads of K_{t+1} and V_t into the
-    // buffers read two half-steps earlier (its four waves share the tile's load instructions);
-    // every wave waits for its loads before the barrier that ends half-step 2t+1.
+    // The loads of K_{t+1} and V_t (into the buffers read two half-steps earlier) go out in
+    // half-step 2t from the lagging group, which is then in its softmax phase: the wave that
+    // feeds the matrix core issues nothing but MFMAs and LDS reads (vector memory instructions
+    // in its stream would hold back the MFMAs behind them). The lagging group's four waves
+    // share the tile's load instructions and wait for them before the barrier that ends
+    // half-step 2t+1.
     constexpr int kKInstr = KDma::kInstr, kVInstr = VDma::kInstr;
     constexpr int kLoadsPerWave = (kKInstr + kVInstr + 3) / 4;
-    // lane offsets of this wave's load instructions (leading group only), for whole tiles
+    // lane offsets of this wave's load instructions, for whole tiles
     int loff[kLoadsPerWave];
 #pragma unroll
     for (int d = 0; d < kLoadsPerWave; ++d) {
@@ -655,48 +658,56 @@ attn_fwd_pp(FwdArgs a) {
     // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j. Always the full phase: a P of zeros (no
     // previous tile, or one this wave skips) adds nothing, and scores of a skipped or
     // past-the-end tile are not used.
+    // Loads of half-step 2j: K_{j+1} and V_j (tiles that reach past n take the clamping path).
+    auto tile_loads = [&](int j) {
+        const bool k_next = j + 1 < ntiles, v_cur = j < ntiles;
+        uint16_t* kdst = kbuf[(j + 1) & 1];
+        uint16_t* vdst = vbuf[j & 1];
+        const bool k_whole = (j + 2) * kBlockN <= n32, v_whole = (j + 1) * kBlockN <= n32;
+#pragma unroll
+        for (int d = 0; d < kLoadsPerWave; ++d) {
+            const int q = (wave & 3) + 4 * d;  // this wave's share of the tile's instructions
+            if (q < kKInstr) {
+                if (k_next && k_whole)
+                    load_lds16(rk, lds_address(kdst + 8 * 64 * q), loff[d], (j + 1) * kBlockN * D * 2);
+                else if (k_next)
+                    KDma::issue_one(rk, kdst, (j + 1) * kBlockN, n32, q, lane);
+            } else if (q < kKInstr + kVInstr) {
+                const int qv = q - kKInstr;
+                if (v_cur && v_whole)
+                    load_lds16(rv, lds_address(vdst + 8 * 64 * qv), loff[d], j * kBlockN * D * 2);
+                else if (v_cur)
+                    VDma::issue_one(rv, vdst, j * kBlockN, n32, qv, lane);
+            }
+        }
+    };
+    // The barriers between half-steps wait for LDS accesses only (lds_barrier), so the tile
+    // loads stay in flight from their half-step 2t to the end of 2t+1.
     if (group == 0) {
         for (int j = 0; j <= ntiles; ++j) {
-            const bool k_next = j + 1 < ntiles, v_cur = j < ntiles;
-            uint16_t* kdst = kbuf[(j + 1) & 1];
-            uint16_t* vdst = vbuf[j & 1];
-            // tiles that reach past n take the clamping path
-            const bool k_whole = (j + 2) * kBlockN <= n32, v_whole = (j + 1) * kBlockN <= n32;
-            auto load = [&](int d) {
-                const int q = wave + 4 * d;  // this wave's share of the tile's instructions
-                if (q < kKInstr) {
-                    if (k_next && k_whole)
-                        load_lds16(rk, lds_address(kdst + 8 * 64 * q), loff[d], (j + 1) * kBlockN * D * 2);
-                    else if (k_next)
-                        KDma::issue_one(rk, kdst, (j + 1) * kBlockN, n32, q, lane);
-                } else if (q < kKInstr + kVInstr) {
-                    const int qv = q - kKInstr;
-                    if (v_cur && v_whole)
-                        load_lds16(rv, lds_address(vdst + 8 * 64 * qv), loff[d], j * kBlockN * D * 2);
-                    else if (v_cur)
-                        VDma::issue_one(rv, vdst, j * kBlockN, n32, qv, lane);
-                }
-            };
             __builtin_amdgcn_s_setprio(1);  // half-step 2j
-            mfma_phase<D, true, true, kLoadsPerWave>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s, load);
+            mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
             __builtin_amdgcn_s_setprio(0);
-            __syncthreads();
+            lds_barrier();
             if (j < ntiles) softmax(j);  // half-step 2j+1
-            landed();
-            __syncthreads();
+            lds_barrier();
         }
     } else {
-        __syncthreads();  // half-step 0
+        tile_loads(0);
+        lds_barrier();  // half-step 0
         for (int j = 0; j <= ntiles; ++j) {
             __builtin_amdgcn_s_setprio(1);  // half-step 2j+1
             mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
             __builtin_amdgcn_s_setprio(0);
-            __syncthreads();
+            landed();
+            lds_barrier();
             if (j < ntiles) {  // half-step 2j+2
+                tile_loads(j + 1);
                 softmax(j);
-                __syncthreads();
+                lds_barrier();
             }
         }
+        landed();
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -762,11 +773,12 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
 // ---------------------------------------------------------------------------- backward
 //
 // Pre-pass: rowstat[bh, i] = sum_d dO[i, d] * O[i, d] (F32). With O = P V this equals
-// sum_j P_ij dP_ij, the softmax-backward row term of row_programs.rs:152-163.
+// sum_j P_ij dP_ij, the softmax-backward row term of row_programs.rs:152-163. It also writes
+// lse2 = lse * log2(e), the form in which the gradient kernels use the row's log-sum-exp.
 template <int D>
 __global__ void __launch_bounds__(256)
-attn_bwd_rowstat(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout, float* __restrict__ stat,
-                 int64_t rows) {
+attn_bwd_rowstat(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+                 float* __restrict__ stat, float* __restrict__ lse2, int64_t rows) {
     constexpr int kLanesPerRow = D / 8;  // each lane reads 8 elements
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t row = gid / kLanesPerRow;
@@ -781,7 +793,10 @@ attn_bwd_rowstat(const uint16_t* __restrict__ o, const uint16_t* __restrict__ do
     }
 #pragma unroll
     for (int off = kLanesPerRow / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanesPerRow);
-    if (row < rows && part == 0) stat[row] = s;
+    if (row < rows && part == 0) {
+        stat[row] = s;
+        lse2[row] = lse[row] * kLog2e;
+    }
 }
 
 struct BwdArgs {
@@ -789,7 +804,7 @@ struct BwdArgs {
     const uint16_t* k;
     const uint16_t* v;
     const uint16_t* dout;
-    const float* lse;
+    const float* lse2;  // lse * log2(e), per row
     const float* stat;
     void* dq;
     void* dk;
@@ -802,29 +817,29 @@ struct BwdArgs {
     int blocks;  // key blocks (dK/dV kernel) or query blocks (dQ kernel) per head
 };
 
-// Rows [row0, row0+rows) of a [*, D] matrix -> LDS [rows][DP] through registers (rows past
-// `limit` clamp to limit-1; columns >= D are zero).
-template <int D, int DP, int ROWS>
-struct RowsLoader {
-    static constexpr int kChunks = DP / 8;
-    static constexpr int kPerThread = ROWS * kChunks / kThreads;
-    u32x4_t r[kPerThread];
-    __device__ __forceinline__ void load(const uint16_t* base, int64_t row0, int64_t limit, int t) {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int idx = t + i * kThreads;
-            const int row = idx / kChunks, chunk = idx % kChunks;
-            int64_t gr = row0 + row;
-            gr = gr < limit ? gr : limit - 1;
-            r[i] = (chunk * 8 < D) ? *reinterpret_cast<const u32x4_t*>(base + gr * D + chunk * 8) : u32x4_t{0, 0, 0, 0};
-        }
+// A [64][DP] tile (tile_off<DP> swizzle) of rows row0 .. row0+63 of a row-major [*, D] BF16
+// matrix, filled through the global->LDS path: DP / 8 instructions of 1 KB, instruction q
+// covering tile rows (512 / DP) * q onwards. Lane l lands at tile position 512 q + 8 l and so
+// fetches the global chunk the swizzle puts there. The row offset is part of the per-lane
+// offset, which the hardware checks against the buffer size: rows past the end read as zero
+// (as do, for D < DP, the pad chunks, given an offset past any buffer). Wave w issues the
+// instructions q = w, w + 4, ..., which all see the same swizzle, so one lane offset serves.
+template <int D, int DP>
+struct SwzTileDma {
+    static constexpr int kInstr = DP / 8;
+    static constexpr int kPerWave = kInstr / 4;
+    static constexpr int kRowsPerInstr = 512 / DP;
+    __device__ __forceinline__ static int lane_offset(int wave, int lane) {
+        constexpr int kLanesPerRow = DP / 8;
+        const int r_in = lane / kLanesPerRow, pchunk = lane % kLanesPerRow;
+        const int c = pchunk ^ tile_swz<DP>(kRowsPerInstr * wave + r_in);
+        return c * 8 < D ? (r_in * D + c * 8) * 2 : 0x7fff0000;
     }
-    __device__ __forceinline__ void store(uint16_t* tile, int t) const {
+    __device__ __forceinline__ static void issue(i32x4_t rsrc, uint32_t tile_lds, int row0, int voff, int wave) {
 #pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int idx = t + i * kThreads;
-            const int row = idx / kChunks, chunk = idx % kChunks;
-            *reinterpret_cast<u32x4_t*>(tile + tile_off<DP>(row, chunk * 8)) = r[i];
+        for (int i = 0; i < kPerWave; ++i) {
+            const int q = wave + 4 * i;
+            load_lds16(rsrc, tile_lds + 1024 * q, voff + (row0 + kRowsPerInstr * q) * D * 2, 0);
         }
     }
 };
@@ -852,6 +867,32 @@ __device__ __forceinline__ void store_row4(void* base, bool bf16_out, int64_t ro
     }
 }
 
+// N MFMAs, MFMA i taking the LDS operand fetch(i): the operand of MFMA i + kAhead is read while
+// MFMA i runs, through a ring of kAhead + 1 registers, so no MFMA waits on an LDS round trip
+// (left to itself, with the registers of these kernels in use, the compiler reads each
+// operand into one register right before its MFMA). The fences and the empty asm are those of
+// mfma_phase.
+template <int N, class Fetch, class Mma>
+__device__ __forceinline__ void mfma_ring(Fetch&& fetch, Mma&& mma) {
+    constexpr int R = kAhead + 1;
+    bf16x8_t ring[R];
+#pragma unroll
+    for (int i = 0; i < kAhead && i < N; ++i) ring[i % R] = fetch(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (i + kAhead < N) ring[(i + kAhead) % R] = fetch(i + kAhead);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8_t x = ring[i % R];
+        asm volatile("" : "+v"(x));
+        mma(i, x);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+__device__ __forceinline__ uint32_t lds_address_f(const float* p) {
+    return lds_address(reinterpret_cast<const uint16_t*>(p));
+}
+
 constexpr int kQStep = 64;    // queries per step of the dK/dV kernel
 constexpr int kKBlock = 128;  // keys per dK/dV workgroup (4 waves x 32)
 
@@ -861,16 +902,21 @@ constexpr int kKBlock = 128;  // keys per dK/dV workgroup (4 waves x 32)
 //   as columns, so the accumulators (keys in lanes) are directly the B operands of
 //   dV^T += dO^T P and dK^T += Q^T dS, whose A operands (dO^T, Q^T) come from the row-major
 //   Q and dO tiles through transposing LDS reads.
+//   The Q/dO tiles and the rows' statistics of step it+1 are fetched straight into LDS (no
+//   staging registers) while step it is computed, and waited for before the barrier that ends
+//   step it.
 template <int D>
 __global__ void __launch_bounds__(kThreads, 1)
 attn_bwd_dkdv(BwdArgs a) {
     constexpr int DP = D < 32 ? 32 : D;
     constexpr int KS = DP / 16;
     constexpr int DT = DP / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t tiles[2][2][kQStep * DP];  // [buf][Q, dO]
-    __shared__ __attribute__((aligned(16))) float stats[2][2][kQStep];         // [buf][lse*log2e, rowstat]
+    using TDma = SwzTileDma<D, DP>;
+    __shared__ __attribute__((aligned(1024))) uint16_t tiles[2][2][kQStep * DP];  // [buf][Q, dO]
+    __shared__ __attribute__((aligned(256))) float stats[2][2][kQStep];          // [buf][lse*log2e, rowstat]
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int lq = lane & 31, lg = lane >> 5;
     // logical order: (batch, KV head), key block heaviest first -- the workgroups resident on
     // one XCD read the same Q / dO heads
@@ -896,12 +942,15 @@ attn_bwd_dkdv(BwdArgs a) {
     settle(vf);
     f32x16_t dk[DT], dv[DT];
 #pragma unroll
-    for (int i = 0; i < DT; ++i)
+    for (int i = 0; i < DT; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             dk[i][v] = 0.0f;
             dv[i][v] = 0.0f;
         }
+        asm volatile("" : "+a"(dk[i]));  // the accumulators live in the AGPR file
+        asm volatile("" : "+a"(dv[i]));
+    }
 
     // query steps that can see a key of this block: causal -> from the block's first key on
     int64_t qfirst = 0;
@@ -913,59 +962,59 @@ attn_bwd_dkdv(BwdArgs a) {
     const int nsteps_head = qfirst < a.m ? static_cast<int>((a.m + kQStep - 1) / kQStep) - step0 : 0;
     const int total = nsteps_head * static_cast<int>(group);
 
-    RowsLoader<D, DP, kQStep> lq_ld, ldo;
-    float st_lse = 0.0f, st_stat = 0.0f;  // thread t < 64 prefetches row t's statistics
-    auto load_step = [&](int it) {
-        const int64_t h = kvh * group + it / nsteps_head;
-        const int64_t q0 = static_cast<int64_t>(step0 + it % nsteps_head) * kQStep;
-        const int64_t bh = b * a.heads + h;
-        lq_ld.load(a.q + bh * a.m * D, q0, a.m, t);
-        ldo.load(a.dout + bh * a.m * D, q0, a.m, t);
-        if (t < kQStep) {
-            const int64_t qi = q0 + t < a.m ? q0 + t : a.m - 1;
-            st_lse = a.lse[bh * a.m + qi] * kLog2e;
-            st_stat = a.stat[bh * a.m + qi];
+    const int tile_voff = TDma::lane_offset(wave, lane);
+    const int m32 = static_cast<int>(a.m);  // the launcher keeps m * D * 2 below 2^31
+    // Loads of step it into buffer buf: this wave's share of the Q and dO tiles; waves 0 and 1
+    // also fetch the 64 rows' lse*log2(e) and row statistic (rows past m read as zero).
+    auto issue_step = [&](int it, int buf) {
+        const int64_t bh = b * a.heads + kvh * group + it / nsteps_head;
+        const int q0 = (step0 + it % nsteps_head) * kQStep;
+        const i32x4_t rq = buffer_resource(a.q + bh * a.m * D, m32 * D * 2);
+        const i32x4_t ro = buffer_resource(a.dout + bh * a.m * D, m32 * D * 2);
+        TDma::issue(rq, lds_address(tiles[buf][0]), q0, tile_voff, wave);
+        TDma::issue(ro, lds_address(tiles[buf][1]), q0, tile_voff, wave);
+        if (wave < 2) {
+            const float* src = (wave == 0 ? a.lse2 : a.stat) + bh * a.m;
+            load_lds4(buffer_resource(src, m32 * 4), lds_address_f(stats[buf][wave]), (q0 + lane) * 4, 0);
         }
     };
-    auto store_step = [&](int buf) {
-        lq_ld.store(tiles[buf][0], t);
-        ldo.store(tiles[buf][1], t);
-        if (t < kQStep) {
-            stats[buf][0][t] = st_lse;
-            stats[buf][1][t] = st_stat;
-        }
-    };
-    if (total > 0) {
-        load_step(0);
-        store_step(0);
-        if (total > 1) load_step(1);
-    }
-    __syncthreads();
+    auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    if (total > 0) issue_step(0, 0);
+    landed();
+    lds_barrier();
 
     for (int it = 0; it < total; ++it) {
         const int cur = it & 1;
+        // buffer cur^1 was last read in step it-1, which the previous barrier closed
+        if (it + 1 < total) issue_step(it + 1, cur ^ 1);
         const int64_t q0 = static_cast<int64_t>(step0 + it % nsteps_head) * kQStep;
         const uint16_t* Qt = tiles[cur][0];
         const uint16_t* Ot = tiles[cur][1];
         const bool skip = a.causal && (n0w > q0 + kQStep - 1 + a.diag);
         if (!skip) {
+            // S (even i) and dP (odd i) for query tiles qt, k slices ks: MFMA i = 4 ks + 2 qt + which
             f32x16_t s[2], dp[2];
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    s[qt][v] = 0.0f;
-                    dp[qt][v] = 0.0f;
-                }
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    s[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Qt, 32 * qt + lq, 2 * ks + lg),
-                                                                    kf[ks], s[qt], 0, 0, 0);
-                    dp[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Ot, 32 * qt + lq, 2 * ks + lg),
-                                                                     vf[ks], dp[qt], 0, 0, 0);
-                }
-            }
-            // P and dS; lane holds key my_key, queries q0 + 32*qt + 8*(v/4) + 4*lg + v%4
+            const f32x16_t zero = {};
+            mfma_ring<4 * KS>(
+                [&](int i) {
+                    const int ks = i >> 2, qt = (i >> 1) & 1;
+                    return tile_read16<DP>((i & 1) ? Ot : Qt, 32 * qt + lq, 2 * ks + lg);
+                },
+                [&](int i, bf16x8_t x) {
+                    const int ks = i >> 2, qt = (i >> 1) & 1;
+                    if (i & 1) dp[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, vf[ks], ks == 0 ? zero : dp[qt], 0, 0, 0);
+                    else s[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, kf[ks], ks == 0 ? zero : s[qt], 0, 0, 0);
+                });
+            // P and dS; lane holds key my_key, queries q0 + 32*qt + 8*(v/4) + 4*lg + v%4. Steps
+            // whose 64 queries all see this wave's 32 keys (the common case) skip the mask; the
+            // others test one 32-bit offset per element: query q0 + qq sees my_key iff
+            // qq + rel >= 0 (causal), qq < qlim and my_key < n.
+            const bool full = (!a.causal || q0 + a.diag >= n0w + 31) && q0 + kQStep <= a.m && n0w + 32 <= a.n;
+            int64_t rel64 = q0 + a.diag - my_key;
+            rel64 = rel64 < -(int64_t{1} << 30) ? -(int64_t{1} << 30) : (rel64 > (int64_t{1} << 30) ? (int64_t{1} << 30) : rel64);
+            const int rel = a.causal ? static_cast<int>(rel64) : (1 << 30);
+            const int qlim = static_cast<int>(a.m - q0 < kQStep ? a.m - q0 : kQStep);
+            const bool key_ok = my_key < a.n;
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
@@ -976,33 +1025,37 @@ attn_bwd_dkdv(BwdArgs a) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int v = 4 * g4 + e;
-                        const int64_t query = q0 + qi + e;
-                        const bool vis = query < a.m && my_key < a.n && (!a.causal || my_key <= query + a.diag);
-                        const float p = vis ? fast_exp2(s[qt][v] * a.scale_log2 - l4[e]) : 0.0f;
+                        float p = fast_exp2(__builtin_fmaf(s[qt][v], a.scale_log2, -l4[e]));
+                        if (!full) {
+                            const int qq = qi + e;
+                            p = key_ok && qq < qlim && qq + rel >= 0 ? p : 0.0f;
+                        }
                         s[qt][v] = p;
                         dp[qt][v] = a.scale * (p * (dp[qt][v] - d4[e]));
                     }
                 }
-            // dV^T += dO^T P ; dK^T += Q^T dS  (k = 64 queries in 4 steps of 16)
+            // dV^T += dO^T P ; dK^T += Q^T dS  (k = 64 queries in 4 steps of 16):
+            // MFMA i = 2 (DT ks + dt) + which, which 0: dV, 1: dK
+            bf16x8_t pb[4], sb[4];
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8_t pb = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
-                const bf16x8_t sb = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
-                const int kb0 = 16 * ks + 4 * lg;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Ot, lane, kb0, kb0 + 8, 32 * dt),
-                                                                     pb, dv[dt], 0, 0, 0);
-                    dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Qt, lane, kb0, kb0 + 8, 32 * dt),
-                                                                     sb, dk[dt], 0, 0, 0);
-                }
+                pb[ks] = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
+                sb[ks] = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
             }
+            mfma_ring<8 * DT>(
+                [&](int i) {
+                    const int ks = i / (2 * DT), dt = (i >> 1) % DT;
+                    const int kb0 = 16 * ks + 4 * lg;
+                    return tile_read_tr<DP>((i & 1) ? Qt : Ot, lane, kb0, kb0 + 8, 32 * dt);
+                },
+                [&](int i, bf16x8_t x) {
+                    const int ks = i / (2 * DT), dt = (i >> 1) % DT;
+                    if (i & 1) dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[ks], dk[dt], 0, 0, 0);
+                    else dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, pb[ks], dv[dt], 0, 0, 0);
+                });
         }
-        if (it + 1 < total) {
-            store_step(cur ^ 1);
-            if (it + 2 < total) load_step(it + 2);
-        }
-        __syncthreads();
+        landed();
+        lds_barrier();
     }
 
     if (my_key < a.n) {
@@ -1023,16 +1076,19 @@ attn_bwd_dkdv(BwdArgs a) {
 // dQ of 128 queries of one (batch, head), looping over 64-key tiles up to the diagonal:
 // S^T = K Q^T and dP^T = V dO^T with keys as rows (each lane owns one query, so the softmax
 // row statistics are per-lane scalars), dS^T is the B operand of dQ^T += K^T dS^T with K^T
-// read from the row-major K tile through transposing LDS reads.
+// read from the row-major K tile through transposing LDS reads. The K/V tiles of step j+1 are
+// fetched straight into LDS while step j is computed.
 template <int D>
 __global__ void __launch_bounds__(kThreads, 1)
 attn_bwd_dq(BwdArgs a) {
     constexpr int DP = D < 32 ? 32 : D;
     constexpr int KS = DP / 16;
     constexpr int DT = DP / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][kBlockN * DP];  // [buf][K, V]
+    using TDma = SwzTileDma<D, DP>;
+    __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2][kBlockN * DP];  // [buf][K, V]
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int lq = lane & 31, lg = lane >> 5;
     // same logical order as the forward kernel: KV head group, query block heaviest first,
     // query head in the group
@@ -1054,7 +1110,7 @@ attn_bwd_dq(BwdArgs a) {
     bf16x8_t qf[KS], of[KS];
     load_row_operand<D, KS>(a.q + static_cast<int64_t>(bh) * a.m * D, qr, lg, qf);
     load_row_operand<D, KS>(a.dout + static_cast<int64_t>(bh) * a.m * D, qr, lg, of);
-    float lse2 = a.lse[static_cast<int64_t>(bh) * a.m + qr] * kLog2e;
+    float lse2 = a.lse2[static_cast<int64_t>(bh) * a.m + qr];
     float rstat = a.stat[static_cast<int64_t>(bh) * a.m + qr];
     settle(qf);
     settle(of);
@@ -1063,9 +1119,11 @@ attn_bwd_dq(BwdArgs a) {
 
     f32x16_t dq[DT];
 #pragma unroll
-    for (int i = 0; i < DT; ++i)
+    for (int i = 0; i < DT; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) dq[i][v] = 0.0f;
+        asm volatile("" : "+a"(dq[i]));
+    }
 
     int64_t kv_end = a.n;
     if (a.causal) {
@@ -1074,70 +1132,78 @@ attn_bwd_dq(BwdArgs a) {
     }
     const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
 
-    TileLoader<D, DP> lk, lv;
-    if (ntiles > 0) {
-        lk.load(K, 0, a.n, t);
-        lv.load(V, 0, a.n, t);
-        lk.store(lds[0][0], t);
-        lv.store(lds[0][1], t);
-        if (ntiles > 1) {
-            lk.load(K, kBlockN, a.n, t);
-            lv.load(V, kBlockN, a.n, t);
-        }
-    }
-    __syncthreads();
+    const int tile_voff = TDma::lane_offset(wave, lane);
+    const int n32 = static_cast<int>(a.n);  // the launcher keeps n * D * 2 below 2^31
+    const i32x4_t rk = buffer_resource(K, n32 * D * 2);
+    const i32x4_t rv = buffer_resource(V, n32 * D * 2);
+    auto issue_tile = [&](int j, int buf) {
+        TDma::issue(rk, lds_address(lds[buf][0]), j * kBlockN, tile_voff, wave);
+        TDma::issue(rv, lds_address(lds[buf][1]), j * kBlockN, tile_voff, wave);
+    };
+    auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    if (ntiles > 0) issue_tile(0, 0);
+    landed();
+    lds_barrier();
 
     for (int j = 0; j < ntiles; ++j) {
         const int cur = j & 1;
+        if (j + 1 < ntiles) issue_tile(j + 1, cur ^ 1);
         const int64_t kv0 = static_cast<int64_t>(j) * kBlockN;
         const uint16_t* Kt = lds[cur][0];
         const uint16_t* Vt = lds[cur][1];
         const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
         if (!skip) {
+            // S^T (even i) and dP^T (odd i) for key tiles tt, k slices ks: MFMA i = 4 ks + 2 tt + which
             f32x16_t s[2], dp[2];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    s[tt][v] = 0.0f;
-                    dp[tt][v] = 0.0f;
-                }
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Kt, 32 * tt + lq, 2 * ks + lg),
-                                                                    qf[ks], s[tt], 0, 0, 0);
-                    dp[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read16<DP>(Vt, 32 * tt + lq, 2 * ks + lg),
-                                                                     of[ks], dp[tt], 0, 0, 0);
-                }
-            }
+            const f32x16_t zero = {};
+            mfma_ring<4 * KS>(
+                [&](int i) {
+                    const int ks = i >> 2, tt = (i >> 1) & 1;
+                    return tile_read16<DP>((i & 1) ? Vt : Kt, 32 * tt + lq, 2 * ks + lg);
+                },
+                [&](int i, bf16x8_t x) {
+                    const int ks = i >> 2, tt = (i >> 1) & 1;
+                    if (i & 1) dp[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, of[ks], ks == 0 ? zero : dp[tt], 0, 0, 0);
+                    else s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, qf[ks], ks == 0 ? zero : s[tt], 0, 0, 0);
+                });
+            // Lane holds query my_q, keys kv0 + 32*tt + 8*(v/4) + 4*lg + v%4. Tiles whose 64 keys
+            // all lie at or below every query of this wave skip the mask; the others compare one
+            // 32-bit offset per element (key offset <= rel, < klim).
+            const bool full = (!a.causal || kv0 + kBlockN - 1 <= q0w + a.diag) && q0w + 32 <= a.m &&
+                              kv0 + kBlockN <= a.n;
+            int64_t rel64 = my_q + a.diag - kv0;
+            rel64 = rel64 < -(int64_t{1} << 30) ? -(int64_t{1} << 30) : (rel64 > (int64_t{1} << 30) ? (int64_t{1} << 30) : rel64);
+            const int rel = (a.causal ? static_cast<int>(rel64) : (1 << 30)) - 4 * lg;
+            const int klim = static_cast<int>(a.n - kv0 < kBlockN ? a.n - kv0 : kBlockN) - 4 * lg;
+            const bool q_ok = my_q < a.m;
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int64_t key = kv0 + 32 * tt + (v >> 2) * 8 + lg * 4 + (v & 3);
-                    const bool vis = my_q < a.m && key < a.n && (!a.causal || key <= my_q + a.diag);
-                    const float p = vis ? fast_exp2(s[tt][v] * a.scale_log2 - lse2) : 0.0f;
+                    float p = fast_exp2(__builtin_fmaf(s[tt][v], a.scale_log2, -lse2));
+                    if (!full) {
+                        const int kk = 32 * tt + (v >> 2) * 8 + (v & 3);
+                        p = q_ok && kk <= rel && kk < klim ? p : 0.0f;
+                    }
                     dp[tt][v] = a.scale * (p * (dp[tt][v] - rstat));
                 }
+            bf16x8_t sb[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const bf16x8_t sb = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
-                const int kb0 = 16 * ks + 4 * lg;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt)
-                    dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_read_tr<DP>(Kt, lane, kb0, kb0 + 8, 32 * dt),
-                                                                     sb, dq[dt], 0, 0, 0);
-            }
+            for (int ks = 0; ks < 4; ++ks) sb[ks] = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
+            // dQ^T += K^T dS^T: MFMA i = DT ks + dt
+            mfma_ring<4 * DT>(
+                [&](int i) {
+                    const int ks = i / DT, dt = i % DT;
+                    const int kb0 = 16 * ks + 4 * lg;
+                    return tile_read_tr<DP>(Kt, lane, kb0, kb0 + 8, 32 * dt);
+                },
+                [&](int i, bf16x8_t x) {
+                    const int ks = i / DT, dt = i % DT;
+                    dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[ks], dq[dt], 0, 0, 0);
+                });
         }
-        if (j + 1 < ntiles) {
-            lk.store(lds[cur ^ 1][0], t);
-            lv.store(lds[cur ^ 1][1], t);
-            if (j + 2 < ntiles) {
-                lk.load(K, kv0 + 2 * kBlockN, a.n, t);
-                lv.load(V, kv0 + 2 * kBlockN, a.n, t);
-            }
-        }
-        __syncthreads();
+        landed();
+        lds_barrier();
     }
 
     if (my_q < a.m) {
@@ -1159,14 +1225,17 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
     const int64_t rows = sh.batch * sh.heads * sh.m;
     constexpr int lanes = D / 8;
     const int64_t threads = rows * lanes;
+    // the gradient kernels address one Q/dO/K/V head with 32-bit buffer offsets
+    if (sh.m * D * 2 >= (int64_t{1} << 31) || sh.n * D * 2 >= (int64_t{1} << 31)) return hipErrorInvalidValue;
+    float* lse2 = stat + rows;
     hipLaunchKernelGGL((attn_bwd_rowstat<D>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), stat, rows);
+                       static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, stat, lse2, rows);
     BwdArgs a;
     a.q = static_cast<const uint16_t*>(q);
     a.k = static_cast<const uint16_t*>(k);
     a.v = static_cast<const uint16_t*>(v);
     a.dout = static_cast<const uint16_t*>(dout);
-    a.lse = lse;
+    a.lse2 = lse2;
     a.stat = stat;
     a.dq = dq;
     a.dk = dk;
@@ -1193,7 +1262,7 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
 }  // namespace
 
 size_t attention_bwd_workspace_bytes(const AttnShape& sh) {
-    return static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float);
+    return 2 * static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float);  // row statistic, lse2
 }
 
 hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o, float* lse,

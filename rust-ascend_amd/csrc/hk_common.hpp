@@ -127,4 +127,24 @@ __device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds, int voff,
                  : "memory");
 }
 
+// The 4-byte form: lane l's dword lands at lds + 4 * l (one instruction moves 256 bytes).
+__device__ __forceinline__ void load_lds4(i32x4_t rsrc, uint32_t lds, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, %3 offen lds"
+                 :
+                 : "v"(voff), "s"(lds), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
+
+// Workgroup barrier for kernels whose global->LDS loads must stay in flight across it: every
+// LDS access this wave issued before it has completed (lgkmcnt 0), but outstanding vector
+// memory operations are not waited for (the release fence of __syncthreads would wait for
+// them too). The empty asm statements keep the compiler from moving memory accesses across.
+// gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63 (no wait), expcnt 7 (no wait), lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 }  // namespace hk

@@ -380,9 +380,11 @@ gemm_nt_dma_kernel(GemmArgs p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, lk = lane >> 5;
 
-    // Loads go through buffer resources over this batch's A and B: one per-lane offset and a
-    // uniform offset per instruction. Rows past M (N) fall outside the resource and are not
-    // fetched; they only feed outputs that are not stored.
+    // Loads go through buffer resources over this batch's A and B. The row offset is part of
+    // the per-lane (VGPR) offset, which the hardware checks against the buffer's size, so rows
+    // past M (N) read as zero instead of reading past the matrix (the scalar offset, which
+    // carries only the K position, is not range-checked); they only feed outputs that are not
+    // stored.
     const i32x4_t ra = buffer_resource(A, p.m * p.k * 2);
     const i32x4_t rb = buffer_resource(B, p.n * p.k * 2);
     // instruction i of this wave fills stage rows 16*(wave + 4*i) .. +15
@@ -391,9 +393,9 @@ gemm_nt_dma_kernel(GemmArgs p) {
     auto fetch_one = [&](uint16_t* stage, int kt, int i) {
         const uint32_t dst = lds_address(stage + (16 * wave + 64 * i) * kSBK);
         if (i < BM / 64)
-            load_lds16(ra, dst, voff, ((tm * BM + 64 * i) * p.k + kt * kSBK) * 2);
+            load_lds16(ra, dst, voff + (tm * BM + 64 * i) * p.k * 2, kt * kSBK * 2);
         else
-            load_lds16(rb, dst, voff, ((tn * BN + 64 * (i - BM / 64)) * p.k + kt * kSBK) * 2);
+            load_lds16(rb, dst, voff + (tn * BN + 64 * (i - BM / 64)) * p.k * 2, kt * kSBK * 2);
     };
     auto fetch = [&](uint16_t* stage, int kt) {
 #pragma unroll
@@ -505,8 +507,9 @@ gemm_nt_pp_kernel(GemmArgs p) {
     const int group = wave >> 2, q = wave & 3;
     const int lr = lane & 31, lk = lane >> 5;
 
-    // Rows past M (N) fall outside the buffer ranges and read as zero; they only feed outputs
-    // that are not stored.
+    // The row offset of every load is in its per-lane offset, which the hardware checks
+    // against the buffer's size (the scalar offset is not checked): rows past M (N) read as
+    // zero; they only feed outputs that are not stored.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, p.m * p.k * 2,
                                                                         kBufferConfig);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, p.n * p.k * 2,
@@ -523,10 +526,10 @@ gemm_nt_pp_kernel(GemmArgs p) {
         const int blk = wave + 8 * d;
         if (d < 4)
             stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     ra, voff, ((tm * kPPTile + 8 * blk) * p.k + kt * kPK) * 2, 0));
+                                                     ra, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2, 0));
         else
             stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     rb, voff, ((tn * kPPTile + 8 * (blk - 32)) * p.k + kt * kPK) * 2, 0));
+                                                     rb, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2, 0));
     };
     const int wlane = wave * 8 * kPK + lane * 8;  // element offset of this lane's chunk in block d = 0
     auto lwrite = [&](uint16_t* slot, int d) __attribute__((always_inline)) {
