@@ -43,7 +43,36 @@ def parse():
     p.add_argument("--no-secondary", action="store_true", help="headline workload only")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    p.add_argument("--stream-ceilings", action="store_true",
+                   help="only measure plain HBM streams (read, write, copy, 2 reads + 1 write) on 1 GiB "
+                        "buffers with PyTorch's own kernels and print them")
     return p.parse_args()
+
+
+def stream_ceilings(gib=1, iters=10):
+    """Plain HBM streaming rates on buffers far larger than the 256 MB on-package cache, with
+    PyTorch's own kernels: sum (read), fill_ (write), copy_ (read + write), add (2 reads + 1
+    write). They bound what an HBM-bound kernel with the same stream mix can reach here."""
+    import torch
+    n = gib * (1 << 30) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.ones(n, device="cuda")
+    c = torch.empty(n, device="cuda")
+    cases = [("read", 1, lambda: a.sum()), ("write", 1, lambda: c.fill_(1.0)),
+             ("copy", 2, lambda: c.copy_(a)), ("2 reads + 1 write", 3, lambda: torch.add(a, b, out=c))]
+    out = {}
+    for name, streams, fn in cases:
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / iters
+        out[name] = round(streams * n * 4 / (ms * 1e-3) / 1e9, 1)
+    return out
 
 
 def event_ms(pairs):
@@ -225,6 +254,9 @@ def main():
     import torch
     from rust_ascend_hip import HipRuntime
     torch.cuda.set_device(0)
+    if args.stream_ceilings:
+        print(json.dumps({"hbm_stream_GBps_1GiB_buffers": stream_ceilings()}))
+        return
     HipRuntime.initialize_exclusive()
     HipRuntime.set_async(True)
 
