@@ -198,6 +198,19 @@ hk_status hk_softmax(hk_context* ctx, const hk_tensor* x, int32_t logarithmic, h
 hk_status hk_softmax_backward(hk_context* ctx, const hk_tensor* y, const hk_tensor* dy, int32_t logarithmic,
                               hk_tensor* dx);
 
+/* ---------------------------------------------------------------- SwiGLU gate */
+
+/* y = SiLU(gate) * up = gate * sigmoid(gate) * up, element-wise over contiguous tensors of one
+ * shape, F32 (the reference's dtype) or BF16 storage with F32 arithmetic; at most 2^32-1
+ * elements. Reference: AscendRuntime::silu_mul, runtime/mod.rs:282-285 (elementwise.rs:13-19;
+ * arithmetic rust-ascend-compiler/src/ascend/programs.rs:41). */
+hk_status hk_silu_mul(hk_context* ctx, const hk_tensor* gate, const hk_tensor* up, hk_tensor* y);
+/* dgate = dy * up * s (1 + gate (1 - s)), dup = dy * gate * s with s = sigmoid(gate).
+ * Reference: AscendRuntime::silu_mul_backward, runtime/mod.rs:287-290 (elementwise.rs:21-30;
+ * programs.rs:43). */
+hk_status hk_silu_mul_backward(hk_context* ctx, const hk_tensor* gate, const hk_tensor* up, const hk_tensor* dy,
+                               hk_tensor* dgate, hk_tensor* dup);
+
 /* ---------------------------------------------------------------- composed-attention shims */
 
 /* The fused attention entry points apply the mask and the KV-head mapping themselves; these

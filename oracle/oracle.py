@@ -38,6 +38,10 @@ a wrong sign or index, or a transposed operand fails at least one check:
   per-row shift, and torch float64 autograd (the backward must be the forward's
   vector-Jacobian product) on the reference's own inputs and shapes
   (examples/common_rows_validate.rs:7-9,100).
+* ``silu_mul_f64``/``silu_mul_backward_f64``: torch float64 autograd of
+  torch.nn.functional.silu(g) * u (an independent implementation; the backward must be its
+  vector-Jacobian product), known answers at g = 0 (y = 0, dgate = dy*u/2, dup = 0) and for
+  large |g| (silu(g) -> g or 0), on the reference's own inputs of examples/silu_mul_tensor.rs:25-27.
 * ``repeat_kv``/``repeat_kv_backward``: the backward is the repeat's transpose (inner products
   <repeat(x), dy> == <x, backward(dy)> in float64), equals the float64 group sum within
   rounding, and follows the pairwise level order exactly on inputs where the order decides the
@@ -328,6 +332,23 @@ def softmax_backward_f64(y, dy, logarithmic: bool = False) -> np.ndarray:
     out = np.empty(y.shape, np.float64)
     lib().or_softmax_backward_f64(y, dy, y.size // width if width else 0, width, int(logarithmic), out)
     return out
+
+
+def silu_mul_f64(gate, up) -> np.ndarray:
+    """gate * sigmoid(gate) * up in float64 (examples/silu_mul_tensor.rs:40-42)."""
+    g = np.asarray(gate, np.float64)
+    s = 1.0 / (1.0 + np.exp(-g))
+    return g * s * np.asarray(up, np.float64)
+
+
+def silu_mul_backward_f64(gate, up, dy):
+    """(dgate, dup) in float64: derivative = s (1 + g (1 - s)); dgate = dy u derivative,
+    dup = dy g s (examples/silu_mul_tensor.rs:40-44)."""
+    g = np.asarray(gate, np.float64)
+    u = np.asarray(up, np.float64)
+    d = np.asarray(dy, np.float64)
+    s = 1.0 / (1.0 + np.exp(-g))
+    return d * u * (s * (1.0 + g * (1.0 - s))), d * g * s
 
 
 def repeat_kv(x, query_heads: int) -> np.ndarray:

@@ -608,6 +608,49 @@ hk_status hk_cast_into(hk_context* h, const hk_tensor* in, hk_tensor* out) {
 
 // ------------------------------------------------------------------ RMSNorm
 
+namespace {
+// Reference: elementwise.rs:5-11 (check_for: contiguous, one shape; element count <= u32).
+bool gate_shapes(std::initializer_list<const hk_tensor*> ts, const char* op) {
+    const hk_tensor* first = *ts.begin();
+    if (first->dtype != HK_F32 && first->dtype != HK_BF16)
+        return fail(HK_INVALID_ARGUMENT, "%s requires F32 or BF16 tensors", op), false;
+    for (const hk_tensor* t : ts)
+        if (t->dtype != first->dtype || !same_shape(t, first))
+            return fail(HK_INVALID_ARGUMENT, "%s requires tensors of one dtype and shape", op), false;
+    if (numel(first) > static_cast<int64_t>(UINT32_MAX))
+        return fail(HK_INVALID_ARGUMENT, "%s element count exceeds u32", op), false;
+    return true;
+}
+}  // namespace
+
+hk_status hk_silu_mul(hk_context* h, const hk_tensor* gate, const hk_tensor* up, hk_tensor* y) {
+    // Reference: elementwise.rs:13-19.
+    if (!tensor_ok(gate, "gate") || !tensor_ok(up, "up") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    if (!gate_shapes({gate, up, y}, "SiLU Mul")) return HK_INVALID_ARGUMENT;
+    if (!disjoint({y}, {gate, up})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t n = numel(gate);
+    hipError_t e = hk::silu_mul(gate->dtype == HK_BF16, gate->data, up->data, y->data, n, g.c->stream);
+    return complete(g.c, e, "silu_mul", n ? 1 : 0);
+}
+
+hk_status hk_silu_mul_backward(hk_context* h, const hk_tensor* gate, const hk_tensor* up, const hk_tensor* dy,
+                               hk_tensor* dgate, hk_tensor* dup) {
+    // Reference: elementwise.rs:21-30.
+    if (!tensor_ok(gate, "gate") || !tensor_ok(up, "up") || !tensor_ok(dy, "dY") || !tensor_ok(dgate, "dGate") ||
+        !tensor_ok(dup, "dUp"))
+        return HK_INVALID_ARGUMENT;
+    if (!gate_shapes({gate, up, dy, dgate, dup}, "SiLU Mul backward")) return HK_INVALID_ARGUMENT;
+    if (!disjoint({dgate, dup}, {gate, up, dy})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t n = numel(gate);
+    hipError_t e = hk::silu_mul_backward(gate->dtype == HK_BF16, gate->data, up->data, dy->data, dgate->data,
+                                         dup->data, n, g.c->stream);
+    return complete(g.c, e, "silu_mul_backward", n ? 1 : 0);
+}
+
 hk_status hk_softmax(hk_context* h, const hk_tensor* x, int32_t logarithmic, hk_tensor* y) {
     // Reference: rows.rs:50-62 (layout_for / check_for: contiguous F32, positive width).
     if (!tensor_ok(x, "X") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;

@@ -40,6 +40,11 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
                      int64_t n, int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s);
 
 // ---- attention (hk_attention.hip)
+// SwiGLU gate, element-wise over n values of F32 or BF16 storage (hk_elementwise.hip).
+hipError_t silu_mul(int dtype_bf16, const void* gate, const void* up, void* y, int64_t n, hipStream_t s);
+hipError_t silu_mul_backward(int dtype_bf16, const void* gate, const void* up, const void* dy, void* dgate,
+                             void* dup, int64_t n, hipStream_t s);
+
 // Row softmax / log-softmax over the last axis of contiguous F32 [rows, width] (hk_softmax.hip).
 hipError_t softmax_forward(const float* x, float* y, int64_t rows, int64_t width, int logarithmic, hipStream_t s);
 hipError_t softmax_backward(const float* y, const float* dy, float* dx, int64_t rows, int64_t width, int logarithmic,

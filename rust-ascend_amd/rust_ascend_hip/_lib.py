@@ -79,6 +79,8 @@ SIGNATURES = {
     "hk_linear_bf16_fp32": [_CTX, _T, _T, _T, _T, _T],
     "hk_linear_bf16_fp32_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_cast_into": [_CTX, _T, _T],
+    "hk_silu_mul": [_CTX, _T, _T, _T],
+    "hk_silu_mul_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_softmax": [_CTX, _T, _i32, _T],
     "hk_softmax_backward": [_CTX, _T, _T, _i32, _T],
     "hk_causal_mask": [_CTX, _u64, _u64, _T],

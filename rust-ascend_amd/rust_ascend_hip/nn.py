@@ -119,6 +119,42 @@ def log_softmax(x: torch.Tensor) -> torch.Tensor:
     return _Softmax.apply(x.contiguous(), True)
 
 
+class _SiluMul(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gate, up):
+        ctx.save_for_backward(gate, up)
+        return HipRuntime.silu_mul(gate, up)
+
+    @staticmethod
+    def backward(ctx, dy):
+        gate, up = ctx.saved_tensors
+        dg, du = HipRuntime.silu_mul_backward(gate, up, dy.contiguous().to(gate.dtype))
+        return dg, du
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """SiLU(gate) * up (F32 or BF16). Reference: nn::silu_mul / SiluMulBackend (src/nn.rs:109-119,
+    334-349); when gate and up are the same tensor autograd adds both gradients, as the
+    reference's shared-node case does (examples/silu_mul_tensor.rs:51-53)."""
+    return _SiluMul.apply(gate.contiguous(), up.contiguous())
+
+
+def swiglu_bf16_fp32(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """(SiLU(x gate^T) * (x up^T)) down^T with F32 storage and BF16 linear compute.
+    Reference: nn::swiglu_bf16_fp32 (src/nn/feed_forward.rs:24-42): gate/up [H,K], down [N,H],
+    every dimension a positive multiple of 16."""
+    m, k = x.shape
+    h, gk = gate.shape
+    n, dh = down.shape
+    if gk != k or tuple(up.shape) != (h, k) or dh != h or any(d <= 0 or d % 16 for d in (m, n, k, h)):
+        raise ValueError("SwiGLU requires aligned X[M,K], gate/up[H,K] and down[N,H]")
+    if any(t.dtype != torch.float32 for t in (x, gate, up, down)):
+        raise ValueError("SwiGLU requires FP32 input and weights")
+    g = linear_bf16_fp32(x, gate)
+    u = linear_bf16_fp32(x, up)
+    return linear_bf16_fp32(silu_mul(g, u), down)
+
+
 class _Rotary(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, cos, sin, layout, width):

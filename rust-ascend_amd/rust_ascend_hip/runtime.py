@@ -194,6 +194,23 @@ class HipRuntime:
         """Reference: AscendRuntime::cast_into (mod.rs:276-279)."""
         _call("hk_cast_into", desc(x), desc(out))
 
+    # ---------------------------------------------------------------- SwiGLU gate
+
+    @staticmethod
+    def silu_mul(gate, up):
+        """SiLU(gate) * up. Reference: AscendRuntime::silu_mul (mod.rs:282-285)."""
+        y = _empty(gate.shape, gate.dtype, gate)
+        _call("hk_silu_mul", desc(gate), desc(up), desc(y))
+        return y
+
+    @staticmethod
+    def silu_mul_backward(gate, up, grad):
+        """[dGate, dUp]. Reference: AscendRuntime::silu_mul_backward (mod.rs:287-290)."""
+        dg = _empty(gate.shape, gate.dtype, gate)
+        du = _empty(gate.shape, gate.dtype, gate)
+        _call("hk_silu_mul_backward", desc(gate), desc(up), desc(grad), desc(dg), desc(du))
+        return dg, du
+
     # ---------------------------------------------------------------- composed-attention shims
 
     @staticmethod

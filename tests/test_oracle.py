@@ -408,3 +408,53 @@ def test_repeat_kv_backward_catches_planted_mistakes(oracle):
     for bad in (wrong_map, dropped):
         with pytest.raises(AssertionError):
             close(bad, want, 5e-4, 5e-4)
+
+
+# ------------------------------------------------------------------ SwiGLU gate
+
+def _silu_inputs(n):
+    # examples/silu_mul_tensor.rs:25-27
+    i = np.arange(n)
+    x = ((i % 41).astype(np.float32) * np.float32(0.6) - np.float32(12.0)).astype(np.float32)
+    u = ((i % 13).astype(np.float32) * np.float32(0.125) - np.float32(0.5)).astype(np.float32)
+    dy = ((i % 7).astype(np.float32) * np.float32(0.25) - np.float32(0.75)).astype(np.float32)
+    return x, u, dy
+
+
+def test_silu_mul_known_answers(oracle):
+    g = np.array([0.0, 40.0, -40.0, 1.0], np.float32)
+    u = np.array([3.0, 2.0, 5.0, 1.0], np.float32)
+    dy = np.array([2.0, 1.0, 1.0, 1.0], np.float32)
+    y = oracle.silu_mul_f64(g, u)
+    dg, du = oracle.silu_mul_backward_f64(g, u, dy)
+    assert y[0] == 0.0 and dg[0] == 2.0 * 3.0 * 0.5 and du[0] == 0.0   # sigmoid(0) = 1/2
+    close(y[1:3], [80.0, 0.0], 1e-12, 1e-12)                            # silu(g) -> g, -> 0
+    close(dg[1:3], [2.0, 0.0], 1e-12, 1e-12)                            # derivative -> 1, -> 0
+    s1 = 1.0 / (1.0 + np.exp(-1.0))
+    close([y[3], dg[3], du[3]], [s1, s1 * (1 + (1 - s1)), s1], 1e-15, 1e-15)
+
+
+@pytest.mark.parametrize("n", [1, 65, 1025])
+def test_silu_mul_vs_autograd(oracle, n):
+    x, u, dy = _silu_inputs(n)
+    g64 = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    u64 = torch.tensor(u, dtype=torch.float64, requires_grad=True)
+    y = torch.nn.functional.silu(g64) * u64
+    y.backward(torch.tensor(dy, dtype=torch.float64))
+    close(oracle.silu_mul_f64(x, u), y.detach().numpy(), 1e-13, 1e-12)
+    dg, du = oracle.silu_mul_backward_f64(x, u, dy)
+    close(dg, g64.grad.numpy(), 1e-13, 1e-12)
+    close(du, u64.grad.numpy(), 1e-13, 1e-12)
+
+
+def test_silu_mul_backward_catches_planted_mistakes(oracle):
+    x, u, dy = _silu_inputs(1025)
+    dg, du = oracle.silu_mul_backward_f64(x, u, dy)
+    s = 1 / (1 + np.exp(-x.astype(np.float64)))
+    wrong_derivative = dy * u * s                 # drops the x s (1 - s) term
+    wrong_sign = dy * u * s * (1 - x * (1 - s))
+    for bad in (wrong_derivative, wrong_sign):
+        with pytest.raises(AssertionError):
+            close(bad, dg, 2e-5, 1e-4)
+    with pytest.raises(AssertionError):
+        close(dy * u, du, 2e-5, 1e-4)             # dup must carry silu(g), not u
