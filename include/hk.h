@@ -50,6 +50,8 @@ typedef enum hk_status {
 typedef enum hk_dtype {
     HK_F32 = 0,
     HK_F16 = 1,
+    HK_I32 = 3,   /* embedding IDs only */
+    HK_I64 = 9,   /* embedding IDs only */
     HK_BF16 = 27,
 } hk_dtype;
 
@@ -210,6 +212,40 @@ hk_status hk_silu_mul(hk_context* ctx, const hk_tensor* gate, const hk_tensor* u
  * programs.rs:43). */
 hk_status hk_silu_mul_backward(hk_context* ctx, const hk_tensor* gate, const hk_tensor* up, const hk_tensor* dy,
                                hk_tensor* dgate, hk_tensor* dup);
+
+/* ---------------------------------------------------------------- bias and residual add */
+
+/* y = (x + residual) + bias[c] over the last axis c, in that F32 order; residual may be NULL
+ * (y = x + bias). X rank 1..8 with a positive last axis and at most 2^32-1 elements; X, residual
+ * and Y F32 (the reference's dtype) or BF16 storage with F32 arithmetic; bias F32 [width];
+ * residual exactly X's shape. Reference: AscendRuntime::bias_add, runtime/mod.rs:177-181
+ * (runtime/affine.rs:10-22; nn::bias_add / residual_bias_add, src/nn/affine.rs:14-25). */
+hk_status hk_bias_add(hk_context* ctx, const hk_tensor* x, const hk_tensor* bias, const hk_tensor* residual,
+                      hk_tensor* y);
+/* dbias [width] F32 = dY summed over every leading axis, pairwise in the reference's order (row i
+ * plus row i + floor(r/2) per level, odd last row carried), so bit-identical to it; zeros when
+ * there are no rows. Reference: AscendRuntime::bias_add_backward, runtime/mod.rs:182-185
+ * (runtime/affine.rs:23-26, normalization.rs:95-114). */
+hk_status hk_bias_add_backward(hk_context* ctx, const hk_tensor* dy, hk_tensor* dbias);
+
+/* ---------------------------------------------------------------- embedding */
+
+/* No padding row (the SDK's unsigned sentinel, rust-ascend-driver/src/tensor/embedding.rs:14-15). */
+#define HK_NO_PADDING UINT64_MAX
+
+/* out [ids..., H] = weight[ids, :] for an F32/F16/BF16 table weight [V, H] and INT32/INT64 IDs of
+ * rank 1..7 with values in [0, V); out has the table's dtype. An ID outside [0, V) writes a zero
+ * row and, in synchronous mode, returns HK_INVALID_ARGUMENT after the call (asynchronous mode does
+ * not check). Reference: AscendRuntime::embedding, runtime/mod.rs:237-241 (runtime/indexing.rs:33-37,
+ * embedding.rs:21-34,46-60). */
+hk_status hk_embedding(hk_context* ctx, const hk_tensor* weight, const hk_tensor* ids, hk_tensor* out);
+/* dweight [num_weights, H] = sum of grad[t, :] over the positions t of each ID, in increasing
+ * position order with F32 accumulation (deterministic); the padding row (padding_idx, or
+ * HK_NO_PADDING) stays zero; with scale_grad_by_freq = 1 each row is divided by its ID count.
+ * grad [ids..., H] F32/F16/BF16, dweight in grad's dtype. Reference: AscendRuntime::embedding_backward,
+ * runtime/mod.rs:252-256 (runtime/indexing.rs:60-64, embedding.rs:35-44,60-79). */
+hk_status hk_embedding_backward(hk_context* ctx, const hk_tensor* grad, const hk_tensor* ids, uint64_t num_weights,
+                                uint64_t padding_idx, int32_t scale_grad_by_freq, hk_tensor* dweight);
 
 /* ---------------------------------------------------------------- composed-attention shims */
 

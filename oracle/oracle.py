@@ -42,6 +42,16 @@ a wrong sign or index, or a transposed operand fails at least one check:
   torch.nn.functional.silu(g) * u (an independent implementation; the backward must be its
   vector-Jacobian product), known answers at g = 0 (y = 0, dgate = dy*u/2, dup = 0) and for
   large |g| (silu(g) -> g or 0), on the reference's own inputs of examples/silu_mul_tensor.rs:25-27.
+* ``bias_add_f32``/``bias_add_backward`` (and ``column_sum_pairwise``): the reference's own
+  cases of examples/bias_tensor.rs (integer-formula inputs on seven shapes, exact results; the
+  ordered case (1e20 + -1e20) + 1 == 1, which x + (r + b) gets wrong; -0, NaN and infinities), the
+  exact integer column sum, and inputs on which the pairwise halving order decides the float32
+  result ([1e8, -1e8, 1, 1] sums to 0 pairwise, to 2 left to right or in adjacent pairs).
+* ``embedding``/``embedding_backward_f64``: torch float64 autograd of
+  torch.nn.functional.embedding with the same padding_idx and scale_grad_by_freq (an independent
+  implementation of these semantics) on the reference's inputs of
+  examples/embedding_tensor.rs:20-24 (V = 7, H = 65, repeated IDs) for all four option pairs and on
+  random cases; the empty-ID gradient is zero (embedding_tensor.rs:47-53).
 * ``repeat_kv``/``repeat_kv_backward``: the backward is the repeat's transpose (inner products
   <repeat(x), dy> == <x, backward(dy)> in float64), equals the float64 group sum within
   rounding, and follows the pairwise level order exactly on inputs where the order decides the
@@ -349,6 +359,51 @@ def silu_mul_backward_f64(gate, up, dy):
     d = np.asarray(dy, np.float64)
     s = 1.0 / (1.0 + np.exp(-g))
     return d * u * (s * (1.0 + g * (1.0 - s))), d * g * s
+
+
+def bias_add_f32(x, bias, residual=None) -> np.ndarray:
+    """(x + residual) + bias[c] in float32, in that order (src/nn/affine.rs:21-25; the
+    reference's BiasAddSpec program, runtime/affine.rs:10-22)."""
+    x = np.asarray(x, np.float32)
+    s = x + np.asarray(residual, np.float32) if residual is not None else x
+    return (s + np.asarray(bias, np.float32)).astype(np.float32)
+
+
+def bias_add_backward(dy) -> np.ndarray:
+    """dbias = dY summed over the leading axes by the pairwise tree of
+    runtime/normalization.rs:95-114 (runtime/affine.rs:23-26)."""
+    dy = np.asarray(dy, np.float32)
+    width = dy.shape[-1]
+    return column_sum_pairwise(dy.reshape(-1, width))
+
+
+def embedding(weight, ids) -> np.ndarray:
+    """weight[ids]: [ids..., H] in the table's dtype (embedding.rs:27-34, the aclnnEmbedding
+    lookup). IDs must lie in [0, V)."""
+    weight = np.asarray(weight)
+    ids = np.asarray(ids, np.int64)
+    if ids.size and (ids.min() < 0 or ids.max() >= weight.shape[0]):
+        raise ValueError("embedding index outside the table")
+    return weight[ids]
+
+
+def embedding_backward_f64(grad, ids, num_weights: int, padding_idx=None, scale_grad_by_freq=False):
+    """Dense weight gradient in float64 (embedding.rs:60-79, the aclnnEmbeddingDenseBackward
+    semantics the reference's examples/embedding_tensor.rs:31-39 checks): every position adds its
+    gradient row to its ID's row; the padding row stays zero; with frequency scaling each row is
+    divided by how often its ID occurs."""
+    grad = np.asarray(grad, np.float64)
+    ids = np.asarray(ids, np.int64).reshape(-1)
+    g = grad.reshape(ids.size, grad.shape[-1])
+    dw = np.zeros((int(num_weights), g.shape[1]), np.float64)
+    np.add.at(dw, ids, g)
+    if scale_grad_by_freq:
+        counts = np.bincount(ids, minlength=int(num_weights)).astype(np.float64)
+        nz = counts > 0
+        dw[nz] /= counts[nz, None]
+    if padding_idx is not None:
+        dw[padding_idx] = 0.0
+    return dw
 
 
 def repeat_kv(x, query_heads: int) -> np.ndarray:

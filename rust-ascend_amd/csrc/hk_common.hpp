@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 namespace hk {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -78,6 +80,53 @@ __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
     f32x4_t b = {v[4], v[5], v[6], v[7]};
     *reinterpret_cast<f32x4_t*>(p) = a;
     *reinterpret_cast<f32x4_t*>(p + 4) = b;
+}
+
+// IEEE half storage (F16), converted with the hardware round-to-nearest-even converter.
+template <> struct Elem<_Float16> {
+    static __device__ __forceinline__ float load(const _Float16* p, int64_t i) { return static_cast<float>(p[i]); }
+    static __device__ __forceinline__ void store(_Float16* p, int64_t i, float v) { p[i] = static_cast<_Float16>(v); }
+};
+
+// 16-byte chunks of kPer consecutive elements as floats (one vector load/store per chunk).
+template <typename T> struct Chunk;
+template <> struct Chunk<float> {
+    static constexpr int kPer = 4;
+    __device__ static void load(const float* p, float (&v)[4]) {
+        const f32x4_t w = *reinterpret_cast<const f32x4_t*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = w[i];
+    }
+    __device__ static void store(float* p, const float (&v)[4]) {
+        *reinterpret_cast<f32x4_t*>(p) = f32x4_t{v[0], v[1], v[2], v[3]};
+    }
+};
+template <> struct Chunk<uint16_t> {
+    static constexpr int kPer = 8;
+    __device__ static void load(const uint16_t* p, float (&v)[8]) { load8(p, v); }
+    __device__ static void store(uint16_t* p, const float (&v)[8]) { store8(p, v); }
+};
+template <> struct Chunk<_Float16> {
+    static constexpr int kPer = 8;
+    typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+    __device__ static void load(const _Float16* p, float (&v)[8]) {
+        const h8_t w = *reinterpret_cast<const h8_t*>(p);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = static_cast<float>(w[i]);
+    }
+    __device__ static void store(_Float16* p, const float (&v)[8]) {
+        h8_t w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = static_cast<_Float16>(v[i]);
+        *reinterpret_cast<h8_t*>(p) = w;
+    }
+};
+
+// Every pointer 16-byte aligned (the vector chunk paths need it).
+__host__ __forceinline__ bool aligned16(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+    return true;
 }
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.

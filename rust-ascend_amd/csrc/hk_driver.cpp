@@ -56,18 +56,24 @@ Ctx* g_ctx = nullptr;
 
 int64_t dtype_size(int32_t dt) {
     switch (dt) {
-        case HK_F32: return 4;
+        case HK_F32:
+        case HK_I32: return 4;
+        case HK_I64: return 8;
         case HK_F16:
         case HK_BF16: return 2;
         default: return 0;
     }
 }
 
+bool is_float(int32_t dt) { return dt == HK_F32 || dt == HK_F16 || dt == HK_BF16; }
+
 const char* dtype_name(int32_t dt) {
     switch (dt) {
         case HK_F32: return "F32";
         case HK_F16: return "F16";
         case HK_BF16: return "BF16";
+        case HK_I32: return "I32";
+        case HK_I64: return "I64";
         default: return "?";
     }
 }
@@ -95,13 +101,14 @@ std::string shape_str(const hk_tensor* t) {
     return s + "]";
 }
 
-// Basic descriptor check: known dtype, valid rank/shape, non-null data unless empty.
-bool tensor_ok(const hk_tensor* t, const char* name) {
+// Basic descriptor check: floating dtype, valid rank/shape, non-null data unless empty.
+// Integer tensors (embedding IDs) are checked by ids_ok instead.
+bool tensor_ok(const hk_tensor* t, const char* name, bool integer = false) {
     if (!t) {
         fail(HK_INVALID_ARGUMENT, "%s: null tensor descriptor", name);
         return false;
     }
-    if (dtype_size(t->dtype) == 0) {
+    if (integer ? (t->dtype != HK_I32 && t->dtype != HK_I64) : !is_float(t->dtype)) {
         fail(HK_INVALID_ARGUMENT, "%s: unsupported dtype code %d", name, t->dtype);
         return false;
     }
@@ -649,6 +656,144 @@ hk_status hk_silu_mul_backward(hk_context* h, const hk_tensor* gate, const hk_te
     hipError_t e = hk::silu_mul_backward(gate->dtype == HK_BF16, gate->data, up->data, dy->data, dgate->data,
                                          dup->data, n, g.c->stream);
     return complete(g.c, e, "silu_mul_backward", n ? 1 : 0);
+}
+
+// ------------------------------------------------------------------ bias and residual add
+
+namespace {
+// Reference: affine.rs:6-9 with wide_rows.rs:13-20 (rank 1..8, positive width, count <= u32).
+bool affine_layout(const hk_tensor* t, int64_t* rows, int64_t* width, const char* op) {
+    if (t->rank < 1 || t->rank > 8) return fail(HK_INVALID_ARGUMENT, "%s requires rank 1..8", op), false;
+    *width = t->shape[t->rank - 1];
+    if (*width <= 0) return fail(HK_INVALID_ARGUMENT, "%s requires a positive last axis", op), false;
+    const int64_t n = numel(t);
+    if (n > static_cast<int64_t>(UINT32_MAX)) return fail(HK_INVALID_ARGUMENT, "%s element count exceeds u32", op), false;
+    *rows = n / *width;
+    return true;
+}
+}  // namespace
+
+hk_status hk_bias_add(hk_context* h, const hk_tensor* x, const hk_tensor* bias, const hk_tensor* residual,
+                      hk_tensor* y) {
+    // Reference: runtime/affine.rs:10-22 (forward), src/nn/affine.rs:17-25.
+    if (!tensor_ok(x, "X") || !tensor_ok(bias, "bias") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    if (residual && !tensor_ok(residual, "residual")) return HK_INVALID_ARGUMENT;
+    int64_t rows, width;
+    if (!affine_layout(x, &rows, &width, "bias add")) return HK_INVALID_ARGUMENT;
+    if (x->dtype != HK_F32 && x->dtype != HK_BF16) return fail(HK_INVALID_ARGUMENT, "bias add requires F32 or BF16 X");
+    if (bias->dtype != HK_F32 || bias->rank != 1 || bias->shape[0] != width)
+        return fail(HK_INVALID_ARGUMENT, "bias must be F32 [%lld]", static_cast<long long>(width));
+    if (residual && (residual->dtype != x->dtype || !same_shape(residual, x)))
+        return fail(HK_INVALID_ARGUMENT, "residual must match X exactly");
+    if (y->dtype != x->dtype || !same_shape(y, x)) return fail(HK_INVALID_ARGUMENT, "bias add output must match X");
+    if (residual ? !disjoint({y}, {x, bias, residual}) : !disjoint({y}, {x, bias})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t n = rows * width;
+    hipError_t e = hk::bias_add(x->dtype == HK_BF16, x->data, static_cast<const float*>(bias->data),
+                                residual ? residual->data : nullptr, y->data, n, width, g.c->stream);
+    return complete(g.c, e, residual ? "residual_bias_add" : "bias_add", n ? 1 : 0);
+}
+
+hk_status hk_bias_add_backward(hk_context* h, const hk_tensor* dy, hk_tensor* dbias) {
+    // Reference: runtime/affine.rs:23-26 -> normalization.rs:95-114 (column_sum).
+    if (!tensor_ok(dy, "dY") || !tensor_ok(dbias, "dbias")) return HK_INVALID_ARGUMENT;
+    int64_t rows, width;
+    if (!affine_layout(dy, &rows, &width, "bias add backward")) return HK_INVALID_ARGUMENT;
+    if (dy->dtype != HK_F32) return fail(HK_INVALID_ARGUMENT, "bias add backward requires F32 dY");
+    if (dbias->dtype != HK_F32 || dbias->rank != 1 || dbias->shape[0] != width)
+        return fail(HK_INVALID_ARGUMENT, "dbias must be F32 [%lld]", static_cast<long long>(width));
+    if (!disjoint({dbias}, {dy})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hk_status st = ensure_workspace(g.c, hk::column_sum_workspace_bytes(rows, width));
+    if (st != HK_OK) return st;
+    hipError_t e = hk::column_sum(static_cast<const float*>(dy->data), static_cast<float*>(dbias->data), rows, width,
+                                  g.c->workspace, g.c->stream);
+    return complete(g.c, e, "bias_add_backward", 1);
+}
+
+// ------------------------------------------------------------------ embedding
+
+namespace {
+// Reference: embedding.rs:21-26 (indices_layout: contiguous rank 1..7 INT32/INT64).
+bool ids_layout(const hk_tensor* ids, int64_t* tokens) {
+    if (!tensor_ok(ids, "IDs", true)) return false;
+    if (ids->rank < 1 || ids->rank > 7)
+        return fail(HK_INVALID_ARGUMENT, "embedding indices require contiguous rank 1..7 INT32/INT64 storage"), false;
+    *tokens = numel(ids);
+    if (*tokens > INT32_MAX) return fail(HK_INVALID_ARGUMENT, "embedding supports at most 2^31-1 IDs"), false;
+    return true;
+}
+bool ids_prefix(const hk_tensor* ids, const hk_tensor* t) {  // t = ids.shape + [H]
+    if (t->rank != ids->rank + 1) return false;
+    for (int i = 0; i < ids->rank; ++i)
+        if (t->shape[i] != ids->shape[i]) return false;
+    return true;
+}
+// After a synchronous call: read the kernel's out-of-range flag (the workspace's first int).
+hk_status ids_in_range(Ctx* c, hk_status st, int64_t vocab) {
+    if (st != HK_OK || c->async) return st;
+    int flag = 0;
+    if (hipMemcpy(&flag, c->workspace, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) {
+        c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "embedding: reading the index check failed");
+    }
+    if (flag) return fail(HK_INVALID_ARGUMENT, "embedding index outside [0, %lld)", static_cast<long long>(vocab));
+    return HK_OK;
+}
+}  // namespace
+
+hk_status hk_embedding(hk_context* h, const hk_tensor* weight, const hk_tensor* ids, hk_tensor* out) {
+    // Reference: runtime/indexing.rs:33-37, embedding.rs:27-34 (forward_layout) and :46-60.
+    int64_t tokens;
+    if (!tensor_ok(weight, "weight") || !ids_layout(ids, &tokens) || !tensor_ok(out, "out")) return HK_INVALID_ARGUMENT;
+    if (weight->rank != 2 || (weight->shape[0] == 0 && tokens != 0))
+        return fail(HK_INVALID_ARGUMENT,
+                    "embedding weight requires a rank-2 FP32/FP16/BF16 table; nonempty indices require weight rows");
+    if (weight->shape[0] > INT32_MAX) return fail(HK_INVALID_ARGUMENT, "embedding supports at most 2^31-1 table rows");
+    if (out->dtype != weight->dtype || !ids_prefix(ids, out) || out->shape[ids->rank] != weight->shape[1])
+        return fail(HK_INVALID_ARGUMENT, "embedding output must be [ids..., H] in the table's dtype");
+    if (!disjoint({out}, {weight, ids})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t vocab = weight->shape[0];
+    hk_status st = ensure_workspace(g.c, hk::embedding_workspace_bytes(tokens, vocab, false));
+    if (st != HK_OK) return st;
+    hipError_t e = hk::embedding(weight->data, static_cast<int>(dtype_size(ids->dtype)), ids->data, out->data, tokens,
+                                 vocab, weight->shape[1] * dtype_size(weight->dtype), g.c->workspace, g.c->stream);
+    return ids_in_range(g.c, complete(g.c, e, "embedding", 2), vocab);
+}
+
+hk_status hk_embedding_backward(hk_context* h, const hk_tensor* grad, const hk_tensor* ids, uint64_t num_weights,
+                                uint64_t padding_idx, int32_t scale_grad_by_freq, hk_tensor* dweight) {
+    // Reference: runtime/indexing.rs:60-64, embedding.rs:35-44 (backward_layout), :9-18 (padding
+    // sentinel) and :60-79 (dense backward).
+    int64_t tokens;
+    if (!tensor_ok(grad, "grad") || !ids_layout(ids, &tokens) || !tensor_ok(dweight, "dweight"))
+        return HK_INVALID_ARGUMENT;
+    if (num_weights > static_cast<uint64_t>(INT32_MAX))
+        return fail(HK_INVALID_ARGUMENT, "embedding supports at most 2^31-1 table rows");
+    if (padding_idx != HK_NO_PADDING && padding_idx >= num_weights)
+        return fail(HK_INVALID_ARGUMENT, "embedding padding index must be within the weight rows");
+    if (scale_grad_by_freq != 0 && scale_grad_by_freq != 1)
+        return fail(HK_INVALID_ARGUMENT, "scale_grad_by_freq must be 0 or 1");
+    const int64_t vocab = static_cast<int64_t>(num_weights);
+    if (!ids_prefix(ids, grad) || (vocab == 0 && tokens != 0))
+        return fail(HK_INVALID_ARGUMENT,
+                    "embedding gradient must have the index shape followed by the embedding width and floating dtype");
+    const int64_t width = grad->shape[ids->rank];
+    if (dweight->dtype != grad->dtype || dweight->rank != 2 || dweight->shape[0] != vocab || dweight->shape[1] != width)
+        return fail(HK_INVALID_ARGUMENT, "dweight must be [num_weights, H] in the gradient's dtype");
+    if (!disjoint({dweight}, {grad, ids})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hk_status st = ensure_workspace(g.c, hk::embedding_workspace_bytes(tokens, vocab, true));
+    if (st != HK_OK) return st;
+    hipError_t e = hk::embedding_backward(grad->dtype, grad->data, static_cast<int>(dtype_size(ids->dtype)), ids->data,
+                                          dweight->data, tokens, vocab, width, padding_idx, scale_grad_by_freq,
+                                          g.c->workspace, g.c->stream);
+    return ids_in_range(g.c, complete(g.c, e, "embedding_backward", tokens ? 5 : 3), vocab);
 }
 
 hk_status hk_softmax(hk_context* h, const hk_tensor* x, int32_t logarithmic, hk_tensor* y) {

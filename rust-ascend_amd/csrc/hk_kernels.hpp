@@ -39,11 +39,30 @@ size_t gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k, int 
 hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_t batch, int64_t m,
                      int64_t n, int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s);
 
-// ---- attention (hk_attention.hip)
-// SwiGLU gate, element-wise over n values of F32 or BF16 storage (hk_elementwise.hip).
+// ---- element-wise (hk_elementwise.hip)
+// SwiGLU gate, element-wise over n values of F32 or BF16 storage.
 hipError_t silu_mul(int dtype_bf16, const void* gate, const void* up, void* y, int64_t n, hipStream_t s);
 hipError_t silu_mul_backward(int dtype_bf16, const void* gate, const void* up, const void* dy, void* dgate,
                              void* dup, int64_t n, hipStream_t s);
+// y = (x + residual) + bias[i % width] over n values (residual may be null); x/residual/y F32 or
+// BF16 storage, bias F32.
+hipError_t bias_add(int dtype_bf16, const void* x, const float* bias, const void* residual, void* y, int64_t n,
+                    int64_t width, hipStream_t s);
+// out[width] = pairwise column sum of dy[rows, width] (F32) in the order of repeated halving.
+size_t column_sum_workspace_bytes(int64_t rows, int64_t width);
+hipError_t column_sum(const float* dy, float* out, int64_t rows, int64_t width, void* workspace, hipStream_t s);
+
+// ---- embedding (hk_embedding.hip)
+// Lookup of `tokens` rows of `row_bytes` bytes from a [vocab, .] table by INT32/INT64 IDs
+// (id_bytes 4 or 8); the workspace's first int becomes nonzero if an ID lies outside [0, vocab).
+size_t embedding_workspace_bytes(int64_t tokens, int64_t vocab, bool backward);
+hipError_t embedding(const void* table, int id_bytes, const void* ids, void* out, int64_t tokens, int64_t vocab,
+                     int64_t row_bytes, void* workspace, hipStream_t s);
+// Dense gradient dw[vocab, width] from grad[tokens, width]; dtype is the hk_dtype code of grad/dw
+// (F32, F16 or BF16); padding == UINT64_MAX means no padding row.
+hipError_t embedding_backward(int dtype, const void* grad, int id_bytes, const void* ids, void* dw, int64_t tokens,
+                              int64_t vocab, int64_t width, uint64_t padding, int scale, void* workspace,
+                              hipStream_t s);
 
 // Row softmax / log-softmax over the last axis of contiguous F32 [rows, width] (hk_softmax.hip).
 hipError_t softmax_forward(const float* x, float* y, int64_t rows, int64_t width, int logarithmic, hipStream_t s);
@@ -59,6 +78,7 @@ size_t repeat_kv_backward_workspace_bytes(int64_t batch, int64_t kv_heads, int64
 hipError_t repeat_kv_heads_backward(const float* dy, float* dx, int64_t batch, int64_t kv_heads,
                                     int64_t query_heads, int64_t plane, void* workspace, hipStream_t s);
 
+// ---- attention (hk_attention.hip)
 struct AttnShape {
     int64_t batch, heads, kv_heads, m, n, d;
     float scale;

@@ -22,6 +22,8 @@ STATUS_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", HIP_ERROR: "HIP_
 
 # Element type codes (reference DType codes, rust-ascend-driver/src/tensor/layout.rs:5-17).
 F32, F16, BF16 = 0, 1, 27
+I32, I64 = 3, 9
+NO_PADDING = (1 << 64) - 1  # HK_NO_PADDING
 MAX_RANK = 8
 
 
@@ -81,6 +83,10 @@ SIGNATURES = {
     "hk_cast_into": [_CTX, _T, _T],
     "hk_silu_mul": [_CTX, _T, _T, _T],
     "hk_silu_mul_backward": [_CTX, _T, _T, _T, _T, _T],
+    "hk_bias_add": [_CTX, _T, _T, _T, _T],
+    "hk_bias_add_backward": [_CTX, _T, _T],
+    "hk_embedding": [_CTX, _T, _T, _T],
+    "hk_embedding_backward": [_CTX, _T, _T, _u64, _u64, _i32, _T],
     "hk_softmax": [_CTX, _T, _i32, _T],
     "hk_softmax_backward": [_CTX, _T, _T, _i32, _T],
     "hk_causal_mask": [_CTX, _u64, _u64, _T],

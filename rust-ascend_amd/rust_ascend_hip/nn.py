@@ -139,6 +139,56 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return _SiluMul.apply(gate.contiguous(), up.contiguous())
 
 
+class _BiasAdd(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, bias, residual):
+        ctx.has_residual = residual is not None
+        return HipRuntime.bias_add(x, bias, residual)
+
+    @staticmethod
+    def backward(ctx, dy):
+        dy = dy.contiguous()
+        # only a bias that needs a gradient pays for the column reduction (affine.rs:52-58)
+        db = HipRuntime.bias_add_backward(dy) if ctx.needs_input_grad[1] else None
+        return dy, db, (dy if ctx.has_residual else None)
+
+
+def bias_add(x: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """X[..., H] + bias[H] (F32; BF16 X also accepted). Reference: nn::bias_add (src/nn/affine.rs:14-20)."""
+    return _BiasAdd.apply(x.contiguous(), bias.contiguous(), None)
+
+
+def residual_bias_add(x: torch.Tensor, residual: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """(X + residual) + bias in that F32 order; residual must match X exactly. Reference:
+    nn::residual_bias_add (src/nn/affine.rs:21-25)."""
+    return _BiasAdd.apply(x.contiguous(), bias.contiguous(), residual.contiguous())
+
+
+class _Embedding(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, weight, ids, padding_idx, scale_grad_by_freq):
+        out = HipRuntime.embedding(weight, ids)
+        ctx.save_for_backward(ids.clone())  # an independent snapshot of the IDs (mod.rs:248-251)
+        ctx.rows = weight.shape[0]
+        ctx.options = (padding_idx, scale_grad_by_freq)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        (ids,) = ctx.saved_tensors
+        padding_idx, scale = ctx.options
+        dw = HipRuntime.embedding_backward(dy.contiguous(), ids, ctx.rows, padding_idx, scale)
+        return dw, None, None, None
+
+
+def embedding(weight: torch.Tensor, ids: torch.Tensor, padding_idx=None, scale_grad_by_freq: bool = False):
+    """weight[ids] with a dense weight gradient; padding affects only the derivative. Reference:
+    nn::embedding / embedding_nd with EmbeddingOptions (src/nn/embedding.rs:14-31, 54-90)."""
+    if padding_idx is not None and not 0 <= padding_idx < weight.shape[0]:
+        raise ValueError("embedding padding row is outside its table")
+    return _Embedding.apply(weight.contiguous(), ids.contiguous(), padding_idx, bool(scale_grad_by_freq))
+
+
 def swiglu_bf16_fp32(x: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
     """(SiLU(x gate^T) * (x up^T)) down^T with F32 storage and BF16 linear compute.
     Reference: nn::swiglu_bf16_fp32 (src/nn/feed_forward.rs:24-42): gate/up [H,K], down [N,H],

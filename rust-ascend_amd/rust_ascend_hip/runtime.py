@@ -16,7 +16,7 @@ import threading
 import torch
 
 from . import _lib
-from ._lib import BF16, F16, F32, HkError, check, tensor_desc
+from ._lib import BF16, F16, F32, I32, I64, NO_PADDING, HkError, check, tensor_desc
 
 
 class Transpose(enum.IntEnum):
@@ -31,7 +31,7 @@ class RotaryLayout(enum.IntEnum):
     SplitHalf = 1
 
 
-_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32, torch.int64: I64}
 _TORCH = {v: k for k, v in _DTYPES.items()}
 
 _ctx = None
@@ -210,6 +210,44 @@ class HipRuntime:
         du = _empty(gate.shape, gate.dtype, gate)
         _call("hk_silu_mul_backward", desc(gate), desc(up), desc(grad), desc(dg), desc(du))
         return dg, du
+
+    # ---------------------------------------------------------------- bias and residual add
+
+    @staticmethod
+    def bias_add(x, bias, residual=None):
+        """(X + residual) + bias over the last axis (residual optional). Reference:
+        AscendRuntime::bias_add (mod.rs:177-181)."""
+        y = _empty(x.shape, x.dtype, x)
+        _call("hk_bias_add", desc(x), desc(bias), desc(residual) if residual is not None else None, desc(y))
+        return y
+
+    @staticmethod
+    def bias_add_backward(grad):
+        """dbias = dY summed over the leading axes in the reference's pairwise order. Reference:
+        AscendRuntime::bias_add_backward (mod.rs:182-185)."""
+        db = _empty((grad.shape[-1],), torch.float32, grad)
+        _call("hk_bias_add_backward", desc(grad), desc(db))
+        return db
+
+    # ---------------------------------------------------------------- embedding
+
+    @staticmethod
+    def embedding(weight, ids):
+        """weight[ids] -> [ids..., H]. Reference: AscendRuntime::embedding (mod.rs:237-241)."""
+        out = _empty(tuple(ids.shape) + (weight.shape[1],), weight.dtype, weight)
+        _call("hk_embedding", desc(weight), desc(ids), desc(out))
+        return out
+
+    @staticmethod
+    def embedding_backward(grad, ids, num_weights: int, padding_idx=None, scale_grad_by_freq: bool = False):
+        """Dense [num_weights, H] weight gradient. Reference: AscendRuntime::embedding_backward
+        (mod.rs:252-256) with EmbeddingOptions {padding_idx, scale_grad_by_freq}."""
+        if padding_idx is not None and (padding_idx < 0 or padding_idx >= num_weights):
+            raise HkError(_lib.INVALID_ARGUMENT, "embedding padding index must be within the weight rows")
+        dw = _empty((int(num_weights), grad.shape[-1]), grad.dtype, grad)
+        _call("hk_embedding_backward", desc(grad), desc(ids), int(num_weights),
+              NO_PADDING if padding_idx is None else int(padding_idx), int(bool(scale_grad_by_freq)), desc(dw))
+        return dw
 
     # ---------------------------------------------------------------- composed-attention shims
 

@@ -458,3 +458,82 @@ def test_silu_mul_backward_catches_planted_mistakes(oracle):
             close(bad, dg, 2e-5, 1e-4)
     with pytest.raises(AssertionError):
         close(dy * u, du, 2e-5, 1e-4)             # dup must carry silu(g), not u
+
+
+# ------------------------------------------------------------------ bias / residual add
+
+from ref_cases import BIAS_SHAPES, bias_inputs, embedding_reference_inputs  # noqa: E402
+
+
+@pytest.mark.parametrize("shape", BIAS_SHAPES)
+def test_bias_add_reference_cases(oracle, shape):
+    x, r, b, dy = bias_inputs(shape)
+    x64, r64, b64 = (t.astype(np.float64) for t in (x, r, b))
+    # every value is a multiple of 1/16, so float32 sums are exact: compare with float64 exactly
+    np.testing.assert_array_equal(oracle.bias_add_f32(x, b), x64 + b64)
+    np.testing.assert_array_equal(oracle.bias_add_f32(x, b, r), x64 + r64 + b64)
+    np.testing.assert_array_equal(oracle.bias_add_f32(x, b, x), 2 * x64 + b64)
+    width = shape[-1]
+    want = dy.astype(np.float64).reshape(-1, width).sum(0) if dy.size else np.zeros(width)
+    np.testing.assert_array_equal(oracle.bias_add_backward(dy), want)
+
+
+def test_bias_add_order_and_nonfinite(oracle):
+    # bias_tensor.rs:60-61: (1e20 + -1e20) + 1 == 1; x + (r + b) would give 0
+    one = np.ones(1, np.float32)
+    assert oracle.bias_add_f32(1e20 * one, one, -1e20 * one)[0] == 1.0
+    # bias_tensor.rs:62-65: -0, NaN and infinities follow IEEE float32 addition
+    data = np.array([0.0, -0.0, np.nan, np.inf, -np.inf, 1.0, -1.0], np.float32)
+    got = oracle.bias_add_f32(data, np.ones(7, np.float32))
+    np.testing.assert_array_equal(got, data + np.float32(1))
+
+
+def test_column_sum_follows_the_halving_order(oracle):
+    # runtime/normalization.rs:95-114 adds row i and row i + floor(r/2) per level; on these
+    # columns that order decides the float32 result
+    parts = np.array([[1e8], [-1e8], [1.0], [1.0]], np.float32)
+    assert oracle.column_sum_pairwise(parts)[0] == 0.0          # (1e8+1) + (-1e8+1) -> 0
+    assert np.float32(np.float32(np.float32(1e8) - np.float32(1e8)) + 1) + 1 == 2.0  # left to right
+    parts5 = np.array([[1e8], [1.0], [-1e8], [1.0], [0.0]], np.float32)
+    assert oracle.column_sum_pairwise(parts5)[0] == 2.0         # (1e8-1e8)+(1+1), then + 0
+    seq = np.float32(0)
+    for v in parts5[:, 0]:
+        seq = np.float32(seq + v)
+    assert seq == 1.0                                            # the sequential sum differs
+
+
+# ------------------------------------------------------------------ embedding
+
+def _torch_embedding(weights, ids, dy, padding_idx, scale):
+    w = torch.tensor(weights, dtype=torch.float64, requires_grad=True)
+    y = torch.nn.functional.embedding(torch.tensor(ids, dtype=torch.int64), w, padding_idx=padding_idx,
+                                      scale_grad_by_freq=scale)
+    y.backward(torch.tensor(dy, dtype=torch.float64))
+    return y.detach().numpy(), w.grad.numpy()
+
+
+@pytest.mark.parametrize("padding_idx", [None, 0])
+@pytest.mark.parametrize("scale", [False, True])
+def test_embedding_vs_torch_reference_cases(oracle, padding_idx, scale):
+    weights, ids, upstream = embedding_reference_inputs()
+    dy = 2 * upstream  # the example's loss y*dy + y*dy
+    want_y, want_dw = _torch_embedding(weights, ids, dy, padding_idx, scale)
+    np.testing.assert_array_equal(oracle.embedding(weights, ids), want_y)
+    close(oracle.embedding_backward_f64(dy, ids, 7, padding_idx, scale), want_dw, 1e-12, 1e-12)
+
+
+def test_embedding_random_and_empty(oracle):
+    rng = np.random.default_rng(4)
+    weights = rng.standard_normal((50, 24)).astype(np.float32)
+    ids = rng.integers(0, 50, (6, 40))
+    dy = rng.standard_normal((6, 40, 24)).astype(np.float32)
+    for padding_idx, scale in [(None, False), (7, True), (ids[0, 0], False)]:
+        want_y, want_dw = _torch_embedding(weights, ids, dy, padding_idx, scale)
+        np.testing.assert_array_equal(oracle.embedding(weights, ids), want_y)
+        close(oracle.embedding_backward_f64(dy, ids, 50, padding_idx, scale), want_dw, 1e-12, 1e-12)
+    # embedding_tensor.rs:47-53: no IDs -> zero gradient
+    empty = np.zeros((0, 3), np.int32)
+    assert oracle.embedding(weights, empty).shape == (0, 3, 24)
+    np.testing.assert_array_equal(oracle.embedding_backward_f64(np.zeros((0, 3, 24)), empty, 50), np.zeros((50, 24)))
+    with pytest.raises(ValueError):
+        oracle.embedding(weights, np.array([50]))
