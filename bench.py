@@ -5,8 +5,8 @@ Prints ONE JSON line. The headline workload is BASELINE config C2, RMSNorm forwa
 x[16384,4096] BF16 / weight F32 / eps 1e-6 (configs[1]; configs[0] is the reference's small
 CPU-runnable Linear). A step is one forward plus one backward over that batch; `value` is
 algorithmic HBM bytes per step / wall time per step. The BF16 GEMM (C3), RoPE (C4's Q/K), the
-C1 Linear and, when built, fused attention (C4) are measured in the same run and reported
-under "secondary", each with its own roofline. Inputs are synthetic, seeded and resident in
+C1 Linear, fused attention (C4) and one decoder layer forward+backward (C5) are measured in the
+same run and reported under "secondary", the kernels each with its own roofline. Inputs are synthetic, seeded and resident in
 HBM before timing starts. Kernel durations come from HIP events recorded on the stream the
 kernels run on (torch's current stream, which libhk.so is bound to for every call).
 
@@ -245,6 +245,32 @@ def bench_attention(iters=5):
     return event_ms(fw), event_ms(bw), fwd_flops, 2.5 * fwd_flops
 
 
+def bench_decoder(steps=5, warmup=2):
+    """C5: one Llama-style decoder layer forward + backward (hidden 4096, 32/8 heads, SwiGLU 14336,
+    batch 2 x seq 2048, token IDs uniform in [0, 32000), N(0, 0.02) BF16 weights)."""
+    import torch
+    from rust_ascend_hip import DecoderConfig, DecoderLayer
+    cfg = DecoderConfig()
+    layer = DecoderLayer(cfg, seed=5)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    layer.ids.copy_(torch.randint(0, cfg.vocab, (cfg.batch, cfg.seq), generator=g, device="cuda"))
+    layer.dy.copy_(torch.randn(layer.dy.shape, generator=g, device="cuda").to(torch.bfloat16))
+    for _ in range(warmup):
+        layer.step()
+    fw, bw = [], []
+    for _ in range(steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        layer._run(layer._forward)
+        e[1].record()
+        layer._run(layer._backward)
+        e[2].record()
+        fw.append((e[0], e[1]))
+        bw.append((e[1], e[2]))
+    return cfg, event_ms(fw), event_ms(bw)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -311,6 +337,18 @@ def main():
                         "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq")})
         except Exception as exc:  # reported, never silently replaced by another path
             sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
+        try:
+            cfg, f_ms, b_ms = bench_decoder()
+            step_ms = f_ms + b_ms
+            fl = cfg.flops_per_step()
+            sec.append({"workload": "C5 Llama decoder layer fwd+bwd: hidden 4096, 32/8 heads, SwiGLU 14336, "
+                                    "B2 x S2048, vocab 32000, BF16",
+                        "value": round(cfg.tokens / (step_ms * 1e-3), 1), "unit": "tokens/s",
+                        "ms": round(step_ms, 4), "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+                        "model_TFLOPs": round(fl["total"] / (step_ms * 1e-3) / 1e12, 1),
+                        "frac_of_bf16_peak": round(fl["total"] / (step_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
+        except Exception as exc:
+            sec.append({"workload": "C5 decoder layer", "error": str(exc)[:200]})
         line["secondary"] = sec
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")

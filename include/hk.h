@@ -218,7 +218,8 @@ hk_status hk_silu_mul_backward(hk_context* ctx, const hk_tensor* gate, const hk_
 /* y = (x + residual) + bias[c] over the last axis c, in that F32 order; residual may be NULL
  * (y = x + bias). X rank 1..8 with a positive last axis and at most 2^32-1 elements; X, residual
  * and Y F32 (the reference's dtype) or BF16 storage with F32 arithmetic; bias F32 [width];
- * residual exactly X's shape. Reference: AscendRuntime::bias_add, runtime/mod.rs:177-181
+ * residual exactly X's shape. Beyond the reference, bias may be NULL when a residual is given
+ * (y = x + residual: the decoder layer's bias-free residual adds). Reference: AscendRuntime::bias_add, runtime/mod.rs:177-181
  * (runtime/affine.rs:10-22; nn::bias_add / residual_bias_add, src/nn/affine.rs:14-25). */
 hk_status hk_bias_add(hk_context* ctx, const hk_tensor* x, const hk_tensor* bias, const hk_tensor* residual,
                       hk_tensor* y);
@@ -227,6 +228,24 @@ hk_status hk_bias_add(hk_context* ctx, const hk_tensor* x, const hk_tensor* bias
  * there are no rows. Reference: AscendRuntime::bias_add_backward, runtime/mod.rs:182-185
  * (runtime/affine.rs:23-26, normalization.rs:95-114). */
 hk_status hk_bias_add_backward(hk_context* ctx, const hk_tensor* dy, hk_tensor* dbias);
+
+/* ---------------------------------------------------------------- decoder-layer relayouts */
+
+/* These have no counterpart in the reference, whose composed layers keep one tensor per
+ * projection; they serve a decoder layer built on one fused QKV projection. BF16, 16-byte aligned
+ * tensors, D % 16 == 0.
+ * qkv [B, S, (Hq + 2 Hkv) D] (per token: Q heads, K heads, V heads) -> q [B, Hq, S, D],
+ * k, v [B, Hkv, S, D], with RoPE applied to Q and K in the same pass (the rotation of hk_rotary,
+ * same layout codes, F32 tables cos/sin [S, D/2] indexed by the position s; bit-identical to
+ * hk_rotary_prefix on [1,1,S,D/2] tables) and V copied bit-exactly. */
+hk_status hk_qkv_rope_split(hk_context* ctx, const hk_tensor* qkv, const hk_tensor* cos, const hk_tensor* sin,
+                            int32_t layout, hk_tensor* q, hk_tensor* k, hk_tensor* v);
+/* The transpose: dQ, dK (rotated back) and dV -> dqkv [B, S, (Hq + 2 Hkv) D]. */
+hk_status hk_qkv_rope_merge(hk_context* ctx, const hk_tensor* dq, const hk_tensor* dk, const hk_tensor* dv,
+                            const hk_tensor* cos, const hk_tensor* sin, int32_t layout, hk_tensor* dqkv);
+/* x [B, H, S, D] -> y [B, S, H D] (attention output into token rows), and the reverse; D % 8 == 0. */
+hk_status hk_heads_to_rows(hk_context* ctx, const hk_tensor* x, hk_tensor* y);
+hk_status hk_rows_to_heads(hk_context* ctx, const hk_tensor* x, hk_tensor* y);
 
 /* ---------------------------------------------------------------- embedding */
 

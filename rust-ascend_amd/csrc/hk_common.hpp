@@ -122,6 +122,22 @@ template <> struct Chunk<_Float16> {
     }
 };
 
+// RoPE rotation of the pair (a, b) by (c, s) = (cos, sin) of its angle, in the reference's
+// expression order (rust-ascend-compiler/src/ascend/rotary_programs.rs:47-156): forward
+// y_a = a c - b s, y_b = b c + a s; backward (the transpose Jacobian) y_a = a c + b s,
+// y_b = b c - a s. Every kernel that rotates calls this, so fused and standalone RoPE agree bit
+// for bit.
+template <bool BWD>
+__device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, float& ya, float& yb) {
+    if constexpr (!BWD) {
+        ya = a * c - b * s;
+        yb = b * c + a * s;
+    } else {
+        ya = a * c + b * s;
+        yb = b * c - a * s;
+    }
+}
+
 // Every pointer 16-byte aligned (the vector chunk paths need it).
 __host__ __forceinline__ bool aligned16(std::initializer_list<const void*> ptrs) {
     for (const void* p : ptrs)

@@ -617,7 +617,7 @@ hk_status hk_cast_into(hk_context* h, const hk_tensor* in, hk_tensor* out) {
 
 namespace {
 // Reference: elementwise.rs:5-11 (check_for: contiguous, one shape; element count <= u32).
-bool gate_shapes(std::initializer_list<const hk_tensor*> ts, const char* op) {
+static bool gate_shapes(std::initializer_list<const hk_tensor*> ts, const char* op) {
     const hk_tensor* first = *ts.begin();
     if (first->dtype != HK_F32 && first->dtype != HK_BF16)
         return fail(HK_INVALID_ARGUMENT, "%s requires F32 or BF16 tensors", op), false;
@@ -662,7 +662,7 @@ hk_status hk_silu_mul_backward(hk_context* h, const hk_tensor* gate, const hk_te
 
 namespace {
 // Reference: affine.rs:6-9 with wide_rows.rs:13-20 (rank 1..8, positive width, count <= u32).
-bool affine_layout(const hk_tensor* t, int64_t* rows, int64_t* width, const char* op) {
+static bool affine_layout(const hk_tensor* t, int64_t* rows, int64_t* width, const char* op) {
     if (t->rank < 1 || t->rank > 8) return fail(HK_INVALID_ARGUMENT, "%s requires rank 1..8", op), false;
     *width = t->shape[t->rank - 1];
     if (*width <= 0) return fail(HK_INVALID_ARGUMENT, "%s requires a positive last axis", op), false;
@@ -676,21 +676,23 @@ bool affine_layout(const hk_tensor* t, int64_t* rows, int64_t* width, const char
 hk_status hk_bias_add(hk_context* h, const hk_tensor* x, const hk_tensor* bias, const hk_tensor* residual,
                       hk_tensor* y) {
     // Reference: runtime/affine.rs:10-22 (forward), src/nn/affine.rs:17-25.
-    if (!tensor_ok(x, "X") || !tensor_ok(bias, "bias") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
-    if (residual && !tensor_ok(residual, "residual")) return HK_INVALID_ARGUMENT;
+    if (!tensor_ok(x, "X") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    if (!bias && !residual) return fail(HK_INVALID_ARGUMENT, "bias add needs a bias, a residual or both");
+    if ((bias && !tensor_ok(bias, "bias")) || (residual && !tensor_ok(residual, "residual"))) return HK_INVALID_ARGUMENT;
     int64_t rows, width;
     if (!affine_layout(x, &rows, &width, "bias add")) return HK_INVALID_ARGUMENT;
     if (x->dtype != HK_F32 && x->dtype != HK_BF16) return fail(HK_INVALID_ARGUMENT, "bias add requires F32 or BF16 X");
-    if (bias->dtype != HK_F32 || bias->rank != 1 || bias->shape[0] != width)
+    if (bias && (bias->dtype != HK_F32 || bias->rank != 1 || bias->shape[0] != width))
         return fail(HK_INVALID_ARGUMENT, "bias must be F32 [%lld]", static_cast<long long>(width));
     if (residual && (residual->dtype != x->dtype || !same_shape(residual, x)))
         return fail(HK_INVALID_ARGUMENT, "residual must match X exactly");
     if (y->dtype != x->dtype || !same_shape(y, x)) return fail(HK_INVALID_ARGUMENT, "bias add output must match X");
-    if (residual ? !disjoint({y}, {x, bias, residual}) : !disjoint({y}, {x, bias})) return HK_INVALID_ARGUMENT;
+    if (!disjoint({y}, {x}) || (bias && !disjoint({y}, {bias})) || (residual && !disjoint({y}, {residual})))
+        return HK_INVALID_ARGUMENT;
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
     const int64_t n = rows * width;
-    hipError_t e = hk::bias_add(x->dtype == HK_BF16, x->data, static_cast<const float*>(bias->data),
+    hipError_t e = hk::bias_add(x->dtype == HK_BF16, x->data, bias ? static_cast<const float*>(bias->data) : nullptr,
                                 residual ? residual->data : nullptr, y->data, n, width, g.c->stream);
     return complete(g.c, e, residual ? "residual_bias_add" : "bias_add", n ? 1 : 0);
 }
@@ -713,11 +715,84 @@ hk_status hk_bias_add_backward(hk_context* h, const hk_tensor* dy, hk_tensor* db
     return complete(g.c, e, "bias_add_backward", 1);
 }
 
+// ------------------------------------------------------------------ decoder-layer relayouts
+
+namespace {
+static bool aligned_bf16(std::initializer_list<const hk_tensor*> ts, const char* op) {
+    for (const hk_tensor* t : ts) {
+        if (t->dtype != HK_BF16) return fail(HK_INVALID_ARGUMENT, "%s requires BF16 tensors", op), false;
+        if (reinterpret_cast<uintptr_t>(t->data) % 16 != 0)
+            return fail(HK_INVALID_ARGUMENT, "%s requires 16-byte aligned tensors", op), false;
+    }
+    return true;
+}
+static bool dims_are(const hk_tensor* t, std::initializer_list<int64_t> dims) {
+    if (t->rank != static_cast<int32_t>(dims.size())) return false;
+    int i = 0;
+    for (int64_t d : dims)
+        if (t->shape[i++] != d) return false;
+    return true;
+}
+// rows [B,S,(Hq+2Hkv)D], q [B,Hq,S,D], k/v [B,Hkv,S,D], tables [S, D/2] F32.
+static hk_status qkv_rope_common(hk_context* h, bool merge, const hk_tensor* rows, const hk_tensor* q, const hk_tensor* k,
+                          const hk_tensor* v, const hk_tensor* c, const hk_tensor* s, int32_t layout) {
+    const char* op = merge ? "qkv_rope_merge" : "qkv_rope_split";
+    if (!tensor_ok(rows, "QKV rows") || !tensor_ok(q, "Q") || !tensor_ok(k, "K") || !tensor_ok(v, "V") ||
+        !tensor_ok(c, "cos") || !tensor_ok(s, "sin"))
+        return HK_INVALID_ARGUMENT;
+    if (layout != HK_ROTARY_INTERLEAVED && layout != HK_ROTARY_SPLIT_HALF)
+        return fail(HK_INVALID_ARGUMENT, "rotary layout must be 0 (Interleaved) or 1 (SplitHalf)");
+    if (!aligned_bf16({rows, q, k, v}, op)) return HK_INVALID_ARGUMENT;
+    if (q->rank != 4 || k->rank != 4) return fail(HK_INVALID_ARGUMENT, "%s requires Q[B,Hq,S,D] and K/V[B,Hkv,S,D]", op);
+    const int64_t B = q->shape[0], Hq = q->shape[1], S = q->shape[2], D = q->shape[3], Hkv = k->shape[1];
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || D <= 0 || D % 16 != 0)
+        return fail(HK_INVALID_ARGUMENT, "%s requires positive dimensions and D %% 16 == 0", op);
+    if (!dims_are(k, {B, Hkv, S, D}) || !dims_are(v, {B, Hkv, S, D}) || !dims_are(rows, {B, S, (Hq + 2 * Hkv) * D}))
+        return fail(HK_INVALID_ARGUMENT, "%s requires rows [B,S,(Hq+2Hkv)D], Q [B,Hq,S,D], K/V [B,Hkv,S,D]", op);
+    if (c->dtype != HK_F32 || s->dtype != HK_F32 || !dims_are(c, {S, D / 2}) || !dims_are(s, {S, D / 2}) ||
+        reinterpret_cast<uintptr_t>(c->data) % 16 != 0 || reinterpret_cast<uintptr_t>(s->data) % 16 != 0)
+        return fail(HK_INVALID_ARGUMENT, "%s requires 16-byte aligned F32 cos/sin tables [S, D/2]", op);
+    if (merge ? !disjoint({rows}, {q, k, v, c, s}) : !disjoint({q, k, v}, {rows, c, s})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::qkv_rope(merge, layout, rows->data, q->data, k->data, v->data, static_cast<const float*>(c->data),
+                                static_cast<const float*>(s->data), B, S, Hq, Hkv, D, g.c->stream);
+    return complete(g.c, e, op, 1);
+}
+static hk_status heads_rows_common(hk_context* h, bool to_rows, const hk_tensor* x, hk_tensor* y) {
+    const char* op = to_rows ? "heads_to_rows" : "rows_to_heads";
+    if (!tensor_ok(x, "X") || !tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    if (!aligned_bf16({x, y}, op)) return HK_INVALID_ARGUMENT;
+    const hk_tensor* planes = to_rows ? x : y;
+    const hk_tensor* rows = to_rows ? y : x;
+    if (planes->rank != 4) return fail(HK_INVALID_ARGUMENT, "%s requires head planes [B,H,S,D]", op);
+    const int64_t B = planes->shape[0], H = planes->shape[1], S = planes->shape[2], D = planes->shape[3];
+    if (D <= 0 || D % 8 != 0 || !dims_are(rows, {B, S, H * D}))
+        return fail(HK_INVALID_ARGUMENT, "%s requires planes [B,H,S,D] (D %% 8 == 0) and rows [B,S,H*D]", op);
+    if (!disjoint({y}, {x})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::heads_rows(to_rows, x->data, y->data, B, H, S, D, g.c->stream);
+    return complete(g.c, e, op, 1);
+}
+}  // namespace
+
+hk_status hk_qkv_rope_split(hk_context* h, const hk_tensor* qkv, const hk_tensor* cos, const hk_tensor* sin,
+                            int32_t layout, hk_tensor* q, hk_tensor* k, hk_tensor* v) {
+    return qkv_rope_common(h, false, qkv, q, k, v, cos, sin, layout);
+}
+hk_status hk_qkv_rope_merge(hk_context* h, const hk_tensor* dq, const hk_tensor* dk, const hk_tensor* dv,
+                            const hk_tensor* cos, const hk_tensor* sin, int32_t layout, hk_tensor* dqkv) {
+    return qkv_rope_common(h, true, dqkv, dq, dk, dv, cos, sin, layout);
+}
+hk_status hk_heads_to_rows(hk_context* h, const hk_tensor* x, hk_tensor* y) { return heads_rows_common(h, true, x, y); }
+hk_status hk_rows_to_heads(hk_context* h, const hk_tensor* x, hk_tensor* y) { return heads_rows_common(h, false, x, y); }
+
 // ------------------------------------------------------------------ embedding
 
 namespace {
 // Reference: embedding.rs:21-26 (indices_layout: contiguous rank 1..7 INT32/INT64).
-bool ids_layout(const hk_tensor* ids, int64_t* tokens) {
+static bool ids_layout(const hk_tensor* ids, int64_t* tokens) {
     if (!tensor_ok(ids, "IDs", true)) return false;
     if (ids->rank < 1 || ids->rank > 7)
         return fail(HK_INVALID_ARGUMENT, "embedding indices require contiguous rank 1..7 INT32/INT64 storage"), false;
@@ -725,14 +800,14 @@ bool ids_layout(const hk_tensor* ids, int64_t* tokens) {
     if (*tokens > INT32_MAX) return fail(HK_INVALID_ARGUMENT, "embedding supports at most 2^31-1 IDs"), false;
     return true;
 }
-bool ids_prefix(const hk_tensor* ids, const hk_tensor* t) {  // t = ids.shape + [H]
+static bool ids_prefix(const hk_tensor* ids, const hk_tensor* t) {  // t = ids.shape + [H]
     if (t->rank != ids->rank + 1) return false;
     for (int i = 0; i < ids->rank; ++i)
         if (t->shape[i] != ids->shape[i]) return false;
     return true;
 }
 // After a synchronous call: read the kernel's out-of-range flag (the workspace's first int).
-hk_status ids_in_range(Ctx* c, hk_status st, int64_t vocab) {
+static hk_status ids_in_range(Ctx* c, hk_status st, int64_t vocab) {
     if (st != HK_OK || c->async) return st;
     int flag = 0;
     if (hipMemcpy(&flag, c->workspace, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) {
@@ -852,7 +927,7 @@ hk_status hk_causal_mask(hk_context* h, uint64_t query_start, uint64_t key_start
 
 namespace {
 // [B, H, N, D] F32 with both element counts within u32 (RepeatKvSpec::elements, heads_programs.rs:5-18).
-bool kv_shapes(const hk_tensor* kv, const hk_tensor* qh, const char* kv_name, const char* q_name) {
+static bool kv_shapes(const hk_tensor* kv, const hk_tensor* qh, const char* kv_name, const char* q_name) {
     if (kv->dtype != HK_F32 || qh->dtype != HK_F32 || kv->rank != 4 || qh->rank != 4)
         return fail(HK_INVALID_ARGUMENT, "KV repetition requires F32 [B,Hkv,N,D] %s and [B,Hq,N,D] %s", kv_name, q_name),
                false;

@@ -86,8 +86,8 @@ silu_mul_bwd_kernel(const T* __restrict__ g, const T* __restrict__ u, const T* _
     }
 }
 
-// y = (x + r) + b[i % width]; with vec, width % P == 0 so a chunk never crosses a row and its
-// bias slice b[c .. c+P) is 16-byte aligned.
+// y = (x + r) + b[i % width] (b may be null: y = x + r); with vec, width % P == 0 so a chunk
+// never crosses a row and its bias slice b[c .. c+P) is 16-byte aligned.
 template <typename T, bool RES>
 __global__ void __launch_bounds__(kEwThreads)
 bias_add_kernel(const T* __restrict__ x, const float* __restrict__ b, const T* __restrict__ r, T* __restrict__ y,
@@ -98,20 +98,25 @@ bias_add_kernel(const T* __restrict__ x, const float* __restrict__ b, const T* _
         float xv[P], rv[P], bv[P], o[P];
         Chunk<T>::load(x + i0, xv);
         if (RES) Chunk<T>::load(r + i0, rv);
-        const float* bp = b + i0 % width;
+        if (b) {
+            const float* bp = b + i0 % width;
 #pragma unroll
-        for (int q = 0; q < P / 4; ++q) {
-            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bp + 4 * q);
+            for (int q = 0; q < P / 4; ++q) {
+                const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bp + 4 * q);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) bv[4 * q + e] = w[e];
+                for (int e = 0; e < 4; ++e) bv[4 * q + e] = w[e];
+            }
         }
 #pragma unroll
-        for (int e = 0; e < P; ++e) o[e] = (RES ? xv[e] + rv[e] : xv[e]) + bv[e];
+        for (int e = 0; e < P; ++e) {
+            const float sum = RES ? xv[e] + rv[e] : xv[e];
+            o[e] = b ? sum + bv[e] : sum;
+        }
         Chunk<T>::store(y + i0, o);
     } else {
         for (int64_t i = i0; i < n && i < i0 + P; ++i) {
             const float s = RES ? Elem<T>::load(x, i) + Elem<T>::load(r, i) : Elem<T>::load(x, i);
-            Elem<T>::store(y, i, s + b[i % width]);
+            Elem<T>::store(y, i, b ? s + b[i % width] : s);
         }
     }
 }

@@ -78,6 +78,15 @@ size_t repeat_kv_backward_workspace_bytes(int64_t batch, int64_t kv_heads, int64
 hipError_t repeat_kv_heads_backward(const float* dy, float* dx, int64_t batch, int64_t kv_heads,
                                     int64_t query_heads, int64_t plane, void* workspace, hipStream_t s);
 
+// ---- decoder-layer relayouts (hk_layout.hip); BF16, D % 16 == 0, 16-byte aligned bases.
+// merge = false: rows [B,S,(Hq+2Hkv)D] -> q [B,Hq,S,D], k/v [B,Hkv,S,D], RoPE on q/k;
+// merge = true: the transpose (dq, dk, dv -> rows) with the backward rotation.
+hipError_t qkv_rope(bool merge, int layout, void* rows, void* q, void* k, void* v, const float* cos_t,
+                    const float* sin_t, int64_t batch, int64_t seq, int64_t hq, int64_t hkv, int64_t d, hipStream_t s);
+// to_rows: x [B,H,S,D] -> y [B,S,H*D]; otherwise the reverse (D % 8 == 0).
+hipError_t heads_rows(bool to_rows, const void* x, void* y, int64_t batch, int64_t heads, int64_t seq, int64_t d,
+                      hipStream_t s);
+
 // ---- attention (hk_attention.hip)
 struct AttnShape {
     int64_t batch, heads, kv_heads, m, n, d;

@@ -92,16 +92,7 @@ rope_pairs(const T* __restrict__ x, const float* __restrict__ cos_t, const float
     }
     float ya[V], yb[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-        // out = x*cos + sign*(paired*sin), sign = -1 on side a, +1 on side b (negated backward)
-        if constexpr (!BWD) {
-            ya[i] = a[i] * c[i] - b[i] * s[i];
-            yb[i] = b[i] * c[i] + a[i] * s[i];
-        } else {
-            ya[i] = a[i] * c[i] + b[i] * s[i];
-            yb[i] = b[i] * c[i] - a[i] * s[i];
-        }
-    }
+    for (int i = 0; i < V; ++i) rope_rotate<BWD>(a[i], b[i], c[i], s[i], ya[i], yb[i]);
     if constexpr (LAYOUT == 1) {
         store_v<T, V>(yr + p0, ya);
         store_v<T, V>(yr + half + p0, yb);

@@ -3,5 +3,6 @@ rust-ascend's AscendRuntime / nn::* hot path, over libhk.so (include/hk.h)."""
 from ._lib import HkError, LIB_PATH, load
 from .runtime import HipRuntime, RotaryLayout, Transpose, gemm_plan
 from . import nn
+from .decoder import DecoderConfig, DecoderLayer
 
-__all__ = ["HkError", "LIB_PATH", "load", "HipRuntime", "RotaryLayout", "Transpose", "gemm_plan", "nn"]
+__all__ = ["HkError", "LIB_PATH", "load", "HipRuntime", "RotaryLayout", "Transpose", "gemm_plan", "nn", "DecoderConfig", "DecoderLayer"]

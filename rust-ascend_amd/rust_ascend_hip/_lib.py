@@ -87,6 +87,10 @@ SIGNATURES = {
     "hk_bias_add_backward": [_CTX, _T, _T],
     "hk_embedding": [_CTX, _T, _T, _T],
     "hk_embedding_backward": [_CTX, _T, _T, _u64, _u64, _i32, _T],
+    "hk_qkv_rope_split": [_CTX, _T, _T, _T, _i32, _T, _T, _T],
+    "hk_qkv_rope_merge": [_CTX, _T, _T, _T, _T, _T, _i32, _T],
+    "hk_heads_to_rows": [_CTX, _T, _T],
+    "hk_rows_to_heads": [_CTX, _T, _T],
     "hk_softmax": [_CTX, _T, _i32, _T],
     "hk_softmax_backward": [_CTX, _T, _T, _i32, _T],
     "hk_causal_mask": [_CTX, _u64, _u64, _T],

@@ -215,10 +215,50 @@ class HipRuntime:
 
     @staticmethod
     def bias_add(x, bias, residual=None):
-        """(X + residual) + bias over the last axis (residual optional). Reference:
-        AscendRuntime::bias_add (mod.rs:177-181)."""
+        """(X + residual) + bias over the last axis (residual optional; bias may be None when a
+        residual is given). Reference: AscendRuntime::bias_add (mod.rs:177-181)."""
         y = _empty(x.shape, x.dtype, x)
-        _call("hk_bias_add", desc(x), desc(bias), desc(residual) if residual is not None else None, desc(y))
+        _call("hk_bias_add", desc(x), desc(bias) if bias is not None else None,
+              desc(residual) if residual is not None else None, desc(y))
+        return y
+
+    # ---------------------------------------------------------------- decoder-layer relayouts
+
+    @staticmethod
+    def qkv_rope_split(qkv, cos, sin, q_heads: int, kv_heads: int, layout=None):
+        """qkv [B,S,(Hq+2Hkv)D] -> (q [B,Hq,S,D], k, v [B,Hkv,S,D]) with RoPE on q and k; tables [S, D/2]."""
+        layout = RotaryLayout.SplitHalf if layout is None else layout
+        b, s, w = qkv.shape
+        d = w // (q_heads + 2 * kv_heads)
+        q = _empty((b, q_heads, s, d), qkv.dtype, qkv)
+        k = _empty((b, kv_heads, s, d), qkv.dtype, qkv)
+        v = _empty((b, kv_heads, s, d), qkv.dtype, qkv)
+        _call("hk_qkv_rope_split", desc(qkv), desc(cos), desc(sin), int(layout), desc(q), desc(k), desc(v))
+        return q, k, v
+
+    @staticmethod
+    def qkv_rope_merge(dq, dk, dv, cos, sin, layout=None):
+        """(dq, dk, dv) -> dqkv [B,S,(Hq+2Hkv)D], the transpose of qkv_rope_split."""
+        layout = RotaryLayout.SplitHalf if layout is None else layout
+        b, hq, s, d = dq.shape
+        out = _empty((b, s, (hq + 2 * dk.shape[1]) * d), dq.dtype, dq)
+        _call("hk_qkv_rope_merge", desc(dq), desc(dk), desc(dv), desc(cos), desc(sin), int(layout), desc(out))
+        return out
+
+    @staticmethod
+    def heads_to_rows(x):
+        """[B,H,S,D] -> [B,S,H*D]."""
+        b, h, s, d = x.shape
+        y = _empty((b, s, h * d), x.dtype, x)
+        _call("hk_heads_to_rows", desc(x), desc(y))
+        return y
+
+    @staticmethod
+    def rows_to_heads(x, heads: int):
+        """[B,S,H*D] -> [B,H,S,D]."""
+        b, s, w = x.shape
+        y = _empty((b, heads, s, w // heads), x.dtype, x)
+        _call("hk_rows_to_heads", desc(x), desc(y))
         return y
 
     @staticmethod
