@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true", help="headline workload only")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    p.add_argument("--only-c5", action="store_true",
+                   help="only run the C5 decoder layer (forward + backward, --warmup and --steps) and print its line")
     p.add_argument("--stream-ceilings", action="store_true",
                    help="only measure plain HBM streams (read, write, copy, 2 reads + 1 write) on 1 GiB "
                         "buffers with PyTorch's own kernels and print them")
@@ -271,6 +273,18 @@ def bench_decoder(steps=5, warmup=2):
     return cfg, event_ms(fw), event_ms(bw)
 
 
+def c5_line(steps=5, warmup=2):
+    cfg, f_ms, b_ms = bench_decoder(steps, warmup)
+    step_ms = f_ms + b_ms
+    fl = cfg.flops_per_step()
+    return {"workload": "C5 Llama decoder layer fwd+bwd: hidden 4096, 32/8 heads, SwiGLU 14336, "
+                        "B2 x S2048, vocab 32000, BF16",
+            "value": round(cfg.tokens / (step_ms * 1e-3), 1), "unit": "tokens/s",
+            "ms": round(step_ms, 4), "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
+            "model_TFLOPs": round(fl["total"] / (step_ms * 1e-3) / 1e12, 1),
+            "frac_of_bf16_peak": round(fl["total"] / (step_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -285,6 +299,9 @@ def main():
         return
     HipRuntime.initialize_exclusive()
     HipRuntime.set_async(True)
+    if args.only_c5:
+        print(json.dumps(c5_line(args.steps, args.warmup)), flush=True)
+        return
 
     wall_ms, fwd_ms, bwd_ms = bench_c2(args.steps, args.warmup)
     step_bytes = C2_FWD_BYTES + C2_BWD_BYTES
@@ -338,15 +355,7 @@ def main():
         except Exception as exc:  # reported, never silently replaced by another path
             sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
         try:
-            cfg, f_ms, b_ms = bench_decoder()
-            step_ms = f_ms + b_ms
-            fl = cfg.flops_per_step()
-            sec.append({"workload": "C5 Llama decoder layer fwd+bwd: hidden 4096, 32/8 heads, SwiGLU 14336, "
-                                    "B2 x S2048, vocab 32000, BF16",
-                        "value": round(cfg.tokens / (step_ms * 1e-3), 1), "unit": "tokens/s",
-                        "ms": round(step_ms, 4), "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
-                        "model_TFLOPs": round(fl["total"] / (step_ms * 1e-3) / 1e12, 1),
-                        "frac_of_bf16_peak": round(fl["total"] / (step_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
+            sec.append(c5_line())
         except Exception as exc:
             sec.append({"workload": "C5 decoder layer", "error": str(exc)[:200]})
         line["secondary"] = sec

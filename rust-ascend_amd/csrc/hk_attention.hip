@@ -42,8 +42,6 @@ constexpr int kBlockN = 64;   // keys per K/V tile
 constexpr int kThreads = 256;
 constexpr int kXcds = 8;     // accelerator complex dies; workgroups are dispatched round-robin over them
 
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
 // 16-byte chunk swizzle of a tile row (XOR applied to the chunk index). gfx950's LDS has 64
 // banks: one clock serves 16 lanes of a 16-byte read or 32 lanes of an 8-byte read, i.e. one

@@ -138,6 +138,10 @@ __device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, 
     }
 }
 
+// LDS vector types for the transposing reads (ds_read_b64_tr_b16).
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
 // Every pointer 16-byte aligned (the vector chunk paths need it).
 __host__ __forceinline__ bool aligned16(std::initializer_list<const void*> ptrs) {
     for (const void* p : ptrs)

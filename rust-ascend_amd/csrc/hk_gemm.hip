@@ -468,6 +468,12 @@ gemm_nt_dma_kernel(GemmArgs p) {
 //   * A stage is consumed in four turns of 32 k (16 MFMAs per wave): group 0 reads the first
 //     half in turn 4s and multiplies it in 4s+1, reads the second half in 4s+2 and multiplies
 //     it in 4s+3; group 1 runs one turn behind. Stage s is read in turns 4s..4s+3 only.
+//   * Either operand may instead be MN-major (A stored [K,M] or B stored [K,N], the layouts of
+//     the backward's dY^T X and dY W): its stage is then 64 k-rows of 256 columns (512-byte rows,
+//     the 64-byte blocks of a row XORed with row%4) and its fragments are read with gfx950's
+//     transposing LDS read (ds_read_b64_tr_b16, two per fragment, eight k-rows per instruction in
+//     two LDS cycles), which yields the same "32 rows x 8 consecutive k per lane" operand as the
+//     K-major 16-byte read. No transpose pass through HBM is needed.
 //   * Tile data travels global -> registers -> LDS: each wave owns eight 1 KB row blocks of a
 //     stage (32 staging registers per lane). In each of its two memory turns of stage s a wave
 //     writes half of its staged stage s+1 into the free slot and reloads those registers with
@@ -482,7 +488,10 @@ __device__ __forceinline__ int swz64(int row, int chunk) {  // element offset in
     return row * kPK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
-template <bool OUT_BF16>
+// Element offset of (k-row r, column col) in the 64 x 256 stage of an MN-major operand.
+__device__ __forceinline__ int mn_off(int r, int col) { return r * kPPTile + ((((col >> 5) ^ (r & 3))) << 5) + (col & 31); }
+
+template <bool OUT_BF16, bool A_MN, bool B_MN>
 __global__ void __launch_bounds__(kPPThreads, 1)
 gemm_nt_pp_kernel(GemmArgs p) {
     constexpr int kStage = 2 * kPPTile * kPK;  // A rows 0..255, then B rows 0..255
@@ -521,34 +530,73 @@ gemm_nt_pp_kernel(GemmArgs p) {
     const int r_in = lane >> 3;
     const int src_chunk = (lane & 7) ^ ((4 * (wave & 1) + (r_in >> 1)) & 7);
     const int voff = (r_in * p.k + src_chunk * 8) * 2;
+    // MN-major block d: k-rows 2(wave + 8d) + mn_r of the stage, lane chunk mn_c of the 512-byte
+    // row. The k-row and column both go into the range-checked offset (K * M * 2 < 2^31), so
+    // columns past M (N) in the last k-row read as zero instead of past the buffer.
+    const int mn_r = lane >> 5, mn_c = lane & 31;
+    const int mn_voff_a = ((2 * wave + mn_r) * p.m + tm * kPPTile + mn_c * 8) * 2;
+    const int mn_voff_b = ((2 * wave + mn_r) * p.n + tn * kPPTile + mn_c * 8) * 2;
     u32x4_t stg[8];
     auto gload = [&](int kt, int d) __attribute__((always_inline)) {
         const int blk = wave + 8 * d;
-        if (d < 4)
-            stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     ra, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2, 0));
-        else
-            stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     rb, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2, 0));
+        if (d < 4) {
+            if constexpr (A_MN)
+                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         ra, mn_voff_a + (kt * kPK + 16 * d) * p.m * 2, 0, 0));
+            else
+                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         ra, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2, 0));
+        } else {
+            if constexpr (B_MN)
+                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rb, mn_voff_b + (kt * kPK + 16 * (d - 4)) * p.n * 2, 0, 0));
+            else
+                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rb, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2, 0));
+        }
     };
-    const int wlane = wave * 8 * kPK + lane * 8;  // element offset of this lane's chunk in block d = 0
+    // Element offset of this lane's chunk for block d = 0 (block d adds d * 4096 in both layouts:
+    // eight 128-byte rows or two 512-byte k-rows per block).
+    const int wlane = wave * 8 * kPK + lane * 8;
+    const int mn_row = 2 * wave + mn_r;
+    const int wlane_mn = mn_row * kPPTile + ((((mn_c >> 2) ^ (mn_row & 3))) << 5) + (mn_c & 3) * 8;
+    const int wl_a = A_MN ? wlane_mn : wlane, wl_b = B_MN ? wlane_mn : wlane;
     auto lwrite = [&](uint16_t* slot, int d) __attribute__((always_inline)) {
-        *reinterpret_cast<u32x4_t*>(slot + wlane + d * 64 * kPK) = stg[d];
+        *reinterpret_cast<u32x4_t*>(slot + (d < 4 ? wl_a : wl_b) + d * 64 * kPK) = stg[d];
     };
 
     // Fragments of one half stage (k slices 2h and 2h+1): A fragment i, B fragment j.
     const int a_row = 128 * group + lr, b_row = kPPTile + 64 * q + lr;
+    // Transposing read of an MN-major fragment: columns col0 .. col0+31 (col0 % 32 == 0), k-rows
+    // k0 .. k0+7 (k0 % 4 == 0). In each 16-lane group, lane i reads 4 columns of k-row k0 + i/4
+    // (and k0 + 4 + i/4); the hardware hands lane i the 4 k values of column i. Since k0 % 4 == 0
+    // the row's XOR term is i/4 for every fragment.
+    const int tr_i = lane & 15;
+    const int tr_lane = (tr_i >> 2) * kPPTile + 16 * ((lane >> 4) & 1) + 4 * (tr_i & 3);
+    auto read_tr = [&](const uint16_t* base, int k0, int blk32) __attribute__((always_inline)) {
+        const uint16_t* at = base + k0 * kPPTile + tr_lane + ((blk32 ^ (tr_i >> 2)) << 5);
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at + 4 * kPPTile));
+        typedef short v8i16_t __attribute__((ext_vector_type(8)));
+        const v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(bf16x8_t, v);
+    };
     bf16x8_t fa[2][4], fb[2][2];
     auto read = [&](const uint16_t* slot, int h) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const int c = 2 * (2 * h + t) + lk;
+            const int c = 2 * (2 * h + t) + lk;       // K-major: 16-byte chunk of k 8c .. 8c+7
+            const int k0 = 16 * (2 * h + t) + 8 * lk;  // MN-major: the same k as the first k-row
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                fa[t][i] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 32 * i, c));
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (A_MN) fa[t][i] = read_tr(slot, k0, 4 * group + i);
+                else fa[t][i] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 32 * i, c));
+            }
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                fb[t][j] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 32 * j, c));
+            for (int j = 0; j < 2; ++j) {
+                if constexpr (B_MN) fb[t][j] = read_tr(slot + kPPTile * kPK, k0, 2 * q + j);
+                else fb[t][j] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 32 * j, c));
+            }
         }
     };
 
@@ -671,6 +719,26 @@ transpose_bf16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int6
     }
 }
 
+// The ping-pong kernel takes each operand K-major or MN-major; true when it applies (enough
+// 256x256 tiles to fill the GPU, whole 64-deep stages, 32-bit byte offsets).
+bool pp_applies(int64_t batch, int64_t m, int64_t n, int64_t k, int num_cus) {
+    const int64_t tiles = ((m + kPPTile - 1) / kPPTile) * ((n + kPPTile - 1) / kPPTile) * batch;
+    return tiles >= num_cus && k > 0 && k % kPK == 0 && m * k * 2 < (int64_t{1} << 31) &&
+           n * k * 2 < (int64_t{1} << 31);
+}
+
+template <bool OUT_BF16>
+void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, hipStream_t s) {
+    GemmArgs p = a;
+    p.tiles_m = (p.m + kPPTile - 1) / kPPTile;
+    p.tiles_n = (p.n + kPPTile - 1) / kPPTile;
+    const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), 1, static_cast<unsigned>(batch));
+    if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, true, true>), grid, dim3(kPPThreads), 0, s, p);
+    else if (a_mn) hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, true, false>), grid, dim3(kPPThreads), 0, s, p);
+    else if (b_mn) hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, false, true>), grid, dim3(kPPThreads), 0, s, p);
+    else hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, false, false>), grid, dim3(kPPThreads), 0, s, p);
+}
+
 template <int BM, int BN>
 void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
     GemmArgs p = a;
@@ -681,8 +749,8 @@ void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
     const bool whole_steps = p.k % kSBK == 0 && p.k > 0 && static_cast<int64_t>(p.m) * p.k * 2 < (int64_t{1} << 31) &&
                              static_cast<int64_t>(p.n) * p.k * 2 < (int64_t{1} << 31);
     if (whole_steps && p.k % kPK == 0 && BM == kPPTile && BN == kPPTile) {
-        if (out_bf16) hipLaunchKernelGGL((gemm_nt_pp_kernel<true>), grid, dim3(kPPThreads), 0, s, p);
-        else hipLaunchKernelGGL((gemm_nt_pp_kernel<false>), grid, dim3(kPPThreads), 0, s, p);
+        if (out_bf16) launch_pp<true>(p, batch, false, false, s);
+        else launch_pp<false>(p, batch, false, false, s);
     } else if (whole_steps && out_bf16)
         hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
     else if (whole_steps)
@@ -708,6 +776,18 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
                      int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s) {
     const uint16_t* ak = static_cast<const uint16_t*>(a);
     const uint16_t* bk = static_cast<const uint16_t*>(b);
+    if (pp_applies(batch, m, n, k, num_cus)) {  // MN-major operands are read in place
+        GemmArgs p{};
+        p.a = ak;
+        p.b = bk;
+        p.c = c;
+        p.m = static_cast<int>(m);
+        p.n = static_cast<int>(n);
+        p.k = static_cast<int>(k);
+        if (out_bf16) launch_pp<true>(p, batch, ta != 0, tb == 0, s);
+        else launch_pp<false>(p, batch, ta != 0, tb == 0, s);
+        return hipGetLastError();
+    }
     char* ws = static_cast<char*>(workspace);
     if (ta) {  // A stored [K,M] -> [M,K]
         uint16_t* t = reinterpret_cast<uint16_t*>(ws);

@@ -82,27 +82,35 @@ def test_gemm_random_vs_oracle(m, n, k, ta, tb):
             f32_close(y, want, f"GEMM {m}x{n}x{k} {ta}{tb} f32")
 
 
-@pytest.mark.parametrize("batch,m,n,k", [(1, 4000, 4112, 512), (1, 4096, 4096, 64), (1, 4096, 4096, 128),
-                                         (1, 4096, 4096, 96), (2, 2048, 4096, 320), (1, 4368, 3856, 1216)])
-def test_gemm_256_tile_paths(batch, m, n, k):
+TILE_SHAPES = [(1, 4000, 4112, 512), (1, 4096, 4096, 64), (1, 4096, 4096, 128), (1, 4096, 4096, 96),
+               (2, 2048, 4096, 320), (1, 4368, 3856, 1216)]
+TRANSPOSES = [(0, 1), (0, 0), (1, 0), (1, 1)]
+
+
+@pytest.mark.parametrize("batch,m,n,k", TILE_SHAPES)
+@pytest.mark.parametrize("ta,tb", TRANSPOSES)
+def test_gemm_256_tile_paths(batch, m, n, k, ta, tb):
     """Shapes that fill the GPU with 256x256 tiles: ragged M/N edges (rows past the matrix read as
     zero, outputs masked), one and two 64-deep K stages, K not a multiple of 64 (the 32-deep
-    kernel), batches. Sampled rows/columns include the last ones."""
-    a_t, a = randn_bf16((batch, m, k), seed=m + k, std=1 / np.sqrt(k))
-    b_t, b = randn_bf16((batch, n, k), seed=n + k, std=1.0)
+    kernel), batches; every transpose pair, so the ping-pong kernel's MN-major operand reads
+    (A stored [K,M], B stored [K,N]) are covered. Sampled rows/columns include the last ones."""
+    if (ta, tb) != (0, 1) and (m, n, k) in ((4096, 4096, 64), (4096, 4096, 96)):
+        pytest.skip("one and 1.5 stage cases run NT only")
+    a_t, a = randn_bf16((batch, k, m) if ta else (batch, m, k), seed=m + k, std=1 / np.sqrt(k))
+    b_t, b = randn_bf16((batch, n, k) if tb else (batch, k, n), seed=n + k, std=1.0)
     a_t, b_t = a_t.squeeze(0), b_t.squeeze(0)
     rows = np.concatenate([np.arange(0, m, 13)[:300], np.arange(m - 40, m)])
     cols = np.concatenate([np.arange(0, n, 11)[:300], np.arange(n - 40, n)])
     r, c = np.meshgrid(rows, cols, indexing="ij")
     for out in (torch.bfloat16, torch.float32):
-        y = host(HipRuntime.gemm(a_t, b_t, Transpose.No, Transpose.Yes, out)).reshape(batch, m, n)
+        y = host(HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), out)).reshape(batch, m, n)
         for g in range(batch):
-            want = oracle.gemm_f64_sampled(a[g], b[g], 0, 1, r.ravel(), c.ravel())
+            want = oracle.gemm_f64_sampled(a[g], b[g], ta, tb, r.ravel(), c.ravel())
             got = y[g][r.ravel(), c.ravel()]
             if out == torch.bfloat16:
-                rel_ok(got, want, 1e-2, f"GEMM {batch}x{m}x{n}x{k} bf16 [{g}]")
+                rel_ok(got, want, 1e-2, f"GEMM {batch}x{m}x{n}x{k} {ta}{tb} bf16 [{g}]")
             else:
-                f32_close(got, want, f"GEMM {batch}x{m}x{n}x{k} f32 [{g}]")
+                f32_close(got, want, f"GEMM {batch}x{m}x{n}x{k} {ta}{tb} f32 [{g}]")
 
 
 def test_gemm_batched_vs_oracle():
