@@ -211,6 +211,13 @@ def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
     return event_ms(pairs)
 
 
+def gemm_kernel_name(m, n, k, ta, tb):
+    """The kernel libhk.so runs for this shape (hk_gemm.hip's selection on 256 CUs)."""
+    if ((m + 255) // 256) * ((n + 255) // 256) >= 256 and k % 64 == 0:
+        return "gemm_nt_m16_kernel" if (ta, tb) == (0, 1) else "gemm_nt_pp_kernel"
+    return "gemm_nt_dma_kernel"
+
+
 def bench_rope(iters=10):
     import numpy as np
     import torch
@@ -353,9 +360,7 @@ def main():
             flops = 2 * m * n * k
             sec.append({"workload": name, "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
                         "ms": round(ms, 5),
-                        "roofline": roofline("mfma", flops, ms,
-                                             "gemm_nt_pp_kernel" if (m // 256) * (n // 256) >= 256 and k % 64 == 0
-                                             else "gemm_nt_dma_kernel")})
+                        "roofline": roofline("mfma", flops, ms, gemm_kernel_name(m, n, k, ta, tb))})
         ms, algo = bench_rope()
         sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
                     "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
