@@ -81,7 +81,7 @@ typedef struct hk_stats {
 } hk_stats;
 
 /* Host-only result of a GEMM contract check; reference: GemmSpec,
- * deepgemm/plan.rs:31-86. kind: 0 dense, 1 batched. */
+ * deepgemm/plan.rs:31-86. kind: 0 dense, 1 batched, 2 M-grouped. */
 typedef struct hk_gemm_plan {
     int32_t kind;
     int32_t out_rank;
@@ -141,6 +141,29 @@ hk_status hk_gemm_into(hk_context* ctx, const hk_tensor* a, const hk_tensor* b,
  * Reference: AscendRuntime::linear_nt_backward, runtime/mod.rs:357-362 (matrix.rs:60-74). */
 hk_status hk_linear_nt_backward(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
                                 const hk_tensor* dy, hk_tensor* dx, hk_tensor* dw);
+
+/* M-grouped (mixture-of-experts) NT GEMM: out[i,:] = A[i,:] W[g]^T for the rows i of group g,
+ * A [M,K] BF16, W [G,N,K] BF16, out [M,N] BF16 or F32. Groups are "aligned physical" row
+ * ranges: ends[g] is the row after group g, nondecreasing multiples of 256, ends[G-1] = M;
+ * a repeated end is an empty expert (no rows).
+ *
+ * Host-only check of the ends. Reference: GroupEnds::new, deepgemm/plan.rs:16-26 (1..=4096
+ * groups, nondecreasing multiples of 256, not all empty). */
+hk_status hk_group_ends_check(const int32_t* ends, int32_t count);
+/* Opaque, immutable device copy of checked group ends, uploaded once and reused by every
+ * grouped call. Reference: DeepGemm::upload_group_ends / DeviceGroupEnds, deepgemm/mod.rs:61-67. */
+typedef struct hk_group_ends hk_group_ends;
+hk_status hk_group_ends_upload(hk_context* ctx, const int32_t* ends, int32_t count, hk_group_ends** out);
+/* Frees the device copy after the context's queued work has completed. */
+hk_status hk_group_ends_free(hk_context* ctx, hk_group_ends* ends);
+/* Host-only contract check (plan->kind 2, key "bf16_mgrouped_nt_<out>"). Reference:
+ * GemmSpec::grouped_nt, deepgemm/plan.rs:61-67, then GemmSpec::checked (:68-80). */
+hk_status hk_gemm_grouped_plan_check(const hk_tensor* a, const hk_tensor* weights, const int32_t* ends,
+                                     int32_t count, int32_t out_dtype, hk_gemm_plan* plan);
+/* Reference: DeepGemm::grouped_nt_into, deepgemm/mod.rs:74-78 (grouped_nt, :68-73, is
+ * hk_alloc + this call). */
+hk_status hk_gemm_grouped_nt_into(hk_context* ctx, const hk_tensor* a, const hk_tensor* weights,
+                                  const hk_group_ends* ends, hk_tensor* out);
 
 /* FP32-storage, BF16-compute GEMM: rounds A and B to BF16 into a_bf16/b_bf16
  * (the saved snapshots), then out(F32) = op(A) @ op(B).

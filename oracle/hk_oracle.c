@@ -95,6 +95,27 @@ void or_gemm_f64(const float* a, const float* b, int64_t batch, int64_t m, int64
     }
 }
 
+/* M-grouped NT: out[i,j] = sum_q A[i,q] * W[g,j,q] in f64, q ascending, where g is the first
+ * group whose end exceeds i (empty groups, whose end repeats the previous one, own no row).
+ * A [m,k], W [groups,n,k]. Reference: rust-ascend-kernels/src/tests.rs:89-103 (group lookup
+ * :95, weight address :99). */
+void or_gemm_grouped_nt_f64(const float* a, const float* w, int64_t m, int64_t n, int64_t k,
+                            const int32_t* ends, int64_t groups, double* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < m; ++i) {
+        int64_t g = 0;
+        while (g < groups && i >= (int64_t)ends[g]) ++g;
+        for (int64_t j = 0; j < n; ++j) {
+            double s = 0.0;
+            if (g < groups) {
+                const float* wr = w + (g * n + j) * k;
+                for (int64_t q = 0; q < k; ++q) s += (double)a[i * k + q] * (double)wr[q];
+            }
+            out[i * n + j] = g < groups ? s : NAN;
+        }
+    }
+}
+
 /* Same, evaluated only at the listed (row, col) pairs of batch 0 (sampled parity
  * for shapes too large to evaluate whole on the CPU). */
 void or_gemm_f64_sampled(const float* a, const float* b, int64_t m, int64_t n, int64_t k,

@@ -14,6 +14,10 @@ a wrong sign or index, or a transposed operand fails at least one check:
 
 * ``bf16_round``: bit patterns of hand-picked values (ties to even, Inf/NaN, -0,
   overflow to Inf) and agreement with torch's float32->bfloat16 conversion.
+* ``gemm_grouped_nt_f64``: per-group numpy float64 matmul of the row slices on the reference's
+  grouped cases (rust-ascend-kernels/src/tests.rs:89-103,130-132: 768x16x144 with ends
+  [0,256,256,768], two empty experts; deepgemm_validate.rs:45-53: 512x64x48 with ends
+  [256,256,512]), plus the identity with one group == the dense NT product.
 * ``gemm_f64``/``gemm_f32``: numpy float64 matmul for all four transposes and
   batches; the reference's integer-formula cases of
   rust-ascend-kernels/src/tests.rs:89-103,124-129 (80x96x144 dense, 3x16x32x16
@@ -78,6 +82,7 @@ _lib = None
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
 _i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
 
@@ -102,6 +107,7 @@ def lib():
         L.or_gemm_f64.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _int, _int, _f64p]
         L.or_gemm_f64_sampled.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _int, _int, _i64p, _i64p, _i64, _f64p]
         L.or_gemm_f32.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i64, _int, _int, _f32p]
+        L.or_gemm_grouped_nt_f64.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _i32p, _i64, _f64p]
         L.or_rms_norm_f64.argtypes = [_f32p, _f32p, _i64, _i64, ctypes.c_double, _f64p, _f64p]
         L.or_rms_norm_backward_f64.argtypes = [_f32p, _f32p, _f32p, _f64p, _i64, _i64, _f64p, _f64p]
         L.or_rms_norm_lanes_f32.argtypes = [_f32p, _f32p, _i64, _i64, ctypes.c_float, _f32p, _f32p]
@@ -219,6 +225,20 @@ def gemm_f32(a, b, ta: bool, tb: bool) -> np.ndarray:
     out = np.empty((g, m, n), dtype=np.float32)
     lib().or_gemm_f32(a.reshape(-1), b.reshape(-1), g, m, n, k, int(ta), int(tb), out.reshape(-1))
     return out if batched else out[0]
+
+
+def gemm_grouped_nt_f64(a, w, ends) -> np.ndarray:
+    """M-grouped NT product in f64: rows [ends[g-1], ends[g]) of A times W[g]^T.
+    A [M,K], W [G,N,K]; rows past the last end are NaN."""
+    a = _c32(a)
+    w = _c32(w)
+    ends = np.ascontiguousarray(ends, dtype=np.int32)
+    m, k = a.shape
+    g, n, kw = w.shape
+    assert kw == k and ends.shape == (g,)
+    out = np.empty((m, n), dtype=np.float64)
+    lib().or_gemm_grouped_nt_f64(a.reshape(-1), w.reshape(-1), m, n, k, ends, g, out.reshape(-1))
+    return out
 
 
 def gemm_f64_sampled(a, b, ta: bool, tb: bool, rows, cols) -> np.ndarray:

@@ -268,9 +268,62 @@ hk_status gemm_spec(const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t 
     return HK_OK;
 }
 
+// Reference: GroupEnds::new, deepgemm/plan.rs:16-26.
+hk_status group_ends_check(const int32_t* ends, int32_t count) {
+    if (count <= 0 || count > 4096 || ends == nullptr) return fail(HK_INVALID_ARGUMENT, "group count must be 1..=4096");
+    int32_t previous = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (ends[i] < previous || ends[i] % 256 != 0)
+            return fail(HK_INVALID_ARGUMENT, "group ends must be nondecreasing multiples of 256");
+        previous = ends[i];
+    }
+    if (previous == 0) return fail(HK_INVALID_ARGUMENT, "all-empty grouped GEMM is not implemented");
+    return HK_OK;
+}
+
+// Reference: GemmSpec::grouped_nt (deepgemm/plan.rs:61-67), then GemmSpec::checked (:68-80) with
+// 256-row M blocks for the tile-range bound.
+hk_status grouped_spec(const hk_tensor* a, const hk_tensor* w, const int32_t* ends, int32_t count, int32_t out_dtype,
+                       GemmSpec* s) {
+    if (!tensor_ok(a, "A") || !tensor_ok(w, "weights")) return HK_INVALID_ARGUMENT;
+    hk_status st = group_ends_check(ends, count);
+    if (st != HK_OK) return st;
+    if (a->rank != 2 || w->rank != 3) return fail(HK_INVALID_ARGUMENT, "grouped NT requires [M,K] and [G,N,K]");
+    if (a->shape[0] != ends[count - 1] || w->shape[0] != count || a->shape[1] != w->shape[2])
+        return fail(HK_INVALID_ARGUMENT, "grouped NT dimensions do not match the physical prefix sums");
+    if (a->dtype != HK_BF16 || w->dtype != HK_BF16 || !(out_dtype == HK_BF16 || out_dtype == HK_F32))
+        return fail(HK_INVALID_ARGUMENT, "GEMM accepts BF16 inputs and BF16/F32 output only (got %s, %s -> %s)",
+                    dtype_name(a->dtype), dtype_name(w->dtype), dtype_name(out_dtype));
+    const int64_t m = a->shape[0], n = w->shape[1], k = a->shape[1];
+    for (int64_t x : {m, n, k})
+        if (x <= 0 || x % 16 != 0 || x > INT32_MAX)
+            return fail(HK_INVALID_ARGUMENT,
+                        "M/N/K must be positive multiples of 16 <= INT32_MAX; batches/groups 1..=4096 (M=%lld N=%lld K=%lld)",
+                        (long long)m, (long long)n, (long long)k);
+    const int64_t tiles = ((m + 255) / 256) * ((n + 63) / 64);
+    if (tiles > static_cast<int64_t>(INT32_MAX) - 32) return fail(HK_INVALID_ARGUMENT, "tile range overflows");
+    s->kind = 2;
+    s->batch = count;
+    s->m = m;
+    s->n = n;
+    s->k = k;
+    s->out_dtype = out_dtype;
+    return HK_OK;
+}
+
+// Uploaded group ends: the checked host copy and, on the device, the group of every 256-row
+// block of A (what the kernels index).
+constexpr uint64_t kGroupEndsMagic = 0x686b5f67726f7570ULL;
+struct GroupEndsDev {
+    uint64_t magic = kGroupEndsMagic;
+    Ctx* ctx = nullptr;
+    std::vector<int32_t> ends;
+    int32_t* block_group = nullptr;
+};
+
 bool out_matches(const GemmSpec& s, const hk_tensor* out) {
     if (out->dtype != s.out_dtype) return false;
-    if (s.kind == 0) return out->rank == 2 && out->shape[0] == s.m && out->shape[1] == s.n;
+    if (s.kind != 1) return out->rank == 2 && out->shape[0] == s.m && out->shape[1] == s.n;
     return out->rank == 3 && out->shape[0] == s.batch && out->shape[1] == s.m && out->shape[2] == s.n;
 }
 
@@ -493,6 +546,94 @@ hk_status hk_gemm_into(hk_context* h, const hk_tensor* a, const hk_tensor* b, in
     hipError_t e;
     run_gemm(g.c, s, a->data, b->data, out->data, ta, tb, g.c->workspace, &e);
     return complete(g.c, e, "gemm", 1);
+}
+
+hk_status hk_group_ends_check(const int32_t* ends, int32_t count) { return group_ends_check(ends, count); }
+
+hk_status hk_group_ends_upload(hk_context* h, const int32_t* ends, int32_t count, hk_group_ends** out) {
+    // Reference: DeepGemm::upload_group_ends, deepgemm/mod.rs:61-67.
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    hk_status st = group_ends_check(ends, count);
+    if (st != HK_OK) return st;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t blocks = ends[count - 1] / 256;
+    std::vector<int32_t> table(static_cast<size_t>(blocks));
+    int32_t grp = 0;
+    for (int64_t b = 0; b < blocks; ++b) {
+        while (ends[grp] <= b * 256) ++grp;  // first group whose end lies beyond the block's first row
+        table[static_cast<size_t>(b)] = grp;
+    }
+    GroupEndsDev* d = new GroupEndsDev();
+    d->ctx = g.c;
+    d->ends.assign(ends, ends + count);
+    hipError_t e = hipMalloc(&d->block_group, table.size() * sizeof(int32_t));
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(d->block_group, table.data(), table.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+                           g.c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.c->stream);
+    if (e != hipSuccess) {
+        if (d->block_group) (void)hipFree(d->block_group);
+        delete d;
+        return fail(HK_HIP_ERROR, "group ends upload: %s", hipGetErrorString(e));
+    }
+    *out = reinterpret_cast<hk_group_ends*>(d);
+    return HK_OK;
+}
+
+hk_status hk_group_ends_free(hk_context* h, hk_group_ends* ends) {
+    if (!ends) return HK_OK;
+    GroupEndsDev* d = reinterpret_cast<GroupEndsDev*>(ends);
+    OpGuard g(h);
+    if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
+    if (d->magic != kGroupEndsMagic || d->ctx != g.c) return fail(HK_INVALID_ARGUMENT, "not a group-ends handle of this context");
+    if (g.c->poisoned) return fail(HK_POISONED, "poisoned context: memory is leaked rather than freed");
+    hipError_t e = hipStreamSynchronize(g.c->stream);  // queued grouped GEMMs may still read the table
+    if (e == hipSuccess) e = hipFree(d->block_group);
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "group ends free: %s", hipGetErrorString(e));
+    d->magic = 0;
+    delete d;
+    return HK_OK;
+}
+
+hk_status hk_gemm_grouped_plan_check(const hk_tensor* a, const hk_tensor* w, const int32_t* ends, int32_t count,
+                                     int32_t out_dtype, hk_gemm_plan* plan) {
+    GemmSpec s;
+    hk_status st = grouped_spec(a, w, ends, count, out_dtype, &s);
+    if (st != HK_OK) return st;
+    if (plan) {
+        std::memset(plan, 0, sizeof *plan);
+        plan->kind = 2;
+        plan->batch = s.batch;
+        plan->m = s.m;
+        plan->n = s.n;
+        plan->k = s.k;
+        plan->out_rank = 2;
+        plan->out_shape[0] = s.m;
+        plan->out_shape[1] = s.n;
+        std::snprintf(plan->key, sizeof plan->key, "bf16_mgrouped_nt_%s", out_dtype == HK_BF16 ? "bf16" : "f32");
+    }
+    return HK_OK;
+}
+
+hk_status hk_gemm_grouped_nt_into(hk_context* h, const hk_tensor* a, const hk_tensor* w, const hk_group_ends* ends,
+                                  hk_tensor* out) {
+    // Reference: DeepGemm::grouped_nt_into, deepgemm/mod.rs:74-78 and run (:87-97).
+    if (!tensor_ok(out, "out")) return HK_INVALID_ARGUMENT;
+    const GroupEndsDev* d = reinterpret_cast<const GroupEndsDev*>(ends);
+    if (!d || d->magic != kGroupEndsMagic) return fail(HK_INVALID_ARGUMENT, "grouped GEMM requires uploaded group ends");
+    GemmSpec s;
+    hk_status st = grouped_spec(a, w, d->ends.data(), static_cast<int32_t>(d->ends.size()), out->dtype, &s);
+    if (st != HK_OK) return st;
+    if (!out_matches(s, out)) return fail(HK_INVALID_ARGUMENT, "grouped GEMM output layout mismatch: %s", shape_str(out).c_str());
+    if (!disjoint({out}, {a, w})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (d->ctx != g.c) return fail(HK_INVALID_ARGUMENT, "group ends belong to another context");
+    hipError_t e = hk::gemm_bf16_grouped_nt(a->data, w->data, out->data, s.out_dtype == HK_BF16, s.m, s.n, s.k,
+                                            d->block_group, g.c->num_cus, g.c->stream);
+    return complete(g.c, e, "grouped_nt", 1);
 }
 
 hk_status hk_linear_nt_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,

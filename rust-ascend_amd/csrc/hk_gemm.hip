@@ -39,11 +39,20 @@ constexpr int kThreads = 256;
 
 struct GemmArgs {
     const uint16_t* a;  // [batch][m][k]
-    const uint16_t* b;  // [batch][n][k]
+    const uint16_t* b;  // [batch][n][k], or [groups][n][k] for the M-grouped form
     void* c;            // [batch][m][n]
     int m, n, k;
     int tiles_m, tiles_n;
+    // M-grouped form (batch 1): block_group[r / 256] is the weight slice of rows r of A and C.
+    // Group ends are multiples of 256, so an output tile (256, 128 or 64 rows) has one group.
+    const int32_t* block_group;
 };
+
+// B operand of the tile whose first output row is row0 in batch g.
+__device__ __forceinline__ const uint16_t* weight_slice(const GemmArgs& p, int row0, int64_t g) {
+    const int64_t slice = p.block_group ? static_cast<int64_t>(p.block_group[row0 >> 8]) : g;
+    return p.b + slice * static_cast<int64_t>(p.n) * p.k;
+}
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
 
@@ -69,7 +78,7 @@ gemm_nt_kernel(GemmArgs p) {
     const int64_t g = blockIdx.z;
 
     const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
-    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+    const uint16_t* B = weight_slice(p, tm * BM, g);
 
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -375,7 +384,7 @@ gemm_nt_dma_kernel(GemmArgs p) {
     const int tn = (bid % per_group) / gsize;
     const int64_t g = blockIdx.z;
     const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
-    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+    const uint16_t* B = weight_slice(p, tm * BM, g);
 
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -512,7 +521,7 @@ gemm_nt_pp_kernel(GemmArgs p) {
     const int tn = (bid % per_group) / gsize;
     const int64_t g = blockIdx.z;
     const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
-    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+    const uint16_t* B = weight_slice(p, tm * kPPTile, g);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -740,7 +749,7 @@ gemm_nt_m16_kernel(GemmArgs p) {
     const int tn = (bid % per_group) / gsize;
     const int64_t g = blockIdx.z;
     const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
-    const uint16_t* B = p.b + g * static_cast<int64_t>(p.n) * p.k;
+    const uint16_t* B = weight_slice(p, tm * kPPTile, g);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -903,6 +912,16 @@ void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
         hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, false>), grid, dim3(kThreads), 0, s, p);
 }
 
+// Output tile of 256, 128 or 64: the largest whose grid still fills the CUs.
+void launch_nt_sized(const GemmArgs& p, int64_t batch, bool out_bf16, int num_cus, hipStream_t s) {
+    const int64_t m = p.m, n = p.n;
+    const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
+    const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128) * batch;
+    if (t256 >= num_cus) launch_nt<256, 256>(p, batch, out_bf16, s);
+    else if (t128 >= num_cus) launch_nt<128, 128>(p, batch, out_bf16, s);
+    else launch_nt<64, 64>(p, batch, out_bf16, s);
+}
+
 size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
 
 }  // namespace
@@ -951,11 +970,26 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
     p.m = static_cast<int>(m);
     p.n = static_cast<int>(n);
     p.k = static_cast<int>(k);
-    const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
-    const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128) * batch;
-    if (t256 >= num_cus) launch_nt<256, 256>(p, batch, out_bf16, s);
-    else if (t128 >= num_cus) launch_nt<128, 128>(p, batch, out_bf16, s);
-    else launch_nt<64, 64>(p, batch, out_bf16, s);
+    launch_nt_sized(p, batch, out_bf16, num_cus, s);
+    return hipGetLastError();
+}
+
+hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_bf16, int64_t m, int64_t n, int64_t k,
+                                const int32_t* block_group, int num_cus, hipStream_t s) {
+    GemmArgs p{};
+    p.a = static_cast<const uint16_t*>(a);
+    p.b = static_cast<const uint16_t*>(w);
+    p.c = c;
+    p.m = static_cast<int>(m);
+    p.n = static_cast<int>(n);
+    p.k = static_cast<int>(k);
+    p.block_group = block_group;
+    if (pp_applies(1, m, n, k, num_cus)) {
+        if (out_bf16) launch_pp<true>(p, 1, false, false, s);
+        else launch_pp<false>(p, 1, false, false, s);
+    } else {
+        launch_nt_sized(p, 1, out_bf16, num_cus, s);
+    }
     return hipGetLastError();
 }
 

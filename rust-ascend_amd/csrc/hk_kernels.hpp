@@ -38,6 +38,10 @@ hipError_t cast_apply(int to_bf16, const void* in, void* out, int64_t n, hipStre
 size_t gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k, int ta, int tb);
 hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_t batch, int64_t m,
                      int64_t n, int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s);
+// M-grouped NT GEMM: C[i, :] = A[i, :] W[g(i)]^T with A [m, k], W [groups, n, k], C [m, n];
+// g(i) = block_group[i / 256] (group ends are multiples of 256). No workspace.
+hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_bf16, int64_t m, int64_t n,
+                                int64_t k, const int32_t* block_group, int num_cus, hipStream_t s);
 
 // ---- element-wise (hk_elementwise.hip)
 // SwiGLU gate, element-wise over n values of F32 or BF16 storage.

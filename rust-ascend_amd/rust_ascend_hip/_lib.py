@@ -75,6 +75,11 @@ SIGNATURES = {
     "hk_download": [_CTX, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t],
     "hk_gemm_plan_check": [_T, _T, _i32, _i32, _i32, ctypes.POINTER(HkGemmPlan)],
     "hk_gemm_into": [_CTX, _T, _T, _i32, _i32, _T],
+    "hk_group_ends_check": [ctypes.POINTER(_i32), _i32],
+    "hk_group_ends_upload": [_CTX, ctypes.POINTER(_i32), _i32, ctypes.POINTER(ctypes.c_void_p)],
+    "hk_group_ends_free": [_CTX, ctypes.c_void_p],
+    "hk_gemm_grouped_plan_check": [_T, _T, ctypes.POINTER(_i32), _i32, _i32, ctypes.POINTER(HkGemmPlan)],
+    "hk_gemm_grouped_nt_into": [_CTX, _T, _T, ctypes.c_void_p, _T],
     "hk_linear_nt_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_gemm_bf16_fp32": [_CTX, _T, _T, _i32, _i32, _T, _T, _T],
     "hk_gemm_bf16_fp32_backward": [_CTX, _T, _T, _T, _i32, _i32, _T, _T],

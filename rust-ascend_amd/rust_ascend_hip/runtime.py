@@ -93,6 +93,55 @@ def gemm_plan(a_shape, b_shape, ta, tb, out_dtype=torch.bfloat16, a_dtype=torch.
             "k": plan.k, "out_shape": tuple(plan.out_shape[:plan.out_rank]), "key": plan.key.decode()}
 
 
+def _ends_array(ends):
+    ends = [int(e) for e in ends]
+    return (ctypes.c_int32 * max(len(ends), 1))(*ends), len(ends)
+
+
+def grouped_gemm_plan(a_shape, w_shape, ends, out_dtype=torch.bfloat16, a_dtype=torch.bfloat16,
+                      w_dtype=torch.bfloat16):
+    """Host-only M-grouped NT contract check (GemmSpec::grouped_nt, plan.rs:61-67); needs no GPU."""
+    lib = _lib.load()
+    ta_ = tensor_desc(256, _DTYPES[a_dtype], a_shape)
+    tw_ = tensor_desc(256, _DTYPES[w_dtype], w_shape)
+    arr, count = _ends_array(ends)
+    plan = _lib.HkGemmPlan()
+    check(lib.hk_gemm_grouped_plan_check(ctypes.byref(ta_), ctypes.byref(tw_), arr, count, _DTYPES[out_dtype],
+                                         ctypes.byref(plan)))
+    return {"kind": "mgrouped", "groups": plan.batch, "m": plan.m, "n": plan.n, "k": plan.k,
+            "out_shape": tuple(plan.out_shape[:plan.out_rank]), "key": plan.key.decode()}
+
+
+def check_group_ends(ends) -> None:
+    """Reference: GroupEnds::new (deepgemm/plan.rs:16-26): 1..=4096 nondecreasing multiples of
+    256, not all zero. Raises HkError."""
+    arr, count = _ends_array(ends)
+    check(_lib.load().hk_group_ends_check(arr, count))
+
+
+class DeviceGroupEnds:
+    """Checked group ends uploaded once (DeepGemm::upload_group_ends / DeviceGroupEnds,
+    deepgemm/mod.rs:61-67); immutable, reused by every grouped call, freed on close()."""
+
+    def __init__(self, ends):
+        arr, count = _ends_array(ends)
+        h = ctypes.c_void_p()
+        _call("hk_group_ends_upload", arr, count, ctypes.byref(h))
+        self.ends = tuple(int(e) for e in ends)
+        self._handle = h
+
+    @property
+    def handle(self):
+        if self._handle is None:
+            raise HkError(_lib.INVALID_ARGUMENT, "group ends already freed")
+        return self._handle
+
+    def close(self) -> None:
+        if self._handle is not None:
+            _call("hk_group_ends_free", self._handle)
+            self._handle = None
+
+
 class HipRuntime:
     """Static entry points mirroring AscendRuntime (runtime/mod.rs:147-435)."""
 
@@ -137,6 +186,24 @@ class HipRuntime:
     def gemm_into(a, b, ta, tb, out) -> None:
         """Reference: AscendRuntime::gemm_into (mod.rs:350-354)."""
         _call("hk_gemm_into", desc(a), desc(b), int(ta), int(tb), desc(out))
+
+    @staticmethod
+    def upload_group_ends(ends) -> DeviceGroupEnds:
+        """Reference: DeepGemm::upload_group_ends (deepgemm/mod.rs:61-67)."""
+        return DeviceGroupEnds(ends)
+
+    @staticmethod
+    def grouped_nt(a, weights, groups: DeviceGroupEnds, dtype=torch.bfloat16):
+        """out[M,N] = A[M,K] W[g]^T per aligned row group. Reference: DeepGemm::grouped_nt (mod.rs:68-73)."""
+        plan = grouped_gemm_plan(a.shape, weights.shape, groups.ends, dtype, a.dtype, weights.dtype)
+        out = _empty(plan["out_shape"], dtype, a)
+        HipRuntime.grouped_nt_into(a, weights, groups, out)
+        return out
+
+    @staticmethod
+    def grouped_nt_into(a, weights, groups: DeviceGroupEnds, out) -> None:
+        """Reference: DeepGemm::grouped_nt_into (mod.rs:74-78)."""
+        _call("hk_gemm_grouped_nt_into", desc(a), desc(weights), groups.handle, desc(out))
 
     @staticmethod
     def linear_nt_backward(x, w, dy):

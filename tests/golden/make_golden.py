@@ -72,6 +72,30 @@ def main():
                 g[key + "_a"] = A
                 g[key + "_b"] = B
                 g[key + "_out"] = gemm_np(A, B, ta, tb)
+    # M-grouped NT, rust-ascend-kernels/src/tests.rs:89-103,130-132: m,n,k = 768,16,144, ends
+    # [0,256,256,768] (experts 0 and 2 empty), the formulas above over m*k and groups*n*k values.
+    # Expected: numpy float64 per row slice with the slice's own weight matrix.
+    def grouped_np(a, w, ends):
+        out = np.full((a.shape[0], w.shape[1]), np.nan)
+        begin = 0
+        for e, end in enumerate(ends):
+            out[begin:end] = a[begin:end].astype(np.float64) @ w[e].astype(np.float64).T
+            begin = end
+        return out
+    m, n, k, ends = 768, 16, 144, [0, 256, 256, 768]
+    a = bf16(((np.arange(m * k) % 23).astype(np.float32) - 11) / 16).reshape(m, k)
+    w = bf16(((np.arange(len(ends) * n * k) % 17).astype(np.float32) - 8) / 8).reshape(len(ends), n, k)
+    g["grouped_vm_a"], g["grouped_vm_w"], g["grouped_vm_ends"] = a, w, np.array(ends, dtype=np.int32)
+    g["grouped_vm_out"] = grouped_np(a, w, ends)
+    # rust-ascend-driver/examples/deepgemm_validate.rs:45-53: m,n,k = 512,64,48, ends [256,256,512],
+    # A = host(m*k, 2), W = host(3*n*k, 5) (host as above); rows 256.. use W[2].
+    m, n, k, ends = 512, 64, 48, [256, 256, 512]
+    a = host(m * k, 2).reshape(m, k)
+    w = host(3 * n * k, 5).reshape(3, n, k)
+    g["grouped_dv_a"], g["grouped_dv_w"], g["grouped_dv_ends"] = a, w, np.array(ends, dtype=np.int32)
+    g["grouped_dv_out"] = np.concatenate([a[:256].astype(np.float64) @ w[0].astype(np.float64).T,
+                                          a[256:].astype(np.float64) @ w[2].astype(np.float64).T])
+
     # examples/matrix_runtime.rs:70-77: linear_nt_backward, m,n,k = 32,48,16,
     # x = ((i%17)-8)*0.125, w = ((i%13)-6)*0.25, dy = ((i%11)-5)*0.0625.
     m, n, k = 32, 48, 16

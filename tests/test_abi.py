@@ -81,6 +81,38 @@ def test_gemm_contract_rejections():
     assert rh.gemm_plan((32, 64), (32, 48), 1, 0)["out_shape"] == (64, 48)
 
 
+def test_group_ends_contract():
+    # GroupEnds::new, deepgemm/plan.rs:16-26 and its tests :105-106
+    rh.check_group_ends([0, 256, 256, 768])
+    rh.check_group_ends([256])
+    for ends in ([1, 17], [256, 0], [0, 0], [], [-256, 256], [256] * 4097):
+        with pytest.raises(HkError):
+            rh.check_group_ends(ends)
+    # GemmSpec::grouped_nt, plan.rs:61-67,105: A [768,64], W [4,128,64] -> [768,128]
+    p = rh.grouped_gemm_plan((768, 64), (4, 128, 64), [0, 256, 256, 768])
+    assert p["kind"] == "mgrouped" and p["groups"] == 4 and p["out_shape"] == (768, 128)
+    assert (p["m"], p["n"], p["k"]) == (768, 128, 64) and p["key"] == "bf16_mgrouped_nt_bf16"
+    import torch
+    assert rh.grouped_gemm_plan((512, 48), (3, 64, 48), [256, 256, 512], torch.float32)["key"] == "bf16_mgrouped_nt_f32"
+    for a, w, ends in [((768, 64), (3, 128, 64), [0, 256, 256, 768]),   # group count != W's
+                       ((512, 64), (4, 128, 64), [0, 256, 256, 768]),   # rows != last end
+                       ((768, 64), (4, 128, 48), [0, 256, 256, 768]),   # K mismatch
+                       ((768, 64), (128, 64), [768]),                   # W rank
+                       ((768, 64), (1, 120, 64), [768])]:               # N % 16
+        with pytest.raises(HkError):
+            rh.grouped_gemm_plan(a, w, ends)
+    with pytest.raises(HkError):
+        rh.grouped_gemm_plan((256, 64), (1, 128, 64), [256], a_dtype=torch.float32)
+    lib = _lib.load()
+    a, w = fake(BF16, (512, 48), 1 << 20), fake(BF16, (3, 64, 48), 1 << 24)
+    out = fake(BF16, (512, 64), 1 << 28)
+    assert lib.hk_gemm_grouped_nt_into(None, a, w, None, out) == _lib.INVALID_ARGUMENT  # no uploaded ends
+    arr = (ctypes.c_int32 * 3)(256, 256, 512)
+    assert lib.hk_group_ends_upload(None, arr, 3, ctypes.byref(ctypes.c_void_p())) == _lib.NOT_INITIALIZED
+    bad = (ctypes.c_int32 * 2)(256, 128)
+    assert lib.hk_group_ends_upload(None, bad, 2, ctypes.byref(ctypes.c_void_p())) == _lib.INVALID_ARGUMENT
+
+
 def test_overlap_and_shape_checks_run_before_the_context():
     lib = _lib.load()
     a = fake(BF16, (32, 48), ptr=1 << 20)

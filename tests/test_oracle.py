@@ -67,6 +67,28 @@ def test_gemm_kernel_vm_cases(oracle, golden, shape, ta, tb):
     close(oracle.gemm_f32(a, b, ta, tb), want, 1e-4, 0)
 
 
+@pytest.mark.parametrize("case", ["vm", "dv"])
+def test_gemm_grouped_reference_cases(oracle, golden, case):
+    # rust-ascend-kernels/src/tests.rs:130-132 (two empty experts) and deepgemm_validate.rs:45-53
+    a, w, ends = golden[f"grouped_{case}_a"], golden[f"grouped_{case}_w"], golden[f"grouped_{case}_ends"]
+    close(oracle.gemm_grouped_nt_f64(a, w, ends), golden[f"grouped_{case}_out"], 1e-12, 0)
+
+
+def test_gemm_grouped_identities(oracle):
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((512, 32)).astype(np.float32)
+    w = rng.standard_normal((3, 48, 32)).astype(np.float32)
+    # one group is the dense NT product
+    close(oracle.gemm_grouped_nt_f64(a, w[:1], [512]), oracle.gemm_f64(a, w[0], 0, 1), 1e-12, 1e-12)
+    # a leading and a middle empty expert take no rows; each row slice uses its own weights
+    y = oracle.gemm_grouped_nt_f64(a, w, [0, 256, 512])
+    close(y[:256], a[:256].astype(np.float64) @ w[1].T.astype(np.float64), 1e-10, 1e-12)
+    close(y[256:], a[256:].astype(np.float64) @ w[2].T.astype(np.float64), 1e-10, 1e-12)
+    y = oracle.gemm_grouped_nt_f64(a, w, [256, 256, 512])
+    close(y[256:], a[256:].astype(np.float64) @ w[2].T.astype(np.float64), 1e-10, 1e-12)
+    assert not np.allclose(y[256:], a[256:].astype(np.float64) @ w[1].T.astype(np.float64))
+
+
 def test_gemm_random_vs_numpy_and_transpose_identity(oracle):
     a = oracle.normal((3, 40, 24), 1, 1)
     b = oracle.normal((3, 24, 56), 1, 2)
