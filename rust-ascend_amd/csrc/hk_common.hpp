@@ -82,6 +82,26 @@ __device__ __forceinline__ void store8(float* p, const float (&v)[8]) {
     *reinterpret_cast<f32x4_t*>(p + 4) = b;
 }
 
+// Streaming (non-temporal) 16-byte accesses for rows that are read or written once: the nt bit
+// marks the lines as streaming in L2 and in the on-package cache. Measured on MI355X over 1 GiB
+// buffers: copy 6.4 TB/s with nt loads and stores vs 5.5-5.7 TB/s without; two reads + one
+// write 6.4 vs 5.5-5.7 TB/s; read-only 7.1 vs 6.3 TB/s.
+template <class V>
+__device__ __forceinline__ V stream_load(const V* p) { return __builtin_nontemporal_load(p); }
+template <class V>
+__device__ __forceinline__ void stream_store(const V& v, V* p) { __builtin_nontemporal_store(v, p); }
+
+__device__ __forceinline__ void store8_stream(uint16_t* p, const float (&v)[8]) {
+    u32x4_t w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    stream_store(w, reinterpret_cast<u32x4_t*>(p));
+}
+__device__ __forceinline__ void store8_stream(float* p, const float (&v)[8]) {
+    stream_store(f32x4_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4_t*>(p));
+    stream_store(f32x4_t{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4_t*>(p + 4));
+}
+
 // IEEE half storage (F16), converted with the hardware round-to-nearest-even converter.
 template <> struct Elem<_Float16> {
     static __device__ __forceinline__ float load(const _Float16* p, int64_t i) { return static_cast<float>(p[i]); }

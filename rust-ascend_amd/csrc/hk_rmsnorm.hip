@@ -39,7 +39,7 @@ constexpr int kBwdThreads = 512;   // 8 waves per workgroup (backward)
 template <typename T> struct Raw8;
 template <> struct Raw8<uint16_t> {
     u32x4_t w;
-    __device__ __forceinline__ void load(const uint16_t* p) { w = *reinterpret_cast<const u32x4_t*>(p); }
+    __device__ __forceinline__ void load(const uint16_t* p) { w = stream_load(reinterpret_cast<const u32x4_t*>(p)); }
     // Opaque to the optimizer: the widening below is recomputed after this point instead
     // of being kept live (as 8 extra VGPRs per chunk) across the row reduction.
     __device__ __forceinline__ void pin() { asm volatile("" : "+v"(w)); }
@@ -54,8 +54,8 @@ template <> struct Raw8<uint16_t> {
 template <> struct Raw8<float> {
     f32x4_t a, b;
     __device__ __forceinline__ void load(const float* p) {
-        a = *reinterpret_cast<const f32x4_t*>(p);
-        b = *reinterpret_cast<const f32x4_t*>(p + 4);
+        a = stream_load(reinterpret_cast<const f32x4_t*>(p));
+        b = stream_load(reinterpret_cast<const f32x4_t*>(p + 4));
     }
     __device__ __forceinline__ void pin() {}
     __device__ __forceinline__ void get(float (&v)[8]) const {
@@ -72,7 +72,7 @@ template <> struct Raw8<float> {
 // occupancy and every wave has its whole row of loads in flight at once. The workgroup
 // stages w in LDS with loads issued together with the rows', so a row costs one memory
 // round trip, not two (x, then w after the reduction).
-template <typename T, int MAXJ>
+template <typename T, int MAXJ, bool FULL>
 __global__ void __launch_bounds__(kRowsThreads)
 rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y,
              float* __restrict__ rstd, int64_t rows, int width, float eps) {
@@ -87,7 +87,7 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int c = lane + 64 * j;
-            if (c < chunks) xs[j].load(xr + 8 * c);
+            if (FULL || c < chunks) xs[j].load(xr + 8 * c);
         }
     }
     for (int c = threadIdx.x; c < chunks; c += kRowsThreads) {
@@ -101,7 +101,7 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
         const int c = lane + 64 * j;
-        if (c < chunks) {
+        if (FULL || c < chunks) {
             float v[8];
             xs[j].get(v);
 #pragma unroll
@@ -114,20 +114,20 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j) {
         const int c = lane + 64 * j;
-        if (c < chunks) {
+        if (FULL || c < chunks) {
             float v[8], wv[8], o[8];
             xs[j].pin();
             xs[j].get(v);
             load8(w_lds + 8 * c, wv);
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = (v[e] * r) * wv[e];
-            store8(yr + 8 * c, o);
+            store8_stream(yr + 8 * c, o);
         }
     }
     if (lane == 0) rstd[row] = r;
 }
 
-template <typename T, int MAXJ>
+template <typename T, int MAXJ, bool FULL>
 __global__ void __launch_bounds__(kBwdThreads)
 rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
              const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ partial,
@@ -136,7 +136,8 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
     float* w_lds = lds;
     float* p_lds = lds + width;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform, so row addresses and the rstd load are scalar
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int waves_per_block = blockDim.x >> 6;
     const int chunks = width >> 3;
     for (int c = threadIdx.x; c < width; c += blockDim.x) w_lds[c] = w[c];
@@ -147,25 +148,26 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
     const float inv_w = 1.0f / static_cast<float>(width);
-    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows;
-         row += static_cast<int64_t>(gridDim.x) * waves_per_block) {
+    // rstd is loaded ahead of the row's loads, so waiting for the row covers it.
+    auto load_row = [&](Raw8<T> (&xs)[MAXJ], Raw8<T> (&gs)[MAXJ], float& r, int64_t row) __attribute__((always_inline)) {
+        r = rstd[row];
         const T* xr = x + row * width;
         const T* gr = dy + row * width;
-        Raw8<T> xs[MAXJ], gs[MAXJ];
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int c = lane + 64 * j;
-            if (c < chunks) {
+            if (FULL || c < chunks) {
                 xs[j].load(xr + 8 * c);
                 gs[j].load(gr + 8 * c);
             }
         }
-        const float r = rstd[row];
+    };
+    auto process_row = [&](Raw8<T> (&xs)[MAXJ], Raw8<T> (&gs)[MAXJ], float r, int64_t row) __attribute__((always_inline)) {
         float dot = 0.0f;
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int c = lane + 64 * j;
-            if (c < chunks) {
+            if (FULL || c < chunks) {
                 float xv[8], gv[8], wv[8];
                 xs[j].get(xv);
                 gs[j].get(gv);
@@ -183,7 +185,7 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int c = lane + 64 * j;
-            if (c < chunks) {
+            if (FULL || c < chunks) {
                 float xv[8], gv[8], wv[8], o[8];
                 xs[j].pin();
                 gs[j].pin();
@@ -192,9 +194,18 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
                 load8(w_lds + 8 * c, wv);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o[e] = (gv[e] * wv[e] - xv[e] * corr) * r;
-                store8(dr + 8 * c, o);
+                store8_stream(dr + 8 * c, o);
             }
         }
+    };
+    // Rows in a grid-stride walk, one at a time. (Issuing the next row's loads before the current
+    // row's reduction and stores, with two register sets, measured 1-2% slower on C2.)
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * waves_per_block;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows; row += stride) {
+        Raw8<T> xs[MAXJ], gs[MAXJ];
+        float r;
+        load_row(xs, gs, r, row);
+        process_row(xs, gs, r, row);
     }
     // Combine the waves' dw partial sums in wave order, then write the workgroup's.
     for (int src = 0; src < waves_per_block; ++src) {
@@ -202,7 +213,7 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
 #pragma unroll
             for (int j = 0; j < MAXJ; ++j) {
                 const int c = lane + 64 * j;
-                if (c < chunks) {
+                if (FULL || c < chunks) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         float* p = &p_lds[8 * c + e];
@@ -327,7 +338,8 @@ template <typename T, int MAXJ>
 void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_t rows, int width,
                      float eps, hipStream_t s) {
     const int64_t grid = (rows + kRowsThreads / 64 - 1) / (kRowsThreads / 64);  // one row per wave
-    hipLaunchKernelGGL((rms_fwd_fast<T, MAXJ>), dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads),
+    auto kernel = width == 512 * MAXJ ? rms_fwd_fast<T, MAXJ, true> : rms_fwd_fast<T, MAXJ, false>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads),
                        static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x), w,
                        static_cast<T*>(y), rstd, rows, width, eps);
 }
@@ -335,7 +347,8 @@ void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_
 template <typename T, int MAXJ>
 void launch_bwd_fast(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
                      float* partial, int parts, int64_t rows, int width, hipStream_t s) {
-    hipLaunchKernelGGL((rms_bwd_fast<T, MAXJ>), dim3(parts), dim3(kBwdThreads),
+    auto kernel = width == 512 * MAXJ ? rms_bwd_fast<T, MAXJ, true> : rms_bwd_fast<T, MAXJ, false>;
+    hipLaunchKernelGGL(kernel, dim3(parts), dim3(kBwdThreads),
                        2 * static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x), w,
                        static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
 }
