@@ -17,6 +17,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -47,7 +48,7 @@ def parse():
                    help="only run the C5 decoder layer (forward + backward, --warmup and --steps) and print its line")
     p.add_argument("--stream-ceilings", action="store_true",
                    help="only measure plain HBM streams (read, write, copy, 2 reads + 1 write) on 1 GiB "
-                        "buffers with PyTorch's own kernels and print them")
+                        "buffers (PyTorch's kernels and rust-ascend_amd/lib/hk_stream_probe) and print them")
     return p.parse_args()
 
 
@@ -316,7 +317,12 @@ def main():
     from rust_ascend_hip import HipRuntime
     torch.cuda.set_device(0)
     if args.stream_ceilings:
-        print(json.dumps({"hbm_stream_GBps_1GiB_buffers": stream_ceilings()}))
+        # rust-ascend_amd/lib/hk_stream_probe (built with libhk.so): the same mixes with 16-byte
+        # plain and non-temporal accesses, run as its own process
+        probe = os.path.join(ROOT, "rust-ascend_amd", "lib", "hk_stream_probe")
+        res = subprocess.run([probe], capture_output=True, text=True, check=True)
+        print(json.dumps({"hbm_stream_GBps_1GiB_buffers": {"torch": stream_ceilings(),
+                                                           "hk_stream_probe": json.loads(res.stdout)}}))
         return
     HipRuntime.initialize_exclusive()
     HipRuntime.set_async(True)

@@ -25,6 +25,7 @@
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
 
+#include <algorithm>
 #include <initializer_list>
 
 namespace hk {
@@ -32,7 +33,11 @@ namespace hk {
 namespace {
 
 constexpr int kRowsThreads = 256;  // 4 waves per workgroup (forward)
-constexpr int kBwdThreads = 512;   // 8 waves per workgroup (backward)
+// Backward: one 4-wave workgroup per CU, so one wave per SIMD walks its rows. Fewer rows in
+// flight stream faster here: on C2 (16384 x 4096 BF16) 4 waves per CU measured 5.1-5.2 TB/s,
+// 3 or 5 waves 4.7-4.9, 8 waves 4.6, 12 waves 4.2; a second workgroup per CU, a smaller grid or
+// prefetching the next row (the VGPRs for it are free at this occupancy) did not help.
+constexpr int kBwdThreads = 256;
 
 // Eight elements kept in their storage form between the two passes over a row
 // (4 VGPRs for BF16, 8 for F32) and widened to float on use.
@@ -353,8 +358,7 @@ void launch_bwd_fast(const void* x, const float* w, const void* dy, const float*
                        static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
 }
 
-// One 8-wave workgroup per CU is resident (2 waves per SIMD at the fast kernel's register use):
-// a grid of exactly one round of workgroups, each wave walking rows/2048 rows.
+// One workgroup per CU is resident: a grid of exactly one round of workgroups.
 int parts_fast(int64_t rows) { return grid_for_rows(rows, kBwdThreads / 64, 256); }
 int parts_general(int64_t rows) {
     int64_t parts = (rows + 63) / 64;  // at most 64 rows per column chunk
@@ -413,7 +417,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
 }  // namespace
 
 size_t rms_backward_workspace_bytes(int64_t rows, int64_t width) {
-    const int parts = parts_fast(rows) > parts_general(rows) ? parts_fast(rows) : parts_general(rows);
+    const int parts = std::max(parts_fast(rows), parts_general(rows));
     return static_cast<size_t>(parts) * static_cast<size_t>(width) * sizeof(float);
 }
 
