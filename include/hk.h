@@ -186,6 +186,35 @@ hk_status hk_linear_bf16_fp32_backward(hk_context* ctx, const hk_tensor* x_bf16,
                                        const hk_tensor* w_bf16, const hk_tensor* dy,
                                        hk_tensor* dx, hk_tensor* dw);
 
+/* Padded BF16-compute GEMM for any positive M/N/K (no multiple-of-16 rule): the matrix axes of
+ * F32 A and B are rounded to BF16 and zero-padded up to multiples of 16 into a_pad/b_pad (the
+ * saved snapshots, "native" shapes), the native GEMM runs with F32 output, and the result is
+ * cropped to out's logical shape ([M,N] or [batch,M,N]). Rank 2 or equal-batch rank 3, all four
+ * transposes. Reference: AscendRuntime::gemm_padded_bf16_fp32, runtime/mod.rs:186-190
+ * (padded_matrix.rs:39-46, PaddedGemmSpec::new in deepgemm/padded.rs:13-36). */
+hk_status hk_gemm_padded_bf16_fp32(hk_context* ctx, const hk_tensor* a, const hk_tensor* b,
+                                   int32_t ta, int32_t tb, hk_tensor* out,
+                                   hk_tensor* a_pad, hk_tensor* b_pad);
+/* F32 gradients cropped to the original physical input shapes, which da/db carry, from the
+ * saved padded snapshots and the logical F32 dY. Reference:
+ * AscendRuntime::gemm_padded_bf16_fp32_backward, runtime/mod.rs:191-195 (padded_matrix.rs:47-63,
+ * PaddedGemmSpec::backward_specs, deepgemm/padded.rs:39-50). */
+hk_status hk_gemm_padded_bf16_fp32_backward(hk_context* ctx, const hk_tensor* a_pad,
+                                            const hk_tensor* b_pad, const hk_tensor* dy,
+                                            int32_t ta, int32_t tb, hk_tensor* da, hk_tensor* db);
+/* Y[M,N] (F32) = bf16(X[M,K]) W[N,K]^T with a fixed BF16 weight. w_pad (BF16, both axes rounded
+ * up to 16) receives the zero-padded weight the backward uses; it may be NULL when W's axes are
+ * already multiples of 16 (W itself is then the saved weight, as the reference reuses the aligned
+ * handle). Reference: AscendRuntime::linear_frozen_padded_bf16_fp32, runtime/mod.rs:196-200
+ * (padded_matrix.rs:64-76). */
+hk_status hk_linear_frozen_padded_bf16_fp32(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
+                                            hk_tensor* y, hk_tensor* w_pad);
+/* dX[M,K] (F32) from the saved padded weight and the logical F32 dY[M,N]. Reference:
+ * AscendRuntime::linear_frozen_padded_bf16_fp32_backward, runtime/mod.rs:201-204
+ * (padded_matrix.rs:77-87). */
+hk_status hk_linear_frozen_padded_bf16_fp32_backward(hk_context* ctx, const hk_tensor* w_pad,
+                                                     const hk_tensor* dy, hk_tensor* dx);
+
 /* Elementwise F32 <-> BF16 conversion (RNE, NaN kept quiet, Inf kept).
  * Reference: AscendRuntime::cast_into, runtime/mod.rs:276-279 (conversion.rs:21-62). */
 hk_status hk_cast_into(hk_context* ctx, const hk_tensor* in, hk_tensor* out);

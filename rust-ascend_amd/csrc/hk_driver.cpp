@@ -740,6 +740,253 @@ hk_status hk_linear_bf16_fp32_backward(hk_context* h, const hk_tensor* x, const 
     return hk_gemm_bf16_fp32_backward(h, x, w, dy, HK_NO, HK_YES, dx, dw);
 }
 
+// ------------------------------------------------------------------ padded GEMM
+
+namespace {
+
+int64_t round16(int64_t x) { return (x + 15) / 16 * 16; }
+
+// Reference: PaddedGemmSpec::new, deepgemm/padded.rs:13-36. The matrix axes of A and B are
+// rounded up to multiples of 16 (the "native" BF16 layouts); the logical output is F32.
+struct PaddedSpec {
+    int rank = 2;
+    int64_t batch = 1, m = 0, n = 0, k = 0;
+    int64_t a_rows = 0, a_cols = 0, b_rows = 0, b_cols = 0;  // physical matrix axes
+    hk_tensor a_pad{}, b_pad{};                              // native BF16 layouts (data unset)
+    GemmSpec native;
+};
+
+hk_status padded_spec(const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb, PaddedSpec* p) {
+    if (!tensor_ok(a, "A") || !tensor_ok(b, "B")) return HK_INVALID_ARGUMENT;
+    if ((ta != HK_NO && ta != HK_YES) || (tb != HK_NO && tb != HK_YES))
+        return fail(HK_INVALID_ARGUMENT, "transpose flags must be 0 (No) or 1 (Yes)");
+    const int r = a->rank;
+    if (!(r == 2 || r == 3) || b->rank != r || !(a->dtype == HK_F32 || a->dtype == HK_BF16) ||
+        !(b->dtype == HK_F32 || b->dtype == HK_BF16))
+        return fail(HK_INVALID_ARGUMENT, "padded GEMM requires matching rank-2/3 FP32/BF16 inputs");
+    if (r == 3 && a->shape[0] != b->shape[0]) return fail(HK_INVALID_ARGUMENT, "padded GEMM does not broadcast batches");
+    const int64_t *a2 = a->shape + (r - 2), *b2 = b->shape + (r - 2);
+    const int64_t m = ta == HK_NO ? a2[0] : a2[1], k = ta == HK_NO ? a2[1] : a2[0];
+    const int64_t kb = tb == HK_NO ? b2[0] : b2[1], n = tb == HK_NO ? b2[1] : b2[0];
+    if (k != kb) return fail(HK_INVALID_ARGUMENT, "padded GEMM logical contraction mismatch");
+    p->a_pad = *a;
+    p->b_pad = *b;
+    for (hk_tensor* t : {&p->a_pad, &p->b_pad}) {
+        t->dtype = HK_BF16;
+        t->data = reinterpret_cast<void*>(uintptr_t{256});  // layout only; never dereferenced
+        for (int i = r - 2; i < r; ++i) {
+            if (t->shape[i] <= 0) return fail(HK_INVALID_ARGUMENT, "padded GEMM matrix axes must be positive");
+            if (round16(t->shape[i]) > INT32_MAX) return fail(HK_INVALID_ARGUMENT, "padded GEMM aligned axis exceeds INT32_MAX");
+            t->shape[i] = round16(t->shape[i]);
+        }
+    }
+    hk_status st = gemm_spec(&p->a_pad, &p->b_pad, ta, tb, HK_F32, &p->native);
+    if (st != HK_OK) return st;
+    p->rank = r;
+    p->batch = r == 3 ? a->shape[0] : 1;
+    p->m = m;
+    p->n = n;
+    p->k = k;
+    p->a_rows = a2[0];
+    p->a_cols = a2[1];
+    p->b_rows = b2[0];
+    p->b_cols = b2[1];
+    return HK_OK;
+}
+
+bool is_logical_out(const PaddedSpec& p, const hk_tensor* t) {
+    if (t->dtype != HK_F32 || t->rank != p.rank) return false;
+    const int64_t* s = t->shape + (p.rank - 2);
+    return (p.rank == 2 || t->shape[0] == p.batch) && s[0] == p.m && s[1] == p.n;
+}
+
+bool same_layout(const hk_tensor* t, const hk_tensor& want) { return t->dtype == want.dtype && same_shape(t, &want); }
+
+size_t ws_round(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+hk_status hk_gemm_padded_bf16_fp32(hk_context* h, const hk_tensor* a, const hk_tensor* b, int32_t ta, int32_t tb,
+                                   hk_tensor* out, hk_tensor* a_pad, hk_tensor* b_pad) {
+    // Reference: padded_matrix::forward, runtime/padded_matrix.rs:39-46.
+    PaddedSpec p;
+    hk_status st = padded_spec(a, b, ta, tb, &p);
+    if (st != HK_OK) return st;
+    if (a->dtype != HK_F32 || b->dtype != HK_F32)
+        return fail(HK_INVALID_ARGUMENT, "padded trainable matmul requires FP32 inputs");
+    if (!tensor_ok(out, "out") || !tensor_ok(a_pad, "A_pad") || !tensor_ok(b_pad, "B_pad")) return HK_INVALID_ARGUMENT;
+    if (!is_logical_out(p, out)) return fail(HK_INVALID_ARGUMENT, "output must be F32 of the logical shape");
+    if (!same_layout(a_pad, p.a_pad) || !same_layout(b_pad, p.b_pad))
+        return fail(HK_INVALID_ARGUMENT, "padded snapshots must be BF16 with matrix axes rounded up to 16");
+    if (!disjoint({out, a_pad, b_pad}, {a, b})) return HK_INVALID_ARGUMENT;
+    const GemmSpec& s = p.native;
+    const bool crop = s.m != p.m || s.n != p.n;
+    const size_t out_bytes = crop ? ws_round(static_cast<size_t>(s.batch * s.m * s.n) * 4) : 0;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, out_bytes + hk::gemm_workspace_bytes(s.batch, s.m, s.n, s.k, ta, tb))) != HK_OK)
+        return st;
+    float* native_out = crop ? static_cast<float*>(g.c->workspace) : static_cast<float*>(out->data);
+    void* gws = static_cast<char*>(g.c->workspace) + out_bytes;
+    const int64_t ar = p.a_pad.shape[p.rank - 2], ac = p.a_pad.shape[p.rank - 1];
+    const int64_t br = p.b_pad.shape[p.rank - 2], bc = p.b_pad.shape[p.rank - 1];
+    hipError_t e = hk::pad_bf16(0, a->data, a_pad->data, p.batch, p.a_rows, p.a_cols, ar, ac, g.c->stream);
+    if (e == hipSuccess) e = hk::pad_bf16(0, b->data, b_pad->data, p.batch, p.b_rows, p.b_cols, br, bc, g.c->stream);
+    if (e == hipSuccess) run_gemm(g.c, s, a_pad->data, b_pad->data, native_out, ta, tb, gws, &e);
+    if (e == hipSuccess && crop)
+        e = hk::crop_f32(native_out, static_cast<float*>(out->data), p.batch, p.m, p.n, s.m, s.n, g.c->stream);
+    return complete(g.c, e, "gemm_padded_bf16_fp32", crop ? 4 : 3);
+}
+
+hk_status hk_gemm_padded_bf16_fp32_backward(hk_context* h, const hk_tensor* a_pad, const hk_tensor* b_pad,
+                                            const hk_tensor* dy, int32_t ta, int32_t tb, hk_tensor* da,
+                                            hk_tensor* db) {
+    // Reference: padded_matrix::backward, runtime/padded_matrix.rs:47-63, and
+    // PaddedGemmSpec::backward_specs, deepgemm/padded.rs:39-50. da/db carry the original
+    // physical input shapes (the reference's a_shape/b_shape).
+    if (!tensor_ok(da, "dA") || !tensor_ok(db, "dB")) return HK_INVALID_ARGUMENT;
+    if (da->dtype != HK_F32 || db->dtype != HK_F32) return fail(HK_INVALID_ARGUMENT, "padded gradients are F32");
+    PaddedSpec p;
+    hk_status st = padded_spec(da, db, ta, tb, &p);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(a_pad, "A_pad") || !tensor_ok(b_pad, "B_pad") || !tensor_ok(dy, "dY")) return HK_INVALID_ARGUMENT;
+    if (!same_layout(a_pad, p.a_pad) || !same_layout(b_pad, p.b_pad) || !is_logical_out(p, dy))
+        return fail(HK_INVALID_ARGUMENT, "padded matmul backward saved input or logical dY layout mismatch");
+    if (!disjoint({da, db}, {a_pad, b_pad, dy})) return HK_INVALID_ARGUMENT;
+    const GemmSpec& s = p.native;
+    hk_tensor dyp{};  // dY rounded to BF16 and padded to [batch, M16, N16]
+    dyp.dtype = HK_BF16;
+    dyp.rank = p.rank;
+    dyp.data = reinterpret_cast<void*>(uintptr_t{256});
+    if (p.rank == 3) dyp.shape[0] = p.batch;
+    dyp.shape[p.rank - 2] = s.m;
+    dyp.shape[p.rank - 1] = s.n;
+    const int opp_ta = ta == HK_NO ? HK_YES : HK_NO, opp_tb = tb == HK_NO ? HK_YES : HK_NO;
+    const hk_tensor *da_a = ta == HK_NO ? &dyp : b_pad, *da_b = ta == HK_NO ? b_pad : &dyp;
+    const int da_ta = ta == HK_NO ? HK_NO : tb, da_tb = ta == HK_NO ? opp_tb : HK_YES;
+    const hk_tensor *db_a = tb == HK_NO ? a_pad : &dyp, *db_b = tb == HK_NO ? &dyp : a_pad;
+    const int db_ta = tb == HK_NO ? opp_ta : HK_YES, db_tb = tb == HK_NO ? HK_NO : ta;
+    GemmSpec sda, sdb;
+    if ((st = gemm_spec(da_a, da_b, da_ta, da_tb, HK_F32, &sda)) != HK_OK) return st;
+    if ((st = gemm_spec(db_a, db_b, db_ta, db_tb, HK_F32, &sdb)) != HK_OK) return st;
+    const bool crop_a = !same_shape(da, &p.a_pad), crop_b = !same_shape(db, &p.b_pad);
+    const size_t dy_bytes = ws_round(static_cast<size_t>(s.batch * s.m * s.n) * 2);
+    const size_t pa_bytes = crop_a ? ws_round(static_cast<size_t>(numel(&p.a_pad)) * 4) : 0;
+    const size_t pb_bytes = crop_b ? ws_round(static_cast<size_t>(numel(&p.b_pad)) * 4) : 0;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const size_t gws_bytes = std::max(hk::gemm_workspace_bytes(sda.batch, sda.m, sda.n, sda.k, da_ta, da_tb),
+                                      hk::gemm_workspace_bytes(sdb.batch, sdb.m, sdb.n, sdb.k, db_ta, db_tb));
+    if ((st = ensure_workspace(g.c, dy_bytes + pa_bytes + pb_bytes + gws_bytes)) != HK_OK) return st;
+    char* w = static_cast<char*>(g.c->workspace);
+    dyp.data = w;
+    float* pa = crop_a ? reinterpret_cast<float*>(w + dy_bytes) : static_cast<float*>(da->data);
+    float* pb = crop_b ? reinterpret_cast<float*>(w + dy_bytes + pa_bytes) : static_cast<float*>(db->data);
+    void* gws = w + dy_bytes + pa_bytes + pb_bytes;
+    int kernels = 3;
+    hipError_t e = hk::pad_bf16(0, dy->data, dyp.data, p.batch, p.m, p.n, s.m, s.n, g.c->stream);
+    if (e == hipSuccess) run_gemm(g.c, sda, da_a->data, da_b->data, pa, da_ta, da_tb, gws, &e);
+    if (e == hipSuccess) run_gemm(g.c, sdb, db_a->data, db_b->data, pb, db_ta, db_tb, gws, &e);
+    const int64_t ar = p.a_pad.shape[p.rank - 2], ac = p.a_pad.shape[p.rank - 1];
+    const int64_t br = p.b_pad.shape[p.rank - 2], bc = p.b_pad.shape[p.rank - 1];
+    if (e == hipSuccess && crop_a) {
+        e = hk::crop_f32(pa, static_cast<float*>(da->data), p.batch, p.a_rows, p.a_cols, ar, ac, g.c->stream);
+        ++kernels;
+    }
+    if (e == hipSuccess && crop_b) {
+        e = hk::crop_f32(pb, static_cast<float*>(db->data), p.batch, p.b_rows, p.b_cols, br, bc, g.c->stream);
+        ++kernels;
+    }
+    return complete(g.c, e, "gemm_padded_bf16_fp32_backward", kernels);
+}
+
+hk_status hk_linear_frozen_padded_bf16_fp32(hk_context* h, const hk_tensor* x, const hk_tensor* w, hk_tensor* y,
+                                            hk_tensor* w_pad) {
+    // Reference: padded_matrix::frozen_forward, runtime/padded_matrix.rs:64-76.
+    if (!tensor_ok(x, "input") || !tensor_ok(w, "weight")) return HK_INVALID_ARGUMENT;
+    if (x->rank != 2 || w->rank != 2 || x->dtype != HK_F32 || w->dtype != HK_BF16)
+        return fail(HK_INVALID_ARGUMENT, "frozen padded linear requires rank-2 FP32 input and fixed BF16 weight");
+    PaddedSpec p;
+    hk_status st = padded_spec(x, w, HK_NO, HK_YES, &p);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(y, "out")) return HK_INVALID_ARGUMENT;
+    if (!is_logical_out(p, y)) return fail(HK_INVALID_ARGUMENT, "output must be F32 [M,N]");
+    const bool w_tail = !same_shape(w, &p.b_pad);
+    if (w_pad) {
+        if (!tensor_ok(w_pad, "W_pad") || !same_layout(w_pad, p.b_pad))
+            return fail(HK_INVALID_ARGUMENT, "padded weight must be BF16 with both axes rounded up to 16");
+        if (!disjoint({y, w_pad}, {x, w})) return HK_INVALID_ARGUMENT;
+    } else if (!disjoint({y}, {x, w})) {
+        return HK_INVALID_ARGUMENT;
+    }
+    const GemmSpec& s = p.native;
+    const bool crop = s.m != p.m || s.n != p.n;
+    const size_t xb = ws_round(static_cast<size_t>(s.m * s.k) * 2);
+    const size_t wb = (w_tail && !w_pad) ? ws_round(static_cast<size_t>(s.n * s.k) * 2) : 0;
+    const size_t ob = crop ? ws_round(static_cast<size_t>(s.m * s.n) * 4) : 0;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, xb + wb + ob + hk::gemm_workspace_bytes(1, s.m, s.n, s.k, HK_NO, HK_YES))) != HK_OK)
+        return st;
+    char* ws = static_cast<char*>(g.c->workspace);
+    void* xpad = ws;
+    // aligned weights are used in place (reference: "aligned weights reuse their actual handle")
+    const void* wuse = w->data;
+    int kernels = 2;
+    hipError_t e = hk::pad_bf16(0, x->data, xpad, 1, p.m, p.k, s.m, s.k, g.c->stream);
+    if (e == hipSuccess && (w_tail || w_pad)) {
+        void* wdst = w_pad ? w_pad->data : ws + xb;
+        e = hk::pad_bf16(1, w->data, wdst, 1, p.n, p.k, s.n, s.k, g.c->stream);
+        wuse = wdst;
+        ++kernels;
+    }
+    float* native_out = crop ? reinterpret_cast<float*>(ws + xb + wb) : static_cast<float*>(y->data);
+    if (e == hipSuccess) run_gemm(g.c, s, xpad, wuse, native_out, HK_NO, HK_YES, ws + xb + wb + ob, &e);
+    if (e == hipSuccess && crop) {
+        e = hk::crop_f32(native_out, static_cast<float*>(y->data), 1, p.m, p.n, s.m, s.n, g.c->stream);
+        ++kernels;
+    }
+    return complete(g.c, e, "linear_frozen_padded_bf16_fp32", kernels);
+}
+
+hk_status hk_linear_frozen_padded_bf16_fp32_backward(hk_context* h, const hk_tensor* w_pad, const hk_tensor* dy,
+                                                     hk_tensor* dx) {
+    // Reference: padded_matrix::frozen_backward, runtime/padded_matrix.rs:77-87. The logical
+    // input shape is dx's; the logical weight shape is [dy's N, dx's K].
+    if (!tensor_ok(w_pad, "weight") || !tensor_ok(dy, "dY") || !tensor_ok(dx, "dX")) return HK_INVALID_ARGUMENT;
+    if (dx->rank != 2 || dy->rank != 2 || w_pad->rank != 2)
+        return fail(HK_INVALID_ARGUMENT, "frozen padded linear backward requires rank-2 shapes");
+    if (dx->dtype != HK_F32) return fail(HK_INVALID_ARGUMENT, "dX must be F32");
+    hk_tensor wl = *w_pad;  // the logical weight layout [N, K]
+    wl.shape[0] = dy->shape[1];
+    wl.shape[1] = dx->shape[1];
+    wl.dtype = HK_BF16;
+    PaddedSpec p;
+    hk_status st = padded_spec(dx, &wl, HK_NO, HK_YES, &p);
+    if (st != HK_OK) return st;
+    if (!same_layout(w_pad, p.b_pad) || !is_logical_out(p, dy))
+        return fail(HK_INVALID_ARGUMENT, "frozen padded linear saved weight or dY layout mismatch");
+    if (!disjoint({dx}, {w_pad, dy})) return HK_INVALID_ARGUMENT;
+    const GemmSpec& s = p.native;
+    hk_tensor dyp = make_view(reinterpret_cast<void*>(uintptr_t{256}), HK_BF16, {s.m, s.n});
+    GemmSpec sdx;
+    if ((st = gemm_spec(&dyp, w_pad, HK_NO, HK_NO, HK_F32, &sdx)) != HK_OK) return st;
+    const bool crop = s.m != p.m || s.k != p.k;
+    const size_t db = ws_round(static_cast<size_t>(s.m * s.n) * 2);
+    const size_t ob = crop ? ws_round(static_cast<size_t>(s.m * s.k) * 4) : 0;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, db + ob + hk::gemm_workspace_bytes(1, sdx.m, sdx.n, sdx.k, HK_NO, HK_NO))) != HK_OK)
+        return st;
+    char* ws = static_cast<char*>(g.c->workspace);
+    float* native_out = crop ? reinterpret_cast<float*>(ws + db) : static_cast<float*>(dx->data);
+    hipError_t e = hk::pad_bf16(0, dy->data, ws, 1, p.m, p.n, s.m, s.n, g.c->stream);
+    if (e == hipSuccess) run_gemm(g.c, sdx, ws, w_pad->data, native_out, HK_NO, HK_NO, ws + db + ob, &e);
+    if (e == hipSuccess && crop)
+        e = hk::crop_f32(native_out, static_cast<float*>(dx->data), 1, p.m, p.k, s.m, s.k, g.c->stream);
+    return complete(g.c, e, "linear_frozen_padded_bf16_fp32_backward", crop ? 3 : 2);
+}
+
 hk_status hk_cast_into(hk_context* h, const hk_tensor* in, hk_tensor* out) {
     // Reference: conversion.rs:21-62 (shape retained, distinct output storage).
     if (!tensor_ok(in, "input") || !tensor_ok(out, "output")) return HK_INVALID_ARGUMENT;

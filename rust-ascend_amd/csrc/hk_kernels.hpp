@@ -43,6 +43,15 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
 hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_bf16, int64_t m, int64_t n,
                                 int64_t k, const int32_t* block_group, int num_cus, hipStream_t s);
 
+// ---- matrix tails (hk_pad.hip)
+// dst [batch, R, C] BF16 = src [batch, rows, cols] (F32 rounded to BF16 with RNE, or BF16 copied)
+// zero-padded (rows <= R, cols <= C, C even).
+hipError_t pad_bf16(int src_bf16, const void* src, void* dst, int64_t batch, int64_t rows, int64_t cols, int64_t R,
+                    int64_t C, hipStream_t s);
+// dst [batch, rows, cols] = the leading window of src [batch, R, C] (F32).
+hipError_t crop_f32(const float* src, float* dst, int64_t batch, int64_t rows, int64_t cols, int64_t R, int64_t C,
+                    hipStream_t s);
+
 // ---- element-wise (hk_elementwise.hip)
 // SwiGLU gate, element-wise over n values of F32 or BF16 storage.
 hipError_t silu_mul(int dtype_bf16, const void* gate, const void* up, void* y, int64_t n, hipStream_t s);

@@ -83,6 +83,10 @@ SIGNATURES = {
     "hk_linear_nt_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_gemm_bf16_fp32": [_CTX, _T, _T, _i32, _i32, _T, _T, _T],
     "hk_gemm_bf16_fp32_backward": [_CTX, _T, _T, _T, _i32, _i32, _T, _T],
+    "hk_gemm_padded_bf16_fp32": [_CTX, _T, _T, _i32, _i32, _T, _T, _T],
+    "hk_gemm_padded_bf16_fp32_backward": [_CTX, _T, _T, _T, _i32, _i32, _T, _T],
+    "hk_linear_frozen_padded_bf16_fp32": [_CTX, _T, _T, _T, _T],
+    "hk_linear_frozen_padded_bf16_fp32_backward": [_CTX, _T, _T, _T],
     "hk_linear_bf16_fp32": [_CTX, _T, _T, _T, _T, _T],
     "hk_linear_bf16_fp32_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_cast_into": [_CTX, _T, _T],

@@ -3,7 +3,8 @@
 for RUDA's autodiff graph. Saved state matches the reference's Backward nodes:
 
 * linear_bf16_fp32 / matmul_bf16_fp32 save the BF16 snapshots of both operands
-  (src/nn.rs:375-453), and their backward rounds dY to BF16 before the two GEMMs;
+  (src/nn.rs:375-453), and their backward rounds dY to BF16 before the two GEMMs; the padded
+  forms save the zero-padded snapshots and the original shapes (src/nn/padded.rs:29-57);
 * rms_norm saves (x, w, rstd) and the backward reuses rstd (src/nn.rs:203-232);
 * rotary/rotary_prefix save nothing but the fixed tables (src/nn/rotary.rs:32-105);
 * the fused attention saves (q, k, v, o, lse) instead of the materialized score,
@@ -53,6 +54,55 @@ class _MatmulBf16Fp32(torch.autograd.Function):
 def matmul_bf16_fp32(a, b, ta=Transpose.No, tb=Transpose.No) -> torch.Tensor:
     """op(A) op(B) with BF16 compute and F32 storage. Reference: nn::matmul_bf16_fp32 (src/nn.rs:70-78)."""
     return _MatmulBf16Fp32.apply(a, b, Transpose(ta), Transpose(tb))
+
+
+class _MatmulPaddedBf16Fp32(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b, ta, tb):
+        out, ap, bp = HipRuntime.gemm_padded_bf16_fp32(a.contiguous(), b.contiguous(), ta, tb)
+        ctx.save_for_backward(ap, bp)
+        ctx.shapes = (tuple(a.shape), tuple(b.shape))
+        ctx.ta, ctx.tb = ta, tb
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        ap, bp = ctx.saved_tensors
+        da, db = HipRuntime.gemm_padded_bf16_fp32_backward(ap, bp, dy.contiguous().float(), ctx.shapes[0],
+                                                           ctx.shapes[1], ctx.ta, ctx.tb)
+        return da, db, None, None
+
+
+def matmul_padded_bf16_fp32(a, b, ta=Transpose.No, tb=Transpose.No) -> torch.Tensor:
+    """op(A) op(B) for any positive M/N/K, BF16 compute with on-device zero padding and an F32
+    crop. Saves the padded BF16 snapshots and the original shapes. Reference:
+    nn::matmul_padded_bf16_fp32 and PaddedMatmulBackward (src/nn/padded.rs:16-57)."""
+    return _MatmulPaddedBf16Fp32.apply(a, b, Transpose(ta), Transpose(tb))
+
+
+def linear_padded_bf16_fp32(x, w) -> torch.Tensor:
+    """X[M,K] W[N,K]^T with explicit padding. Reference: nn::linear_padded_bf16_fp32 (src/nn/padded.rs:22-25)."""
+    return matmul_padded_bf16_fp32(x, w, Transpose.No, Transpose.Yes)
+
+
+class _LinearFrozenPadded(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight):
+        y, wp = HipRuntime.linear_frozen_padded_bf16_fp32(x.contiguous(), weight.contiguous())
+        ctx.save_for_backward(wp)
+        ctx.x_shape = tuple(x.shape)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (wp,) = ctx.saved_tensors
+        return HipRuntime.linear_frozen_padded_bf16_fp32_backward(wp, dy.contiguous().float(), ctx.x_shape), None
+
+
+def linear_frozen_padded_bf16_fp32(x, weight) -> torch.Tensor:
+    """F32 X and a fixed BF16 W: input-only differentiation with logical tails (the weight never
+    receives a gradient). Reference: nn::linear_frozen_padded_bf16_fp32 (src/nn/padded.rs:58-100)."""
+    return _LinearFrozenPadded.apply(x, weight)
 
 
 class _LinearBf16(torch.autograd.Function):

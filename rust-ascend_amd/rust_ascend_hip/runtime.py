@@ -142,6 +142,12 @@ class DeviceGroupEnds:
             self._handle = None
 
 
+def _padded(shape):
+    """Shape with its two matrix axes rounded up to multiples of 16 (deepgemm/padded.rs:26-31)."""
+    shape = tuple(int(d) for d in shape)
+    return shape[:-2] + tuple((d + 15) // 16 * 16 for d in shape[-2:])
+
+
 class HipRuntime:
     """Static entry points mirroring AscendRuntime (runtime/mod.rs:147-435)."""
 
@@ -231,6 +237,57 @@ class HipRuntime:
         _call("hk_gemm_bf16_fp32_backward", desc(a_bf16), desc(b_bf16), desc(grad), int(ta), int(tb), desc(da),
               desc(db))
         return da, db
+
+    @staticmethod
+    def gemm_padded_bf16_fp32(a, b, ta=Transpose.No, tb=Transpose.No):
+        """[F32 logical out, padded BF16 A snapshot, padded BF16 B snapshot] for any positive
+        M/N/K. Reference: AscendRuntime::gemm_padded_bf16_fp32 (mod.rs:186-190)."""
+        r = a.dim()
+        if r not in (2, 3) or b.dim() != r:
+            raise HkError(_lib.INVALID_ARGUMENT, "padded GEMM requires matching rank-2/3 FP32/BF16 inputs")
+        m = a.shape[-1] if int(ta) else a.shape[-2]
+        n = b.shape[-2] if int(tb) else b.shape[-1]
+        lead = tuple(a.shape[:-2])
+        out = _empty(lead + (m, n), torch.float32, a)
+        ap = _empty(_padded(a.shape), torch.bfloat16, a)
+        bp = _empty(_padded(b.shape), torch.bfloat16, a)
+        _call("hk_gemm_padded_bf16_fp32", desc(a), desc(b), int(ta), int(tb), desc(out), desc(ap), desc(bp))
+        return out, ap, bp
+
+    @staticmethod
+    def gemm_padded_bf16_fp32_backward(a_pad, b_pad, grad, a_shape, b_shape, ta=Transpose.No, tb=Transpose.No):
+        """[F32 dA in a_shape, F32 dB in b_shape] (the original physical input shapes).
+        Reference: AscendRuntime::gemm_padded_bf16_fp32_backward (mod.rs:191-195)."""
+        da = _empty(tuple(a_shape), torch.float32, grad)
+        db = _empty(tuple(b_shape), torch.float32, grad)
+        _call("hk_gemm_padded_bf16_fp32_backward", desc(a_pad), desc(b_pad), desc(grad), int(ta), int(tb), desc(da),
+              desc(db))
+        return da, db
+
+    @staticmethod
+    def linear_frozen_padded_bf16_fp32(x, weight):
+        """[F32 Y, the BF16 weight the backward uses]: the weight itself when its axes are multiples
+        of 16, else a zero-padded copy. Reference: AscendRuntime::linear_frozen_padded_bf16_fp32
+        (mod.rs:196-200)."""
+        if x.dim() != 2 or weight.dim() != 2:
+            raise HkError(_lib.INVALID_ARGUMENT, "frozen padded linear requires rank-2 FP32 input and fixed BF16 weight")
+        y = _empty((x.shape[0], weight.shape[0]), torch.float32, x)
+        if tuple(weight.shape) == _padded(weight.shape):
+            _call("hk_linear_frozen_padded_bf16_fp32", desc(x), desc(weight), desc(y), None)
+            return y, weight
+        wp = _empty(_padded(weight.shape), torch.bfloat16, x)
+        _call("hk_linear_frozen_padded_bf16_fp32", desc(x), desc(weight), desc(y), desc(wp))
+        return y, wp
+
+    @staticmethod
+    def linear_frozen_padded_bf16_fp32_backward(weight_pad, grad, input_shape, weight_shape=None):
+        """F32 dX in input_shape. weight_shape (the logical [N, K]) is implied by grad and
+        input_shape and only checked. Reference: linear_frozen_padded_bf16_fp32_backward (mod.rs:201-204)."""
+        if weight_shape is not None and (tuple(weight_shape) != (grad.shape[-1], input_shape[-1])):
+            raise HkError(_lib.INVALID_ARGUMENT, "frozen padded linear saved weight or dY layout mismatch")
+        dx = _empty(tuple(input_shape), torch.float32, grad)
+        _call("hk_linear_frozen_padded_bf16_fp32_backward", desc(weight_pad), desc(grad), desc(dx))
+        return dx
 
     @staticmethod
     def linear_bf16_fp32(x, w):

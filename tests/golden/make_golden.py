@@ -96,6 +96,36 @@ def main():
     g["grouped_dv_out"] = np.concatenate([a[:256].astype(np.float64) @ w[0].astype(np.float64).T,
                                           a[256:].astype(np.float64) @ w[2].astype(np.float64).T])
 
+    # Padded BF16-compute GEMM, examples/padded_matrix_tensor.rs:12-45,77-80: (m,n,k) in
+    # {(1,1,1),(3,17,7),(17,33,65),(16,32,48)}, all transposes, rank 2 and batch-2 rank 3;
+    # a = ((i%17)-8)/59, b = ((i%13)-6)/43, dy = ((i%11)-5)/37 (F32). Expected (the reference's host
+    # loop): f64 sums of BF16-rounded products, Y and the gradients of sum(Y * dy).
+    for batch in (None, 2):
+        nb = batch or 1
+        for (m, n, k) in ((1, 1, 1), (3, 17, 7), (17, 33, 65), (16, 32, 48)):
+            for ta in (0, 1):
+                for tb in (0, 1):
+                    a = ((np.arange(nb * m * k) % 17).astype(np.float32) - 8) / 59
+                    b = ((np.arange(nb * k * n) % 13).astype(np.float32) - 6) / 43
+                    dy = ((np.arange(nb * m * n) % 11).astype(np.float32) - 5) / 37
+                    ash = (k, m) if ta else (m, k)
+                    bsh = (n, k) if tb else (k, n)
+                    A = a.reshape((nb,) + ash)
+                    B = b.reshape((nb,) + bsh)
+                    DY = dy.reshape(nb, m, n)
+                    Ar, Br, Dr = (bf16(t).astype(np.float64) for t in (A, B, DY))
+                    opA = Ar.transpose(0, 2, 1) if ta else Ar
+                    opB = Br.transpose(0, 2, 1) if tb else Br
+                    Y = opA @ opB
+                    dopA = Dr @ opB.transpose(0, 2, 1)
+                    dopB = opA.transpose(0, 2, 1) @ Dr
+                    dA = dopA.transpose(0, 2, 1) if ta else dopA
+                    dB = dopB.transpose(0, 2, 1) if tb else dopB
+                    sq = (lambda t: t) if batch else (lambda t: t[0])
+                    key = f"padded_{nb}_{m}x{n}x{k}_{'nt'[ta]}{'nt'[tb]}"
+                    g[key + "_a"], g[key + "_b"], g[key + "_dy"] = sq(A), sq(B), sq(DY)
+                    g[key + "_y"], g[key + "_da"], g[key + "_db"] = sq(Y), sq(dA), sq(dB)
+
     # examples/matrix_runtime.rs:70-77: linear_nt_backward, m,n,k = 32,48,16,
     # x = ((i%17)-8)*0.125, w = ((i%13)-6)*0.25, dy = ((i%11)-5)*0.0625.
     m, n, k = 32, 48, 16

@@ -113,6 +113,50 @@ def test_group_ends_contract():
     assert lib.hk_group_ends_upload(None, bad, 2, ctypes.byref(ctypes.c_void_p())) == _lib.INVALID_ARGUMENT
 
 
+def test_padded_gemm_contract():
+    # deepgemm/padded.rs:54-80: tails are accepted; contract, batch, dtype and native-domain errors
+    # are not disguised by padding. Valid calls reach the (missing) context.
+    lib = _lib.load()
+
+    def call(a, b, ta=0, tb=0, adt=F32, bdt=F32):
+        ra, rb = len(a), len(b)
+        m = a[-1] if ta else a[-2]
+        n = b[-2] if tb else b[-1]
+        out = a[:-2] + (m, n)
+        pad = lambda s: tuple(s[:-2]) + tuple((d + 15) // 16 * 16 for d in s[-2:])
+        return lib.hk_gemm_padded_bf16_fp32(None, fake(adt, a, 1 << 20), fake(bdt, b, 1 << 30), ta, tb,
+                                            fake(F32, out, 1 << 34), fake(BF16, pad(a), 1 << 36),
+                                            fake(BF16, pad(b), 1 << 38))
+
+    for (m, n, k) in [(1, 1, 1), (3, 17, 7), (17, 33, 65), (16, 32, 48)]:
+        for ta in (0, 1):
+            for tb in (0, 1):
+                a = (k, m) if ta else (m, k)
+                b = (n, k) if tb else (k, n)
+                assert call(a, b, ta, tb) == _lib.NOT_INITIALIZED, (m, n, k, ta, tb)
+                assert call((2,) + a, (2,) + b, ta, tb) == _lib.NOT_INITIALIZED
+    for a, b, adt in [((3, 7), (8, 17), F32), ((0, 7), (7, 17), F32), ((2, 3, 7), (1, 7, 17), F32),
+                      ((3, 7), (7, 17), F16), ((2**31 - 1, 7), (7, 17), F32), ((4097, 3, 7), (4097, 7, 17), F32)]:
+        assert call(a, b, adt=adt) == _lib.INVALID_ARGUMENT, (a, b)
+    # the trainable form takes F32 inputs only (padded_matrix.rs:42)
+    assert call((3, 7), (7, 17), bdt=BF16) == _lib.INVALID_ARGUMENT
+    # snapshots must have the native (rounded) shapes
+    assert lib.hk_gemm_padded_bf16_fp32(None, fake(F32, (3, 7), 1 << 20), fake(F32, (7, 17), 1 << 30), 0, 0,
+                                        fake(F32, (3, 17), 1 << 34), fake(BF16, (3, 7), 1 << 36),
+                                        fake(BF16, (16, 32), 1 << 38)) == _lib.INVALID_ARGUMENT
+    # frozen form: rank-2 F32 input, BF16 weight; the padded weight may be omitted
+    assert lib.hk_linear_frozen_padded_bf16_fp32(None, fake(F32, (3, 35), 1 << 20), fake(BF16, (19, 35), 1 << 30),
+                                                 fake(F32, (3, 19), 1 << 34), None) == _lib.NOT_INITIALIZED
+    assert lib.hk_linear_frozen_padded_bf16_fp32(None, fake(F32, (3, 35), 1 << 20), fake(F32, (19, 35), 1 << 30),
+                                                 fake(F32, (3, 19), 1 << 34), None) == _lib.INVALID_ARGUMENT
+    assert lib.hk_linear_frozen_padded_bf16_fp32_backward(None, fake(BF16, (32, 48), 1 << 20),
+                                                          fake(F32, (3, 19), 1 << 30),
+                                                          fake(F32, (3, 35), 1 << 34)) == _lib.NOT_INITIALIZED
+    assert lib.hk_linear_frozen_padded_bf16_fp32_backward(None, fake(BF16, (19, 35), 1 << 20),
+                                                          fake(F32, (3, 19), 1 << 30),
+                                                          fake(F32, (3, 35), 1 << 34)) == _lib.INVALID_ARGUMENT
+
+
 def test_overlap_and_shape_checks_run_before_the_context():
     lib = _lib.load()
     a = fake(BF16, (32, 48), ptr=1 << 20)

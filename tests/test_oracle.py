@@ -89,6 +89,18 @@ def test_gemm_grouped_identities(oracle):
     assert not np.allclose(y[256:], a[256:].astype(np.float64) @ w[1].T.astype(np.float64))
 
 
+@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("mnk", ["1x1x1", "3x17x7", "17x33x65", "16x32x48"])
+@pytest.mark.parametrize("ta", [0, 1])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_on_padded_reference_cases(oracle, golden, batch, mnk, ta, tb):
+    # examples/padded_matrix_tensor.rs:12-45: logical shapes that are not multiples of 16; the
+    # oracle's product of BF16-rounded operands is the padded GEMM's expectation
+    key = f"padded_{batch}_{mnk}_{'nt'[ta]}{'nt'[tb]}"
+    a, b = oracle.bf16_round(golden[key + "_a"]), oracle.bf16_round(golden[key + "_b"])
+    close(oracle.gemm_f64(a, b, ta, tb), golden[key + "_y"], 1e-12, 1e-12)
+
+
 def test_gemm_random_vs_numpy_and_transpose_identity(oracle):
     a = oracle.normal((3, 40, 24), 1, 1)
     b = oracle.normal((3, 24, 56), 1, 2)
