@@ -46,6 +46,9 @@ struct GemmArgs {
     // M-grouped form (batch 1): block_group[r / 256] is the weight slice of rows r of A and C.
     // Group ends are multiples of 256, so an output tile (256, 128 or 64 rows) has one group.
     const int32_t* block_group;
+    // 4-wave kernel tile order: 0 = bands of 4 M-tile rows per XCD, else bands of this many
+    // N-tile columns.
+    int band_n;
 };
 
 // B operand of the tile whose first output row is row0 in batch g.
@@ -728,7 +731,8 @@ gemm_nt_pp_kernel(GemmArgs p) {
 //   * within a slice, a fragment read for the next slice follows every fourth MFMA and a load
 //     follows every fourth MFMA two later, so no gap between MFMAs holds more than one memory
 //     instruction (bunching them cost 3-8%);
-//   * bands of 4 M-tiles per XCD (8 measured 2% slower at 8192^3, 16 8%).
+//   * bands of 4 M-tiles per XCD for square tile grids (8 measured 2% slower at 8192^3, 16 8%), of
+//     8 N-tiles otherwise (see launch_pp).
 constexpr int kW4Threads = 256;
 
 template <bool OUT_BF16>
@@ -741,12 +745,21 @@ gemm_nt_m16_kernel(GemmArgs p) {
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
     if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-    constexpr int GROUP = 4;
-    const int per_group = GROUP * p.tiles_n;
-    const int first_m = (bid / per_group) * GROUP;
-    const int gsize = min(p.tiles_m - first_m, GROUP);
-    const int tm = first_m + (bid % per_group) % gsize;
-    const int tn = (bid % per_group) / gsize;
+    int tm, tn;
+    if (p.band_n == 0) {
+        constexpr int GROUP = 4;
+        const int per_group = GROUP * p.tiles_n;
+        const int first_m = (bid / per_group) * GROUP;
+        const int gsize = min(p.tiles_m - first_m, GROUP);
+        tm = first_m + (bid % per_group) % gsize;
+        tn = (bid % per_group) / gsize;
+    } else {
+        const int per_group = p.band_n * p.tiles_m;
+        const int first_n = (bid / per_group) * p.band_n;
+        const int gsize = min(p.tiles_n - first_n, p.band_n);
+        tn = first_n + (bid % per_group) % gsize;
+        tm = (bid % per_group) / gsize;
+    }
     const int64_t g = blockIdx.z;
     const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
     const uint16_t* B = weight_slice(p, tm * kPPTile, g);
@@ -881,6 +894,11 @@ void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, hipStream
     p.tiles_n = (p.n + kPPTile - 1) / kPPTile;
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), 1, static_cast<unsigned>(batch));
     if (!a_mn && !b_mn) {
+        // Square tile grids run bands of 4 M-tile rows per XCD; other grids bands of 8 N-tile
+        // columns, so an XCD's L2 holds a narrow slice of B (Llama projections 8192x4096->14336
+        // and 8192x14336->4096: 1.40 -> 1.49 and 1.38 -> 1.47 PFLOP/s; 8192^3 keeps 1.54 with
+        // M bands vs 1.50 with N bands).
+        p.band_n = p.tiles_m == p.tiles_n ? 0 : 8;
         hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16>), grid, dim3(kW4Threads), 0, s, p);
         return;
     }
