@@ -215,7 +215,7 @@ def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
 def gemm_kernel_name(m, n, k, ta, tb):
     """The kernel libhk.so runs for this shape (hk_gemm.hip's selection on 256 CUs)."""
     if ((m + 255) // 256) * ((n + 255) // 256) >= 256 and k % 64 == 0:
-        return "gemm_nt_m16_kernel" if (ta, tb) == (0, 1) else "gemm_nt_pp_kernel"
+        return "gemm_nt_m16_kernel"
     return "gemm_nt_dma_kernel"
 
 

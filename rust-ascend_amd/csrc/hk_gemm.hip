@@ -8,11 +8,10 @@
 //
 // Design (MI355X-first, not a translation of the reference's 64x64 Ascend tiles):
 //   * Large problems (at least one 256x256 tile per CU, K % 64 == 0), every transpose read in
-//     place: both operands K-contiguous ("NT": A [M,K], B [N,K]) -> gemm_nt_m16_kernel, four
-//     wavefronts of 128x128 with 16x16x32 MFMAs and global->LDS loads; an MN-contiguous operand
-//     (A stored [K,M] or B stored [K,N]) -> gemm_nt_pp_kernel, eight wavefronts in two groups
-//     that alternate between MFMA turns and memory turns, MN-major tiles read with transposing
-//     LDS reads.
+//     place -> gemm_nt_m16_kernel: four wavefronts of 128x128 with 16x16x32 MFMAs and
+//     global->LDS loads; a K-contiguous operand (A [M,K], B [N,K]) is staged in 128-byte k-rows
+//     and read with 16-byte LDS reads, an MN-contiguous one (A stored [K,M] or B stored [K,N]) in
+//     512-byte rows of 256 columns and read with transposing LDS reads.
 //   * Smaller problems: MN-contiguous operands are first transposed into the workspace by an
 //     HBM-bound kernel, then a workgroup of 4 wavefronts (2x2) computes a BMxBN output tile (256, 128 or 64
 //     when a larger grid would not fill the 256 CUs). Each wave owns a (BM/2)x(BN/2) block of
@@ -468,34 +467,7 @@ gemm_nt_dma_kernel(GemmArgs p) {
     store_tile<BM, BN, OUT_BF16>(p, acc, tm, tn, g, wm, wn, lr, lk);
 }
 
-// 256x256 output tiles with eight wavefronts in two groups of four that take turns ("ping-pong"):
-// the waves w and w+4 share a SIMD, and while one group issues MFMAs the other moves data (its
-// next operand fragments from LDS into registers, staged tile data from registers into LDS, and
-// the global loads of a later stage), so each SIMD's matrix core is fed by one wave while its
-// partner works the memory pipelines. A workgroup barrier separates the turns.
-//   * Group g (waves 4g..4g+3) computes rows 128g..128g+127 of the tile; wave q of the group
-//     columns 64q..64q+63: 4x2 MFMA tiles of 32x32, 128 accumulators per lane (AGPRs).
-//   * K advances in stages of 64 through two 64 KB LDS slots. A stage row is 64 BF16 = 128 B,
-//     so each global request is a whole 128-byte line (in this access pattern the L2 delivers
-//     26 TB/s to the CUs against 16 TB/s with 64-byte rows). The 16-byte chunks of a row are
-//     XORed with (row/2)%8, so a fragment read (16 consecutive rows at one chunk per 16-lane
-//     group) touches 16 distinct 16-byte bank groups of the 64-bank LDS.
-//   * A stage is consumed in four turns of 32 k (16 MFMAs per wave): group 0 reads the first
-//     half in turn 4s and multiplies it in 4s+1, reads the second half in 4s+2 and multiplies
-//     it in 4s+3; group 1 runs one turn behind. Stage s is read in turns 4s..4s+3 only.
-//   * Either operand may instead be MN-major (A stored [K,M] or B stored [K,N], the layouts of
-//     the backward's dY^T X and dY W): its stage is then 64 k-rows of 256 columns (512-byte rows,
-//     the 64-byte blocks of a row XORed with row%4) and its fragments are read with gfx950's
-//     transposing LDS read (ds_read_b64_tr_b16, two per fragment, eight k-rows per instruction in
-//     two LDS cycles), which yields the same "32 rows x 8 consecutive k per lane" operand as the
-//     K-major 16-byte read. No transpose pass through HBM is needed.
-//   * Tile data travels global -> registers -> LDS: each wave owns eight 1 KB row blocks of a
-//     stage (32 staging registers per lane). In each of its two memory turns of stage s a wave
-//     writes half of its staged stage s+1 into the free slot and reloads those registers with
-//     stage s+2, so the loads are spread evenly over the turns (the vector memory path moves
-//     about 64 bytes per clock per CU, half of what a stage needs at the MFMA rate) and each
-//     has four turns to arrive.
-constexpr int kPPThreads = 512;
+// 256x256-tile stages: 64 k deep, two 64 KB LDS slots (A half, then B half).
 constexpr int kPPTile = 256;
 constexpr int kPK = 64;  // K per stage
 
@@ -503,228 +475,19 @@ __device__ __forceinline__ int swz64(int row, int chunk) {  // element offset in
     return row * kPK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
-// Element offset of (k-row r, column col) in the 64 x 256 stage of an MN-major operand.
-__device__ __forceinline__ int mn_off(int r, int col) { return r * kPPTile + ((((col >> 5) ^ (r & 3))) << 5) + (col & 31); }
-
-template <bool OUT_BF16, bool A_MN, bool B_MN>
-__global__ void __launch_bounds__(kPPThreads, 1)
-gemm_nt_pp_kernel(GemmArgs p) {
-    constexpr int kStage = 2 * kPPTile * kPK;  // A rows 0..255, then B rows 0..255
-    __shared__ __attribute__((aligned(1024))) uint16_t slot0[kStage];
-    __shared__ __attribute__((aligned(1024))) uint16_t slot1[kStage];
-
-    const int tiles = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
-    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-    constexpr int GROUP = 8;
-    const int per_group = GROUP * p.tiles_n;
-    const int first_m = (bid / per_group) * GROUP;
-    const int gsize = min(p.tiles_m - first_m, GROUP);
-    const int tm = first_m + (bid % per_group) % gsize;
-    const int tn = (bid % per_group) / gsize;
-    const int64_t g = blockIdx.z;
-    const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
-    const uint16_t* B = weight_slice(p, tm * kPPTile, g);
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int group = wave >> 2, q = wave & 3;
-    const int lr = lane & 31, lk = lane >> 5;
-
-    // The row offset of every load is in its per-lane offset, which the hardware checks
-    // against the buffer's size (the scalar offset is not checked): rows past M (N) read as
-    // zero; they only feed outputs that are not stored.
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, p.m * p.k * 2,
-                                                                        kBufferConfig);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, p.n * p.k * 2,
-                                                                        kBufferConfig);
-    // Block d (0..7) of this wave is the 8-row block wave + 8d of a stage: blocks 0..31 are A
-    // rows, 32..63 B rows, so blocks 0..3 come from A and 4..7 from B. Lane l owns row l/8,
-    // chunk position l%8 of the block, which holds the global chunk the swizzle puts there (the
-    // block's parity, that of the wave, sets bit 2 of the row's XOR).
-    const int r_in = lane >> 3;
-    const int src_chunk = (lane & 7) ^ ((4 * (wave & 1) + (r_in >> 1)) & 7);
-    const int voff = (r_in * p.k + src_chunk * 8) * 2;
-    // MN-major block d: k-rows 2(wave + 8d) + mn_r of the stage, lane chunk mn_c of the 512-byte
-    // row. The k-row and column both go into the range-checked offset (K * M * 2 < 2^31), so
-    // columns past M (N) in the last k-row read as zero instead of past the buffer.
-    const int mn_r = lane >> 5, mn_c = lane & 31;
-    const int mn_voff_a = ((2 * wave + mn_r) * p.m + tm * kPPTile + mn_c * 8) * 2;
-    const int mn_voff_b = ((2 * wave + mn_r) * p.n + tn * kPPTile + mn_c * 8) * 2;
-    u32x4_t stg[8];
-    auto gload = [&](int kt, int d) __attribute__((always_inline)) {
-        const int blk = wave + 8 * d;
-        if (d < 4) {
-            if constexpr (A_MN)
-                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         ra, mn_voff_a + (kt * kPK + 16 * d) * p.m * 2, 0, 0));
-            else
-                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         ra, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2, 0));
-        } else {
-            if constexpr (B_MN)
-                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         rb, mn_voff_b + (kt * kPK + 16 * (d - 4)) * p.n * 2, 0, 0));
-            else
-                stg[d] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         rb, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2, 0));
-        }
-    };
-    // Element offset of this lane's chunk for block d = 0 (block d adds d * 4096 in both layouts:
-    // eight 128-byte rows or two 512-byte k-rows per block).
-    const int wlane = wave * 8 * kPK + lane * 8;
-    const int mn_row = 2 * wave + mn_r;
-    const int wlane_mn = mn_row * kPPTile + ((((mn_c >> 2) ^ (mn_row & 3))) << 5) + (mn_c & 3) * 8;
-    const int wl_a = A_MN ? wlane_mn : wlane, wl_b = B_MN ? wlane_mn : wlane;
-    auto lwrite = [&](uint16_t* slot, int d) __attribute__((always_inline)) {
-        *reinterpret_cast<u32x4_t*>(slot + (d < 4 ? wl_a : wl_b) + d * 64 * kPK) = stg[d];
-    };
-
-    // Fragments of one half stage (k slices 2h and 2h+1): A fragment i, B fragment j.
-    const int a_row = 128 * group + lr, b_row = kPPTile + 64 * q + lr;
-    // Transposing read of an MN-major fragment: columns col0 .. col0+31 (col0 % 32 == 0), k-rows
-    // k0 .. k0+7 (k0 % 4 == 0). In each 16-lane group, lane i reads 4 columns of k-row k0 + i/4
-    // (and k0 + 4 + i/4); the hardware hands lane i the 4 k values of column i. Since k0 % 4 == 0
-    // the row's XOR term is i/4 for every fragment.
-    const int tr_i = lane & 15;
-    const int tr_lane = (tr_i >> 2) * kPPTile + 16 * ((lane >> 4) & 1) + 4 * (tr_i & 3);
-    auto read_tr = [&](const uint16_t* base, int k0, int blk32) __attribute__((always_inline)) {
-        const uint16_t* at = base + k0 * kPPTile + tr_lane + ((blk32 ^ (tr_i >> 2)) << 5);
-        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at));
-        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at + 4 * kPPTile));
-        typedef short v8i16_t __attribute__((ext_vector_type(8)));
-        const v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        return __builtin_bit_cast(bf16x8_t, v);
-    };
-    bf16x8_t fa[2][4], fb[2][2];
-    auto read = [&](const uint16_t* slot, int h) __attribute__((always_inline)) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int c = 2 * (2 * h + t) + lk;       // K-major: 16-byte chunk of k 8c .. 8c+7
-            const int k0 = 16 * (2 * h + t) + 8 * lk;  // MN-major: the same k as the first k-row
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if constexpr (A_MN) fa[t][i] = read_tr(slot, k0, 4 * group + i);
-                else fa[t][i] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 32 * i, c));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if constexpr (B_MN) fb[t][j] = read_tr(slot + kPPTile * kPK, k0, 2 * q + j);
-                else fb[t][j] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 32 * j, c));
-            }
-        }
-    };
-
-    f32x16_t acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-    // The accumulators live in the AGPR file, the fragments and staging data in VGPRs.
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) asm volatile("" : "+a"(acc[i][j]));
-
-    auto compute = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(fa[t][i]));
-#pragma unroll
-            for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(fb[t][j]));
-        }
-        phase_fence();
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t][j], fa[t][i], acc[i][j], 0, 0, 0);
-        phase_fence();
-    };
-
-    // Memory turn h of stage s (slot R; the other slot W is free from turn 4s on): staged
-    // blocks 4h..4h+3 of stage s+1 go to W, those registers are reloaded with stage s+2, and
-    // the fragments of half h of stage s are read. Near the end the loads repeat the last
-    // stage and the writes land in a slot that is no longer read: every turn issues the same
-    // loads, so the compiler's wait counts stay those of the steady state (a wave's loads of
-    // the other half, issued two turns later, may remain in flight).
-    const int nk = p.k / kPK;
-    auto memory_turn = [&](const uint16_t* R, uint16_t* W, int s, int h) __attribute__((always_inline)) {
-#pragma unroll
-        for (int d = 4 * h; d < 4 * h + 4; ++d) lwrite(W, d);
-        const int ahead = s + 2 < nk ? s + 2 : nk - 1;
-#pragma unroll
-        for (int d = 4 * h; d < 4 * h + 4; ++d) gload(ahead, d);
-        read(R, h);
-    };
-    auto stage = [&](const uint16_t* R, uint16_t* W, int s) __attribute__((always_inline)) {
-        stage_barrier<63>();
-        memory_turn(R, W, s, 0);
-        stage_barrier<63>();
-        compute();
-        stage_barrier<63>();
-        memory_turn(R, W, s, 1);
-        stage_barrier<63>();
-        compute();
-    };
-
-    // Prologue: stage 0 into slot 0, stage 1 into the staging registers.
-#pragma unroll
-    for (int d = 0; d < 8; ++d) gload(0, d);
-#pragma unroll
-    for (int d = 0; d < 8; ++d) lwrite(slot0, d);
-#pragma unroll
-    for (int d = 0; d < 8; ++d) gload(nk > 1 ? 1 : 0, d);
-    if (group == 1) stage_barrier<63>();  // turn 0: group 1 has nothing to multiply yet
-    int s = 0;
-    do {
-        stage(slot0, slot1, s);
-        if (s + 1 < nk) stage(slot1, slot0, s + 1);
-        s += 2;
-    } while (s < nk);
-    if (group == 0) stage_barrier<63>();  // the turn in which group 1 multiplies the last half stage
-
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = tm * kPPTile + 128 * group + 32 * i + lr;
-        if (m >= p.m) continue;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int grp = 0; grp < 4; ++grp) {
-                const int n = tn * kPPTile + 64 * q + 32 * j + grp * 8 + lk * 4;
-                if (n >= p.n) continue;
-                const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
-                if constexpr (OUT_BF16) {
-                    u32x2_t w = {pack_bf16x2(acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1]),
-                                 pack_bf16x2(acc[i][j][grp * 4 + 2], acc[i][j][grp * 4 + 3])};
-                    *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = w;
-                } else {
-                    f32x4_t w = {acc[i][j][grp * 4 + 0], acc[i][j][grp * 4 + 1], acc[i][j][grp * 4 + 2],
-                                 acc[i][j][grp * 4 + 3]};
-                    *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.c) + off) = w;
-                }
-            }
-        }
-    }
-}
 
 // 256x256 output tiles with four wavefronts, one per SIMD, each owning a 128x128 block of 8x8
 // v_mfma_f32_16x16x32_bf16 tiles (4 accumulators per lane each: the whole AGPR file). Measured
-// against the ping-pong kernel at 8192^3 on N(0,1) data, this runs ~15% faster:
+// against an 8-wave "ping-pong" design (two groups of four waves alternating MFMA turns and
+// memory turns, 32x32x16 MFMAs) at 8192^3 on N(0,1) data, this runs ~15% faster:
 //   * one wave per SIMD interleaves its own memory instructions between its MFMAs, and a 128x128
 //     block reads 0.5 KB of LDS operands per 32x32x16-equivalent MFMA instead of 0.75 KB;
 //   * the 16x16x32 shape moves fewer register-file bytes per multiply-accumulate than 32x32x16
 //     (4 accumulator registers per lane per MFMA instead of 16), and this part is power-limited:
 //     the clock it sustains depends on the work per flop;
 //   * tiles travel straight from global memory into LDS (buffer_load ... lds; no staging
-//     registers, no LDS write instructions). K stages of 64 use the ping-pong kernel's two 64 KB
-//     slots and 128-byte swizzled rows. A stage is two k-slices of 32 (64 MFMAs each) with one
+//     registers, no LDS write instructions). K stages of 64 in two 64 KB slots, 128-byte
+//     swizzled rows (full 128-byte lines per global request). A stage is two k-slices of 32 (64 MFMAs each) with one
 //     barrier between them; all of stage s+2 is fetched during slice 1 of stage s into the slot
 //     that barrier has just freed, so every load has one to two slices to land before the
 //     barrier that needs it (issuing the same loads half a stage later cost ~10%);
@@ -732,10 +495,18 @@ gemm_nt_pp_kernel(GemmArgs p) {
 //     follows every fourth MFMA two later, so no gap between MFMAs holds more than one memory
 //     instruction (bunching them cost 3-8%);
 //   * bands of 4 M-tiles per XCD for square tile grids (8 measured 2% slower at 8192^3, 16 8%), of
-//     8 N-tiles otherwise (see launch_pp).
+//     8 N-tiles otherwise (see launch_pp);
+//   * an MN-major operand (the backward's dY W and dY^T X) is read in place: its half of a stage
+//     is 64 k-rows of 256 columns (512-byte rows, 64-byte blocks XORed with k-row % 4) filled by
+//     the same 1 KB global->LDS loads (two k-rows each), and each fragment is two
+//     ds_read_b64_tr_b16 transposing reads, which hand every lane the 8 consecutive k of its
+//     column that the K-major 16-byte read gives. The four 16-lane groups read the same 16
+//     columns at k-rows 8 apart, so two groups share banks (a 2-way conflict: ~128 LDS cycles
+//     per 1024-cycle slice). 8192^3 NN/TN/TT: 1.48-1.51 PFLOP/s, against 1.30 for the 8-wave
+//     ping-pong design with register-staged loads and transposing reads that this replaced.
 constexpr int kW4Threads = 256;
 
-template <bool OUT_BF16>
+template <bool OUT_BF16, bool A_MN, bool B_MN>
 __global__ void __launch_bounds__(kW4Threads, 1)
 gemm_nt_m16_kernel(GemmArgs p) {
     constexpr int kStage = 2 * kPPTile * kPK;
@@ -773,20 +544,54 @@ gemm_nt_m16_kernel(GemmArgs p) {
     const int src_chunk = (lane & 7) ^ ((4 * (wave & 1) + (r_in >> 1)) & 7);
     const int voff = (r_in * p.k + src_chunk * 8) * 2;
     const i32x4_t ra4 = buffer_resource(A, p.m * p.k * 2), rb4 = buffer_resource(B, p.n * p.k * 2);
+    // MN-major operand (A stored [K,M] or B stored [K,N]): its half of a stage is 64 k-rows x 256
+    // columns, 512-byte rows whose 64-byte blocks are XORed with k-row % 4. Load d of a wave fills
+    // k-rows 2(wave + 4d) + {0, 1}; lane l takes position l % 32 of k-row l / 32, which holds the
+    // global chunk the swizzle puts there (k-row % 4 is the same for every d). The k-row and column
+    // are in the range-checked offset (K * M * 2 < 2^31): columns past M (N) in the last k-row read
+    // as zero, elsewhere they feed only outputs that are not stored.
+    const int mn_row0 = 2 * wave + (lane >> 5), mn_pos = lane & 31;
+    const int mn_c = (((mn_pos >> 2) ^ (mn_row0 & 3)) << 2) | (mn_pos & 3);
+    const int mn_voff_a = (mn_row0 * p.m + tm * kPPTile + mn_c * 8) * 2;
+    const int mn_voff_b = (mn_row0 * p.n + tn * kPPTile + mn_c * 8) * 2;
     const uint32_t lds0 = lds_address(slot0), lds1 = lds_address(slot1);
     auto dload = [&](uint32_t lds_slot, int kt, int d) __attribute__((always_inline)) {
         const int blk = wave + 4 * d;
         const uint32_t dst = lds_slot + (wave * 8 * kPK + d * 4 * 8 * kPK) * 2;
-        if (d < 8) load_lds16(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2);
-        else load_lds16(rb4, dst, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2);
+        if (d < 8) {
+            if constexpr (A_MN) load_lds16(ra4, dst, mn_voff_a + (kt * kPK + 8 * d) * p.m * 2, 0);
+            else load_lds16(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2);
+        } else {
+            if constexpr (B_MN) load_lds16(rb4, dst, mn_voff_b + (kt * kPK + 8 * (d - 8)) * p.n * 2, 0);
+            else load_lds16(rb4, dst, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2);
+        }
     };
 
     const int a_row = 128 * wm + l16, b_row = kPPTile + 128 * wn + l16;
+    // Transposing read of an MN-major 16x16x32 operand: columns col0 .. col0+15 (col0 % 16 == 0),
+    // k-rows k0 .. k0+7 with k0 = 32 ks + 8 lg (each 16-lane group its own k0; k0 % 4 == 0, so the
+    // k-row's XOR term is i/4). Lane i of a group reads 4 columns of k-row k0 + i/4 (then k0 + 4 +
+    // i/4), and the hardware hands lane i the 4 k values of column col0 + i.
+    const int tr_i = lane & 15;
+    const int tr_lane = (tr_i >> 2) * kPPTile + 4 * (tr_i & 3);
+    auto read_tr = [&](const uint16_t* stage, int k0, int col0) __attribute__((always_inline)) {
+        const uint16_t* at = stage + k0 * kPPTile + tr_lane + ((((col0 >> 5) ^ (tr_i >> 2)) << 5) | (col0 & 31));
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at));
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at + 4 * kPPTile));
+        typedef short v8i16_t __attribute__((ext_vector_type(8)));
+        const v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(bf16x8_t, v);
+    };
     bf16x8_t fa[2][8], fb[2][8];
     auto read1 = [&](const uint16_t* slot, int ks, int buf, int f) __attribute__((always_inline)) {
         const int c = 4 * ks + lg;
-        if (f < 8) fa[buf][f] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 16 * f, c));
-        else fb[buf][f - 8] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 16 * (f - 8), c));
+        if (f < 8) {
+            if constexpr (A_MN) fa[buf][f] = read_tr(slot, 8 * c, 128 * wm + 16 * f);
+            else fa[buf][f] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 16 * f, c));
+        } else {
+            if constexpr (B_MN) fb[buf][f - 8] = read_tr(slot + kPPTile * kPK, 8 * c, 128 * wn + 16 * (f - 8));
+            else fb[buf][f - 8] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 16 * (f - 8), c));
+        }
     };
 
     f32x4_t acc[8][8];
@@ -878,9 +683,8 @@ transpose_bf16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int6
     }
 }
 
-// The 256x256-tile kernels (both operands K-major: the 4-wave kernel; an MN-major operand: the
-// ping-pong kernel) apply when there are enough tiles to fill the GPU, whole 64-deep stages and
-// 32-bit byte offsets.
+// The 256x256-tile 4-wave kernel (every transpose) applies when there are enough tiles to fill
+// the GPU, whole 64-deep stages and 32-bit byte offsets.
 bool pp_applies(int64_t batch, int64_t m, int64_t n, int64_t k, int num_cus) {
     const int64_t tiles = ((m + kPPTile - 1) / kPPTile) * ((n + kPPTile - 1) / kPPTile) * batch;
     return tiles >= num_cus && k > 0 && k % kPK == 0 && m * k * 2 < (int64_t{1} << 31) &&
@@ -893,19 +697,15 @@ void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, hipStream
     p.tiles_m = (p.m + kPPTile - 1) / kPPTile;
     p.tiles_n = (p.n + kPPTile - 1) / kPPTile;
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), 1, static_cast<unsigned>(batch));
-    if (!a_mn && !b_mn) {
-        // Square tile grids run bands of 4 M-tile rows per XCD; other grids bands of 8 N-tile
-        // columns, so an XCD's L2 holds a narrow slice of B (Llama projections 8192x4096->14336
-        // and 8192x14336->4096: 1.40 -> 1.49 and 1.38 -> 1.47 PFLOP/s; 8192^3 keeps 1.54 with
-        // M bands vs 1.50 with N bands).
-        p.band_n = p.tiles_m == p.tiles_n ? 0 : 8;
-        hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16>), grid, dim3(kW4Threads), 0, s, p);
-        return;
-    }
-    if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, true, true>), grid, dim3(kPPThreads), 0, s, p);
-    else if (a_mn) hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, true, false>), grid, dim3(kPPThreads), 0, s, p);
-    else if (b_mn) hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, false, true>), grid, dim3(kPPThreads), 0, s, p);
-    else hipLaunchKernelGGL((gemm_nt_pp_kernel<OUT_BF16, false, false>), grid, dim3(kPPThreads), 0, s, p);
+    // Square tile grids run bands of 4 M-tile rows per XCD; other grids bands of 8 N-tile
+    // columns, so an XCD's L2 holds a narrow slice of B (Llama projections 8192x4096->14336
+    // and 8192x14336->4096: 1.40 -> 1.49 and 1.38 -> 1.47 PFLOP/s; 8192^3 keeps 1.54 with
+    // M bands vs 1.50 with N bands).
+    p.band_n = p.tiles_m == p.tiles_n ? 0 : 8;
+    if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, true>), grid, dim3(kW4Threads), 0, s, p);
+    else if (a_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, false>), grid, dim3(kW4Threads), 0, s, p);
+    else if (b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, true>), grid, dim3(kW4Threads), 0, s, p);
+    else hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, false>), grid, dim3(kW4Threads), 0, s, p);
 }
 
 template <int BM, int BN>
