@@ -191,8 +191,14 @@ def cpu_baseline_c2(threads):
 
 
 def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
+    """Average GPU time of one GEMM over `iters` back-to-back calls of the C ABI (descriptors
+    built once, as a native caller's would be), between one pair of events on the stream the
+    kernels run on. Timing each call with its own event pair around the Python-level call would
+    add the host's per-call work to small GEMMs (C1's 7 us kernel measured 16.6 us that way)."""
+    import ctypes
     import torch
-    from rust_ascend_hip import HipRuntime, Transpose
+    from rust_ascend_hip import HipRuntime, Transpose, _lib, runtime
+    from rust_ascend_hip._lib import check
     out = out or torch.bfloat16
     g = torch.Generator(device="cuda")
     g.manual_seed(m + n + k)
@@ -201,15 +207,21 @@ def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
     c = torch.empty((m, n), device="cuda", dtype=out)
     for _ in range(warmup):
         HipRuntime.gemm_into(a, b, Transpose(ta), Transpose(tb), c)
-    warm(lambda: HipRuntime.gemm_into(a, b, Transpose(ta), Transpose(tb), c))
-    pairs = []
-    for _ in range(iters):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        HipRuntime.gemm_into(a, b, Transpose(ta), Transpose(tb), c)
-        e1.record()
-        pairs.append((e0, e1))
-    return event_ms(pairs)
+    lib, ctx = _lib.load(), runtime._context()
+    check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    d_a, d_b, d_c = runtime.desc(a), runtime.desc(b), runtime.desc(c)
+
+    def call():
+        check(lib.hk_gemm_into(ctx, d_a, d_b, int(ta), int(tb), d_c))
+
+    warm(call)
+    reps = max(iters, int(2e-3 / max(2 * m * n * k / 1.5e15, 1e-6)))  # >= ~2 ms of work
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    return event_ms([(e0, e1)]) / reps
 
 
 def gemm_kernel_name(m, n, k, ta, tb):

@@ -318,6 +318,31 @@ hk_status hk_embedding(hk_context* ctx, const hk_tensor* weight, const hk_tensor
 hk_status hk_embedding_backward(hk_context* ctx, const hk_tensor* grad, const hk_tensor* ids, uint64_t num_weights,
                                 uint64_t padding_idx, int32_t scale_grad_by_freq, hk_tensor* dweight);
 
+/* ---------------------------------------------------------------- NLLLoss */
+
+/* Reference: LossReduction {None=0, Mean=1, Sum=2}, rust-ascend-driver/src/tensor/loss.rs:3-6. */
+typedef enum hk_loss_reduction { HK_LOSS_NONE = 0, HK_LOSS_MEAN = 1, HK_LOSS_SUM = 2 } hk_loss_reduction;
+
+/* NLLLoss over log-probabilities input [N,C] (F32/F16/BF16) with INT32/INT64 labels target [N]
+ * and class weights weight [C] (input's dtype). Row loss l_n = -weight[t_n] input[n,t_n]; a row
+ * whose label equals ignore_index contributes nothing (pass NllLossOptions::ignore(): the ignore
+ * label, or -1 when none is set, loss.rs:10-12). out: [N] (None) or [1] = sum (Sum) or sum / W
+ * (Mean); total_weight [1] = W, the summed weight of the non-ignored labels (Sum, Mean; 0 for None).
+ * A label outside [0, C) that is not ignore_index contributes nothing and, in synchronous mode,
+ * returns HK_INVALID_ARGUMENT after the call. Sums over rows are deterministic.
+ * Reference: AscendRuntime::nll_loss, runtime/mod.rs:227-228 (runtime/loss.rs:15-20,
+ * CannSession::nll_loss, tensor/loss.rs:31-46, aclnnNLLLoss). */
+hk_status hk_nll_loss(hk_context* ctx, const hk_tensor* input, const hk_tensor* target,
+                      const hk_tensor* weight, int32_t reduction, int64_t ignore_index,
+                      hk_tensor* out, hk_tensor* total_weight);
+/* Dense dinput [N,C]: -weight[t_n] g_n at (n, t_n), zero elsewhere, g_n = grad[n] (None),
+ * grad[0] (Sum) or grad[0] / total_weight (Mean). Reference: AscendRuntime::nll_loss_backward,
+ * runtime/mod.rs:233-236 (tensor/loss.rs:47-60, aclnnNLLLossBackward). */
+hk_status hk_nll_loss_backward(hk_context* ctx, const hk_tensor* grad, const hk_tensor* input,
+                               const hk_tensor* target, const hk_tensor* weight,
+                               const hk_tensor* total_weight, int32_t reduction,
+                               int64_t ignore_index, hk_tensor* dinput);
+
 /* ---------------------------------------------------------------- composed-attention shims */
 
 /* The fused attention entry points apply the mask and the KV-head mapping themselves; these

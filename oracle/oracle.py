@@ -42,6 +42,11 @@ a wrong sign or index, or a transposed operand fails at least one check:
   per-row shift, and torch float64 autograd (the backward must be the forward's
   vector-Jacobian product) on the reference's own inputs and shapes
   (examples/common_rows_validate.rs:7-9,100).
+* ``nll_loss_f64``/``nll_loss_backward_f64``: torch float64 ``nll_loss`` and ``cross_entropy`` (an
+  independent implementation of the same semantics, with autograd for the backward) for all three
+  reductions, with and without class weights and an ignore label, on the reference's inputs of
+  examples/cross_entropy_tensor.rs:19-24; the direct known answer of :55-59 (19/4); a Mean over
+  only ignored rows is 0/0 = NaN.
 * ``silu_mul_f64``/``silu_mul_backward_f64``: torch float64 autograd of
   torch.nn.functional.silu(g) * u (an independent implementation; the backward must be its
   vector-Jacobian product), known answers at g = 0 (y = 0, dgate = dy*u/2, dup = 0) and for
@@ -361,6 +366,44 @@ def softmax_backward_f64(y, dy, logarithmic: bool = False) -> np.ndarray:
     width = y.shape[-1]
     out = np.empty(y.shape, np.float64)
     lib().or_softmax_backward_f64(y, dy, y.size // width if width else 0, width, int(logarithmic), out)
+    return out
+
+
+def nll_loss_f64(logp, target, weight, reduction: int, ignore_index: int):
+    """NLLLoss in float64: row loss -w[t] * logp[n, t], 0 for rows labelled ignore_index;
+    reduction 0 None ([N]), 1 Mean (sum / W), 2 Sum; returns (loss, W) with W the summed weight of
+    the non-ignored labels. Restates the expectation loop of examples/cross_entropy_tensor.rs:38-52
+    (the reference's NLLLoss itself is the closed aclnnNLLLoss, tensor/loss.rs:31-46)."""
+    logp = np.asarray(logp, np.float64)
+    w = np.asarray(weight, np.float64)
+    t = np.asarray(target, np.int64)
+    rows = np.zeros(t.shape[0], np.float64)
+    total = 0.0
+    for n, label in enumerate(t):
+        if label == ignore_index:
+            continue
+        rows[n] = -w[label] * logp[n, label]
+        total += w[label]
+    if reduction == 0:
+        return rows, total
+    s = rows.sum()
+    if reduction == 1:
+        return np.array([s / total if total != 0 else np.nan]), total
+    return np.array([s]), total
+
+
+def nll_loss_backward_f64(grad, shape, target, weight, total, reduction: int, ignore_index: int) -> np.ndarray:
+    """Dense d loss / d logp in float64: -w[t_n] g_n at (n, t_n), g_n = grad[n] (None), grad[0]
+    (Sum), grad[0] / total (Mean) (the derivative of nll_loss_f64; cross_entropy_tensor.rs:48-50
+    for the composed cross entropy)."""
+    g = np.asarray(grad, np.float64)
+    w = np.asarray(weight, np.float64)
+    out = np.zeros(shape, np.float64)
+    for n, label in enumerate(np.asarray(target, np.int64)):
+        if label == ignore_index:
+            continue
+        gn = g[n] if reduction == 0 else (g[0] / total if reduction == 1 else g[0])
+        out[n, label] = -w[label] * gn
     return out
 
 

@@ -1207,6 +1207,76 @@ static hk_status ids_in_range(Ctx* c, hk_status st, int64_t vocab) {
 }
 }  // namespace
 
+// ------------------------------------------------------------------ NLLLoss
+
+namespace {
+int float_code(int32_t dt) { return dt == HK_F32 ? 0 : (dt == HK_F16 ? 1 : 2); }
+
+// Reference: forward_layouts, rust-ascend-driver/src/tensor/loss.rs:17-27.
+hk_status nll_layouts(const hk_tensor* input, const hk_tensor* target, const hk_tensor* weight, int32_t reduction) {
+    if (!tensor_ok(input, "input") || !tensor_ok(weight, "weight") || !tensor_ok(target, "target", true))
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss requires floating input[N,C], matching integer target[N] and same-dtype class weight[C]");
+    if (input->rank != 2 || input->shape[1] <= 0 || target->rank != 1 || target->shape[0] != input->shape[0] ||
+        weight->rank != 1 || weight->shape[0] != input->shape[1] || weight->dtype != input->dtype)
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss requires floating input[N,C], matching integer target[N] and same-dtype class weight[C]");
+    if (reduction < HK_LOSS_NONE || reduction > HK_LOSS_SUM)
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss reduction must be None (0), Mean (1) or Sum (2)");
+    return HK_OK;
+}
+bool nll_out_ok(const hk_tensor* t, int64_t len, int32_t dtype) {
+    return t && t->dtype == dtype && t->rank == 1 && t->shape[0] == len && (len == 0 || t->data);
+}
+}  // namespace
+
+hk_status hk_nll_loss(hk_context* h, const hk_tensor* input, const hk_tensor* target, const hk_tensor* weight,
+                      int32_t reduction, int64_t ignore_index, hk_tensor* out, hk_tensor* total_weight) {
+    // Reference: CannSession::nll_loss, tensor/loss.rs:31-46 (runtime/loss.rs:15-20).
+    hk_status st = nll_layouts(input, target, weight, reduction);
+    if (st != HK_OK) return st;
+    const int64_t rows = input->shape[0], classes = input->shape[1];
+    if (!nll_out_ok(out, reduction == HK_LOSS_NONE ? rows : 1, input->dtype) || !nll_out_ok(total_weight, 1, input->dtype))
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss output must be [N] (None) or [1], total weight [1], in the input's dtype");
+    if (!disjoint({out, total_weight}, {input, target, weight})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, 256)) != HK_OK) return st;
+    hipError_t e = hk::nll_loss(float_code(input->dtype), target->dtype == HK_I64 ? 8 : 4, input->data, target->data,
+                                weight->data, out->data, total_weight->data, rows, classes, reduction, ignore_index,
+                                static_cast<int*>(g.c->workspace), g.c->stream);
+    st = complete(g.c, e, "nll_loss", 1);
+    if (st != HK_OK || g.c->async) return st;
+    int flag = 0;
+    if (hipMemcpy(&flag, g.c->workspace, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) {
+        g.c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "nll_loss: reading the label check failed");
+    }
+    if (flag)
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss target outside [0, %lld) that is not the ignore index %lld",
+                    static_cast<long long>(classes), static_cast<long long>(ignore_index));
+    return HK_OK;
+}
+
+hk_status hk_nll_loss_backward(hk_context* h, const hk_tensor* grad, const hk_tensor* input, const hk_tensor* target,
+                               const hk_tensor* weight, const hk_tensor* total_weight, int32_t reduction,
+                               int64_t ignore_index, hk_tensor* dinput) {
+    // Reference: CannSession::nll_loss_backward, tensor/loss.rs:47-60 (backward_layout, :28-36).
+    hk_status st = nll_layouts(input, target, weight, reduction);
+    if (st != HK_OK) return st;
+    const int64_t rows = input->shape[0], classes = input->shape[1];
+    if (!nll_out_ok(grad, reduction == HK_LOSS_NONE ? rows : 1, input->dtype) ||
+        !nll_out_ok(total_weight, 1, input->dtype))
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss upstream gradient or saved total weight does not match forward reduction/dtype");
+    if (!tensor_ok(dinput, "dinput") || dinput->dtype != input->dtype || !same_shape(dinput, input))
+        return fail(HK_INVALID_ARGUMENT, "NLLLoss input gradient must match the input");
+    if (!disjoint({dinput}, {grad, input, target, weight, total_weight})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::nll_loss_backward(float_code(input->dtype), target->dtype == HK_I64 ? 8 : 4, grad->data,
+                                         target->data, weight->data, total_weight->data, dinput->data, rows, classes,
+                                         reduction, ignore_index, g.c->stream);
+    return complete(g.c, e, "nll_loss_backward", 1);
+}
+
 hk_status hk_embedding(hk_context* h, const hk_tensor* weight, const hk_tensor* ids, hk_tensor* out) {
     // Reference: runtime/indexing.rs:33-37, embedding.rs:27-34 (forward_layout) and :46-60.
     int64_t tokens;

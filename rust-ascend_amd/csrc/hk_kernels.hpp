@@ -43,6 +43,16 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
 hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_bf16, int64_t m, int64_t n,
                                 int64_t k, const int32_t* block_group, int num_cus, hipStream_t s);
 
+// ---- NLLLoss (hk_loss.hip)
+// dtype 0 F32, 1 F16, 2 BF16 (input, weight, out, total, grad, dinput); id_bytes 4 or 8;
+// reduction 0 None, 1 Mean, 2 Sum. The forward writes *bad = 1 if a label outside [0, classes)
+// that is not `ignore` occurs.
+hipError_t nll_loss(int dtype, int id_bytes, const void* input, const void* target, const void* weight, void* out,
+                    void* total, int64_t rows, int64_t classes, int reduction, int64_t ignore, int* bad, hipStream_t s);
+hipError_t nll_loss_backward(int dtype, int id_bytes, const void* grad, const void* target, const void* weight,
+                             const void* total, void* dinput, int64_t rows, int64_t classes, int reduction,
+                             int64_t ignore, hipStream_t s);
+
 // ---- matrix tails (hk_pad.hip)
 // dst [batch, R, C] BF16 = src [batch, rows, cols] (F32 rounded to BF16 with RNE, or BF16 copied)
 // zero-padded (rows <= R, cols <= C, C even).

@@ -94,6 +94,8 @@ SIGNATURES = {
     "hk_silu_mul_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_bias_add": [_CTX, _T, _T, _T, _T],
     "hk_bias_add_backward": [_CTX, _T, _T],
+    "hk_nll_loss": [_CTX, _T, _T, _T, _i32, ctypes.c_int64, _T, _T],
+    "hk_nll_loss_backward": [_CTX, _T, _T, _T, _T, _T, _i32, ctypes.c_int64, _T],
     "hk_embedding": [_CTX, _T, _T, _T],
     "hk_embedding_backward": [_CTX, _T, _T, _u64, _u64, _i32, _T],
     "hk_qkv_rope_split": [_CTX, _T, _T, _T, _i32, _T, _T, _T],

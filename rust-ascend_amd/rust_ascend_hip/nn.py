@@ -14,7 +14,7 @@ from __future__ import annotations
 
 import torch
 
-from .runtime import HipRuntime, RotaryLayout, Transpose
+from .runtime import HipRuntime, LossReduction, RotaryLayout, Transpose
 
 
 class _LinearBf16Fp32(torch.autograd.Function):
@@ -313,3 +313,46 @@ def causal_grouped_query_attention_bf16(q, k, v, scale: float, query_start: int 
     nn::causal_grouped_query_attention_bf16_fp32 (src/nn/attention.rs:68-80)."""
     return _Attention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale), True, int(query_start),
                             int(key_start))
+
+
+class _NllLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, input, target, weight, reduction, ignore_index):
+        out, total, t, w = HipRuntime.nll_loss_with_saved_inputs(input.contiguous(), target.contiguous(),
+                                                                 weight.contiguous(), reduction, ignore_index)
+        ctx.save_for_backward(input, t, w, total)
+        ctx.reduction, ctx.ignore_index = reduction, ignore_index
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        input, t, w, total = ctx.saved_tensors
+        dx = HipRuntime.nll_loss_backward(grad.contiguous().to(input.dtype), input, t, w, total, ctx.reduction,
+                                          ctx.ignore_index)
+        return dx, None, None, None, None
+
+
+def nll_loss(input, target, weight, reduction=LossReduction.Mean, ignore_index=None):
+    """NLLLoss of log-probabilities input [N, C] with fixed class weights (no gradient for the
+    weights or labels). Returns [N] (None) or [1]. Reference: nn::nll_loss and NllBackward
+    (src/nn/loss.rs:34-41, 88-132): the backward saves the input, label and weight snapshots and
+    the forward's total weight."""
+    return _NllLoss.apply(input, target, weight, LossReduction(reduction), ignore_index)
+
+
+def weighted_cross_entropy(logits, target, weight, reduction=LossReduction.Mean, ignore_index=None):
+    """nll_loss(log_softmax(logits)) with fixed class weights: F32 logits [N, C], integer labels [N],
+    F32 weights [C]. Reference: nn::weighted_cross_entropy (src/nn/loss.rs:52-64)."""
+    if logits.dim() != 2 or logits.dtype != torch.float32 or weight.dtype != torch.float32 or \
+            target.dtype not in (torch.int32, torch.int64) or tuple(target.shape) != (logits.shape[0],) or \
+            tuple(weight.shape) != (logits.shape[1],):
+        from ._lib import INVALID_ARGUMENT, HkError
+        raise HkError(INVALID_ARGUMENT, "cross entropy requires same-device FP32 logits[N,C], integer labels[N] "
+                                        "and FP32 weights[C]")
+    return nll_loss(log_softmax(logits), target, weight, reduction, ignore_index)
+
+
+def cross_entropy(logits, target, reduction=LossReduction.Mean, ignore_index=None):
+    """Unweighted cross entropy (class weights of one). Reference: nn::cross_entropy (src/nn/loss.rs:42-50)."""
+    weight = torch.ones((logits.shape[1],), dtype=torch.float32, device=logits.device)
+    return weighted_cross_entropy(logits, target, weight, reduction, ignore_index)

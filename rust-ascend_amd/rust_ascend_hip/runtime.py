@@ -25,6 +25,18 @@ class Transpose(enum.IntEnum):
     Yes = 1
 
 
+class LossReduction(enum.IntEnum):
+    """Reference: LossReduction (rust-ascend-driver/src/tensor/loss.rs:3-6)."""
+    None_ = 0
+    Mean = 1
+    Sum = 2
+
+
+def _ignore(ignore_index):
+    """NllLossOptions::ignore (tensor/loss.rs:10-12): the explicit ignore label, else -1."""
+    return -1 if ignore_index is None else int(ignore_index)
+
+
 class RotaryLayout(enum.IntEnum):
     """Reference: RotaryLayout (rust-ascend-compiler/src/ascend/rotary_programs.rs:5-6)."""
     Interleaved = 0
@@ -394,6 +406,37 @@ class HipRuntime:
         return db
 
     # ---------------------------------------------------------------- embedding
+
+    @staticmethod
+    def nll_loss(input, target, weight, reduction=LossReduction.Mean, ignore_index=None):
+        """[loss, total weight] from log-probabilities input [N, C], labels target [N] and class
+        weights weight [C]; loss is [N] for None, [1] otherwise. Reference: AscendRuntime::nll_loss
+        (mod.rs:226-228)."""
+        red = LossReduction(reduction)
+        rows = input.shape[0] if input.dim() == 2 else 0
+        out = _empty((rows if red == LossReduction.None_ else 1,), input.dtype, input)
+        total = _empty((1,), input.dtype, input)
+        _call("hk_nll_loss", desc(input), desc(target), desc(weight), int(red), _ignore(ignore_index), desc(out),
+              desc(total))
+        return out, total
+
+    @staticmethod
+    def nll_loss_with_saved_inputs(input, target, weight, reduction=LossReduction.Mean, ignore_index=None):
+        """[loss, total weight, saved labels, saved weights]: the forward plus independent device
+        copies of the labels and weights. Reference: AscendRuntime::nll_loss_with_saved_inputs
+        (mod.rs:229-231, runtime/loss.rs:21-26)."""
+        t, w = target.clone(), weight.clone()
+        out, total = HipRuntime.nll_loss(input, t, w, reduction, ignore_index)
+        return out, total, t, w
+
+    @staticmethod
+    def nll_loss_backward(grad, input, target, weight, total_weight, reduction=LossReduction.Mean, ignore_index=None):
+        """Dense derivative with respect to the log-probabilities. Reference:
+        AscendRuntime::nll_loss_backward (mod.rs:232-236)."""
+        dx = _empty(input.shape, input.dtype, input)
+        _call("hk_nll_loss_backward", desc(grad), desc(input), desc(target), desc(weight), desc(total_weight),
+              int(LossReduction(reduction)), _ignore(ignore_index), desc(dx))
+        return dx
 
     @staticmethod
     def embedding(weight, ids):

@@ -157,6 +157,43 @@ def test_padded_gemm_contract():
                                                           fake(F32, (3, 35), 1 << 34)) == _lib.INVALID_ARGUMENT
 
 
+def test_nll_loss_contract():
+    # tensor/loss.rs:64-99: layouts for every dtype, label width and reduction; invalid labels,
+    # weights and upstream layouts are rejected before any device work
+    from rust_ascend_hip._lib import I32, I64
+    lib = _lib.load()
+
+    def fwd(x, t, w, red, out, tot):
+        return lib.hk_nll_loss(None, fake(*x, 1 << 20), fake(*t, 1 << 24), fake(*w, 1 << 26), red, -100,
+                               fake(*out, 1 << 28), fake(*tot, 1 << 30))
+
+    for dt in (F32, F16, BF16):
+        for it in (I32, I64):
+            for rows in (0, 3):
+                for red in (0, 1, 2):
+                    n_out = rows if red == 0 else 1
+                    assert fwd((dt, (rows, 65)), (it, (rows,)), (dt, (65,)), red, (dt, (n_out,)),
+                               (dt, (1,))) == _lib.NOT_INITIALIZED, (dt, it, rows, red)
+    ok = ((F32, (3, 65)), (I64, (3,)), (F32, (65,)), 1, (F32, (1,)), (F32, (1,)))
+    assert fwd(*ok) == _lib.NOT_INITIALIZED
+    bad = [((F32, (3, 65)), (F32, (3,)), (F32, (65,))), ((F32, (3, 65)), (I64, (3, 1)), (F32, (65,))),
+           ((F32, (3, 65)), (I64, (3,)), (F32, (64,))), ((F32, (3, 65)), (I64, (3,)), (BF16, (65,))),
+           ((F32, (3, 0)), (I64, (3,)), (F32, (0,)))]
+    for x, t, w in bad:
+        assert fwd(x, t, w, 1, (F32, (1,)), (F32, (1,))) == _lib.INVALID_ARGUMENT, (x, t, w)
+    assert fwd((F32, (3, 65)), (I64, (3,)), (F32, (65,)), 3, (F32, (1,)), (F32, (1,))) == _lib.INVALID_ARGUMENT
+    assert fwd((F32, (3, 65)), (I64, (3,)), (F32, (65,)), 0, (F32, (1,)), (F32, (1,))) == _lib.INVALID_ARGUMENT
+
+    def bwd(g, tot, red=1):
+        return lib.hk_nll_loss_backward(None, fake(*g, 1 << 32), fake(F32, (3, 65), 1 << 20), fake(I64, (3,), 1 << 24),
+                                        fake(F32, (65,), 1 << 26), fake(*tot, 1 << 30), red, -1,
+                                        fake(F32, (3, 65), 1 << 34))
+    assert bwd((F32, (1,)), (F32, (1,))) == _lib.NOT_INITIALIZED
+    assert bwd((F32, (3,)), (F32, (1,))) == _lib.INVALID_ARGUMENT   # Mean takes a [1] upstream
+    assert bwd((F32, (1,)), (BF16, (1,))) == _lib.INVALID_ARGUMENT  # total weight dtype
+    assert bwd((F32, (3,)), (F32, (1,)), red=0) == _lib.NOT_INITIALIZED
+
+
 def test_overlap_and_shape_checks_run_before_the_context():
     lib = _lib.load()
     a = fake(BF16, (32, 48), ptr=1 << 20)

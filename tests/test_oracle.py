@@ -571,3 +571,49 @@ def test_embedding_random_and_empty(oracle):
     np.testing.assert_array_equal(oracle.embedding_backward_f64(np.zeros((0, 3, 24)), empty, 50), np.zeros((50, 24)))
     with pytest.raises(ValueError):
         oracle.embedding(weights, np.array([50]))
+
+
+# ------------------------------------------------------------------ NLLLoss / cross entropy
+
+def _ce_case(classes, ignore, weighted):
+    # examples/cross_entropy_tensor.rs:19-24
+    rows = 5
+    x = ((np.arange(rows * classes) % 23).astype(np.float32) / 8 - 1000).reshape(rows, classes)
+    labels = np.array([0, 31 % classes, 7 % classes, 0, 2 % classes], np.int64)
+    if ignore is not None:
+        labels[1] = ignore
+    w = (0.5 + (np.arange(classes) % 7) / 4).astype(np.float32) if weighted else np.ones(classes, np.float32)
+    return x, labels, w
+
+
+@pytest.mark.parametrize("classes", [1, 3, 33, 4097])
+@pytest.mark.parametrize("reduction", [0, 1, 2])
+@pytest.mark.parametrize("ignore", [None, -100])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_nll_oracle_vs_torch_cross_entropy(oracle, classes, reduction, ignore, weighted):
+    x, labels, w = _ce_case(classes, ignore, weighted)
+    ii = -1 if ignore is None else ignore
+    tx = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    red = ["none", "mean", "sum"][reduction]
+    want = torch.nn.functional.cross_entropy(tx, torch.tensor(labels), weight=torch.tensor(w, dtype=torch.float64),
+                                             reduction=red, ignore_index=ii)
+    logp = torch.log_softmax(tx.detach(), -1).numpy()
+    got, total = oracle.nll_loss_f64(logp, labels, w, reduction, ii)
+    close(got, np.atleast_1d(want.detach().numpy()), 1e-9, 1e-12)
+    close([total], [sum(w[t] for t in labels if t != ii)], 0, 1e-12)
+    # backward: the oracle's d/dlogp chained through log-softmax equals torch's d/dlogits
+    grad = (1.25 + np.arange(5 if reduction == 0 else 1) / 4)
+    (want * torch.tensor(grad)).sum().backward()
+    dlogp = oracle.nll_loss_backward_f64(grad, x.shape, labels, w, total, reduction, ii)
+    p = np.exp(logp)
+    dlogits = dlogp - p * dlogp.sum(-1, keepdims=True)
+    close(dlogits, tx.grad.numpy(), 1e-9, 1e-9)
+
+
+def test_nll_known_answers(oracle):
+    # examples/cross_entropy_tensor.rs:55-59: Mean over [-1,-2,-3],[-4,-5,-6], labels [0,2], w [1,2,3]
+    got, total = oracle.nll_loss_f64(np.array([[-1.0, -2, -3], [-4, -5, -6]]), [0, 2], [1.0, 2, 3], 1, -1)
+    assert got.tolist() == [19 / 4] and total == 4
+    # every row ignored: Mean is 0/0
+    got, total = oracle.nll_loss_f64(np.zeros((2, 3)), [-100, -100], np.ones(3), 1, -100)
+    assert np.isnan(got[0]) and total == 0
