@@ -887,6 +887,27 @@ __device__ __forceinline__ void mfma_ring(Fetch&& fetch, Mma&& mma) {
     }
 }
 
+// mfma_ring with between(i) after MFMA i: VALU work that does not depend on these MFMAs, issued
+// while the matrix core runs them (one wave per SIMD: nothing else would fill the VALU).
+template <int N, class Fetch, class Mma, class Between>
+__device__ __forceinline__ void mfma_ring_x(Fetch&& fetch, Mma&& mma, Between&& between) {
+    constexpr int R = kAhead + 1;
+    bf16x8_t ring[R];
+#pragma unroll
+    for (int i = 0; i < kAhead && i < N; ++i) ring[i % R] = fetch(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (i + kAhead < N) ring[(i + kAhead) % R] = fetch(i + kAhead);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8_t x = ring[i % R];
+        asm volatile("" : "+v"(x));
+        mma(i, x);
+        __builtin_amdgcn_sched_barrier(0);
+        between(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 __device__ __forceinline__ uint32_t lds_address_f(const float* p) {
     return lds_address(reinterpret_cast<const uint16_t*>(p));
 }
@@ -990,19 +1011,25 @@ attn_bwd_dkdv(BwdArgs a) {
         const uint16_t* Ot = tiles[cur][1];
         const bool skip = a.causal && (n0w > q0 + kQStep - 1 + a.diag);
         if (!skip) {
-            // S (even i) and dP (odd i) for query tiles qt, k slices ks: MFMA i = 4 ks + 2 qt + which
+            // Query tile qt of S (even i) and dP (odd i): MFMA i = 2 ks + which. The P / dS
+            // arithmetic of tile 0 runs between the MFMAs of tile 1, that of tile 1 between the
+            // dV / dK MFMAs of k-slices 0-1 (which use only tile 0): one wave per SIMD, so the
+            // exponentials would otherwise leave the matrix core idle.
             f32x16_t s[2], dp[2];
             const f32x16_t zero = {};
-            mfma_ring<4 * KS>(
-                [&](int i) {
-                    const int ks = i >> 2, qt = (i >> 1) & 1;
+            auto sdp = [&](int qt) {
+                return [&, qt](int i) {
+                    const int ks = i >> 1;
                     return tile_read16<DP>((i & 1) ? Ot : Qt, 32 * qt + lq, 2 * ks + lg);
-                },
-                [&](int i, bf16x8_t x) {
-                    const int ks = i >> 2, qt = (i >> 1) & 1;
+                };
+            };
+            auto sdp_mma = [&](int qt) {
+                return [&, qt](int i, bf16x8_t x) {
+                    const int ks = i >> 1;
                     if (i & 1) dp[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, vf[ks], ks == 0 ? zero : dp[qt], 0, 0, 0);
                     else s[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, kf[ks], ks == 0 ? zero : s[qt], 0, 0, 0);
-                });
+                };
+            };
             // P and dS; lane holds key my_key, queries q0 + 32*qt + 8*(v/4) + 4*lg + v%4. Steps
             // whose 64 queries all see this wave's 32 keys (the common case) skip the mask; the
             // others test one 32-bit offset per element: query q0 + qq sees my_key iff
@@ -1013,44 +1040,57 @@ attn_bwd_dkdv(BwdArgs a) {
             const int rel = a.causal ? static_cast<int>(rel64) : (1 << 30);
             const int qlim = static_cast<int>(a.m - q0 < kQStep ? a.m - q0 : kQStep);
             const bool key_ok = my_key < a.n;
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int qi = 32 * qt + 8 * g4 + 4 * lg;
-                    const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(&stats[cur][0][qi]);
-                    const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(&stats[cur][1][qi]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int v = 4 * g4 + e;
-                        float p = fast_exp2(__builtin_fmaf(s[qt][v], a.scale_log2, -l4[e]));
-                        if (!full) {
-                            const int qq = qi + e;
-                            p = key_ok && qq < qlim && qq + rel >= 0 ? p : 0.0f;
-                        }
-                        s[qt][v] = p;
-                        dp[qt][v] = a.scale * (p * (dp[qt][v] - d4[e]));
-                    }
+            // score v of tile qt; the statistics of its 4 rows come in as one 16-byte read each
+            f32x4_t l4, d4;
+            auto pds = [&](int qt, int v) __attribute__((always_inline)) {
+                const int qi = 32 * qt + 8 * (v >> 2) + 4 * lg + (v & 3);
+                if ((v & 3) == 0) {
+                    l4 = *reinterpret_cast<const f32x4_t*>(&stats[cur][0][qi]);
+                    d4 = *reinterpret_cast<const f32x4_t*>(&stats[cur][1][qi]);
                 }
-            // dV^T += dO^T P ; dK^T += Q^T dS  (k = 64 queries in 4 steps of 16):
-            // MFMA i = 2 (DT ks + dt) + which, which 0: dV, 1: dK
+                const float l = l4[v & 3], d = d4[v & 3];
+                float p = fast_exp2(__builtin_fmaf(s[qt][v], a.scale_log2, -l));
+                if (!full) p = key_ok && qi < qlim && qi + rel >= 0 ? p : 0.0f;
+                s[qt][v] = p;
+                dp[qt][v] = a.scale * (p * (dp[qt][v] - d));
+            };
+            // dV^T += dO^T P ; dK^T += Q^T dS  (k = 64 queries in 4 steps of 16), k-slices
+            // 2h, 2h+1: MFMA i = 2 (DT kk + dt) + which, which 0: dV, 1: dK
             bf16x8_t pb[4], sb[4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                pb[ks] = pack_bf16x8(s[ks >> 1], 8 * (ks & 1));
-                sb[ks] = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
-            }
-            mfma_ring<8 * DT>(
-                [&](int i) {
-                    const int ks = i / (2 * DT), dt = (i >> 1) % DT;
+            auto dkv = [&](int h) {
+                return [&, h](int i) {
+                    const int ks = 2 * h + i / (2 * DT), dt = (i >> 1) % DT;
                     const int kb0 = 16 * ks + 4 * lg;
                     return tile_read_tr<DP>((i & 1) ? Qt : Ot, lane, kb0, kb0 + 8, 32 * dt);
-                },
-                [&](int i, bf16x8_t x) {
-                    const int ks = i / (2 * DT), dt = (i >> 1) % DT;
+                };
+            };
+            auto dkv_mma = [&](int h) {
+                return [&, h](int i, bf16x8_t x) {
+                    const int ks = 2 * h + i / (2 * DT), dt = (i >> 1) % DT;
                     if (i & 1) dk[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[ks], dk[dt], 0, 0, 0);
                     else dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, pb[ks], dv[dt], 0, 0, 0);
-                });
+                };
+            };
+            // the 16 scores of a tile spread evenly over the ring's MFMAs (16 of them for D = 128)
+            static_assert(16 % (2 * KS) == 0 && 16 % (4 * DT) == 0, "scores per MFMA");
+            mfma_ring<2 * KS>(sdp(0), sdp_mma(0));
+            mfma_ring_x<2 * KS>(sdp(1), sdp_mma(1), [&](int i) {
+#pragma unroll
+                for (int v = i * 16 / (2 * KS); v < (i + 1) * 16 / (2 * KS); ++v) pds(0, v);
+            });
+            pb[0] = pack_bf16x8(s[0], 0);
+            pb[1] = pack_bf16x8(s[0], 8);
+            sb[0] = pack_bf16x8(dp[0], 0);
+            sb[1] = pack_bf16x8(dp[0], 8);
+            mfma_ring_x<4 * DT>(dkv(0), dkv_mma(0), [&](int i) {
+#pragma unroll
+                for (int v = i * 16 / (4 * DT); v < (i + 1) * 16 / (4 * DT); ++v) pds(1, v);
+            });
+            pb[2] = pack_bf16x8(s[1], 0);
+            pb[3] = pack_bf16x8(s[1], 8);
+            sb[2] = pack_bf16x8(dp[1], 0);
+            sb[3] = pack_bf16x8(dp[1], 8);
+            mfma_ring<4 * DT>(dkv(1), dkv_mma(1));
         }
         landed();
         lds_barrier();
