@@ -46,6 +46,9 @@ def parse():
                    help="also run a 1 GiB device copy (for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     p.add_argument("--only-c5", action="store_true",
                    help="only run the C5 decoder layer (forward + backward, --warmup and --steps) and print its line")
+    p.add_argument("--only-widened", action="store_true",
+                   help="only run the lines of the rows widened around the path (grouped and padded GEMM, "
+                        "softmax, cross entropy, SwiGLU, bias add, embedding) and print them, one JSON line each")
     p.add_argument("--stream-ceilings", action="store_true",
                    help="only measure plain HBM streams (read, write, copy, 2 reads + 1 write) on 1 GiB "
                         "buffers (PyTorch's kernels and rust-ascend_amd/lib/hk_stream_probe) and print them")
@@ -280,6 +283,117 @@ def bench_attention(iters=5):
     return event_ms(fw), event_ms(bw), fwd_flops, 2.5 * fwd_flops
 
 
+def time_gpu(fn, iters=10):
+    """Average HIP-event time (ms) of fn() over iters back-to-back launches after a warm-up."""
+    import torch
+    warm(fn)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_widened():
+    """One line per widened row next to the path (M-grouped and padded GEMM, softmax rows, cross
+    entropy, SwiGLU, bias/residual add, embedding), each at a Llama-sized shape with seeded data:
+    TFLOP/s against the BF16 MFMA peak for the GEMMs, algorithmic HBM bytes against 8 TB/s for
+    the row and elementwise kernels (every tensor read once and written once)."""
+    import torch
+    from rust_ascend_hip import HipRuntime, LossReduction
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    out = []
+
+    def add(name, ms, bound, algo, kernel, unit):
+        val = algo / ms / 1e9 if unit == "TFLOP/s" else algo / ms / 1e6
+        out.append({"workload": name, "value": round(val, 2), "unit": unit, "ms": round(ms, 5),
+                    "roofline": roofline(bound, algo, ms, kernel)})
+
+    def guarded(name, fn):
+        try:
+            fn()
+        except Exception as exc:  # reported, never silently replaced by another path
+            out.append({"workload": name, "error": str(exc)[:200]})
+
+    def grouped():
+        E, rows, K, N = 8, 1024, 4096, 14336
+        a = torch.randn((E * rows, K), generator=g, device="cuda").to(torch.bfloat16)
+        w = torch.randn((E, N, K), generator=g, device="cuda").to(torch.bfloat16)
+        ends = HipRuntime.upload_group_ends([rows * (i + 1) for i in range(E)])
+        y = HipRuntime.grouped_nt(a, w, ends)
+        ms = time_gpu(lambda: HipRuntime.grouped_nt_into(a, w, ends, y))
+        add(f"(f) M-grouped NT GEMM (MoE): {E} experts x {rows} rows, K {K}, N {N}, BF16 out", ms, "mfma",
+            2 * E * rows * N * K, "gemm_nt_m16_kernel", "TFLOP/s")
+    guarded("(f) M-grouped NT GEMM", grouped)
+
+    def padded():
+        M = N = K = 4000
+        a = torch.randn((M, K), generator=g, device="cuda")
+        b = torch.randn((K, N), generator=g, device="cuda")
+        ms = time_gpu(lambda: HipRuntime.gemm_padded_bf16_fp32(a, b))
+        add(f"(f) padded BF16-compute GEMM F32 [{M},{K}]x[{K},{N}] (pad + GEMM + crop)", ms, "mfma", 2 * M * N * K,
+            "pad_bf16+gemm+crop_f32", "TFLOP/s")
+    guarded("(f) padded GEMM", padded)
+
+    R, C = 8192, 32000
+    x = torch.randn((R, C), generator=g, device="cuda")
+
+    def softmax():
+        y = HipRuntime.softmax(x)
+        ms = time_gpu(lambda: HipRuntime.softmax(x))
+        add(f"(f) softmax rows F32 [{R},{C}]", ms, "hbm", 2 * 4 * R * C, "softmax", "GB/s")
+        dy = torch.randn((R, C), generator=g, device="cuda")
+        ms = time_gpu(lambda: HipRuntime.softmax_backward(y, dy))
+        add(f"(f) softmax backward rows F32 [{R},{C}]", ms, "hbm", 3 * 4 * R * C, "softmax_backward", "GB/s")
+    guarded("(f) softmax rows", softmax)
+
+    def cross_entropy():
+        labels = torch.randint(0, C, (R,), generator=g, device="cuda", dtype=torch.int64)
+        wt = torch.ones((C,), device="cuda")
+
+        def ce():
+            lp = HipRuntime.log_softmax(x)
+            return HipRuntime.nll_loss(lp, labels, wt, LossReduction.Mean)
+        ms = time_gpu(ce)
+        add(f"(f) cross entropy fwd F32 [{R},{C}] (log-softmax + NLLLoss mean, INT64 labels)", ms, "hbm",
+            2 * 4 * R * C + 8 * R + 4 * C, "softmax+nll_loss", "GB/s")
+    guarded("(f) cross entropy", cross_entropy)
+
+    def swiglu():
+        T, F = 4096, 14336
+        gate = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
+        up = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
+        ms = time_gpu(lambda: HipRuntime.silu_mul(gate, up))
+        add(f"(f) SwiGLU silu_mul BF16 [{T},{F}]", ms, "hbm", 3 * 2 * T * F, "silu_mul_kernel", "GB/s")
+        gr = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
+        ms = time_gpu(lambda: HipRuntime.silu_mul_backward(gate, up, gr))
+        add(f"(f) SwiGLU silu_mul backward BF16 [{T},{F}]", ms, "hbm", 5 * 2 * T * F, "silu_mul_bwd_kernel", "GB/s")
+    guarded("(f) SwiGLU", swiglu)
+
+    def bias():
+        T, H = 4096, 4096
+        xb = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+        res = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
+        bb = torch.randn((H,), generator=g, device="cuda")
+        ms = time_gpu(lambda: HipRuntime.bias_add(xb, bb, res))
+        add(f"(f) bias + residual add BF16 [{T},{H}], F32 bias", ms, "hbm", 3 * 2 * T * H + 4 * H, "bias_add_kernel",
+            "GB/s")
+    guarded("(f) bias add", bias)
+
+    def embedding():
+        V, H, T = 32000, 4096, 4096
+        table = torch.randn((V, H), generator=g, device="cuda").to(torch.bfloat16)
+        ids = torch.randint(0, V, (T,), generator=g, device="cuda", dtype=torch.int64)
+        ms = time_gpu(lambda: HipRuntime.embedding(table, ids))
+        add(f"(f) embedding gather BF16 table [{V},{H}], {T} INT64 IDs", ms, "hbm", 2 * 2 * T * H + 8 * T,
+            "embedding_gather_kernel", "GB/s")
+    guarded("(f) embedding", embedding)
+    return out
+
+
 def bench_decoder(steps=5, warmup=2):
     """C5: one Llama-style decoder layer forward + backward (hidden 4096, 32/8 heads, SwiGLU 14336,
     batch 2 x seq 2048, token IDs uniform in [0, 32000), N(0, 0.02) BF16 weights)."""
@@ -341,6 +455,10 @@ def main():
     if args.only_c5:
         print(json.dumps(c5_line(args.steps, args.warmup)), flush=True)
         return
+    if args.only_widened:
+        for entry in bench_widened():
+            print(json.dumps(entry), flush=True)
+        return
 
     wall_ms, fwd_ms, bwd_ms = bench_c2(args.steps, args.warmup)
     step_bytes = C2_FWD_BYTES + C2_BWD_BYTES
@@ -395,6 +513,7 @@ def main():
             sec.append(c5_line())
         except Exception as exc:
             sec.append({"workload": "C5 decoder layer", "error": str(exc)[:200]})
+        sec.extend(bench_widened())
         line["secondary"] = sec
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")

@@ -14,8 +14,12 @@
 //
 // Fast path (W % 4 == 0, W <= 4096, 16-byte aligned): one wavefront owns one row; lane l holds
 // the float4 chunks l, l+64, ... of the row in registers, so the row is read once, and row
-// maxima and sums are butterfly reductions across the wave. General path: one workgroup per
-// row, the row re-read from cache for each pass, reductions through LDS.
+// maxima and sums are butterfly reductions across the wave. Wide path (W % 4 == 0,
+// 4096 < W <= 32768, aligned; vocabulary-sized rows): one 1024-thread workgroup owns one row,
+// thread t holding the float4 chunks t, t+1024, ... in registers, so the row is again read once
+// (non-temporal: these working sets exceed the on-package cache), with wave then workgroup
+// reductions. General path: one workgroup per row, the row re-read from cache for each pass,
+// reductions through LDS.
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
 
@@ -27,6 +31,8 @@ namespace {
 
 constexpr int kFastThreads = 256;  // 4 rows per workgroup on the fast path
 constexpr int kRowThreads = 256;   // one row per workgroup on the general path
+constexpr int kWideThreads = 1024; // one row per workgroup on the wide path
+constexpr int kWideMaxWidth = kWideThreads * 4 * 8;  // 8 float4 chunks per thread
 
 template <int MAXJ>
 __device__ __forceinline__ void load_row4(const float* rowp, int lane, int chunks, f32x4_t (&v)[MAXJ]) {
@@ -125,7 +131,7 @@ softmax_bwd_fast(const float* __restrict__ y, const float* __restrict__ dy, floa
 }
 
 // Workgroup-wide reduction through LDS (wave results combined in wave order).
-template <bool MAX>
+template <bool MAX, int NT = kRowThreads>
 __device__ __forceinline__ float block_reduce(float v, float* scratch) {
     v = MAX ? wave_max(v) : wave_sum(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -133,9 +139,90 @@ __device__ __forceinline__ float block_reduce(float v, float* scratch) {
     __syncthreads();
     float r = scratch[0];
 #pragma unroll
-    for (int i = 1; i < kRowThreads / 64; ++i) r = MAX ? fmaxf(r, scratch[i]) : r + scratch[i];
+    for (int i = 1; i < NT / 64; ++i) r = MAX ? fmaxf(r, scratch[i]) : r + scratch[i];
     __syncthreads();  // scratch is reused by the next reduction
     return r;
+}
+
+// chunks past the row's end read as `pad`
+template <int MAXJ>
+__device__ __forceinline__ void load_row_wide(const float* rowp, int chunks, f32x4_t (&v)[MAXJ], float pad = 0.0f) {
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = threadIdx.x + kWideThreads * j;
+        v[j] = c < chunks ? stream_load(reinterpret_cast<const f32x4_t*>(rowp) + c) : f32x4_t{pad, pad, pad, pad};
+    }
+}
+
+// At most 64 VGPRs (8 waves per SIMD), so two rows' workgroups share a CU and one streams
+// while the other waits in its reductions.
+template <int MAXJ, bool LOG>
+__global__ void __launch_bounds__(kWideThreads) __attribute__((amdgpu_waves_per_eu(8)))
+softmax_fwd_wide(const float* __restrict__ x, float* __restrict__ y, int width) {
+    __shared__ float scratch[kWideThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int chunks = width >> 2;
+    // chunks past the end hold -inf: they leave the maximum alone and add exp(-inf) = 0
+    f32x4_t v[MAXJ];
+    load_row_wide<MAXJ>(x + row * width, chunks, v, -INFINITY);
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, v[j][e]);
+    m = block_reduce<true, kWideThreads>(m, scratch);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float ex = expf(v[j][e] - m);
+            s += ex;
+            if (!LOG) v[j][e] = ex;
+        }
+    s = block_reduce<false, kWideThreads>(s, scratch);
+    f32x4_t* yr = reinterpret_cast<f32x4_t*>(y + row * width);
+    const float ls = LOG ? logf(s) : 0.0f, inv = LOG ? 0.0f : 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = threadIdx.x + kWideThreads * j;
+        if (c < chunks) {
+            f32x4_t o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = LOG ? (v[j][e] - m) - ls : v[j][e] * inv;
+            stream_store(o, yr + c);
+        }
+    }
+}
+
+template <int MAXJ, bool LOG>
+__global__ void __launch_bounds__(kWideThreads)
+softmax_bwd_wide(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx, int width) {
+    __shared__ float scratch[kWideThreads / 64];
+    const int64_t row = blockIdx.x;
+    const int chunks = width >> 2;
+    f32x4_t yv[MAXJ], gv[MAXJ];
+    load_row_wide<MAXJ>(y + row * width, chunks, yv);
+    load_row_wide<MAXJ>(dy + row * width, chunks, gv);
+    float dot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j)
+        if (static_cast<int>(threadIdx.x) + kWideThreads * j < chunks)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot += LOG ? gv[j][e] : yv[j][e] * gv[j][e];
+    dot = block_reduce<false, kWideThreads>(dot, scratch);
+    f32x4_t* dr = reinterpret_cast<f32x4_t*>(dx + row * width);
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+        const int c = threadIdx.x + kWideThreads * j;
+        if (c < chunks) {
+            f32x4_t o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = LOG ? gv[j][e] - expf(yv[j][e]) * dot : yv[j][e] * (gv[j][e] - dot);
+            stream_store(o, dr + c);
+        }
+    }
 }
 
 template <bool LOG>
@@ -176,11 +263,24 @@ softmax_bwd_general(const float* __restrict__ y, const float* __restrict__ dy, f
         dr[c] = LOG ? gr[c] - expf(yr[c]) * dot : yr[c] * (gr[c] - dot);
 }
 
-bool fast_softmax(int64_t width, std::initializer_list<const void*> ptrs) {
-    if (width % 4 != 0 || width > 4096) return false;
+bool aligned16(std::initializer_list<const void*> ptrs) {
     for (const void* p : ptrs)
         if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
     return true;
+}
+
+bool fast_softmax(int64_t width, std::initializer_list<const void*> ptrs) {
+    return width % 4 == 0 && width <= 4096 && aligned16(ptrs);
+}
+
+bool wide_softmax(int64_t width, std::initializer_list<const void*> ptrs) {
+    return width % 4 == 0 && width > 4096 && width <= kWideMaxWidth && aligned16(ptrs);
+}
+
+// float4 chunks per thread of the wide path: 2, 4 or 8
+int wide_per_thread(int64_t width) {
+    const int64_t per = (width / 4 + kWideThreads - 1) / kWideThreads;
+    return per <= 2 ? 2 : (per <= 4 ? 4 : 8);
 }
 
 template <bool LOG>
@@ -194,6 +294,14 @@ void launch_fwd(const float* x, float* y, int64_t rows, int64_t width, hipStream
         else if (per_lane <= 4) hipLaunchKernelGGL((softmax_fwd_fast<4, LOG>), grid, dim3(kFastThreads), 0, s, x, y, rows, w);
         else if (per_lane <= 8) hipLaunchKernelGGL((softmax_fwd_fast<8, LOG>), grid, dim3(kFastThreads), 0, s, x, y, rows, w);
         else hipLaunchKernelGGL((softmax_fwd_fast<16, LOG>), grid, dim3(kFastThreads), 0, s, x, y, rows, w);
+    } else if (wide_softmax(width, {x, y})) {
+        const dim3 grid(static_cast<unsigned>(rows));
+        const int w = static_cast<int>(width);
+        switch (wide_per_thread(width)) {
+            case 2: hipLaunchKernelGGL((softmax_fwd_wide<2, LOG>), grid, dim3(kWideThreads), 0, s, x, y, w); break;
+            case 4: hipLaunchKernelGGL((softmax_fwd_wide<4, LOG>), grid, dim3(kWideThreads), 0, s, x, y, w); break;
+            default: hipLaunchKernelGGL((softmax_fwd_wide<8, LOG>), grid, dim3(kWideThreads), 0, s, x, y, w); break;
+        }
     } else {
         hipLaunchKernelGGL((softmax_fwd_general<LOG>), dim3(static_cast<unsigned>(rows)), dim3(kRowThreads), 0, s, x, y,
                            width);
@@ -211,6 +319,14 @@ void launch_bwd(const float* y, const float* dy, float* dx, int64_t rows, int64_
         else if (per_lane <= 4) hipLaunchKernelGGL((softmax_bwd_fast<4, LOG>), grid, dim3(kFastThreads), 0, s, y, dy, dx, rows, w);
         else if (per_lane <= 8) hipLaunchKernelGGL((softmax_bwd_fast<8, LOG>), grid, dim3(kFastThreads), 0, s, y, dy, dx, rows, w);
         else hipLaunchKernelGGL((softmax_bwd_fast<16, LOG>), grid, dim3(kFastThreads), 0, s, y, dy, dx, rows, w);
+    } else if (wide_softmax(width, {y, dy, dx})) {
+        const dim3 grid(static_cast<unsigned>(rows));
+        const int w = static_cast<int>(width);
+        switch (wide_per_thread(width)) {
+            case 2: hipLaunchKernelGGL((softmax_bwd_wide<2, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, w); break;
+            case 4: hipLaunchKernelGGL((softmax_bwd_wide<4, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, w); break;
+            default: hipLaunchKernelGGL((softmax_bwd_wide<8, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, w); break;
+        }
     } else {
         hipLaunchKernelGGL((softmax_bwd_general<LOG>), dim3(static_cast<unsigned>(rows)), dim3(kRowThreads), 0, s, y, dy,
                            dx, width);

@@ -36,7 +36,8 @@ def test_softmax_reference_cases(rows, width, logarithmic):
     close(host(dx), oracle.softmax_backward_f64(yh, dy, logarithmic), 5e-4, 5e-4, "dX")
 
 
-@pytest.mark.parametrize("shape", [(64, 4096), (5, 3, 128), (9, 4100), (2, 7), (4, 8224), (1000, 64), (3, 1)])
+@pytest.mark.parametrize("shape", [(64, 4096), (5, 3, 128), (9, 4100), (2, 7), (4, 8224), (1000, 64), (3, 1),
+                                   (3, 12000), (2, 20004), (5, 32000), (2, 32768), (2, 32772), (3, 4102)])
 @pytest.mark.parametrize("logarithmic", [False, True])
 def test_softmax_random_rows(shape, logarithmic):
     x = oracle.normal(shape, seed=sum(shape), stream=41, std=4.0)
