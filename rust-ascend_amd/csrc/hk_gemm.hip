@@ -506,7 +506,15 @@ __device__ __forceinline__ int swz64(int row, int chunk) {  // element offset in
 //     ping-pong design with register-staged loads and transposing reads that this replaced.
 constexpr int kW4Threads = 256;
 
-template <bool OUT_BF16, bool A_MN, bool B_MN>
+// Byte offset past any operand's buffer range (operands stay below 2^31 bytes): a buffer load
+// at it reads zero.
+constexpr int kOutOfRange = 0x7fff0000;
+
+// KTAIL: K % 64 != 0 (K % 8 == 0), so the last stage is partial. Its K-major 16-byte chunks past
+// K take an out-of-range offset and read as zero; the k-rows of an MN-major operand past K lie
+// past the end of that operand's range already. Zeros add nothing to the accumulators, so the
+// result equals that of K zero-padded to a multiple of 64.
+template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL = false>
 __global__ void __launch_bounds__(kW4Threads, 1)
 gemm_nt_m16_kernel(GemmArgs p) {
     constexpr int kStage = 2 * kPPTile * kPK;
@@ -555,15 +563,22 @@ gemm_nt_m16_kernel(GemmArgs p) {
     const int mn_voff_a = (mn_row0 * p.m + tm * kPPTile + mn_c * 8) * 2;
     const int mn_voff_b = (mn_row0 * p.n + tn * kPPTile + mn_c * 8) * 2;
     const uint32_t lds0 = lds_address(slot0), lds1 = lds_address(slot1);
+    // K-major load: the stage offset moves into the lane's offset, which the range check sees
+    auto kmajor = [&](const i32x4_t& r, uint32_t dst, int row_off, int kt) __attribute__((always_inline)) {
+        if constexpr (KTAIL)
+            load_lds16(r, dst, kt * kPK + src_chunk * 8 < p.k ? row_off + kt * kPK * 2 : kOutOfRange, 0);
+        else
+            load_lds16(r, dst, row_off, kt * kPK * 2);
+    };
     auto dload = [&](uint32_t lds_slot, int kt, int d) __attribute__((always_inline)) {
         const int blk = wave + 4 * d;
         const uint32_t dst = lds_slot + (wave * 8 * kPK + d * 4 * 8 * kPK) * 2;
         if (d < 8) {
             if constexpr (A_MN) load_lds16(ra4, dst, mn_voff_a + (kt * kPK + 8 * d) * p.m * 2, 0);
-            else load_lds16(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt * kPK * 2);
+            else kmajor(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt);
         } else {
             if constexpr (B_MN) load_lds16(rb4, dst, mn_voff_b + (kt * kPK + 8 * (d - 8)) * p.n * 2, 0);
-            else load_lds16(rb4, dst, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt * kPK * 2);
+            else kmajor(rb4, dst, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt);
         }
     };
 
@@ -604,7 +619,7 @@ gemm_nt_m16_kernel(GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc[i][j]));
 
-    const int nk = p.k / kPK;
+    const int nk = KTAIL ? (p.k + kPK - 1) / kPK : p.k / kPK;
     // 64 MFMAs on buffer `cur`; after MFMA 4t: fragment read t of slice `next_ks` from `next_slot`
     // into the other buffer; after MFMA 4t + 2: the direct load of block d0 + t (if below d1).
     auto slice = [&](int cur, const uint16_t* next_slot, int next_ks, uint32_t load_slot, int d0, int d1,
@@ -684,11 +699,13 @@ transpose_bf16(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int6
 }
 
 // The 256x256-tile 4-wave kernel (every transpose) applies when there are enough tiles to fill
-// the GPU, whole 64-deep stages and 32-bit byte offsets.
+// the GPU, K % 8 == 0 (a partial last stage takes the KTAIL variant) and 32-bit byte offsets
+// up to the end of the last (zero-padded) stage.
 bool pp_applies(int64_t batch, int64_t m, int64_t n, int64_t k, int num_cus) {
     const int64_t tiles = ((m + kPPTile - 1) / kPPTile) * ((n + kPPTile - 1) / kPPTile) * batch;
-    return tiles >= num_cus && k > 0 && k % kPK == 0 && m * k * 2 < (int64_t{1} << 31) &&
-           n * k * 2 < (int64_t{1} << 31);
+    const int64_t k64 = (k + kPK - 1) / kPK * kPK;
+    return tiles >= num_cus && k > 0 && k % 8 == 0 && m * k64 * 2 < (int64_t{1} << 31) &&
+           n * k64 * 2 < (int64_t{1} << 31);
 }
 
 template <bool OUT_BF16>
@@ -702,6 +719,13 @@ void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, hipStream
     // and 8192x14336->4096: 1.40 -> 1.49 and 1.38 -> 1.47 PFLOP/s; 8192^3 keeps 1.54 with
     // M bands vs 1.50 with N bands).
     p.band_n = p.tiles_m == p.tiles_n ? 0 : 8;
+    if (p.k % kPK != 0) {
+        if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, true, true>), grid, dim3(kW4Threads), 0, s, p);
+        else if (a_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, false, true>), grid, dim3(kW4Threads), 0, s, p);
+        else if (b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, true, true>), grid, dim3(kW4Threads), 0, s, p);
+        else hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, false, true>), grid, dim3(kW4Threads), 0, s, p);
+        return;
+    }
     if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, true>), grid, dim3(kW4Threads), 0, s, p);
     else if (a_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, false>), grid, dim3(kW4Threads), 0, s, p);
     else if (b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, true>), grid, dim3(kW4Threads), 0, s, p);

@@ -83,7 +83,7 @@ def test_gemm_random_vs_oracle(m, n, k, ta, tb):
 
 
 TILE_SHAPES = [(1, 4000, 4112, 512), (1, 4096, 4096, 64), (1, 4096, 4096, 128), (1, 4096, 4096, 96),
-               (2, 2048, 4096, 320), (1, 4368, 3856, 1216)]
+               (2, 2048, 4096, 320), (1, 4368, 3856, 1216), (1, 4096, 4112, 1040), (1, 4000, 4096, 2032)]
 TRANSPOSES = [(0, 1), (0, 0), (1, 0), (1, 1)]
 
 
@@ -111,6 +111,35 @@ def test_gemm_256_tile_paths(batch, m, n, k, ta, tb):
                 rel_ok(got, want, 1e-2, f"GEMM {batch}x{m}x{n}x{k} {ta}{tb} bf16 [{g}]")
             else:
                 f32_close(got, want, f"GEMM {batch}x{m}x{n}x{k} {ta}{tb} f32 [{g}]")
+
+
+@pytest.mark.parametrize("k", [16, 48, 1040, 2032, 4000])
+@pytest.mark.parametrize("ta,tb", TRANSPOSES)
+def test_gemm_partial_last_stage_equals_zero_padded_k(k, ta, tb):
+    """K % 64 != 0 on the 256x256-tile kernel: the chunks or k-rows of the partial last stage
+    past K read as zero, so the result is bit-identical to the same product with K zero-padded
+    to a multiple of 64 (which runs whole stages only)."""
+    m, n = 4096, 4352
+    k64 = (k + 63) // 64 * 64
+    a_t, _ = randn_bf16((k, m) if ta else (m, k), seed=k + 1, std=1 / np.sqrt(k))
+    b_t, _ = randn_bf16((n, k) if tb else (k, n), seed=k + 2, std=1.0)
+    if ta:
+        a_p = torch.zeros((k64, m), dtype=torch.bfloat16, device=DEV)
+        a_p[:k] = a_t
+    else:
+        a_p = torch.zeros((m, k64), dtype=torch.bfloat16, device=DEV)
+        a_p[:, :k] = a_t
+    if tb:
+        b_p = torch.zeros((n, k64), dtype=torch.bfloat16, device=DEV)
+        b_p[:, :k] = b_t
+    else:
+        b_p = torch.zeros((k64, n), dtype=torch.bfloat16, device=DEV)
+        b_p[:k] = b_t
+    for out in (torch.bfloat16, torch.float32):
+        got = HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), out)
+        want = HipRuntime.gemm(a_p, b_p, Transpose(ta), Transpose(tb), out)
+        assert torch.equal(got.view(torch.int16) if out == torch.bfloat16 else got.view(torch.int32),
+                           want.view(torch.int16) if out == torch.bfloat16 else want.view(torch.int32)), (k, ta, tb, out)
 
 
 def test_gemm_batched_vs_oracle():
