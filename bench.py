@@ -17,7 +17,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import subprocess
 import sys
 import time
 
@@ -51,7 +50,7 @@ def parse():
                         "softmax, cross entropy, SwiGLU, bias add, embedding) and print them, one JSON line each")
     p.add_argument("--stream-ceilings", action="store_true",
                    help="only measure plain HBM streams (read, write, copy, 2 reads + 1 write) on 1 GiB "
-                        "buffers (PyTorch's kernels and rust-ascend_amd/lib/hk_stream_probe) and print them")
+                        "buffers with PyTorch's kernels and print them")
     return p.parse_args()
 
 
@@ -443,12 +442,7 @@ def main():
     from rust_ascend_hip import HipRuntime
     torch.cuda.set_device(0)
     if args.stream_ceilings:
-        # rust-ascend_amd/lib/hk_stream_probe (built with libhk.so): the same mixes with 16-byte
-        # plain and non-temporal accesses, run as its own process
-        probe = os.path.join(ROOT, "rust-ascend_amd", "lib", "hk_stream_probe")
-        res = subprocess.run([probe], capture_output=True, text=True, check=True)
-        print(json.dumps({"hbm_stream_GBps_1GiB_buffers": {"torch": stream_ceilings(),
-                                                           "hk_stream_probe": json.loads(res.stdout)}}))
+        print(json.dumps({"hbm_stream_GBps_1GiB_buffers": {"torch": stream_ceilings()}}))
         return
     HipRuntime.initialize_exclusive()
     HipRuntime.set_async(True)

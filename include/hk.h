@@ -215,6 +215,16 @@ hk_status hk_linear_frozen_padded_bf16_fp32(hk_context* ctx, const hk_tensor* x,
 hk_status hk_linear_frozen_padded_bf16_fp32_backward(hk_context* ctx, const hk_tensor* w_pad,
                                                      const hk_tensor* dy, hk_tensor* dx);
 
+/* Y[M,N] (F32) = bf16(X[M,K]) W[N,K]^T for a fixed BF16 weight used in place (no cast or copy of
+ * W); M/N/K positive multiples of 16. Reference: AscendRuntime::linear_frozen_bf16_fp32,
+ * runtime/mod.rs:379-382 (matrix.rs:147-159). */
+hk_status hk_linear_frozen_bf16_fp32(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, hk_tensor* y);
+/* dX[M,K] (F32) = bf16(dY[M,N]) W[N,K]; the weight receives no gradient. dX carries the input's
+ * shape. Reference: AscendRuntime::linear_frozen_bf16_fp32_backward, runtime/mod.rs:383-386
+ * (matrix.rs:160-172). */
+hk_status hk_linear_frozen_bf16_fp32_backward(hk_context* ctx, const hk_tensor* w, const hk_tensor* dy,
+                                              hk_tensor* dx);
+
 /* Elementwise F32 <-> BF16 conversion (RNE, NaN kept quiet, Inf kept).
  * Reference: AscendRuntime::cast_into, runtime/mod.rs:276-279 (conversion.rs:21-62). */
 hk_status hk_cast_into(hk_context* ctx, const hk_tensor* in, hk_tensor* out);

@@ -569,3 +569,21 @@ def rel_err(actual, expected, atol_frac: float = 1e-3) -> float:
     rms = float(np.sqrt(np.mean(b * b)))
     atol = atol_frac * rms if rms > 0 else 1e-30
     return float(np.max(np.abs(a - b) / (np.abs(b) + atol)))
+
+
+def row_err(actual, expected) -> float:
+    """max over rows (the last axis) of ||a_row - b_row||_2 / ||b_row||_2; a row whose expected
+    norm is zero contributes ||a_row||_2 divided by the largest row norm (so an all-zero row must
+    come back near zero). Infinite when a has a non-finite value."""
+    a = np.asarray(actual, dtype=np.float64)
+    b = np.asarray(expected, dtype=np.float64)
+    if a.size == 0:
+        return 0.0
+    a = a.reshape(-1, a.shape[-1])
+    b = b.reshape(-1, b.shape[-1])
+    if not np.all(np.isfinite(a)):
+        return float("inf")
+    nb = np.sqrt(np.sum(b * b, axis=1))
+    ne = np.sqrt(np.sum((a - b) ** 2, axis=1))
+    floor = max(float(np.max(nb)), 1e-300)
+    return float(np.max(np.where(nb > 0, ne / np.where(nb > 0, nb, 1.0), ne / floor)))

@@ -756,7 +756,6 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
     a.scale_log2 = sh.scale * kLog2e;
     a.causal = sh.causal;
     if constexpr (D >= 64) {
-        if (sh.n * D * 2 >= (int64_t{1} << 31)) return hipErrorInvalidValue;  // 32-bit buffer offsets
         a.mblocks = static_cast<int>((sh.m + kPPBlockM - 1) / kPPBlockM);
         const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
         hipLaunchKernelGGL((attn_fwd_pp<D>), grid, dim3(kPPThreads), 0, s, a);
@@ -778,22 +777,23 @@ __global__ void __launch_bounds__(256)
 attn_bwd_rowstat(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout, const float* __restrict__ lse,
                  float* __restrict__ stat, float* __restrict__ lse2, int64_t rows) {
     constexpr int kLanesPerRow = D / 8;  // each lane reads 8 elements
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t row = gid / kLanesPerRow;
-    const int part = static_cast<int>(gid % kLanesPerRow);
-    float s = 0.0f;
-    if (row < rows) {
+    constexpr int kRowsPerBlock = 256 / kLanesPerRow;
+    const int part = static_cast<int>(threadIdx.x % kLanesPerRow);
+    // grid-stride over rows; the kLanesPerRow lanes of a row (the shuffle's segment) share its trip count
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanesPerRow; row < rows;
+         row += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
+        float s = 0.0f;
         float a[8], b[8];
         load8(o + row * D + part * 8, a);
         load8(dout + row * D + part * 8, b);
 #pragma unroll
         for (int e = 0; e < 8; ++e) s += a[e] * b[e];
-    }
 #pragma unroll
-    for (int off = kLanesPerRow / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanesPerRow);
-    if (row < rows && part == 0) {
-        stat[row] = s;
-        lse2[row] = lse[row] * kLog2e;
+        for (int off = kLanesPerRow / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanesPerRow);
+        if (part == 0) {
+            stat[row] = s;
+            lse2[row] = lse[row] * kLog2e;
+        }
     }
 }
 
@@ -1263,10 +1263,8 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
     const int64_t rows = sh.batch * sh.heads * sh.m;
     constexpr int lanes = D / 8;
     const int64_t threads = rows * lanes;
-    // the gradient kernels address one Q/dO/K/V head with 32-bit buffer offsets
-    if (sh.m * D * 2 >= (int64_t{1} << 31) || sh.n * D * 2 >= (int64_t{1} << 31)) return hipErrorInvalidValue;
     float* lse2 = stat + rows;
-    hipLaunchKernelGGL((attn_bwd_rowstat<D>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((attn_bwd_rowstat<D>), dim3(flat_blocks(threads, 256)), dim3(256), 0, s,
                        static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, stat, lse2, rows);
     BwdArgs a;
     a.q = static_cast<const uint16_t*>(q);
@@ -1298,6 +1296,17 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
 }
 
 }  // namespace
+
+bool attention_shape_fits(const AttnShape& sh) {
+    constexpr int64_t kOffsetLimit = int64_t{1} << 31, kItemLimit = int64_t{1} << 32;
+    if (sh.m * sh.d * 2 >= kOffsetLimit || sh.n * sh.d * 2 >= kOffsetLimit) return false;
+    const bool pp = sh.d >= 64;
+    const int64_t fwd_rows = pp ? kPPBlockM : kBlockM, fwd_threads = pp ? kPPThreads : kThreads;
+    const int64_t fwd = sh.batch * sh.heads * ((sh.m + fwd_rows - 1) / fwd_rows) * fwd_threads;
+    const int64_t dkdv = sh.batch * sh.kv_heads * ((sh.n + kKBlock - 1) / kKBlock) * kThreads;
+    const int64_t dq = sh.batch * sh.heads * ((sh.m + kBlockM - 1) / kBlockM) * kThreads;
+    return fwd < kItemLimit && dkdv < kItemLimit && dq < kItemLimit;
+}
 
 size_t attention_bwd_workspace_bytes(const AttnShape& sh) {
     return 2 * static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float);  // row statistic, lse2

@@ -189,6 +189,19 @@ __host__ __forceinline__ bool aligned16(std::initializer_list<const void*> ptrs)
     return true;
 }
 
+// Flat (one work item per element or chunk) launches. A dispatch's work-item count is a 32-bit
+// quantity, so these grids are capped at 2^20 workgroups (2^28 work items at 256 threads, which
+// still fills 256 CUs many times over) and the kernels walk their index space with a grid stride.
+constexpr int64_t kMaxFlatBlocks = int64_t{1} << 20;
+__host__ __forceinline__ unsigned flat_blocks(int64_t work, int threads) {
+    const int64_t b = (work + threads - 1) / threads;
+    return static_cast<unsigned>(b < kMaxFlatBlocks ? b : kMaxFlatBlocks);
+}
+__device__ __forceinline__ int64_t flat_begin(int threads) {
+    return static_cast<int64_t>(blockIdx.x) * threads + threadIdx.x;
+}
+__device__ __forceinline__ int64_t flat_stride(int threads) { return static_cast<int64_t>(gridDim.x) * threads; }
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 // Butterfly order is fixed, so the result is deterministic.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -362,6 +362,10 @@ bool row_layout(const hk_tensor* x, int64_t* rows, int64_t* width, const char* o
         fail(HK_INVALID_ARGUMENT, "%s width must be positive", op);
         return false;
     }
+    if (*width > INT32_MAX) {
+        fail(HK_INVALID_ARGUMENT, "%s width must not exceed INT32_MAX", op);
+        return false;
+    }
     *rows = numel(x) / *width;
     return true;
 }
@@ -421,7 +425,20 @@ hk_status hk_shutdown(hk_context* h) {
 hk_status hk_set_stream(hk_context* h, void* stream) {
     OpGuard g(h);
     if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
-    g.c->stream = static_cast<hipStream_t>(stream);
+    hipStream_t next = static_cast<hipStream_t>(stream);
+    if (next == g.c->stream) return HK_OK;
+    // The context's workspace serves one stream at a time: in async mode, work queued on the old
+    // stream may still use it, so that stream drains before ops on the new one can reuse it.
+    if (g.c->async && !g.c->poisoned) {
+        hipError_t e = hipStreamSynchronize(g.c->stream);
+        g.c->stats.synchronizations += 1;
+        if (e != hipSuccess) {
+            g.c->poisoned = true;
+            return fail(HK_COMPLETION_ERROR, "stream switch: synchronization status %d (%s)", static_cast<int>(e),
+                        hipGetErrorString(e));
+        }
+    }
+    g.c->stream = next;
     return HK_OK;
 }
 
@@ -738,6 +755,65 @@ hk_status hk_linear_bf16_fp32_backward(hk_context* h, const hk_tensor* x, const 
     if (x->rank != 2 || w->rank != 2)
         return fail(HK_INVALID_ARGUMENT, "BF16-compute linear backward requires saved rank-2 inputs");
     return hk_gemm_bf16_fp32_backward(h, x, w, dy, HK_NO, HK_YES, dx, dw);
+}
+
+namespace {
+// Reference: frozen_linear_spec, matrix.rs:147-153: rank-2 F32 X, fixed rank-2 BF16 W, NT, F32 out.
+hk_status frozen_spec(const hk_tensor* x, const hk_tensor* w, GemmSpec* s) {
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "W")) return HK_INVALID_ARGUMENT;
+    if (x->rank != 2 || w->rank != 2 || x->dtype != HK_F32 || w->dtype != HK_BF16)
+        return fail(HK_INVALID_ARGUMENT, "frozen BF16 linear requires rank-2 FP32 input and fixed BF16 weight");
+    hk_tensor xb = *x;
+    xb.dtype = HK_BF16;
+    return gemm_spec(&xb, w, HK_NO, HK_YES, HK_F32, s);
+}
+}  // namespace
+
+hk_status hk_linear_frozen_bf16_fp32(hk_context* h, const hk_tensor* x, const hk_tensor* w, hk_tensor* y) {
+    // Reference: matrix.rs:154-159: X rounded to BF16 on the device, the fixed W used in place.
+    GemmSpec s;
+    hk_status st = frozen_spec(x, w, &s);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(y, "Y")) return HK_INVALID_ARGUMENT;
+    if (!out_matches(s, y)) return fail(HK_INVALID_ARGUMENT, "output must be F32 [%lld,%lld]", (long long)s.m, (long long)s.n);
+    if (!disjoint({y}, {x, w})) return HK_INVALID_ARGUMENT;
+    const size_t x_bytes = (static_cast<size_t>(numel(x)) * 2 + 255) & ~size_t(255);
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, x_bytes + hk::gemm_workspace_bytes(1, s.m, s.n, s.k, HK_NO, HK_YES))) != HK_OK)
+        return st;
+    void* xb = g.c->workspace;
+    hipError_t e = hk::cast_apply(1, x->data, xb, numel(x), g.c->stream);
+    if (e == hipSuccess)
+        run_gemm(g.c, s, xb, w->data, y->data, HK_NO, HK_YES, static_cast<char*>(g.c->workspace) + x_bytes, &e);
+    return complete(g.c, e, "linear_frozen_bf16_fp32", 2);
+}
+
+hk_status hk_linear_frozen_bf16_fp32_backward(hk_context* h, const hk_tensor* w, const hk_tensor* dy, hk_tensor* dx) {
+    // Reference: matrix.rs:160-172: dX = bf16(dY) W (NN, F32 out); the weight gets no gradient.
+    if (!tensor_ok(w, "W") || !tensor_ok(dy, "dY") || !tensor_ok(dx, "dX")) return HK_INVALID_ARGUMENT;
+    if (dx->rank != 2 || dx->dtype != HK_F32)
+        return fail(HK_INVALID_ARGUMENT, "frozen BF16 linear input gradient must be rank-2 FP32");
+    GemmSpec fwd;
+    hk_status st = frozen_spec(dx, w, &fwd);
+    if (st != HK_OK) return st;
+    if (!out_matches(fwd, dy)) return fail(HK_INVALID_ARGUMENT, "frozen BF16 linear backward requires matching FP32 dY");
+    hk_tensor dyb = *dy;
+    dyb.dtype = HK_BF16;
+    GemmSpec s;
+    if ((st = gemm_spec(&dyb, w, HK_NO, HK_NO, HK_F32, &s)) != HK_OK) return st;
+    if (!out_matches(s, dx)) return fail(HK_INVALID_ARGUMENT, "frozen BF16 linear input gradient shape mismatch");
+    if (!disjoint({dx}, {w, dy})) return HK_INVALID_ARGUMENT;
+    const size_t dy_bytes = (static_cast<size_t>(numel(dy)) * 2 + 255) & ~size_t(255);
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, dy_bytes + hk::gemm_workspace_bytes(1, s.m, s.n, s.k, HK_NO, HK_NO))) != HK_OK)
+        return st;
+    void* dyb_ptr = g.c->workspace;
+    hipError_t e = hk::cast_apply(1, dy->data, dyb_ptr, numel(dy), g.c->stream);
+    if (e == hipSuccess)
+        run_gemm(g.c, s, dyb_ptr, w->data, dx->data, HK_NO, HK_NO, static_cast<char*>(g.c->workspace) + dy_bytes, &e);
+    return complete(g.c, e, "linear_frozen_bf16_fp32_backward", 2);
 }
 
 // ------------------------------------------------------------------ padded GEMM
@@ -1584,6 +1660,12 @@ static hk_status attention_shape(const hk_tensor* q, const hk_tensor* k, const h
     sh->causal = causal ? 1 : 0;
     sh->query_start = causal ? qs : 0;
     sh->key_start = causal ? ks : 0;
+    // Rejected here, before any device work, so an oversized shape leaves the context healthy.
+    if (!hk::attention_shape_fits(*sh))
+        return fail(HK_INVALID_ARGUMENT,
+                    "attention shape too large for the fused kernels: M*D and N*D must stay below 2^30 elements per "
+                    "head and each launch below 2^32 work items (M=%lld N=%lld D=%lld)",
+                    (long long)M, (long long)N, (long long)D);
     return HK_OK;
 }
 

@@ -45,18 +45,18 @@ template <typename T>
 __global__ void __launch_bounds__(kEwThreads)
 silu_mul_kernel(const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ y, int64_t n, bool vec) {
     constexpr int P = Chunk<T>::kPer;
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
-    const int64_t i0 = c * P;
-    if (vec && i0 + P <= n) {
-        float gv[P], uv[P], o[P];
-        Chunk<T>::load(g + i0, gv);
-        Chunk<T>::load(u + i0, uv);
+    for (int64_t i0 = flat_begin(kEwThreads) * P; i0 < n; i0 += flat_stride(kEwThreads) * P) {
+        if (vec && i0 + P <= n) {
+            float gv[P], uv[P], o[P];
+            Chunk<T>::load(g + i0, gv);
+            Chunk<T>::load(u + i0, uv);
 #pragma unroll
-        for (int e = 0; e < P; ++e) o[e] = silu_mul1(gv[e], uv[e]);
-        Chunk<T>::store(y + i0, o);
-    } else {
-        for (int64_t i = i0; i < n && i < i0 + P; ++i)
-            Elem<T>::store(y, i, silu_mul1(Elem<T>::load(g, i), Elem<T>::load(u, i)));
+            for (int e = 0; e < P; ++e) o[e] = silu_mul1(gv[e], uv[e]);
+            Chunk<T>::store(y + i0, o);
+        } else {
+            for (int64_t i = i0; i < n && i < i0 + P; ++i)
+                Elem<T>::store(y, i, silu_mul1(Elem<T>::load(g, i), Elem<T>::load(u, i)));
+        }
     }
 }
 
@@ -65,23 +65,23 @@ __global__ void __launch_bounds__(kEwThreads)
 silu_mul_bwd_kernel(const T* __restrict__ g, const T* __restrict__ u, const T* __restrict__ dy,
                     T* __restrict__ dg, T* __restrict__ du, int64_t n, bool vec) {
     constexpr int P = Chunk<T>::kPer;
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
-    const int64_t i0 = c * P;
-    if (vec && i0 + P <= n) {
-        float gv[P], uv[P], dv[P], og[P], ou[P];
-        Chunk<T>::load(g + i0, gv);
-        Chunk<T>::load(u + i0, uv);
-        Chunk<T>::load(dy + i0, dv);
+    for (int64_t i0 = flat_begin(kEwThreads) * P; i0 < n; i0 += flat_stride(kEwThreads) * P) {
+        if (vec && i0 + P <= n) {
+            float gv[P], uv[P], dv[P], og[P], ou[P];
+            Chunk<T>::load(g + i0, gv);
+            Chunk<T>::load(u + i0, uv);
+            Chunk<T>::load(dy + i0, dv);
 #pragma unroll
-        for (int e = 0; e < P; ++e) silu_mul_bwd1(gv[e], uv[e], dv[e], og[e], ou[e]);
-        Chunk<T>::store(dg + i0, og);
-        Chunk<T>::store(du + i0, ou);
-    } else {
-        for (int64_t i = i0; i < n && i < i0 + P; ++i) {
-            float a, b;
-            silu_mul_bwd1(Elem<T>::load(g, i), Elem<T>::load(u, i), Elem<T>::load(dy, i), a, b);
-            Elem<T>::store(dg, i, a);
-            Elem<T>::store(du, i, b);
+            for (int e = 0; e < P; ++e) silu_mul_bwd1(gv[e], uv[e], dv[e], og[e], ou[e]);
+            Chunk<T>::store(dg + i0, og);
+            Chunk<T>::store(du + i0, ou);
+        } else {
+            for (int64_t i = i0; i < n && i < i0 + P; ++i) {
+                float a, b;
+                silu_mul_bwd1(Elem<T>::load(g, i), Elem<T>::load(u, i), Elem<T>::load(dy, i), a, b);
+                Elem<T>::store(dg, i, a);
+                Elem<T>::store(du, i, b);
+            }
         }
     }
 }
@@ -93,30 +93,31 @@ __global__ void __launch_bounds__(kEwThreads)
 bias_add_kernel(const T* __restrict__ x, const float* __restrict__ b, const T* __restrict__ r, T* __restrict__ y,
                 int64_t n, int64_t width, bool vec) {
     constexpr int P = Chunk<T>::kPer;
-    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x) * P;
-    if (vec && i0 + P <= n) {
-        float xv[P], rv[P], bv[P], o[P];
-        Chunk<T>::load(x + i0, xv);
-        if (RES) Chunk<T>::load(r + i0, rv);
-        if (b) {
-            const float* bp = b + i0 % width;
+    for (int64_t i0 = flat_begin(kEwThreads) * P; i0 < n; i0 += flat_stride(kEwThreads) * P) {
+        if (vec && i0 + P <= n) {
+            float xv[P], rv[P], bv[P], o[P];
+            Chunk<T>::load(x + i0, xv);
+            if (RES) Chunk<T>::load(r + i0, rv);
+            if (b) {
+                const float* bp = b + i0 % width;
 #pragma unroll
-            for (int q = 0; q < P / 4; ++q) {
-                const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bp + 4 * q);
+                for (int q = 0; q < P / 4; ++q) {
+                    const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bp + 4 * q);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) bv[4 * q + e] = w[e];
+                    for (int e = 0; e < 4; ++e) bv[4 * q + e] = w[e];
+                }
             }
-        }
 #pragma unroll
-        for (int e = 0; e < P; ++e) {
-            const float sum = RES ? xv[e] + rv[e] : xv[e];
-            o[e] = b ? sum + bv[e] : sum;
-        }
-        Chunk<T>::store(y + i0, o);
-    } else {
-        for (int64_t i = i0; i < n && i < i0 + P; ++i) {
-            const float s = RES ? Elem<T>::load(x, i) + Elem<T>::load(r, i) : Elem<T>::load(x, i);
-            Elem<T>::store(y, i, b ? s + b[i % width] : s);
+            for (int e = 0; e < P; ++e) {
+                const float sum = RES ? xv[e] + rv[e] : xv[e];
+                o[e] = b ? sum + bv[e] : sum;
+            }
+            Chunk<T>::store(y + i0, o);
+        } else {
+            for (int64_t i = i0; i < n && i < i0 + P; ++i) {
+                const float s = RES ? Elem<T>::load(x, i) + Elem<T>::load(r, i) : Elem<T>::load(x, i);
+                Elem<T>::store(y, i, b ? s + b[i % width] : s);
+            }
         }
     }
 }
@@ -141,17 +142,15 @@ template <int D>
 __global__ void __launch_bounds__(kEwThreads)
 fold_rows_kernel(const float* __restrict__ v, float* __restrict__ out, int64_t rows, int64_t width) {
     const int64_t out_rows = (rows + (int64_t(1) << D) - 1) >> D;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
-    if (idx >= out_rows * width) return;
-    out[idx] = fold_eval<D>(v, rows, width, idx / width, idx % width);
+    for (int64_t idx = flat_begin(kEwThreads); idx < out_rows * width; idx += flat_stride(kEwThreads))
+        out[idx] = fold_eval<D>(v, rows, width, idx / width, idx % width);
 }
 
 __global__ void __launch_bounds__(kEwThreads) zero_f32_kernel(float* __restrict__ p, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
+    for (int64_t i = flat_begin(kEwThreads); i < n; i += flat_stride(kEwThreads)) p[i] = 0.0f;
 }
 
-unsigned blocks_for(int64_t work) { return static_cast<unsigned>((work + kEwThreads - 1) / kEwThreads); }
+unsigned blocks_for(int64_t work) { return flat_blocks(work, kEwThreads); }
 
 template <typename T>
 unsigned grid_for(int64_t n) {

@@ -33,18 +33,19 @@ template <typename Idx, typename U>
 __global__ void __launch_bounds__(kEmbThreads)
 embedding_gather_kernel(const U* __restrict__ table, const Idx* __restrict__ ids, U* __restrict__ out, int64_t tokens,
                         int64_t vocab, int64_t units, int* __restrict__ flag) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kTokensPerBlock + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    if (t >= tokens) return;
-    const int64_t id = static_cast<int64_t>(ids[t]);
-    const bool valid = id >= 0 && id < vocab;
-    U* dst = out + t * units;
-    if (valid) {
-        const U* src = table + id * units;
-        for (int64_t u = lane; u < units; u += kWave) dst[u] = src[u];
-    } else {
-        for (int64_t u = lane; u < units; u += kWave) dst[u] = U{};
-        if (lane == 0) *flag = 1;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * kTokensPerBlock + threadIdx.x / kWave; t < tokens;
+         t += static_cast<int64_t>(gridDim.x) * kTokensPerBlock) {
+        const int64_t id = static_cast<int64_t>(ids[t]);
+        const bool valid = id >= 0 && id < vocab;
+        U* dst = out + t * units;
+        if (valid) {
+            const U* src = table + id * units;
+            for (int64_t u = lane; u < units; u += kWave) dst[u] = src[u];
+        } else {
+            for (int64_t u = lane; u < units; u += kWave) dst[u] = U{};
+            if (lane == 0) *flag = 1;
+        }
     }
 }
 
@@ -53,22 +54,21 @@ template <typename Idx>
 __global__ void __launch_bounds__(kEmbThreads)
 embedding_keys_kernel(const Idx* __restrict__ ids, int64_t tokens, int64_t vocab, uint32_t* __restrict__ keys,
                       uint32_t* __restrict__ pos, uint32_t* __restrict__ counts, int* __restrict__ flag) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kEmbThreads + threadIdx.x;
-    if (t >= tokens) return;
-    const int64_t id = static_cast<int64_t>(ids[t]);
-    const bool valid = id >= 0 && id < vocab;
-    const uint32_t key = static_cast<uint32_t>(valid ? id : vocab);
-    keys[t] = key;
-    pos[t] = static_cast<uint32_t>(t);
-    atomicAdd(counts + key, 1u);
-    if (!valid) *flag = 1;
+    for (int64_t t = flat_begin(kEmbThreads); t < tokens; t += flat_stride(kEmbThreads)) {
+        const int64_t id = static_cast<int64_t>(ids[t]);
+        const bool valid = id >= 0 && id < vocab;
+        const uint32_t key = static_cast<uint32_t>(valid ? id : vocab);
+        keys[t] = key;
+        pos[t] = static_cast<uint32_t>(t);
+        atomicAdd(counts + key, 1u);
+        if (!valid) *flag = 1;
+    }
 }
 
 __global__ void __launch_bounds__(kEmbThreads)
 clear_counts_kernel(uint32_t* __restrict__ counts, int64_t n, int* __restrict__ flag) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kEmbThreads + threadIdx.x;
-    if (i < n) counts[i] = 0;
-    if (i == 0) *flag = 0;
+    for (int64_t i = flat_begin(kEmbThreads); i < n; i += flat_stride(kEmbThreads)) counts[i] = 0;
+    if (flat_begin(kEmbThreads) == 0) *flag = 0;
 }
 
 __global__ void clear_flag_kernel(int* __restrict__ flag) { *flag = 0; }
@@ -160,7 +160,7 @@ EmbWs carve(void* base, int64_t tokens, int64_t vocab) {
 template <typename Idx, typename U>
 void launch_gather(const void* table, const void* ids, void* out, int64_t tokens, int64_t vocab, int64_t row_bytes,
                    int* flag, hipStream_t s) {
-    const unsigned grid = static_cast<unsigned>((tokens + kTokensPerBlock - 1) / kTokensPerBlock);
+    const unsigned grid = flat_blocks(tokens, kTokensPerBlock);
     hipLaunchKernelGGL((embedding_gather_kernel<Idx, U>), dim3(grid), dim3(kEmbThreads), 0, s,
                        static_cast<const U*>(table), static_cast<const Idx*>(ids), static_cast<U*>(out), tokens,
                        vocab, row_bytes / static_cast<int64_t>(sizeof(U)), flag);
@@ -209,10 +209,10 @@ hipError_t embedding_backward(int dtype, const void* grad, int id_bytes, const v
                               int64_t vocab, int64_t width, uint64_t padding, int scale, void* workspace,
                               hipStream_t s) {
     EmbWs w = carve(workspace, tokens, vocab);
-    const unsigned cgrid = static_cast<unsigned>((vocab + 1 + kEmbThreads - 1) / kEmbThreads);
+    const unsigned cgrid = flat_blocks(vocab + 1, kEmbThreads);
     hipLaunchKernelGGL(clear_counts_kernel, dim3(cgrid), dim3(kEmbThreads), 0, s, w.counts, vocab + 1, w.flag);
     if (tokens > 0) {
-        const unsigned tgrid = static_cast<unsigned>((tokens + kEmbThreads - 1) / kEmbThreads);
+        const unsigned tgrid = flat_blocks(tokens, kEmbThreads);
         if (id_bytes == 8)
             hipLaunchKernelGGL(embedding_keys_kernel<int64_t>, dim3(tgrid), dim3(kEmbThreads), 0, s,
                                static_cast<const int64_t*>(ids), tokens, vocab, w.keys, w.pos, w.counts, w.flag);

@@ -506,9 +506,10 @@ __device__ __forceinline__ int swz64(int row, int chunk) {  // element offset in
 //     ping-pong design with register-staged loads and transposing reads that this replaced.
 constexpr int kW4Threads = 256;
 
-// Byte offset past any operand's buffer range (operands stay below 2^31 bytes): a buffer load
-// at it reads zero.
-constexpr int kOutOfRange = 0x7fff0000;
+// Byte offset past any operand's buffer range: a buffer load at it reads zero. The range check
+// compares the unsigned 32-bit offset with the resource's byte count, which pp_applies keeps
+// below 2^31 (m * k * 2 <= m * k64 * 2 < 2^31), so 2^31 is out of range for every operand.
+constexpr int kOutOfRange = static_cast<int>(0x80000000u);
 
 // KTAIL: K % 64 != 0 (K % 8 == 0), so the last stage is partial. Its K-major 16-byte chunks past
 // K take an out-of-range offset and read as zero; the k-rows of an MN-major operand past K lie

@@ -25,20 +25,20 @@ constexpr int kThreads = 256;
 __global__ void __launch_bounds__(kThreads)
 causal_mask_kernel(float* __restrict__ out, int64_t total, int64_t queries, int64_t keys, uint64_t query_start,
                    uint64_t key_start) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= total) return;
-    const int64_t k = i % keys, q = (i / keys) % queries;
-    out[i] = key_start + static_cast<uint64_t>(k) > query_start + static_cast<uint64_t>(q) ? -INFINITY : 0.0f;
+    for (int64_t i = flat_begin(kThreads); i < total; i += flat_stride(kThreads)) {
+        const int64_t k = i % keys, q = (i / keys) % queries;
+        out[i] = key_start + static_cast<uint64_t>(k) > query_start + static_cast<uint64_t>(q) ? -INFINITY : 0.0f;
+    }
 }
 
 // Y[(b, h), c] = X[(b, h / group), c] over the columns c of one (n, d) plane; with Hq = Hkv * group the
 // flattened head index (b * Hq + h) / group is b * Hkv + h / group.
 __global__ void __launch_bounds__(kThreads)
 repeat_kv_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t total, int64_t plane, int64_t group) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= total) return;
-    const int64_t head = i / plane;  // flattened (b, h)
-    y[i] = x[(head / group) * plane + i % plane];
+    for (int64_t i = flat_begin(kThreads); i < total; i += flat_stride(kThreads)) {
+        const int64_t head = i / plane;  // flattened (b, h)
+        y[i] = x[(head / group) * plane + i % plane];
+    }
 }
 
 // One tree level over [rows, groups, width]: next[r, i] = value[r, 2i] + value[r, 2i+1]
@@ -48,14 +48,14 @@ pair_level_kernel(const float* __restrict__ value, float* __restrict__ next, int
                   int64_t width) {
     const int64_t next_groups = (groups + 1) / 2;
     const int64_t total = rows * next_groups * width;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= total) return;
-    const int64_t c = i % width, g = (i / width) % next_groups, r = i / (width * next_groups);
-    const float* src = value + (r * groups + 2 * g) * width + c;
-    next[i] = 2 * g + 1 < groups ? src[0] + src[width] : src[0];
+    for (int64_t i = flat_begin(kThreads); i < total; i += flat_stride(kThreads)) {
+        const int64_t c = i % width, g = (i / width) % next_groups, r = i / (width * next_groups);
+        const float* src = value + (r * groups + 2 * g) * width + c;
+        next[i] = 2 * g + 1 < groups ? src[0] + src[width] : src[0];
+    }
 }
 
-unsigned blocks(int64_t n) { return static_cast<unsigned>((n + kThreads - 1) / kThreads); }
+unsigned blocks(int64_t n) { return flat_blocks(n, kThreads); }
 
 }  // namespace
 

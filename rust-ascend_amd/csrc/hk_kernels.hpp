@@ -118,6 +118,9 @@ struct AttnShape {
     uint64_t query_start, key_start;
 };
 size_t attention_bwd_workspace_bytes(const AttnShape& sh);
+// Whether the fused kernels can take the shape: one head of Q/K/V (M*D and N*D BF16 elements)
+// within 32-bit buffer offsets, and every launch's work items within a dispatch's 32-bit count.
+bool attention_shape_fits(const AttnShape& sh);
 hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o,
                              float* lse, hipStream_t s);
 hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k, const void* v,

@@ -82,33 +82,33 @@ __global__ void __launch_bounds__(kLayoutThreads)
 qkv_rope_kernel(uint16_t* __restrict__ rows, uint16_t* __restrict__ q, uint16_t* __restrict__ k,
                 uint16_t* __restrict__ v, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                 int64_t seq, int64_t hq, int64_t hkv, int64_t d, int64_t total) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kLayoutThreads + threadIdx.x;
-    if (idx >= total) return;
-    const int64_t half = d / 2, chunks = half / 8, heads = hq + 2 * hkv;
-    const int64_t chunk = idx % chunks;
-    const int64_t head_row = idx / chunks;
-    const int64_t h = head_row % heads, t = head_row / heads;
-    const int64_t b = t / seq, s = t - b * seq;
-    const int64_t p0 = chunk * 8;
-    uint16_t* row = rows + t * heads * d + h * d;
-    uint16_t* plane;
-    if (h < hq) plane = q + ((b * hq + h) * seq + s) * d;
-    else if (h < hq + hkv) plane = k + ((b * hkv + (h - hq)) * seq + s) * d;
-    else plane = v + ((b * hkv + (h - hq - hkv)) * seq + s) * d;
-    if (h >= hq + hkv) {
-        if (MERGE) copy_pairs<LAYOUT>(plane, row, half, p0);
-        else copy_pairs<LAYOUT>(row, plane, half, p0);
-        return;
-    }
-    float c[8], sn[8], a[8], bb[8], ya[8], yb[8];
-    const float* ct = cos_t + s * half + p0;
-    const float* st = sin_t + s * half + p0;
-    load8(ct, c);
-    load8(st, sn);
-    load_pairs<LAYOUT>(MERGE ? plane : row, half, p0, a, bb);
+    for (int64_t idx = flat_begin(kLayoutThreads); idx < total; idx += flat_stride(kLayoutThreads)) {
+        const int64_t half = d / 2, chunks = half / 8, heads = hq + 2 * hkv;
+        const int64_t chunk = idx % chunks;
+        const int64_t head_row = idx / chunks;
+        const int64_t h = head_row % heads, t = head_row / heads;
+        const int64_t b = t / seq, s = t - b * seq;
+        const int64_t p0 = chunk * 8;
+        uint16_t* row = rows + t * heads * d + h * d;
+        uint16_t* plane;
+        if (h < hq) plane = q + ((b * hq + h) * seq + s) * d;
+        else if (h < hq + hkv) plane = k + ((b * hkv + (h - hq)) * seq + s) * d;
+        else plane = v + ((b * hkv + (h - hq - hkv)) * seq + s) * d;
+        if (h >= hq + hkv) {
+            if (MERGE) copy_pairs<LAYOUT>(plane, row, half, p0);
+            else copy_pairs<LAYOUT>(row, plane, half, p0);
+            return;
+        }
+        float c[8], sn[8], a[8], bb[8], ya[8], yb[8];
+        const float* ct = cos_t + s * half + p0;
+        const float* st = sin_t + s * half + p0;
+        load8(ct, c);
+        load8(st, sn);
+        load_pairs<LAYOUT>(MERGE ? plane : row, half, p0, a, bb);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) rope_rotate<MERGE>(a[i], bb[i], c[i], sn[i], ya[i], yb[i]);
-    store_pairs<LAYOUT>(MERGE ? row : plane, half, p0, ya, yb);
+        for (int i = 0; i < 8; ++i) rope_rotate<MERGE>(a[i], bb[i], c[i], sn[i], ya[i], yb[i]);
+        store_pairs<LAYOUT>(MERGE ? row : plane, half, p0, ya, yb);
+    }
 }
 
 // TO_ROWS: x [B, H, S, D] -> y [B, S, H D]; otherwise the reverse. 8 elements per thread.
@@ -116,21 +116,21 @@ template <bool TO_ROWS>
 __global__ void __launch_bounds__(kLayoutThreads)
 heads_rows_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t heads, int64_t seq, int64_t d,
                   int64_t total) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * kLayoutThreads + threadIdx.x;
-    if (idx >= total) return;
-    const int64_t chunks = d / 8;
-    const int64_t c = idx % chunks;
-    // idx enumerates the row layout [B, S, H, D/8] so the row-side accesses are contiguous
-    const int64_t h = (idx / chunks) % heads;
-    const int64_t t = idx / (chunks * heads);  // b * seq + s
-    const int64_t b = t / seq, s = t - b * seq;
-    const int64_t row_off = (t * heads + h) * d + c * 8;
-    const int64_t plane_off = ((b * heads + h) * seq + s) * d + c * 8;
-    const int64_t from = TO_ROWS ? plane_off : row_off, to = TO_ROWS ? row_off : plane_off;
-    *reinterpret_cast<u32x4_t*>(y + to) = *reinterpret_cast<const u32x4_t*>(x + from);
+    for (int64_t idx = flat_begin(kLayoutThreads); idx < total; idx += flat_stride(kLayoutThreads)) {
+        const int64_t chunks = d / 8;
+        const int64_t c = idx % chunks;
+        // idx enumerates the row layout [B, S, H, D/8] so the row-side accesses are contiguous
+        const int64_t h = (idx / chunks) % heads;
+        const int64_t t = idx / (chunks * heads);  // b * seq + s
+        const int64_t b = t / seq, s = t - b * seq;
+        const int64_t row_off = (t * heads + h) * d + c * 8;
+        const int64_t plane_off = ((b * heads + h) * seq + s) * d + c * 8;
+        const int64_t from = TO_ROWS ? plane_off : row_off, to = TO_ROWS ? row_off : plane_off;
+        *reinterpret_cast<u32x4_t*>(y + to) = *reinterpret_cast<const u32x4_t*>(x + from);
+    }
 }
 
-unsigned blocks_of(int64_t work) { return static_cast<unsigned>((work + kLayoutThreads - 1) / kLayoutThreads); }
+unsigned blocks_of(int64_t work) { return flat_blocks(work, kLayoutThreads); }
 
 }  // namespace
 

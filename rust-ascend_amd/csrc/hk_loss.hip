@@ -76,17 +76,18 @@ __global__ void __launch_bounds__(kNllBwdThreads)
 nll_backward_kernel(const T* __restrict__ grad, const I* __restrict__ target, const T* __restrict__ weight,
                     const T* __restrict__ total, T* __restrict__ dinput, int64_t rows, int64_t classes,
                     int reduction, int64_t ignore) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kNllBwdThreads + threadIdx.x;
-    if (i >= rows * classes) return;
-    const int64_t r = i / classes, c = i - r * classes;
-    const int64_t t = static_cast<int64_t>(target[r]);
-    float v = 0.0f;
-    if (c == t && t != ignore) {
-        float g = Elem<T>::load(grad, reduction == 0 ? r : 0);
-        if (reduction == 1) g = g / Elem<T>::load(total, 0);
-        v = -(Elem<T>::load(weight, t) * g);
+    const int64_t count = rows * classes;
+    for (int64_t i = flat_begin(kNllBwdThreads); i < count; i += flat_stride(kNllBwdThreads)) {
+        const int64_t r = i / classes, c = i - r * classes;
+        const int64_t t = static_cast<int64_t>(target[r]);
+        float v = 0.0f;
+        if (c == t && t != ignore) {
+            float g = Elem<T>::load(grad, reduction == 0 ? r : 0);
+            if (reduction == 1) g = g / Elem<T>::load(total, 0);
+            v = -(Elem<T>::load(weight, t) * g);
+        }
+        Elem<T>::store(dinput, i, v);
     }
-    Elem<T>::store(dinput, i, v);
 }
 
 template <typename T, typename I>
@@ -103,7 +104,7 @@ hipError_t nll_backward_t(const void* grad, const void* target, const void* weig
                           int64_t rows, int64_t classes, int reduction, int64_t ignore, hipStream_t s) {
     const int64_t n = rows * classes;
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL((nll_backward_kernel<T, I>), dim3(static_cast<unsigned>((n + kNllBwdThreads - 1) / kNllBwdThreads)),
+    hipLaunchKernelGGL((nll_backward_kernel<T, I>), dim3(flat_blocks(n, kNllBwdThreads)),
                        dim3(kNllBwdThreads), 0, s, static_cast<const T*>(grad), static_cast<const I*>(target),
                        static_cast<const T*>(weight), static_cast<const T*>(total), static_cast<T*>(dinput), rows,
                        classes, reduction, ignore);

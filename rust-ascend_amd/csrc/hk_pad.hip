@@ -8,8 +8,9 @@
 //
 // Layout: [batch, rows, cols] row-major on both sides. pad_bf16 writes the whole padded
 // [batch, R, C] destination (zeros outside the source), so no separate clearing pass is needed;
-// crop_f32 reads only the retained [batch, rows, cols] window. Both are HBM-bound: one thread per
-// destination element pair (BF16) or element (F32), coalesced along the last axis.
+// crop_f32 reads only the retained [batch, rows, cols] window. Both are HBM-bound: one work item per
+// destination element pair (BF16) or element (F32) in a grid-stride walk, coalesced along the
+// last axis.
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
 
@@ -24,38 +25,38 @@ template <typename T>
 __global__ void __launch_bounds__(kPadThreads)
 pad_bf16_kernel(const T* __restrict__ src, uint16_t* __restrict__ dst, int64_t rows, int64_t cols, int64_t R,
                 int64_t C, int64_t total_pairs) {
-    const int64_t pair = static_cast<int64_t>(blockIdx.x) * kPadThreads + threadIdx.x;
-    if (pair >= total_pairs) return;
-    const int64_t i = 2 * pair;  // C is even (a multiple of 16), so a pair never crosses a row
-    const int64_t c = i % C, rb = i / C;
-    const int64_t r = rb % R, b = rb / R;
-    uint16_t v[2];
+    for (int64_t pair = flat_begin(kPadThreads); pair < total_pairs; pair += flat_stride(kPadThreads)) {
+        const int64_t i = 2 * pair;  // C is even (a multiple of 16), so a pair never crosses a row
+        const int64_t c = i % C, rb = i / C;
+        const int64_t r = rb % R, b = rb / R;
+        uint16_t v[2];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int64_t cc = c + e;
-        if (r < rows && cc < cols) {
-            const int64_t s = (b * rows + r) * cols + cc;
-            if constexpr (sizeof(T) == 4) v[e] = f32_to_bf16(src[s]);
-            else v[e] = src[s];
-        } else {
-            v[e] = 0;
+        for (int e = 0; e < 2; ++e) {
+            const int64_t cc = c + e;
+            if (r < rows && cc < cols) {
+                const int64_t s = (b * rows + r) * cols + cc;
+                if constexpr (sizeof(T) == 4) v[e] = f32_to_bf16(src[s]);
+                else v[e] = src[s];
+            } else {
+                v[e] = 0;
+            }
         }
+        *reinterpret_cast<uint32_t*>(dst + i) = static_cast<uint32_t>(v[0]) | (static_cast<uint32_t>(v[1]) << 16);
     }
-    *reinterpret_cast<uint32_t*>(dst + i) = static_cast<uint32_t>(v[0]) | (static_cast<uint32_t>(v[1]) << 16);
 }
 
 // dst[b, r, c] = src[b, r, c] for the retained window of a [batch, R, C] F32 source.
 __global__ void __launch_bounds__(kPadThreads)
 crop_f32_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t rows, int64_t cols, int64_t R,
                 int64_t C, int64_t total) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kPadThreads + threadIdx.x;
-    if (i >= total) return;
-    const int64_t c = i % cols, rb = i / cols;
-    const int64_t r = rb % rows, b = rb / rows;
-    dst[i] = src[(b * R + r) * C + c];
+    for (int64_t i = flat_begin(kPadThreads); i < total; i += flat_stride(kPadThreads)) {
+        const int64_t c = i % cols, rb = i / cols;
+        const int64_t r = rb % rows, b = rb / rows;
+        dst[i] = src[(b * R + r) * C + c];
+    }
 }
 
-unsigned blocks_for(int64_t work) { return static_cast<unsigned>((work + kPadThreads - 1) / kPadThreads); }
+unsigned blocks_for(int64_t work) { return flat_blocks(work, kPadThreads); }
 
 }  // namespace
 

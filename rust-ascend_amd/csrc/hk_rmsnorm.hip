@@ -319,9 +319,8 @@ rms_bwd_dw_general(const T* __restrict__ x, const T* __restrict__ dy, const floa
     partial[chunk * width + col] = s;
 }
 
-__global__ void fill_zero_f32(float* p, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
+__global__ void __launch_bounds__(256) fill_zero_f32(float* p, int64_t n) {
+    for (int64_t i = flat_begin(256); i < n; i += flat_stride(256)) p[i] = 0.0f;
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -342,11 +341,17 @@ int grid_for_rows(int64_t rows, int waves_per_block, int cap) {
 template <typename T, int MAXJ>
 void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_t rows, int width,
                      float eps, hipStream_t s) {
-    const int64_t grid = (rows + kRowsThreads / 64 - 1) / (kRowsThreads / 64);  // one row per wave
+    // One row per wave. Launches take at most 2^22 rows each (2^20 workgroups), so a launch's
+    // work items stay within a dispatch's 32-bit count; C2's 16384 rows are one launch.
+    constexpr int64_t kRowsPerLaunch = int64_t{1} << 22;
     auto kernel = width == 512 * MAXJ ? rms_fwd_fast<T, MAXJ, true> : rms_fwd_fast<T, MAXJ, false>;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads),
-                       static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x), w,
-                       static_cast<T*>(y), rstd, rows, width, eps);
+    for (int64_t r0 = 0; r0 < rows; r0 += kRowsPerLaunch) {
+        const int64_t n = rows - r0 < kRowsPerLaunch ? rows - r0 : kRowsPerLaunch;
+        const int64_t grid = (n + kRowsThreads / 64 - 1) / (kRowsThreads / 64);
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(kRowsThreads),
+                           static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x) + r0 * width, w,
+                           static_cast<T*>(y) + r0 * width, rstd + r0, n, width, eps);
+    }
 }
 
 template <typename T, int MAXJ>
@@ -388,7 +393,7 @@ template <typename T>
 hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
                           float* dw, float* workspace, int64_t rows, int64_t width, hipStream_t s) {
     if (rows == 0) {
-        hipLaunchKernelGGL(fill_zero_f32, dim3((width + 255) / 256), dim3(256), 0, s, dw, width);
+        hipLaunchKernelGGL(fill_zero_f32, dim3(flat_blocks(width, 256)), dim3(256), 0, s, dw, width);
         return hipGetLastError();
     }
     if (fast_rows(width, {x, w, dy, dx})) {

@@ -53,66 +53,66 @@ __global__ void __launch_bounds__(256)
 rope_pairs(const T* __restrict__ x, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
            T* __restrict__ y, int64_t rows, int64_t width, int64_t half, RopeMap map) {
     const int64_t per_row = half / V;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= rows * per_row) return;
-    const int64_t row = idx / per_row;
-    const int64_t p0 = (idx - row * per_row) * V;
-    const int64_t t = table_row(row, map) * half + p0;
-    float c[V], s[V], a[V], b[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-        c[i] = cos_t[t + i];
-        s[i] = sin_t[t + i];
-    }
-    const T* xr = x + row * width;
-    T* yr = y + row * width;
-    if constexpr (LAYOUT == 1) {
-        load_v<T, V>(xr + p0, a);
-        load_v<T, V>(xr + half + p0, b);
-    } else {
-        float ab[2 * V];
-        if constexpr (V == 8) {
-            float lo[8], hi[8];
-            load8(xr + 2 * p0, lo);
-            load8(xr + 2 * p0 + 8, hi);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                ab[i] = lo[i];
-                ab[8 + i] = hi[i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 2 * V; ++i) ab[i] = Elem<T>::load(xr, 2 * p0 + i);
-        }
+    for (int64_t idx = flat_begin(256); idx < rows * per_row; idx += flat_stride(256)) {
+        const int64_t row = idx / per_row;
+        const int64_t p0 = (idx - row * per_row) * V;
+        const int64_t t = table_row(row, map) * half + p0;
+        float c[V], s[V], a[V], b[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-            a[i] = ab[2 * i];
-            b[i] = ab[2 * i + 1];
+            c[i] = cos_t[t + i];
+            s[i] = sin_t[t + i];
         }
-    }
-    float ya[V], yb[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) rope_rotate<BWD>(a[i], b[i], c[i], s[i], ya[i], yb[i]);
-    if constexpr (LAYOUT == 1) {
-        store_v<T, V>(yr + p0, ya);
-        store_v<T, V>(yr + half + p0, yb);
-    } else {
-        if constexpr (V == 8) {
-            float lo[8], hi[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                lo[2 * i] = ya[i];
-                lo[2 * i + 1] = yb[i];
-                hi[2 * i] = ya[4 + i];
-                hi[2 * i + 1] = yb[4 + i];
-            }
-            store8(yr + 2 * p0, lo);
-            store8(yr + 2 * p0 + 8, hi);
+        const T* xr = x + row * width;
+        T* yr = y + row * width;
+        if constexpr (LAYOUT == 1) {
+            load_v<T, V>(xr + p0, a);
+            load_v<T, V>(xr + half + p0, b);
         } else {
+            float ab[2 * V];
+            if constexpr (V == 8) {
+                float lo[8], hi[8];
+                load8(xr + 2 * p0, lo);
+                load8(xr + 2 * p0 + 8, hi);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    ab[i] = lo[i];
+                    ab[8 + i] = hi[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2 * V; ++i) ab[i] = Elem<T>::load(xr, 2 * p0 + i);
+            }
 #pragma unroll
             for (int i = 0; i < V; ++i) {
-                Elem<T>::store(yr, 2 * (p0 + i), ya[i]);
-                Elem<T>::store(yr, 2 * (p0 + i) + 1, yb[i]);
+                a[i] = ab[2 * i];
+                b[i] = ab[2 * i + 1];
+            }
+        }
+        float ya[V], yb[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) rope_rotate<BWD>(a[i], b[i], c[i], s[i], ya[i], yb[i]);
+        if constexpr (LAYOUT == 1) {
+            store_v<T, V>(yr + p0, ya);
+            store_v<T, V>(yr + half + p0, yb);
+        } else {
+            if constexpr (V == 8) {
+                float lo[8], hi[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo[2 * i] = ya[i];
+                    lo[2 * i + 1] = yb[i];
+                    hi[2 * i] = ya[4 + i];
+                    hi[2 * i + 1] = yb[4 + i];
+                }
+                store8(yr + 2 * p0, lo);
+                store8(yr + 2 * p0 + 8, hi);
+            } else {
+#pragma unroll
+                for (int i = 0; i < V; ++i) {
+                    Elem<T>::store(yr, 2 * (p0 + i), ya[i]);
+                    Elem<T>::store(yr, 2 * (p0 + i) + 1, yb[i]);
+                }
             }
         }
     }
@@ -123,18 +123,18 @@ template <typename T>
 __global__ void __launch_bounds__(256)
 copy_tail(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int64_t width, int64_t p) {
     const int64_t tail = width - p;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= rows * tail) return;
-    const int64_t row = idx / tail;
-    const int64_t col = p + (idx - row * tail);
-    y[row * width + col] = x[row * width + col];
+    for (int64_t idx = flat_begin(256); idx < rows * tail; idx += flat_stride(256)) {
+        const int64_t row = idx / tail;
+        const int64_t col = p + (idx - row * tail);
+        y[row * width + col] = x[row * width + col];
+    }
 }
 
 template <typename T, int V, int LAYOUT>
 void launch_pairs(bool bwd, const void* x, const float* c, const float* s, void* y, int64_t rows,
                   int64_t width, int64_t half, const RopeMap& map, hipStream_t st) {
     const int64_t n = rows * (half / V);
-    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    const dim3 grid(flat_blocks(n, 256));
     if (bwd)
         hipLaunchKernelGGL((rope_pairs<T, V, LAYOUT, true>), grid, dim3(256), 0, st, static_cast<const T*>(x), c,
                            s, static_cast<T*>(y), rows, width, half, map);
@@ -161,35 +161,37 @@ hipError_t rope_t(const void* x, const float* c, const float* s, void* y, int64_
     }
     if (p < width) {
         const int64_t n = rows * (width - p);
-        hipLaunchKernelGGL((copy_tail<T>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+        hipLaunchKernelGGL((copy_tail<T>), dim3(flat_blocks(n, 256)), dim3(256), 0, st,
                            static_cast<const T*>(x), static_cast<T*>(y), rows, width, p);
     }
     return hipGetLastError();
 }
 
-// Each thread converts 8 consecutive elements; `vec` (16-byte aligned bases) selects
+// Each work item converts 8 consecutive elements (grid-stride); `vec` (16-byte aligned bases) selects
 // the vector loads/stores, otherwise element accesses.
 __global__ void __launch_bounds__(256)
 cast_f32_to_bf16(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n, int vec) {
-    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
-    if (vec && i + 8 <= n) {
-        float v[8];
-        load8(in + i, v);
-        store8(out + i, v);
-    } else {
-        for (int64_t j = i; j < n && j < i + 8; ++j) out[j] = f32_to_bf16(in[j]);
+    for (int64_t i = flat_begin(256) * 8; i < n; i += flat_stride(256) * 8) {
+        if (vec && i + 8 <= n) {
+            float v[8];
+            load8(in + i, v);
+            store8(out + i, v);
+        } else {
+            for (int64_t j = i; j < n && j < i + 8; ++j) out[j] = f32_to_bf16(in[j]);
+        }
     }
 }
 
 __global__ void __launch_bounds__(256)
 cast_bf16_to_f32(const uint16_t* __restrict__ in, float* __restrict__ out, int64_t n, int vec) {
-    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
-    if (vec && i + 8 <= n) {
-        float v[8];
-        load8(in + i, v);
-        store8(out + i, v);
-    } else {
-        for (int64_t j = i; j < n && j < i + 8; ++j) out[j] = bf16_to_f32(in[j]);
+    for (int64_t i = flat_begin(256) * 8; i < n; i += flat_stride(256) * 8) {
+        if (vec && i + 8 <= n) {
+            float v[8];
+            load8(in + i, v);
+            store8(out + i, v);
+        } else {
+            for (int64_t j = i; j < n && j < i + 8; ++j) out[j] = bf16_to_f32(in[j]);
+        }
     }
 }
 
@@ -205,7 +207,7 @@ hipError_t rope_apply(int dtype_bf16, const void* x, const float* cos_t, const f
 hipError_t cast_apply(int to_bf16, const void* in, void* out, int64_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     const int64_t threads = (n + 7) / 8;
-    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    const dim3 grid(flat_blocks(threads, 256));
     const int vec = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
     if (to_bf16)
         hipLaunchKernelGGL(cast_f32_to_bf16, grid, dim3(256), 0, s, static_cast<const float*>(in),

@@ -47,52 +47,53 @@ template <int MAXJ, bool LOG>
 __global__ void __launch_bounds__(kFastThreads)
 softmax_fwd_fast(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int width) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kFastThreads / 64) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const int chunks = width >> 2;
-    f32x4_t v[MAXJ];
-    load_row4<MAXJ>(x + row * width, lane, chunks, v);
-    float m = -INFINITY;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * (kFastThreads / 64) + (threadIdx.x >> 6); row < rows;
+         row += static_cast<int64_t>(gridDim.x) * (kFastThreads / 64)) {
+        const int chunks = width >> 2;
+        f32x4_t v[MAXJ];
+        load_row4<MAXJ>(x + row * width, lane, chunks, v);
+        float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
-        if (lane + 64 * j < chunks)
+        for (int j = 0; j < MAXJ; ++j)
+            if (lane + 64 * j < chunks)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) m = fmaxf(m, v[j][e]);
-    m = wave_max(m);
-    float s = 0.0f;
+                for (int e = 0; e < 4; ++e) m = fmaxf(m, v[j][e]);
+        m = wave_max(m);
+        float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
-        if (lane + 64 * j < chunks)
+        for (int j = 0; j < MAXJ; ++j)
+            if (lane + 64 * j < chunks)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float ex = expf(v[j][e] - m);
-                s += ex;
-                if (!LOG) v[j][e] = ex;
+                for (int e = 0; e < 4; ++e) {
+                    const float ex = expf(v[j][e] - m);
+                    s += ex;
+                    if (!LOG) v[j][e] = ex;
+                }
+        s = wave_sum(s);
+        float* yr = y + row * width;
+        if (LOG) {
+            const float ls = logf(s);
+#pragma unroll
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = lane + 64 * j;
+                if (c < chunks) {
+                    f32x4_t o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - m) - ls;
+                    *reinterpret_cast<f32x4_t*>(yr + 4 * c) = o;
+                }
             }
-    s = wave_sum(s);
-    float* yr = y + row * width;
-    if (LOG) {
-        const float ls = logf(s);
+        } else {
+            const float inv = 1.0f / s;
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
-            if (c < chunks) {
-                f32x4_t o;
+            for (int j = 0; j < MAXJ; ++j) {
+                const int c = lane + 64 * j;
+                if (c < chunks) {
+                    f32x4_t o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = (v[j][e] - m) - ls;
-                *reinterpret_cast<f32x4_t*>(yr + 4 * c) = o;
-            }
-        }
-    } else {
-        const float inv = 1.0f / s;
-#pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
-            if (c < chunks) {
-                f32x4_t o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = v[j][e] * inv;
-                *reinterpret_cast<f32x4_t*>(yr + 4 * c) = o;
+                    for (int e = 0; e < 4; ++e) o[e] = v[j][e] * inv;
+                    *reinterpret_cast<f32x4_t*>(yr + 4 * c) = o;
+                }
             }
         }
     }
@@ -103,29 +104,30 @@ __global__ void __launch_bounds__(kFastThreads)
 softmax_bwd_fast(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx,
                  int64_t rows, int width) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (kFastThreads / 64) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const int chunks = width >> 2;
-    f32x4_t yv[MAXJ], gv[MAXJ];
-    load_row4<MAXJ>(y + row * width, lane, chunks, yv);
-    load_row4<MAXJ>(dy + row * width, lane, chunks, gv);
-    float dot = 0.0f;
+    for (int64_t row = static_cast<int64_t>(blockIdx.x) * (kFastThreads / 64) + (threadIdx.x >> 6); row < rows;
+         row += static_cast<int64_t>(gridDim.x) * (kFastThreads / 64)) {
+        const int chunks = width >> 2;
+        f32x4_t yv[MAXJ], gv[MAXJ];
+        load_row4<MAXJ>(y + row * width, lane, chunks, yv);
+        load_row4<MAXJ>(dy + row * width, lane, chunks, gv);
+        float dot = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
-        if (lane + 64 * j < chunks)
+        for (int j = 0; j < MAXJ; ++j)
+            if (lane + 64 * j < chunks)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dot += LOG ? gv[j][e] : yv[j][e] * gv[j][e];
-    dot = wave_sum(dot);
-    float* dr = dx + row * width;
+                for (int e = 0; e < 4; ++e) dot += LOG ? gv[j][e] : yv[j][e] * gv[j][e];
+        dot = wave_sum(dot);
+        float* dr = dx + row * width;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c < chunks) {
-            f32x4_t o;
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) {
+                f32x4_t o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                o[e] = LOG ? gv[j][e] - expf(yv[j][e]) * dot : yv[j][e] * (gv[j][e] - dot);
-            *reinterpret_cast<f32x4_t*>(dr + 4 * c) = o;
+                for (int e = 0; e < 4; ++e)
+                    o[e] = LOG ? gv[j][e] - expf(yv[j][e]) * dot : yv[j][e] * (gv[j][e] - dot);
+                *reinterpret_cast<f32x4_t*>(dr + 4 * c) = o;
+            }
         }
     }
 }
@@ -158,109 +160,113 @@ __device__ __forceinline__ void load_row_wide(const float* rowp, int chunks, f32
 // while the other waits in its reductions.
 template <int MAXJ, bool LOG>
 __global__ void __launch_bounds__(kWideThreads) __attribute__((amdgpu_waves_per_eu(8)))
-softmax_fwd_wide(const float* __restrict__ x, float* __restrict__ y, int width) {
+softmax_fwd_wide(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int width) {
     __shared__ float scratch[kWideThreads / 64];
-    const int64_t row = blockIdx.x;
-    const int chunks = width >> 2;
-    // chunks past the end hold -inf: they leave the maximum alone and add exp(-inf) = 0
-    f32x4_t v[MAXJ];
-    load_row_wide<MAXJ>(x + row * width, chunks, v, -INFINITY);
-    float m = -INFINITY;
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {  // uniform per workgroup
+        const int chunks = width >> 2;
+        // chunks past the end hold -inf: they leave the maximum alone and add exp(-inf) = 0
+        f32x4_t v[MAXJ];
+        load_row_wide<MAXJ>(x + row * width, chunks, v, -INFINITY);
+        float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
+        for (int j = 0; j < MAXJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) m = fmaxf(m, v[j][e]);
-    m = block_reduce<true, kWideThreads>(m, scratch);
-    float s = 0.0f;
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, v[j][e]);
+        m = block_reduce<true, kWideThreads>(m, scratch);
+        float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
+        for (int j = 0; j < MAXJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float ex = expf(v[j][e] - m);
-            s += ex;
-            if (!LOG) v[j][e] = ex;
-        }
-    s = block_reduce<false, kWideThreads>(s, scratch);
-    f32x4_t* yr = reinterpret_cast<f32x4_t*>(y + row * width);
-    const float ls = LOG ? logf(s) : 0.0f, inv = LOG ? 0.0f : 1.0f / s;
+            for (int e = 0; e < 4; ++e) {
+                const float ex = expf(v[j][e] - m);
+                s += ex;
+                if (!LOG) v[j][e] = ex;
+            }
+        s = block_reduce<false, kWideThreads>(s, scratch);
+        f32x4_t* yr = reinterpret_cast<f32x4_t*>(y + row * width);
+        const float ls = LOG ? logf(s) : 0.0f, inv = LOG ? 0.0f : 1.0f / s;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int c = threadIdx.x + kWideThreads * j;
-        if (c < chunks) {
-            f32x4_t o;
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = threadIdx.x + kWideThreads * j;
+            if (c < chunks) {
+                f32x4_t o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = LOG ? (v[j][e] - m) - ls : v[j][e] * inv;
-            stream_store(o, yr + c);
+                for (int e = 0; e < 4; ++e) o[e] = LOG ? (v[j][e] - m) - ls : v[j][e] * inv;
+                stream_store(o, yr + c);
+            }
         }
     }
 }
 
 template <int MAXJ, bool LOG>
 __global__ void __launch_bounds__(kWideThreads)
-softmax_bwd_wide(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx, int width) {
+softmax_bwd_wide(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx, int64_t rows, int width) {
     __shared__ float scratch[kWideThreads / 64];
-    const int64_t row = blockIdx.x;
-    const int chunks = width >> 2;
-    f32x4_t yv[MAXJ], gv[MAXJ];
-    load_row_wide<MAXJ>(y + row * width, chunks, yv);
-    load_row_wide<MAXJ>(dy + row * width, chunks, gv);
-    float dot = 0.0f;
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {  // uniform per workgroup
+        const int chunks = width >> 2;
+        f32x4_t yv[MAXJ], gv[MAXJ];
+        load_row_wide<MAXJ>(y + row * width, chunks, yv);
+        load_row_wide<MAXJ>(dy + row * width, chunks, gv);
+        float dot = 0.0f;
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
-        if (static_cast<int>(threadIdx.x) + kWideThreads * j < chunks)
+        for (int j = 0; j < MAXJ; ++j)
+            if (static_cast<int>(threadIdx.x) + kWideThreads * j < chunks)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dot += LOG ? gv[j][e] : yv[j][e] * gv[j][e];
-    dot = block_reduce<false, kWideThreads>(dot, scratch);
-    f32x4_t* dr = reinterpret_cast<f32x4_t*>(dx + row * width);
+                for (int e = 0; e < 4; ++e) dot += LOG ? gv[j][e] : yv[j][e] * gv[j][e];
+        dot = block_reduce<false, kWideThreads>(dot, scratch);
+        f32x4_t* dr = reinterpret_cast<f32x4_t*>(dx + row * width);
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j) {
-        const int c = threadIdx.x + kWideThreads * j;
-        if (c < chunks) {
-            f32x4_t o;
+        for (int j = 0; j < MAXJ; ++j) {
+            const int c = threadIdx.x + kWideThreads * j;
+            if (c < chunks) {
+                f32x4_t o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                o[e] = LOG ? gv[j][e] - expf(yv[j][e]) * dot : yv[j][e] * (gv[j][e] - dot);
-            stream_store(o, dr + c);
+                for (int e = 0; e < 4; ++e)
+                    o[e] = LOG ? gv[j][e] - expf(yv[j][e]) * dot : yv[j][e] * (gv[j][e] - dot);
+                stream_store(o, dr + c);
+            }
         }
     }
 }
 
 template <bool LOG>
 __global__ void __launch_bounds__(kRowThreads)
-softmax_fwd_general(const float* __restrict__ x, float* __restrict__ y, int64_t width) {
+softmax_fwd_general(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int64_t width) {
     __shared__ float scratch[kRowThreads / 64];
-    const int64_t row = blockIdx.x;
-    const float* xr = x + row * width;
-    float* yr = y + row * width;
-    float m = -INFINITY;
-    for (int64_t c = threadIdx.x; c < width; c += kRowThreads) m = fmaxf(m, xr[c]);
-    m = block_reduce<true>(m, scratch);
-    float s = 0.0f;
-    for (int64_t c = threadIdx.x; c < width; c += kRowThreads) s += expf(xr[c] - m);
-    s = block_reduce<false>(s, scratch);
-    if (LOG) {
-        const float ls = logf(s);
-        for (int64_t c = threadIdx.x; c < width; c += kRowThreads) yr[c] = (xr[c] - m) - ls;
-    } else {
-        const float inv = 1.0f / s;
-        for (int64_t c = threadIdx.x; c < width; c += kRowThreads) yr[c] = expf(xr[c] - m) * inv;
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {  // uniform per workgroup
+        const float* xr = x + row * width;
+        float* yr = y + row * width;
+        float m = -INFINITY;
+        for (int64_t c = threadIdx.x; c < width; c += kRowThreads) m = fmaxf(m, xr[c]);
+        m = block_reduce<true>(m, scratch);
+        float s = 0.0f;
+        for (int64_t c = threadIdx.x; c < width; c += kRowThreads) s += expf(xr[c] - m);
+        s = block_reduce<false>(s, scratch);
+        if (LOG) {
+            const float ls = logf(s);
+            for (int64_t c = threadIdx.x; c < width; c += kRowThreads) yr[c] = (xr[c] - m) - ls;
+        } else {
+            const float inv = 1.0f / s;
+            for (int64_t c = threadIdx.x; c < width; c += kRowThreads) yr[c] = expf(xr[c] - m) * inv;
+        }
     }
 }
 
 template <bool LOG>
 __global__ void __launch_bounds__(kRowThreads)
 softmax_bwd_general(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx,
-                    int64_t width) {
+                    int64_t rows, int64_t width) {
     __shared__ float scratch[kRowThreads / 64];
-    const int64_t row = blockIdx.x;
-    const float* yr = y + row * width;
-    const float* gr = dy + row * width;
-    float* dr = dx + row * width;
-    float dot = 0.0f;
-    for (int64_t c = threadIdx.x; c < width; c += kRowThreads) dot += LOG ? gr[c] : yr[c] * gr[c];
-    dot = block_reduce<false>(dot, scratch);
-    for (int64_t c = threadIdx.x; c < width; c += kRowThreads)
-        dr[c] = LOG ? gr[c] - expf(yr[c]) * dot : yr[c] * (gr[c] - dot);
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {  // uniform per workgroup
+        const float* yr = y + row * width;
+        const float* gr = dy + row * width;
+        float* dr = dx + row * width;
+        float dot = 0.0f;
+        for (int64_t c = threadIdx.x; c < width; c += kRowThreads) dot += LOG ? gr[c] : yr[c] * gr[c];
+        dot = block_reduce<false>(dot, scratch);
+        for (int64_t c = threadIdx.x; c < width; c += kRowThreads)
+            dr[c] = LOG ? gr[c] - expf(yr[c]) * dot : yr[c] * (gr[c] - dot);
+    }
 }
 
 bool aligned16(std::initializer_list<const void*> ptrs) {
@@ -286,7 +292,7 @@ int wide_per_thread(int64_t width) {
 template <bool LOG>
 void launch_fwd(const float* x, float* y, int64_t rows, int64_t width, hipStream_t s) {
     if (fast_softmax(width, {x, y})) {
-        const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+        const dim3 grid(flat_blocks(rows, 4));
         const int per_lane = static_cast<int>((width / 4 + 63) / 64);
         const int w = static_cast<int>(width);
         if (per_lane <= 1) hipLaunchKernelGGL((softmax_fwd_fast<1, LOG>), grid, dim3(kFastThreads), 0, s, x, y, rows, w);
@@ -295,23 +301,23 @@ void launch_fwd(const float* x, float* y, int64_t rows, int64_t width, hipStream
         else if (per_lane <= 8) hipLaunchKernelGGL((softmax_fwd_fast<8, LOG>), grid, dim3(kFastThreads), 0, s, x, y, rows, w);
         else hipLaunchKernelGGL((softmax_fwd_fast<16, LOG>), grid, dim3(kFastThreads), 0, s, x, y, rows, w);
     } else if (wide_softmax(width, {x, y})) {
-        const dim3 grid(static_cast<unsigned>(rows));
+        const dim3 grid(flat_blocks(rows, 1));
         const int w = static_cast<int>(width);
         switch (wide_per_thread(width)) {
-            case 2: hipLaunchKernelGGL((softmax_fwd_wide<2, LOG>), grid, dim3(kWideThreads), 0, s, x, y, w); break;
-            case 4: hipLaunchKernelGGL((softmax_fwd_wide<4, LOG>), grid, dim3(kWideThreads), 0, s, x, y, w); break;
-            default: hipLaunchKernelGGL((softmax_fwd_wide<8, LOG>), grid, dim3(kWideThreads), 0, s, x, y, w); break;
+            case 2: hipLaunchKernelGGL((softmax_fwd_wide<2, LOG>), grid, dim3(kWideThreads), 0, s, x, y, rows, w); break;
+            case 4: hipLaunchKernelGGL((softmax_fwd_wide<4, LOG>), grid, dim3(kWideThreads), 0, s, x, y, rows, w); break;
+            default: hipLaunchKernelGGL((softmax_fwd_wide<8, LOG>), grid, dim3(kWideThreads), 0, s, x, y, rows, w); break;
         }
     } else {
-        hipLaunchKernelGGL((softmax_fwd_general<LOG>), dim3(static_cast<unsigned>(rows)), dim3(kRowThreads), 0, s, x, y,
-                           width);
+        hipLaunchKernelGGL((softmax_fwd_general<LOG>), dim3(flat_blocks(rows, 1)), dim3(kRowThreads), 0, s, x, y,
+                           rows, width);
     }
 }
 
 template <bool LOG>
 void launch_bwd(const float* y, const float* dy, float* dx, int64_t rows, int64_t width, hipStream_t s) {
     if (fast_softmax(width, {y, dy, dx})) {
-        const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+        const dim3 grid(flat_blocks(rows, 4));
         const int per_lane = static_cast<int>((width / 4 + 63) / 64);
         const int w = static_cast<int>(width);
         if (per_lane <= 1) hipLaunchKernelGGL((softmax_bwd_fast<1, LOG>), grid, dim3(kFastThreads), 0, s, y, dy, dx, rows, w);
@@ -320,16 +326,16 @@ void launch_bwd(const float* y, const float* dy, float* dx, int64_t rows, int64_
         else if (per_lane <= 8) hipLaunchKernelGGL((softmax_bwd_fast<8, LOG>), grid, dim3(kFastThreads), 0, s, y, dy, dx, rows, w);
         else hipLaunchKernelGGL((softmax_bwd_fast<16, LOG>), grid, dim3(kFastThreads), 0, s, y, dy, dx, rows, w);
     } else if (wide_softmax(width, {y, dy, dx})) {
-        const dim3 grid(static_cast<unsigned>(rows));
+        const dim3 grid(flat_blocks(rows, 1));
         const int w = static_cast<int>(width);
         switch (wide_per_thread(width)) {
-            case 2: hipLaunchKernelGGL((softmax_bwd_wide<2, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, w); break;
-            case 4: hipLaunchKernelGGL((softmax_bwd_wide<4, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, w); break;
-            default: hipLaunchKernelGGL((softmax_bwd_wide<8, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, w); break;
+            case 2: hipLaunchKernelGGL((softmax_bwd_wide<2, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, rows, w); break;
+            case 4: hipLaunchKernelGGL((softmax_bwd_wide<4, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, rows, w); break;
+            default: hipLaunchKernelGGL((softmax_bwd_wide<8, LOG>), grid, dim3(kWideThreads), 0, s, y, dy, dx, rows, w); break;
         }
     } else {
-        hipLaunchKernelGGL((softmax_bwd_general<LOG>), dim3(static_cast<unsigned>(rows)), dim3(kRowThreads), 0, s, y, dy,
-                           dx, width);
+        hipLaunchKernelGGL((softmax_bwd_general<LOG>), dim3(flat_blocks(rows, 1)), dim3(kRowThreads), 0, s, y, dy,
+                           dx, rows, width);
     }
 }
 

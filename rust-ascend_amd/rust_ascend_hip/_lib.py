@@ -85,6 +85,8 @@ SIGNATURES = {
     "hk_gemm_bf16_fp32_backward": [_CTX, _T, _T, _T, _i32, _i32, _T, _T],
     "hk_gemm_padded_bf16_fp32": [_CTX, _T, _T, _i32, _i32, _T, _T, _T],
     "hk_gemm_padded_bf16_fp32_backward": [_CTX, _T, _T, _T, _i32, _i32, _T, _T],
+    "hk_linear_frozen_bf16_fp32": [_CTX, _T, _T, _T],
+    "hk_linear_frozen_bf16_fp32_backward": [_CTX, _T, _T, _T],
     "hk_linear_frozen_padded_bf16_fp32": [_CTX, _T, _T, _T, _T],
     "hk_linear_frozen_padded_bf16_fp32_backward": [_CTX, _T, _T, _T],
     "hk_linear_bf16_fp32": [_CTX, _T, _T, _T, _T, _T],

@@ -85,6 +85,25 @@ def linear_padded_bf16_fp32(x, w) -> torch.Tensor:
     return matmul_padded_bf16_fp32(x, w, Transpose.No, Transpose.Yes)
 
 
+class _LinearFrozen(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight):
+        ctx.save_for_backward(weight)  # the fixed BF16 weight itself (frozen.rs:51-70)
+        ctx.x_shape = tuple(x.shape)
+        return HipRuntime.linear_frozen_bf16_fp32(x, weight)
+
+    @staticmethod
+    def backward(ctx, dy):
+        (weight,) = ctx.saved_tensors
+        return HipRuntime.linear_frozen_bf16_fp32_backward(ctx.x_shape, weight, dy.contiguous().float()), None
+
+
+def linear_frozen_bf16_fp32(x, weight) -> torch.Tensor:
+    """F32 X[M,K] and a fixed BF16 W[N,K] (aligned to 16): input-only differentiation, the weight
+    never receives a gradient. Reference: nn::linear_frozen_bf16_fp32 (src/nn/frozen.rs:44-70)."""
+    return _LinearFrozen.apply(x.contiguous(), weight.contiguous())
+
+
 class _LinearFrozenPadded(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight):

@@ -277,6 +277,24 @@ class HipRuntime:
         return da, db
 
     @staticmethod
+    def linear_frozen_bf16_fp32(x, weight):
+        """F32 Y = bf16(X) W^T for a fixed BF16 weight used in place. Reference:
+        AscendRuntime::linear_frozen_bf16_fp32 (mod.rs:379-382)."""
+        if x.dim() != 2 or weight.dim() != 2:
+            raise HkError(_lib.INVALID_ARGUMENT, "frozen BF16 linear requires rank-2 FP32 input and fixed BF16 weight")
+        y = _empty((x.shape[0], weight.shape[0]), torch.float32, x)
+        _call("hk_linear_frozen_bf16_fp32", desc(x), desc(weight), desc(y))
+        return y
+
+    @staticmethod
+    def linear_frozen_bf16_fp32_backward(input_shape, weight, grad):
+        """F32 dX in input_shape from the fixed BF16 weight and F32 dY. Reference:
+        AscendRuntime::linear_frozen_bf16_fp32_backward (mod.rs:383-386)."""
+        dx = _empty(tuple(input_shape), torch.float32, grad)
+        _call("hk_linear_frozen_bf16_fp32_backward", desc(weight), desc(grad), desc(dx))
+        return dx
+
+    @staticmethod
     def linear_frozen_padded_bf16_fp32(x, weight):
         """[F32 Y, the BF16 weight the backward uses]: the weight itself when its axes are multiples
         of 16, else a zero-padded copy. Reference: AscendRuntime::linear_frozen_padded_bf16_fp32

@@ -72,3 +72,12 @@ def mag_ok(actual, expected, magnitude, tol, name=""):
     e = oracle.mag_err(actual, expected, magnitude)
     assert e <= tol, f"{name}: max err / magnitude {e:.3e} > {tol}"
     return e
+
+
+def rows_ok(actual, expected, tol, name=""):
+    """Per-row normwise parity: max over rows (last axis) of ||a-b|| / ||b|| <= tol. Unlike
+    mag_ok, this is measured against each row's own norm, so an error that is small next to the
+    sum of |terms| but not next to the row (a dropped key or query tile) fails."""
+    e = oracle.row_err(actual, expected)
+    assert e <= tol, f"{name}: max per-row normwise err {e:.3e} > {tol}"
+    return e

@@ -265,3 +265,47 @@ def test_attention_contract():
                     ((4096, 2, 32, 64), (4096, 1, 96, 64), (4096, 1, 96, 64)), ((2, 6, 32, 48), (2, 3, 96, 48), (2, 3, 96, 48))]:
         assert call(q, k, v) == _lib.INVALID_ARGUMENT, (q, k, v)
     assert call((2, 2, 32, 64), (2, 1, 96, 64), (2, 1, 96, 64), scale=float("nan")) == _lib.INVALID_ARGUMENT
+
+
+def test_attention_oversized_shapes_are_invalid_arguments():
+    """The fused kernels address one Q/K/V head with 32-bit byte offsets and launch at most 2^32
+    work items per grid dimension: larger shapes are invalid arguments, reported before the
+    context is touched (so they can never poison it)."""
+    lib = _lib.load()
+
+    def call(q, k):
+        o = fake(BF16, q, 1 << 44)
+        lse = fake(F32, q[:3], 1 << 45)
+        return lib.hk_attention_forward(None, fake(BF16, q, 1 << 20), fake(BF16, k, 1 << 36), fake(BF16, k, 1 << 40),
+                                        0.1, 1, 0, 0, o, lse)
+
+    assert call((1, 1, 64, 128), (1, 1, (1 << 23) - 16, 128)) == _lib.NOT_INITIALIZED   # N*D*2 < 2^31
+    assert call((1, 1, 64, 128), (1, 1, 1 << 23, 128)) == _lib.INVALID_ARGUMENT        # N*D*2 == 2^31
+    assert "too large" in _lib.last_error()
+    assert call((1, 1, 1 << 23, 128), (1, 1, 64, 128)) == _lib.INVALID_ARGUMENT        # M*D*2 == 2^31
+    # D = 16: one head fits the offsets, but 4096 heads of 2^25 rows exceed 2^32 work items
+    assert call((1, 1, 1 << 25, 16), (1, 1, 64, 16)) == _lib.NOT_INITIALIZED
+    assert call((1, 4096, 1 << 25, 16), (1, 1, 64, 16)) == _lib.INVALID_ARGUMENT
+
+
+def test_linear_frozen_contract():
+    # matrix.rs:147-172: rank-2 F32 X with a fixed rank-2 BF16 W (aligned to 16), F32 Y; the
+    # backward takes matching F32 dY and writes F32 dX in the input's shape
+    lib = _lib.load()
+    x, w = fake(F32, (32, 48), 1 << 20), fake(BF16, (64, 48), 1 << 24)
+    assert lib.hk_linear_frozen_bf16_fp32(None, x, w, fake(F32, (32, 64), 1 << 28)) == _lib.NOT_INITIALIZED
+    for xd, wd, yd in [((F32, (32, 48)), (F32, (64, 48)), (F32, (32, 64))),      # F32 weight
+                       ((BF16, (32, 48)), (BF16, (64, 48)), (F32, (32, 64))),    # BF16 input
+                       ((F32, (32, 40)), (BF16, (64, 40)), (F32, (32, 64))),     # K % 16
+                       ((F32, (2, 32, 48)), (BF16, (64, 48)), (F32, (2, 32, 64))),  # rank 3
+                       ((F32, (32, 48)), (BF16, (64, 48)), (BF16, (32, 64)))]:   # BF16 output
+        assert lib.hk_linear_frozen_bf16_fp32(None, fake(*xd, 1 << 20), fake(*wd, 1 << 24),
+                                              fake(*yd, 1 << 28)) == _lib.INVALID_ARGUMENT, (xd, wd, yd)
+    assert lib.hk_linear_frozen_bf16_fp32_backward(None, w, fake(F32, (32, 64), 1 << 28),
+                                                   fake(F32, (32, 48), 1 << 30)) == _lib.NOT_INITIALIZED
+    assert lib.hk_linear_frozen_bf16_fp32_backward(None, w, fake(F32, (32, 60), 1 << 28),
+                                                   fake(F32, (32, 48), 1 << 30)) == _lib.INVALID_ARGUMENT
+    assert lib.hk_linear_frozen_bf16_fp32_backward(None, w, fake(F32, (32, 64), 1 << 28),
+                                                   fake(F32, (32, 32), 1 << 30)) == _lib.INVALID_ARGUMENT
+    assert lib.hk_linear_frozen_bf16_fp32_backward(None, w, fake(F32, (32, 64), 1 << 28),
+                                                   fake(F32, (32, 48), (1 << 28) + 64)) == _lib.INVALID_ARGUMENT

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import DEV, close, dev_bf16, host, mag_ok, randn_bf16, rel_ok
+from gpu_util import DEV, close, dev_bf16, host, mag_ok, randn_bf16, rel_ok, rows_ok
 from rust_ascend_hip import HipRuntime, HkError
 
 pytestmark = pytest.mark.gpu
@@ -73,7 +73,17 @@ def test_forward_random_vs_oracle(d, causal, m, n):
     o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, d ** -0.5, causal, qs, 0)
     ref = oracle.attention_f64(q, k, v, scale=d ** -0.5, causal=causal, query_start=qs, key_start=0, magnitudes=True)
     mag_ok(host(o), ref["out"], ref["out_mag"], 1e-2, "O")
+    rows_ok(host(o), ref["out"], 1e-2, "O rows")
     close(host(lse), ref["lse"], 1e-3, 1e-4, "lse")
+
+
+def long_rows(m, n, causal, qs=0, min_keys=64):
+    """Query rows that see at least min_keys keys. dQ's per-row check is applied to these: its row
+    term rowsum(dO * O) comes from the BF16 O (the fused formulation), an error of ~2^-9 |dO . O|
+    that on a row seeing only a few keys can be a visible part of a row of dQ whose terms cancel
+    (the magnitude check covers those rows)."""
+    seen = np.minimum(qs + np.arange(m) + 1, n) if causal else np.full(m, n)
+    return np.nonzero(seen >= min_keys)[0]
 
 
 def test_forward_fully_masked_rows_and_positions():
@@ -92,18 +102,27 @@ def test_forward_fully_masked_rows_and_positions():
     assert torch.count_nonzero(o2) == 0 and torch.all(torch.isneginf(lse2))
 
 
+# (batch, KV group) pairs of C4 checked against the oracle: the first and the last, whose
+# workgroups sit at opposite ends of the XCD-grouped launch order
+C4_SAMPLES = [(0, 0), (3, 7)]
+
+
 def test_forward_c4_full_size_sampled():
     """B4, S4096, Hq32/Hkv8, D128, causal, scale 1/sqrt(128); parity on
-    batch 0 x KV group 0 (4 query heads) over all 4096 rows."""
+    batch 0 x KV group 0 and batch 3 x KV group 7 (4 query heads each) over all 4096 rows, by
+    the magnitude check and the per-row normwise check."""
     B, H, HKV, S, D = 4, 32, 8, 4096, 128
     q_t, _ = randn_bf16((B, H, S, D), seed=41)
     k_t, _ = randn_bf16((B, HKV, S, D), seed=42)
     v_t, _ = randn_bf16((B, HKV, S, D), seed=43)
     o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, D ** -0.5, True)
-    ref = oracle.attention_f64(host(q_t[:1, :4]), host(k_t[:1, :1]), host(v_t[:1, :1]), scale=D ** -0.5,
-                               causal=True, magnitudes=True)
-    mag_ok(host(o[:1, :4]), ref["out"], ref["out_mag"], 1e-2, "O")
-    close(host(lse[:1, :4]), ref["lse"], 1e-3, 1e-4, "lse")
+    for b, grp in C4_SAMPLES:
+        hs = slice(4 * grp, 4 * grp + 4)
+        ref = oracle.attention_f64(host(q_t[b:b + 1, hs]), host(k_t[b:b + 1, grp:grp + 1]),
+                                   host(v_t[b:b + 1, grp:grp + 1]), scale=D ** -0.5, causal=True, magnitudes=True)
+        mag_ok(host(o[b:b + 1, hs]), ref["out"], ref["out_mag"], 1e-2, f"O (b{b}, g{grp})")
+        rows_ok(host(o[b:b + 1, hs]), ref["out"], 1e-2, f"O rows (b{b}, g{grp})")
+        close(host(lse[b:b + 1, hs]), ref["lse"], 1e-3, 1e-4, f"lse (b{b}, g{grp})")
 
 
 def test_forward_rejects_bad_shapes():
@@ -173,6 +192,10 @@ def test_backward_random_vs_oracle(d, causal, m, n):
     ref = oracle.attention_f64(q, k, v, do, scale=d ** -0.5, causal=causal, query_start=qs, magnitudes=True)
     for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
         mag_ok(host(got), ref[name], ref[name + "_mag"], 1e-2, name)
+    rows = long_rows(m, n, causal, qs)
+    rows_ok(host(dq)[:, :, rows], ref["dq"][:, :, rows], 1e-2, "dq rows")
+    rows_ok(host(dk), ref["dk"], 1e-2, "dk rows")
+    rows_ok(host(dv), ref["dv"], 1e-2, "dv rows")
 
 
 def test_backward_bf16_grads_and_determinism():
@@ -192,15 +215,47 @@ def test_backward_bf16_grads_and_determinism():
 
 def test_backward_c4_full_size_sampled():
     """BASELINE config C4 backward: B4, S4096, Hq32/Hkv8, D128, causal; parity on batch 0 x KV
-    group 0 (the 4 query heads that share KV head 0) over all rows."""
+    group 0 and batch 3 x KV group 7 (the 4 query heads that share the KV head) over all rows, by
+    the magnitude check and the per-row normwise check (dQ's on rows that see at least 64 keys)."""
     B, H, HKV, S, D = 4, 32, 8, 4096, 128
     q_t, _ = randn_bf16((B, H, S, D), seed=61)
     k_t, _ = randn_bf16((B, HKV, S, D), seed=62)
     v_t, _ = randn_bf16((B, HKV, S, D), seed=63)
     do_t, _ = randn_bf16((B, H, S, D), seed=64)
     _, _, dq, dk, dv = run_fwd_bwd(q_t, k_t, v_t, do_t, D ** -0.5, True)
-    ref = oracle.attention_f64(host(q_t[:1, :4]), host(k_t[:1, :1]), host(v_t[:1, :1]), host(do_t[:1, :4]),
-                               scale=D ** -0.5, causal=True, magnitudes=True)
-    mag_ok(host(dq[:1, :4]), ref["dq"], ref["dq_mag"], 1e-2, "dq")
-    mag_ok(host(dk[:1, :1]), ref["dk"], ref["dk_mag"], 1e-2, "dk")
-    mag_ok(host(dv[:1, :1]), ref["dv"], ref["dv_mag"], 1e-2, "dv")
+    rows = long_rows(S, S, True)
+    for b, grp in C4_SAMPLES:
+        hs, ks = slice(4 * grp, 4 * grp + 4), slice(grp, grp + 1)
+        ref = oracle.attention_f64(host(q_t[b:b + 1, hs]), host(k_t[b:b + 1, ks]), host(v_t[b:b + 1, ks]),
+                                   host(do_t[b:b + 1, hs]), scale=D ** -0.5, causal=True, magnitudes=True)
+        tag = f"(b{b}, g{grp})"
+        mag_ok(host(dq[b:b + 1, hs]), ref["dq"], ref["dq_mag"], 1e-2, "dq " + tag)
+        mag_ok(host(dk[b:b + 1, ks]), ref["dk"], ref["dk_mag"], 1e-2, "dk " + tag)
+        mag_ok(host(dv[b:b + 1, ks]), ref["dv"], ref["dv_mag"], 1e-2, "dv " + tag)
+        rows_ok(host(dq[b:b + 1, hs])[:, :, rows], ref["dq"][:, :, rows], 1e-2, "dq rows " + tag)
+        rows_ok(host(dk[b:b + 1, ks]), ref["dk"], 1e-2, "dk rows " + tag)
+        rows_ok(host(dv[b:b + 1, ks]), ref["dv"], 1e-2, "dv rows " + tag)
+
+
+def test_oversized_shape_is_rejected_and_leaves_the_context_healthy():
+    """A shape past the fused kernels' 32-bit limits (here N * D >= 2^30 elements per KV head) is
+    an invalid argument found before any device work: the context is not poisoned, and the next
+    call runs. The descriptors point at a small real buffer; nothing is read."""
+    import ctypes
+    from rust_ascend_hip import _lib, runtime
+    from rust_ascend_hip._lib import BF16, F32, tensor_desc
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device=DEV)
+    p = buf.data_ptr()
+    lib, ctx = _lib.load(), runtime._context()
+    q = tensor_desc(p, BF16, (1, 1, 64, 128))
+    kv = tensor_desc(p, BF16, (1, 1, 1 << 23, 128))
+    o = tensor_desc(p + (1 << 19), BF16, (1, 1, 64, 128))
+    lse = tensor_desc(p + (1 << 19) + 64 * 128 * 2, F32, (1, 1, 64))
+    st = lib.hk_attention_forward(ctx, ctypes.byref(q), ctypes.byref(kv), ctypes.byref(kv), 0.1, 1, 0, 0,
+                                  ctypes.byref(o), ctypes.byref(lse))
+    assert st == _lib.INVALID_ARGUMENT and "too large" in _lib.last_error()
+    q_t, q_h = randn_bf16((1, 2, 64, 64), seed=71)
+    k_t, k_h = randn_bf16((1, 1, 64, 64), seed=72)
+    o2, _ = HipRuntime.attention_forward(q_t, k_t, k_t, 0.125, True)
+    ref = oracle.attention_f64(q_h, k_h, k_h, scale=0.125, causal=True, magnitudes=True)
+    mag_ok(host(o2), ref["out"], ref["out_mag"], 1e-2, "O after rejection")

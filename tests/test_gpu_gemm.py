@@ -113,28 +113,31 @@ def test_gemm_256_tile_paths(batch, m, n, k, ta, tb):
                 f32_close(got, want, f"GEMM {batch}x{m}x{n}x{k} {ta}{tb} f32 [{g}]")
 
 
-@pytest.mark.parametrize("k", [16, 48, 1040, 2032, 4000])
+@pytest.mark.parametrize("batch,k", [(1, 16), (1, 48), (1, 1040), (1, 2032), (1, 4000), (2, 48), (2, 1040)])
 @pytest.mark.parametrize("ta,tb", TRANSPOSES)
-def test_gemm_partial_last_stage_equals_zero_padded_k(k, ta, tb):
+def test_gemm_partial_last_stage_equals_zero_padded_k(batch, k, ta, tb):
     """K % 64 != 0 on the 256x256-tile kernel: the chunks or k-rows of the partial last stage
     past K read as zero, so the result is bit-identical to the same product with K zero-padded
-    to a multiple of 64 (which runs whole stages only)."""
+    to a multiple of 64 (which runs whole stages only). With two batches, the MN-major k-rows
+    past K of batch 0 must read as zero, not as batch 1's first k-rows."""
     m, n = 4096, 4352
     k64 = (k + 63) // 64 * 64
-    a_t, _ = randn_bf16((k, m) if ta else (m, k), seed=k + 1, std=1 / np.sqrt(k))
-    b_t, _ = randn_bf16((n, k) if tb else (k, n), seed=k + 2, std=1.0)
+    a_t, _ = randn_bf16((batch, k, m) if ta else (batch, m, k), seed=k + 1, std=1 / np.sqrt(k))
+    b_t, _ = randn_bf16((batch, n, k) if tb else (batch, k, n), seed=k + 2, std=1.0)
     if ta:
-        a_p = torch.zeros((k64, m), dtype=torch.bfloat16, device=DEV)
-        a_p[:k] = a_t
-    else:
-        a_p = torch.zeros((m, k64), dtype=torch.bfloat16, device=DEV)
+        a_p = torch.zeros((batch, k64, m), dtype=torch.bfloat16, device=DEV)
         a_p[:, :k] = a_t
-    if tb:
-        b_p = torch.zeros((n, k64), dtype=torch.bfloat16, device=DEV)
-        b_p[:, :k] = b_t
     else:
-        b_p = torch.zeros((k64, n), dtype=torch.bfloat16, device=DEV)
-        b_p[:k] = b_t
+        a_p = torch.zeros((batch, m, k64), dtype=torch.bfloat16, device=DEV)
+        a_p[:, :, :k] = a_t
+    if tb:
+        b_p = torch.zeros((batch, n, k64), dtype=torch.bfloat16, device=DEV)
+        b_p[:, :, :k] = b_t
+    else:
+        b_p = torch.zeros((batch, k64, n), dtype=torch.bfloat16, device=DEV)
+        b_p[:, :k] = b_t
+    if batch == 1:
+        a_t, b_t, a_p, b_p = a_t[0], b_t[0], a_p[0], b_p[0]
     for out in (torch.bfloat16, torch.float32):
         got = HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), out)
         want = HipRuntime.gemm(a_p, b_p, Transpose(ta), Transpose(tb), out)
@@ -150,19 +153,24 @@ def test_gemm_batched_vs_oracle():
         f32_close(y, oracle.gemm_f64(a, b, ta, tb), f"batched {ta}{tb}")
 
 
-@pytest.mark.parametrize("m,n,k", [(8192, 8192, 8192), (8192, 14336, 4096), (8192, 4096, 14336)])
-def test_gemm_c3_full_size_sampled(m, n, k):
-    """A, B ~N(0,1)/sqrt(K) BF16, NT (Linear weights [N,K]), BF16 out; sampled
-    parity on 4096 random (i, j) plus a full row and a full column."""
+C3_CASES = [(8192, 8192, 8192, 1), (8192, 8192, 8192, 0), (8192, 14336, 4096, 1), (8192, 4096, 14336, 1),
+            (4096, 4096, 4096, 1), (4096, 4096, 4096, 0), (1024, 1024, 1024, 1), (1024, 1024, 1024, 0)]
+
+
+@pytest.mark.parametrize("m,n,k,tb", C3_CASES)
+def test_gemm_c3_full_size_sampled(m, n, k, tb):
+    """BASELINE config C3, every shape and layout the sweep times: A, B ~N(0,1)/sqrt(K) BF16, NT
+    (Linear weights [N,K]) or NN (B stored [K,N]), BF16 out; sampled parity on 4096 random (i, j)
+    plus a full row and a full column (the last)."""
     a_t, a = randn_bf16((m, k), seed=1, std=1 / np.sqrt(k))
-    b_t, b = randn_bf16((n, k), seed=2, std=1 / np.sqrt(k))
-    y_t = HipRuntime.gemm(a_t, b_t, Transpose.No, Transpose.Yes, torch.bfloat16)
+    b_t, b = randn_bf16((n, k) if tb else (k, n), seed=2, std=1 / np.sqrt(k))
+    y_t = HipRuntime.gemm(a_t, b_t, Transpose.No, Transpose(tb), torch.bfloat16)
     rng = np.random.default_rng(0)
     rows = np.concatenate([rng.integers(0, m, 4096), np.full(n, m // 3), np.arange(m)])
     cols = np.concatenate([rng.integers(0, n, 4096), np.arange(n), np.full(m, n - 1)])
     y = host(y_t[torch.from_numpy(rows).to(DEV), torch.from_numpy(cols).to(DEV)])
-    want = oracle.gemm_f64_sampled(a, b, 0, 1, rows, cols)
-    rel_ok(y, want, 1e-2, f"C3 {m}x{n}x{k}")
+    want = oracle.gemm_f64_sampled(a, b, 0, tb, rows, cols)
+    rel_ok(y, want, 1e-2, f"C3 {m}x{n}x{k} {'NT' if tb else 'NN'}")
 
 
 def test_c1_linear_forward():

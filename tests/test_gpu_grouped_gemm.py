@@ -80,6 +80,7 @@ def test_grouped_small_paths_vs_oracle(m, n, k, ends):
 @pytest.mark.parametrize("m,n,k,ends", [
     (8192, 2048, 1024, [1024, 1024, 3072, 3328, 5120, 8192]),   # 256x256 4-wave kernel, empty expert
     (16384, 1792, 4096, [2048 * (i + 1) for i in range(8)]),     # 8 experts, TP-8 Llama FFN width
+    (8192, 2048, 1040, [1024, 1024, 3072, 3328, 5120, 8192]),   # K % 64 != 0: partial last K stage
 ])
 def test_grouped_large_paths_vs_oracle_sampled(m, n, k, ends):
     _check_grouped(m, n, k, ends, seed=m + n, sampled=True)

@@ -97,3 +97,30 @@ def test_out_of_range_label_is_reported():
         HipRuntime.nll_loss(x, torch.tensor([0, 3], device=DEV), w, LossReduction.Sum)
     out, _ = HipRuntime.nll_loss(x, torch.tensor([0, 2], device=DEV), w, LossReduction.Sum)  # context healthy
     assert host(out).tolist() == [0.0]
+
+
+def test_nll_backward_past_32_bit_work_items():
+    """The dense gradient of a [33000, 131072] BF16 input (4.33e9 elements, more than a dispatch's
+    32-bit work-item count): every element is written, the last rows included. The output buffer
+    starts as NaN so an element the kernel skipped would show."""
+    from rust_ascend_hip import runtime
+    rows, classes = 33000, 131072
+    assert rows * classes > 1 << 32
+    inp = torch.empty((rows, classes), dtype=torch.bfloat16, device=DEV)  # only its layout is read
+    labels = torch.arange(rows, device=DEV, dtype=torch.int64) * 7919 % classes
+    labels[5] = -100
+    w = torch.ones((classes,), dtype=torch.bfloat16, device=DEV)
+    g = (1 + torch.arange(rows, device=DEV, dtype=torch.float32) % 5).to(torch.bfloat16)
+    total = torch.zeros((1,), dtype=torch.bfloat16, device=DEV)
+    dx = torch.full((rows, classes), float("nan"), dtype=torch.bfloat16, device=DEV)
+    runtime._call("hk_nll_loss_backward", runtime.desc(g), runtime.desc(inp), runtime.desc(labels), runtime.desc(w),
+                  runtime.desc(total), int(LossReduction.None_), -100, runtime.desc(dx))
+    del inp
+    assert not bool(torch.isnan(dx).any())
+    per_row = (dx != 0).sum(dim=1)
+    keep = torch.arange(rows, device=DEV) != 5
+    assert bool((per_row[keep] == 1).all()) and int(per_row[5]) == 0  # one entry per row but the ignored one
+    picked = dx.gather(1, labels.clamp(min=0)[:, None])[:, 0]
+    assert torch.equal(picked[keep], -g[keep])
+    del dx
+    torch.cuda.empty_cache()

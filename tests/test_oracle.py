@@ -340,6 +340,48 @@ def test_attention_magnitudes_bound_the_outputs(oracle):
     np.testing.assert_allclose(r2["out_mag"], 2 * r["out_mag"], rtol=1e-12)
 
 
+def test_row_normwise_check_rejects_dropped_tiles(oracle):
+    """The C4 attention checks (per-row normwise error <= 1e-2 next to the magnitude check) must
+    reject a kernel that drops one 64-key tile from P V, or one 32-query tile from dK/dV, on long
+    causal rows (S = 2048, D = 128): on a row that sees i keys, a tile holds ~64/i of the row's
+    sum of |terms| (what the magnitude check measures against, so it passes such a tile on rows
+    of C4's length, i ~ 4096) but ~sqrt(64/i) of the row's norm. The planted mistakes are built
+    from the oracle's own outputs on the CPU."""
+    S, D = 2048, 128
+    q = oracle.bf16_round(oracle.normal((1, 1, S, D), 7, 1))
+    k = oracle.bf16_round(oracle.normal((1, 1, S, D), 7, 2))
+    v = oracle.bf16_round(oracle.normal((1, 1, S, D), 7, 3))
+    dy = oracle.bf16_round(oracle.normal((1, 1, S, D), 7, 4))
+    scale = D ** -0.5
+    r = oracle.attention_f64(q, k, v, dy, scale=scale, causal=True)
+    q2, k2, v2, dy2 = (x[0, 0].astype(np.float64) for x in (q, k, v, dy))
+    s = scale * q2 @ k2.T
+    s[np.triu_indices(S, 1)] = -np.inf
+    p = np.exp(s - r["lse"][0, 0][:, None])
+    keys = slice(1024, 1088)
+    out_bad = r["out"][0, 0] - p[:, keys] @ v2[keys]
+    dp = dy2 @ v2.T
+    ds = p * (dp - (p * dp).sum(1, keepdims=True))
+    rows = slice(1024, 1056)
+    dv_bad = r["dv"][0, 0] - p[rows].T @ dy2[rows]
+    dk_bad = r["dk"][0, 0] - scale * ds[rows].T @ q2[rows]
+    for name, bad in (("out", out_bad), ("dv", dv_bad), ("dk", dk_bad)):
+        want = r[name][0, 0]
+        assert oracle.row_err(bad, want) > 1e-2, name             # the per-row check rejects it
+        assert oracle.row_err(want, want) == 0.0
+        # within rounding of the exact result, the per-row check passes
+        assert oracle.row_err(want * (1 + 2.0 ** -9), want) <= 1e-2
+
+
+def test_row_err_definition(oracle):
+    b = np.array([[3.0, 4.0], [0.0, 0.0], [1.0, 0.0]])
+    assert oracle.row_err(b, b) == 0.0
+    assert abs(oracle.row_err(b + np.array([[0.05, 0.0], [0.0, 0.0], [0.0, 0.0]]), b) - 0.01) < 1e-15
+    # an all-zero expected row is measured against the largest row norm (5)
+    assert abs(oracle.row_err(b + np.array([[0.0, 0.0], [0.0, 0.1], [0.0, 0.0]]), b) - 0.02) < 1e-15
+    assert oracle.row_err(np.array([[np.nan, 0.0]]), np.array([[1.0, 0.0]])) == float("inf")
+
+
 # ------------------------------------------------------------------ softmax rows
 
 def _reference_row_inputs(rows, width):
