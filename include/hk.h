@@ -247,6 +247,16 @@ hk_status hk_rms_norm(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, d
 hk_status hk_rms_norm_backward(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
                                const hk_tensor* dy, const hk_tensor* rstd,
                                hk_tensor* dx, hk_tensor* dw);
+/* hk_rms_norm_backward without any allocation: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, checks and results as hk_rms_norm_backward (the same
+ * kernels); its dgamma partials live in a fixed 8 MiB device array of the library (one per GPU,
+ * held until the process ends) instead of the context workspace. Shapes whose partials exceed
+ * it (widths above 4096 with many rows) are invalid arguments. Calls that overlap on one GPU
+ * share the array and race. */
+hk_status hk_rms_norm_backward_noalloc(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
+                                       const hk_tensor* dy, const hk_tensor* rstd,
+                                       hk_tensor* dx, hk_tensor* dw);
 
 /* ---------------------------------------------------------------- softmax rows */
 

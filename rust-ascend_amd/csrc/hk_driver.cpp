@@ -49,7 +49,16 @@ struct Ctx {
     hk_stats stats{};
     void* workspace = nullptr;
     size_t ws_bytes = 0;
+    void* scratch = nullptr;  // device address of `scratch` below on this context's device
 };
+
+// Device memory of the allocation-free entry point (hk_rms_norm_backward_noalloc): its dgamma
+// partials live in this fixed array instead of the context workspace, so the call makes no
+// allocation. The array exists once per GPU for the life of the process. In host code its name
+// is only a stand-in for the symbol, not a device address: hk_init resolves the address with
+// hipGetSymbolAddress on the context's device, and every host-side use goes through Ctx::scratch.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 std::mutex g_init_mu;
 Ctx* g_ctx = nullptr;
@@ -397,8 +406,13 @@ hk_status hk_init(int32_t device, hk_context** out) {
     // Reference: NativeApi::check_soc requires the one supported SoC (deepgemm/native.rs:16-35).
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(HK_LOAD_ERROR, "device %d is %s; libhk.so carries gfx950 code only", device, prop.gcnArchName);
+    void* scratch_ptr = nullptr;
+    e = hipGetSymbolAddress(&scratch_ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || scratch_ptr == nullptr)
+        return fail(HK_LOAD_ERROR, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
     Ctx* c = new Ctx();
     c->device = device;
+    c->scratch = scratch_ptr;
     c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     c->stats.modules_loaded = 1;  // the fat binary linked into this library
     g_ctx = c;
@@ -1529,8 +1543,8 @@ hk_status hk_rms_norm(hk_context* h, const hk_tensor* x, const hk_tensor* w, dou
     return complete(g.c, e, "rms_norm", rows ? 1 : 0);
 }
 
-hk_status hk_rms_norm_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
-                               const hk_tensor* rstd, hk_tensor* dx, hk_tensor* dw) {
+static hk_status rms_backward_args(const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy, const hk_tensor* rstd,
+                                   const hk_tensor* dx, const hk_tensor* dw, int64_t* rows_out, int64_t* width_out) {
     // Reference: normalization.rs:168-186.
     if (!tensor_ok(x, "X") || !tensor_ok(w, "weight") || !tensor_ok(dy, "dY") || !tensor_ok(rstd, "rstd") ||
         !tensor_ok(dx, "dX") || !tensor_ok(dw, "dW"))
@@ -1545,14 +1559,44 @@ hk_status hk_rms_norm_backward(hk_context* h, const hk_tensor* x, const hk_tenso
     if (rstd->dtype != HK_F32 || numel(rstd) != rows) return fail(HK_INVALID_ARGUMENT, "rstd must be F32 [rows]");
     if (dw->dtype != HK_F32 || numel(dw) != width) return fail(HK_INVALID_ARGUMENT, "dW must be F32 [width]");
     if (!disjoint({dx, dw}, {x, w, dy, rstd})) return HK_INVALID_ARGUMENT;
+    *rows_out = rows;
+    *width_out = width;
+    return HK_OK;
+}
+
+hk_status hk_rms_norm_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                               const hk_tensor* rstd, hk_tensor* dx, hk_tensor* dw) {
+    int64_t rows, width;
+    hk_status st = rms_backward_args(x, w, dy, rstd, dx, dw, &rows, &width);
+    if (st != HK_OK) return st;
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
-    hk_status st = ensure_workspace(g.c, hk::rms_backward_workspace_bytes(rows, width));
-    if (st != HK_OK) return st;
+    if ((st = ensure_workspace(g.c, hk::rms_backward_workspace_bytes(rows, width))) != HK_OK) return st;
     hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
                                          static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
                                          static_cast<float*>(g.c->workspace), rows, width, g.c->stream);
     return complete(g.c, e, "rms_norm_backward", 2);
+}
+
+hk_status hk_rms_norm_backward_noalloc(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                                       const hk_tensor* rstd, hk_tensor* dx, hk_tensor* dw) {
+    int64_t rows, width;
+    hk_status st = rms_backward_args(x, w, dy, rstd, dx, dw, &rows, &width);
+    if (st != HK_OK) return st;
+    const size_t need = hk::rms_backward_workspace_bytes(rows, width);
+    if (need > kScratchBytes)
+        return fail(HK_INVALID_ARGUMENT,
+                    "rms_norm_backward_noalloc: %zu bytes of dgamma partials exceed its fixed %zu-byte device scratch "
+                    "(widths up to 4096 always fit; use hk_rms_norm_backward)",
+                    need, kScratchBytes);
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    // The same kernels as hk_rms_norm_backward; every partial is written before it is read, so the
+    // scratch needs no clearing. Overlapping calls on one GPU share the array and race.
+    hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
+                                         static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
+                                         static_cast<float*>(g.c->scratch), rows, width, g.c->stream);
+    return complete(g.c, e, "rms_norm_backward_noalloc", 2);
 }
 
 // ------------------------------------------------------------------ RoPE
