@@ -1,8 +1,13 @@
 """GPU: one Llama-style decoder layer (BASELINE C5's composition) forward and backward through
 libhk.so against float64 torch autograd of the same layer on the CPU, with the layer's own BF16
 parameters. The layer keeps BF16 activations (each rounding ~2^-9 relative), so the comparison is
-normwise: ||a - b|| / ||b|| <= 1e-2 for the output and every gradient, a bound that a wiring
-mistake (a missing residual, a transposed projection, an unrotated head) exceeds by far.
+normwise, ||a - b|| / ||b|| for the output and every gradient, against plain float64, with a bound
+set per tensor by the drift that BF16 storage causes: a float32 CPU evaluation of the same layer
+that rounds to BF16 wherever the layer stores BF16 (activations and their gradients) is measured
+against float64 in the same test, and the GPU may drift at most 1.5 times as far (+1e-3), never
+beyond 2e-2. At C5 both drift ~1e-2 (measured: GPU y 9.74e-3 / table 1.12e-2, model 9.75e-3 /
+1.11e-2), at the small shape ~5e-3. A wiring mistake (a missing residual, a transposed
+projection, an unrotated head) exceeds these by far.
 
 C5 itself (hidden 4096, 32/8 heads, FFN 14336, 2 x 2048 tokens) runs at full size on the GPU with
 dY nonzero only on the first 128 positions of each sequence. Attention is causal, so those
@@ -19,18 +24,51 @@ from rust_ascend_hip.decoder import rope_tables
 pytestmark = pytest.mark.gpu
 
 SMALL = DecoderConfig(hidden=256, heads=4, kv_heads=2, ffn=512, vocab=1000, batch=2, seq=128)
-TOL = 1e-2
+DRIFT_FACTOR = 1.5  # GPU's normwise distance from float64 <= 1.5 x the BF16-storage model's (+1e-3)
+PLAIN_TOL = 2e-2    # and never above 2e-2 (the model's drift is ~5e-3 here, ~1e-2 at C5)
 
 
-def reference(layer: DecoderLayer, ids, dy):
-    """float64 autograd of the layer over ids [B, S'] (S' <= the layer's seq: a prefix of each
-    sequence) with upstream dy [B*S', H]."""
+class _Bf16Storage(torch.autograd.Function):
+    """Where the GPU layer stores a BF16 activation: the forward value and the gradient that flows
+    back into it are both rounded to BF16 (RNE)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.to(torch.bfloat16).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+class _Bf16Grad(torch.autograd.Function):
+    """A consumer's copy of an already-rounded activation: the value passes, the gradient that
+    consumer produces is rounded (the GPU stores each consumer's gradient before adding them)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
+def reference(layer: DecoderLayer, ids, dy, emulate_bf16=False, dtype=torch.float64):
+    """Autograd of the layer in `dtype` (float64 by default) over ids [B, S'] (S' <= the layer's
+    seq: a prefix of each sequence) with upstream dy [B*S', H]. With emulate_bf16, every activation and activation
+    gradient the GPU layer stores in BF16 is rounded to BF16 at the same point (the weight
+    gradients stay unrounded, as the GPU keeps them in F32), so only accumulation order and the
+    fused attention's internal roundings remain as differences."""
     c = layer.cfg
-    P = {k: getattr(layer, k).detach().double().cpu().requires_grad_(True)
+    P = {k: getattr(layer, k).detach().cpu().to(dtype).requires_grad_(True)
          for k in ("table", "wqkv", "wo", "wg", "wu", "wd", "w1", "w2")}
     seq = ids.shape[1]
     T, H, D, hq, hkv = c.batch * seq, c.hidden, c.head_dim, c.heads, c.kv_heads
-    cos, sin = (torch.from_numpy(t).double() for t in rope_tables(seq, D, c.theta))
+    cos, sin = (torch.from_numpy(t).to(dtype) for t in rope_tables(seq, D, c.theta))
+    dy = dy.to(dtype)
+    R = _Bf16Storage.apply if emulate_bf16 else (lambda t: t)
+    G = _Bf16Grad.apply if emulate_bf16 else (lambda t: t)
 
     def rms(x, w):
         return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + c.eps) * w
@@ -39,18 +77,18 @@ def reference(layer: DecoderLayer, ids, dy):
         a, b = x[..., :D // 2], x[..., D // 2:]
         return torch.cat([a * cos - b * sin, b * cos + a * sin], -1)
 
-    x0 = P["table"][ids.reshape(-1)]
-    n1 = rms(x0, P["w1"])
-    qkv = (n1 @ P["wqkv"].T).reshape(c.batch, seq, hq + 2 * hkv, D).permute(0, 2, 1, 3)
-    q, k, v = rope(qkv[:, :hq]), rope(qkv[:, hq:hq + hkv]), qkv[:, hq + hkv:]
+    x0 = R(P["table"][ids.reshape(-1)])                      # dx0 = bf16(dx0_norm + dh1)
+    n1 = R(rms(G(x0), P["w1"]))                               # dx0_norm rounded
+    qkv = R(n1 @ P["wqkv"].T).reshape(c.batch, seq, hq + 2 * hkv, D).permute(0, 2, 1, 3)
+    q, k, v = R(rope(qkv[:, :hq])), R(rope(qkv[:, hq:hq + hkv])), G(qkv[:, hq + hkv:])
     k, v = k.repeat_interleave(hq // hkv, 1), v.repeat_interleave(hq // hkv, 1)
     s = (q @ k.transpose(-1, -2)) * D ** -0.5
     s = s.masked_fill(torch.triu(torch.ones(seq, seq, dtype=torch.bool), 1), float("-inf"))
-    o = (torch.softmax(s, -1) @ v).permute(0, 2, 1, 3).reshape(T, H)
-    h1 = x0 + o @ P["wo"].T
-    n2 = rms(h1, P["w2"])
-    m = torch.nn.functional.silu(n2 @ P["wg"].T) * (n2 @ P["wu"].T)
-    y = h1 + m @ P["wd"].T
+    o = R(torch.softmax(s, -1) @ v).permute(0, 2, 1, 3).reshape(T, H)
+    h1 = R(x0 + R(o @ P["wo"].T))                              # dh1 = bf16(dh1_norm + dy)
+    n2 = R(rms(G(h1), P["w2"]))                                # dn2 = bf16(dn2_g + dn2_u)
+    m = R(torch.nn.functional.silu(R(G(n2) @ P["wg"].T)) * R(G(n2) @ P["wu"].T))
+    y = R(h1 + R(m @ P["wd"].T))
     (y * dy).sum().backward()
     return y.detach(), {k: t.grad for k, t in P.items()}
 
@@ -62,23 +100,29 @@ def normwise(a, b):
 
 def check_layer(layer: DecoderLayer, ids, dy, prefix: int):
     """Run the layer on the GPU and compare the first `prefix` positions of each sequence (dy must
-    be zero after them) and every parameter gradient with the float64 reference."""
+    be zero after them) and every parameter gradient with plain float64 autograd of the same
+    layer. The layer stores BF16 activations, so it drifts from float64 by an amount its depth
+    and widths set; the bound is that drift as a float32 CPU evaluation of the same layer with
+    the same BF16 storage points shows it (the model), times DRIFT_FACTOR, per tensor, and never
+    more than PLAIN_TOL."""
     c = layer.cfg
     y = layer.forward(ids)[:, :prefix].float().cpu().numpy().reshape(c.batch * prefix, c.hidden)
     grads = {k: v.float().cpu().numpy() for k, v in layer.backward(dy).items()}
-    y_ref, g_ref = reference(layer, ids[:, :prefix].cpu(),
-                             dy[:, :prefix].double().cpu().reshape(c.batch * prefix, c.hidden))
-    errors = {"y": normwise(y, y_ref.numpy())}
     used = np.unique(ids[:, :prefix].cpu().numpy())
-    for k, ref in g_ref.items():
-        ref = ref.numpy()
-        got = grads[k]
+    assert not np.any(np.delete(grads["table"], used, axis=0)), "rows of IDs without a gradient must stay zero"
+    args = (ids[:, :prefix].cpu(), dy[:, :prefix].double().cpu().reshape(c.batch * prefix, c.hidden))
+    y64, g64 = reference(layer, *args)
+    y32, g32 = reference(layer, *args, emulate_bf16=True, dtype=torch.float32)
+    gpu, model = {"y": normwise(y, y64.numpy())}, {"y": normwise(y32.numpy(), y64.numpy())}
+    for k, ref in g64.items():
+        ref, got, mod = ref.numpy(), grads[k], g32[k].numpy()
         if k == "table":
-            assert not np.any(np.delete(got, used, axis=0)), "rows of IDs without a gradient must stay zero"
-            got, ref = got[used], ref[used]
-        errors[k] = normwise(got, ref)
-    print({k: f"{v:.2e}" for k, v in errors.items()}, flush=True)
-    assert max(errors.values()) <= TOL, errors
+            ref, got, mod = ref[used], got[used], mod[used]
+        gpu[k], model[k] = normwise(got, ref), normwise(mod, ref)
+    print("GPU vs float64", {k: f"{v:.2e}" for k, v in gpu.items()}, flush=True)
+    print("model vs float64", {k: f"{v:.2e}" for k, v in model.items()}, flush=True)
+    for k in gpu:
+        assert gpu[k] <= min(DRIFT_FACTOR * model[k] + 1e-3, PLAIN_TOL), (k, gpu[k], model[k])
     return grads
 
 
