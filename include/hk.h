@@ -406,7 +406,9 @@ hk_status hk_rotary_prefix_backward(hk_context* ctx, const hk_tensor* dy, const 
 
 /* Fused causal/non-causal grouped-query attention forward (FlashAttention-style,
  * online softmax, nothing materialized).
- *   q [B,Hq,M,D], k/v [B,Hkv,N,D] BF16; o [B,Hq,M,D] BF16; lse [B,Hq,M] F32
+ *   q [B,Hq,M,D], k/v [B,Hkv,N,D] all BF16, or all F32 (the reference's FP32 surface: rounded
+ *   to BF16 in the workspace first, as its matmul_bf16_fp32 rounds GEMM operands);
+ *   o [B,Hq,M,D] BF16 or F32; lse [B,Hq,M] F32
  *   (natural-log logsumexp of the scaled, masked scores, saved for backward).
  *   Hq % Hkv == 0 and query head h reads KV head h / (Hq/Hkv) (heads_programs.rs:5-60).
  *   Causal: key j is excluded when key_start + j > query_start + i (mask_programs.rs:5-40).
@@ -418,8 +420,30 @@ hk_status hk_attention_forward(hk_context* ctx, const hk_tensor* q, const hk_ten
                                const hk_tensor* v, float scale, int32_t causal,
                                uint64_t query_start, uint64_t key_start,
                                hk_tensor* o, hk_tensor* lse);
+/* Materialized attention with an optional additive mask, the reference's composed path:
+ * scaled_dot_product_attention_bf16_fp32 (rank 3: Q[B,M,D], K[B,N,D], V[B,N,Dv], mask F32 [B,M,N])
+ * and grouped_query_attention_bf16_fp32 (rank 4: Q[B,Hq,M,D], K[B,Hkv,N,D], V[B,Hkv,N,Dv], mask F32
+ * [B,Hq,M,N]), src/nn/attention.rs:10-67. O = bf16(softmax(bf16(Q) bf16(K)^T * scale + mask))
+ * bf16(V), scores and softmax F32, O [.., M, Dv] F32 (or BF16). Q/K/V are F32 as in the reference
+ * (BF16 also accepted); mask may be NULL. validate_dimensions' rules apply (src/nn/attention.rs:
+ * 95-104): B*Hq in 1..4096, M/D/Dv positive multiples of 16, N a positive multiple of 32, a finite
+ * scale, B*Hq*M*N within u32. Rows whose mask excludes every key give NaN, as the reference's
+ * softmax does. */
+hk_status hk_attention_masked_forward(hk_context* ctx, const hk_tensor* q, const hk_tensor* k,
+                                      const hk_tensor* v, float scale, const hk_tensor* mask,
+                                      hk_tensor* o);
+/* Backward of hk_attention_masked_forward (the reference's autodiff chain: matmul_bf16_fp32 and
+ * SoftmaxBackward, src/nn.rs:234-278,375-453): P is recomputed from Q, K and the mask; dP =
+ * bf16(dO) bf16(V)^T, dS = P * (dP - rowsum(P * dP)), dMask = dS (F32, shaped like the mask;
+ * NULL when not wanted), dQ = bf16(scale dS) bf16(K), dK = bf16(scale dS)^T bf16(Q) summed over
+ * each KV head's query heads, dV = bf16(P)^T bf16(dO). dO F32 (or BF16); dq/dk/dv F32 or BF16. */
+hk_status hk_attention_masked_backward(hk_context* ctx, const hk_tensor* q, const hk_tensor* k,
+                                       const hk_tensor* v, const hk_tensor* mask,
+                                       const hk_tensor* dout, float scale, hk_tensor* dq,
+                                       hk_tensor* dk, hk_tensor* dv, hk_tensor* dmask);
 /* Backward of hk_attention_forward from saved o and lse: dq [B,Hq,M,D],
- * dk/dv [B,Hkv,N,D] (F32 or BF16). dK/dV sum over the query heads of each group in a
+ * dk/dv [B,Hkv,N,D] (F32 or BF16). Q/K/V, O and dO may each be F32 (F32 inputs are rounded to
+ * BF16 first; an F32 O enters the row term rowsum(dO * O) unrounded). dK/dV sum over the query heads of each group in a
  * fixed order (no atomics), the deterministic analogue of repeat_kv_heads_backward
  * (runtime/heads.rs:29-51). dS is scaled then rounded to BF16, as the reference's
  * MatmulBf16Fp32Backward chain does (examples/grouped_attention_tensor.rs:30-40). */

@@ -408,24 +408,30 @@ int or_rotary_prefix(const float* x, const int64_t* in_shape, const int64_t* tab
  * excluded). `mask` (optional, [B,Hq,M,N] additive) is used when causal == 0.
  * Rows whose keys are all excluded produce zeros and lse = -inf (the composed
  * reference produces NaN there; see the attention kernel's documentation).
- * Any of out/lse/dq/dk/dv/mag may be NULL; dq/dk/dv require dy. Outputs are overwritten. */
+ * V, dY and the output have the value width dw (d == dw in the fused kernels' domain;
+ * src/nn/attention.rs:49-52 allows any). dmask (optional, [B,Hq,M,N]) receives the mask
+ * gradient dS = P (dP - rowsum(P dP)), the scores' gradient before the scale.
+ * Any of out/lse/dq/dk/dv/mag/dmask may be NULL; dq/dk/dv/dmask require dy. Outputs are
+ * overwritten. */
 void or_attention_f64(const float* q, const float* k, const float* v, const float* dy,
                       const float* mask, int64_t batch, int64_t heads, int64_t kv_heads,
-                      int64_t m, int64_t n, int64_t d, double scale, int causal,
+                      int64_t m, int64_t n, int64_t d, int64_t dw, double scale, int causal,
                       uint64_t query_start, uint64_t key_start, double* out, double* lse,
-                      double* dq, double* dk, double* dv, double* mag) {
+                      double* dq, double* dk, double* dv, double* mag, double* dmask) {
     int64_t group = heads / kv_heads;
-    if (out) memset(out, 0, sizeof(double) * (size_t)(batch * heads * m * d));
+    if (out) memset(out, 0, sizeof(double) * (size_t)(batch * heads * m * dw));
     if (dq) memset(dq, 0, sizeof(double) * (size_t)(batch * heads * m * d));
     if (dk) memset(dk, 0, sizeof(double) * (size_t)(batch * kv_heads * n * d));
-    if (dv) memset(dv, 0, sizeof(double) * (size_t)(batch * kv_heads * n * d));
+    if (dv) memset(dv, 0, sizeof(double) * (size_t)(batch * kv_heads * n * dw));
+    if (dmask) memset(dmask, 0, sizeof(double) * (size_t)(batch * heads * m * n));
     /* mag (optional): the same sums over the absolute values of their terms, laid out as
      * [out | dq | dk | dv]; sum |terms| bounds the effect of rounding any term. */
     double* out_m = mag;
-    double* dq_m = mag ? mag + batch * heads * m * d : NULL;
+    double* dq_m = mag ? mag + batch * heads * m * dw : NULL;
     double* dk_m = mag ? dq_m + batch * heads * m * d : NULL;
     double* dv_m = mag ? dk_m + batch * kv_heads * n * d : NULL;
-    if (mag) memset(mag, 0, sizeof(double) * (size_t)(2 * batch * heads * m * d + 2 * batch * kv_heads * n * d));
+    if (mag)
+        memset(mag, 0, sizeof(double) * (size_t)(batch * heads * m * (d + dw) + batch * kv_heads * n * (d + dw)));
     /* Parallel over (batch, kv head): the group's query heads run sequentially inside,
      * so dk/dv accumulate in a fixed order without races. */
 #pragma omp parallel for schedule(dynamic) collapse(2)
@@ -437,7 +443,7 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
             for (int64_t h = kv * group; h < (kv + 1) * group; ++h) {
                 const float* qh = q + ((b * heads + h) * m) * d;
                 const float* kh = k + ((b * kv_heads + kv) * n) * d;
-                const float* vh = v + ((b * kv_heads + kv) * n) * d;
+                const float* vh = v + ((b * kv_heads + kv) * n) * dw;
                 for (int64_t row = 0; row < m; ++row) {
                     double mx = -INFINITY;
                     for (int64_t j = 0; j < n; ++j) {
@@ -463,32 +469,33 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
                         for (int64_t j = 0; j < n; ++j) {
                             double pb = (double)bf16r((float)p[j]);
                             if (pb == 0.0) continue;
-                            for (int64_t c = 0; c < d; ++c) out[oi * d + c] += pb * (double)bf16r(vh[j * d + c]);
+                            for (int64_t c = 0; c < dw; ++c) out[oi * dw + c] += pb * (double)bf16r(vh[j * dw + c]);
                             if (out_m)
-                                for (int64_t c = 0; c < d; ++c) out_m[oi * d + c] += fabs(pb * (double)bf16r(vh[j * d + c]));
+                                for (int64_t c = 0; c < dw; ++c) out_m[oi * dw + c] += fabs(pb * (double)bf16r(vh[j * dw + c]));
                         }
                     }
                     if (!dy) continue;
-                    const float* g = dy + oi * d;
+                    const float* g = dy + oi * dw;
                     double dot = 0.0, dot_mag = 0.0, dot_mag_o = 0.0;
                     for (int64_t j = 0; j < n; ++j) {
                         double acc = 0.0;
-                        for (int64_t c = 0; c < d; ++c) acc += (double)bf16r(g[c]) * (double)bf16r(vh[j * d + c]);
+                        for (int64_t c = 0; c < dw; ++c) acc += (double)bf16r(g[c]) * (double)bf16r(vh[j * dw + c]);
                         dp[j] = acc;
                         dot += p[j] * acc;
                         dot_mag += p[j] * fabs(acc);
                     }
                     if (mag && out) {
-                        for (int64_t c = 0; c < d; ++c) dot_mag_o += fabs((double)bf16r(g[c]) * out[oi * d + c]);
+                        for (int64_t c = 0; c < dw; ++c) dot_mag_o += fabs((double)bf16r(g[c]) * out[oi * dw + c]);
                         if (dot_mag_o > dot_mag) dot_mag = dot_mag_o;
                     }
                     for (int64_t j = 0; j < n; ++j) {
                         double ds = p[j] * (dp[j] - dot);
                         double pb = (double)bf16r((float)p[j]);
                         double dsb = (double)bf16r((float)(scale * ds));
+                        if (dmask) dmask[oi * n + j] = ds;
                         if (dv) {
-                            double* dvh = dv + ((b * kv_heads + kv) * n + j) * d;
-                            for (int64_t c = 0; c < d; ++c) dvh[c] += pb * (double)bf16r(g[c]);
+                            double* dvh = dv + ((b * kv_heads + kv) * n + j) * dw;
+                            for (int64_t c = 0; c < dw; ++c) dvh[c] += pb * (double)bf16r(g[c]);
                         }
                         if (dq) {
                             for (int64_t c = 0; c < d; ++c) dq[oi * d + c] += dsb * (double)bf16r(kh[j * d + c]);
@@ -502,10 +509,10 @@ void or_attention_f64(const float* q, const float* k, const float* v, const floa
                              * magnitude is the larger of sum_j p_j |dp_j| (its form here) and
                              * sum_d |dY_d O_d| (the form rowsum(dY o O) a fused kernel uses). */
                             double dsm = scale * p[j] * (fabs(dp[j]) + dot_mag);
-                            double* dvm = dv_m + ((b * kv_heads + kv) * n + j) * d;
+                            double* dvm = dv_m + ((b * kv_heads + kv) * n + j) * dw;
                             double* dkm = dk_m + ((b * kv_heads + kv) * n + j) * d;
+                            for (int64_t c = 0; c < dw; ++c) dvm[c] += fabs(pb * (double)bf16r(g[c]));
                             for (int64_t c = 0; c < d; ++c) {
-                                dvm[c] += fabs(pb * (double)bf16r(g[c]));
                                 dq_m[oi * d + c] += dsm * fabs((double)bf16r(kh[j * d + c]));
                                 dkm[c] += dsm * fabs((double)bf16r(qh[row * d + c]));
                             }

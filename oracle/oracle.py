@@ -70,7 +70,9 @@ a wrong sign or index, or a transposed operand fails at least one check:
   examples/causal_attention_tensor.rs:31-55 (Q=K=0 causal -> running means), the
   exact mask patterns of causal_attention_tensor.rs:23-30, and torch float64
   autograd of softmax(scale*QK^T+mask)V at the reference's tolerance
-  (grouped_attention_tensor.rs:10, 2e-3+3e-3|b|) on the reference's five GQA cases.
+  (grouped_attention_tensor.rs:10, 2e-3+3e-3|b|) on the reference's five GQA cases,
+  the mask gradient included, and on random cases with a value width other than the
+  head width.
 """
 from __future__ import annotations
 
@@ -125,9 +127,9 @@ def lib():
         L.or_rotary_prefix.argtypes = [_f32p, _i64p, _i64p, _int, _i64, _int, _int, _f32p, _f32p, _f32p]
         L.or_rotary_prefix.restype = _int
         _vp = ctypes.c_void_p
-        L.or_attention_f64.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+        L.or_attention_f64.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                        ctypes.c_double, _int, ctypes.c_uint64, ctypes.c_uint64,
-                                       _vp, _vp, _vp, _vp, _vp, _vp]
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp]
         L.or_causal_mask.argtypes = [_i64, _i64, _i64, ctypes.c_uint64, ctypes.c_uint64, _f32p]
         L.or_softmax_f64.argtypes = [_f32p, _i64, _i64, _int, _f64p]
         L.or_repeat_kv_backward.argtypes = [_f32p, _i64, _i64, _i64, _f32p]
@@ -499,40 +501,45 @@ def rope_tables(positions, dim: int, theta: float):
 
 def attention_f64(q, k, v, dy=None, scale=0.25, causal=False, query_start=0, key_start=0,
                   mask=None, want_grads=True, magnitudes=False):
-    """Returns dict(out, lse[, dq, dk, dv]) in f64 for q [B,Hq,M,D], k/v [B,Hkv,N,D]. With
-    magnitudes=True also out_mag/dq_mag/dk_mag/dv_mag: each output's sum over the absolute
-    values of its terms (the scale against which a rounding of any term is measured)."""
+    """Returns dict(out, lse[, dq, dk, dv[, dmask]]) in f64 for q [B,Hq,M,D], k [B,Hkv,N,D],
+    v [B,Hkv,N,Dv]. With a mask (additive, [B,Hq,M,N], used when not causal) and dy, also dmask,
+    the gradient of the masked scores. With magnitudes=True also out_mag/dq_mag/dk_mag/dv_mag:
+    each output's sum over the absolute values of its terms (the scale against which a rounding
+    of any term is measured)."""
     q = _c32(q)
     k = _c32(k)
     v = _c32(v)
     B, H, M, D = q.shape
-    Hkv, N = k.shape[1], k.shape[2]
-    out = np.empty((B, H, M, D), dtype=np.float64)
+    Hkv, N, Dv = k.shape[1], k.shape[2], v.shape[3]
+    out = np.empty((B, H, M, Dv), dtype=np.float64)
     lse = np.empty((B, H, M), dtype=np.float64)
     res = {"out": out, "lse": lse}
     ptr = lambda a: None if a is None else a.ctypes.data
-    dq = dk = dv = None
+    dq = dk = dv = dmask = None
     dyc = None
+    maskc = None if mask is None else _c32(mask)
     if dy is not None:
         dyc = _c32(dy)
         if want_grads:
-            dq = np.empty_like(out)
+            dq = np.empty((B, H, M, D), dtype=np.float64)
             dk = np.empty((B, Hkv, N, D), dtype=np.float64)
-            dv = np.empty_like(dk)
+            dv = np.empty((B, Hkv, N, Dv), dtype=np.float64)
             res.update(dq=dq, dk=dk, dv=dv)
-    maskc = None if mask is None else _c32(mask)
+        if maskc is not None and not causal:
+            dmask = np.empty((B, H, M, N), dtype=np.float64)
+            res["dmask"] = dmask
     mag = None
     if magnitudes:
-        mag = np.empty(2 * B * H * M * D + 2 * B * Hkv * N * D, dtype=np.float64)
-    lib().or_attention_f64(ptr(q), ptr(k), ptr(v), ptr(dyc), ptr(maskc), B, H, Hkv, M, N, D,
+        mag = np.empty(B * H * M * (D + Dv) + B * Hkv * N * (D + Dv), dtype=np.float64)
+    lib().or_attention_f64(ptr(q), ptr(k), ptr(v), ptr(dyc), ptr(maskc), B, H, Hkv, M, N, D, Dv,
                            float(scale), int(bool(causal)), int(query_start), int(key_start),
-                           ptr(out), ptr(lse), ptr(dq), ptr(dk), ptr(dv), ptr(mag))
+                           ptr(out), ptr(lse), ptr(dq), ptr(dk), ptr(dv), ptr(mag), ptr(dmask))
     if magnitudes:
-        a, c = B * H * M * D, B * Hkv * N * D
+        a, aq, c, cv = B * H * M * Dv, B * H * M * D, B * Hkv * N * D, B * Hkv * N * Dv
         res["out_mag"] = mag[:a].reshape(out.shape)
-        res["dq_mag"] = mag[a:2 * a].reshape(out.shape)
-        res["dk_mag"] = mag[2 * a:2 * a + c].reshape((B, Hkv, N, D))
-        res["dv_mag"] = mag[2 * a + c:].reshape((B, Hkv, N, D))
+        res["dq_mag"] = mag[a:a + aq].reshape((B, H, M, D))
+        res["dk_mag"] = mag[a + aq:a + aq + c].reshape((B, Hkv, N, D))
+        res["dv_mag"] = mag[a + aq + c:a + aq + c + cv].reshape((B, Hkv, N, Dv))
     return res
 
 

@@ -125,7 +125,8 @@ struct FwdArgs {
     const uint16_t* q;
     const uint16_t* k;
     const uint16_t* v;
-    uint16_t* o;
+    void* o;     // BF16, or F32 when o_f32 (the reference's FP32 output surface)
+    int o_f32;
     float* lse;
     int64_t heads, kv_heads, m, n;
     int64_t diag;  // key j is visible to query i iff j <= i + diag (causal only)
@@ -133,6 +134,17 @@ struct FwdArgs {
     int causal;
     int mblocks;
 };
+
+// Four consecutive output elements of O at element offset `off` (a multiple of 4): packed BF16
+// (RNE), or F32 when the caller asked for the FP32 output.
+__device__ __forceinline__ void store_o4(const FwdArgs& a, int64_t off, float x0, float x1, float x2, float x3) {
+    if (a.o_f32) {
+        *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.o) + off) = f32x4_t{x0, x1, x2, x3};
+    } else {
+        const u32x2_t w = {pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(a.o) + off) = w;
+    }
+}
 
 // Tile rows [row0, row0+64) of a [N, D] matrix -> registers (rows >= n clamp to n-1), laid
 // out in LDS as [64][DP] with DP = max(D, 32); columns >= D are zero.
@@ -377,16 +389,15 @@ attn_fwd(FwdArgs a) {
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < a.m) {
-        uint16_t* orow = a.o + (bh * a.m + my_q) * D;
+        const int64_t obase = (bh * a.m + my_q) * D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d = 32 * dt + 8 * g + 4 * lg;
                 if (d >= D) continue;
-                u32x2_t w = {pack_bf16x2(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv),
-                             pack_bf16x2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
-                *reinterpret_cast<u32x2_t*>(orow + d) = w;
+                store_o4(a, obase + d, o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                         o[dt][4 * g + 3] * inv);
             }
         if (lg == 0)
             a.lse[bh * a.m + my_q] = l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
@@ -711,15 +722,14 @@ attn_fwd_pp(FwdArgs a) {
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < a.m) {
-        uint16_t* orow = a.o + (bh * a.m + my_q) * D;
+        const int64_t obase = (bh * a.m + my_q) * D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d = 32 * dt + 8 * g + 4 * lg;
-                u32x2_t w = {pack_bf16x2(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv),
-                             pack_bf16x2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
-                *reinterpret_cast<u32x2_t*>(orow + d) = w;
+                store_o4(a, obase + d, o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                         o[dt][4 * g + 3] * inv);
             }
         if (lg == 0)
             a.lse[bh * a.m + my_q] = l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
@@ -746,7 +756,8 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
     a.q = static_cast<const uint16_t*>(q);
     a.k = static_cast<const uint16_t*>(k);
     a.v = static_cast<const uint16_t*>(v);
-    a.o = static_cast<uint16_t*>(o);
+    a.o = o;
+    a.o_f32 = sh.o_f32;
     a.lse = lse;
     a.heads = sh.heads;
     a.kv_heads = sh.kv_heads;
@@ -772,9 +783,10 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
 // Pre-pass: rowstat[bh, i] = sum_d dO[i, d] * O[i, d] (F32). With O = P V this equals
 // sum_j P_ij dP_ij, the softmax-backward row term of row_programs.rs:152-163. It also writes
 // lse2 = lse * log2(e), the form in which the gradient kernels use the row's log-sum-exp.
-template <int D>
+// O is BF16, or F32 (the FP32 output surface: the row term then carries no rounding of O).
+template <int D, typename TO>
 __global__ void __launch_bounds__(256)
-attn_bwd_rowstat(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dout, const float* __restrict__ lse,
+attn_bwd_rowstat(const TO* __restrict__ o, const uint16_t* __restrict__ dout, const float* __restrict__ lse,
                  float* __restrict__ stat, float* __restrict__ lse2, int64_t rows) {
     constexpr int kLanesPerRow = D / 8;  // each lane reads 8 elements
     constexpr int kRowsPerBlock = 256 / kLanesPerRow;
@@ -1264,8 +1276,12 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
     constexpr int lanes = D / 8;
     const int64_t threads = rows * lanes;
     float* lse2 = stat + rows;
-    hipLaunchKernelGGL((attn_bwd_rowstat<D>), dim3(flat_blocks(threads, 256)), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, stat, lse2, rows);
+    if (sh.o_f32)
+        hipLaunchKernelGGL((attn_bwd_rowstat<D, float>), dim3(flat_blocks(threads, 256)), dim3(256), 0, s,
+                           static_cast<const float*>(o), static_cast<const uint16_t*>(dout), lse, stat, lse2, rows);
+    else
+        hipLaunchKernelGGL((attn_bwd_rowstat<D, uint16_t>), dim3(flat_blocks(threads, 256)), dim3(256), 0, s,
+                           static_cast<const uint16_t*>(o), static_cast<const uint16_t*>(dout), lse, stat, lse2, rows);
     BwdArgs a;
     a.q = static_cast<const uint16_t*>(q);
     a.k = static_cast<const uint16_t*>(k);

@@ -1677,8 +1677,8 @@ static hk_status attention_shape(const hk_tensor* q, const hk_tensor* k, const h
     if (!tensor_ok(q, "Q") || !tensor_ok(k, "K") || !tensor_ok(v, "V")) return HK_INVALID_ARGUMENT;
     if (q->rank != 4 || k->rank != 4 || v->rank != 4)
         return fail(HK_INVALID_ARGUMENT, "attention requires rank-4 Q[B,Hq,M,D], K/V[B,Hkv,N,D]");
-    if (q->dtype != HK_BF16 || k->dtype != HK_BF16 || v->dtype != HK_BF16)
-        return fail(HK_INVALID_ARGUMENT, "fused attention requires BF16 Q/K/V");
+    if ((q->dtype != HK_BF16 && q->dtype != HK_F32) || k->dtype != q->dtype || v->dtype != q->dtype)
+        return fail(HK_INVALID_ARGUMENT, "fused attention requires Q/K/V all BF16 or all F32");
     const int64_t B = q->shape[0], H = q->shape[1], M = q->shape[2], D = q->shape[3];
     const int64_t Hkv = k->shape[1], N = k->shape[2];
     // Reference: validate_gqa / validate_dimensions, src/nn/attention.rs:81-104.
@@ -1713,22 +1713,49 @@ static hk_status attention_shape(const hk_tensor* q, const hk_tensor* k, const h
     return HK_OK;
 }
 
+namespace {
+// F32 Q/K/V/dO (the reference's FP32 attention surface) are rounded to BF16 (RNE) into the
+// workspace before the fused kernels run, as the reference's matmul_bf16_fp32 rounds every GEMM
+// operand; BF16 inputs are used in place.
+struct Staged {
+    const void* p;
+    size_t bytes;  // workspace bytes it takes (0 when used in place)
+};
+Staged staged(const hk_tensor* t) {
+    return {t->data, t->dtype == HK_F32 ? ws_round(static_cast<size_t>(numel(t)) * 2) : 0};
+}
+hipError_t stage(const hk_tensor* t, Staged& st, char*& cursor, hipStream_t s) {
+    if (!st.bytes) return hipSuccess;
+    st.p = cursor;
+    cursor += st.bytes;
+    return hk::cast_apply(1, t->data, const_cast<void*>(st.p), numel(t), s);
+}
+}  // namespace
+
 hk_status hk_attention_forward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v, float scale,
                                int32_t causal, uint64_t qs, uint64_t ks, hk_tensor* o, hk_tensor* lse) {
     hk::AttnShape sh;
     hk_status st = attention_shape(q, k, v, scale, causal, qs, ks, &sh);
     if (st != HK_OK) return st;
     if (!tensor_ok(o, "O") || !tensor_ok(lse, "lse")) return HK_INVALID_ARGUMENT;
-    if (o->dtype != HK_BF16 || !same_shape(o, q)) return fail(HK_INVALID_ARGUMENT, "O must be BF16 shaped like Q");
+    if ((o->dtype != HK_BF16 && o->dtype != HK_F32) || !same_shape(o, q))
+        return fail(HK_INVALID_ARGUMENT, "O must be BF16 or F32 shaped like Q");
     if (lse->dtype != HK_F32 || lse->rank != 3 || lse->shape[0] != sh.batch || lse->shape[1] != sh.heads ||
         lse->shape[2] != sh.m)
         return fail(HK_INVALID_ARGUMENT, "lse must be F32 [B,Hq,M]");
     if (!disjoint({o, lse}, {q, k, v})) return HK_INVALID_ARGUMENT;
+    sh.o_f32 = o->dtype == HK_F32;
+    Staged sq = staged(q), sk = staged(k), sv = staged(v);
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
-    hipError_t e = hk::attention_forward(sh, q->data, k->data, v->data, o->data, static_cast<float*>(lse->data),
-                                         g.c->stream);
-    return complete(g.c, e, "attention_forward", 1);
+    if ((st = ensure_workspace(g.c, sq.bytes + sk.bytes + sv.bytes)) != HK_OK) return st;
+    char* cursor = static_cast<char*>(g.c->workspace);
+    hipError_t e = stage(q, sq, cursor, g.c->stream);
+    if (e == hipSuccess) e = stage(k, sk, cursor, g.c->stream);
+    if (e == hipSuccess) e = stage(v, sv, cursor, g.c->stream);
+    if (e == hipSuccess)
+        e = hk::attention_forward(sh, sq.p, sk.p, sv.p, o->data, static_cast<float*>(lse->data), g.c->stream);
+    return complete(g.c, e, "attention_forward", 1 + (sq.bytes ? 3 : 0));
 }
 
 hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
@@ -1741,8 +1768,9 @@ hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tens
     if (!tensor_ok(o, "O") || !tensor_ok(lse, "lse") || !tensor_ok(dout, "dO") || !tensor_ok(dq, "dQ") ||
         !tensor_ok(dk, "dK") || !tensor_ok(dv, "dV"))
         return HK_INVALID_ARGUMENT;
-    if (o->dtype != HK_BF16 || !same_shape(o, q) || dout->dtype != HK_BF16 || !same_shape(dout, q))
-        return fail(HK_INVALID_ARGUMENT, "O and dO must be BF16 shaped like Q");
+    if ((o->dtype != HK_BF16 && o->dtype != HK_F32) || !same_shape(o, q) ||
+        (dout->dtype != HK_BF16 && dout->dtype != HK_F32) || !same_shape(dout, q))
+        return fail(HK_INVALID_ARGUMENT, "O and dO must be BF16 or F32 shaped like Q");
     if (lse->dtype != HK_F32 || lse->rank != 3 || lse->shape[0] != sh.batch || lse->shape[1] != sh.heads ||
         lse->shape[2] != sh.m)
         return fail(HK_INVALID_ARGUMENT, "lse must be F32 [B,Hq,M]");
@@ -1752,13 +1780,241 @@ hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tens
         dv->dtype != dk->dtype)
         return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must be F32 or BF16 (dK and dV alike)");
     if (!disjoint({dq, dk, dv}, {q, k, v, o, lse, dout})) return HK_INVALID_ARGUMENT;
+    sh.o_f32 = o->dtype == HK_F32;
+    Staged sq = staged(q), sk = staged(k), sv = staged(v), sd = staged(dout);
+    const size_t stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
-    if ((st = ensure_workspace(g.c, hk::attention_bwd_workspace_bytes(sh))) != HK_OK) return st;
-    hipError_t e = hk::attention_backward(sh, q->data, k->data, v->data, o->data, static_cast<const float*>(lse->data),
-                                          dout->data, dq->data, dq->dtype == HK_BF16, dk->data, dv->data,
-                                          dk->dtype == HK_BF16, g.c->workspace, g.c->stream);
-    return complete(g.c, e, "attention_backward", 3);
+    if ((st = ensure_workspace(g.c, stat_bytes + sq.bytes + sk.bytes + sv.bytes + sd.bytes)) != HK_OK) return st;
+    char* cursor = static_cast<char*>(g.c->workspace) + stat_bytes;
+    hipError_t e = stage(q, sq, cursor, g.c->stream);
+    if (e == hipSuccess) e = stage(k, sk, cursor, g.c->stream);
+    if (e == hipSuccess) e = stage(v, sv, cursor, g.c->stream);
+    if (e == hipSuccess) e = stage(dout, sd, cursor, g.c->stream);
+    if (e == hipSuccess)
+        e = hk::attention_backward(sh, sq.p, sk.p, sv.p, o->data, static_cast<const float*>(lse->data), sd.p,
+                                   dq->data, dq->dtype == HK_BF16, dk->data, dv->data, dk->dtype == HK_BF16,
+                                   g.c->workspace, g.c->stream);
+    return complete(g.c, e, "attention_backward", 3 + (sq.bytes ? 3 : 0) + (sd.bytes ? 1 : 0));
+}
+
+// ------------------------------------------------------------------ composed attention
+//
+// The reference's materialized attention (src/nn/attention.rs:10-67): additive masks, value widths
+// other than the head width, and head widths the fused kernels do not take. Same rounding points as
+// the reference's chain of matmul_bf16_fp32 / softmax: S = bf16(Q) bf16(K)^T (F32), S = S * scale
+// (+ mask), P = softmax(S) (F32), O = bf16(P) bf16(V). GQA needs no repeated K/V: the Hq/Hkv query
+// heads of one KV head are consecutive, so Q viewed as [B*Hkv, (Hq/Hkv)*M, D] multiplies that KV
+// head's [N, D] directly, and the scores come out in the [B, Hq, M, N] layout of the mask.
+
+namespace {
+
+struct ComposedShape {
+    int64_t batch = 0, heads = 1, kv_heads = 1, m = 0, n = 0, d = 0, dv = 0;
+    int64_t groups() const { return batch * kv_heads; }      // GEMM batches: one per (b, KV head)
+    int64_t rows() const { return heads / kv_heads * m; }    // query rows per GEMM batch
+    int64_t scores() const { return batch * heads * m * n; }
+};
+
+hk_status composed_shape(const hk_tensor* q, const hk_tensor* k, const hk_tensor* v, float scale,
+                         const hk_tensor* mask, ComposedShape* sh) {
+    if (!tensor_ok(q, "Q") || !tensor_ok(k, "K") || !tensor_ok(v, "V")) return HK_INVALID_ARGUMENT;
+    if (q->rank != k->rank || q->rank != v->rank || (q->rank != 3 && q->rank != 4))
+        return fail(HK_INVALID_ARGUMENT,
+                    "attention requires rank-3 Q[B,M,D], K[B,N,D], V[B,N,Dv] or rank-4 Q[B,Hq,M,D], K[B,Hkv,N,D], "
+                    "V[B,Hkv,N,Dv]");
+    if ((q->dtype != HK_F32 && q->dtype != HK_BF16) || k->dtype != q->dtype || v->dtype != q->dtype)
+        return fail(HK_INVALID_ARGUMENT, "attention requires FP32 (or BF16) Q/K/V of one dtype");
+    const bool r4 = q->rank == 4;
+    const int o = r4 ? 1 : 0;
+    const int64_t B = q->shape[0], H = r4 ? q->shape[1] : 1, M = q->shape[1 + o], D = q->shape[2 + o];
+    const int64_t Hkv = r4 ? k->shape[1] : 1, N = k->shape[1 + o], Dv = v->shape[2 + o];
+    // Reference: validate_gqa and validate_dimensions, src/nn/attention.rs:81-104.
+    if (H <= 0 || Hkv <= 0 || H % Hkv != 0 || k->shape[0] != B || v->shape[0] != B || (r4 && v->shape[1] != Hkv) ||
+        k->shape[2 + o] != D || v->shape[1 + o] != N)
+        return fail(HK_INVALID_ARGUMENT,
+                    "GQA requires matching batches, positive divisible Q/KV heads and matching K/V lengths and Q/K widths");
+    const int64_t flat = B * H;
+    auto aligned = [](int64_t x) { return x > 0 && x % 16 == 0 && x <= INT32_MAX; };
+    if (flat <= 0 || flat > 4096 || !aligned(M) || !aligned(D) || !aligned(Dv) || N <= 0 || N > INT32_MAX ||
+        N % 32 != 0 || !std::isfinite(scale) || flat * M * N > static_cast<int64_t>(UINT32_MAX))
+        return fail(HK_INVALID_ARGUMENT,
+                    "attention requires matching batches/contractions, aligned positive matrix dimensions, positive N "
+                    "divisible by 32 within INT32_MAX, a finite FP32 scale and scores within u32");
+    if (flat * N * std::max(D, Dv) > static_cast<int64_t>(UINT32_MAX))  // RepeatKvSpec::elements, heads_programs.rs:9-17
+        return fail(HK_INVALID_ARGUMENT, "KV repetition complete domain exceeds u32");
+    if (mask) {
+        if (!tensor_ok(mask, "mask")) return HK_INVALID_ARGUMENT;
+        const bool ok = mask->dtype == HK_F32 && mask->rank == q->rank && mask->shape[0] == B &&
+                        (!r4 || mask->shape[1] == H) && mask->shape[1 + o] == M && mask->shape[2 + o] == N;
+        if (!ok)
+            return fail(HK_INVALID_ARGUMENT, r4 ? "GQA additive mask must be FP32 [B,Hq,M,N]"
+                                               : "attention additive mask must be FP32 [B,M,N]");
+    }
+    sh->batch = B;
+    sh->heads = H;
+    sh->kv_heads = Hkv;
+    sh->m = M;
+    sh->n = N;
+    sh->d = D;
+    sh->dv = Dv;
+    return HK_OK;
+}
+
+bool shaped_like(const hk_tensor* t, const hk_tensor* like, int64_t last) {
+    if (t->rank != like->rank) return false;
+    for (int i = 0; i + 1 < t->rank; ++i)
+        if (t->shape[i] != like->shape[i]) return false;
+    return t->shape[t->rank - 1] == last;
+}
+
+// Workspace carving for the composed path (256-byte aligned pieces).
+struct Carve {
+    char* base;
+    size_t used = 0;
+    void* take(size_t bytes) {
+        void* p = base ? base + used : nullptr;
+        used += ws_round(bytes);
+        return p;
+    }
+};
+
+// BF16 operand: `t` itself when BF16, else its RNE rounding into the workspace.
+const void* bf16_operand(const hk_tensor* t, Carve& w, hipError_t* e, hipStream_t s) {
+    if (t->dtype == HK_BF16) return t->data;
+    void* p = w.take(static_cast<size_t>(numel(t)) * 2);
+    if (w.base && *e == hipSuccess) *e = hk::cast_apply(1, t->data, p, numel(t), s);
+    return p;
+}
+
+// S = bf16(Q) bf16(K)^T * scale (+ mask) and P = softmax(S), both F32 [B*Hkv, rows, N].
+void composed_probs(const ComposedShape& sh, const void* qb, const void* kb, float scale, const hk_tensor* mask,
+                    float* sbuf, float* p, void* gws, int num_cus, hipStream_t s, hipError_t* e) {
+    const int64_t G = sh.groups(), R = sh.rows();
+    if (*e == hipSuccess) *e = hk::gemm_bf16(qb, kb, sbuf, false, G, R, sh.n, sh.d, HK_NO, HK_YES, gws, num_cus, s);
+    if (*e == hipSuccess)
+        *e = hk::scale_mask(sbuf, mask ? static_cast<const float*>(mask->data) : nullptr, scale, sh.scores(), s);
+    if (*e == hipSuccess) *e = hk::softmax_forward(sbuf, p, G * R, sh.n, 0, s);
+}
+
+size_t composed_gemm_ws(const ComposedShape& sh) {
+    const int64_t G = sh.groups(), R = sh.rows();
+    size_t w = hk::gemm_workspace_bytes(G, R, sh.n, sh.d, HK_NO, HK_YES);
+    w = std::max(w, hk::gemm_workspace_bytes(G, R, sh.dv, sh.n, HK_NO, HK_NO));   // O, dQ (Dv or D wide)
+    w = std::max(w, hk::gemm_workspace_bytes(G, R, sh.d, sh.n, HK_NO, HK_NO));
+    w = std::max(w, hk::gemm_workspace_bytes(G, R, sh.n, sh.dv, HK_NO, HK_YES));  // dP
+    w = std::max(w, hk::gemm_workspace_bytes(G, sh.n, sh.d, R, HK_YES, HK_NO));   // dK
+    w = std::max(w, hk::gemm_workspace_bytes(G, sh.n, sh.dv, R, HK_YES, HK_NO));  // dV
+    return w;
+}
+
+}  // namespace
+
+hk_status hk_attention_masked_forward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                      float scale, const hk_tensor* mask, hk_tensor* o) {
+    ComposedShape sh;
+    hk_status st = composed_shape(q, k, v, scale, mask, &sh);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(o, "O")) return HK_INVALID_ARGUMENT;
+    if ((o->dtype != HK_F32 && o->dtype != HK_BF16) || !shaped_like(o, q, sh.dv))
+        return fail(HK_INVALID_ARGUMENT, "O must be F32 (or BF16) shaped like Q with the value width");
+    if (mask ? !disjoint({o}, {q, k, v, mask}) : !disjoint({o}, {q, k, v})) return HK_INVALID_ARGUMENT;
+    const int64_t G = sh.groups(), R = sh.rows();
+    auto plan = [&](Carve& w, hipError_t* e, Ctx* c) {
+        const void* qb = bf16_operand(q, w, e, c ? c->stream : nullptr);
+        const void* kb = bf16_operand(k, w, e, c ? c->stream : nullptr);
+        const void* vb = bf16_operand(v, w, e, c ? c->stream : nullptr);
+        float* sbuf = static_cast<float*>(w.take(sh.scores() * 4));
+        float* p = static_cast<float*>(w.take(sh.scores() * 4));
+        void* pb = w.take(sh.scores() * 2);
+        void* gws = w.take(composed_gemm_ws(sh));
+        if (!c) return;
+        composed_probs(sh, qb, kb, scale, mask, sbuf, p, gws, c->num_cus, c->stream, e);
+        if (*e == hipSuccess) *e = hk::cast_apply(1, p, pb, sh.scores(), c->stream);
+        if (*e == hipSuccess)
+            *e = hk::gemm_bf16(pb, vb, o->data, o->dtype == HK_BF16, G, R, sh.dv, sh.n, HK_NO, HK_NO, gws,
+                               c->num_cus, c->stream);
+    };
+    Carve size{nullptr};
+    hipError_t e = hipSuccess;
+    plan(size, &e, nullptr);
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, size.used)) != HK_OK) return st;
+    Carve w{static_cast<char*>(g.c->workspace)};
+    plan(w, &e, g.c);
+    return complete(g.c, e, "attention_masked_forward", 6);
+}
+
+hk_status hk_attention_masked_backward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                       const hk_tensor* mask, const hk_tensor* dout, float scale, hk_tensor* dq,
+                                       hk_tensor* dk, hk_tensor* dv, hk_tensor* dmask) {
+    ComposedShape sh;
+    hk_status st = composed_shape(q, k, v, scale, mask, &sh);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(dout, "dO") || !tensor_ok(dq, "dQ") || !tensor_ok(dk, "dK") || !tensor_ok(dv, "dV"))
+        return HK_INVALID_ARGUMENT;
+    if ((dout->dtype != HK_F32 && dout->dtype != HK_BF16) || !shaped_like(dout, q, sh.dv))
+        return fail(HK_INVALID_ARGUMENT, "dO must be F32 (or BF16) shaped like the output");
+    if (!same_shape(dq, q) || !same_shape(dk, k) || !same_shape(dv, v) ||
+        (dq->dtype != HK_F32 && dq->dtype != HK_BF16) || (dk->dtype != HK_F32 && dk->dtype != HK_BF16) ||
+        dv->dtype != dk->dtype)
+        return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must be F32 or BF16 (dK and dV alike) with the shapes of Q/K/V");
+    if (dmask) {
+        if (!mask) return fail(HK_INVALID_ARGUMENT, "a mask gradient needs the mask");
+        if (!tensor_ok(dmask, "dMask")) return HK_INVALID_ARGUMENT;
+        if (dmask->dtype != HK_F32 || !same_shape(dmask, mask))
+            return fail(HK_INVALID_ARGUMENT, "the mask gradient must be F32 shaped like the mask");
+    }
+    std::vector<const hk_tensor*> ins = {q, k, v, dout};
+    if (mask) ins.push_back(mask);
+    std::vector<const hk_tensor*> outs = {dq, dk, dv};
+    if (dmask) outs.push_back(dmask);
+    for (size_t i = 0; i < outs.size(); ++i) {
+        for (const hk_tensor* x : ins)
+            if (overlaps(outs[i], x)) return fail(HK_INVALID_ARGUMENT, "output overlaps an input");
+        for (size_t j = i + 1; j < outs.size(); ++j)
+            if (overlaps(outs[i], outs[j])) return fail(HK_INVALID_ARGUMENT, "outputs overlap each other");
+    }
+    const int64_t G = sh.groups(), R = sh.rows();
+    auto plan = [&](Carve& w, hipError_t* e, Ctx* c) {
+        hipStream_t s = c ? c->stream : nullptr;
+        const void* qb = bf16_operand(q, w, e, s);
+        const void* kb = bf16_operand(k, w, e, s);
+        const void* vb = bf16_operand(v, w, e, s);
+        const void* dob = bf16_operand(dout, w, e, s);
+        float* sbuf = static_cast<float*>(w.take(sh.scores() * 4));  // scores, then dP
+        float* p = static_cast<float*>(w.take(sh.scores() * 4));
+        float* ds = dmask ? static_cast<float*>(dmask->data) : static_cast<float*>(w.take(sh.scores() * 4));
+        void* b16 = w.take(sh.scores() * 2);  // bf16(scale * dS), then bf16(P)
+        void* gws = w.take(composed_gemm_ws(sh));
+        if (!c) return;
+        const int cus = c->num_cus;
+        // recompute P (the reference keeps it in its autodiff graph)
+        composed_probs(sh, qb, kb, scale, mask, sbuf, p, gws, cus, s, e);
+        // dP = bf16(dO) bf16(V)^T; dS = P * (dP - rowsum(P * dP)) (softmax_backward); dMask = dS
+        if (*e == hipSuccess) *e = hk::gemm_bf16(dob, vb, sbuf, false, G, R, sh.n, sh.dv, HK_NO, HK_YES, gws, cus, s);
+        if (*e == hipSuccess) *e = hk::softmax_backward(p, sbuf, ds, G * R, sh.n, 0, s);
+        // dQ = bf16(scale dS) bf16(K); dK = bf16(scale dS)^T bf16(Q) (the group's heads summed in the GEMM)
+        if (*e == hipSuccess) *e = hk::scale_to_bf16(ds, scale, b16, sh.scores(), s);
+        if (*e == hipSuccess)
+            *e = hk::gemm_bf16(b16, kb, dq->data, dq->dtype == HK_BF16, G, R, sh.d, sh.n, HK_NO, HK_NO, gws, cus, s);
+        if (*e == hipSuccess)
+            *e = hk::gemm_bf16(b16, qb, dk->data, dk->dtype == HK_BF16, G, sh.n, sh.d, R, HK_YES, HK_NO, gws, cus, s);
+        // dV = bf16(P)^T bf16(dO)
+        if (*e == hipSuccess) *e = hk::cast_apply(1, p, b16, sh.scores(), s);
+        if (*e == hipSuccess)
+            *e = hk::gemm_bf16(b16, dob, dv->data, dv->dtype == HK_BF16, G, sh.n, sh.dv, R, HK_YES, HK_NO, gws, cus, s);
+    };
+    Carve size{nullptr};
+    hipError_t e = hipSuccess;
+    plan(size, &e, nullptr);
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, size.used)) != HK_OK) return st;
+    Carve w{static_cast<char*>(g.c->workspace)};
+    plan(w, &e, g.c);
+    return complete(g.c, e, "attention_masked_backward", 11);
 }
 
 }  // extern "C"

@@ -160,7 +160,38 @@ unsigned grid_for(int64_t n) {
 
 constexpr int kFoldLevels = 5;  // pairwise levels per launch (32 rows read per output)
 
+// Attention scores of the composed (materialized) path, in place: s = s * scale, then + mask
+// when a mask is given (two F32 roundings, the reference's `scores * scale + mask` of
+// src/nn/attention.rs:25-26).
+__global__ void __launch_bounds__(kEwThreads)
+scale_mask_kernel(float* __restrict__ s, const float* __restrict__ mask, float scale, int64_t n) {
+    for (int64_t i = flat_begin(kEwThreads); i < n; i += flat_stride(kEwThreads)) {
+        const float v = s[i] * scale;
+        s[i] = mask ? v + mask[i] : v;
+    }
+}
+
+// out = bf16(scale * x): the gradient of `scores * scale` rounded to BF16 as the score GEMM's
+// backward rounds its upstream gradient (matmul_bf16_fp32's backward).
+__global__ void __launch_bounds__(kEwThreads)
+scale_to_bf16_kernel(const float* __restrict__ x, float scale, uint16_t* __restrict__ out, int64_t n) {
+    for (int64_t i = flat_begin(kEwThreads); i < n; i += flat_stride(kEwThreads)) out[i] = f32_to_bf16(x[i] * scale);
+}
+
 }  // namespace
+
+hipError_t scale_mask(float* scores, const float* mask, float scale, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(scale_mask_kernel, dim3(blocks_for(n)), dim3(kEwThreads), 0, s, scores, mask, scale, n);
+    return hipGetLastError();
+}
+
+hipError_t scale_to_bf16(const float* x, float scale, void* out, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(scale_to_bf16_kernel, dim3(blocks_for(n)), dim3(kEwThreads), 0, s, x, scale,
+                       static_cast<uint16_t*>(out), n);
+    return hipGetLastError();
+}
 
 hipError_t silu_mul(int dtype_bf16, const void* gate, const void* up, void* y, int64_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;

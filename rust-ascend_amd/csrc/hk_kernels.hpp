@@ -65,6 +65,9 @@ hipError_t crop_f32(const float* src, float* dst, int64_t batch, int64_t rows, i
 // ---- element-wise (hk_elementwise.hip)
 // SwiGLU gate, element-wise over n values of F32 or BF16 storage.
 hipError_t silu_mul(int dtype_bf16, const void* gate, const void* up, void* y, int64_t n, hipStream_t s);
+// Composed attention helpers: scores = scores * scale (+ mask), in place; out = bf16(scale * x).
+hipError_t scale_mask(float* scores, const float* mask, float scale, int64_t n, hipStream_t s);
+hipError_t scale_to_bf16(const float* x, float scale, void* out, int64_t n, hipStream_t s);
 hipError_t silu_mul_backward(int dtype_bf16, const void* gate, const void* up, const void* dy, void* dgate,
                              void* dup, int64_t n, hipStream_t s);
 // y = (x + residual) + bias[i % width] over n values (residual may be null); x/residual/y F32 or
@@ -116,6 +119,7 @@ struct AttnShape {
     float scale;
     int32_t causal;
     uint64_t query_start, key_start;
+    int32_t o_f32 = 0;  // O (forward output, backward input) is F32 instead of BF16
 };
 size_t attention_bwd_workspace_bytes(const AttnShape& sh);
 // Whether the fused kernels can take the shape: one head of Q/K/V (M*D and N*D BF16 elements)

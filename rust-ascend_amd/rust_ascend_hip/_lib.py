@@ -118,6 +118,8 @@ SIGNATURES = {
     "hk_rotary_prefix_backward": [_CTX, _T, _T, _T, _i32, _i32, _T],
     "hk_attention_forward": [_CTX, _T, _T, _T, _f32, _i32, _u64, _u64, _T, _T],
     "hk_attention_backward": [_CTX, _T, _T, _T, _T, _T, _T, _f32, _i32, _u64, _u64, _T, _T, _T],
+    "hk_attention_masked_forward": [_CTX, _T, _T, _T, _f32, _T, _T],
+    "hk_attention_masked_backward": [_CTX, _T, _T, _T, _T, _T, _f32, _T, _T, _T, _T],
 }
 _RESTYPE = {"hk_last_error": ctypes.c_char_p, "hk_abi_version": ctypes.c_int32, "hk_get_stream": ctypes.c_void_p}
 

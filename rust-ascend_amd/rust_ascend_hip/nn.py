@@ -8,7 +8,8 @@ for RUDA's autodiff graph. Saved state matches the reference's Backward nodes:
 * rms_norm saves (x, w, rstd) and the backward reuses rstd (src/nn.rs:203-232);
 * rotary/rotary_prefix save nothing but the fixed tables (src/nn/rotary.rs:32-105);
 * the fused attention saves (q, k, v, o, lse) instead of the materialized score,
-  mask and probability tensors of the composed reference (src/nn/attention.rs:10-80).
+  mask and probability tensors of the composed reference (src/nn/attention.rs:10-80); the
+  materialized (additive-mask) attention saves (q, k, v, mask) and recomputes the probabilities.
 """
 from __future__ import annotations
 
@@ -332,6 +333,99 @@ def causal_grouped_query_attention_bf16(q, k, v, scale: float, query_start: int 
     nn::causal_grouped_query_attention_bf16_fp32 (src/nn/attention.rs:68-80)."""
     return _Attention.apply(q.contiguous(), k.contiguous(), v.contiguous(), float(scale), True, int(query_start),
                             int(key_start))
+
+
+class _AttentionF32(torch.autograd.Function):
+    """The FP32 surface on the fused kernels: F32 Q/K/V are rounded to BF16 by the library, O is
+    written in F32 and enters the backward's row term unrounded; F32 gradients."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, causal, query_start, key_start):
+        o, lse = HipRuntime.attention_forward(q, k, v, scale, causal, query_start, key_start, out_dtype=torch.float32)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.args = (scale, causal, query_start, key_start)
+        return o
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, o, lse = ctx.saved_tensors
+        scale, causal, qs, ks = ctx.args
+        dq, dk, dv = HipRuntime.attention_backward(q, k, v, o, lse, dy.contiguous().float(), scale, causal, qs, ks,
+                                                   grad_dtype=torch.float32)
+        return dq, dk, dv, None, None, None, None
+
+
+class _MaskedAttention(torch.autograd.Function):
+    """The reference's materialized attention (additive mask, any value width): saves Q, K, V and
+    the mask and recomputes the probabilities in the backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale):
+        o = HipRuntime.attention_masked_forward(q, k, v, scale, mask)
+        ctx.save_for_backward(q, k, v, mask)
+        ctx.scale = scale
+        return o
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, mask = ctx.saved_tensors
+        want_dmask = mask is not None and ctx.needs_input_grad[3]
+        dq, dk, dv, dmask = HipRuntime.attention_masked_backward(q, k, v, mask, dy.contiguous().float(), ctx.scale,
+                                                                 mask_grad=want_dmask)
+        return dq, dk, dv, dmask, None
+
+
+_FUSED_WIDTHS = (16, 32, 64, 128)
+
+
+def _fused_ok(q, v) -> bool:
+    return q.shape[-1] == v.shape[-1] and q.shape[-1] in _FUSED_WIDTHS
+
+
+def _f32(*ts):
+    return [t.contiguous() for t in ts]
+
+
+def grouped_query_attention_bf16_fp32(q, k, v, scale: float, additive_mask=None) -> torch.Tensor:
+    """F32 Q[B,Hq,M,D], K[B,Hkv,N,D], V[B,Hkv,N,Dv] -> F32 O[B,Hq,M,Dv] with an optional F32
+    additive mask [B,Hq,M,N] (differentiable). Without a mask and with Dv == D in {16,32,64,128}
+    this runs the fused kernels; otherwise the materialized path of the reference. Reference:
+    nn::grouped_query_attention_bf16_fp32 (src/nn/attention.rs:49-67)."""
+    q, k, v = _f32(q, k, v)
+    if additive_mask is None and _fused_ok(q, v):
+        return _AttentionF32.apply(q, k, v, float(scale), False, 0, 0)
+    mask = None if additive_mask is None else additive_mask.contiguous()
+    return _MaskedAttention.apply(q, k, v, mask, float(scale))
+
+
+def causal_grouped_query_attention_bf16_fp32(q, k, v, scale: float, query_start: int = 0, key_start: int = 0):
+    """F32 GQA with the exact-position causal mask (key j excluded when key_start + j >
+    query_start + i). Fused when Dv == D in {16,32,64,128}, else the materialized path with the
+    device-generated mask. Reference: nn::causal_grouped_query_attention_bf16_fp32
+    (src/nn/attention.rs:68-80)."""
+    q, k, v = _f32(q, k, v)
+    if _fused_ok(q, v):
+        return _AttentionF32.apply(q, k, v, float(scale), True, int(query_start), int(key_start))
+    b, h, m, _ = q.shape
+    mask = HipRuntime.causal_mask(b * h, m, k.shape[2], query_start, key_start, q.device).view(b, h, m, k.shape[2])
+    return _MaskedAttention.apply(q, k, v, mask, float(scale))
+
+
+def scaled_dot_product_attention_bf16_fp32(q, k, v, scale: float, additive_mask=None) -> torch.Tensor:
+    """Rank-3 F32 attention Q[B,M,D], K[B,N,D], V[B,N,Dv] with an optional F32 additive mask
+    [B,M,N]. Reference: nn::scaled_dot_product_attention_bf16_fp32 (src/nn/attention.rs:10-29)."""
+    q, k, v = _f32(q, k, v)
+    if additive_mask is None and _fused_ok(q, v):
+        return _AttentionF32.apply(q[:, None], k[:, None], v[:, None], float(scale), False, 0, 0)[:, 0]
+    mask = None if additive_mask is None else additive_mask.contiguous()
+    return _MaskedAttention.apply(q, k, v, mask, float(scale))
+
+
+def causal_attention_bf16_fp32(q, k, v, scale: float, query_start: int = 0, key_start: int = 0) -> torch.Tensor:
+    """Rank-3 F32 causal attention with absolute positions. Reference: nn::causal_attention_bf16_fp32
+    (src/nn/attention.rs:30-43)."""
+    return causal_grouped_query_attention_bf16_fp32(q[:, None], k[:, None], v[:, None], scale, query_start,
+                                                    key_start)[:, 0]
 
 
 class _NllLoss(torch.autograd.Function):

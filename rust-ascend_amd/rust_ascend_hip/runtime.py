@@ -584,10 +584,12 @@ class HipRuntime:
     # ---------------------------------------------------------------- attention
 
     @staticmethod
-    def attention_forward(q, k, v, scale: float, causal: bool = True, query_start: int = 0, key_start: int = 0):
-        """Fused GQA attention forward: [O (BF16), lse (F32 [B,Hq,M])]. Replaces the composed
-        chain of src/nn/attention.rs:10-80."""
-        o = _empty(q.shape, torch.bfloat16, q)
+    def attention_forward(q, k, v, scale: float, causal: bool = True, query_start: int = 0, key_start: int = 0,
+                          out_dtype=torch.bfloat16):
+        """Fused GQA attention forward: [O (out_dtype: BF16, or F32 for the reference's FP32
+        surface), lse (F32 [B,Hq,M])]. Q/K/V all BF16 or all F32. Replaces the composed chain of
+        src/nn/attention.rs:10-80."""
+        o = _empty(q.shape, out_dtype, q)
         lse = _empty(q.shape[:3], torch.float32, q)
         _call("hk_attention_forward", desc(q), desc(k), desc(v), float(scale), int(bool(causal)), int(query_start),
               int(key_start), desc(o), desc(lse))
@@ -603,3 +605,25 @@ class HipRuntime:
         _call("hk_attention_backward", desc(q), desc(k), desc(v), desc(o), desc(lse), desc(grad), float(scale),
               int(bool(causal)), int(query_start), int(key_start), desc(dq), desc(dk), desc(dv))
         return dq, dk, dv
+
+    @staticmethod
+    def attention_masked_forward(q, k, v, scale: float, mask=None, out_dtype=torch.float32):
+        """The reference's materialized attention with an optional additive F32 mask: rank 3
+        (scaled_dot_product_attention_bf16_fp32) or rank 4 (grouped_query_attention_bf16_fp32),
+        any value width (src/nn/attention.rs:10-67). Returns O [.., M, Dv]."""
+        o = _empty(tuple(q.shape[:-1]) + (v.shape[-1],), out_dtype, q)
+        _call("hk_attention_masked_forward", desc(q), desc(k), desc(v), float(scale),
+              None if mask is None else desc(mask), desc(o))
+        return o
+
+    @staticmethod
+    def attention_masked_backward(q, k, v, mask, grad, scale: float, grad_dtype=torch.float32, mask_grad=False):
+        """[dQ, dK, dV, dMask or None] of attention_masked_forward; dMask = dS (F32, the mask's
+        shape) when mask_grad is set."""
+        dq = _empty(q.shape, grad_dtype, q)
+        dk = _empty(k.shape, grad_dtype, q)
+        dv = _empty(v.shape, grad_dtype, q)
+        dmask = _empty(mask.shape, torch.float32, q) if mask_grad else None
+        _call("hk_attention_masked_backward", desc(q), desc(k), desc(v), None if mask is None else desc(mask),
+              desc(grad), float(scale), desc(dq), desc(dk), desc(dv), None if dmask is None else desc(dmask))
+        return dq, dk, dv, dmask

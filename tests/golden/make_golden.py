@@ -262,7 +262,8 @@ def main():
         tv = torch.tensor(bf16(v), dtype=torch.float64, requires_grad=True)
         kk = tk.repeat_interleave(group, dim=1)
         vv = tv.repeat_interleave(group, dim=1)
-        sc = 0.25 * tq @ kk.transpose(-1, -2) + torch.tensor(mask, dtype=torch.float64)
+        tm = torch.tensor(mask, dtype=torch.float64, requires_grad=True)
+        sc = 0.25 * tq @ kk.transpose(-1, -2) + tm
         p = torch.softmax(sc, dim=-1)
         o = p @ vv
         (o * torch.tensor(bf16(dy), dtype=torch.float64)).sum().backward()
@@ -274,6 +275,8 @@ def main():
         g[key + "_dq"] = tq.grad.numpy()
         g[key + "_dk"] = tk.grad.numpy()
         g[key + "_dv"] = tv.grad.numpy()
+        if not causal:  # the mask gradient, checked by the reference at grouped_attention_tensor.rs:95
+            g[key + "_dmask"] = tm.grad.numpy()
 
     # examples/attention_tensor.rs:22-66: orthogonal Q (column 0) and K (column 1) give zero
     # scores -> uniform probabilities; closed forms for out, dQ, dK, dV (no BF16 rounding

@@ -309,3 +309,40 @@ def test_linear_frozen_contract():
                                                    fake(F32, (32, 32), 1 << 30)) == _lib.INVALID_ARGUMENT
     assert lib.hk_linear_frozen_bf16_fp32_backward(None, w, fake(F32, (32, 64), 1 << 28),
                                                    fake(F32, (32, 48), (1 << 28) + 64)) == _lib.INVALID_ARGUMENT
+
+
+def test_masked_attention_contract():
+    # validate_dimensions / validate_gqa (src/nn/attention.rs:81-133): N % 32, M/D/Dv % 16, batches,
+    # u32 scores; masks exactly [B,M,N] (rank 3) or [B,Hq,M,N] (rank 4), F32; Dv may differ from D
+    lib = _lib.load()
+
+    def call(q, k, v, mask=None, o=None, dt=F32):
+        o = o or q[:-1] + (v[-1],)
+        return lib.hk_attention_masked_forward(None, fake(dt, q, 1 << 20), fake(dt, k, 1 << 26), fake(dt, v, 1 << 30),
+                                               0.25, None if mask is None else fake(F32, mask, 1 << 34),
+                                               fake(F32, o, 1 << 38))
+
+    assert call((2, 32, 16), (2, 8192, 16), (2, 8192, 32)) == _lib.NOT_INITIALIZED        # rank 3, Dv != D
+    assert call((2, 6, 32, 16), (2, 3, 96, 16), (2, 3, 96, 48), mask=(2, 6, 32, 96)) == _lib.NOT_INITIALIZED
+    assert call((2, 6, 32, 16), (2, 3, 96, 16), (2, 3, 96, 16), dt=BF16) == _lib.NOT_INITIALIZED
+    for n in (0, 31, 4097):                                                                # attention.rs:111-113
+        assert call((2, 32, 16), (2, n, 16), (2, n, 32)) == _lib.INVALID_ARGUMENT, n
+    for q, k, v in [((2, 5, 32, 16), (2, 3, 96, 16), (2, 3, 96, 16)), ((2, 6, 32, 16), (2, 3, 96, 16), (2, 2, 96, 16)),
+                    ((2, 6, 32, 16), (2, 3, 96, 16), (1, 3, 96, 16)), ((2, 6, 32, 16), (2, 3, 96, 16), (2, 3, 32, 16)),
+                    ((4096, 2, 32, 16), (4096, 1, 96, 16), (4096, 1, 96, 16)), ((2, 6, 32, 24), (2, 3, 96, 24), (2, 3, 96, 24)),
+                    ((4096, 65536, 16), (4096, 8192, 16), (4096, 8192, 16))]:              # attention.rs:114,127-130
+        assert call(q, k, v) == _lib.INVALID_ARGUMENT, (q, k, v)
+    assert call((2, 6, 32, 16), (2, 3, 96, 16), (2, 3, 96, 16), mask=(2, 6, 32, 64)) == _lib.INVALID_ARGUMENT
+    assert call((2, 32, 16), (2, 96, 16), (2, 96, 16), mask=(2, 1, 32, 96)) == _lib.INVALID_ARGUMENT
+    assert call((2, 32, 16), (2, 96, 16), (2, 96, 16), o=(2, 32, 32)) == _lib.INVALID_ARGUMENT  # O's value width
+    # the backward: a mask gradient needs the mask and the mask's shape
+    q, k = fake(F32, (1, 2, 16, 16), 1 << 20), fake(F32, (1, 1, 64, 16), 1 << 24)
+    grads = [fake(F32, (1, 2, 16, 16), 1 << 28), fake(F32, (1, 1, 64, 16), 1 << 30), fake(F32, (1, 1, 64, 16), 1 << 32)]
+    assert lib.hk_attention_masked_backward(None, q, k, k, None, fake(F32, (1, 2, 16, 16), 1 << 26), 0.25, *grads,
+                                            fake(F32, (1, 2, 16, 64), 1 << 36)) == _lib.INVALID_ARGUMENT
+    assert lib.hk_attention_masked_backward(None, q, k, k, fake(F32, (1, 2, 16, 64), 1 << 34),
+                                            fake(F32, (1, 2, 16, 16), 1 << 26), 0.25, *grads,
+                                            fake(F32, (1, 2, 16, 64), 1 << 36)) == _lib.NOT_INITIALIZED
+    assert lib.hk_attention_masked_backward(None, q, k, k, fake(F32, (1, 2, 16, 64), 1 << 34),
+                                            fake(F32, (1, 2, 16, 16), 1 << 26), 0.25, *grads,
+                                            fake(F32, (1, 2, 16, 64), (1 << 20) + 1024)) == _lib.INVALID_ARGUMENT  # dMask overlaps Q

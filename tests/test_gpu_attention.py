@@ -4,9 +4,9 @@ rounding points), the reference's closed forms and the golden vectors.
 
 Tolerances: the reference's GQA check (grouped_attention_tensor.rs:10: 2e-3 + 3e-3|b|) on its
 own cases, the closed-form checks' 5e-4 + 5e-4|b| (attention_tensor.rs), and max rel err
-<= 1e-2 on BF16 outputs elsewhere. The fused kernel takes the causal mask or no mask; the
-reference's arbitrary additive masks are not on the fused path, so its non-causal GQA cases
-run here without the mask (against the oracle evaluated the same way).
+<= 1e-2 on BF16 outputs elsewhere. The fused kernel takes the causal mask or no mask, so the
+reference's non-causal GQA cases run here without their mask (against the oracle evaluated the
+same way); with the mask they run on the materialized path in test_gpu_attention_masked.py.
 """
 import numpy as np
 import pytest

@@ -271,6 +271,35 @@ def test_attention_reference_cases_vs_autograd(oracle, golden, case):
     close(r["dq"], g["dq"], **tol)
     close(r["dk"], g["dk"], **tol)
     close(r["dv"], g["dv"], **tol)
+    if not causal:  # grouped_attention_tensor.rs:95: the mask gradient
+        close(r["dmask"], g["dmask"], **tol)
+
+
+@pytest.mark.parametrize("d,dv", [(16, 48), (48, 16), (32, 32)])
+def test_attention_value_width_and_mask_grad_vs_autograd(oracle, d, dv):
+    """A value width other than the head width (src/nn/attention.rs:49-52 allows any) and the
+    mask gradient, against torch float64 autograd of softmax(scale QK^T + mask) V with GQA by
+    repeated heads; inputs exactly representable in BF16, so only the oracle's BF16 rounding of
+    P and dS separates the two (the reference's tolerance 2e-3 + 3e-3|b|)."""
+    B, H, Hkv, M, N = 2, 4, 2, 16, 64
+    # magnitudes like the reference's cases (|x| <= 0.5), where its absolute tolerance applies
+    q = oracle.bf16_round(oracle.normal((B, H, M, d), 9, 1, std=0.25))
+    k = oracle.bf16_round(oracle.normal((B, Hkv, N, d), 9, 2, std=0.25))
+    v = oracle.bf16_round(oracle.normal((B, Hkv, N, dv), 9, 3, std=0.25))
+    dy = oracle.bf16_round(oracle.normal((B, H, M, dv), 9, 4, std=0.25))
+    mask = (oracle.normal((B, H, M, N), 9, 5) * 0.5).astype(np.float32)
+    mask[:, :, 3, 10:40] = -np.inf
+    r = oracle.attention_f64(q, k, v, dy, scale=0.3, mask=mask)
+    tq, tk, tv, tm = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v, mask))
+    kk, vv = tk.repeat_interleave(H // Hkv, 1), tv.repeat_interleave(H // Hkv, 1)
+    p = torch.softmax(0.3 * tq @ kk.transpose(-1, -2) + tm, -1)
+    o = p @ vv
+    (o * torch.tensor(dy, dtype=torch.float64)).sum().backward()
+    tol = dict(atol=2e-3, rtol=3e-3)
+    close(r["out"], o.detach().numpy(), **tol)
+    for name, t in (("dq", tq), ("dk", tk), ("dv", tv), ("dmask", tm)):
+        close(r[name], t.grad.numpy(), **tol)
+    assert r["out"].shape == (B, H, M, dv) and r["dv"].shape == (B, Hkv, N, dv)
 
 
 def test_attention_causal_equals_explicit_mask(oracle, golden):
