@@ -34,6 +34,21 @@ C2_FWD_BYTES = 2 * C2_ROWS * C2_WIDTH * 2 + C2_WIDTH * 4 + C2_ROWS * 4          
 C2_BWD_BYTES = 3 * C2_ROWS * C2_WIDTH * 2 + 2 * C2_WIDTH * 4 + C2_ROWS * 4       # x, dy, dx, w, dw, rstd = 402,751,488
 
 
+# C1/C3 GEMM workloads: name -> (M, N, K, transpose A, transpose B, label)
+GEMMS = {
+    "gemm8192_nt": (8192, 8192, 8192, 0, 1, "C3 GEMM 8192^3 NT"),
+    "gemm8192_nn": (8192, 8192, 8192, 0, 0, "C3 GEMM 8192^3 NN"),
+    "llama_up": (8192, 14336, 4096, 0, 1, "C3 Llama 8192x4096->14336 NT"),
+    "llama_down": (8192, 4096, 14336, 0, 1, "C3 Llama 8192x14336->4096 NT"),
+    "gemm4096_nt": (4096, 4096, 4096, 0, 1, "C3 GEMM 4096^3 NT"),
+    "gemm1024_nt": (1024, 1024, 1024, 0, 1, "C3 GEMM 1024^3 NT"),
+    "c1": (512, 1024, 1024, 0, 1, "C1 Linear X[512,1024] W[1024,1024]^T"),
+}
+# CPU-baseline sample rows per GEMM workload (None: the whole product)
+CPU_ROWS = {"gemm8192_nt": 256, "gemm8192_nn": 64, "llama_up": 256, "llama_down": 256}
+KERNELS = sorted(list(GEMMS) + ["c2", "attn_fwd", "attn_bwd", "rope"])
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -48,6 +63,12 @@ def parse():
     p.add_argument("--only-widened", action="store_true",
                    help="only run the lines of the rows widened around the path (grouped and padded GEMM, "
                         "softmax, cross entropy, SwiGLU, bias add, embedding) and print them, one JSON line each")
+    p.add_argument("--kernel", choices=sorted(KERNELS),
+                   help="only run one workload's kernels --steps times (after --warmup) and print its timing: "
+                        "the unit that rocprofv3 profiles")
+    p.add_argument("--vendor", action="store_true",
+                   help="only time the vendor libraries on the same data (hipBLASLt through torch.matmul for C1/C3, "
+                        "PyTorch SDPA for C4) next to this library and print one JSON line each")
     p.add_argument("--stream-ceilings", action="store_true",
                    help="only measure plain HBM streams (read, write, copy, 2 reads + 1 write) on 1 GiB "
                         "buffers with PyTorch's kernels and print them")
@@ -78,6 +99,16 @@ def stream_ceilings(gib=1, iters=10):
         ms = e0.elapsed_time(e1) / iters
         out[name] = round(streams * n * 4 / (ms * 1e-3) / 1e9, 1)
     return out
+
+
+def copy_calibration():
+    """A 1 GiB device-to-device copy (reads 1 GiB, writes 1 GiB): the known-size launch against
+    which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled."""
+    import torch
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def warm(fn, seconds=0.3):
@@ -114,16 +145,35 @@ def read_traffic(kernel: str):
     return None
 
 
-def roofline(bound, algo, ms, kernel):
+def read_counters(key: str):
+    """Per-launch counters of an MFMA-bound workload from profiles/kernel_counters.txt
+    (`<key> <traffic bytes> <MFMA utilisation> <executed flops>`), or None."""
+    path = os.path.join(ROOT, "profiles", "kernel_counters.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 4 and parts[0] == key:
+            return {"traffic": int(float(parts[1])), "mfma_util": float(parts[2]), "executed_flops": float(parts[3])}
+    return None
+
+
+def roofline(bound, algo, ms, kernel, key=None):
     if bound == "hbm":
         achieved = algo / (ms * 1e-3) / 1e9
         peak, unit = HBM_PEAK_GBS, "GB/s"
     else:
         achieved = algo / (ms * 1e-3) / 1e12
         peak, unit = BF16_PEAK_TFLOPS, "TFLOP/s"
-    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": read_traffic(kernel), "kernel": kernel,
-            "algorithmic_per_launch": algo, "avg_launch_ms": round(ms, 5)}
+    out = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+           "frac": round(achieved / peak, 4), "traffic": read_traffic(kernel), "kernel": kernel,
+           "algorithmic_per_launch": algo, "avg_launch_ms": round(ms, 5)}
+    counters = read_counters(key) if key else None
+    if counters:  # MFMA-bound workloads: measured traffic, utilisation and executed work (profiles/)
+        out["traffic"] = counters["traffic"]
+        out["mfma_util"] = counters["mfma_util"]
+        out["executed_flops_per_launch"] = counters["executed_flops"]
+    return out
 
 
 def bench_c2(steps, warmup):
@@ -192,6 +242,64 @@ def cpu_baseline_c2(threads):
                       "median of 3"}
 
 
+def cpu_threads():
+    """Host threads of the CPU baselines: OMP_NUM_THREADS (16 on the GPU box, its CPU share for
+    one GPU), else the visible cores."""
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def cpu_baseline_gemm(m, n, k, ta, tb, rows=None):
+    """The oracle's restatement of the reference's host GEMM (deepgemm_validate.rs:19-21: f32
+    products summed over k in order, no FMA) on BF16-valued inputs of the workload's shape. With
+    `rows`, only that many output rows are computed (the rate is theirs; `seconds` projects it to
+    the full M)."""
+    import numpy as np
+    import oracle
+    threads = cpu_threads()
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(m + n + k)
+    mr = rows or m
+    a = oracle.bf16_round(rng.standard_normal((k, mr) if ta else (mr, k), dtype=np.float32) / np.float32(k ** 0.5))
+    b = oracle.bf16_round(rng.standard_normal((n, k) if tb else (k, n), dtype=np.float32) / np.float32(k ** 0.5))
+    reps = 3 if mr * n * k <= (1 << 31) else 1
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle.gemm_f32(a, b, ta, tb)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    return {"value": round(2 * mr * n * k / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "seconds": round(t * m / mr, 3),
+            "sample": (f"full {m}x{n}x{k} {'NT' if tb else 'NN'}" if mr == m else
+                       f"{mr} of {m} output rows of {m}x{n}x{k} {'NT' if tb else 'NN'} (seconds projected to all rows)") +
+                      f", f32 sequential-k host loop, {'median of 3' if reps == 3 else 'timed once'}"}
+
+
+def cpu_baseline_attention():
+    """The oracle's restatement of the reference's host attention (grouped_attention_tensor.rs:
+    14-44, f64 with its BF16 rounding points), forward and backward, on a sample of C4: batch 0,
+    all 32 query / 8 KV heads, the first 1024 positions (1/64 of the causal work; the oracle is
+    parallel over the 8 (batch, KV head) pairs). The rate is the sample's causal-useful flops over
+    its time; `seconds` projects it to the whole config."""
+    import numpy as np
+    import oracle
+    threads = cpu_threads()
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(4)
+    S, D = 1024, 128
+    q, do = (oracle.bf16_round(rng.standard_normal((1, 32, S, D), dtype=np.float32)) for _ in range(2))
+    k, v = (oracle.bf16_round(rng.standard_normal((1, 8, S, D), dtype=np.float32)) for _ in range(2))
+    t0 = time.perf_counter()
+    oracle.attention_f64(q, k, v, do, scale=D ** -0.5, causal=True)
+    t = time.perf_counter() - t0
+    flops = 3.5 * 2 * 32 * S * S * D  # forward + backward, causal-useful (the GPU lines' count)
+    return {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": min(threads, 8), "kind": "port",
+            "seconds": round(t * 64, 1),
+            "sample": "C4 batch 0, 32/8 heads, first 1024 positions (1/64 of the causal work), forward + backward, "
+                      "f64 host loop with BF16 rounding points, timed once; parallel over the 8 (batch, KV head) "
+                      "pairs; seconds = projected to the whole config"}
+
+
 def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
     """Average GPU time of one GEMM over `iters` back-to-back calls of the C ABI (descriptors
     built once, as a native caller's would be), between one pair of events on the stream the
@@ -224,6 +332,125 @@ def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
         call()
     e1.record()
     return event_ms([(e0, e1)]) / reps
+
+
+def run_kernel(name, steps, warmup):
+    """One workload's kernels only, `warmup` then `steps` back-to-back calls through the C ABI
+    with descriptors built once, timed by HIP events on the kernels' stream: the unit that
+    rocprofv3 --pmc / --kernel-trace profiles (bench.py --kernel NAME)."""
+    import ctypes
+    import torch
+    from rust_ascend_hip import HipRuntime, _lib, runtime
+    from rust_ascend_hip._lib import check
+    lib, ctx = _lib.load(), runtime._context()
+    check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    if name in GEMMS:
+        m, n, k, ta, tb, _ = GEMMS[name]
+        a = (torch.randn((k, m) if ta else (m, k), generator=g, device="cuda") / k ** 0.5).to(torch.bfloat16)
+        b = (torch.randn((n, k) if tb else (k, n), generator=g, device="cuda") / k ** 0.5).to(torch.bfloat16)
+        c = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        d = (runtime.desc(a), runtime.desc(b), runtime.desc(c))
+        calls = [lambda: check(lib.hk_gemm_into(ctx, d[0], d[1], int(ta), int(tb), d[2]))]
+    elif name == "c2":
+        x = torch.randn((C2_ROWS, C2_WIDTH), generator=g, device="cuda").to(torch.bfloat16)
+        dy = torch.randn((C2_ROWS, C2_WIDTH), generator=g, device="cuda").to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn((C2_WIDTH,), generator=g, device="cuda")).float()
+        y, rstd = HipRuntime.rms_norm(x, w, 1e-6)
+        dx, dw = HipRuntime.rms_norm_backward(x, w, dy, rstd)
+        d = [runtime.desc(t) for t in (x, w, dy, y, rstd, dx, dw)]
+        eps = ctypes.c_double(1e-6)
+        calls = [lambda: check(lib.hk_rms_norm(ctx, d[0], d[1], eps, d[3], d[4])),
+                 lambda: check(lib.hk_rms_norm_backward(ctx, d[0], d[1], d[2], d[4], d[5], d[6]))]
+    elif name in ("attn_fwd", "attn_bwd"):
+        B, H, HKV, S, D = 4, 32, 8, 4096, 128
+        q = torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16)
+        k = torch.randn((B, HKV, S, D), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((B, HKV, S, D), generator=g, device="cuda").to(torch.bfloat16)
+        do = torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16)
+        o, lse = HipRuntime.attention_forward(q, k, v, D ** -0.5, True)
+        grads = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)]
+        dq, dk, dv = (runtime.desc(t) for t in grads)
+        dqkv = (runtime.desc(q), runtime.desc(k), runtime.desc(v), runtime.desc(o), runtime.desc(lse), runtime.desc(do))
+        sc, z = ctypes.c_float(D ** -0.5), ctypes.c_uint64(0)
+        if name == "attn_fwd":
+            calls = [lambda: check(lib.hk_attention_forward(ctx, dqkv[0], dqkv[1], dqkv[2], sc, 1, z, z, dqkv[3],
+                                                            dqkv[4]))]
+        else:
+            calls = [lambda: check(lib.hk_attention_backward(ctx, *dqkv, sc, 1, z, z, dq, dk, dv))]
+    else:  # rope
+        import numpy as np
+        pos = np.arange(4096, dtype=np.float64)[:, None]
+        ang = pos * (5e5 ** (-np.arange(0, 128, 2) / 128))[None, :]
+        cos = torch.from_numpy(np.cos(ang).astype(np.float32)).cuda()[None, None]
+        sin = torch.from_numpy(np.sin(ang).astype(np.float32)).cuda()[None, None]
+        q = torch.randn((4, 32, 4096, 128), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty_like(q)
+        d = (runtime.desc(q), runtime.desc(cos), runtime.desc(sin), runtime.desc(y))
+        calls = [lambda: check(lib.hk_rotary_prefix(ctx, d[0], d[1], d[2], 128, 1, d[3]))]
+    for _ in range(warmup):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        for c in calls:
+            c()
+    e1.record()
+    torch.cuda.synchronize()
+    return {"kernel": name, "steps": steps, "ms_per_step": round(e0.elapsed_time(e1) / max(steps, 1), 5)}
+
+
+def bench_vendor():
+    """The vendor libraries on the same shapes and data layout: hipBLASLt through torch.matmul
+    for C1/C3 (the weight stored [N,K] and read transposed for NT), PyTorch's scaled_dot_product_
+    attention for C4 (its K/V heads expanded to 32, which does not change its flop count). One
+    JSON line per workload with both rates. Evidence for where the kernels stand, not the metric."""
+    import torch
+    import torch.nn.functional as F
+    lines = []
+    for key in ("gemm8192_nt", "gemm8192_nn", "llama_up", "llama_down", "gemm4096_nt", "gemm1024_nt", "c1"):
+        m, n, k, ta, tb, label = GEMMS[key]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(m + n + k)
+        a = (torch.randn((m, k), generator=g, device="cuda") / k ** 0.5).to(torch.bfloat16)
+        b = (torch.randn((n, k) if tb else (k, n), generator=g, device="cuda") / k ** 0.5).to(torch.bfloat16)
+        bt = b.t() if tb else b
+        vendor_ms = time_gpu(lambda: torch.matmul(a, bt), iters=max(10, int(2e-3 / (2 * m * n * k / 1.5e15))))
+        ours_ms = bench_gemm(m, n, k, ta, tb)
+        fl = 2 * m * n * k
+        lines.append({"workload": label, "unit": "TFLOP/s", "hk": round(fl / ours_ms / 1e9, 1),
+                      "hipblaslt_torch_matmul": round(fl / vendor_ms / 1e9, 1), "hk_ms": round(ours_ms, 5),
+                      "vendor_ms": round(vendor_ms, 5)})
+    B, H, HKV, S, D = 4, 32, 8, 4096, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    q = torch.randn((B, H, S, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn((B, HKV, S, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn((B, HKV, S, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    kk = k.repeat_interleave(H // HKV, 1).contiguous()
+    vv = v.repeat_interleave(H // HKV, 1).contiguous()
+    f_ms, b_ms, ff, bf = bench_attention()
+    entry = {"workload": "C4 causal GQA attention B4 S4096 Hq32 Hkv8 D128", "unit": "TFLOP/s",
+             "hk_fwd": round(ff / f_ms / 1e9, 1), "hk_bwd": round(bf / b_ms / 1e9, 1)}
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for backend, tag in ((SDPBackend.FLASH_ATTENTION, "flash"), (SDPBackend.EFFICIENT_ATTENTION, "efficient")):
+        try:
+            with sdpa_kernel(backend):
+                qg, kg, vg = (t.clone().requires_grad_() for t in (q, kk, vv))
+                fwd = lambda: F.scaled_dot_product_attention(qg, kg, vg, is_causal=True)
+                fms = time_gpu(fwd, iters=5)
+                out = fwd()
+                go = torch.randn_like(out)
+                bms = time_gpu(lambda: torch.autograd.grad(out, (qg, kg, vg), go, retain_graph=True), iters=5)
+            entry[f"sdpa_{tag}_fwd"] = round(ff / fms / 1e9, 1)
+            entry[f"sdpa_{tag}_bwd"] = round(bf / bms / 1e9, 1)
+        except Exception as exc:  # a backend this build lacks is reported, not replaced
+            entry[f"sdpa_{tag}"] = f"unavailable: {str(exc)[:80]}"
+    lines.append(entry)
+    return lines
 
 
 def gemm_kernel_name(m, n, k, ta, tb):
@@ -446,6 +673,15 @@ def main():
         return
     HipRuntime.initialize_exclusive()
     HipRuntime.set_async(True)
+    if args.kernel:
+        print(json.dumps(run_kernel(args.kernel, args.steps, args.warmup)), flush=True)
+        if args.copy_calibration:
+            copy_calibration()
+        return
+    if args.vendor:
+        for entry in bench_vendor():
+            print(json.dumps(entry), flush=True)
+        return
     if args.only_c5:
         print(json.dumps(c5_line(args.steps, args.warmup)), flush=True)
         return
@@ -479,18 +715,15 @@ def main():
     }
     if not args.no_secondary:
         sec = []
-        for (m, n, k, ta, tb, name) in [(8192, 8192, 8192, 0, 1, "C3 GEMM 8192^3 NT"),
-                                        (8192, 8192, 8192, 0, 0, "C3 GEMM 8192^3 NN"),
-                                        (8192, 14336, 4096, 0, 1, "C3 Llama 8192x4096->14336 NT"),
-                                        (8192, 4096, 14336, 0, 1, "C3 Llama 8192x14336->4096 NT"),
-                                        (4096, 4096, 4096, 0, 1, "C3 GEMM 4096^3 NT"),
-                                        (1024, 1024, 1024, 0, 1, "C3 GEMM 1024^3 NT"),
-                                        (512, 1024, 1024, 0, 1, "C1 Linear X[512,1024] W[1024,1024]^T")]:
+        for key in ("gemm8192_nt", "gemm8192_nn", "llama_up", "llama_down", "gemm4096_nt", "gemm1024_nt", "c1"):
+            m, n, k, ta, tb, name = GEMMS[key]
             ms = bench_gemm(m, n, k, ta, tb)
             flops = 2 * m * n * k
             sec.append({"workload": name, "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
                         "ms": round(ms, 5),
-                        "roofline": roofline("mfma", flops, ms, gemm_kernel_name(m, n, k, ta, tb))})
+                        "roofline": roofline("mfma", flops, ms, gemm_kernel_name(m, n, k, ta, tb), key)})
+            if not args.no_cpu:
+                sec[-1]["cpu_baseline"] = cpu_baseline_gemm(m, n, k, ta, tb, CPU_ROWS.get(key))
         ms, algo = bench_rope()
         sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
                     "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
@@ -498,9 +731,11 @@ def main():
         try:
             f_ms, b_ms, ff, bf = bench_attention()
             sec.append({"workload": "C4 causal GQA attention fwd B4 S4096 Hq32 Hkv8 D128", "value": round(ff / f_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd_pp")})
+                        "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd_pp", "attn_fwd")})
             sec.append({"workload": "C4 causal GQA attention bwd B4 S4096 Hq32 Hkv8 D128", "value": round(bf / b_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq")})
+                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq", "attn_bwd")})
+            if not args.no_cpu:
+                sec[-1]["cpu_baseline"] = sec[-2]["cpu_baseline"] = cpu_baseline_attention()
         except Exception as exc:  # reported, never silently replaced by another path
             sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
         try:
@@ -510,10 +745,7 @@ def main():
         sec.extend(bench_widened())
         line["secondary"] = sec
     if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
+        copy_calibration()
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
         line["cpu_baseline"] = cpu_baseline_c2(threads)
