@@ -45,7 +45,7 @@ GEMMS = {
     "c1": (512, 1024, 1024, 0, 1, "C1 Linear X[512,1024] W[1024,1024]^T"),
 }
 # CPU-baseline sample rows per GEMM workload (None: the whole product)
-CPU_ROWS = {"gemm8192_nt": 256, "gemm8192_nn": 64, "llama_up": 256, "llama_down": 256}
+CPU_ROWS = {"gemm8192_nt": 256, "gemm8192_nn": 16, "llama_up": 256, "llama_down": 256}
 KERNELS = sorted(list(GEMMS) + ["c2", "attn_fwd", "attn_bwd", "rope"])
 
 
