@@ -165,6 +165,64 @@ hk_status hk_gemm_grouped_plan_check(const hk_tensor* a, const hk_tensor* weight
 hk_status hk_gemm_grouped_nt_into(hk_context* ctx, const hk_tensor* a, const hk_tensor* weights,
                                   const hk_group_ends* ends, hk_tensor* out);
 
+/* ------------------------------------------------ GEMM device programs (code object) */
+
+/* The reference's launch ABI for its 18 BF16 GEMM device programs
+ * (rust-ascend-kernels/src/ascend.rs:88-114, deepgemm/native.rs:80-93):
+ *   ruda_rust_bf16_{dense,batched}_{n,t}{n,t}_{bf16,f32}, ruda_rust_bf16_mgrouped_nt_{bf16,f32}
+ *   (hk_gm a, hk_gm b, hk_gm d, uint32_t m, uint32_t n, uint32_t k, int32_t* grouped_layout,
+ *    uint32_t num_groups, hk_epilogue epilogue)
+ * D = op(A) op(B), FP32 accumulation, BF16 (RNE) or F32 out; "t" in the name means A stored
+ * [K,M] (first letter) or B stored [N,K] (second letter). The programs ship ahead of time as one
+ * gfx950 code object, rust-ascend_amd/lib/hk_programs.hsaco (the reference's per-key checked
+ * artifacts, deepgemm/artifact.rs:6-27). The argument structs are the reference's, field for
+ * field (GmPtr / Epilogue, native.rs:80-86; sizes 24 and 32 bytes, native.rs:96). */
+typedef struct hk_gm {
+    uint64_t addr;          /* device address of the operand */
+    uint64_t stride_outer;  /* elements per row: the operand's last physical dimension */
+    uint64_t stride_batch;  /* elements per batch: m*k, n*k, m*n for batched programs, else 0 */
+} hk_gm;
+typedef struct hk_epilogue {
+    float alpha;  /* 1 */
+    uint32_t pad0;
+    uint64_t sfd;
+    uint64_t stride;
+    uint32_t n;   /* N */
+    uint32_t pad1;
+} hk_epilogue;
+typedef struct hk_module hk_module;
+typedef struct hk_function hk_function;
+
+/* Loads a code object image (an unbundled little-endian ELF64 gfx950 object of at most 128 MiB;
+ * the bytes are copied). Reference: Kernel::load's aclrtBinaryLoadFromData (native.rs:46-52),
+ * after artifact::read's size and ELF checks (artifact.rs:18-22). Counts in modules_loaded. */
+hk_status hk_module_load_data(hk_context* ctx, const void* image, size_t bytes, hk_module** out);
+/* Entry point `name` of a loaded module (one of the 18 names above; a repeated lookup returns the
+ * same handle, valid until the module is unloaded). Reference: aclrtBinaryGetFunction,
+ * native.rs:53-63. */
+hk_status hk_module_get_function(hk_context* ctx, hk_module* module, const char* name, hk_function** out);
+/* Launches a device program on the context's stream with `args`, the nine argument pointers in
+ * parameter order (&a, &b, &d, &m, &n, &k, &grouped_layout, &num_groups, &epilogue), then
+ * synchronizes unless async mode is on. block_dim is the reference's core count (it passes 32);
+ * any positive value is accepted, the grid being one 256-thread workgroup per 256x256 output
+ * tile. Before the launch every argument is checked against the reference's contract
+ * (GemmSpec::checked, plan.rs:68-80; the packing of execute_addresses, mod.rs:122-132): M/N/K
+ * positive multiples of 16; packed row-major strides; num_groups 0 (dense), 1..=4096 (batched)
+ * or the group count with grouped_layout from hk_group_ends_data and M its last end
+ * (M-grouped); epilogue {1, 0, 0, 0, N, 0}; 16-byte aligned operands, each inside one device
+ * allocation; the output overlapping no input. The 256x256 kernel's 32-bit offsets add one
+ * limit: M*K and N*K (K rounded up to 64) below 2^30 elements. Reference:
+ * aclrtLaunchKernelWithArgsArray (native.rs:11), as DeepGemm::execute_addresses calls it
+ * (mod.rs:122-145). */
+hk_status hk_launch_kernel_with_args(hk_context* ctx, const hk_function* fn, uint32_t block_dim, void** args);
+/* Unloads a module after the context's queued work completes; its function handles end with it.
+ * A poisoned context keeps the code loaded (HK_POISONED). Reference: Drop for Kernel,
+ * native.rs:66-76. */
+hk_status hk_module_unload(hk_context* ctx, hk_module* module);
+/* The device copy of uploaded group ends: the grouped_layout argument of the M-grouped
+ * programs. Reference: DeviceGroupEnds' device tensor (deepgemm/mod.rs:63-67,101). */
+hk_status hk_group_ends_data(hk_context* ctx, const hk_group_ends* ends, const int32_t** out);
+
 /* FP32-storage, BF16-compute GEMM: rounds A and B to BF16 into a_bf16/b_bf16
  * (the saved snapshots), then out(F32) = op(A) @ op(B).
  * Reference: AscendRuntime::gemm_bf16_fp32, runtime/mod.rs:388-392 (matrix.rs:84-93). */

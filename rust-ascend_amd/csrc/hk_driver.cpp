@@ -14,10 +14,12 @@
 // the HIP runtime when the library loads; there is no JIT build step and no CPU fallback.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -39,6 +41,9 @@ hk_status fail(hk_status st, const char* fmt, ...) {
     return st;
 }
 
+struct GroupEndsDev;
+struct ModuleDev;
+
 struct Ctx {
     int device = 0;
     int num_cus = 256;
@@ -50,6 +55,8 @@ struct Ctx {
     void* workspace = nullptr;
     size_t ws_bytes = 0;
     void* scratch = nullptr;  // device address of `scratch` below on this context's device
+    std::vector<GroupEndsDev*> group_tables;  // live uploads, for the device programs' checks
+    std::vector<ModuleDev*> modules;          // loaded device-program code objects
 };
 
 // Device memory of the allocation-free entry point (hk_rms_norm_backward_noalloc): its dgamma
@@ -320,15 +327,51 @@ hk_status grouped_spec(const hk_tensor* a, const hk_tensor* w, const int32_t* en
     return HK_OK;
 }
 
-// Uploaded group ends: the checked host copy and, on the device, the group of every 256-row
-// block of A (what the kernels index).
-constexpr uint64_t kGroupEndsMagic = 0x686b5f67726f7570ULL;
+// Uploaded group ends: the checked host copy and, in one device allocation, the ends themselves
+// (the grouped_layout argument of the M-grouped device programs) followed by the group of every
+// 256-row block of A (what libhk.so's grouped kernels index).
 struct GroupEndsDev {
-    uint64_t magic = kGroupEndsMagic;
     Ctx* ctx = nullptr;
     std::vector<int32_t> ends;
-    int32_t* block_group = nullptr;
+    int32_t* mem = nullptr;          // the allocation
+    int32_t* ends_dev = nullptr;     // mem: the ends, padded to 64 entries
+    int32_t* block_group = nullptr;  // after the padded ends
 };
+
+bool live_group_table(const Ctx* c, const void* h) {
+    return std::find(c->group_tables.begin(), c->group_tables.end(), h) != c->group_tables.end();
+}
+
+// A loaded device-program code object and the entry points looked up in it. The image stays
+// allocated with the module, as the reference keeps the verified ELF bytes alive
+// (deepgemm/native.rs:41-43).
+enum class ProgramKind { Dense, Batched, MGrouped };
+struct FunctionDev {
+    hipFunction_t fn = nullptr;
+    std::string name;
+    ProgramKind kind = ProgramKind::Dense;
+    bool ta = false, tb = false, out_bf16 = true;
+};
+struct ModuleDev {
+    Ctx* ctx = nullptr;
+    hipModule_t module = nullptr;
+    std::vector<unsigned char> image;
+    std::vector<std::unique_ptr<FunctionDev>> functions;
+};
+
+// Unload every module and free every group-ends table of a context whose stream has completed.
+void release_programs(Ctx* c) {
+    for (ModuleDev* m : c->modules) {
+        (void)hipModuleUnload(m->module);
+        delete m;
+    }
+    c->modules.clear();
+    for (GroupEndsDev* d : c->group_tables) {
+        (void)hipFree(d->mem);
+        delete d;
+    }
+    c->group_tables.clear();
+}
 
 bool out_matches(const GemmSpec& s, const hk_tensor* out) {
     if (out->dtype != s.out_dtype) return false;
@@ -426,9 +469,11 @@ hk_status hk_shutdown(hk_context* h) {
     if (!c || c != g_ctx) return fail(HK_NOT_INITIALIZED, "runtime is not initialized");
     {
         std::lock_guard<std::mutex> g(c->mu);
-        if (c->workspace) {
-            if (hipStreamSynchronize(c->stream) == hipSuccess) (void)hipFree(c->workspace);
-            // after a failed synchronization the buffer is leaked, never freed under queued work
+        // after a failed synchronization (or on a poisoned context) device memory and code objects
+        // are leaked, never freed under queued work
+        if (!c->poisoned && hipStreamSynchronize(c->stream) == hipSuccess) {
+            if (c->workspace) (void)hipFree(c->workspace);
+            release_programs(c);
         }
     }
     delete c;
@@ -596,19 +641,25 @@ hk_status hk_group_ends_upload(hk_context* h, const int32_t* ends, int32_t count
         while (ends[grp] <= b * 256) ++grp;  // first group whose end lies beyond the block's first row
         table[static_cast<size_t>(b)] = grp;
     }
+    const size_t padded = (static_cast<size_t>(count) + 63) & ~size_t(63);
+    std::vector<int32_t> image(padded + table.size(), 0);
+    std::copy(ends, ends + count, image.begin());
+    std::copy(table.begin(), table.end(), image.begin() + static_cast<std::ptrdiff_t>(padded));
     GroupEndsDev* d = new GroupEndsDev();
     d->ctx = g.c;
     d->ends.assign(ends, ends + count);
-    hipError_t e = hipMalloc(&d->block_group, table.size() * sizeof(int32_t));
+    hipError_t e = hipMalloc(&d->mem, image.size() * sizeof(int32_t));
     if (e == hipSuccess)
-        e = hipMemcpyAsync(d->block_group, table.data(), table.size() * sizeof(int32_t), hipMemcpyHostToDevice,
-                           g.c->stream);
+        e = hipMemcpyAsync(d->mem, image.data(), image.size() * sizeof(int32_t), hipMemcpyHostToDevice, g.c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g.c->stream);
     if (e != hipSuccess) {
-        if (d->block_group) (void)hipFree(d->block_group);
+        if (d->mem) (void)hipFree(d->mem);
         delete d;
         return fail(HK_HIP_ERROR, "group ends upload: %s", hipGetErrorString(e));
     }
+    d->ends_dev = d->mem;
+    d->block_group = d->mem + padded;
+    g.c->group_tables.push_back(d);
     *out = reinterpret_cast<hk_group_ends*>(d);
     return HK_OK;
 }
@@ -618,12 +669,13 @@ hk_status hk_group_ends_free(hk_context* h, hk_group_ends* ends) {
     GroupEndsDev* d = reinterpret_cast<GroupEndsDev*>(ends);
     OpGuard g(h);
     if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
-    if (d->magic != kGroupEndsMagic || d->ctx != g.c) return fail(HK_INVALID_ARGUMENT, "not a group-ends handle of this context");
+    if (!live_group_table(g.c, d)) return fail(HK_INVALID_ARGUMENT, "not a live group-ends handle of this context");
     if (g.c->poisoned) return fail(HK_POISONED, "poisoned context: memory is leaked rather than freed");
     hipError_t e = hipStreamSynchronize(g.c->stream);  // queued grouped GEMMs may still read the table
-    if (e == hipSuccess) e = hipFree(d->block_group);
+    if (e == hipSuccess) e = hipFree(d->mem);
     if (e != hipSuccess) return fail(HK_HIP_ERROR, "group ends free: %s", hipGetErrorString(e));
-    d->magic = 0;
+    auto& live = g.c->group_tables;
+    live.erase(std::remove(live.begin(), live.end(), d), live.end());
     delete d;
     return HK_OK;
 }
@@ -652,19 +704,304 @@ hk_status hk_gemm_grouped_nt_into(hk_context* h, const hk_tensor* a, const hk_te
                                   hk_tensor* out) {
     // Reference: DeepGemm::grouped_nt_into, deepgemm/mod.rs:74-78 and run (:87-97).
     if (!tensor_ok(out, "out")) return HK_INVALID_ARGUMENT;
+    if (!ends) return fail(HK_INVALID_ARGUMENT, "grouped GEMM requires uploaded group ends");
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
     const GroupEndsDev* d = reinterpret_cast<const GroupEndsDev*>(ends);
-    if (!d || d->magic != kGroupEndsMagic) return fail(HK_INVALID_ARGUMENT, "grouped GEMM requires uploaded group ends");
+    if (!live_group_table(g.c, d))
+        return fail(HK_INVALID_ARGUMENT, "grouped GEMM requires group ends uploaded to this context");
     GemmSpec s;
     hk_status st = grouped_spec(a, w, d->ends.data(), static_cast<int32_t>(d->ends.size()), out->dtype, &s);
     if (st != HK_OK) return st;
     if (!out_matches(s, out)) return fail(HK_INVALID_ARGUMENT, "grouped GEMM output layout mismatch: %s", shape_str(out).c_str());
     if (!disjoint({out}, {a, w})) return HK_INVALID_ARGUMENT;
-    OpGuard g(h);
-    if (g.st != HK_OK) return g.st;
-    if (d->ctx != g.c) return fail(HK_INVALID_ARGUMENT, "group ends belong to another context");
     hipError_t e = hk::gemm_bf16_grouped_nt(a->data, w->data, out->data, s.out_dtype == HK_BF16, s.m, s.n, s.k,
                                             d->block_group, g.c->num_cus, g.c->stream);
     return complete(g.c, e, "grouped_nt", 1);
+}
+
+// ------------------------------------------------------------------ GEMM device programs
+//
+// The reference reads each GEMM program from a checked artifact (deepgemm/artifact.rs:6-27), loads
+// it with aclrtBinaryLoadFromData, looks its entry up with aclrtBinaryGetFunction (native.rs:46-64)
+// and launches it with aclrtLaunchKernelWithArgsArray and a nine-pointer argv (native.rs:87-93,
+// deepgemm/mod.rs:122-145). Here the 18 programs are one gfx950 code object built ahead of time
+// (hk_programs.hip -> hk_programs.hsaco), loaded with hipModuleLoadData; the argv goes to
+// hipModuleLaunchKernel unchanged, since it is the programs' own parameter list. The programs trust
+// their arguments, so the launch checks every one against the reference's contract first.
+
+namespace {
+
+constexpr size_t kMaxImageBytes = size_t(128) << 20;  // artifact.rs:19
+constexpr uint32_t kEfAmdgpuMachGfx950 = 0x4f;
+
+uint16_t rd16(const unsigned char* p) {
+    uint16_t v;
+    std::memcpy(&v, p, sizeof v);
+    return v;
+}
+uint32_t rd32(const unsigned char* p) {
+    uint32_t v;
+    std::memcpy(&v, p, sizeof v);
+    return v;
+}
+uint64_t rd64(const unsigned char* p) {
+    uint64_t v;
+    std::memcpy(&v, p, sizeof v);
+    return v;
+}
+
+// A complete little-endian ELF64 AMDGPU code object for gfx950 whose headers and sections lie
+// inside the image (reference check: artifact.rs:18-22 for its own ELF64 object).
+hk_status check_code_object(const unsigned char* p, size_t n) {
+    if (n < 64 || n > kMaxImageBytes) return fail(HK_LOAD_ERROR, "invalid code object size %zu", n);
+    if (std::memcmp(p, "\x7f" "ELF\x02\x01", 6) != 0)
+        return fail(HK_LOAD_ERROR, "expected a little-endian ELF64 code object (an unbundled --genco image)");
+    if (rd16(p + 16) != 3 || rd16(p + 18) != 224)
+        return fail(HK_LOAD_ERROR, "not an AMDGPU code object (e_type %u, e_machine %u)", rd16(p + 16),
+                    rd16(p + 18));
+    const uint32_t mach = rd32(p + 48) & 0xff;
+    if (mach != kEfAmdgpuMachGfx950)
+        return fail(HK_LOAD_ERROR, "code object is for another GPU (e_flags machine 0x%x; gfx950 is 0x%x)", mach,
+                    kEfAmdgpuMachGfx950);
+    const uint64_t phoff = rd64(p + 32), shoff = rd64(p + 40);
+    const uint16_t phentsize = rd16(p + 54), phnum = rd16(p + 56);
+    const uint16_t shentsize = rd16(p + 58), shnum = rd16(p + 60);
+    if (phoff > n || uint64_t(phentsize) * phnum > n - phoff || shoff > n || shentsize < 64 ||
+        uint64_t(shentsize) * shnum > n - shoff)
+        return fail(HK_LOAD_ERROR, "truncated code object (header tables past the end of %zu bytes)", n);
+    for (uint16_t i = 0; i < shnum; ++i) {
+        const unsigned char* sh = p + shoff + uint64_t(i) * shentsize;
+        const uint32_t type = rd32(sh + 4);
+        const uint64_t off = rd64(sh + 24), size = rd64(sh + 32);
+        if (type != 8 /* SHT_NOBITS */ && (off > n || size > n - off))
+            return fail(HK_LOAD_ERROR, "truncated code object (section %u past the end of %zu bytes)", i, n);
+    }
+    return HK_OK;
+}
+
+// The code object's entry points, by name: ruda_rust_bf16_{dense,batched}_{n,t}{n,t}_{bf16,f32} and
+// ruda_rust_bf16_mgrouped_nt_{bf16,f32} (rust-ascend-kernels/src/config.rs:14-40; the name is
+// "ruda_rust_" + GemmSpec::key, deepgemm/plan.rs:84-85).
+bool program_spec(const char* name, FunctionDev* f) {
+    for (int kind = 0; kind < 3; ++kind)
+        for (int ta = 0; ta < 2; ++ta)
+            for (int tb = 0; tb < 2; ++tb)
+                for (int bf16 = 0; bf16 < 2; ++bf16) {
+                    if (kind == 2 && (ta || !tb)) continue;  // M-grouped is NT only
+                    char want[64];
+                    std::snprintf(want, sizeof want, "ruda_rust_bf16_%s_%c%c_%s",
+                                  kind == 0 ? "dense" : kind == 1 ? "batched" : "mgrouped", ta ? 't' : 'n',
+                                  tb ? 't' : 'n', bf16 ? "bf16" : "f32");
+                    if (std::strcmp(name, want) != 0) continue;
+                    f->name = want;
+                    f->kind = static_cast<ProgramKind>(kind);
+                    f->ta = ta;
+                    f->tb = tb;
+                    f->out_bf16 = bf16;
+                    return true;
+                }
+    return false;
+}
+
+ModuleDev* live_module(const Ctx* c, const void* h) {
+    for (ModuleDev* m : c->modules)
+        if (m == h) return m;
+    return nullptr;
+}
+
+const FunctionDev* live_function(const Ctx* c, const void* h) {
+    for (const ModuleDev* m : c->modules)
+        for (const auto& f : m->functions)
+            if (f.get() == h) return f.get();
+    return nullptr;
+}
+
+// [addr, addr + bytes) inside one device allocation of this process.
+bool in_device_allocation(uint64_t addr, uint64_t bytes) {
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(addr)) != hipSuccess) {
+        (void)hipGetLastError();  // not device memory: clear the error so no later launch check sees it
+        return false;
+    }
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return addr >= b && bytes <= size && addr - b <= size - bytes;
+}
+
+}  // namespace
+
+hk_status hk_module_load_data(hk_context* h, const void* image, size_t bytes, hk_module** out) {
+    // Reference: Kernel::load (aclrtBinaryLoadFromData), deepgemm/native.rs:46-52, after
+    // artifact::read's checks (artifact.rs:18-22).
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    if (!image) return fail(HK_INVALID_ARGUMENT, "null code object image");
+    const unsigned char* p = static_cast<const unsigned char*>(image);
+    hk_status st = check_code_object(p, bytes);
+    if (st != HK_OK) return st;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    auto m = std::make_unique<ModuleDev>();
+    m->ctx = g.c;
+    m->image.assign(p, p + bytes);
+    hipError_t e = hipModuleLoadData(&m->module, m->image.data());
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(HK_LOAD_ERROR, "hipModuleLoadData: %s", hipGetErrorString(e));
+    }
+    g.c->modules.push_back(m.get());
+    g.c->stats.modules_loaded += 1;
+    *out = reinterpret_cast<hk_module*>(m.release());
+    return HK_OK;
+}
+
+hk_status hk_module_get_function(hk_context* h, hk_module* module, const char* name, hk_function** out) {
+    // Reference: Kernel::load's aclrtBinaryGetFunction, deepgemm/native.rs:53-63.
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    if (!name) return fail(HK_INVALID_ARGUMENT, "null program name");
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    ModuleDev* m = live_module(g.c, module);
+    if (!m) return fail(HK_INVALID_ARGUMENT, "not a loaded module of this context");
+    auto f = std::make_unique<FunctionDev>();
+    if (!program_spec(name, f.get()))
+        return fail(HK_INVALID_ARGUMENT,
+                    "unknown device program \"%.80s\" (the code object holds ruda_rust_bf16_{dense,batched}_{n,t}{n,t}_"
+                    "{bf16,f32} and ruda_rust_bf16_mgrouped_nt_{bf16,f32})", name);
+    for (const auto& have : m->functions)
+        if (have->name == f->name) {
+            *out = reinterpret_cast<hk_function*>(have.get());
+            return HK_OK;
+        }
+    hipError_t e = hipModuleGetFunction(&f->fn, m->module, f->name.c_str());
+    if (e != hipSuccess || !f->fn) {
+        (void)hipGetLastError();
+        return fail(HK_LOAD_ERROR, "hipModuleGetFunction(%s): %s", f->name.c_str(), hipGetErrorString(e));
+    }
+    m->functions.push_back(std::move(f));
+    *out = reinterpret_cast<hk_function*>(m->functions.back().get());
+    return HK_OK;
+}
+
+hk_status hk_launch_kernel_with_args(hk_context* h, const hk_function* function, uint32_t block_dim, void** args) {
+    // Reference: aclrtLaunchKernelWithArgsArray(function, 32, stream, NULL, argv) and the argv it is
+    // given, deepgemm/native.rs:11,87-93 and deepgemm/mod.rs:122-145; the contract checked here is
+    // GemmSpec::checked's (plan.rs:68-80) plus the packing execute_addresses writes (mod.rs:125-131).
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const FunctionDev* f = live_function(g.c, function);
+    if (!f) return fail(HK_INVALID_ARGUMENT, "not a device program of a module loaded in this context");
+    if (block_dim == 0) return fail(HK_INVALID_ARGUMENT, "block_dim must be positive");
+    if (!args) return fail(HK_INVALID_ARGUMENT, "null argument array");
+    for (int i = 0; i < 9; ++i)
+        if (!args[i]) return fail(HK_INVALID_ARGUMENT, "argument pointer %d of 9 is null", i);
+    hk_gm a, b, d;
+    uint32_t m, n, k, groups;
+    const int32_t* ends_ptr;
+    hk_epilogue ep;
+    std::memcpy(&a, args[0], sizeof a);
+    std::memcpy(&b, args[1], sizeof b);
+    std::memcpy(&d, args[2], sizeof d);
+    std::memcpy(&m, args[3], sizeof m);
+    std::memcpy(&n, args[4], sizeof n);
+    std::memcpy(&k, args[5], sizeof k);
+    std::memcpy(&ends_ptr, args[6], sizeof ends_ptr);
+    std::memcpy(&groups, args[7], sizeof groups);
+    std::memcpy(&ep, args[8], sizeof ep);
+    for (uint32_t x : {m, n, k})
+        if (x == 0 || x % 16 != 0 || x > INT32_MAX)
+            return fail(HK_INVALID_ARGUMENT,
+                        "M/N/K must be positive multiples of 16 <= INT32_MAX; batches/groups 1..=4096 (M=%u N=%u K=%u)",
+                        m, n, k);
+    if (ep.alpha != 1.0f || ep.pad0 != 0 || ep.sfd != 0 || ep.stride != 0 || ep.n != n || ep.pad1 != 0)
+        return fail(HK_INVALID_ARGUMENT, "epilogue must be {alpha 1, pad 0, sfd 0, stride 0, n = N} (mod.rs:132)");
+    int64_t batches = 1, slices = 1;
+    if (f->kind == ProgramKind::Dense) {
+        if (groups != 0 || ends_ptr) return fail(HK_INVALID_ARGUMENT, "dense programs take num_groups 0 and no grouped_layout");
+    } else if (f->kind == ProgramKind::Batched) {
+        if (groups == 0 || groups > 4096 || ends_ptr)
+            return fail(HK_INVALID_ARGUMENT, "batched programs take num_groups 1..=4096 (the batch) and no grouped_layout");
+        batches = slices = groups;
+    } else {
+        const GroupEndsDev* t = nullptr;
+        for (const GroupEndsDev* x : g.c->group_tables)
+            if (x->ends_dev == ends_ptr) t = x;
+        if (!t) return fail(HK_INVALID_ARGUMENT, "grouped_layout must be the device ends of group ends uploaded to this context");
+        if (groups != t->ends.size() || static_cast<int64_t>(m) != t->ends.back())
+            return fail(HK_INVALID_ARGUMENT, "grouped NT dimensions do not match the physical prefix sums");
+        slices = groups;
+    }
+    const bool batched = f->kind == ProgramKind::Batched;
+    const uint64_t want_a = f->ta ? m : k, want_b = f->tb ? k : n;
+    const uint64_t mk = uint64_t(m) * k, nk = uint64_t(n) * k, mn = uint64_t(m) * n;
+    if (a.stride_outer != want_a || a.stride_batch != (batched ? mk : 0) || b.stride_outer != want_b ||
+        b.stride_batch != (batched ? nk : 0) || d.stride_outer != n || d.stride_batch != (batched ? mn : 0))
+        return fail(HK_INVALID_ARGUMENT,
+                    "device programs take packed row-major operands: strides (outer, batch) A (%llu, %llu) B (%llu, "
+                    "%llu) D (%llu, %llu), expected A (%llu, %llu) B (%llu, %llu) D (%u, %llu)",
+                    (unsigned long long)a.stride_outer, (unsigned long long)a.stride_batch,
+                    (unsigned long long)b.stride_outer, (unsigned long long)b.stride_batch,
+                    (unsigned long long)d.stride_outer, (unsigned long long)d.stride_batch,
+                    (unsigned long long)want_a, (unsigned long long)(batched ? mk : 0), (unsigned long long)want_b,
+                    (unsigned long long)(batched ? nk : 0), n, (unsigned long long)(batched ? mn : 0));
+    // The 256x256 tile kernel addresses each operand slice with 32-bit byte offsets up to the end of
+    // the last 64-deep K stage.
+    const uint64_t k64 = (uint64_t(k) + 63) / 64 * 64;
+    if (uint64_t(m) * k64 * 2 >= (uint64_t(1) << 31) || uint64_t(n) * k64 * 2 >= (uint64_t(1) << 31))
+        return fail(HK_INVALID_ARGUMENT,
+                    "operand slice too large for the device programs' 32-bit offsets (M*K and N*K, K rounded up to "
+                    "64, must stay below 2^30 elements)");
+    for (const hk_gm* x : {&a, &b, &d})
+        if (x->addr == 0 || x->addr % 16 != 0)
+            return fail(HK_INVALID_ARGUMENT, "operand addresses must be non-null and 16-byte aligned");
+    const uint64_t a_bytes = uint64_t(batches) * mk * 2, b_bytes = uint64_t(slices) * nk * 2;
+    const uint64_t d_bytes = uint64_t(batches) * mn * (f->out_bf16 ? 2 : 4);
+    auto overlap = [](uint64_t p, uint64_t pn, uint64_t q, uint64_t qn) { return p < q + qn && q < p + pn; };
+    if (overlap(d.addr, d_bytes, a.addr, a_bytes) || overlap(d.addr, d_bytes, b.addr, b_bytes))
+        return fail(HK_INVALID_ARGUMENT, "GEMM output overlaps input");
+    if (!in_device_allocation(a.addr, a_bytes) || !in_device_allocation(b.addr, b_bytes) ||
+        !in_device_allocation(d.addr, d_bytes))
+        return fail(HK_INVALID_ARGUMENT, "an operand range is not inside one device allocation of this process");
+    const unsigned tiles = ((m + 255) / 256) * ((n + 255) / 256);
+    hipError_t e = hipModuleLaunchKernel(f->fn, tiles, 1, static_cast<unsigned>(batches), 256, 1, 1, 0, g.c->stream,
+                                         args, nullptr);
+    return complete(g.c, e, f->name.c_str(), 1);
+}
+
+hk_status hk_module_unload(hk_context* h, hk_module* module) {
+    // Reference: Drop for Kernel (aclrtBinaryUnLoad once the session's work is complete, else the
+    // code is leaked), deepgemm/native.rs:66-76.
+    if (!module) return HK_OK;
+    OpGuard g(h);
+    if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
+    ModuleDev* m = live_module(g.c, module);
+    if (!m) return fail(HK_INVALID_ARGUMENT, "not a loaded module of this context");
+    if (g.c->poisoned) return fail(HK_POISONED, "poisoned context: the code object stays loaded under queued work");
+    hipError_t e = hipStreamSynchronize(g.c->stream);
+    if (e != hipSuccess) {
+        g.c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "module unload: synchronization status %d (%s)", static_cast<int>(e),
+                    hipGetErrorString(e));
+    }
+    e = hipModuleUnload(m->module);
+    auto& live = g.c->modules;
+    live.erase(std::remove(live.begin(), live.end(), m), live.end());
+    delete m;
+    if (e != hipSuccess) return fail(HK_HIP_ERROR, "hipModuleUnload: %s", hipGetErrorString(e));
+    return HK_OK;
+}
+
+hk_status hk_group_ends_data(hk_context* h, const hk_group_ends* ends, const int32_t** out) {
+    // Reference: DeviceGroupEnds' device tensor, the grouped_layout argument (deepgemm/mod.rs:70,101).
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (!live_group_table(g.c, ends)) return fail(HK_INVALID_ARGUMENT, "not a live group-ends handle of this context");
+    *out = reinterpret_cast<const GroupEndsDev*>(ends)->ends_dev;
+    return HK_OK;
 }
 
 hk_status hk_linear_nt_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,

@@ -27,6 +27,7 @@
 //     contiguous range of tiles, then grouped in 8-tile-row bands, so tiles that share A/B
 //     slices run on the same XCD's L2.
 #include "hk_common.hpp"
+#include "hk_gemm_device.hpp"
 #include "hk_kernels.hpp"
 
 namespace hk {
@@ -35,26 +36,6 @@ namespace {
 
 constexpr int kBK = 64;
 constexpr int kThreads = 256;
-
-struct GemmArgs {
-    const uint16_t* a;  // [batch][m][k]
-    const uint16_t* b;  // [batch][n][k], or [groups][n][k] for the M-grouped form
-    void* c;            // [batch][m][n]
-    int m, n, k;
-    int tiles_m, tiles_n;
-    // M-grouped form (batch 1): block_group[r / 256] is the weight slice of rows r of A and C.
-    // Group ends are multiples of 256, so an output tile (256, 128 or 64 rows) has one group.
-    const int32_t* block_group;
-    // 4-wave kernel tile order: 0 = bands of 4 M-tile rows per XCD, else bands of this many
-    // N-tile columns.
-    int band_n;
-};
-
-// B operand of the tile whose first output row is row0 in batch g.
-__device__ __forceinline__ const uint16_t* weight_slice(const GemmArgs& p, int row0, int64_t g) {
-    const int64_t slice = p.block_group ? static_cast<int64_t>(p.block_group[row0 >> 8]) : g;
-    return p.b + slice * static_cast<int64_t>(p.n) * p.k;
-}
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kBK + ((chunk ^ (row & 7)) << 3); }
 
@@ -250,9 +231,6 @@ __device__ __forceinline__ void mma_frags(Frags<BM, BN>& f, f32x16_t (&acc)[BM /
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
 }
 
-// The compiler may not move instructions across this point.
-__device__ __forceinline__ void phase_fence() { __builtin_amdgcn_sched_barrier(0); }
-
 // Fragment r of a slice: r < TI is A fragment r, otherwise B fragment r - TI.
 template <int BM, int BN>
 __device__ __forceinline__ void read_frag(const uint16_t* stage, int ks, int r, int wm, int wn, int lr, int lk,
@@ -320,20 +298,6 @@ __device__ __forceinline__ void mma_frags_loads(Frags<BM, BN>& f, f32x16_t (&acc
     }
 }
 
-// Workgroup barrier after which the loads of the step before the last N outstanding ones
-// (per wave, in issue order) have landed in LDS and every LDS read issued before it has
-// completed. A plain barrier without the memory fence of __syncthreads, whose release
-// semantics would wait for every outstanding load, including the prefetches meant to stay in
-// flight. The empty asm statements keep the compiler from moving memory accesses across it.
-// gfx9 s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
-template <int N>
-__device__ __forceinline__ void stage_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 template <int BM, int BN, bool OUT_BF16>
 __device__ __forceinline__ void store_tile(const GemmArgs& p, const f32x16_t (&acc)[BM / 64][BN / 64], int tm,
@@ -465,218 +429,6 @@ gemm_nt_dma_kernel(GemmArgs p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     store_tile<BM, BN, OUT_BF16>(p, acc, tm, tn, g, wm, wn, lr, lk);
-}
-
-// 256x256-tile stages: 64 k deep, two 64 KB LDS slots (A half, then B half).
-constexpr int kPPTile = 256;
-constexpr int kPK = 64;  // K per stage
-
-__device__ __forceinline__ int swz64(int row, int chunk) {  // element offset in a [rows][64] stage
-    return row * kPK + ((chunk ^ ((row >> 1) & 7)) << 3);
-}
-
-
-// 256x256 output tiles with four wavefronts, one per SIMD, each owning a 128x128 block of 8x8
-// v_mfma_f32_16x16x32_bf16 tiles (4 accumulators per lane each: the whole AGPR file). Measured
-// against an 8-wave "ping-pong" design (two groups of four waves alternating MFMA turns and
-// memory turns, 32x32x16 MFMAs) at 8192^3 on N(0,1) data, this runs ~15% faster:
-//   * one wave per SIMD interleaves its own memory instructions between its MFMAs, and a 128x128
-//     block reads 0.5 KB of LDS operands per 32x32x16-equivalent MFMA instead of 0.75 KB;
-//   * the 16x16x32 shape moves fewer register-file bytes per multiply-accumulate than 32x32x16
-//     (4 accumulator registers per lane per MFMA instead of 16), and this part is power-limited:
-//     the clock it sustains depends on the work per flop;
-//   * tiles travel straight from global memory into LDS (buffer_load ... lds; no staging
-//     registers, no LDS write instructions). K stages of 64 in two 64 KB slots, 128-byte
-//     swizzled rows (full 128-byte lines per global request). A stage is two k-slices of 32 (64 MFMAs each) with one
-//     barrier between them; all of stage s+2 is fetched during slice 1 of stage s into the slot
-//     that barrier has just freed, so every load has one to two slices to land before the
-//     barrier that needs it (issuing the same loads half a stage later cost ~10%);
-//   * within a slice, a fragment read for the next slice follows every fourth MFMA and a load
-//     follows every fourth MFMA two later, so no gap between MFMAs holds more than one memory
-//     instruction (bunching them cost 3-8%);
-//   * bands of 4 M-tiles per XCD for square tile grids (8 measured 2% slower at 8192^3, 16 8%), of
-//     8 N-tiles otherwise (see launch_pp);
-//   * an MN-major operand (the backward's dY W and dY^T X) is read in place: its half of a stage
-//     is 64 k-rows of 256 columns (512-byte rows, 64-byte blocks XORed with k-row % 4) filled by
-//     the same 1 KB global->LDS loads (two k-rows each), and each fragment is two
-//     ds_read_b64_tr_b16 transposing reads, which hand every lane the 8 consecutive k of its
-//     column that the K-major 16-byte read gives. The four 16-lane groups read the same 16
-//     columns at k-rows 8 apart, so two groups share banks (a 2-way conflict: ~128 LDS cycles
-//     per 1024-cycle slice). 8192^3 NN/TN/TT: 1.48-1.51 PFLOP/s, against 1.30 for the 8-wave
-//     ping-pong design with register-staged loads and transposing reads that this replaced.
-constexpr int kW4Threads = 256;
-
-// Byte offset past any operand's buffer range: a buffer load at it reads zero. The range check
-// compares the unsigned 32-bit offset with the resource's byte count, which pp_applies keeps
-// below 2^31 (m * k * 2 <= m * k64 * 2 < 2^31), so 2^31 is out of range for every operand.
-constexpr int kOutOfRange = static_cast<int>(0x80000000u);
-
-// KTAIL: K % 64 != 0 (K % 8 == 0), so the last stage is partial. Its K-major 16-byte chunks past
-// K take an out-of-range offset and read as zero; the k-rows of an MN-major operand past K lie
-// past the end of that operand's range already. Zeros add nothing to the accumulators, so the
-// result equals that of K zero-padded to a multiple of 64.
-template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL = false>
-__global__ void __launch_bounds__(kW4Threads, 1)
-gemm_nt_m16_kernel(GemmArgs p) {
-    constexpr int kStage = 2 * kPPTile * kPK;
-    __shared__ __attribute__((aligned(1024))) uint16_t slot0[kStage];
-    __shared__ __attribute__((aligned(1024))) uint16_t slot1[kStage];
-
-    const int tiles = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
-    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-    int tm, tn;
-    if (p.band_n == 0) {
-        constexpr int GROUP = 4;
-        const int per_group = GROUP * p.tiles_n;
-        const int first_m = (bid / per_group) * GROUP;
-        const int gsize = min(p.tiles_m - first_m, GROUP);
-        tm = first_m + (bid % per_group) % gsize;
-        tn = (bid % per_group) / gsize;
-    } else {
-        const int per_group = p.band_n * p.tiles_m;
-        const int first_n = (bid / per_group) * p.band_n;
-        const int gsize = min(p.tiles_n - first_n, p.band_n);
-        tn = first_n + (bid % per_group) % gsize;
-        tm = (bid % per_group) / gsize;
-    }
-    const int64_t g = blockIdx.z;
-    const uint16_t* A = p.a + g * static_cast<int64_t>(p.m) * p.k;
-    const uint16_t* B = weight_slice(p, tm * kPPTile, g);
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int l16 = lane & 15, lg = lane >> 4;  // 16x16x32 operand: row l16, k chunk lg of the slice
-
-    const int r_in = lane >> 3;
-    const int src_chunk = (lane & 7) ^ ((4 * (wave & 1) + (r_in >> 1)) & 7);
-    const int voff = (r_in * p.k + src_chunk * 8) * 2;
-    const i32x4_t ra4 = buffer_resource(A, p.m * p.k * 2), rb4 = buffer_resource(B, p.n * p.k * 2);
-    // MN-major operand (A stored [K,M] or B stored [K,N]): its half of a stage is 64 k-rows x 256
-    // columns, 512-byte rows whose 64-byte blocks are XORed with k-row % 4. Load d of a wave fills
-    // k-rows 2(wave + 4d) + {0, 1}; lane l takes position l % 32 of k-row l / 32, which holds the
-    // global chunk the swizzle puts there (k-row % 4 is the same for every d). The k-row and column
-    // are in the range-checked offset (K * M * 2 < 2^31): columns past M (N) in the last k-row read
-    // as zero, elsewhere they feed only outputs that are not stored.
-    const int mn_row0 = 2 * wave + (lane >> 5), mn_pos = lane & 31;
-    const int mn_c = (((mn_pos >> 2) ^ (mn_row0 & 3)) << 2) | (mn_pos & 3);
-    const int mn_voff_a = (mn_row0 * p.m + tm * kPPTile + mn_c * 8) * 2;
-    const int mn_voff_b = (mn_row0 * p.n + tn * kPPTile + mn_c * 8) * 2;
-    const uint32_t lds0 = lds_address(slot0), lds1 = lds_address(slot1);
-    // K-major load: the stage offset moves into the lane's offset, which the range check sees
-    auto kmajor = [&](const i32x4_t& r, uint32_t dst, int row_off, int kt) __attribute__((always_inline)) {
-        if constexpr (KTAIL)
-            load_lds16(r, dst, kt * kPK + src_chunk * 8 < p.k ? row_off + kt * kPK * 2 : kOutOfRange, 0);
-        else
-            load_lds16(r, dst, row_off, kt * kPK * 2);
-    };
-    auto dload = [&](uint32_t lds_slot, int kt, int d) __attribute__((always_inline)) {
-        const int blk = wave + 4 * d;
-        const uint32_t dst = lds_slot + (wave * 8 * kPK + d * 4 * 8 * kPK) * 2;
-        if (d < 8) {
-            if constexpr (A_MN) load_lds16(ra4, dst, mn_voff_a + (kt * kPK + 8 * d) * p.m * 2, 0);
-            else kmajor(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt);
-        } else {
-            if constexpr (B_MN) load_lds16(rb4, dst, mn_voff_b + (kt * kPK + 8 * (d - 8)) * p.n * 2, 0);
-            else kmajor(rb4, dst, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt);
-        }
-    };
-
-    const int a_row = 128 * wm + l16, b_row = kPPTile + 128 * wn + l16;
-    // Transposing read of an MN-major 16x16x32 operand: columns col0 .. col0+15 (col0 % 16 == 0),
-    // k-rows k0 .. k0+7 with k0 = 32 ks + 8 lg (each 16-lane group its own k0; k0 % 4 == 0, so the
-    // k-row's XOR term is i/4). Lane i of a group reads 4 columns of k-row k0 + i/4 (then k0 + 4 +
-    // i/4), and the hardware hands lane i the 4 k values of column col0 + i.
-    const int tr_i = lane & 15;
-    const int tr_lane = (tr_i >> 2) * kPPTile + 4 * (tr_i & 3);
-    auto read_tr = [&](const uint16_t* stage, int k0, int col0) __attribute__((always_inline)) {
-        const uint16_t* at = stage + k0 * kPPTile + tr_lane + ((((col0 >> 5) ^ (tr_i >> 2)) << 5) | (col0 & 31));
-        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at));
-        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(at + 4 * kPPTile));
-        typedef short v8i16_t __attribute__((ext_vector_type(8)));
-        const v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        return __builtin_bit_cast(bf16x8_t, v);
-    };
-    bf16x8_t fa[2][8], fb[2][8];
-    auto read1 = [&](const uint16_t* slot, int ks, int buf, int f) __attribute__((always_inline)) {
-        const int c = 4 * ks + lg;
-        if (f < 8) {
-            if constexpr (A_MN) fa[buf][f] = read_tr(slot, 8 * c, 128 * wm + 16 * f);
-            else fa[buf][f] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 16 * f, c));
-        } else {
-            if constexpr (B_MN) fb[buf][f - 8] = read_tr(slot + kPPTile * kPK, 8 * c, 128 * wn + 16 * (f - 8));
-            else fb[buf][f - 8] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 16 * (f - 8), c));
-        }
-    };
-
-    f32x4_t acc[8][8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc[i][j]));
-
-    const int nk = KTAIL ? (p.k + kPK - 1) / kPK : p.k / kPK;
-    // 64 MFMAs on buffer `cur`; after MFMA 4t: fragment read t of slice `next_ks` from `next_slot`
-    // into the other buffer; after MFMA 4t + 2: the direct load of block d0 + t (if below d1).
-    auto slice = [&](int cur, const uint16_t* next_slot, int next_ks, uint32_t load_slot, int d0, int d1,
-                     int kt) __attribute__((always_inline)) {
-        const int nxt = cur ^ 1;
-#pragma unroll
-        for (int e = 0; e < 64; ++e) {
-            const int i = e >> 3, j = e & 7;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
-            phase_fence();
-            if ((e & 3) == 0) read1(next_slot, next_ks, nxt, e >> 2);
-            else if ((e & 3) == 2 && d0 + (e >> 2) < d1) dload(load_slot, kt, d0 + (e >> 2));
-            phase_fence();
-        }
-    };
-
-    // Prologue: stage 0 into slot 0, stage 1 into slot 1, slice 0's fragments.
-#pragma unroll
-    for (int d = 0; d < 16; ++d) dload(lds0, 0, d);
-    stage_barrier<0>();
-#pragma unroll
-    for (int d = 0; d < 16; ++d) dload(lds1, nk > 1 ? 1 : 0, d);
-#pragma unroll
-    for (int f = 0; f < 16; ++f) read1(slot0, 0, 0, f);
-
-    auto stage = [&](const uint16_t* R, const uint16_t* W, uint32_t Rl, int s) __attribute__((always_inline)) {
-        const int ahead = s + 2 < nk ? s + 2 : nk - 1;
-        slice(0, R, 1, Rl, 0, 0, ahead);      // reads only
-        stage_barrier<0>();                   // stage s+1 complete in W; every read of R done
-        slice(1, W, 0, Rl, 0, 16, ahead);     // + all of stage s+2 into the freed R
-    };
-    int s = 0;
-    do {
-        stage(slot0, slot1, lds0, s);
-        if (s + 1 < nk) stage(slot1, slot0, lds1, s + 1);
-        s += 2;
-    } while (s < nk);
-    stage_barrier<0>();  // no load may still be writing LDS at exit
-
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
-        if (m >= p.m) continue;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int n = tn * kPPTile + 128 * wn + 16 * j + 4 * lg;
-            if (n >= p.n) continue;
-            const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
-            if constexpr (OUT_BF16) {
-                u32x2_t w = {pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
-                *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = w;
-            } else {
-                *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.c) + off) = acc[i][j];
-            }
-        }
-    }
 }
 
 // out[g][c][r] = in[g][r][c] for BF16, 64x64 tiles through LDS (padded rows).

@@ -13,6 +13,8 @@ import threading
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.normpath(os.path.join(_PKG, "..", "lib", "libhk.so"))
 HEADER_PATH = os.path.normpath(os.path.join(_PKG, "..", "..", "include", "hk.h"))
+# the GEMM device programs' code object (built with libhk.so, loaded by hk_module_load_data)
+PROGRAMS_PATH = os.path.normpath(os.path.join(_PKG, "..", "lib", "hk_programs.hsaco"))
 
 # Status codes (hk_status) and their reference counterparts (CannError, rust-ascend-driver/src/lib.rs:18-78).
 OK, INVALID_ARGUMENT, HIP_ERROR, COMPLETION_ERROR, POISONED, NOT_INITIALIZED, LOAD_ERROR = range(7)
@@ -52,6 +54,17 @@ class HkGemmPlan(ctypes.Structure):
                 ("out_shape", ctypes.c_int64 * 3), ("key", ctypes.c_char * 32)]
 
 
+class HkGm(ctypes.Structure):
+    """hk_gm: the reference's RudaGm / GmPtr (deepgemm/native.rs:80-82), 24 bytes."""
+    _fields_ = [("addr", ctypes.c_uint64), ("stride_outer", ctypes.c_uint64), ("stride_batch", ctypes.c_uint64)]
+
+
+class HkEpilogue(ctypes.Structure):
+    """hk_epilogue: the reference's RudaEpilogue / Epilogue (deepgemm/native.rs:83-85), 32 bytes."""
+    _fields_ = [("alpha", ctypes.c_float), ("pad0", ctypes.c_uint32), ("sfd", ctypes.c_uint64),
+                ("stride", ctypes.c_uint64), ("n", ctypes.c_uint32), ("pad1", ctypes.c_uint32)]
+
+
 _T = ctypes.POINTER(HkTensor)
 _CTX = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -78,6 +91,11 @@ SIGNATURES = {
     "hk_group_ends_check": [ctypes.POINTER(_i32), _i32],
     "hk_group_ends_upload": [_CTX, ctypes.POINTER(_i32), _i32, ctypes.POINTER(ctypes.c_void_p)],
     "hk_group_ends_free": [_CTX, ctypes.c_void_p],
+    "hk_group_ends_data": [_CTX, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)],
+    "hk_module_load_data": [_CTX, ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)],
+    "hk_module_get_function": [_CTX, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)],
+    "hk_launch_kernel_with_args": [_CTX, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_void_p)],
+    "hk_module_unload": [_CTX, ctypes.c_void_p],
     "hk_gemm_grouped_plan_check": [_T, _T, ctypes.POINTER(_i32), _i32, _i32, ctypes.POINTER(HkGemmPlan)],
     "hk_gemm_grouped_nt_into": [_CTX, _T, _T, ctypes.c_void_p, _T],
     "hk_linear_nt_backward": [_CTX, _T, _T, _T, _T, _T],
