@@ -165,6 +165,22 @@ hk_status hk_gemm_grouped_plan_check(const hk_tensor* a, const hk_tensor* weight
 hk_status hk_gemm_grouped_nt_into(hk_context* ctx, const hk_tensor* a, const hk_tensor* weights,
                                   const hk_group_ends* ends, hk_tensor* out);
 
+/* Generic floating matmul with the inputs' dtype out (aclnnMatmul KEEP_DTYPE): F32, F16 or BF16
+ * A [..., M, K] and B [..., K, N], rank 2..6 each, batch dims broadcast numpy-style, any M/N/K
+ * (K = 0 gives zeros), FP32 products and sums, the output rounded to the dtype (RNE).
+ * Host-only output layout. Reference: generic_matrix::output_layout (runtime/generic_matrix.rs:4-15,
+ * tensor/layout.rs:106-142). */
+hk_status hk_matmul_layout(const hk_tensor* a, const hk_tensor* b, hk_tensor* out);
+/* out = A @ B into a caller-allocated contiguous output of that layout. Reference:
+ * AscendRuntime::tensor_matmul (runtime/mod.rs:156-158; generic_matrix.rs:17-54, worker.rs:128-162),
+ * the op behind RudaAscend::float_matmul (src/backend.rs:692-703). */
+hk_status hk_tensor_matmul(hk_context* ctx, const hk_tensor* a, const hk_tensor* b, hk_tensor* out);
+/* Gradients of hk_tensor_matmul: dA = dY B^T and dB = A^T dY, each summed (FP32, in batch order)
+ * over the batch dims its operand broadcasts along, in A's and B's dtype and shape. The rule is the
+ * autodiff of float_matmul (src/backend.rs:692-703) in the reference's tensor library. */
+hk_status hk_tensor_matmul_backward(hk_context* ctx, const hk_tensor* a, const hk_tensor* b, const hk_tensor* dy,
+                                    hk_tensor* da, hk_tensor* db);
+
 /* ------------------------------------------------ GEMM device programs (code object) */
 
 /* The reference's launch ABI for its 18 BF16 GEMM device programs

@@ -25,6 +25,11 @@ a wrong sign or index, or a transposed operand fails at least one check:
   rust-ascend-driver/examples/deepgemm_validate.rs:30-56, which are exact or
   near-exact in f64; the linear-gradient finite-difference identity of
   tools/ascend/tests/test_adapter.py:89-93.
+* ``matmul_shape``/``tensor_matmul_f64``/``tensor_matmul_backward_f64``: the reference's own
+  shape cases (generic_matrix.rs:59-101, tensor/tests.rs:56-69 for rank >= 2: broadcast
+  [2,1,3,5] @ [1,4,5,7] -> [2,4,3,7], empty and zero-K outputs, contraction, broadcast and rank
+  errors), numpy's float64 matmul (an independent implementation of the same broadcasting) and
+  torch float64 autograd of torch.matmul for the gradients, on broadcast cases of rank 2 to 6.
 * ``rms_norm_f64``/``rms_norm_backward_f64``: torch float64 autograd of
   x*rsqrt(mean(x^2)+eps)*w (the independent reference of
   tools/ascend/tests/test_row_reference.py:65-78); the weight-contribution known
@@ -258,6 +263,66 @@ def gemm_f64_sampled(a, b, ta: bool, tb: bool, rows, cols) -> np.ndarray:
     out = np.empty(rows.shape[0], dtype=np.float64)
     lib().or_gemm_f64_sampled(a.reshape(-1), b.reshape(-1), m, n, k, int(ta), int(tb), rows, cols, rows.shape[0], out)
     return out
+
+
+def matmul_shape(a_shape, b_shape):
+    """Output shape of the generic floating matmul: generic_matrix::output_layout
+    (rust-ascend-driver/src/tensor/runtime/generic_matrix.rs:4-15) over layout::matmul_shape and
+    layout::broadcast (tensor/layout.rs:106-142): rank 2..6 each, A [..., M, K] @ B [..., K, N],
+    batch dims broadcast from the right. Raises ValueError with the reference's reason."""
+    a_shape, b_shape = tuple(int(d) for d in a_shape), tuple(int(d) for d in b_shape)
+    if not (2 <= len(a_shape) <= 6 and 2 <= len(b_shape) <= 6):
+        raise ValueError("generic matmul requires matching floating dtypes and rank 2..6")
+    if a_shape[-1] != b_shape[-2]:
+        raise ValueError("matmul contraction dimensions differ")
+    ba, bb = a_shape[:-2], b_shape[:-2]
+    rank = max(len(ba), len(bb))
+    out = []
+    for i in range(rank):  # from the right
+        x = ba[len(ba) - 1 - i] if i < len(ba) else 1
+        y = bb[len(bb) - 1 - i] if i < len(bb) else 1
+        if x == y or y == 1:
+            out.append(x)
+        elif x == 1:
+            out.append(y)
+        else:
+            raise ValueError("incompatible broadcast dimensions")
+    return tuple(reversed(out)) + (a_shape[-2], b_shape[-1])
+
+
+def _batch_index(batch, shape):
+    """Index of the operand batch that output batch multi-index `batch` reads (broadcast dims -> 0)."""
+    shape = tuple(shape)
+    lead = len(batch) - len(shape)
+    return tuple(0 if shape[d] == 1 else batch[lead + d] for d in range(len(shape)))
+
+
+def tensor_matmul_f64(a, b) -> np.ndarray:
+    """A @ B in float64 over the operands' exact values (F32, F16 or BF16-valued), batch dims
+    broadcast per matmul_shape; each batch's product is the C restatement of the GEMM sum
+    (or_gemm_f64). The KEEP_DTYPE rounding of the output is the caller's."""
+    a, b = np.asarray(a), np.asarray(b)
+    out_shape = matmul_shape(a.shape, b.shape)
+    out = np.empty(out_shape, dtype=np.float64)
+    for batch in np.ndindex(*out_shape[:-2]):
+        ia, ib = _batch_index(batch, a.shape[:-2]), _batch_index(batch, b.shape[:-2])
+        out[batch] = gemm_f64(a[ia].astype(np.float32), b[ib].astype(np.float32), False, False)
+    return out
+
+
+def tensor_matmul_backward_f64(a, b, dy):
+    """(dA, dB) of A @ B in float64: dY B^T and A^T dY, each summed over the output batches that
+    broadcast onto the operand's batch (the autodiff of matmul)."""
+    a, b, dy = np.asarray(a), np.asarray(b), np.asarray(dy)
+    out_shape = matmul_shape(a.shape, b.shape)
+    da = np.zeros(a.shape, dtype=np.float64)
+    db = np.zeros(b.shape, dtype=np.float64)
+    for batch in np.ndindex(*out_shape[:-2]):
+        ia, ib = _batch_index(batch, a.shape[:-2]), _batch_index(batch, b.shape[:-2])
+        g = dy[batch].astype(np.float32)
+        da[ia] += gemm_f64(g, b[ib].astype(np.float32), False, True)
+        db[ib] += gemm_f64(a[ia].astype(np.float32), g, True, False)
+    return da, db
 
 
 # ------------------------------------------------------------------ RMSNorm

@@ -1004,6 +1004,125 @@ hk_status hk_group_ends_data(hk_context* h, const hk_group_ends* ends, const int
     return HK_OK;
 }
 
+// ------------------------------------------------------------------ generic floating matmul
+
+namespace {
+
+// Reference: generic_matrix::output_layout (runtime/generic_matrix.rs:4-15) over
+// layout::matmul_shape and layout::broadcast (tensor/layout.rs:106-142): matching F32/F16/BF16,
+// rank 2..6 each, A [..., M, K] and B [..., K, N], batch dims broadcast from the right.
+hk_status matmul_spec(const hk_tensor* a, const hk_tensor* b, hk::MatmulSpec* s, hk_tensor* out_layout) {
+    if (!tensor_ok(a, "A") || !tensor_ok(b, "B")) return HK_INVALID_ARGUMENT;
+    if (b->dtype != a->dtype || !(a->rank >= 2 && a->rank <= 6) || !(b->rank >= 2 && b->rank <= 6))
+        return fail(HK_INVALID_ARGUMENT, "generic matmul requires matching floating dtypes and rank 2..6");
+    const int64_t m = a->shape[a->rank - 2], k = a->shape[a->rank - 1];
+    const int64_t kb = b->shape[b->rank - 2], n = b->shape[b->rank - 1];
+    if (k != kb) return fail(HK_INVALID_ARGUMENT, "matmul contraction dimensions differ");
+    const int ra = a->rank - 2, rb = b->rank - 2, rank = ra > rb ? ra : rb;
+    int64_t shape[4], sa[4], sb[4];
+    int64_t stride_a = m * k, stride_b = k * n;  // elements per batch step of the innermost batch dim
+    for (int i = 0; i < rank; ++i) {  // i-th batch dim from the right
+        const int64_t x = i < ra ? a->shape[ra - 1 - i] : 1;
+        const int64_t y = i < rb ? b->shape[rb - 1 - i] : 1;
+        int64_t d;
+        if (x == y || y == 1) d = x;
+        else if (x == 1) d = y;
+        else return fail(HK_INVALID_ARGUMENT, "incompatible broadcast dimensions");
+        shape[rank - 1 - i] = d;
+        sa[rank - 1 - i] = x == 1 ? 0 : stride_a;
+        sb[rank - 1 - i] = y == 1 ? 0 : stride_b;
+        stride_a *= x;
+        stride_b *= y;
+    }
+    int64_t count = 1;
+    for (int i = 0; i < rank; ++i) {
+        if (shape[i] != 0 && count > INT64_MAX / 8 / shape[i])
+            return fail(HK_INVALID_ARGUMENT, "matmul output is too large");
+        count *= shape[i];
+    }
+    if (s) {
+        s->dtype = a->dtype;
+        s->m = m;
+        s->n = n;
+        s->k = k;
+        for (hk::MatmulBatch* mb : {&s->batch, &s->a_batch, &s->b_batch}) {
+            mb->dims = rank;
+            mb->count = count;
+            for (int i = 0; i < rank; ++i) mb->shape[i] = shape[i];
+        }
+        for (int i = 0; i < rank; ++i) {
+            s->a_batch.stride[i] = sa[i];
+            s->b_batch.stride[i] = sb[i];
+        }
+    }
+    if (out_layout) {
+        out_layout->dtype = a->dtype;
+        out_layout->rank = rank + 2;
+        for (int i = 0; i < rank; ++i) out_layout->shape[i] = shape[i];
+        out_layout->shape[rank] = m;
+        out_layout->shape[rank + 1] = n;
+    }
+    return HK_OK;
+}
+
+}  // namespace
+
+hk_status hk_matmul_layout(const hk_tensor* a, const hk_tensor* b, hk_tensor* out) {
+    // Reference: generic_matrix::output_layout, runtime/generic_matrix.rs:4-15 (host-only).
+    if (!out) return fail(HK_INVALID_ARGUMENT, "null output layout");
+    hk_tensor layout{};
+    hk_status st = matmul_spec(a, b, nullptr, &layout);
+    if (st != HK_OK) return st;
+    out->dtype = layout.dtype;
+    out->rank = layout.rank;
+    for (int i = 0; i < HK_MAX_RANK; ++i) out->shape[i] = i < layout.rank ? layout.shape[i] : 0;
+    return HK_OK;
+}
+
+hk_status hk_tensor_matmul(hk_context* h, const hk_tensor* a, const hk_tensor* b, hk_tensor* out) {
+    // Reference: AscendRuntime::tensor_matmul (runtime/mod.rs:156-158) -> generic_matrix::matmul
+    // (generic_matrix.rs:17-54) -> AscendState::tensor_matmul (worker.rs:128-162): KEEP_DTYPE.
+    hk::MatmulSpec s;
+    hk_tensor want{};
+    hk_status st = matmul_spec(a, b, &s, &want);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(out, "out")) return HK_INVALID_ARGUMENT;
+    if (out->dtype != want.dtype || !same_shape(out, &want))
+        return fail(HK_INVALID_ARGUMENT, "floating matmul resource/layout contract mismatch (output %s %s, want %s %s)",
+                    dtype_name(out->dtype), shape_str(out).c_str(), dtype_name(want.dtype), shape_str(&want).c_str());
+    if (!disjoint({out}, {a, b})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (numel(out) == 0) return HK_OK;
+    if ((st = ensure_workspace(g.c, hk::matmul_workspace_bytes(s))) != HK_OK) return st;
+    hipError_t e = hk::matmul(s, a->data, b->data, out->data, g.c->workspace, g.c->num_cus, g.c->stream);
+    return complete(g.c, e, "tensor_matmul", 5);
+}
+
+hk_status hk_tensor_matmul_backward(hk_context* h, const hk_tensor* a, const hk_tensor* b, const hk_tensor* dy,
+                                    hk_tensor* da, hk_tensor* db) {
+    // The gradients of out = A @ B: dA = dY B^T and dB = A^T dY, each summed over the batch dims its
+    // operand broadcasts along (the autodiff rule the reference's float_matmul takes from its
+    // tensor library, src/backend.rs:692-703).
+    hk::MatmulSpec s;
+    hk_tensor want{};
+    hk_status st = matmul_spec(a, b, &s, &want);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(dy, "dY") || !tensor_ok(da, "dA") || !tensor_ok(db, "dB")) return HK_INVALID_ARGUMENT;
+    if (dy->dtype != want.dtype || !same_shape(dy, &want))
+        return fail(HK_INVALID_ARGUMENT, "matmul backward: dY must be %s %s", dtype_name(want.dtype), shape_str(&want).c_str());
+    if (da->dtype != a->dtype || !same_shape(da, a) || db->dtype != b->dtype || !same_shape(db, b))
+        return fail(HK_INVALID_ARGUMENT, "matmul backward: dA and dB must match A and B");
+    if (!disjoint({da, db}, {a, b, dy})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (numel(da) == 0 && numel(db) == 0) return HK_OK;
+    if ((st = ensure_workspace(g.c, hk::matmul_backward_workspace_bytes(s))) != HK_OK) return st;
+    hipError_t e = hk::matmul_backward(s, a->data, b->data, dy->data, da->data, db->data, g.c->workspace,
+                                       g.c->num_cus, g.c->stream);
+    return complete(g.c, e, "tensor_matmul_backward", 8);
+}
+
 hk_status hk_linear_nt_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
                                 hk_tensor* dx, hk_tensor* dw) {
     // Reference: matrix.rs:60-74.

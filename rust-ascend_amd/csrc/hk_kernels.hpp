@@ -36,6 +36,27 @@ hipError_t cast_apply(int to_bf16, const void* in, void* out, int64_t n, hipStre
 // reference (0 = row-major [M,K] / [K,N]; 1 = [K,M] / [N,K]). Operands that are not
 // K-contiguous are first transposed into `workspace` (gemm_workspace_bytes).
 size_t gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k, int ta, int tb);
+
+// Generic floating matmul (hk_matmul.hip). MatmulBatch: the output's batch dims (innermost last,
+// at most 4) and one operand's element stride along each (0 where the operand broadcasts).
+struct MatmulBatch {
+    int dims = 0;
+    int64_t count = 1;  // product of shape
+    int64_t shape[4] = {1, 1, 1, 1};
+    int64_t stride[4] = {0, 0, 0, 0};
+};
+struct MatmulSpec {
+    int dtype = 0;  // element type code of A, B and the output (F32 0, F16 1, BF16 27)
+    int64_t m = 0, n = 0, k = 0;
+    MatmulBatch batch, a_batch, b_batch;  // output batch shape; A's and B's strides over it
+};
+size_t matmul_workspace_bytes(const MatmulSpec& s);
+hipError_t matmul(const MatmulSpec& s, const void* a, const void* b, void* out, void* workspace, int num_cus,
+                  hipStream_t st);
+size_t matmul_backward_workspace_bytes(const MatmulSpec& s);
+// dA = dY B^T summed over A's broadcast batches, dB = A^T dY summed over B's, each in the dtype.
+hipError_t matmul_backward(const MatmulSpec& s, const void* a, const void* b, const void* dy, void* da, void* db,
+                           void* workspace, int num_cus, hipStream_t st);
 hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_t batch, int64_t m,
                      int64_t n, int64_t k, int ta, int tb, void* workspace, int num_cus, hipStream_t s);
 // M-grouped NT GEMM: C[i, :] = A[i, :] W[g(i)]^T with A [m, k], W [groups, n, k], C [m, n];

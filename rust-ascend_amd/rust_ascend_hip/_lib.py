@@ -92,6 +92,9 @@ SIGNATURES = {
     "hk_group_ends_upload": [_CTX, ctypes.POINTER(_i32), _i32, ctypes.POINTER(ctypes.c_void_p)],
     "hk_group_ends_free": [_CTX, ctypes.c_void_p],
     "hk_group_ends_data": [_CTX, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)],
+    "hk_matmul_layout": [_T, _T, _T],
+    "hk_tensor_matmul": [_CTX, _T, _T, _T],
+    "hk_tensor_matmul_backward": [_CTX, _T, _T, _T, _T, _T],
     "hk_module_load_data": [_CTX, ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)],
     "hk_module_get_function": [_CTX, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)],
     "hk_launch_kernel_with_args": [_CTX, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_void_p)],

@@ -57,6 +57,26 @@ def matmul_bf16_fp32(a, b, ta=Transpose.No, tb=Transpose.No) -> torch.Tensor:
     return _MatmulBf16Fp32.apply(a, b, Transpose(ta), Transpose(tb))
 
 
+class _FloatMatmul(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b):
+        a, b = a.contiguous(), b.contiguous()
+        ctx.save_for_backward(a, b)
+        return HipRuntime.tensor_matmul(a, b)
+
+    @staticmethod
+    def backward(ctx, dy):
+        a, b = ctx.saved_tensors
+        return HipRuntime.tensor_matmul_backward(a, b, dy.contiguous().to(a.dtype))
+
+
+def float_matmul(a, b) -> torch.Tensor:
+    """A @ B in the inputs' own dtype (F32, F16, BF16), batch dims broadcast; the backend op
+    RudaAscend::float_matmul (src/backend.rs:692-703) with its autodiff (dY B^T, A^T dY, summed
+    over broadcast batch dims)."""
+    return _FloatMatmul.apply(a, b)
+
+
 class _MatmulPaddedBf16Fp32(torch.autograd.Function):
     @staticmethod
     def forward(ctx, a, b, ta, tb):

@@ -131,6 +131,17 @@ def check_group_ends(ends) -> None:
     check(_lib.load().hk_group_ends_check(arr, count))
 
 
+def matmul_layout(a_shape, b_shape, dtype=torch.float32):
+    """Host-only output shape of the generic matmul (generic_matrix::output_layout,
+    runtime/generic_matrix.rs:4-15): matching floating dtypes, rank 2..6, broadcast batch dims."""
+    lib = _lib.load()
+    ta_ = tensor_desc(256, _DTYPES[dtype], a_shape)
+    tb_ = tensor_desc(256, _DTYPES[dtype], b_shape)
+    out = _lib.HkTensor()
+    check(lib.hk_matmul_layout(ctypes.byref(ta_), ctypes.byref(tb_), ctypes.byref(out)))
+    return tuple(int(out.shape[i]) for i in range(out.rank))
+
+
 class DeviceGroupEnds:
     """Checked group ends uploaded once (DeepGemm::upload_group_ends / DeviceGroupEnds,
     deepgemm/mod.rs:61-67); immutable, reused by every grouped call, freed on close()."""
@@ -222,6 +233,32 @@ class HipRuntime:
     def grouped_nt_into(a, weights, groups: DeviceGroupEnds, out) -> None:
         """Reference: DeepGemm::grouped_nt_into (mod.rs:74-78)."""
         _call("hk_gemm_grouped_nt_into", desc(a), desc(weights), groups.handle, desc(out))
+
+    @staticmethod
+    def tensor_matmul(a, b):
+        """A @ B in the inputs' dtype (F32, F16 or BF16), batch dims broadcast, any M/N/K.
+        Reference: AscendRuntime::tensor_matmul (mod.rs:156-158), behind RudaAscend::float_matmul
+        (src/backend.rs:692-703)."""
+        if a.dtype != b.dtype:
+            raise HkError(_lib.INVALID_ARGUMENT, "generic matmul requires matching floating dtypes and rank 2..6")
+        out = _empty(matmul_layout(a.shape, b.shape, a.dtype), a.dtype, a)
+        _call("hk_tensor_matmul", desc(a), desc(b), desc(out))
+        return out
+
+    @staticmethod
+    def matmul_fp32(a, b):
+        """Reference: AscendRuntime::matmul_fp32 (mod.rs:150-155): tensor_matmul on F32 inputs only."""
+        if a.dtype != torch.float32 or b.dtype != torch.float32:
+            raise HkError(_lib.INVALID_ARGUMENT, "matmul_fp32 requires FP32 inputs")
+        return HipRuntime.tensor_matmul(a, b)
+
+    @staticmethod
+    def tensor_matmul_backward(a, b, grad):
+        """[dA, dB] of A @ B: dY B^T and A^T dY, summed over each operand's broadcast batch dims."""
+        da = _empty(a.shape, a.dtype, a)
+        db = _empty(b.shape, b.dtype, a)
+        _call("hk_tensor_matmul_backward", desc(a), desc(b), desc(grad), desc(da), desc(db))
+        return da, db
 
     @staticmethod
     def linear_nt_backward(x, w, dy):
