@@ -52,6 +52,7 @@ typedef enum hk_dtype {
     HK_F16 = 1,
     HK_I32 = 3,   /* embedding IDs only */
     HK_I64 = 9,   /* embedding IDs only */
+    HK_BOOL = 12, /* one byte, nonzero = true: module attention masks only */
     HK_BF16 = 27,
 } hk_dtype;
 
@@ -180,6 +181,28 @@ hk_status hk_tensor_matmul(hk_context* ctx, const hk_tensor* a, const hk_tensor*
  * autodiff of float_matmul (src/backend.rs:692-703) in the reference's tensor library. */
 hk_status hk_tensor_matmul_backward(hk_context* ctx, const hk_tensor* a, const hk_tensor* b, const hk_tensor* dy,
                                     hk_tensor* da, hk_tensor* db);
+
+/* ------------------------------------------------ module attention (the backend's fallback) */
+
+/* RudaAscend's ModuleOps::attention (src/backend.rs:1323-1333) composes the backend's own ops
+ * (ruda_tensor's attention_fallback): scores = Q (K^T) * scale, softcap, + bias, -inf where masked,
+ * softmax over the keys, then P V. With hk_tensor_matmul and hk_softmax these are the remaining
+ * pieces; rust_ascend_hip.nn.module_attention is the composition.
+ *
+ * y = x with its last two dims swapped, materialized (float_swap_dims + contiguous,
+ * src/backend.rs:133-140,641): F32, F16 or BF16, rank >= 2. */
+hk_status hk_swap_last_dims(hk_context* ctx, const hk_tensor* x, hk_tensor* y);
+/* out = masked ? -inf : softcap(s * scale) + bias over F32 scores s [B, H, Sq, Sk]; softcap(x) =
+ * c tanh(x / c) when softcap = c > 0 (0: none); bias (nullable) F32 and mask (nullable, HK_BOOL,
+ * nonzero = masked) rank 4 with each dim equal to the scores' or 1 (broadcast); causal masks the keys
+ * k > q (the top-left-aligned rule of a lower-triangular mask). */
+hk_status hk_attention_scores(hk_context* ctx, const hk_tensor* s, float scale, float softcap, const hk_tensor* bias,
+                              const hk_tensor* mask, int32_t causal, hk_tensor* out);
+/* ds = d out / d s (zero where masked) and, when dbias is given (shaped like the bias), the bias
+ * gradient summed over its broadcast dims in a fixed order. */
+hk_status hk_attention_scores_backward(hk_context* ctx, const hk_tensor* s, const hk_tensor* dout, float scale,
+                                       float softcap, const hk_tensor* mask, int32_t causal, hk_tensor* ds,
+                                       hk_tensor* dbias);
 
 /* ------------------------------------------------ GEMM device programs (code object) */
 

@@ -30,6 +30,12 @@ a wrong sign or index, or a transposed operand fails at least one check:
   [2,1,3,5] @ [1,4,5,7] -> [2,4,3,7], empty and zero-K outputs, contraction, broadcast and rank
   errors), numpy's float64 matmul (an independent implementation of the same broadcasting) and
   torch float64 autograd of torch.matmul for the gradients, on broadcast cases of rank 2 to 6.
+* ``module_attention_f64``: parity unpinned against the RUDA library itself (not vendored); its
+  formula is checked against torch float64 ``scaled_dot_product_attention`` with the bias and the
+  boolean mask folded into a float mask (an independent implementation) and torch float64
+  autograd of the explicit composition (softcap included), the orthogonal-Q/K closed form of
+  examples/attention_tensor.rs:22-66 (uniform probabilities) and the causal running means of
+  examples/causal_attention_tensor.rs:31-55.
 * ``rms_norm_f64``/``rms_norm_backward_f64``: torch float64 autograd of
   x*rsqrt(mean(x^2)+eps)*w (the independent reference of
   tools/ascend/tests/test_row_reference.py:65-78); the weight-contribution known
@@ -323,6 +329,48 @@ def tensor_matmul_backward_f64(a, b, dy):
         da[ia] += gemm_f64(g, b[ib].astype(np.float32), False, True)
         db[ib] += gemm_f64(a[ia].astype(np.float32), g, True, False)
     return da, db
+
+
+def module_attention_f64(q, k, v, dy=None, mask=None, bias=None, scale=None, softcap=None, causal=False):
+    """The backend's module attention in float64 (ModuleOps::attention, src/backend.rs:1323-1333,
+    via the RUDA tensor library's attention_fallback, git rev 126b1c78 -- not vendored; the step
+    order is that library's published composition): x = scale * Q K^T (scale defaults to
+    1/sqrt(D)); t = c tanh(x / c) with a softcap c, else x; z = t + bias; z = -inf where causal
+    (key > query) or mask (True); P = softmax(z) over the keys; O = P V. Q [B,H,Sq,D], K [B,H,Sk,D],
+    V [B,H,Sk,Dv]; mask and bias broadcast onto [B,H,Sq,Sk]. With dy, the gradients dq, dk, dv and
+    dbias (summed to the bias shape) from the chain rule through those steps."""
+    q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    scale = 1.0 / np.sqrt(d) if scale is None else float(scale)
+    x = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
+    t = softcap * np.tanh(x / softcap) if softcap else x
+    z = t + (0.0 if bias is None else np.broadcast_to(np.asarray(bias, dtype=np.float64), x.shape))
+    masked = np.zeros(x.shape, dtype=bool)
+    if causal:
+        masked |= np.arange(sk)[None, :] > np.arange(sq)[:, None]
+    if mask is not None:
+        masked |= np.broadcast_to(np.asarray(mask, dtype=bool), x.shape)
+    z = np.where(masked, -np.inf, z)
+    zmax = z.max(axis=-1, keepdims=True)
+    e = np.exp(z - zmax)
+    p = e / e.sum(axis=-1, keepdims=True)
+    out = {"out": np.einsum("bhqk,bhkd->bhqd", p, v)}
+    if dy is not None:
+        dy = np.asarray(dy, dtype=np.float64)
+        out["dv"] = np.einsum("bhqk,bhqd->bhkd", p, dy)
+        dp = np.einsum("bhqd,bhkd->bhqk", dy, v)
+        dz = p * (dp - (dp * p).sum(axis=-1, keepdims=True))
+        dz = np.where(masked, 0.0, dz)
+        if bias is not None:
+            bshape = np.asarray(bias).shape
+            axes = tuple(i for i in range(4) if bshape[i] == 1 and x.shape[i] != 1)
+            out["dbias"] = dz.sum(axis=axes, keepdims=True) if axes else dz.copy()
+        dx = dz * (1.0 - np.tanh(x / softcap) ** 2) if softcap else dz
+        dx = dx * scale
+        out["dq"] = np.einsum("bhqk,bhkd->bhqd", dx, k)
+        out["dk"] = np.einsum("bhqk,bhqd->bhkd", dx, q)
+    return out
 
 
 # ------------------------------------------------------------------ RMSNorm

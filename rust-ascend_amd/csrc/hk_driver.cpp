@@ -75,6 +75,7 @@ int64_t dtype_size(int32_t dt) {
         case HK_F32:
         case HK_I32: return 4;
         case HK_I64: return 8;
+        case HK_BOOL: return 1;
         case HK_F16:
         case HK_BF16: return 2;
         default: return 0;
@@ -90,6 +91,7 @@ const char* dtype_name(int32_t dt) {
         case HK_BF16: return "BF16";
         case HK_I32: return "I32";
         case HK_I64: return "I64";
+        case HK_BOOL: return "BOOL";
         default: return "?";
     }
 }
@@ -1121,6 +1123,123 @@ hk_status hk_tensor_matmul_backward(hk_context* h, const hk_tensor* a, const hk_
     hipError_t e = hk::matmul_backward(s, a->data, b->data, dy->data, da->data, db->data, g.c->workspace,
                                        g.c->num_cus, g.c->stream);
     return complete(g.c, e, "tensor_matmul_backward", 8);
+}
+
+// ------------------------------------------------------------------ module attention pieces
+
+hk_status hk_swap_last_dims(hk_context* h, const hk_tensor* x, hk_tensor* y) {
+    // Reference: float_swap_dims(x, rank-2, rank-1) then contiguous() (src/backend.rs:133-140,641).
+    if (!tensor_ok(x, "x") || !tensor_ok(y, "y")) return HK_INVALID_ARGUMENT;
+    if (x->rank < 2 || y->rank != x->rank || y->dtype != x->dtype)
+        return fail(HK_INVALID_ARGUMENT, "swap_last_dims requires rank >= 2 and an output of the same dtype and rank");
+    for (int i = 0; i < x->rank - 2; ++i)
+        if (y->shape[i] != x->shape[i]) return fail(HK_INVALID_ARGUMENT, "swap_last_dims output shape mismatch");
+    const int64_t R = x->shape[x->rank - 2], C = x->shape[x->rank - 1];
+    if (y->shape[x->rank - 2] != C || y->shape[x->rank - 1] != R)
+        return fail(HK_INVALID_ARGUMENT, "swap_last_dims output shape mismatch");
+    if (!disjoint({y}, {x})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    const int64_t n = numel(x);
+    if (n == 0) return HK_OK;
+    hipError_t e = hk::swap_last_dims(static_cast<int>(dtype_size(x->dtype)), x->data, y->data, n / (R * C), R, C,
+                                      g.c->stream);
+    return complete(g.c, e, "swap_last_dims", 1);
+}
+
+namespace {
+
+// F32 rank-4 scores with an optional F32 bias and HK_BOOL mask broadcast onto them.
+hk_status scores_spec(const hk_tensor* s, float scale, float softcap, const hk_tensor* bias, const hk_tensor* mask,
+                      int32_t causal, hk::AttnScoreSpec* sp) {
+    if (!tensor_ok(s, "scores")) return HK_INVALID_ARGUMENT;
+    if (s->dtype != HK_F32 || s->rank != 4)
+        return fail(HK_INVALID_ARGUMENT, "attention scores must be F32 [B, H, Sq, Sk], got %s %s", dtype_name(s->dtype),
+                    shape_str(s).c_str());
+    if (!std::isfinite(scale) || !std::isfinite(softcap) || softcap < 0.0f)
+        return fail(HK_INVALID_ARGUMENT, "scale must be finite and softcap finite and >= 0 (0 = none)");
+    if (causal != 0 && causal != 1) return fail(HK_INVALID_ARGUMENT, "causal must be 0 or 1");
+    auto strides = [&](const hk_tensor* t, const char* what, int64_t (&st)[4]) {
+        int64_t run = 1;
+        for (int k = 3; k >= 0; --k) {
+            if (t->shape[k] != s->shape[k] && t->shape[k] != 1) {
+                fail(HK_INVALID_ARGUMENT, "attention %s %s does not broadcast onto the scores %s", what,
+                     shape_str(t).c_str(), shape_str(s).c_str());
+                return false;
+            }
+            st[k] = t->shape[k] == 1 ? 0 : run;
+            run *= t->shape[k];
+        }
+        return true;
+    };
+    for (int k = 0; k < 4; ++k) sp->shape[k] = s->shape[k];
+    if (bias) {
+        if (!tensor_ok(bias, "bias")) return HK_INVALID_ARGUMENT;
+        if (bias->dtype != HK_F32 || bias->rank != 4) return fail(HK_INVALID_ARGUMENT, "attention bias must be F32 rank 4");
+        if (!strides(bias, "bias", sp->bias_stride)) return HK_INVALID_ARGUMENT;
+    }
+    if (mask) {
+        if (mask->dtype != HK_BOOL || mask->rank != 4 || numel(mask) < 0 ||
+            (numel(mask) > 0 && mask->data == nullptr))
+            return fail(HK_INVALID_ARGUMENT, "attention mask must be a BOOL rank-4 tensor");
+        if (!strides(mask, "mask", sp->mask_stride)) return HK_INVALID_ARGUMENT;
+    }
+    sp->scale = scale;
+    sp->softcap = softcap;
+    sp->causal = causal;
+    return HK_OK;
+}
+
+}  // namespace
+
+hk_status hk_attention_scores(hk_context* h, const hk_tensor* s, float scale, float softcap, const hk_tensor* bias,
+                              const hk_tensor* mask, int32_t causal, hk_tensor* out) {
+    hk::AttnScoreSpec sp;
+    hk_status st = scores_spec(s, scale, softcap, bias, mask, causal, &sp);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(out, "out")) return HK_INVALID_ARGUMENT;
+    if (out->dtype != HK_F32 || !same_shape(out, s)) return fail(HK_INVALID_ARGUMENT, "scores output must match the scores");
+    if (!disjoint({out}, {s}) || (bias && !disjoint({out}, {bias})) || (mask && !disjoint({out}, {mask})))
+        return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::attention_scores(sp, static_cast<const float*>(s->data), static_cast<float*>(out->data),
+                                        bias ? static_cast<const float*>(bias->data) : nullptr,
+                                        mask ? static_cast<const uint8_t*>(mask->data) : nullptr, g.c->stream);
+    return complete(g.c, e, "attention_scores", 1);
+}
+
+hk_status hk_attention_scores_backward(hk_context* h, const hk_tensor* s, const hk_tensor* dout, float scale,
+                                       float softcap, const hk_tensor* mask, int32_t causal, hk_tensor* ds,
+                                       hk_tensor* dbias) {
+    hk::AttnScoreSpec sp;
+    hk_status st = scores_spec(s, scale, softcap, nullptr, mask, causal, &sp);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(dout, "dout") || !tensor_ok(ds, "ds")) return HK_INVALID_ARGUMENT;
+    if (dout->dtype != HK_F32 || !same_shape(dout, s) || ds->dtype != HK_F32 || !same_shape(ds, s))
+        return fail(HK_INVALID_ARGUMENT, "dout and ds must be F32 shaped like the scores");
+    int64_t bias_shape[4] = {1, 1, 1, 1};
+    if (dbias) {
+        if (!tensor_ok(dbias, "dbias")) return HK_INVALID_ARGUMENT;
+        if (dbias->dtype != HK_F32 || dbias->rank != 4) return fail(HK_INVALID_ARGUMENT, "dbias must be F32 rank 4");
+        for (int k = 0; k < 4; ++k) {
+            if (dbias->shape[k] != s->shape[k] && dbias->shape[k] != 1)
+                return fail(HK_INVALID_ARGUMENT, "dbias %s does not broadcast onto the scores %s", shape_str(dbias).c_str(),
+                            shape_str(s).c_str());
+            bias_shape[k] = dbias->shape[k];
+        }
+    }
+    if (!disjoint({ds}, {s, dout}) || (dbias && !disjoint({ds, dbias}, {s, dout})) ||
+        (mask && !disjoint({ds}, {mask})) || (mask && dbias && !disjoint({dbias}, {mask})))
+        return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if (dbias && (st = ensure_workspace(g.c, static_cast<size_t>(numel(s)) * sizeof(float))) != HK_OK) return st;
+    hipError_t e = hk::attention_scores_backward(
+        sp, static_cast<const float*>(s->data), static_cast<const float*>(dout->data), static_cast<float*>(ds->data),
+        mask ? static_cast<const uint8_t*>(mask->data) : nullptr, dbias ? static_cast<float*>(dbias->data) : nullptr,
+        bias_shape, static_cast<float*>(g.c->workspace), g.c->stream);
+    return complete(g.c, e, "attention_scores_backward", dbias ? 2 : 1);
 }
 
 hk_status hk_linear_nt_backward(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,

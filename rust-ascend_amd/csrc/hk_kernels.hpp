@@ -53,6 +53,24 @@ struct MatmulSpec {
 size_t matmul_workspace_bytes(const MatmulSpec& s);
 hipError_t matmul(const MatmulSpec& s, const void* a, const void* b, void* out, void* workspace, int num_cus,
                   hipStream_t st);
+// Module attention's score transform (hk_attention_module.hip) over F32 scores [B, H, Sq, Sk]:
+// masked ? -inf : softcap(s * scale) + bias; masked = (causal and key > query) or mask != 0.
+struct AttnScoreSpec {
+    int64_t shape[4] = {0, 0, 0, 0};
+    int64_t bias_stride[4] = {0, 0, 0, 0};  // element strides (0 along a broadcast dim)
+    int64_t mask_stride[4] = {0, 0, 0, 0};
+    float scale = 1.0f;
+    float softcap = 0.0f;  // 0: none
+    int causal = 0;
+};
+hipError_t attention_scores(const AttnScoreSpec& sp, const float* s, float* out, const float* bias,
+                            const uint8_t* mask, hipStream_t st);
+// ds and, when dbias is given, the bias gradient summed to bias_shape (4 dims; needs a workspace of
+// B*H*Sq*Sk floats).
+hipError_t attention_scores_backward(const AttnScoreSpec& sp, const float* s, const float* dout, float* ds,
+                                     const uint8_t* mask, float* dbias, const int64_t* bias_shape, float* workspace,
+                                     hipStream_t st);
+hipError_t swap_last_dims(int elem_bytes, const void* x, void* y, int64_t G, int64_t R, int64_t C, hipStream_t st);
 size_t matmul_backward_workspace_bytes(const MatmulSpec& s);
 // dA = dY B^T summed over A's broadcast batches, dB = A^T dY summed over B's, each in the dtype.
 hipError_t matmul_backward(const MatmulSpec& s, const void* a, const void* b, const void* dy, void* da, void* db,

@@ -25,6 +25,7 @@ STATUS_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", HIP_ERROR: "HIP_
 # Element type codes (reference DType codes, rust-ascend-driver/src/tensor/layout.rs:5-17).
 F32, F16, BF16 = 0, 1, 27
 I32, I64 = 3, 9
+BOOL = 12
 NO_PADDING = (1 << 64) - 1  # HK_NO_PADDING
 MAX_RANK = 8
 
@@ -95,6 +96,9 @@ SIGNATURES = {
     "hk_matmul_layout": [_T, _T, _T],
     "hk_tensor_matmul": [_CTX, _T, _T, _T],
     "hk_tensor_matmul_backward": [_CTX, _T, _T, _T, _T, _T],
+    "hk_swap_last_dims": [_CTX, _T, _T],
+    "hk_attention_scores": [_CTX, _T, _f32, _f32, _T, _T, _i32, _T],
+    "hk_attention_scores_backward": [_CTX, _T, _T, _f32, _f32, _T, _i32, _T, _T],
     "hk_module_load_data": [_CTX, ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)],
     "hk_module_get_function": [_CTX, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)],
     "hk_launch_kernel_with_args": [_CTX, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_void_p)],

@@ -15,6 +15,8 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
+from ._lib import HkError
 from .runtime import HipRuntime, LossReduction, RotaryLayout, Transpose
 
 
@@ -75,6 +77,53 @@ def float_matmul(a, b) -> torch.Tensor:
     RudaAscend::float_matmul (src/backend.rs:692-703) with its autodiff (dY B^T, A^T dY, summed
     over broadcast batch dims)."""
     return _FloatMatmul.apply(a, b)
+
+
+class _SwapLast(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return HipRuntime.swap_last_dims(x.contiguous())
+
+    @staticmethod
+    def backward(ctx, dy):
+        return HipRuntime.swap_last_dims(dy.contiguous())
+
+
+class _AttentionScores(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, s, bias, mask, scale, softcap, causal):
+        s = s.contiguous()
+        bias = None if bias is None else bias.contiguous()
+        mask = None if mask is None else mask.contiguous()
+        ctx.save_for_backward(s, mask)
+        ctx.args = (scale, softcap, causal, None if bias is None else tuple(bias.shape))
+        return HipRuntime.attention_scores(s, scale, softcap, bias, mask, causal)
+
+    @staticmethod
+    def backward(ctx, dout):
+        s, mask = ctx.saved_tensors
+        scale, softcap, causal, bias_shape = ctx.args
+        need_bias = bias_shape is not None and ctx.needs_input_grad[1]
+        ds, dbias = HipRuntime.attention_scores_backward(s, dout.contiguous().float(), scale, softcap, mask, causal,
+                                                         bias_shape if need_bias else None)
+        return ds, dbias, None, None, None, None
+
+
+def module_attention(query, key, value, mask=None, attn_bias=None, scale=None, softcap=None, is_causal=False):
+    """RudaAscend's ModuleOps::attention (src/backend.rs:1323-1333): the tensor library's fallback
+    composed from the backend's own ops, here libhk.so's -- scores = Q swap(K) * scale (scale
+    defaults to 1/sqrt(head width)), softcap c tanh(s/c), + attn_bias, -inf where is_causal (key >
+    query) or mask (True = masked) excludes a key, softmax over the keys, then P V. Q [B, H, Sq, D],
+    K [B, H, Sk, D], V [B, H, Sk, Dv], F32; mask (bool) and attn_bias (F32) [B, H, Sq, Sk] or
+    broadcast along dims of size 1. Gradients flow to Q, K, V and the bias."""
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.dtype != torch.float32 or t.dim() != 4:
+            raise HkError(_lib.INVALID_ARGUMENT, f"module attention takes F32 rank-4 tensors ({name})")
+    if scale is None:
+        scale = 1.0 / float(query.shape[-1]) ** 0.5
+    scores = float_matmul(query, _SwapLast.apply(key))
+    scores = _AttentionScores.apply(scores, attn_bias, mask, float(scale), float(softcap or 0.0), bool(is_causal))
+    return float_matmul(softmax(scores), value)
 
 
 class _MatmulPaddedBf16Fp32(torch.autograd.Function):

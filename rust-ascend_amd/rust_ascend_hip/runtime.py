@@ -16,7 +16,7 @@ import threading
 import torch
 
 from . import _lib
-from ._lib import BF16, F16, F32, I32, I64, NO_PADDING, HkError, check, tensor_desc
+from ._lib import BF16, BOOL, F16, F32, I32, I64, NO_PADDING, HkError, check, tensor_desc
 
 
 class Transpose(enum.IntEnum):
@@ -43,7 +43,8 @@ class RotaryLayout(enum.IntEnum):
     SplitHalf = 1
 
 
-_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32, torch.int64: I64}
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32, torch.int64: I64,
+           torch.bool: BOOL}
 _TORCH = {v: k for k, v in _DTYPES.items()}
 
 _ctx = None
@@ -259,6 +260,33 @@ class HipRuntime:
         db = _empty(b.shape, b.dtype, a)
         _call("hk_tensor_matmul_backward", desc(a), desc(b), desc(grad), desc(da), desc(db))
         return da, db
+
+    @staticmethod
+    def swap_last_dims(x):
+        """x with its last two dims swapped, materialized (float_swap_dims + contiguous,
+        src/backend.rs:133-140,641)."""
+        y = _empty(tuple(x.shape[:-2]) + (x.shape[-1], x.shape[-2]), x.dtype, x)
+        _call("hk_swap_last_dims", desc(x), desc(y))
+        return y
+
+    @staticmethod
+    def attention_scores(s, scale, softcap=0.0, bias=None, mask=None, causal=False):
+        """masked ? -inf : softcap(s * scale) + bias over F32 scores [B, H, Sq, Sk] (module attention's
+        score step, the fallback composition behind ModuleOps::attention, src/backend.rs:1323-1333)."""
+        out = _empty(s.shape, torch.float32, s)
+        _call("hk_attention_scores", desc(s), float(scale), float(softcap or 0.0),
+              None if bias is None else desc(bias), None if mask is None else desc(mask), int(bool(causal)), desc(out))
+        return out
+
+    @staticmethod
+    def attention_scores_backward(s, grad, scale, softcap=0.0, mask=None, causal=False, bias_shape=None):
+        """[dS, dBias or None]: the score step's gradient (zero where masked) and, for a bias of
+        bias_shape, its gradient summed over the broadcast dims."""
+        ds = _empty(s.shape, torch.float32, s)
+        dbias = None if bias_shape is None else _empty(bias_shape, torch.float32, s)
+        _call("hk_attention_scores_backward", desc(s), desc(grad), float(scale), float(softcap or 0.0),
+              None if mask is None else desc(mask), int(bool(causal)), desc(ds), None if dbias is None else desc(dbias))
+        return ds, dbias
 
     @staticmethod
     def linear_nt_backward(x, w, dy):

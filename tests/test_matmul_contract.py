@@ -74,3 +74,68 @@ def test_oracle_gradient_catches_a_dropped_broadcast_sum(oracle):
     da, _ = oracle.tensor_matmul_backward_f64(a, b, dy)
     wrong = dy[0].astype(np.float64) @ b[0].astype(np.float64).T
     assert np.abs(da[0] - wrong).max() > 1e-2
+
+
+# ------------------------------------------------------------------ module attention oracle
+
+def _torch_module_attention(q, k, v, mask, bias, scale, softcap, causal):
+    """Explicit torch float64 composition (independent of the oracle's numpy code)."""
+    s = torch.matmul(q, k.transpose(-1, -2)) * scale
+    if softcap:
+        s = softcap * torch.tanh(s / softcap)
+    if bias is not None:
+        s = s + bias
+    if causal:
+        s = s.masked_fill(torch.ones(s.shape[-2:], dtype=torch.bool).triu(1), float("-inf"))
+    if mask is not None:
+        s = s.masked_fill(mask, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v)
+
+
+@pytest.mark.parametrize("softcap,causal,with_bias,with_mask", [(None, False, True, True), (None, True, False, False),
+                                                                (5.0, False, True, False), (2.0, True, True, True)])
+def test_module_attention_oracle(oracle, softcap, causal, with_bias, with_mask):
+    rng = np.random.default_rng(11)
+    B, H, Sq, Sk, D, Dv = 2, 3, 5, 7, 4, 6
+    q, k = rng.standard_normal((B, H, Sq, D)), rng.standard_normal((B, H, Sk, D))
+    v, dy = rng.standard_normal((B, H, Sk, Dv)), rng.standard_normal((B, H, Sq, Dv))
+    bias = rng.standard_normal((1, H, Sq, Sk)) if with_bias else None
+    mask = (rng.random((B, 1, Sq, Sk)) < 0.3) if with_mask else None
+    if mask is not None:
+        mask[..., 0] = False  # every query keeps a key
+    ref = oracle.module_attention_f64(q, k, v, dy, mask=mask, bias=bias, scale=0.4, softcap=softcap, causal=causal)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    tb = None if bias is None else torch.tensor(bias, requires_grad=True)
+    tm = None if mask is None else torch.tensor(mask)
+    o = _torch_module_attention(tq, tk, tv, tm, tb, 0.4, softcap, causal)
+    o.backward(torch.tensor(dy))
+    np.testing.assert_allclose(ref["out"], o.detach().numpy(), rtol=1e-10, atol=1e-12)
+    for name, t in (("dq", tq), ("dk", tk), ("dv", tv)) + ((("dbias", tb),) if tb is not None else ()):
+        np.testing.assert_allclose(ref[name], t.grad.numpy(), rtol=1e-9, atol=1e-11, err_msg=name)
+    if not softcap:  # torch's own SDPA with the bias and mask folded into one float mask
+        fm = torch.zeros((B, H, Sq, Sk), dtype=torch.float64)
+        if bias is not None:
+            fm = fm + torch.tensor(bias)
+        if causal:
+            fm = fm.masked_fill(torch.ones(Sq, Sk, dtype=torch.bool).triu(1), float("-inf"))
+        if mask is not None:
+            fm = fm.masked_fill(torch.tensor(mask), float("-inf"))
+        sd = torch.nn.functional.scaled_dot_product_attention(torch.tensor(q), torch.tensor(k), torch.tensor(v),
+                                                              attn_mask=fm, scale=0.4)
+        np.testing.assert_allclose(ref["out"], sd.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_module_attention_closed_forms(oracle):
+    """Orthogonal Q/K: uniform probabilities, so O is the mean of V (attention_tensor.rs:22-66);
+    Q = K = 0 causal: O row i is the running mean of V[0..i] (causal_attention_tensor.rs:31-55)."""
+    rng = np.random.default_rng(2)
+    q = np.zeros((1, 1, 4, 8))
+    q[0, 0, :, 0] = 1.0
+    k = np.zeros((1, 1, 6, 8))
+    k[0, 0, :, 1] = 1.0
+    v = rng.standard_normal((1, 1, 6, 3))
+    out = oracle.module_attention_f64(q, k, v)["out"]
+    np.testing.assert_allclose(out[0, 0], np.broadcast_to(v[0, 0].mean(axis=0), (4, 3)), atol=1e-14)
+    out = oracle.module_attention_f64(np.zeros((1, 1, 6, 8)), np.zeros((1, 1, 6, 8)), v, causal=True)["out"]
+    want = np.cumsum(v[0, 0], axis=0) / np.arange(1, 7)[:, None]
+    np.testing.assert_allclose(out[0, 0], want, atol=1e-14)
