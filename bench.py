@@ -188,7 +188,6 @@ def bench_c2(steps, warmup):
     w = (1 + 0.1 * torch.randn((C2_WIDTH,), generator=g, device="cuda")).float()
     y, rstd = HipRuntime.rms_norm(x, w, 1e-6)
     dx, dw = HipRuntime.rms_norm_backward(x, w, dy, rstd)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     # The step calls the C ABI directly with caller-owned outputs and descriptors built once, as
     # a native caller of hk_rms_norm / hk_rms_norm_backward would: the per-call Python
     # allocation and descriptor building of the HipRuntime mirror would otherwise leave the
@@ -199,24 +198,34 @@ def bench_c2(steps, warmup):
     d_y, d_rstd, d_dx, d_dw = runtime.desc(y), runtime.desc(rstd), runtime.desc(dx), runtime.desc(dw)
     eps = ctypes.c_double(1e-6)
 
-    def step(e=None):
-        if e: e[0].record()
+    def fwd():
         check(lib.hk_rms_norm(ctx, d_x, d_w, eps, d_y, d_rstd))
-        if e: e[1].record()
+
+    def bwd():
         check(lib.hk_rms_norm_backward(ctx, d_x, d_w, d_dy, d_rstd, d_dx, d_dw))
-        if e: e[2].record()
 
     for _ in range(warmup):
-        step()
+        fwd()
+        bwd()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        step(ev[i])
+    for _ in range(steps):
+        fwd()
+        bwd()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    fwd_ms = event_ms([(e[0], e[1]) for e in ev])
-    bwd_ms = event_ms([(e[1], e[2]) for e in ev])
-    return wall_ms, fwd_ms, bwd_ms
+    # The per-op split comes from separate loops of one op each, bracketed by two events: an event
+    # recorded between the two ops of every step costs the GPU several microseconds of its own.
+    split = []
+    for op in (fwd, bwd):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            op()
+        e1.record()
+        torch.cuda.synchronize()
+        split.append(e0.elapsed_time(e1) / steps)
+    return wall_ms, split[0], split[1]
 
 
 def cpu_baseline_c2(threads):
@@ -469,15 +478,9 @@ def bench_rope(iters=10):
     c = torch.from_numpy(np.cos(ang).astype(np.float32)).cuda()[None, None]
     s = torch.from_numpy(np.sin(ang).astype(np.float32)).cuda()[None, None]
     q = torch.randn((4, 32, 4096, 128), device="cuda").to(torch.bfloat16)
-    warm(lambda: HipRuntime.rotary_prefix(q, c, s, 128, RotaryLayout.SplitHalf))
-    pairs = []
-    for _ in range(iters):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        HipRuntime.rotary_prefix(q, c, s, 128, RotaryLayout.SplitHalf)
-        e1.record()
-        pairs.append((e0, e1))
-    ms = event_ms(pairs)
+    # back-to-back calls between one pair of events (an event between every two calls costs the
+    # GPU time of its own)
+    ms = time_gpu(lambda: HipRuntime.rotary_prefix(q, c, s, 128, RotaryLayout.SplitHalf), iters)
     algo = 2 * q.numel() * 2 + 2 * c.numel() * 4
     return ms, algo
 
@@ -747,8 +750,7 @@ def main():
     if args.copy_calibration:
         copy_calibration()
     if not args.no_cpu:
-        threads = int(os.environ.get("OMP_NUM_THREADS", min(16, os.cpu_count() or 1)))
-        line["cpu_baseline"] = cpu_baseline_c2(threads)
+        line["cpu_baseline"] = cpu_baseline_c2(cpu_threads())
     print(json.dumps(line), flush=True)
 
 

@@ -316,6 +316,7 @@ hipError_t product(int dtype, int64_t G, const Gather& x, const Gather& y, const
                                    reinterpret_cast<const _Float16*>(xg), reinterpret_cast<const _Float16*>(yg),
                                    reinterpret_cast<_Float16*>(cg), tiles_n, p.M, p.N, p.K);
         } else {
+            // NT operands need no transposition, so the GEMM takes no workspace
             hipError_t e = gemm_bf16(xg, yg, cg, out_f32 ? 0 : 1, gc, p.M, p.N, p.K, 0, 1, nullptr, num_cus, st);
             if (e != hipSuccess) return e;
         }

@@ -18,7 +18,7 @@
 // grid-stride loop over rows, so w is read once per wave, not once per row. Row sums
 // are butterfly reductions across the wave (no LDS, no barriers). The backward writes
 // one FP32 dw partial per workgroup (waves combined through LDS in wave order) and a
-// second kernel sums the partials in workgroup order: deterministic, no atomics.
+// second kernel sums the partials in a fixed order: deterministic, no atomics.
 //
 // General path (any positive W): the same math with one element per lane-step and the
 // row re-read from cache for the second pass; dw comes from a column-parallel kernel.
@@ -233,27 +233,48 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
     for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = p_lds[c];
 }
 
-// dw[c] = sum over p of partial[p][c]: a workgroup covers 64 columns with 16 slices of
-// partial rows (p = slice, slice+16, ... ascending), and the 16 slice sums are then added in
-// slice order: a fixed order for given (parts, width). Sums are kept in double, so this stage
-// adds no rounding beyond the final conversion to F32.
-__global__ void __launch_bounds__(1024)
+// dw[c] = sum over p of partial[p][c]. A workgroup covers 16 columns: thread t takes the four
+// columns 4 (t % 4) .. +3 of its slice of partial rows, p = t/4, t/4 + 64, ... (one row each for 64
+// partials, four for C2's 256), so every load of the kernel is issued at once; the 64 slice sums
+// of each column are then combined in LDS by a fixed pairwise tree. The order is fixed for given
+// (parts, width) and the sums are kept in double, so this stage adds no rounding beyond the final
+// conversion to F32. On C2 (256 partials x 4096) it takes 4.2 us, as the former 64-column
+// workgroups did while leaving 3/4 of the CUs idle: the time is mostly the launch itself.
+constexpr int kSumSlices = 64;
+__global__ void __launch_bounds__(256)
 sum_partials(const float* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
-    __shared__ double red[16][64];
-    const int col = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int slice = threadIdx.x >> 6;
-    double s = 0.0;
-    if (col < width) {
-#pragma unroll 8
-        for (int p = slice; p < parts; p += 16) s += static_cast<double>(partial[static_cast<int64_t>(p) * width + col]);
-    }
-    red[slice][threadIdx.x & 63] = s;
-    __syncthreads();
-    if (slice == 0 && col < width) {
-        double t = red[0][threadIdx.x];
+    __shared__ double red[kSumSlices][16];
+    const int quad = threadIdx.x & 3, slice = threadIdx.x >> 2;
+    const int groups = (width + 15) / 16;
+    for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {  // uniform per workgroup
+        const int col0 = grp * 16 + quad * 4;
+        double s[4] = {0.0, 0.0, 0.0, 0.0};
+        if (col0 + 3 < width && (width & 3) == 0) {
+            for (int p = slice; p < parts; p += kSumSlices) {
+                const f32x4_t v = *reinterpret_cast<const f32x4_t*>(partial + static_cast<int64_t>(p) * width + col0);
 #pragma unroll
-        for (int i = 1; i < 16; ++i) t += red[i][threadIdx.x];
-        dw[col] = static_cast<float>(t);
+                for (int e = 0; e < 4; ++e) s[e] += static_cast<double>(v[e]);
+            }
+        } else {
+            for (int p = slice; p < parts; p += kSumSlices)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col0 + e < width) s[e] += static_cast<double>(partial[static_cast<int64_t>(p) * width + col0 + e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[slice][quad * 4 + e] = s[e];
+        __syncthreads();
+        for (int half = kSumSlices / 2; half >= 1; half >>= 1) {
+            if (slice < half)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[slice][quad * 4 + e] += red[slice + half][quad * 4 + e];
+            __syncthreads();
+        }
+        if (slice == 0)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col0 + e < width) dw[col0 + e] = static_cast<float>(red[0][quad * 4 + e]);
+        __syncthreads();  // red is rewritten by the next group
     }
 }
 
@@ -403,7 +424,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
         else if (chunks_per_lane <= 2) launch_bwd_fast<T, 2>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
         else if (chunks_per_lane <= 4) launch_bwd_fast<T, 4>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
         else launch_bwd_fast<T, 8>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        hipLaunchKernelGGL(sum_partials, dim3((width + 63) / 64), dim3(1024), 0, s, workspace, parts, (int)width, dw);
+        hipLaunchKernelGGL(sum_partials, dim3(flat_blocks((width + 15) / 16, 1)), dim3(256), 0, s, workspace, parts, (int)width, dw);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_bwd_dx_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
@@ -414,7 +435,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
         hipLaunchKernelGGL((rms_bwd_dw_general<T>), dim3((width + 255) / 256, parts), dim3(256), 0, s,
                            static_cast<const T*>(x), static_cast<const T*>(dy), rstd, workspace, rows,
                            width, per);
-        hipLaunchKernelGGL(sum_partials, dim3((width + 63) / 64), dim3(1024), 0, s, workspace, parts, (int)width, dw);
+        hipLaunchKernelGGL(sum_partials, dim3(flat_blocks((width + 15) / 16, 1)), dim3(256), 0, s, workspace, parts, (int)width, dw);
     }
     return hipGetLastError();
 }
