@@ -17,7 +17,7 @@
 // columns' w (and, in the backward, its dw partial sums) in registers across a
 // grid-stride loop over rows, so w is read once per wave, not once per row. Row sums
 // are butterfly reductions across the wave (no LDS, no barriers). The backward writes
-// one FP32 dw partial per workgroup (waves combined through LDS in wave order) and a
+// one FP64 dw partial per workgroup (waves combined through LDS in wave order) and a
 // second kernel sums the partials in a fixed order: deterministic, no atomics.
 //
 // General path (any positive W): the same math with one element per lane-step and the
@@ -135,11 +135,12 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
 template <typename T, int MAXJ, bool FULL>
 __global__ void __launch_bounds__(kBwdThreads)
 rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
-             const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ partial,
+             const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial,
              int64_t rows, int width) {
-    extern __shared__ float lds[];  // [width] weight, then [width] partial of the workgroup
-    float* w_lds = lds;
-    float* p_lds = lds + width;
+    // [width] F32 weight, then the workgroup's [width] FP64 partial (width % 8 == 0: aligned)
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+    float* w_lds = reinterpret_cast<float*>(lds_raw);
+    double* p_lds = reinterpret_cast<double*>(lds_raw + static_cast<size_t>(width) * sizeof(float));
     const int lane = threadIdx.x & 63;
     // wave-uniform, so row addresses and the rstd load are scalar
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -147,11 +148,17 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
     const int chunks = width >> 3;
     for (int c = threadIdx.x; c < width; c += blockDim.x) w_lds[c] = w[c];
     __syncthreads();
-    float acc[MAXJ][8];
+    // dγ sums in FP64: each term x * dy * rstd is formed exactly in the fused multiply-add (x * dy
+    // is exact in FP32 for BF16 storage, and exact in FP64 for F32), so the partial sums carry
+    // only FP64 rounding and the F32 result differs from the exact sum of the terms by the final
+    // conversion alone. (FP32 accumulation put C2's error at 0.8-1.6e-4 of |dγ| + 1e-3 rms(dγ),
+    // against 3.9e-5 now, the part due to rstd being F32; the FP64 sums cost ~3 us of the
+    // backward's 78-81 us there.)
+    double acc[MAXJ][8];
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+        for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
     const float inv_w = 1.0f / static_cast<float>(width);
     // rstd is loaded ahead of the row's loads, so waiting for the row covers it.
     auto load_row = [&](Raw8<T> (&xs)[MAXJ], Raw8<T> (&gs)[MAXJ], float& r, int64_t row) __attribute__((always_inline)) {
@@ -169,6 +176,7 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
     };
     auto process_row = [&](Raw8<T> (&xs)[MAXJ], Raw8<T> (&gs)[MAXJ], float r, int64_t row) __attribute__((always_inline)) {
         float dot = 0.0f;
+        const double rd = r;
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             const int c = lane + 64 * j;
@@ -180,7 +188,10 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     dot += (gv[e] * wv[e]) * xv[e];
-                    acc[j][e] += (xv[e] * r) * gv[e];
+                    if constexpr (sizeof(T) == 2)
+                        acc[j][e] = __builtin_fma(static_cast<double>(xv[e] * gv[e]), rd, acc[j][e]);
+                    else
+                        acc[j][e] = __builtin_fma(static_cast<double>(xv[e]) * gv[e], rd, acc[j][e]);
                 }
             }
         }
@@ -221,7 +232,7 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
                 if (FULL || c < chunks) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        float* p = &p_lds[8 * c + e];
+                        double* p = &p_lds[8 * c + e];
                         *p = (src == 0) ? acc[j][e] : (*p + acc[j][e]);
                     }
                 }
@@ -229,38 +240,30 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
         }
         __syncthreads();
     }
-    float* out = partial + static_cast<int64_t>(blockIdx.x) * width;
+    double* out = partial + static_cast<int64_t>(blockIdx.x) * width;
     for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = p_lds[c];
 }
 
-// dw[c] = sum over p of partial[p][c]. A workgroup covers 16 columns: thread t takes the four
-// columns 4 (t % 4) .. +3 of its slice of partial rows, p = t/4, t/4 + 64, ... (one row each for 64
-// partials, four for C2's 256), so every load of the kernel is issued at once; the 64 slice sums
-// of each column are then combined in LDS by a fixed pairwise tree. The order is fixed for given
-// (parts, width) and the sums are kept in double, so this stage adds no rounding beyond the final
-// conversion to F32. On C2 (256 partials x 4096) it takes 4.2 us, as the former 64-column
+// dw[c] = sum over p of the FP64 partial[p][c]. A workgroup covers 16 columns: thread t takes the
+// four columns 4 (t % 4) .. +3 of its slice of partial rows, p = t/4, t/4 + 64, ... (one row each
+// for 64 partials, four for C2's 256), so every load of the kernel is issued at once; the 64 slice
+// sums of each column are then combined in LDS by a fixed pairwise tree. The order is fixed for
+// given (parts, width) and the sums are kept in double, so this stage adds no rounding beyond the
+// final conversion to F32. On C2 (256 partials x 4096) it takes 4.2 us, as the former 64-column
 // workgroups did while leaving 3/4 of the CUs idle: the time is mostly the launch itself.
 constexpr int kSumSlices = 64;
 __global__ void __launch_bounds__(256)
-sum_partials(const float* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
+sum_partials(const double* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
     __shared__ double red[kSumSlices][16];
     const int quad = threadIdx.x & 3, slice = threadIdx.x >> 2;
     const int groups = (width + 15) / 16;
     for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {  // uniform per workgroup
         const int col0 = grp * 16 + quad * 4;
         double s[4] = {0.0, 0.0, 0.0, 0.0};
-        if (col0 + 3 < width && (width & 3) == 0) {
-            for (int p = slice; p < parts; p += kSumSlices) {
-                const f32x4_t v = *reinterpret_cast<const f32x4_t*>(partial + static_cast<int64_t>(p) * width + col0);
+        for (int p = slice; p < parts; p += kSumSlices)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) s[e] += static_cast<double>(v[e]);
-            }
-        } else {
-            for (int p = slice; p < parts; p += kSumSlices)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (col0 + e < width) s[e] += static_cast<double>(partial[static_cast<int64_t>(p) * width + col0 + e]);
-        }
+            for (int e = 0; e < 4; ++e)
+                if (col0 + e < width) s[e] += partial[static_cast<int64_t>(p) * width + col0 + e];
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[slice][quad * 4 + e] = s[e];
         __syncthreads();
@@ -324,19 +327,21 @@ rms_bwd_dx_general(const T* __restrict__ x, const float* __restrict__ w, const T
     }
 }
 
-// partial[chunk][c] = sum over the chunk's rows of (x*rstd)*dy, rows ascending.
+// partial[chunk][c] = sum over the chunk's rows of x*dy*rstd, rows ascending, in FP64 (each term
+// exact, as in the fast kernel).
 template <typename T>
 __global__ void __launch_bounds__(256)
 rms_bwd_dw_general(const T* __restrict__ x, const T* __restrict__ dy, const float* __restrict__ rstd,
-                   float* __restrict__ partial, int64_t rows, int64_t width, int64_t rows_per_chunk) {
+                   double* __restrict__ partial, int64_t rows, int64_t width, int64_t rows_per_chunk) {
     const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t chunk = blockIdx.y;
     if (col >= width) return;
     const int64_t r0 = chunk * rows_per_chunk;
     const int64_t r1 = (r0 + rows_per_chunk < rows) ? r0 + rows_per_chunk : rows;
-    float s = 0.0f;
+    double s = 0.0;
     for (int64_t r = r0; r < r1; ++r)
-        s += (Elem<T>::load(x, r * width + col) * rstd[r]) * Elem<T>::load(dy, r * width + col);
+        s = __builtin_fma(static_cast<double>(Elem<T>::load(x, r * width + col)) * Elem<T>::load(dy, r * width + col),
+                          static_cast<double>(rstd[r]), s);
     partial[chunk * width + col] = s;
 }
 
@@ -377,10 +382,10 @@ void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_
 
 template <typename T, int MAXJ>
 void launch_bwd_fast(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
-                     float* partial, int parts, int64_t rows, int width, hipStream_t s) {
+                     double* partial, int parts, int64_t rows, int width, hipStream_t s) {
     auto kernel = width == 512 * MAXJ ? rms_bwd_fast<T, MAXJ, true> : rms_bwd_fast<T, MAXJ, false>;
     hipLaunchKernelGGL(kernel, dim3(parts), dim3(kBwdThreads),
-                       2 * static_cast<size_t>(width) * sizeof(float), s, static_cast<const T*>(x), w,
+                       static_cast<size_t>(width) * (sizeof(float) + sizeof(double)), s, static_cast<const T*>(x), w,
                        static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
 }
 
@@ -412,7 +417,8 @@ hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, in
 
 template <typename T>
 hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
-                          float* dw, float* workspace, int64_t rows, int64_t width, hipStream_t s) {
+                          float* dw, void* ws, int64_t rows, int64_t width, hipStream_t s) {
+    double* workspace = static_cast<double*>(ws);  // the FP64 dγ partials
     if (rows == 0) {
         hipLaunchKernelGGL(fill_zero_f32, dim3(flat_blocks(width, 256)), dim3(256), 0, s, dw, width);
         return hipGetLastError();
@@ -444,7 +450,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
 
 size_t rms_backward_workspace_bytes(int64_t rows, int64_t width) {
     const int parts = std::max(parts_fast(rows), parts_general(rows));
-    return static_cast<size_t>(parts) * static_cast<size_t>(width) * sizeof(float);
+    return static_cast<size_t>(parts) * static_cast<size_t>(width) * sizeof(double);
 }
 
 hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void* y, float* rstd,

@@ -47,13 +47,11 @@ def rel_ok(actual, expected, tol, name="", atol_frac=1e-3):
     return e
 
 
-# FP32 weight gradients are sums over R rows of FP32 products; each product carries a
-# rounding error of ~2^-24 of its magnitude, so any FP32 implementation (the reference's
-# pairwise tree included) sits ~2^-24*sqrt(R)*rms(term) from the exact sum: 1.5e-5 at
-# R = 16384, rms(dw) = 128. The dW check therefore uses atol = 1e-2*rms(dw) in the rel err
-# (an absolute floor of 1e-6*rms(dw) at tol 1e-4), and the plain relative error on every
-# element with |dw| >= 1e-2*rms(dw).
-DW_ATOL_FRAC = 1e-2
+# FP32 weight gradients: the rel err's absolute term is 1e-3*rms(dw), the path's own definition
+# of the dγ tolerance (max |a-b| / (|b| + 1e-3 rms(b)) <= 1e-4). The kernels form each term
+# x*dy exactly (BF16 significands) and round it once, with rstd, in a fused multiply-add; with the
+# product rounded twice (x*rstd, then *dy) the C2 error was 1.04e-4 on this measure, 4.0e-5 now.
+DW_ATOL_FRAC = 1e-3
 
 
 def f32_close(actual, expected, name=""):

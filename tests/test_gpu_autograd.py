@@ -156,7 +156,7 @@ def test_rms_norm_autograd_bf16_input():
     assert y.dtype == torch.bfloat16 and x_t.grad.dtype == torch.bfloat16 and wt.grad.dtype == torch.float32
     rel_ok(host(y), y_ref, 1e-2, "Y")
     rel_ok(host(x_t.grad), dx_ref, 1e-2, "dX")
-    rel_ok(host(wt.grad), dw_ref, 1e-4, "dW", atol_frac=1e-2)
+    rel_ok(host(wt.grad), dw_ref, 1e-4, "dW", atol_frac=1e-3)
 
 
 @pytest.mark.parametrize("rows,width", [(1, 2), (3, 6), (2, 96)])

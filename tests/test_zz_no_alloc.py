@@ -50,11 +50,11 @@ def test_noalloc_backward_equals_the_allocating_one_on_two_calls():
         _, r_ref = oracle.rms_norm_f64(x, w, 1e-6)
         dx_ref, dw_ref = oracle.rms_norm_backward_f64(x, w, dy, r_ref)
         rel_ok(host(dx), dx_ref, 1e-2, "dX")
-        rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=1e-2)
+        rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=1e-3)
 
 
 def test_noalloc_backward_rejects_partials_beyond_its_scratch():
-    # width 8192 (the general path) with 32768 rows needs 512 x 8192 F32 partials = 16 MiB
+    # width 8192 (the general path) with 32768 rows needs 512 x 8192 FP64 partials = 32 MiB
     x_t = torch.zeros((32768, 8192), dtype=torch.bfloat16, device=DEV)
     w_t = torch.ones((8192,), dtype=torch.float32, device=DEV)
     rstd = torch.ones((32768,), dtype=torch.float32, device=DEV)
