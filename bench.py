@@ -214,8 +214,11 @@ def bench_c2(steps, warmup):
         bwd()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    # The per-op split comes from separate loops of one op each, bracketed by two events: an event
-    # recorded between the two ops of every step costs the GPU several microseconds of its own.
+    # The per-op split: each op alone, back to back, between one pair of events (its average
+    # launch duration, launch gaps included). An event recorded between the two ops of every step
+    # costs the GPU several microseconds of its own (~12 us per 123 us step), so the step loop above
+    # has none. In the step the backward runs a few microseconds faster than alone: the forward
+    # has just read x, and part of it is still in the on-package cache.
     split = []
     for op in (fwd, bwd):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
