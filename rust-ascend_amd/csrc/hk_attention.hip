@@ -28,6 +28,8 @@
 //   * online softmax in base 2 (scale*log2(e) folded into one multiply, v_exp_f32);
 //   * causal: tiles past the diagonal are never loaded, waves skip tiles that are fully masked
 //     for their 32 rows, and blocks are issued heaviest-first within each (batch, head).
+#include <type_traits>
+
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
 
@@ -1022,7 +1024,12 @@ attn_bwd_dkdv(BwdArgs a) {
         const uint16_t* Qt = tiles[cur][0];
         const uint16_t* Ot = tiles[cur][1];
         const bool skip = a.causal && (n0w > q0 + kQStep - 1 + a.diag);
-        if (!skip) {
+        // Steps whose 64 queries all see this wave's 32 keys (the common case) run a copy of the
+        // step without the mask arithmetic; the others test one 32-bit offset per element:
+        // query q0 + qq sees my_key iff qq + rel >= 0 (causal), qq < qlim and my_key < n.
+        const bool full = (!a.causal || q0 + a.diag >= n0w + 31) && q0 + kQStep <= a.m && n0w + 32 <= a.n;
+        auto step = [&](auto full_c) __attribute__((always_inline)) {
+            constexpr bool FULL = decltype(full_c)::value;
             // Query tile qt of S (even i) and dP (odd i): MFMA i = 2 ks + which. The P / dS
             // arithmetic of tile 0 runs between the MFMAs of tile 1, that of tile 1 between the
             // dV / dK MFMAs of k-slices 0-1 (which use only tile 0): one wave per SIMD, so the
@@ -1042,11 +1049,8 @@ attn_bwd_dkdv(BwdArgs a) {
                     else s[qt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, kf[ks], ks == 0 ? zero : s[qt], 0, 0, 0);
                 };
             };
-            // P and dS; lane holds key my_key, queries q0 + 32*qt + 8*(v/4) + 4*lg + v%4. Steps
-            // whose 64 queries all see this wave's 32 keys (the common case) skip the mask; the
-            // others test one 32-bit offset per element: query q0 + qq sees my_key iff
-            // qq + rel >= 0 (causal), qq < qlim and my_key < n.
-            const bool full = (!a.causal || q0 + a.diag >= n0w + 31) && q0 + kQStep <= a.m && n0w + 32 <= a.n;
+            // P and dS / scale (the scale is applied to dK once, at the end); lane holds key
+            // my_key, queries q0 + 32*qt + 8*(v/4) + 4*lg + v%4.
             int64_t rel64 = q0 + a.diag - my_key;
             rel64 = rel64 < -(int64_t{1} << 30) ? -(int64_t{1} << 30) : (rel64 > (int64_t{1} << 30) ? (int64_t{1} << 30) : rel64);
             const int rel = a.causal ? static_cast<int>(rel64) : (1 << 30);
@@ -1062,9 +1066,9 @@ attn_bwd_dkdv(BwdArgs a) {
                 }
                 const float l = l4[v & 3], d = d4[v & 3];
                 float p = fast_exp2(__builtin_fmaf(s[qt][v], a.scale_log2, -l));
-                if (!full) p = key_ok && qi < qlim && qi + rel >= 0 ? p : 0.0f;
+                if constexpr (!FULL) p = key_ok && qi < qlim && qi + rel >= 0 ? p : 0.0f;
                 s[qt][v] = p;
-                dp[qt][v] = a.scale * (p * (dp[qt][v] - d));
+                dp[qt][v] = p * (dp[qt][v] - d);
             };
             // dV^T += dO^T P ; dK^T += Q^T dS  (k = 64 queries in 4 steps of 16), k-slices
             // 2h, 2h+1: MFMA i = 2 (DT kk + dt) + which, which 0: dV, 1: dK
@@ -1103,11 +1107,19 @@ attn_bwd_dkdv(BwdArgs a) {
             sb[2] = pack_bf16x8(dp[1], 0);
             sb[3] = pack_bf16x8(dp[1], 8);
             mfma_ring<4 * DT>(dkv(1), dkv_mma(1));
+        };
+        if (!skip) {
+            if (full) step(std::integral_constant<bool, true>{});
+            else step(std::integral_constant<bool, false>{});
         }
         landed();
         lds_barrier();
     }
 
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dk[dt][v] *= a.scale;
     if (my_key < a.n) {
         const int64_t row = static_cast<int64_t>(bkv) * a.n + my_key;
 #pragma unroll
@@ -1202,60 +1214,86 @@ attn_bwd_dq(BwdArgs a) {
         const uint16_t* Kt = lds[cur][0];
         const uint16_t* Vt = lds[cur][1];
         const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
-        if (!skip) {
-            // S^T (even i) and dP^T (odd i) for key tiles tt, k slices ks: MFMA i = 4 ks + 2 tt + which
+        // Tiles whose 64 keys all lie at or below every query of this wave run a copy of the
+        // step without the mask arithmetic; the others compare one 32-bit offset per element
+        // (key offset <= rel, < klim).
+        const bool full = (!a.causal || kv0 + kBlockN - 1 <= q0w + a.diag) && q0w + 32 <= a.m &&
+                          kv0 + kBlockN <= a.n;
+        auto step = [&](auto full_c) __attribute__((always_inline)) {
+            constexpr bool FULL = decltype(full_c)::value;
+            // S^T (even i) and dP^T (odd i) of key tile tt: MFMA i = 2 ks + which. The P / dS
+            // arithmetic of key tile 0 runs between the MFMAs of key tile 1, that of key tile 1
+            // between the dQ MFMAs of k-slices 0-1 (which use only key tile 0): one wave per SIMD,
+            // so the exponentials would otherwise leave the matrix core idle.
             f32x16_t s[2], dp[2];
             const f32x16_t zero = {};
-            mfma_ring<4 * KS>(
-                [&](int i) {
-                    const int ks = i >> 2, tt = (i >> 1) & 1;
-                    return tile_read16<DP>((i & 1) ? Vt : Kt, 32 * tt + lq, 2 * ks + lg);
-                },
-                [&](int i, bf16x8_t x) {
-                    const int ks = i >> 2, tt = (i >> 1) & 1;
+            auto sdp = [&](int tt) {
+                return [&, tt](int i) { return tile_read16<DP>((i & 1) ? Vt : Kt, 32 * tt + lq, 2 * (i >> 1) + lg); };
+            };
+            auto sdp_mma = [&](int tt) {
+                return [&, tt](int i, bf16x8_t x) {
+                    const int ks = i >> 1;
                     if (i & 1) dp[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, of[ks], ks == 0 ? zero : dp[tt], 0, 0, 0);
                     else s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, qf[ks], ks == 0 ? zero : s[tt], 0, 0, 0);
-                });
-            // Lane holds query my_q, keys kv0 + 32*tt + 8*(v/4) + 4*lg + v%4. Tiles whose 64 keys
-            // all lie at or below every query of this wave skip the mask; the others compare one
-            // 32-bit offset per element (key offset <= rel, < klim).
-            const bool full = (!a.causal || kv0 + kBlockN - 1 <= q0w + a.diag) && q0w + 32 <= a.m &&
-                              kv0 + kBlockN <= a.n;
+                };
+            };
+            // Lane holds query my_q, keys kv0 + 32*tt + 8*(v/4) + 4*lg + v%4; dS / scale (the scale
+            // is applied to dQ once, at the end).
             int64_t rel64 = my_q + a.diag - kv0;
             rel64 = rel64 < -(int64_t{1} << 30) ? -(int64_t{1} << 30) : (rel64 > (int64_t{1} << 30) ? (int64_t{1} << 30) : rel64);
             const int rel = (a.causal ? static_cast<int>(rel64) : (1 << 30)) - 4 * lg;
             const int klim = static_cast<int>(a.n - kv0 < kBlockN ? a.n - kv0 : kBlockN) - 4 * lg;
             const bool q_ok = my_q < a.m;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    float p = fast_exp2(__builtin_fmaf(s[tt][v], a.scale_log2, -lse2));
-                    if (!full) {
-                        const int kk = 32 * tt + (v >> 2) * 8 + (v & 3);
-                        p = q_ok && kk <= rel && kk < klim ? p : 0.0f;
-                    }
-                    dp[tt][v] = a.scale * (p * (dp[tt][v] - rstat));
+            auto pds = [&](int tt, int v) __attribute__((always_inline)) {
+                float p = fast_exp2(__builtin_fmaf(s[tt][v], a.scale_log2, -lse2));
+                if constexpr (!FULL) {
+                    const int kk = 32 * tt + (v >> 2) * 8 + (v & 3);
+                    p = q_ok && kk <= rel && kk < klim ? p : 0.0f;
                 }
+                dp[tt][v] = p * (dp[tt][v] - rstat);
+            };
+            // dQ^T += K^T dS^T over k-slices 2h, 2h+1 (keys 32h .. 32h+31): MFMA i = DT kk + dt
             bf16x8_t sb[4];
+            auto dqf = [&](int h) {
+                return [&, h](int i) {
+                    const int kb0 = 16 * (2 * h + i / DT) + 4 * lg;
+                    return tile_read_tr<DP>(Kt, lane, kb0, kb0 + 8, 32 * (i % DT));
+                };
+            };
+            auto dq_mma = [&](int h) {
+                return [&, h](int i, bf16x8_t x) {
+                    const int dt = i % DT;
+                    dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[2 * h + i / DT], dq[dt], 0, 0, 0);
+                };
+            };
+            static_assert(16 % (2 * KS) == 0 && 16 % (2 * DT) == 0, "scores per MFMA");
+            mfma_ring<2 * KS>(sdp(0), sdp_mma(0));
+            mfma_ring_x<2 * KS>(sdp(1), sdp_mma(1), [&](int i) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) sb[ks] = pack_bf16x8(dp[ks >> 1], 8 * (ks & 1));
-            // dQ^T += K^T dS^T: MFMA i = DT ks + dt
-            mfma_ring<4 * DT>(
-                [&](int i) {
-                    const int ks = i / DT, dt = i % DT;
-                    const int kb0 = 16 * ks + 4 * lg;
-                    return tile_read_tr<DP>(Kt, lane, kb0, kb0 + 8, 32 * dt);
-                },
-                [&](int i, bf16x8_t x) {
-                    const int ks = i / DT, dt = i % DT;
-                    dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[ks], dq[dt], 0, 0, 0);
-                });
+                for (int v = i * 16 / (2 * KS); v < (i + 1) * 16 / (2 * KS); ++v) pds(0, v);
+            });
+            sb[0] = pack_bf16x8(dp[0], 0);
+            sb[1] = pack_bf16x8(dp[0], 8);
+            mfma_ring_x<2 * DT>(dqf(0), dq_mma(0), [&](int i) {
+#pragma unroll
+                for (int v = i * 16 / (2 * DT); v < (i + 1) * 16 / (2 * DT); ++v) pds(1, v);
+            });
+            sb[2] = pack_bf16x8(dp[1], 0);
+            sb[3] = pack_bf16x8(dp[1], 8);
+            mfma_ring<2 * DT>(dqf(1), dq_mma(1));
+        };
+        if (!skip) {
+            if (full) step(std::integral_constant<bool, true>{});
+            else step(std::integral_constant<bool, false>{});
         }
         landed();
         lds_barrier();
     }
 
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dq[dt][v] *= a.scale;
     if (my_q < a.m) {
         const int64_t row = static_cast<int64_t>(bh) * a.m + my_q;
 #pragma unroll
