@@ -169,10 +169,11 @@ def roofline(bound, algo, ms, kernel, key=None):
            "frac": round(achieved / peak, 4), "traffic": read_traffic(kernel), "kernel": kernel,
            "algorithmic_per_launch": algo, "avg_launch_ms": round(ms, 5)}
     counters = read_counters(key) if key else None
-    if counters:  # MFMA-bound workloads: measured traffic, utilisation and executed work (profiles/)
+    if counters:  # measured per-launch traffic; for MFMA-bound workloads utilisation and executed work
         out["traffic"] = counters["traffic"]
-        out["mfma_util"] = counters["mfma_util"]
-        out["executed_flops_per_launch"] = counters["executed_flops"]
+        if bound == "mfma":
+            out["mfma_util"] = counters["mfma_util"]
+            out["executed_flops_per_launch"] = counters["executed_flops"]
     return out
 
 
@@ -539,10 +540,10 @@ def bench_widened():
     g.manual_seed(11)
     out = []
 
-    def add(name, ms, bound, algo, kernel, unit):
+    def add(name, ms, bound, algo, kernel, unit, key):
         val = algo / ms / 1e9 if unit == "TFLOP/s" else algo / ms / 1e6
         out.append({"workload": name, "value": round(val, 2), "unit": unit, "ms": round(ms, 5),
-                    "roofline": roofline(bound, algo, ms, kernel)})
+                    "roofline": roofline(bound, algo, ms, kernel, key)})
 
     def guarded(name, fn):
         try:
@@ -558,7 +559,7 @@ def bench_widened():
         y = HipRuntime.grouped_nt(a, w, ends)
         ms = time_gpu(lambda: HipRuntime.grouped_nt_into(a, w, ends, y))
         add(f"(f) M-grouped NT GEMM (MoE): {E} experts x {rows} rows, K {K}, N {N}, BF16 out", ms, "mfma",
-            2 * E * rows * N * K, "gemm_nt_m16_kernel", "TFLOP/s")
+            2 * E * rows * N * K, "gemm_nt_m16_kernel", "TFLOP/s", "grouped")
     guarded("(f) M-grouped NT GEMM", grouped)
 
     def padded():
@@ -567,7 +568,7 @@ def bench_widened():
         b = torch.randn((K, N), generator=g, device="cuda")
         ms = time_gpu(lambda: HipRuntime.gemm_padded_bf16_fp32(a, b))
         add(f"(f) padded BF16-compute GEMM F32 [{M},{K}]x[{K},{N}] (pad + GEMM + crop)", ms, "mfma", 2 * M * N * K,
-            "pad_bf16+gemm+crop_f32", "TFLOP/s")
+            "pad_bf16+gemm+crop_f32", "TFLOP/s", "padded")
     guarded("(f) padded GEMM", padded)
 
     R, C = 8192, 32000
@@ -576,10 +577,11 @@ def bench_widened():
     def softmax():
         y = HipRuntime.softmax(x)
         ms = time_gpu(lambda: HipRuntime.softmax(x))
-        add(f"(f) softmax rows F32 [{R},{C}]", ms, "hbm", 2 * 4 * R * C, "softmax", "GB/s")
+        add(f"(f) softmax rows F32 [{R},{C}]", ms, "hbm", 2 * 4 * R * C, "softmax", "GB/s", "softmax")
         dy = torch.randn((R, C), generator=g, device="cuda")
         ms = time_gpu(lambda: HipRuntime.softmax_backward(y, dy))
-        add(f"(f) softmax backward rows F32 [{R},{C}]", ms, "hbm", 3 * 4 * R * C, "softmax_backward", "GB/s")
+        add(f"(f) softmax backward rows F32 [{R},{C}]", ms, "hbm", 3 * 4 * R * C, "softmax_backward", "GB/s",
+            "softmax_bwd")
     guarded("(f) softmax rows", softmax)
 
     def cross_entropy():
@@ -591,7 +593,7 @@ def bench_widened():
             return HipRuntime.nll_loss(lp, labels, wt, LossReduction.Mean)
         ms = time_gpu(ce)
         add(f"(f) cross entropy fwd F32 [{R},{C}] (log-softmax + NLLLoss mean, INT64 labels)", ms, "hbm",
-            2 * 4 * R * C + 8 * R + 4 * C, "softmax+nll_loss", "GB/s")
+            2 * 4 * R * C + 8 * R + 4 * C, "softmax+nll_loss", "GB/s", "cross_entropy")
     guarded("(f) cross entropy", cross_entropy)
 
     def swiglu():
@@ -599,10 +601,11 @@ def bench_widened():
         gate = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
         up = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_gpu(lambda: HipRuntime.silu_mul(gate, up))
-        add(f"(f) SwiGLU silu_mul BF16 [{T},{F}]", ms, "hbm", 3 * 2 * T * F, "silu_mul_kernel", "GB/s")
+        add(f"(f) SwiGLU silu_mul BF16 [{T},{F}]", ms, "hbm", 3 * 2 * T * F, "silu_mul_kernel", "GB/s", "silu_mul")
         gr = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_gpu(lambda: HipRuntime.silu_mul_backward(gate, up, gr))
-        add(f"(f) SwiGLU silu_mul backward BF16 [{T},{F}]", ms, "hbm", 5 * 2 * T * F, "silu_mul_bwd_kernel", "GB/s")
+        add(f"(f) SwiGLU silu_mul backward BF16 [{T},{F}]", ms, "hbm", 5 * 2 * T * F, "silu_mul_bwd_kernel", "GB/s",
+            "silu_mul_bwd")
     guarded("(f) SwiGLU", swiglu)
 
     def bias():
@@ -612,7 +615,7 @@ def bench_widened():
         bb = torch.randn((H,), generator=g, device="cuda")
         ms = time_gpu(lambda: HipRuntime.bias_add(xb, bb, res))
         add(f"(f) bias + residual add BF16 [{T},{H}], F32 bias", ms, "hbm", 3 * 2 * T * H + 4 * H, "bias_add_kernel",
-            "GB/s")
+            "GB/s", "bias_add")
     guarded("(f) bias add", bias)
 
     def embedding():
@@ -621,7 +624,7 @@ def bench_widened():
         ids = torch.randint(0, V, (T,), generator=g, device="cuda", dtype=torch.int64)
         ms = time_gpu(lambda: HipRuntime.embedding(table, ids))
         add(f"(f) embedding gather BF16 table [{V},{H}], {T} INT64 IDs", ms, "hbm", 2 * 2 * T * H + 8 * T,
-            "embedding_gather_kernel", "GB/s")
+            "embedding_gather_kernel", "GB/s", "embedding")
     guarded("(f) embedding", embedding)
     return out
 
@@ -694,6 +697,8 @@ def main():
     if args.only_widened:
         for entry in bench_widened():
             print(json.dumps(entry), flush=True)
+        if args.copy_calibration:
+            copy_calibration()
         return
 
     wall_ms, fwd_ms, bwd_ms = bench_c2(args.steps, args.warmup)
@@ -733,7 +738,7 @@ def main():
         ms, algo = bench_rope()
         sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
                     "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
-                    "roofline": roofline("hbm", algo, ms, "rope_pairs")})
+                    "roofline": roofline("hbm", algo, ms, "rope_pairs", "rope")})
         try:
             f_ms, b_ms, ff, bf = bench_attention()
             sec.append({"workload": "C4 causal GQA attention fwd B4 S4096 Hq32 Hkv8 D128", "value": round(ff / f_ms / 1e9, 2),
