@@ -18,7 +18,9 @@
 // grid-stride loop over rows, so w is read once per wave, not once per row. Row sums
 // are butterfly reductions across the wave (no LDS, no barriers). The backward writes
 // one FP64 dw partial per workgroup (waves combined through LDS in wave order) and a
-// second kernel sums the partials in a fixed order: deterministic, no atomics.
+// second kernel sums the partials in a fixed order: deterministic, no atomics. Widths 2048
+// and 4096 (C2's) take the split backward instead, where four waves share each row (one column
+// quarter each) so that four waves fit on every SIMD.
 //
 // General path (any positive W): the same math with one element per lane-step and the
 // row re-read from cache for the second pass; dw comes from a column-parallel kernel.
@@ -244,6 +246,164 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
     for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = p_lds[c];
 }
 
+// Backward for widths 2048 and 4096 (W = 2048 * CPL): 16-wave workgroups, one per CU, so four
+// waves share each SIMD. A row is split over four waves, one column quarter each (lane l of
+// quarter q owns the chunks 64 CPL q + l + 64 j, j < CPL), so each wave keeps only a quarter of
+// the dγ sums (16 CPL FP64 registers per lane) and a quarter row in flight; the four waves of a
+// row group walk their rows in a grid-stride loop. The row's dot product sum(dy*w*x) is the sum
+// of the four quarter dots, exchanged through LDS without a barrier: each wave posts its
+// quarter's dot, tagged with the row's sequence number, into one of two slots, and reads the
+// other three posts once their tags match. Every wave adds the four in quarter order, so all
+// four compute the same correction. A wave posts row k+2 into the slot of row k only after it
+// has read every post of row k+1, each made after its author had read row k's posts, so no post
+// is overwritten before it is read; all 16 waves of a workgroup are resident together, and every
+// wave posts before it waits, so every wait ends (the spin is also bounded).
+// C2 (16384 x 4096 BF16): 71-72 us against 74-76 us for rms_bwd_fast on the same box: a row per
+// wave needs the whole row's 64 FP64 sums per lane (~230 registers, one wave per SIMD), and
+// four waves per SIMD stream faster than one wave with two to four rows in flight.
+constexpr int kSplitThreads = 1024;
+constexpr int kSplitGroups = 4;  // row groups per workgroup (x 4 column quarters = 16 waves)
+constexpr int kSpinLimit = 1 << 24;
+
+template <typename T, int CPL>
+__global__ void __launch_bounds__(kSplitThreads)
+rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
+              const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial, int64_t rows) {
+    constexpr int W = 2048 * CPL;
+    constexpr int CQ = 64 * CPL;  // chunks per quarter
+    __shared__ __attribute__((aligned(16))) float w_lds[W];
+    __shared__ double p_lds[W];
+    __shared__ uint64_t post[kSplitGroups][2][4];
+    const int lane = threadIdx.x & 63;
+    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = v >> 2, q = v & 3;
+    if (threadIdx.x < kSplitGroups * 2 * 4) (&post[0][0][0])[threadIdx.x] = 0;
+    for (int c = threadIdx.x; c < W; c += kSplitThreads) w_lds[c] = w[c];
+    double acc[CPL][8];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
+    __syncthreads();
+    const float inv_w = 1.0f / static_cast<float>(W);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kSplitGroups;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kSplitGroups + g;
+    const int64_t n = first < rows ? (rows - 1 - first) / stride + 1 : 0;
+    for (int64_t k = 0; k < n; ++k) {
+        const int64_t row = first + k * stride;
+        const float r = rstd[row];
+        const T* xr = x + row * W;
+        const T* gr = dy + row * W;
+        Raw8<T> xs[CPL], gs[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = CQ * q + lane + 64 * j;
+            xs[j].load(xr + 8 * c);
+            gs[j].load(gr + 8 * c);
+        }
+        const double rd = r;
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = CQ * q + lane + 64 * j;
+            float xv[8], gv[8], wv[8];
+            xs[j].get(xv);
+            gs[j].get(gv);
+            load8(w_lds + 8 * c, wv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                dot += (gv[e] * wv[e]) * xv[e];
+                // x * dy is exact in FP32 for BF16 storage and in FP64 for F32: each term exact
+                if constexpr (sizeof(T) == 2)
+                    acc[j][e] = __builtin_fma(static_cast<double>(xv[e] * gv[e]), rd, acc[j][e]);
+                else
+                    acc[j][e] = __builtin_fma(static_cast<double>(xv[e]) * gv[e], rd, acc[j][e]);
+            }
+        }
+        dot = wave_sum(dot);
+        const uint32_t tag = static_cast<uint32_t>(k) + 1;
+        volatile uint64_t* slot = &post[g][k & 1][0];
+        if (lane == 0) slot[q] = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(dot);
+        float part[4];
+        for (int p = 0; p < 4; ++p) {
+            uint64_t val;
+            int spins = 0;
+            do {
+                val = slot[p];
+            } while (static_cast<uint32_t>(val >> 32) != tag && ++spins < kSpinLimit);
+            part[p] = __uint_as_float(static_cast<uint32_t>(val));
+        }
+        const float total = ((part[0] + part[1]) + part[2]) + part[3];
+        const float corr = (total * inv_w) * (r * r);
+        T* dr = dx + row * W;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = CQ * q + lane + 64 * j;
+            float xv[8], gv[8], wv[8], o[8];
+            xs[j].pin();
+            gs[j].pin();
+            xs[j].get(xv);
+            gs[j].get(gv);
+            load8(w_lds + 8 * c, wv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (gv[e] * wv[e] - xv[e] * corr) * r;
+            store8_stream(dr + 8 * c, o);
+        }
+    }
+    // The row groups' dγ sums combined in group order, then the workgroup's FP64 partial row.
+    for (int src = 0; src < kSplitGroups; ++src) {
+        if (g == src) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = CQ * q + lane + 64 * j;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    double* p = &p_lds[8 * c + e];
+                    *p = (src == 0) ? acc[j][e] : (*p + acc[j][e]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    double* out = partial + static_cast<int64_t>(blockIdx.x) * W;
+    for (int c = threadIdx.x; c < W; c += kSplitThreads) out[c] = p_lds[c];
+}
+
+// dw[c] = sum over p of the FP64 partial[p][c] for parts <= 256 and width % 8 == 0 (the fast and
+// split backward kernels): workgroup b covers columns 8b .. 8b+7; thread (slice, pair) loads the
+// 16-byte column pair of partial rows slice, slice + 64, slice + 128, slice + 192 at once and adds
+// them in that order, then the 64 slice sums are combined by a pairwise tree in LDS. The order is
+// sum_partials' (below) for these shapes, so the result is bit-identical to it; C2: 3.1-3.9 us
+// against 3.8-4.8 us.
+typedef double f64x2_t __attribute__((ext_vector_type(2)));
+__global__ void __launch_bounds__(256)
+sum_partials8(const double* __restrict__ partial, int parts, int width, float* __restrict__ dw) {
+    __shared__ f64x2_t red[64][4];
+    const int pr = threadIdx.x & 3, slice = threadIdx.x >> 2;
+    const int col0 = blockIdx.x * 8 + pr * 2;
+    f64x2_t a[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int p = slice + 64 * k;
+        a[k] = p < parts ? *reinterpret_cast<const f64x2_t*>(partial + static_cast<int64_t>(p) * width + col0)
+                         : f64x2_t{0.0, 0.0};
+    }
+    f64x2_t s = {0.0, 0.0};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (slice + 64 * k < parts) s += a[k];
+    red[slice][pr] = s;
+    __syncthreads();
+    for (int half = 32; half >= 1; half >>= 1) {
+        if (slice < half) red[slice][pr] += red[slice + half][pr];
+        __syncthreads();
+    }
+    if (slice == 0) {
+        dw[col0] = static_cast<float>(red[0][pr][0]);
+        dw[col0 + 1] = static_cast<float>(red[0][pr][1]);
+    }
+}
+
 // dw[c] = sum over p of the FP64 partial[p][c]. A workgroup covers 16 columns: thread t takes the
 // four columns 4 (t % 4) .. +3 of its slice of partial rows, p = t/4, t/4 + 64, ... (one row each
 // for 64 partials, four for C2's 256), so every load of the kernel is issued at once; the 64 slice
@@ -389,7 +549,8 @@ void launch_bwd_fast(const void* x, const float* w, const void* dy, const float*
                        static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
 }
 
-// One workgroup per CU is resident: a grid of exactly one round of workgroups.
+// One workgroup per CU is resident: a grid of exactly one round of workgroups (4 rows in flight
+// per workgroup in both the fast and the split kernel).
 int parts_fast(int64_t rows) { return grid_for_rows(rows, kBwdThreads / 64, 256); }
 int parts_general(int64_t rows) {
     int64_t parts = (rows + 63) / 64;  // at most 64 rows per column chunk
@@ -424,13 +585,20 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
         return hipGetLastError();
     }
     if (fast_rows(width, {x, w, dy, dx})) {
-        const int parts = parts_fast(rows);
-        const int chunks_per_lane = static_cast<int>((width / 8 + 63) / 64);
-        if (chunks_per_lane <= 1) launch_bwd_fast<T, 1>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        else if (chunks_per_lane <= 2) launch_bwd_fast<T, 2>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        else if (chunks_per_lane <= 4) launch_bwd_fast<T, 4>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        else launch_bwd_fast<T, 8>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        hipLaunchKernelGGL(sum_partials, dim3(flat_blocks((width + 15) / 16, 1)), dim3(256), 0, s, workspace, parts, (int)width, dw);
+        const int parts = parts_fast(rows);  // <= 256
+        if (width == 2048 || width == 4096) {
+            auto kernel = width == 4096 ? rms_bwd_split<T, 2> : rms_bwd_split<T, 1>;
+            hipLaunchKernelGGL(kernel, dim3(parts), dim3(kSplitThreads), 0, s, static_cast<const T*>(x), w,
+                               static_cast<const T*>(dy), rstd, static_cast<T*>(dx), workspace, rows);
+        } else {
+            const int chunks_per_lane = static_cast<int>((width / 8 + 63) / 64);
+            if (chunks_per_lane <= 1) launch_bwd_fast<T, 1>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+            else if (chunks_per_lane <= 2) launch_bwd_fast<T, 2>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+            else if (chunks_per_lane <= 4) launch_bwd_fast<T, 4>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+            else launch_bwd_fast<T, 8>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
+        }
+        hipLaunchKernelGGL(sum_partials8, dim3(static_cast<unsigned>(width / 8)), dim3(256), 0, s, workspace, parts,
+                           (int)width, dw);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_bwd_dx_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
