@@ -722,7 +722,7 @@ def main():
                    "fwd_ms": round(fwd_ms, 5), "bwd_ms": round(bwd_ms, 5),
                    "fwd_GBps": round(C2_FWD_BYTES / fwd_ms / 1e6, 1),
                    "bwd_GBps": round(C2_BWD_BYTES / bwd_ms / 1e6, 1)},
-        "roofline": roofline("hbm", C2_BWD_BYTES, bwd_ms, "rms_bwd_fast"),
+        "roofline": roofline("hbm", C2_BWD_BYTES, bwd_ms, "rms_bwd_split"),
     }
     if not args.no_secondary:
         sec = []

@@ -321,15 +321,19 @@ rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __r
             }
         }
         dot = wave_sum(dot);
+        // posts and polls are single 64-bit LDS accesses (tag and value together); atomic loads and
+        // stores keep the compiler from caching or reordering them
         const uint32_t tag = static_cast<uint32_t>(k) + 1;
-        volatile uint64_t* slot = &post[g][k & 1][0];
-        if (lane == 0) slot[q] = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(dot);
+        const int sl = static_cast<int>(k & 1);
+        if (lane == 0)
+            __hip_atomic_store(&post[g][sl][q], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(dot),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         float part[4];
         for (int p = 0; p < 4; ++p) {
             uint64_t val;
             int spins = 0;
             do {
-                val = slot[p];
+                val = __hip_atomic_load(&post[g][sl][p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             } while (static_cast<uint32_t>(val >> 32) != tag && ++spins < kSpinLimit);
             part[p] = __uint_as_float(static_cast<uint32_t>(val));
         }
