@@ -48,6 +48,36 @@ def test_rms_norm_bf16_vs_oracle(rows, width):
     rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=DW_ATOL_FRAC)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,width", [(1, 2048), (3, 4096), (5, 2048), (1023, 4096), (1025, 2048), (4099, 4096),
+                                        (2050, 2048)])
+def test_rms_norm_backward_split_path(dtype, rows, width):
+    """Widths 2048 and 4096 take the backward whose rows are split over four waves: row counts
+    that leave row groups idle, uneven grid-stride walks and many rows per group (both posting
+    slots reused), F32 and BF16 storage, against the float64 oracle; bit-identical on a rerun."""
+    seed = rows * 3 + width + (7 if dtype == "bf16" else 0)
+    if dtype == "bf16":
+        x_t, x = randn_bf16((rows, width), seed=seed)
+        dy_t, dy = randn_bf16((rows, width), seed=seed + 1)
+    else:
+        x = oracle.normal((rows, width), 0, seed).astype(np.float32)
+        dy = oracle.normal((rows, width), 0, seed + 1).astype(np.float32)
+        x_t, dy_t = dev_f32(x), dev_f32(dy)
+    w = (1 + oracle.normal((width,), 0, seed + 2, std=0.1)).astype(np.float32)
+    w_t = dev_f32(w)
+    y, rstd = HipRuntime.rms_norm(x_t, w_t, 1e-6)
+    dx, dw = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd)
+    dx2, dw2 = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd)
+    assert torch.equal(dx, dx2) and torch.equal(dw, dw2), "backward must be deterministic"
+    _, r_ref = oracle.rms_norm_f64(x, w, 1e-6)
+    dx_ref, dw_ref = oracle.rms_norm_backward_f64(x, w, dy, r_ref)
+    if dtype == "bf16":
+        rel_ok(host(dx), dx_ref, 1e-2, "dX")
+    else:
+        close(host(dx), dx_ref, 5e-4, 5e-4, "dX")
+    rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=DW_ATOL_FRAC)
+
+
 def test_rms_norm_c2_full_size_and_determinism():
     """x[16384,4096] bf16 ~N(0,1), w F32 ~1+N(0,0.1), eps 1e-6, dy bf16 ~N(0,1)."""
     x_t, x = randn_bf16((16384, 4096), seed=0)
