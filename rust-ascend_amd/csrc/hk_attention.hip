@@ -675,6 +675,20 @@ attn_fwd_pp(FwdArgs a) {
         uint16_t* kdst = kbuf[(j + 1) & 1];
         uint16_t* vdst = vbuf[j & 1];
         const bool k_whole = (j + 2) * kBlockN <= n32, v_whole = (j + 1) * kBlockN <= n32;
+        // Both tiles due and whole (every step but the last ones): one uniform branch, then the
+        // loads alone. Deciding per load, as below, leaves a scalar branch around every load in the
+        // softmax phase that issues them (C4 forward ~3% slower).
+        if (k_next && k_whole && v_cur && v_whole) {
+#pragma unroll
+            for (int d = 0; d < kLoadsPerWave; ++d) {
+                const int q = (wave & 3) + 4 * d;
+                if (q < kKInstr)
+                    load_lds16(rk, lds_address(kdst + 8 * 64 * q), loff[d], (j + 1) * kBlockN * D * 2);
+                else if (q < kKInstr + kVInstr)
+                    load_lds16(rv, lds_address(vdst + 8 * 64 * (q - kKInstr)), loff[d], j * kBlockN * D * 2);
+            }
+            return;
+        }
 #pragma unroll
         for (int d = 0; d < kLoadsPerWave; ++d) {
             const int q = (wave & 3) + 4 * d;  // this wave's share of the tile's instructions
