@@ -11,16 +11,13 @@
 // [rows]; dw is F32 [W]. HBM-bound: per row the forward moves W*(2 sizeof(T)) bytes
 // and the backward W*(3 sizeof(T)) bytes.
 //
-// Fast path (W % 8 == 0, W <= 4096): one wavefront owns one row at a time; lane l
-// owns the 8-element chunks l, l+64, l+128, ... (16-byte loads for BF16, fully
-// coalesced), so a row is MAXJ chunks per lane held in registers. Each wave keeps its
-// columns' w (and, in the backward, its dw partial sums) in registers across a
-// grid-stride loop over rows, so w is read once per wave, not once per row. Row sums
-// are butterfly reductions across the wave (no LDS, no barriers). The backward writes
-// one FP64 dw partial per workgroup (waves combined through LDS in wave order) and a
-// second kernel sums the partials in a fixed order: deterministic, no atomics. Widths 2048
-// and 4096 (C2's) take the split backward instead, where four waves share each row (one column
-// quarter each) so that four waves fit on every SIMD.
+// Forward fast path (W % 8 == 0, W <= 4096): one wavefront owns one row; lane l owns the
+// 8-element chunks l, l+64, l+128, ... (16-byte loads for BF16, fully coalesced), so a row is
+// MAXJ chunks per lane held in registers; the row sum is a butterfly across the wave.
+// Split path (W % 8 == 0, W <= 16384: the backward at every such width, the forward above 4096):
+// a row spread over several waves of a workgroup that exchange their part sums through LDS (see
+// rms_fwd_split / rms_bwd_split). The backward writes one FP64 dw partial row per workgroup and a
+// second kernel sums the partials in a fixed order: deterministic, no atomics.
 //
 // General path (any positive W): the same math with one element per lane-step and the
 // row re-read from cache for the second pass; dw comes from a column-parallel kernel.
@@ -35,11 +32,6 @@ namespace hk {
 namespace {
 
 constexpr int kRowsThreads = 256;  // 4 waves per workgroup (forward)
-// Backward: one 4-wave workgroup per CU, so one wave per SIMD walks its rows. Fewer rows in
-// flight stream faster here: on C2 (16384 x 4096 BF16) 4 waves per CU measured 5.1-5.2 TB/s,
-// 3 or 5 waves 4.7-4.9, 8 waves 4.6, 12 waves 4.2; a second workgroup per CU, a smaller grid or
-// prefetching the next row (the VGPRs for it are free at this occupancy) did not help.
-constexpr int kBwdThreads = 256;
 
 // Eight elements kept in their storage form between the two passes over a row
 // (4 VGPRs for BF16, 8 for F32) and widened to float on use.
@@ -134,54 +126,181 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
     if (lane == 0) rstd[row] = r;
 }
 
-template <typename T, int MAXJ, bool FULL>
-__global__ void __launch_bounds__(kBwdThreads)
-rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
-             const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial,
-             int64_t rows, int width) {
-    // [width] F32 weight, then the workgroup's [width] FP64 partial (width % 8 == 0: aligned)
+// Row-split kernels (W % 8 == 0, W <= 16384). A row of `chunks` = W/8 eight-element chunks is
+// spread over QN waves ("parts"), each holding CPL chunks per lane: lane l of part q owns the
+// chunks 64 CPL q + l + 64 j (j < CPL) that lie below `chunks` (all of them when FULL). A
+// workgroup holds G row groups of QN waves (QN G <= 16, one workgroup per CU, so up to four waves
+// per SIMD); the waves of a row group walk the same rows in a grid-stride loop. The row's sum (of
+// squares in the forward, of dy*w*x in the backward) is the sum of the parts' sums, exchanged
+// through LDS without a barrier: each wave posts its part's sum, tagged with the row's sequence
+// number, as one 64-bit LDS word into one of two slots, and reads the QN posts of the row once
+// their tags match. Every wave adds the QN posts in part order, so all of them compute the same
+// row statistic. A wave posts row k+2 into the slot of row k only after it has read every post of
+// row k+1, each made after its author had read row k's posts, so no post is overwritten before it
+// is read; all waves of a workgroup are resident together and every wave posts before it waits,
+// so every wait ends (the spin is also bounded).
+// Why split rows: a row per wave needs the whole row in flight and, in the backward, all of the
+// row's FP64 dγ sums (64 per lane at W = 4096: ~230 registers, one wave per SIMD), and four waves
+// per SIMD stream faster than one wave with two to four rows in flight. C2 (16384 x 4096 BF16)
+// backward: 71-72 us against 74-76 us for the row-per-wave kernel on the same box; W = 8192 BF16
+// ran at 1.7 TB/s (backward) and 2.9 TB/s (forward) on the column-parallel path before.
+constexpr int kSplitThreads = 1024;
+constexpr int kSplitMaxWaves = 16;
+constexpr int kSplitMaxChunks = 2048;  // W <= 16384
+constexpr int kSpinLimit = 1 << 24;
+constexpr int kPostBytes = 2 * kSplitMaxWaves * 8;  // [G][2][QN] 64-bit posts, G * QN <= 16
+
+struct SplitShape {
+    int chunks;  // W / 8
+    int qn;      // waves per row
+    int groups;  // row groups per workgroup
+    int cpl;     // chunks per lane per wave
+    bool full;   // every lane owns CPL chunks
+};
+
+// Two chunks per lane for rows of at least 256 chunks (W >= 2048), else one, and enough waves to
+// cover the row; W = 2048 keeps one chunk per lane over four waves, the split measured there.
+SplitShape split_shape(int64_t width) {
+    SplitShape sh;
+    sh.chunks = static_cast<int>(width / 8);
+    sh.cpl = sh.chunks >= 256 && width != 2048 ? 2 : 1;
+    const int per_wave = 64 * sh.cpl;
+    sh.qn = (sh.chunks + per_wave - 1) / per_wave;
+    sh.groups = kSplitMaxWaves / sh.qn;
+    sh.full = sh.chunks == sh.qn * per_wave;
+    return sh;
+}
+
+// Sum over the QN parts of row sequence k of group g (every wave of the group calls it with its
+// own part's value).
+__device__ __forceinline__ float split_row_sum(uint64_t* post, int g, int qn, int q, int64_t k, int lane, float part) {
+    const uint32_t tag = static_cast<uint32_t>(k) + 1;
+    uint64_t* slots = post + (2 * g + static_cast<int>(k & 1)) * qn;
+    // single 64-bit LDS accesses (tag and value together); the atomics keep the compiler from
+    // caching or reordering them
+    if (lane == 0)
+        __hip_atomic_store(&slots[q], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(part), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    float total = 0.0f;
+    for (int p = 0; p < qn; ++p) {
+        uint64_t val;
+        int spins = 0;
+        do {
+            val = __hip_atomic_load(&slots[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } while (static_cast<uint32_t>(val >> 32) != tag && ++spins < kSpinLimit);
+        const float v = __uint_as_float(static_cast<uint32_t>(val));
+        total = p == 0 ? v : total + v;
+    }
+    return total;
+}
+
+// LDS: the posts, then w [W] F32, then (backward with G > 1) the FP64 group-combine row [W].
+__host__ __device__ constexpr size_t split_lds_bytes(int chunks, int groups, bool bwd) {
+    return kPostBytes + static_cast<size_t>(chunks) * 8 * 4 + (bwd && groups > 1 ? static_cast<size_t>(chunks) * 8 * 8 : 0);
+}
+
+template <typename T, int CPL, bool FULL>
+__global__ void __launch_bounds__(kSplitThreads)
+rms_fwd_split(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y, float* __restrict__ rstd,
+              int64_t rows, int chunks, int qn, int groups, float eps) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-    float* w_lds = reinterpret_cast<float*>(lds_raw);
-    double* p_lds = reinterpret_cast<double*>(lds_raw + static_cast<size_t>(width) * sizeof(float));
+    uint64_t* post = reinterpret_cast<uint64_t*>(lds_raw);
+    float* w_lds = reinterpret_cast<float*>(lds_raw + kPostBytes);
+    const int W = 8 * chunks;
     const int lane = threadIdx.x & 63;
-    // wave-uniform, so row addresses and the rstd load are scalar
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int waves_per_block = blockDim.x >> 6;
-    const int chunks = width >> 3;
-    for (int c = threadIdx.x; c < width; c += blockDim.x) w_lds[c] = w[c];
+    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = v / qn, q = v - g * qn;
+    if (threadIdx.x < kPostBytes / 8) post[threadIdx.x] = 0;
+    for (int c = threadIdx.x; c < W; c += blockDim.x) w_lds[c] = w[c];
     __syncthreads();
-    // dγ sums in FP64: each term x * dy * rstd is formed exactly in the fused multiply-add (x * dy
-    // is exact in FP32 for BF16 storage, and exact in FP64 for F32), so the partial sums carry
-    // only FP64 rounding and the F32 result differs from the exact sum of the terms by the final
-    // conversion alone. (FP32 accumulation put C2's error at 0.8-1.6e-4 of |dγ| + 1e-3 rms(dγ),
-    // against 3.9e-5 now, the part due to rstd being F32; the FP64 sums cost ~3 us of the
-    // backward's 78-81 us there.)
-    double acc[MAXJ][8];
+    const float inv_w = 1.0f / static_cast<float>(W);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * groups;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * groups + g;
+    const int64_t n = first < rows ? (rows - 1 - first) / stride + 1 : 0;
+    const int cbase = 64 * CPL * q + lane;
+    for (int64_t k = 0; k < n; ++k) {
+        const int64_t row = first + k * stride;
+        const T* xr = x + row * W;
+        Raw8<T> xs[CPL];
 #pragma unroll
-    for (int j = 0; j < MAXJ; ++j)
+        for (int j = 0; j < CPL; ++j)
+            if (FULL || cbase + 64 * j < chunks) xs[j].load(xr + 8 * (cbase + 64 * j));
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (FULL || cbase + 64 * j < chunks) {
+                float xv[8];
+                xs[j].get(xv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+            }
+        }
+        ss = wave_sum(ss);
+        const float total = split_row_sum(post, g, qn, q, k, lane, ss);
+        const float r = 1.0f / sqrtf(total * inv_w + eps);
+        T* yr = y + row * W;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = cbase + 64 * j;
+            if (FULL || c < chunks) {
+                float xv[8], wv[8], o[8];
+                xs[j].pin();
+                xs[j].get(xv);
+                load8(w_lds + 8 * c, wv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (xv[e] * r) * wv[e];
+                store8_stream(yr + 8 * c, o);
+            }
+        }
+        if (lane == 0 && q == 0) rstd[row] = r;
+    }
+}
+
+template <typename T, int CPL, bool FULL>
+__global__ void __launch_bounds__(kSplitThreads)
+rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
+              const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial, int64_t rows,
+              int chunks, int qn, int groups) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+    uint64_t* post = reinterpret_cast<uint64_t*>(lds_raw);
+    float* w_lds = reinterpret_cast<float*>(lds_raw + kPostBytes);
+    const int W = 8 * chunks;
+    double* p_lds = reinterpret_cast<double*>(lds_raw + kPostBytes + static_cast<size_t>(W) * 4);
+    const int lane = threadIdx.x & 63;
+    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = v / qn, q = v - g * qn;
+    if (threadIdx.x < kPostBytes / 8) post[threadIdx.x] = 0;
+    for (int c = threadIdx.x; c < W; c += blockDim.x) w_lds[c] = w[c];
+    double acc[CPL][8];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
-    const float inv_w = 1.0f / static_cast<float>(width);
-    // rstd is loaded ahead of the row's loads, so waiting for the row covers it.
-    auto load_row = [&](Raw8<T> (&xs)[MAXJ], Raw8<T> (&gs)[MAXJ], float& r, int64_t row) __attribute__((always_inline)) {
-        r = rstd[row];
-        const T* xr = x + row * width;
-        const T* gr = dy + row * width;
+    __syncthreads();
+    const float inv_w = 1.0f / static_cast<float>(W);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * groups;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * groups + g;
+    const int64_t n = first < rows ? (rows - 1 - first) / stride + 1 : 0;
+    const int cbase = 64 * CPL * q + lane;
+    for (int64_t k = 0; k < n; ++k) {
+        const int64_t row = first + k * stride;
+        const float r = rstd[row];
+        const T* xr = x + row * W;
+        const T* gr = dy + row * W;
+        Raw8<T> xs[CPL], gs[CPL];
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
+        for (int j = 0; j < CPL; ++j) {
+            const int c = cbase + 64 * j;
             if (FULL || c < chunks) {
                 xs[j].load(xr + 8 * c);
                 gs[j].load(gr + 8 * c);
             }
         }
-    };
-    auto process_row = [&](Raw8<T> (&xs)[MAXJ], Raw8<T> (&gs)[MAXJ], float r, int64_t row) __attribute__((always_inline)) {
-        float dot = 0.0f;
         const double rd = r;
+        float dot = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
+        for (int j = 0; j < CPL; ++j) {
+            const int c = cbase + 64 * j;
             if (FULL || c < chunks) {
                 float xv[8], gv[8], wv[8];
                 xs[j].get(xv);
@@ -190,6 +309,10 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     dot += (gv[e] * wv[e]) * xv[e];
+                    // dγ sums in FP64: x * dy is exact in FP32 for BF16 storage and in FP64 for
+                    // F32, so each term x*dy*rstd is formed exactly in the fused multiply-add and
+                    // the sums carry only FP64 rounding (FP32 sums put C2's error at 0.8-1.6e-4 of
+                    // |dγ| + 1e-3 rms(dγ), against 3.9e-5 now, the part due to rstd being F32).
                     if constexpr (sizeof(T) == 2)
                         acc[j][e] = __builtin_fma(static_cast<double>(xv[e] * gv[e]), rd, acc[j][e]);
                     else
@@ -198,11 +321,12 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
             }
         }
         dot = wave_sum(dot);
-        const float corr = (dot * inv_w) * (r * r);
-        T* dr = dx + row * width;
+        const float total = split_row_sum(post, g, qn, q, k, lane, dot);
+        const float corr = (total * inv_w) * (r * r);
+        T* dr = dx + row * W;
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j) {
-            const int c = lane + 64 * j;
+        for (int j = 0; j < CPL; ++j) {
+            const int c = cbase + 64 * j;
             if (FULL || c < chunks) {
                 float xv[8], gv[8], wv[8], o[8];
                 xs[j].pin();
@@ -215,162 +339,36 @@ rms_bwd_fast(const T* __restrict__ x, const float* __restrict__ w, const T* __re
                 store8_stream(dr + 8 * c, o);
             }
         }
-    };
-    // Rows in a grid-stride walk, one at a time. (Issuing the next row's loads before the current
-    // row's reduction and stores, with two register sets, measured 1-2% slower on C2.)
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * waves_per_block;
-    for (int64_t row = static_cast<int64_t>(blockIdx.x) * waves_per_block + wave; row < rows; row += stride) {
-        Raw8<T> xs[MAXJ], gs[MAXJ];
-        float r;
-        load_row(xs, gs, r, row);
-        process_row(xs, gs, r, row);
     }
-    // Combine the waves' dw partial sums in wave order, then write the workgroup's.
-    for (int src = 0; src < waves_per_block; ++src) {
-        if (wave == src) {
+    // The workgroup's FP64 partial row: the row groups' sums combined in group order through LDS
+    // (one group: each wave writes its own columns).
+    double* out = partial + static_cast<int64_t>(blockIdx.x) * W;
+    if (groups == 1) {
 #pragma unroll
-            for (int j = 0; j < MAXJ; ++j) {
-                const int c = lane + 64 * j;
-                if (FULL || c < chunks) {
+        for (int j = 0; j < CPL; ++j) {
+            const int c = cbase + 64 * j;
+            if (FULL || c < chunks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) out[8 * c + e] = acc[j][e];
+        }
+        return;
+    }
+    for (int src = 0; src < groups; ++src) {
+        if (g == src) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = cbase + 64 * j;
+                if (FULL || c < chunks)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         double* p = &p_lds[8 * c + e];
                         *p = (src == 0) ? acc[j][e] : (*p + acc[j][e]);
                     }
-                }
             }
         }
         __syncthreads();
     }
-    double* out = partial + static_cast<int64_t>(blockIdx.x) * width;
-    for (int c = threadIdx.x; c < width; c += blockDim.x) out[c] = p_lds[c];
-}
-
-// Backward for widths 2048 and 4096 (W = 2048 * CPL): 16-wave workgroups, one per CU, so four
-// waves share each SIMD. A row is split over four waves, one column quarter each (lane l of
-// quarter q owns the chunks 64 CPL q + l + 64 j, j < CPL), so each wave keeps only a quarter of
-// the dγ sums (16 CPL FP64 registers per lane) and a quarter row in flight; the four waves of a
-// row group walk their rows in a grid-stride loop. The row's dot product sum(dy*w*x) is the sum
-// of the four quarter dots, exchanged through LDS without a barrier: each wave posts its
-// quarter's dot, tagged with the row's sequence number, into one of two slots, and reads the
-// other three posts once their tags match. Every wave adds the four in quarter order, so all
-// four compute the same correction. A wave posts row k+2 into the slot of row k only after it
-// has read every post of row k+1, each made after its author had read row k's posts, so no post
-// is overwritten before it is read; all 16 waves of a workgroup are resident together, and every
-// wave posts before it waits, so every wait ends (the spin is also bounded).
-// C2 (16384 x 4096 BF16): 71-72 us against 74-76 us for rms_bwd_fast on the same box: a row per
-// wave needs the whole row's 64 FP64 sums per lane (~230 registers, one wave per SIMD), and
-// four waves per SIMD stream faster than one wave with two to four rows in flight.
-constexpr int kSplitThreads = 1024;
-constexpr int kSplitGroups = 4;  // row groups per workgroup (x 4 column quarters = 16 waves)
-constexpr int kSpinLimit = 1 << 24;
-
-template <typename T, int CPL>
-__global__ void __launch_bounds__(kSplitThreads)
-rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
-              const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial, int64_t rows) {
-    constexpr int W = 2048 * CPL;
-    constexpr int CQ = 64 * CPL;  // chunks per quarter
-    __shared__ __attribute__((aligned(16))) float w_lds[W];
-    __shared__ double p_lds[W];
-    __shared__ uint64_t post[kSplitGroups][2][4];
-    const int lane = threadIdx.x & 63;
-    const int v = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = v >> 2, q = v & 3;
-    if (threadIdx.x < kSplitGroups * 2 * 4) (&post[0][0][0])[threadIdx.x] = 0;
-    for (int c = threadIdx.x; c < W; c += kSplitThreads) w_lds[c] = w[c];
-    double acc[CPL][8];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = 0.0;
-    __syncthreads();
-    const float inv_w = 1.0f / static_cast<float>(W);
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kSplitGroups;
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * kSplitGroups + g;
-    const int64_t n = first < rows ? (rows - 1 - first) / stride + 1 : 0;
-    for (int64_t k = 0; k < n; ++k) {
-        const int64_t row = first + k * stride;
-        const float r = rstd[row];
-        const T* xr = x + row * W;
-        const T* gr = dy + row * W;
-        Raw8<T> xs[CPL], gs[CPL];
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = CQ * q + lane + 64 * j;
-            xs[j].load(xr + 8 * c);
-            gs[j].load(gr + 8 * c);
-        }
-        const double rd = r;
-        float dot = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = CQ * q + lane + 64 * j;
-            float xv[8], gv[8], wv[8];
-            xs[j].get(xv);
-            gs[j].get(gv);
-            load8(w_lds + 8 * c, wv);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                dot += (gv[e] * wv[e]) * xv[e];
-                // x * dy is exact in FP32 for BF16 storage and in FP64 for F32: each term exact
-                if constexpr (sizeof(T) == 2)
-                    acc[j][e] = __builtin_fma(static_cast<double>(xv[e] * gv[e]), rd, acc[j][e]);
-                else
-                    acc[j][e] = __builtin_fma(static_cast<double>(xv[e]) * gv[e], rd, acc[j][e]);
-            }
-        }
-        dot = wave_sum(dot);
-        // posts and polls are single 64-bit LDS accesses (tag and value together); atomic loads and
-        // stores keep the compiler from caching or reordering them
-        const uint32_t tag = static_cast<uint32_t>(k) + 1;
-        const int sl = static_cast<int>(k & 1);
-        if (lane == 0)
-            __hip_atomic_store(&post[g][sl][q], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(dot),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        float part[4];
-        for (int p = 0; p < 4; ++p) {
-            uint64_t val;
-            int spins = 0;
-            do {
-                val = __hip_atomic_load(&post[g][sl][p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            } while (static_cast<uint32_t>(val >> 32) != tag && ++spins < kSpinLimit);
-            part[p] = __uint_as_float(static_cast<uint32_t>(val));
-        }
-        const float total = ((part[0] + part[1]) + part[2]) + part[3];
-        const float corr = (total * inv_w) * (r * r);
-        T* dr = dx + row * W;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = CQ * q + lane + 64 * j;
-            float xv[8], gv[8], wv[8], o[8];
-            xs[j].pin();
-            gs[j].pin();
-            xs[j].get(xv);
-            gs[j].get(gv);
-            load8(w_lds + 8 * c, wv);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (gv[e] * wv[e] - xv[e] * corr) * r;
-            store8_stream(dr + 8 * c, o);
-        }
-    }
-    // The row groups' dγ sums combined in group order, then the workgroup's FP64 partial row.
-    for (int src = 0; src < kSplitGroups; ++src) {
-        if (g == src) {
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const int c = CQ * q + lane + 64 * j;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    double* p = &p_lds[8 * c + e];
-                    *p = (src == 0) ? acc[j][e] : (*p + acc[j][e]);
-                }
-            }
-        }
-        __syncthreads();
-    }
-    double* out = partial + static_cast<int64_t>(blockIdx.x) * W;
-    for (int c = threadIdx.x; c < W; c += kSplitThreads) out[c] = p_lds[c];
+    for (int c = threadIdx.x; c < W; c += blockDim.x) out[c] = p_lds[c];
 }
 
 // dw[c] = sum over p of the FP64 partial[p][c] for parts <= 256 and width % 8 == 0 (the fast and
@@ -544,18 +542,45 @@ void launch_fwd_fast(const void* x, const float* w, void* y, float* rstd, int64_
     }
 }
 
-template <typename T, int MAXJ>
-void launch_bwd_fast(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
-                     double* partial, int parts, int64_t rows, int width, hipStream_t s) {
-    auto kernel = width == 512 * MAXJ ? rms_bwd_fast<T, MAXJ, true> : rms_bwd_fast<T, MAXJ, false>;
-    hipLaunchKernelGGL(kernel, dim3(parts), dim3(kBwdThreads),
-                       static_cast<size_t>(width) * (sizeof(float) + sizeof(double)), s, static_cast<const T*>(x), w,
-                       static_cast<const T*>(dy), rstd, static_cast<T*>(dx), partial, rows, width);
+bool split_rows(int64_t width, std::initializer_list<const void*> ptrs) {
+    if (width % 8 != 0 || width / 8 > kSplitMaxChunks) return false;
+    for (const void* p : ptrs)
+        if (!aligned16(p)) return false;
+    return true;
 }
 
-// One workgroup per CU is resident: a grid of exactly one round of workgroups (4 rows in flight
-// per workgroup in both the fast and the split kernel).
-int parts_fast(int64_t rows) { return grid_for_rows(rows, kBwdThreads / 64, 256); }
+// One round of workgroups: at most 256 (one per CU), each covering `groups` rows at a time.
+int split_grid(int64_t rows, int groups) { return grid_for_rows(rows, groups, 256); }
+
+template <typename T, int CPL>
+void launch_split(bool bwd, const SplitShape& sh, int grid, const void* x, const float* w, const void* dy,
+                  const float* rstd_in, void* out, float* rstd_out, double* partial, int64_t rows, float eps,
+                  hipStream_t s) {
+    const dim3 block(64 * sh.qn * sh.groups);
+    const size_t lds = split_lds_bytes(sh.chunks, sh.groups, bwd);
+    if (bwd) {
+        auto kernel = sh.full ? rms_bwd_split<T, CPL, true> : rms_bwd_split<T, CPL, false>;
+        hipLaunchKernelGGL(kernel, dim3(grid), block, lds, s, static_cast<const T*>(x), w, static_cast<const T*>(dy),
+                           rstd_in, static_cast<T*>(out), partial, rows, sh.chunks, sh.qn, sh.groups);
+    } else {
+        auto kernel = sh.full ? rms_fwd_split<T, CPL, true> : rms_fwd_split<T, CPL, false>;
+        hipLaunchKernelGGL(kernel, dim3(grid), block, lds, s, static_cast<const T*>(x), w, static_cast<T*>(out),
+                           rstd_out, rows, sh.chunks, sh.qn, sh.groups, eps);
+    }
+}
+
+template <typename T>
+void run_split(bool bwd, int64_t width, const void* x, const float* w, const void* dy, const float* rstd_in,
+               void* out, float* rstd_out, double* partial, int* parts, int64_t rows, float eps, hipStream_t s) {
+    const SplitShape sh = split_shape(width);
+    const int grid = split_grid(rows, sh.groups);
+    if (parts) *parts = grid;
+    if (sh.cpl == 2)
+        launch_split<T, 2>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, s);
+    else
+        launch_split<T, 1>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, s);
+}
+
 int parts_general(int64_t rows) {
     int64_t parts = (rows + 63) / 64;  // at most 64 rows per column chunk
     if (parts > 512) parts = 512;
@@ -572,6 +597,8 @@ hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, in
         else if (chunks_per_lane <= 2) launch_fwd_fast<T, 2>(x, w, y, rstd, rows, (int)width, eps, s);
         else if (chunks_per_lane <= 4) launch_fwd_fast<T, 4>(x, w, y, rstd, rows, (int)width, eps, s);
         else launch_fwd_fast<T, 8>(x, w, y, rstd, rows, (int)width, eps, s);
+    } else if (split_rows(width, {x, w, y})) {  // 4096 < W <= 16384
+        run_split<T>(false, width, x, w, nullptr, nullptr, y, rstd, nullptr, nullptr, rows, eps, s);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_fwd_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
@@ -588,19 +615,9 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
         hipLaunchKernelGGL(fill_zero_f32, dim3(flat_blocks(width, 256)), dim3(256), 0, s, dw, width);
         return hipGetLastError();
     }
-    if (fast_rows(width, {x, w, dy, dx})) {
-        const int parts = parts_fast(rows);  // <= 256
-        if (width == 2048 || width == 4096) {
-            auto kernel = width == 4096 ? rms_bwd_split<T, 2> : rms_bwd_split<T, 1>;
-            hipLaunchKernelGGL(kernel, dim3(parts), dim3(kSplitThreads), 0, s, static_cast<const T*>(x), w,
-                               static_cast<const T*>(dy), rstd, static_cast<T*>(dx), workspace, rows);
-        } else {
-            const int chunks_per_lane = static_cast<int>((width / 8 + 63) / 64);
-            if (chunks_per_lane <= 1) launch_bwd_fast<T, 1>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-            else if (chunks_per_lane <= 2) launch_bwd_fast<T, 2>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-            else if (chunks_per_lane <= 4) launch_bwd_fast<T, 4>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-            else launch_bwd_fast<T, 8>(x, w, dy, rstd, dx, workspace, parts, rows, (int)width, s);
-        }
+    if (split_rows(width, {x, w, dy, dx})) {
+        int parts = 0;  // one FP64 partial row per workgroup, at most 256
+        run_split<T>(true, width, x, w, dy, rstd, dx, nullptr, workspace, &parts, rows, 0.0f, s);
         hipLaunchKernelGGL(sum_partials8, dim3(static_cast<unsigned>(width / 8)), dim3(256), 0, s, workspace, parts,
                            (int)width, dw);
     } else {
@@ -621,7 +638,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
 }  // namespace
 
 size_t rms_backward_workspace_bytes(int64_t rows, int64_t width) {
-    const int parts = std::max(parts_fast(rows), parts_general(rows));
+    const int parts = std::max(static_cast<int>(std::min<int64_t>(rows, 256)), parts_general(rows));
     return static_cast<size_t>(parts) * static_cast<size_t>(width) * sizeof(double);
 }
 

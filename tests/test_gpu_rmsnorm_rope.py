@@ -48,13 +48,20 @@ def test_rms_norm_bf16_vs_oracle(rows, width):
     rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=DW_ATOL_FRAC)
 
 
+# Row-split kernels: W = 8 * chunks is spread over QN waves of 64 lanes x CPL chunks (CPL 2 from
+# W = 3072 on, W = 2048 keeps CPL 1 over four waves), G = 16 // QN row groups per workgroup of at
+# most 256: the widths below cover QN = 1..16, a partly filled last wave (520, 12296) and full ones;
+# the row counts leave row groups idle, walk uneven grid strides and reuse both posting slots.
+SPLIT_CASES = [(5, 8), (4099, 512), (1000, 520), (4100, 1024), (1, 2048), (5, 2048), (2050, 2048), (3, 4096),
+               (1023, 4096), (4099, 4096), (1300, 3072), (2, 5120), (1290, 5120), (900, 6144), (515, 8192),
+               (300, 12296), (260, 16384), (7, 16384)]
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("rows,width", [(1, 2048), (3, 4096), (5, 2048), (1023, 4096), (1025, 2048), (4099, 4096),
-                                        (2050, 2048)])
-def test_rms_norm_backward_split_path(dtype, rows, width):
-    """Widths 2048 and 4096 take the backward whose rows are split over four waves: row counts
-    that leave row groups idle, uneven grid-stride walks and many rows per group (both posting
-    slots reused), F32 and BF16 storage, against the float64 oracle; bit-identical on a rerun."""
+@pytest.mark.parametrize("rows,width", SPLIT_CASES)
+def test_rms_norm_split_path(dtype, rows, width):
+    """Forward (above W = 4096) and backward (every W % 8 == 0 up to 16384) on the row-split
+    kernels, against the float64 oracle; the backward bit-identical on a rerun."""
     seed = rows * 3 + width + (7 if dtype == "bf16" else 0)
     if dtype == "bf16":
         x_t, x = randn_bf16((rows, width), seed=seed)
@@ -69,11 +76,17 @@ def test_rms_norm_backward_split_path(dtype, rows, width):
     dx, dw = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd)
     dx2, dw2 = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd)
     assert torch.equal(dx, dx2) and torch.equal(dw, dw2), "backward must be deterministic"
-    _, r_ref = oracle.rms_norm_f64(x, w, 1e-6)
-    dx_ref, dw_ref = oracle.rms_norm_backward_f64(x, w, dy, r_ref)
+    y_ref, r_ref = oracle.rms_norm_f64(x, w, 1e-6)
+    rel_ok(host(rstd), r_ref, 1e-5, "rstd")
+    # the backward is a function of the rstd it is given (the saved F32 tensor): its oracle takes
+    # the same values, so F32 rounding of rstd (up to ~1.2e-4 on this dγ measure at W = 5120 F32)
+    # is charged to the forward's rstd check above, not to the backward
+    dx_ref, dw_ref = oracle.rms_norm_backward_f64(x, w, dy, host(rstd).astype(np.float64))
     if dtype == "bf16":
+        rel_ok(host(y), y_ref, 1e-2, "Y")
         rel_ok(host(dx), dx_ref, 1e-2, "dX")
     else:
+        close(host(y), y_ref, 5e-4, 5e-4, "Y")
         close(host(dx), dx_ref, 5e-4, 5e-4, "dX")
     rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=DW_ATOL_FRAC)
 
