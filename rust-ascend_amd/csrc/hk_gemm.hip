@@ -461,11 +461,39 @@ bool pp_applies(int64_t batch, int64_t m, int64_t n, int64_t k, int num_cus) {
            n * k64 * 2 < (int64_t{1} << 31);
 }
 
+// Output tile width: 256 (NJ = 8) or 192 (NJ = 6) for a grid of `batch` x M/256 x N/(32 NJ) tiles
+// on num_cus CUs, whichever takes fewer rounds of workgroups times the time of one tile. Measured
+// on MI355X with each width forced: a part-empty last round costs nearly a full one, and a narrow
+// tile takes ~1.1-1.15x the square tile's time per flop, so a round costs 80 (square) or 69
+// (192-wide): narrow tiles are taken only when they save a whole round. C3's shapes fill whole
+// rounds of square tiles and stay square; C5's 4096 x 6144 QKV projection (384 square tiles, 1.5
+// rounds) runs 512 narrow tiles in 2 rounds (alone 168 -> 151 us; 180 -> 175 us inside the layer).
+// 224-wide tiles (NJ = 7) for the 896-tile 4096 x 14336 outputs gained 1-4% alone and nothing
+// inside the layer, so they are not built.
+int pick_tile_nj(int64_t batch, int64_t m, int64_t n, int num_cus) {
+    const int64_t tiles_m = (m + kPPTile - 1) / kPPTile;
+    auto cost = [&](int nj, int per_round) {
+        const int64_t tiles = tiles_m * ((n + 32 * nj - 1) / (32 * nj)) * batch;
+        return (tiles + num_cus - 1) / num_cus * per_round;
+    };
+    return cost(6, 69) < cost(8, 80) ? 6 : 8;
+}
+
+template <bool OUT_BF16, int NJ>
+void launch_pp_nj(const GemmArgs& p, const dim3& grid, bool a_mn, bool b_mn, hipStream_t s) {
+    if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, true, false, NJ>), grid, dim3(kW4Threads), 0, s, p);
+    else if (a_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, false, false, NJ>), grid, dim3(kW4Threads), 0, s, p);
+    else if (b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, true, false, NJ>), grid, dim3(kW4Threads), 0, s, p);
+    else hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, false, false, NJ>), grid, dim3(kW4Threads), 0, s, p);
+}
+
 template <bool OUT_BF16>
-void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, hipStream_t s) {
+void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, int num_cus, hipStream_t s) {
     GemmArgs p = a;
+    // narrower tiles only for whole K stages (the KTAIL variants stay square)
+    const int nj = p.k % kPK == 0 ? pick_tile_nj(batch, p.m, p.n, num_cus) : 8;
     p.tiles_m = (p.m + kPPTile - 1) / kPPTile;
-    p.tiles_n = (p.n + kPPTile - 1) / kPPTile;
+    p.tiles_n = (p.n + 32 * nj - 1) / (32 * nj);
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n), 1, static_cast<unsigned>(batch));
     // Square tile grids run bands of 4 M-tile rows per XCD; other grids bands of 8 N-tile
     // columns, so an XCD's L2 holds a narrow slice of B (Llama projections 8192x4096->14336
@@ -479,14 +507,12 @@ void launch_pp(const GemmArgs& a, int64_t batch, bool a_mn, bool b_mn, hipStream
         else hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, false, true>), grid, dim3(kW4Threads), 0, s, p);
         return;
     }
-    if (a_mn && b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, true>), grid, dim3(kW4Threads), 0, s, p);
-    else if (a_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, true, false>), grid, dim3(kW4Threads), 0, s, p);
-    else if (b_mn) hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, true>), grid, dim3(kW4Threads), 0, s, p);
-    else hipLaunchKernelGGL((gemm_nt_m16_kernel<OUT_BF16, false, false>), grid, dim3(kW4Threads), 0, s, p);
+    if (nj == 6) launch_pp_nj<OUT_BF16, 6>(p, grid, a_mn, b_mn, s);
+    else launch_pp_nj<OUT_BF16, 8>(p, grid, a_mn, b_mn, s);
 }
 
 template <int BM, int BN>
-void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
+void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, int num_cus, hipStream_t s) {
     GemmArgs p = a;
     p.tiles_m = (p.m + BM - 1) / BM;
     p.tiles_n = (p.n + BN - 1) / BN;
@@ -495,8 +521,8 @@ void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, hipStream_t s) {
     const bool whole_steps = p.k % kSBK == 0 && p.k > 0 && static_cast<int64_t>(p.m) * p.k * 2 < (int64_t{1} << 31) &&
                              static_cast<int64_t>(p.n) * p.k * 2 < (int64_t{1} << 31);
     if (whole_steps && p.k % kPK == 0 && BM == kPPTile && BN == kPPTile) {
-        if (out_bf16) launch_pp<true>(p, batch, false, false, s);
-        else launch_pp<false>(p, batch, false, false, s);
+        if (out_bf16) launch_pp<true>(p, batch, false, false, num_cus, s);
+        else launch_pp<false>(p, batch, false, false, num_cus, s);
     } else if (whole_steps && out_bf16)
         hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
     else if (whole_steps)
@@ -512,9 +538,9 @@ void launch_nt_sized(const GemmArgs& p, int64_t batch, bool out_bf16, int num_cu
     const int64_t m = p.m, n = p.n;
     const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256) * batch;
     const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128) * batch;
-    if (t256 >= num_cus) launch_nt<256, 256>(p, batch, out_bf16, s);
-    else if (t128 >= num_cus) launch_nt<128, 128>(p, batch, out_bf16, s);
-    else launch_nt<64, 64>(p, batch, out_bf16, s);
+    if (t256 >= num_cus) launch_nt<256, 256>(p, batch, out_bf16, num_cus, s);
+    else if (t128 >= num_cus) launch_nt<128, 128>(p, batch, out_bf16, num_cus, s);
+    else launch_nt<64, 64>(p, batch, out_bf16, num_cus, s);
 }
 
 size_t round256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -540,8 +566,8 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
         p.m = static_cast<int>(m);
         p.n = static_cast<int>(n);
         p.k = static_cast<int>(k);
-        if (out_bf16) launch_pp<true>(p, batch, ta != 0, tb == 0, s);
-        else launch_pp<false>(p, batch, ta != 0, tb == 0, s);
+        if (out_bf16) launch_pp<true>(p, batch, ta != 0, tb == 0, num_cus, s);
+        else launch_pp<false>(p, batch, ta != 0, tb == 0, num_cus, s);
         return hipGetLastError();
     }
     char* ws = static_cast<char*>(workspace);
@@ -580,8 +606,8 @@ hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_b
     p.k = static_cast<int>(k);
     p.block_group = block_group;
     if (pp_applies(1, m, n, k, num_cus)) {
-        if (out_bf16) launch_pp<true>(p, 1, false, false, s);
-        else launch_pp<false>(p, 1, false, false, s);
+        if (out_bf16) launch_pp<true>(p, 1, false, false, num_cus, s);
+        else launch_pp<false>(p, 1, false, false, num_cus, s);
     } else {
         launch_nt_sized(p, 1, out_bf16, num_cus, s);
     }

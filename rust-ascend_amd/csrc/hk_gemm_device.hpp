@@ -102,11 +102,22 @@ constexpr int kOutOfRange = static_cast<int>(0x80000000u);
 // K take an out-of-range offset and read as zero; the k-rows of an MN-major operand past K lie
 // past the end of that operand's range already. Zeros add nothing to the accumulators, so the
 // result equals that of K zero-padded to a multiple of 64.
-// One 256x256 output tile per workgroup: tile blockIdx.x of batch blockIdx.z, the grid being
+// One 256 x (32 NJ) output tile per workgroup: tile blockIdx.x of batch blockIdx.z, the grid being
 // tiles_m * tiles_n x 1 x batch (the libhk.so kernel and the device-program entry points both
-// call it; kW4Threads threads, one workgroup per CU).
-template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL, class Args>
+// call it; kW4Threads threads, one workgroup per CU). NJ = 8 gives the square 256x256 tile; the
+// launcher takes NJ = 6 (192-wide tiles, each wave 128 x 96) when that saves a whole round of
+// workgroups (a 1.5-round grid of square tiles as 2 rounds of narrow ones). The B stage keeps its
+// 256 rows or columns; an MN-major B is staged 256 columns wide as for NJ = 8 (the columns past the
+// tile feed nothing).
+template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL, class Args, int NJ = 8>
 __device__ __forceinline__ void gemm_m16_tile(Args p) {
+    static_assert(NJ >= 1 && NJ <= 8, "B fragments per wave");
+    constexpr int kTileN = 32 * NJ;  // output columns per tile
+    constexpr int kWaveN = 16 * NJ;  // output columns per wave
+    constexpr int kLoadsA = 8, kLoadsB = B_MN ? 8 : NJ;  // 1 KB global->LDS loads per wave per stage
+    constexpr int kLoads = kLoadsA + kLoadsB;
+    constexpr int kReads = 8 + NJ;  // fragment reads per wave per k-slice
+    constexpr int kMfma = 8 * NJ;   // MFMAs per wave per k-slice
     constexpr int kStage = 2 * kPPTile * kPK;
     __shared__ __attribute__((aligned(1024))) uint16_t slot0[kStage];
     __shared__ __attribute__((aligned(1024))) uint16_t slot1[kStage];
@@ -151,7 +162,7 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
     const int mn_row0 = 2 * wave + (lane >> 5), mn_pos = lane & 31;
     const int mn_c = (((mn_pos >> 2) ^ (mn_row0 & 3)) << 2) | (mn_pos & 3);
     const int mn_voff_a = (mn_row0 * p.m + tm * kPPTile + mn_c * 8) * 2;
-    const int mn_voff_b = (mn_row0 * p.n + tn * kPPTile + mn_c * 8) * 2;
+    const int mn_voff_b = (mn_row0 * p.n + tn * kTileN + mn_c * 8) * 2;
     const uint32_t lds0 = lds_address(slot0), lds1 = lds_address(slot1);
     // K-major load: the stage offset moves into the lane's offset, which the range check sees
     auto kmajor = [&](const i32x4_t& r, uint32_t dst, int row_off, int kt) __attribute__((always_inline)) {
@@ -168,11 +179,11 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
             else kmajor(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt);
         } else {
             if constexpr (B_MN) load_lds16(rb4, dst, mn_voff_b + (kt * kPK + 8 * (d - 8)) * p.n * 2, 0);
-            else kmajor(rb4, dst, voff + (tn * kPPTile + 8 * (blk - 32)) * p.k * 2, kt);
+            else kmajor(rb4, dst, voff + (tn * kTileN + 8 * (blk - 32)) * p.k * 2, kt);
         }
     };
 
-    const int a_row = 128 * wm + l16, b_row = kPPTile + 128 * wn + l16;
+    const int a_row = 128 * wm + l16, b_row = kPPTile + kWaveN * wn + l16;
     // Transposing read of an MN-major 16x16x32 operand: columns col0 .. col0+15 (col0 % 16 == 0),
     // k-rows k0 .. k0+7 with k0 = 32 ks + 8 lg (each 16-lane group its own k0; k0 % 4 == 0, so the
     // k-row's XOR term is i/4). Lane i of a group reads 4 columns of k-row k0 + i/4 (then k0 + 4 +
@@ -187,59 +198,66 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
         const v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         return __builtin_bit_cast(bf16x8_t, v);
     };
-    bf16x8_t fa[2][8], fb[2][8];
+    bf16x8_t fa[2][8], fb[2][NJ];
     auto read1 = [&](const uint16_t* slot, int ks, int buf, int f) __attribute__((always_inline)) {
         const int c = 4 * ks + lg;
         if (f < 8) {
             if constexpr (A_MN) fa[buf][f] = read_tr(slot, 8 * c, 128 * wm + 16 * f);
             else fa[buf][f] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(a_row + 16 * f, c));
         } else {
-            if constexpr (B_MN) fb[buf][f - 8] = read_tr(slot + kPPTile * kPK, 8 * c, 128 * wn + 16 * (f - 8));
+            if constexpr (B_MN) fb[buf][f - 8] = read_tr(slot + kPPTile * kPK, 8 * c, kWaveN * wn + 16 * (f - 8));
             else fb[buf][f - 8] = *reinterpret_cast<const bf16x8_t*>(slot + swz64(b_row + 16 * (f - 8), c));
         }
     };
 
-    f32x4_t acc[8][8];
+    f32x4_t acc[8][NJ];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc[i][j]));
+        for (int j = 0; j < NJ; ++j) asm volatile("" : "+a"(acc[i][j]));
 
     const int nk = KTAIL ? (p.k + kPK - 1) / kPK : p.k / kPK;
-    // 64 MFMAs on buffer `cur`; after MFMA 4t: fragment read t of slice `next_ks` from `next_slot`
-    // into the other buffer; after MFMA 4t + 2: the direct load of block d0 + t (if below d1).
+    // kMfma MFMAs on buffer `cur`, with the kReads fragment reads of slice `next_ks` (from
+    // `next_slot` into the other buffer) and the loads d0 .. d1-1 spread evenly between them: read t
+    // follows MFMA ceil(t kMfma / kReads), load t MFMA floor((t + 1/2) kMfma / kLoads), so for NJ = 8
+    // a read follows every fourth MFMA and a load two MFMAs later.
     auto slice = [&](int cur, const uint16_t* next_slot, int next_ks, uint32_t load_slot, int d0, int d1,
                      int kt) __attribute__((always_inline)) {
         const int nxt = cur ^ 1;
 #pragma unroll
-        for (int e = 0; e < 64; ++e) {
-            const int i = e >> 3, j = e & 7;
+        for (int e = 0; e < kMfma; ++e) {
+            const int i = e / NJ, j = e % NJ;
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
             phase_fence();
-            if ((e & 3) == 0) read1(next_slot, next_ks, nxt, e >> 2);
-            else if ((e & 3) == 2 && d0 + (e >> 2) < d1) dload(load_slot, kt, d0 + (e >> 2));
+            // At most one read and one load per MFMA (kReads, kLoads <= kMfma): read t = floor(e kReads /
+            // kMfma) goes here when ceil(t kMfma / kReads) == e, load t = ceil((2 e kLoads - kMfma) /
+            // (2 kMfma)) when floor((2t + 1) kMfma / (2 kLoads)) == e.
+            const int tr = e * kReads / kMfma;
+            if ((tr * kMfma + kReads - 1) / kReads == e) read1(next_slot, next_ks, nxt, tr);
+            const int tl = (2 * e * kLoads - kMfma + 2 * kMfma - 1) / (2 * kMfma);  // ceil, numerator >= -kMfma
+            if (tl < kLoads && ((2 * tl + 1) * kMfma) / (2 * kLoads) == e && d0 + tl < d1) dload(load_slot, kt, d0 + tl);
             phase_fence();
         }
     };
 
     // Prologue: stage 0 into slot 0, stage 1 into slot 1, slice 0's fragments.
 #pragma unroll
-    for (int d = 0; d < 16; ++d) dload(lds0, 0, d);
+    for (int d = 0; d < kLoads; ++d) dload(lds0, 0, d);
     stage_barrier<0>();
 #pragma unroll
-    for (int d = 0; d < 16; ++d) dload(lds1, nk > 1 ? 1 : 0, d);
+    for (int d = 0; d < kLoads; ++d) dload(lds1, nk > 1 ? 1 : 0, d);
 #pragma unroll
-    for (int f = 0; f < 16; ++f) read1(slot0, 0, 0, f);
+    for (int f = 0; f < kReads; ++f) read1(slot0, 0, 0, f);
 
     auto stage = [&](const uint16_t* R, const uint16_t* W, uint32_t Rl, int s) __attribute__((always_inline)) {
         const int ahead = s + 2 < nk ? s + 2 : nk - 1;
         slice(0, R, 1, Rl, 0, 0, ahead);      // reads only
         stage_barrier<0>();                   // stage s+1 complete in W; every read of R done
-        slice(1, W, 0, Rl, 0, 16, ahead);     // + all of stage s+2 into the freed R
+        slice(1, W, 0, Rl, 0, kLoads, ahead);  // + all of stage s+2 into the freed R
     };
     int s = 0;
     do {
@@ -254,8 +272,8 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
         const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
         if (m >= p.m) continue;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int n = tn * kPPTile + 128 * wn + 16 * j + 4 * lg;
+        for (int j = 0; j < NJ; ++j) {
+            const int n = tn * kTileN + kWaveN * wn + 16 * j + 4 * lg;
             if (n >= p.n) continue;
             const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
             if constexpr (OUT_BF16) {
@@ -268,10 +286,10 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
     }
 }
 
-template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL = false>
+template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL = false, int NJ = 8>
 __global__ void __launch_bounds__(kW4Threads, 1)
 gemm_nt_m16_kernel(GemmArgs p) {
-    gemm_m16_tile<OUT_BF16, A_MN, B_MN, KTAIL>(p);
+    gemm_m16_tile<OUT_BF16, A_MN, B_MN, KTAIL, GemmArgs, NJ>(p);
 }
 
 }  // namespace

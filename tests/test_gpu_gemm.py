@@ -113,6 +113,31 @@ def test_gemm_256_tile_paths(batch, m, n, k, ta, tb):
                 f32_close(got, want, f"GEMM {batch}x{m}x{n}x{k} {ta}{tb} f32 [{g}]")
 
 
+@pytest.mark.parametrize("n", [6144, 6128, 4112])
+@pytest.mark.parametrize("ta,tb", TRANSPOSES)
+def test_gemm_narrow_tiles_equal_square_tiles(n, ta, tb):
+    """Grids whose square 256x256 tiles would take a part-empty extra round run 256x192 tiles:
+    N = 6144 (384 -> 512 tiles, two full rounds), 6128 and 4112 (partial last tiles). An output
+    element's K sum does not depend on the tile it belongs to, so the first 4096 columns are
+    bit-identical to the same product with N = 4096 (256 square tiles), in both output types and
+    every transpose (an MN-major B is staged 256 columns wide either way); plus the oracle on the
+    last columns."""
+    m, k = 4096, 320
+    a_t, a = randn_bf16((k, m) if ta else (m, k), seed=n + ta, std=1 / np.sqrt(k))
+    b_t, b = randn_bf16((n, k) if tb else (k, n), seed=n + 2 * tb + 1, std=1.0)
+    b_sq = (b_t[:4096] if tb else b_t[:, :4096]).contiguous()
+    for out in (torch.bfloat16, torch.float32):
+        y = HipRuntime.gemm(a_t, b_t, Transpose(ta), Transpose(tb), out)
+        y_sq = HipRuntime.gemm(a_t, b_sq, Transpose(ta), Transpose(tb), out)
+        view = torch.int16 if out == torch.bfloat16 else torch.int32
+        assert torch.equal(y[:, :4096].contiguous().view(view), y_sq.view(view)), (n, ta, tb, out)
+    rows = np.concatenate([np.arange(0, m, 97), np.arange(m - 8, m)])
+    cols = np.arange(n - 300, n)
+    r, c = np.meshgrid(rows, cols, indexing="ij")
+    want = oracle.gemm_f64_sampled(a, b, ta, tb, r.ravel(), c.ravel())
+    rel_ok(host(y)[r.ravel(), c.ravel()], want, 1e-2, f"narrow tiles {m}x{n}x{k} {ta}{tb}")
+
+
 @pytest.mark.parametrize("batch,k", [(1, 16), (1, 48), (1, 1040), (1, 2032), (1, 4000), (2, 48), (2, 1040)])
 @pytest.mark.parametrize("ta,tb", TRANSPOSES)
 def test_gemm_partial_last_stage_equals_zero_padded_k(batch, k, ta, tb):
