@@ -1904,10 +1904,10 @@ hk_status hk_nll_loss(hk_context* h, const hk_tensor* input, const hk_tensor* ta
     if (!disjoint({out, total_weight}, {input, target, weight})) return HK_INVALID_ARGUMENT;
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
-    if ((st = ensure_workspace(g.c, 256)) != HK_OK) return st;
+    if ((st = ensure_workspace(g.c, hk::nll_loss_workspace_bytes(rows))) != HK_OK) return st;
     hipError_t e = hk::nll_loss(float_code(input->dtype), target->dtype == HK_I64 ? 8 : 4, input->data, target->data,
                                 weight->data, out->data, total_weight->data, rows, classes, reduction, ignore_index,
-                                static_cast<int*>(g.c->workspace), g.c->stream);
+                                g.c->workspace, g.c->stream);
     st = complete(g.c, e, "nll_loss", 1);
     if (st != HK_OK || g.c->async) return st;
     int flag = 0;

@@ -86,8 +86,9 @@ hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_b
 // dtype 0 F32, 1 F16, 2 BF16 (input, weight, out, total, grad, dinput); id_bytes 4 or 8;
 // reduction 0 None, 1 Mean, 2 Sum. The forward writes *bad = 1 if a label outside [0, classes)
 // that is not `ignore` occurs.
+size_t nll_loss_workspace_bytes(int64_t rows);  // the label flag and the per-row terms
 hipError_t nll_loss(int dtype, int id_bytes, const void* input, const void* target, const void* weight, void* out,
-                    void* total, int64_t rows, int64_t classes, int reduction, int64_t ignore, int* bad, hipStream_t s);
+                    void* total, int64_t rows, int64_t classes, int reduction, int64_t ignore, void* workspace, hipStream_t s);
 hipError_t nll_loss_backward(int dtype, int id_bytes, const void* grad, const void* target, const void* weight,
                              const void* total, void* dinput, int64_t rows, int64_t classes, int reduction,
                              int64_t ignore, hipStream_t s);

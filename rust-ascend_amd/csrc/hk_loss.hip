@@ -14,8 +14,9 @@
 // a fixed order (deterministic). A label outside [0, C) that is not ignore_index raises a flag the
 // host checks (the row then contributes nothing).
 //
-// Layout: the forward is one workgroup striding over rows (N is a token count; the loss is tiny
-// next to the logits it follows); the backward writes the dense [N, C] gradient, one element per
+// Layout: the forward computes every row's term in parallel into a workspace, then one workgroup
+// sums the terms in a fixed order (N is a token count; the loss is tiny next to the logits it
+// follows); the backward writes the dense [N, C] gradient, one element per
 // thread, coalesced along C (HBM-bound: sizeof(T) bytes written per element).
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
@@ -27,11 +28,37 @@ namespace {
 constexpr int kNllThreads = 1024;
 constexpr int kNllBwdThreads = 256;
 
+// Per-row terms, one row per thread over every CU: v_n = -weight[t_n] input[n, t_n] and the
+// row's counted weight (0 for an ignored or out-of-range label), both exact in F32; out[n] = v_n
+// for reduction None. The gathers of input[n, t_n] land on a different 128 KB row each (C = 32000
+// F32): spread over the chip they cost ~5 us at 8192 rows, against ~34 us walked by one workgroup.
 template <typename T, typename I>
+__global__ void __launch_bounds__(kNllBwdThreads)
+nll_rows_kernel(const T* __restrict__ input, const I* __restrict__ target, const T* __restrict__ weight,
+                T* __restrict__ out, float* __restrict__ row_v, float* __restrict__ row_w, int64_t rows,
+                int64_t classes, int reduction, int64_t ignore) {
+    for (int64_t r = flat_begin(kNllBwdThreads); r < rows; r += flat_stride(kNllBwdThreads)) {
+        const int64_t t = static_cast<int64_t>(target[r]);
+        float v = 0.0f, wc = 0.0f;
+        if (t != ignore && t >= 0 && t < classes) {
+            const float wt = Elem<T>::load(weight, t);
+            v = -(wt * Elem<T>::load(input, r * classes + t));
+            wc = wt;
+        }
+        if (reduction == 0) Elem<T>::store(out, r, v);
+        row_v[r] = v;
+        row_w[r] = wc;
+    }
+}
+
+// The sums over rows, by one workgroup in a fixed order: thread x adds rows x, x + 1024, ... in
+// double, then the 1024 partial sums are combined by pairwise halving. The label check (a label
+// outside [0, C) that is not ignore_index) raises the flag the host reads.
+template <typename I>
 __global__ void __launch_bounds__(kNllThreads)
-nll_forward_kernel(const T* __restrict__ input, const I* __restrict__ target, const T* __restrict__ weight,
-                   T* __restrict__ out, T* __restrict__ total, int64_t rows, int64_t classes, int reduction,
-                   int64_t ignore, int* __restrict__ bad) {
+nll_reduce_kernel(const I* __restrict__ target, const float* __restrict__ row_v, const float* __restrict__ row_w,
+                  void* __restrict__ out, void* __restrict__ total, int out_dtype, int64_t rows, int64_t classes,
+                  int reduction, int64_t ignore, int* __restrict__ bad) {
     __shared__ double sl[kNllThreads], sw[kNllThreads];
     __shared__ int any_bad;
     if (threadIdx.x == 0) any_bad = 0;
@@ -39,18 +66,9 @@ nll_forward_kernel(const T* __restrict__ input, const I* __restrict__ target, co
     double l = 0.0, w = 0.0;
     for (int64_t r = threadIdx.x; r < rows; r += kNllThreads) {
         const int64_t t = static_cast<int64_t>(target[r]);
-        float v = 0.0f;
-        if (t != ignore) {
-            if (t < 0 || t >= classes) {
-                any_bad = 1;
-            } else {
-                const float wt = Elem<T>::load(weight, t);
-                v = -(wt * Elem<T>::load(input, r * classes + t));
-                w += static_cast<double>(wt);
-            }
-        }
-        if (reduction == 0) Elem<T>::store(out, r, v);
-        l += static_cast<double>(v);
+        if (t != ignore && (t < 0 || t >= classes)) any_bad = 1;
+        l += static_cast<double>(row_v[r]);
+        w += static_cast<double>(row_w[r]);
     }
     sl[threadIdx.x] = l;
     sw[threadIdx.x] = w;
@@ -64,9 +82,18 @@ nll_forward_kernel(const T* __restrict__ input, const I* __restrict__ target, co
     }
     if (threadIdx.x == 0) {
         const double W = sw[0];
-        if (reduction == 2) Elem<T>::store(out, 0, static_cast<float>(sl[0]));
-        else if (reduction == 1) Elem<T>::store(out, 0, static_cast<float>(sl[0] / W));
-        Elem<T>::store(total, 0, reduction == 0 ? 0.0f : static_cast<float>(W));
+        const float value = reduction == 2 ? static_cast<float>(sl[0]) : static_cast<float>(sl[0] / W);
+        const float tw = reduction == 0 ? 0.0f : static_cast<float>(W);
+        if (out_dtype == 0) {
+            if (reduction != 0) static_cast<float*>(out)[0] = value;
+            static_cast<float*>(total)[0] = tw;
+        } else if (out_dtype == 1) {
+            if (reduction != 0) static_cast<_Float16*>(out)[0] = static_cast<_Float16>(value);
+            static_cast<_Float16*>(total)[0] = static_cast<_Float16>(tw);
+        } else {
+            if (reduction != 0) static_cast<uint16_t*>(out)[0] = f32_to_bf16(value);
+            static_cast<uint16_t*>(total)[0] = f32_to_bf16(tw);
+        }
         *bad = any_bad;
     }
 }
@@ -90,12 +117,20 @@ nll_backward_kernel(const T* __restrict__ grad, const I* __restrict__ target, co
     }
 }
 
+// workspace: the flag (first 256 bytes), then the per-row terms row_v[rows] and row_w[rows] (F32)
 template <typename T, typename I>
-hipError_t nll_forward_t(const void* input, const void* target, const void* weight, void* out, void* total,
-                         int64_t rows, int64_t classes, int reduction, int64_t ignore, int* bad, hipStream_t s) {
-    hipLaunchKernelGGL((nll_forward_kernel<T, I>), dim3(1), dim3(kNllThreads), 0, s, static_cast<const T*>(input),
-                       static_cast<const I*>(target), static_cast<const T*>(weight), static_cast<T*>(out),
-                       static_cast<T*>(total), rows, classes, reduction, ignore, bad);
+hipError_t nll_forward_t(int dtype, const void* input, const void* target, const void* weight, void* out,
+                         void* total, int64_t rows, int64_t classes, int reduction, int64_t ignore, void* ws,
+                         hipStream_t s) {
+    int* bad = static_cast<int*>(ws);
+    float* row_v = reinterpret_cast<float*>(static_cast<char*>(ws) + 256);
+    float* row_w = row_v + rows;
+    if (rows > 0)
+        hipLaunchKernelGGL((nll_rows_kernel<T, I>), dim3(flat_blocks(rows, kNllBwdThreads)), dim3(kNllBwdThreads), 0, s,
+                           static_cast<const T*>(input), static_cast<const I*>(target), static_cast<const T*>(weight),
+                           static_cast<T*>(out), row_v, row_w, rows, classes, reduction, ignore);
+    hipLaunchKernelGGL((nll_reduce_kernel<I>), dim3(1), dim3(kNllThreads), 0, s, static_cast<const I*>(target), row_v,
+                       row_w, out, total, dtype, rows, classes, reduction, ignore, bad);
     return hipGetLastError();
 }
 
@@ -114,17 +149,19 @@ hipError_t nll_backward_t(const void* grad, const void* target, const void* weig
 }  // namespace
 
 // dtype: 0 F32, 1 F16, 2 BF16; id_bytes: 4 or 8.
+size_t nll_loss_workspace_bytes(int64_t rows) { return 256 + static_cast<size_t>(rows) * 2 * sizeof(float); }
+
 hipError_t nll_loss(int dtype, int id_bytes, const void* input, const void* target, const void* weight, void* out,
-                    void* total, int64_t rows, int64_t classes, int reduction, int64_t ignore, int* bad, hipStream_t s) {
+                    void* total, int64_t rows, int64_t classes, int reduction, int64_t ignore, void* ws, hipStream_t s) {
     const bool i64 = id_bytes == 8;
     if (dtype == 0)
-        return i64 ? nll_forward_t<float, int64_t>(input, target, weight, out, total, rows, classes, reduction, ignore, bad, s)
-                   : nll_forward_t<float, int32_t>(input, target, weight, out, total, rows, classes, reduction, ignore, bad, s);
+        return i64 ? nll_forward_t<float, int64_t>(dtype, input, target, weight, out, total, rows, classes, reduction, ignore, ws, s)
+                   : nll_forward_t<float, int32_t>(dtype, input, target, weight, out, total, rows, classes, reduction, ignore, ws, s);
     if (dtype == 1)
-        return i64 ? nll_forward_t<_Float16, int64_t>(input, target, weight, out, total, rows, classes, reduction, ignore, bad, s)
-                   : nll_forward_t<_Float16, int32_t>(input, target, weight, out, total, rows, classes, reduction, ignore, bad, s);
-    return i64 ? nll_forward_t<uint16_t, int64_t>(input, target, weight, out, total, rows, classes, reduction, ignore, bad, s)
-               : nll_forward_t<uint16_t, int32_t>(input, target, weight, out, total, rows, classes, reduction, ignore, bad, s);
+        return i64 ? nll_forward_t<_Float16, int64_t>(dtype, input, target, weight, out, total, rows, classes, reduction, ignore, ws, s)
+                   : nll_forward_t<_Float16, int32_t>(dtype, input, target, weight, out, total, rows, classes, reduction, ignore, ws, s);
+    return i64 ? nll_forward_t<uint16_t, int64_t>(dtype, input, target, weight, out, total, rows, classes, reduction, ignore, ws, s)
+               : nll_forward_t<uint16_t, int32_t>(dtype, input, target, weight, out, total, rows, classes, reduction, ignore, ws, s);
 }
 
 hipError_t nll_loss_backward(int dtype, int id_bytes, const void* grad, const void* target, const void* weight,
