@@ -327,17 +327,21 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, const f32x16_t (&a
     }
 }
 
-template <int BM, int BN, bool OUT_BF16>
+// NS LDS stages in a ring: step kt reads stage kt % NS while the loads of steps kt+1 .. kt+NS-1 are
+// in flight. A grid of at most one 64x64 tile per CU (C1's 128 tiles, 1024^3's 256) is bound by
+// that pipeline's depth: each tile walks K in 32-deep steps, each waiting for its loads, so it
+// keeps 8 stages (7 steps in flight, 64 KB of LDS); measured back to back on MI355X that takes
+// 512x1024x1024 from 6.03 to 5.80 us and 1024^3 from 6.44 to 6.15 us. Fuller grids keep 4 (with
+// 8, 512x4096x4096's 512 tiles went from 32.2 to 32.8 us).
+template <int BM, int BN, bool OUT_BF16, int NS>
 __global__ void __launch_bounds__(kThreads, (BM >= 256 ? 1 : 2))
 gemm_nt_dma_kernel(GemmArgs p) {
     constexpr int TI = BM / 64;
     constexpr int TJ = BN / 64;
     constexpr int kStage = (BM + BN) * kSBK;        // elements per stage
     constexpr int kPerWave = (BM + BN) / 16 / 4;    // 1 KB (16-row) load instructions per wave per step
-    __shared__ __attribute__((aligned(1024))) uint16_t stage0[kStage];
-    __shared__ __attribute__((aligned(1024))) uint16_t stage1[kStage];
-    __shared__ __attribute__((aligned(1024))) uint16_t stage2[kStage];
-    __shared__ __attribute__((aligned(1024))) uint16_t stage3[kStage];
+    static_assert(NS >= 4, "the barrier's wait count assumes NS - 3 whole steps in flight");
+    __shared__ __attribute__((aligned(1024))) uint16_t stages[NS][kStage];
 
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -389,41 +393,40 @@ gemm_nt_dma_kernel(GemmArgs p) {
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
     // Step kt multiplies stage X; its first fragments arrive in fa. Its two phases also issue
-    // the loads of step kt+3 into stage Z, freed by the barrier of step kt-1. Between them the
-    // workgroup waits for step kt+1 to land in stage Y (the loads of step kt+2 and the first
-    // half of step kt+3 stay in flight) and meets at the barrier, and Y's first fragments are
-    // read while X's last MFMAs run. Every step issues its loads, so the wait counts are the same for all steps:
-    // past the last step the loads repeat step nk-1 into stages that are no longer read.
+    // the loads of step kt+NS-1 into stage Z, freed by the barrier of step kt-1. Between them the
+    // workgroup waits for step kt+1 to land in stage Y (the loads of steps kt+2 .. kt+NS-2 and the
+    // first half of step kt+NS-1 stay in flight) and meets at the barrier, and Y's first fragments
+    // are read while X's last MFMAs run. Every step issues its loads, so the wait counts are the
+    // same for all steps: past the last step the loads repeat step nk-1 into stages that are no
+    // longer read.
     const int nk = p.k / kSBK;
     const int last = nk - 1;
     Frags<BM, BN> fa, fb;
     auto step = [&](const uint16_t* X, const uint16_t* Y, uint16_t* Z, int kt) {
-        const int ahead = kt + 3 < nk ? kt + 3 : last;
-        // the loads of step kt+3 are split over both phases (stage Z stays free until step
-        // kt+3 reads it); at the barrier the second half is still in flight
+        const int ahead = kt + NS - 1 < nk ? kt + NS - 1 : last;
+        // the loads of step kt+NS-1 are split over both phases (stage Z stays free until that
+        // step reads it); at the barrier the second half is still in flight
         constexpr int P0 = (kPerWave + 1) / 2, P1 = kPerWave - P0;
         mma_phase<BM, BN, P0>(
             fa, acc, [&](int r) { read_frag<BM, BN>(X, 1, r, wm, wn, lr, lk, fb); },
             [&](int d) { fetch_one(Z, ahead, d); });
-        if (kt + 1 < nk) stage_barrier<kPerWave + P0>();
+        if (kt + 1 < nk) stage_barrier<(NS - 3) * kPerWave + P0>();
         // after the last step these reads fetch fragments that are never used
         mma_phase<BM, BN, P1>(
             fb, acc, [&](int r) { read_frag<BM, BN>(Y, 0, r, wm, wn, lr, lk, fa); },
             [&](int d) { fetch_one(Z, ahead, P0 + d); });
     };
 
-    fetch(stage0, 0);
-    fetch(stage1, nk > 1 ? 1 : last);
-    fetch(stage2, nk > 2 ? 2 : last);
-    stage_barrier<2 * kPerWave>();
-    read_frags<BM, BN>(stage0, 0, wm, wn, lr, lk, fa);
+#pragma unroll
+    for (int u = 0; u < NS - 1; ++u) fetch(stages[u], nk > u ? u : last);
+    stage_barrier<(NS - 2) * kPerWave>();
+    read_frags<BM, BN>(stages[0], 0, wm, wn, lr, lk, fa);
     int kt = 0;
     do {  // nk >= 1: the accumulators never bypass the MFMAs on their way to the epilogue
-        step(stage0, stage1, stage3, kt);
-        if (kt + 1 < nk) step(stage1, stage2, stage0, kt + 1);
-        if (kt + 2 < nk) step(stage2, stage3, stage1, kt + 2);
-        if (kt + 3 < nk) step(stage3, stage0, stage2, kt + 3);
-        kt += 4;
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+            if (u == 0 || kt + u < nk) step(stages[u], stages[(u + 1) % NS], stages[(u + NS - 1) % NS], kt + u);
+        kt += NS;
     } while (kt < nk);
     // the trailing loads must land before the workgroup ends and its LDS is handed on
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -523,10 +526,15 @@ void launch_nt(const GemmArgs& a, int64_t batch, bool out_bf16, int num_cus, hip
     if (whole_steps && p.k % kPK == 0 && BM == kPPTile && BN == kPPTile) {
         if (out_bf16) launch_pp<true>(p, batch, false, false, num_cus, s);
         else launch_pp<false>(p, batch, false, false, num_cus, s);
+    } else if (whole_steps && BM == 64 && grid.x * grid.z <= static_cast<unsigned>(num_cus)) {
+        if constexpr (BM == 64) {
+            if (out_bf16) hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true, 8>), grid, dim3(kThreads), 0, s, p);
+            else hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, false, 8>), grid, dim3(kThreads), 0, s, p);
+        }
     } else if (whole_steps && out_bf16)
-        hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, true, 4>), grid, dim3(kThreads), 0, s, p);
     else if (whole_steps)
-        hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, false>), grid, dim3(kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemm_nt_dma_kernel<BM, BN, false, 4>), grid, dim3(kThreads), 0, s, p);
     else if (out_bf16)
         hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, true>), grid, dim3(kThreads), 0, s, p);
     else
