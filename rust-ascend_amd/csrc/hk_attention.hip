@@ -31,6 +31,8 @@
 #include <type_traits>
 
 #include "hk_common.hpp"
+
+#include <cstdlib>
 #include "hk_kernels.hpp"
 
 namespace hk {
@@ -841,7 +843,20 @@ struct BwdArgs {
     int causal;
     int dq_bf16, dkv_bf16;
     int blocks;  // key blocks (dK/dV kernel) or query blocks (dQ kernel) per head
+    // dS (BF16, unscaled) in 4 KB blocks of 32 keys x 64 queries, block (bh, key/32, query/64)
+    // at ((bh * nkb + key/32) * nsq + query/64) * 4096 bytes: written by the dK/dV kernel when
+    // set, read by attn_bwd_dq_ds. Blocks whose pairs no query sees are left unwritten.
+    uint16_t* ds;
+    int64_t nkb, nsq;  // ceil(N / 32), ceil(M / 64)
 };
+
+// Layout inside a dS block: four 1 KB chunks c = 2 qt + h, each holding 64 lanes x 16 bytes as
+// the dK/dV kernel's wave has them (pack_bf16x8 of its dS accumulators): lane L (key L % 32,
+// k-group L / 32) holds queries 32 qt + 16 h + 8 (e / 4) + 4 (L / 32) + e % 4, e = 0..7, of its
+// key. Lane L's 16 bytes sit at slot L ^ 4 (L / 32) ^ 8 (c % 2) of the chunk, so that the dQ
+// kernel's transposing reads (32 lanes: four keys x two k-groups x two chunks, 8 bytes each)
+// fall on 32 distinct 8-byte bank slots.
+__device__ __forceinline__ int ds_slot(int lane, int c) { return lane ^ ((lane >> 5) << 2) ^ ((c & 1) << 3); }
 
 // A [64][DP] tile (tile_off<DP> swizzle) of rows row0 .. row0+63 of a row-major [*, D] BF16
 // matrix, filled through the global->LDS path: DP / 8 instructions of 1 KB, instruction q
@@ -1038,6 +1053,8 @@ attn_bwd_dkdv(BwdArgs a) {
         const uint16_t* Qt = tiles[cur][0];
         const uint16_t* Ot = tiles[cur][1];
         const bool skip = a.causal && (n0w > q0 + kQStep - 1 + a.diag);
+        const int64_t bh_cur = b * a.heads + kvh * group + it / nsteps_head;
+        const bool stores = a.ds && n0w < a.n;  // this wave's dS block exists
         // Steps whose 64 queries all see this wave's 32 keys (the common case) run a copy of the
         // step without the mask arithmetic; the others test one 32-bit offset per element:
         // query q0 + qq sees my_key iff qq + rel >= 0 (causal), qq < qlim and my_key < n.
@@ -1101,6 +1118,18 @@ attn_bwd_dkdv(BwdArgs a) {
                     else dv[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, pb[ks], dv[dt], 0, 0, 0);
                 };
             };
+            // dS of query tile qt (BF16, unscaled: the B operand of dK) into its block for the dQ
+            // kernel: chunks 2 qt and 2 qt + 1, 1 KB each, two 16-byte stores per lane. Pairs past
+            // N or M hold zeros (P is zero there), so the whole block is written. Non-temporal
+            // stores: 2 GB of dS at C4 would otherwise push the shared Q / dO tiles out of L2.
+            auto store_ds = [&](int qt) __attribute__((always_inline)) {
+                char* blk = reinterpret_cast<char*>(a.ds) + ((bh_cur * a.nkb + n0w / 32) * a.nsq + q0 / kQStep) * 4096;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int c = 2 * qt + h;
+                    stream_store(__builtin_bit_cast(u32x4_t, sb[c]), reinterpret_cast<u32x4_t*>(blk + c * 1024 + ds_slot(lane, c) * 16));
+                }
+            };
             // the 16 scores of a tile spread evenly over the ring's MFMAs (16 of them for D = 128)
             static_assert(16 % (2 * KS) == 0 && 16 % (4 * DT) == 0, "scores per MFMA");
             mfma_ring<2 * KS>(sdp(0), sdp_mma(0));
@@ -1121,12 +1150,21 @@ attn_bwd_dkdv(BwdArgs a) {
             sb[2] = pack_bf16x8(dp[1], 0);
             sb[3] = pack_bf16x8(dp[1], 8);
             mfma_ring<4 * DT>(dkv(1), dkv_mma(1));
+            if (stores) {
+                // after the step's last MFMA and the wait for step it+1's loads: the stores go into
+                // an empty memory queue instead of stalling behind those loads mid-step
+                landed();
+                store_ds(0);
+                store_ds(1);
+            }
         };
         if (!skip) {
             if (full) step(std::integral_constant<bool, true>{});
             else step(std::integral_constant<bool, false>{});
         }
-        landed();
+        // a step that stored dS has waited for its loads before the stores, which complete
+        // within the next step (whose own wait covers them)
+        if (!stores || skip) landed();
         lds_barrier();
     }
 
@@ -1320,10 +1358,180 @@ attn_bwd_dq(BwdArgs a) {
     }
 }
 
+// dQ of 128 queries of one (batch, head) from the dS blocks that attn_bwd_dkdv stored: one
+// GEMM, dQ^T += K^T dS^T over 64-key tiles up to the diagonal, with no S or dP recomputed. A
+// tile's dS is four blocks (two of 32 keys x two of 64 queries, 16 KB) copied verbatim into LDS;
+// the B operand (this lane's query, 8 keys) comes from them through transposing reads (each lane
+// reads 4 consecutive queries of one key, 8 contiguous bytes of a block), and K^T from the
+// row-major K tile as in attn_bwd_dq, with the same key order inside each MFMA k-group on both
+// sides. The K tile and dS blocks of step j+1 are fetched straight into LDS while step j is
+// computed. Blocks that no query sees may never have been written: on tiles that hold such pairs
+// the operand is masked (the causal test of attn_bwd_dkdv), so stale memory never reaches an
+// MFMA; blocks past this head's read as zero. Queries past M feed only dQ^T columns that are not
+// stored.
+template <int D>
+__global__ void __launch_bounds__(kThreads, 2)
+attn_bwd_dq_ds(BwdArgs a) {
+    constexpr int DP = D < 32 ? 32 : D;
+    constexpr int DT = DP / 32;
+    using TDma = SwzTileDma<D, DP>;
+    __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][kBlockN * DP];
+    __shared__ __attribute__((aligned(1024))) uint16_t ds_lds[2][4 * 2048];  // 4 blocks of 4 KB
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lq = lane & 31, lg = lane >> 5;
+    // the order of attn_bwd_dq: KV head group, query block heaviest first, query head in the group
+    const int logical = xcd_logical();
+    const int group_heads = static_cast<int>(a.heads / a.kv_heads);
+    const int per_group = a.blocks * group_heads;
+    const int grp = logical / per_group, in_grp = logical % per_group;
+    const int mb = a.blocks - 1 - in_grp / group_heads;
+    const int64_t b = grp / a.kv_heads, kvh = grp % a.kv_heads;
+    const int64_t h = kvh * group_heads + in_grp % group_heads;
+    const int64_t bh = b * a.heads + h;
+    const uint16_t* K = a.k + ((b * a.kv_heads + kvh) * a.n) * D;
+    const int64_t q0 = static_cast<int64_t>(mb) * kBlockM;
+    const int64_t q0w = q0 + wave * 32;
+    const int64_t my_q = q0w + lq;
+
+    f32x16_t dq[DT];
+#pragma unroll
+    for (int i = 0; i < DT; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dq[i][v] = 0.0f;
+        asm volatile("" : "+a"(dq[i]));
+    }
+
+    int64_t kv_end = a.n;
+    if (a.causal) {
+        const int64_t last = q0 + kBlockM - 1 + a.diag;
+        kv_end = last + 1 < kv_end ? last + 1 : kv_end;
+    }
+    const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
+
+    const int tile_voff = TDma::lane_offset(wave, lane);
+    const int n32 = static_cast<int>(a.n);  // the launcher keeps n * D * 2 below 2^31
+    const int nsq = static_cast<int>(a.nsq);
+    const i32x4_t rk = buffer_resource(K, n32 * D * 2);
+    // this head's blocks (the launcher keeps nkb * nsq * 4096 below 2^31)
+    const i32x4_t rds = buffer_resource(reinterpret_cast<const char*>(a.ds) + bh * a.nkb * a.nsq * 4096,
+                                        static_cast<int>(a.nkb * a.nsq * 4096));
+    // DMA instruction q = wave + 4 i of the 16: block q / 4 = 2 (key half) + query half, chunk q % 4
+    auto issue_tile = [&](int j, int buf) {
+        TDma::issue(rk, lds_address(k_lds[buf]), j * kBlockN, tile_voff, wave);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = wave + 4 * i, blk = q >> 2;
+            const int src = ((2 * j + (blk >> 1)) * nsq + 2 * mb + (blk & 1)) * 4096 + (q & 3) * 1024;
+            load_lds16_nt(rds, lds_address(ds_lds[buf]) + 1024 * q, src + 16 * lane, 0);
+        }
+    };
+    // B operand reads: lane (lg, g = lane/16 % 2, i = lane % 16) reads key kbase + i/4 of its
+    // transposing group, queries 32 wave + 16 g + 4 (i % 4) .. +3: block (key / 32, wave / 2),
+    // chunk 2 (wave % 2) + g, k-group lane (key % 32) + 32 (i % 2), element 4 ((i % 4) / 2).
+    const int tg = (lane >> 4) & 1, ti = lane & 15;
+    const int chunk = 2 * (wave & 1) + tg;
+    auto ds_read = [&](const uint16_t* St, int kbase) __attribute__((always_inline)) {
+        const int kk = kbase + (ti >> 2);
+        const int L = (kk & 31) + 32 * (ti & 1);
+        const int byte = (2 * (kk >> 5) + (wave >> 1)) * 4096 + chunk * 1024 + ds_slot(L, chunk) * 16 + 8 * ((ti & 3) >> 1);
+        return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(reinterpret_cast<const char*>(St) + byte));
+    };
+    auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+    if (ntiles > 0) issue_tile(0, 0);
+    landed();
+    lds_barrier();
+
+    for (int j = 0; j < ntiles; ++j) {
+        const int cur = j & 1;
+        if (j + 1 < ntiles) issue_tile(j + 1, cur ^ 1);
+        const int64_t kv0 = static_cast<int64_t>(j) * kBlockN;
+        const uint16_t* Kt = k_lds[cur];
+        const uint16_t* St = ds_lds[cur];
+        const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
+        // every key of the tile visible to every query of the wave, and below N
+        const bool full = (!a.causal || kv0 + kBlockN - 1 <= q0w + a.diag) && kv0 + kBlockN <= a.n;
+        if (!skip) {
+            int64_t rel64 = my_q + a.diag - kv0;
+            rel64 = rel64 < -(int64_t{1} << 30) ? -(int64_t{1} << 30) : (rel64 > (int64_t{1} << 30) ? (int64_t{1} << 30) : rel64);
+            const int rel = a.causal ? static_cast<int>(rel64) : (1 << 30);
+            const int klim = static_cast<int>(a.n - kv0 < kBlockN ? a.n - kv0 : kBlockN);
+            // B operands of the four 16-key slices: keys 16 ks + 4 lg + {0..3, 8..11}
+            bf16x8_t sb[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int kb0 = 16 * ks + 4 * lg;
+                const v4i16_t lo = ds_read(St, kb0), hi = ds_read(St, kb0 + 8);
+                typedef short v8i16_t __attribute__((ext_vector_type(8)));
+                v8i16_t e = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                if (!full) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int kk = kb0 + (u < 4 ? u : u + 4);
+                        e[u] = kk <= rel && kk < klim ? e[u] : static_cast<short>(0);
+                    }
+                }
+                sb[ks] = __builtin_bit_cast(bf16x8_t, e);
+            }
+            mfma_ring<4 * DT>(
+                [&](int i) {
+                    const int kb0 = 16 * (i / DT) + 4 * lg;
+                    return tile_read_tr<DP>(Kt, lane, kb0, kb0 + 8, 32 * (i % DT));
+                },
+                [&](int i, bf16x8_t x) {
+                    const int dt = i % DT;
+                    dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[i / DT], dq[dt], 0, 0, 0);
+                });
+        }
+        landed();
+        lds_barrier();
+    }
+
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dq[dt][v] *= a.scale;
+    if (my_q < a.m) {
+        const int64_t row = static_cast<int64_t>(bh) * a.m + my_q;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float v4[4] = {dq[dt][4 * g4], dq[dt][4 * g4 + 1], dq[dt][4 * g4 + 2], dq[dt][4 * g4 + 3]};
+                store_row4<D>(a.dq, a.dq_bf16, row, 32 * dt + 8 * g4 + 4 * lg, v4);
+            }
+    }
+}
+
+// The stored-dS backward (attn_bwd_dkdv writing dS blocks, attn_bwd_dq_ds reading them) applies
+// when a head's blocks have 32-bit byte offsets and all of them fit the dS budget: 8 GiB, or the
+// byte count in the environment variable HK_ATTN_DS_BUDGET (read on every call; 0 turns the path
+// off). Otherwise attn_bwd_dq recomputes S and dP, with no workspace beyond the row statistics.
+int64_t ds_budget() {
+    const char* env = std::getenv("HK_ATTN_DS_BUDGET");
+    if (env == nullptr || *env == '\0') return int64_t{8} << 30;
+    char* end = nullptr;
+    const long long v = std::strtoll(env, &end, 10);
+    return end != nullptr && *end == '\0' && v >= 0 ? static_cast<int64_t>(v) : int64_t{8} << 30;
+}
+int64_t ds_head_bytes(const AttnShape& sh) { return ((sh.n + 31) / 32) * ((sh.m + kQStep - 1) / kQStep) * 4096; }
+bool bwd_stores_ds(const AttnShape& sh) {
+    // the dQ kernel's block offsets reach two key blocks past the last
+    const int64_t reach = ds_head_bytes(sh) + 2 * ((sh.m + kQStep - 1) / kQStep) * 4096;
+    return reach < (int64_t{1} << 31) && sh.batch * sh.heads * ds_head_bytes(sh) <= ds_budget();
+}
+size_t ds_bytes(const AttnShape& sh) {
+    return sh.store_ds ? static_cast<size_t>(sh.batch * sh.heads * ds_head_bytes(sh)) : 0;
+}
+size_t stat_bytes(const AttnShape& sh) {  // row statistic and lse2, rounded to 256 bytes
+    return (2 * static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float) + 255) & ~size_t(255);
+}
+
 template <int D>
 hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv, int dkv_bf16,
-                      float* stat, hipStream_t s) {
+                      float* stat, uint16_t* ds, hipStream_t s) {
     const int64_t rows = sh.batch * sh.heads * sh.m;
     constexpr int lanes = D / 8;
     const int64_t threads = rows * lanes;
@@ -1355,11 +1563,18 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
     a.dq_bf16 = dq_bf16;
     a.dkv_bf16 = dkv_bf16;
     a.blocks = static_cast<int>((sh.n + kKBlock - 1) / kKBlock);
+    a.ds = ds;
+    a.nkb = (sh.n + 31) / 32;
+    a.nsq = (sh.m + kQStep - 1) / kQStep;
     hipLaunchKernelGGL((attn_bwd_dkdv<D>), dim3(static_cast<unsigned>(sh.batch * sh.kv_heads * a.blocks)),
                        dim3(kThreads), 0, s, a);
     a.blocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
-    hipLaunchKernelGGL((attn_bwd_dq<D>), dim3(static_cast<unsigned>(sh.batch * sh.heads * a.blocks)), dim3(kThreads),
-                       0, s, a);
+    if (ds)
+        hipLaunchKernelGGL((attn_bwd_dq_ds<D>), dim3(static_cast<unsigned>(sh.batch * sh.heads * a.blocks)),
+                           dim3(kThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_bwd_dq<D>), dim3(static_cast<unsigned>(sh.batch * sh.heads * a.blocks)),
+                           dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1376,9 +1591,9 @@ bool attention_shape_fits(const AttnShape& sh) {
     return fwd < kItemLimit && dkdv < kItemLimit && dq < kItemLimit;
 }
 
-size_t attention_bwd_workspace_bytes(const AttnShape& sh) {
-    return 2 * static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float);  // row statistic, lse2
-}
+void attention_bwd_plan(AttnShape& sh) { sh.store_ds = bwd_stores_ds(sh) ? 1 : 0; }
+
+size_t attention_bwd_workspace_bytes(const AttnShape& sh) { return stat_bytes(sh) + ds_bytes(sh); }
 
 hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o, float* lse,
                              hipStream_t s) {
@@ -1395,11 +1610,12 @@ hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k,
                               const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv,
                               int dkv_bf16, void* workspace, hipStream_t s) {
     float* stat = static_cast<float*>(workspace);
+    uint16_t* ds = sh.store_ds ? reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + stat_bytes(sh)) : nullptr;
     switch (sh.d) {
-        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
-        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
-        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
-        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, s);
+        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
+        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
+        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
+        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -249,6 +249,14 @@ __device__ __forceinline__ void load_lds16(i32x4_t rsrc, uint32_t lds, int voff,
                  : "memory");
 }
 
+// load_lds16 for data read once: the non-temporal hint lets the line leave the caches first.
+__device__ __forceinline__ void load_lds16_nt(i32x4_t rsrc, uint32_t lds, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen nt lds"
+                 :
+                 : "v"(voff), "s"(lds), "s"(rsrc), "s"(soff)
+                 : "memory");
+}
+
 // The 4-byte form: lane l's dword lands at lds + 4 * l (one instruction moves 256 bytes).
 __device__ __forceinline__ void load_lds4(i32x4_t rsrc, uint32_t lds, int voff, int soff) {
     asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, %3 offen lds"

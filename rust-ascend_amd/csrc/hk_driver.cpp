@@ -2356,6 +2356,7 @@ hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tens
         return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must be F32 or BF16 (dK and dV alike)");
     if (!disjoint({dq, dk, dv}, {q, k, v, o, lse, dout})) return HK_INVALID_ARGUMENT;
     sh.o_f32 = o->dtype == HK_F32;
+    hk::attention_bwd_plan(sh);
     Staged sq = staged(q), sk = staged(k), sv = staged(v), sd = staged(dout);
     const size_t stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
     OpGuard g(h);

@@ -179,10 +179,26 @@ def test_backward_causal_closed_form(golden, n, cached):
     assert float(torch.max(torch.abs(dq))) < 1e-6 and float(torch.max(torch.abs(dk))) < 1e-6
 
 
+# The backward's two dQ forms: dS stored by the dK/dV kernel and read by a one-GEMM dQ kernel
+# (the default), or S and dP recomputed by the dQ kernel (taken when the dS buffer would exceed
+# HK_ATTN_DS_BUDGET bytes; a budget of 0 forces it).
+DQ_FORMS = {"stored_ds": None, "recompute": "0"}
+
+
+@pytest.fixture(params=sorted(DQ_FORMS))
+def dq_form(request, monkeypatch):
+    budget = DQ_FORMS[request.param]
+    if budget is None:
+        monkeypatch.delenv("HK_ATTN_DS_BUDGET", raising=False)
+    else:
+        monkeypatch.setenv("HK_ATTN_DS_BUDGET", budget)
+    return request.param
+
+
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("m,n", [(256, 256), (200, 328), (64, 1000), (130, 130)])
-def test_backward_random_vs_oracle(d, causal, m, n):
+def test_backward_random_vs_oracle(d, causal, m, n, dq_form):
     h, hkv = 4, 2
     q_t, q = randn_bf16((2, h, m, d), seed=d + m + 7)
     k_t, k = randn_bf16((2, hkv, n, d), seed=d + n + 8)
@@ -202,7 +218,7 @@ def test_backward_random_vs_oracle(d, causal, m, n):
     rows_ok(host(dv), ref["dv"], 1e-2, "dv rows")
 
 
-def test_backward_bf16_grads_and_determinism():
+def test_backward_bf16_grads_and_determinism(dq_form):
     q_t, q = randn_bf16((1, 8, 192, 128), seed=51)
     k_t, k = randn_bf16((1, 2, 192, 128), seed=52)
     v_t, v = randn_bf16((1, 2, 192, 128), seed=53)
@@ -217,7 +233,7 @@ def test_backward_bf16_grads_and_determinism():
         mag_ok(host(got), ref[name], ref[name + "_mag"], 1e-2, name)
 
 
-def test_backward_c4_full_size_sampled():
+def test_backward_c4_full_size_sampled(dq_form):
     """BASELINE config C4 backward: B4, S4096, Hq32/Hkv8, D128, causal; parity on batch 0 x KV
     group 0 and batch 3 x KV group 7 (the 4 query heads that share the KV head) over all rows, by
     the magnitude check and the per-row normwise check (dQ's on rows that see at least 128 keys)."""
