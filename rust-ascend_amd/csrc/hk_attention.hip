@@ -844,8 +844,9 @@ struct BwdArgs {
     int dq_bf16, dkv_bf16;
     int blocks;  // key blocks (dK/dV kernel) or query blocks (dQ kernel) per head
     // dS (BF16, unscaled) in 4 KB blocks of 32 keys x 64 queries, block (bh, key/32, query/64)
-    // at ((bh * nkb + key/32) * nsq + query/64) * 4096 bytes: written by the dK/dV kernel when
-    // set, read by attn_bwd_dq_ds. Blocks whose pairs no query sees are left unwritten.
+    // at ((bh * nsq + query/64) * nkb + key/32) * 4096 bytes (a 64-query row of blocks is
+    // contiguous, in the order the dQ kernel reads it): written by the dK/dV kernel when set,
+    // read by attn_bwd_dq_ds. Blocks whose pairs no query sees are left unwritten.
     uint16_t* ds;
     int64_t nkb, nsq;  // ceil(N / 32), ceil(M / 64)
 };
@@ -1123,7 +1124,7 @@ attn_bwd_dkdv(BwdArgs a) {
             // N or M hold zeros (P is zero there), so the whole block is written. Non-temporal
             // stores: 2 GB of dS at C4 would otherwise push the shared Q / dO tiles out of L2.
             auto store_ds = [&](int qt) __attribute__((always_inline)) {
-                char* blk = reinterpret_cast<char*>(a.ds) + ((bh_cur * a.nkb + n0w / 32) * a.nsq + q0 / kQStep) * 4096;
+                char* blk = reinterpret_cast<char*>(a.ds) + ((bh_cur * a.nsq + q0 / kQStep) * a.nkb + n0w / 32) * 4096;
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int c = 2 * qt + h;
@@ -1364,19 +1365,22 @@ attn_bwd_dq(BwdArgs a) {
 // the B operand (this lane's query, 8 keys) comes from them through transposing reads (each lane
 // reads 4 consecutive queries of one key, 8 contiguous bytes of a block), and K^T from the
 // row-major K tile as in attn_bwd_dq, with the same key order inside each MFMA k-group on both
-// sides. The K tile and dS blocks of step j+1 are fetched straight into LDS while step j is
-// computed. Blocks that no query sees may never have been written: on tiles that hold such pairs
+// sides. The dS blocks go straight into LDS two tiles ahead (three buffers), the K tile one
+// tile ahead (two), and two workgroups share a CU. Blocks that no query sees may never have been written: on tiles that hold such pairs
 // the operand is masked (the causal test of attn_bwd_dkdv), so stale memory never reaches an
 // MFMA; blocks past this head's read as zero. Queries past M feed only dQ^T columns that are not
-// stored.
+// stored. Keys past N in a block that exists (the next query row's first blocks) are masked too.
 template <int D>
 __global__ void __launch_bounds__(kThreads, 2)
 attn_bwd_dq_ds(BwdArgs a) {
     constexpr int DP = D < 32 ? 32 : D;
     constexpr int DT = DP / 32;
     using TDma = SwzTileDma<D, DP>;
+    // dS (from HBM) runs two tiles ahead through three buffers, K (from L2) one tile ahead
+    // through two: 80 KB at D = 128, two workgroups per CU
     __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][kBlockN * DP];
-    __shared__ __attribute__((aligned(1024))) uint16_t ds_lds[2][4 * 2048];  // 4 blocks of 4 KB
+    __shared__ __attribute__((aligned(1024))) uint16_t ds_lds[3][4 * 2048];  // 4 blocks of 4 KB
+    constexpr int kDsInstr = 4;  // global->LDS instructions per wave per dS tile
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1412,18 +1416,18 @@ attn_bwd_dq_ds(BwdArgs a) {
 
     const int tile_voff = TDma::lane_offset(wave, lane);
     const int n32 = static_cast<int>(a.n);  // the launcher keeps n * D * 2 below 2^31
-    const int nsq = static_cast<int>(a.nsq);
+    const int nkb = static_cast<int>(a.nkb);
     const i32x4_t rk = buffer_resource(K, n32 * D * 2);
     // this head's blocks (the launcher keeps nkb * nsq * 4096 below 2^31)
     const i32x4_t rds = buffer_resource(reinterpret_cast<const char*>(a.ds) + bh * a.nkb * a.nsq * 4096,
                                         static_cast<int>(a.nkb * a.nsq * 4096));
     // DMA instruction q = wave + 4 i of the 16: block q / 4 = 2 (key half) + query half, chunk q % 4
-    auto issue_tile = [&](int j, int buf) {
-        TDma::issue(rk, lds_address(k_lds[buf]), j * kBlockN, tile_voff, wave);
+    auto issue_k = [&](int j, int buf) { TDma::issue(rk, lds_address(k_lds[buf]), j * kBlockN, tile_voff, wave); };
+    auto issue_ds = [&](int j, int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int q = wave + 4 * i, blk = q >> 2;
-            const int src = ((2 * j + (blk >> 1)) * nsq + 2 * mb + (blk & 1)) * 4096 + (q & 3) * 1024;
+            const int src = ((2 * mb + (blk & 1)) * nkb + 2 * j + (blk >> 1)) * 4096 + (q & 3) * 1024;
             load_lds16_nt(rds, lds_address(ds_lds[buf]) + 1024 * q, src + 16 * lane, 0);
         }
     };
@@ -1438,16 +1442,30 @@ attn_bwd_dq_ds(BwdArgs a) {
         const int byte = (2 * (kk >> 5) + (wave >> 1)) * 4096 + chunk * 1024 + ds_slot(L, chunk) * 16 + 8 * ((ti & 3) >> 1);
         return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(reinterpret_cast<const char*>(St) + byte));
     };
+    // Loads complete in issue order: when the last loads issued are dS tile t's, vmcnt(kDsInstr)
+    // means everything issued before them has landed.
     auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
-    if (ntiles > 0) issue_tile(0, 0);
-    landed();
+    auto landed_but_ds = [&]() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDsInstr) : "memory"); };
+    if (ntiles > 0) {
+        issue_k(0, 0);
+        issue_ds(0, 0);
+    }
+    if (ntiles > 1) {
+        issue_ds(1, 1);
+        landed_but_ds();
+    } else {
+        landed();
+    }
     lds_barrier();
 
+    int cur = 0;  // dS buffer of tile j (j % 3); K's is j % 2
     for (int j = 0; j < ntiles; ++j) {
-        const int cur = j & 1;
-        if (j + 1 < ntiles) issue_tile(j + 1, cur ^ 1);
+        // K buffer (j+1) % 2 and dS buffer (j+2) % 3 were last read in step j-1, which the
+        // previous barrier closed
+        if (j + 1 < ntiles) issue_k(j + 1, (j + 1) & 1);
+        if (j + 2 < ntiles) issue_ds(j + 2, cur == 0 ? 2 : cur - 1);
         const int64_t kv0 = static_cast<int64_t>(j) * kBlockN;
-        const uint16_t* Kt = k_lds[cur];
+        const uint16_t* Kt = k_lds[j & 1];
         const uint16_t* St = ds_lds[cur];
         const bool skip = a.causal && (kv0 > q0w + 31 + a.diag);
         // every key of the tile visible to every query of the wave, and below N
@@ -1484,8 +1502,11 @@ attn_bwd_dq_ds(BwdArgs a) {
                     dq[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, sb[i / DT], dq[dt], 0, 0, 0);
                 });
         }
-        landed();
+        // K and dS of tile j+1 must have landed; dS tile j+2's loads may stay in flight
+        if (j + 2 < ntiles) landed_but_ds();
+        else landed();
         lds_barrier();
+        cur = cur == 2 ? 0 : cur + 1;
     }
 
 #pragma unroll
@@ -1517,8 +1538,8 @@ int64_t ds_budget() {
 }
 int64_t ds_head_bytes(const AttnShape& sh) { return ((sh.n + 31) / 32) * ((sh.m + kQStep - 1) / kQStep) * 4096; }
 bool bwd_stores_ds(const AttnShape& sh) {
-    // the dQ kernel's block offsets reach two key blocks past the last
-    const int64_t reach = ds_head_bytes(sh) + 2 * ((sh.m + kQStep - 1) / kQStep) * 4096;
+    // the dQ kernel's block offsets reach one query row of blocks past the last
+    const int64_t reach = ds_head_bytes(sh) + ((sh.n + 31) / 32 + 2) * 4096;
     return reach < (int64_t{1} << 31) && sh.batch * sh.heads * ds_head_bytes(sh) <= ds_budget();
 }
 size_t ds_bytes(const AttnShape& sh) {
