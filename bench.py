@@ -744,7 +744,7 @@ def main():
             sec.append({"workload": "C4 causal GQA attention fwd B4 S4096 Hq32 Hkv8 D128", "value": round(ff / f_ms / 1e9, 2),
                         "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd_pp", "attn_fwd")})
             sec.append({"workload": "C4 causal GQA attention bwd B4 S4096 Hq32 Hkv8 D128", "value": round(bf / b_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq", "attn_bwd")})
+                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq_ds", "attn_bwd")})
             if not args.no_cpu:
                 sec[-1]["cpu_baseline"] = sec[-2]["cpu_baseline"] = cpu_baseline_attention()
         except Exception as exc:  # reported, never silently replaced by another path
