@@ -542,8 +542,12 @@ hk_status hk_attention_masked_backward(hk_context* ctx, const hk_tensor* q, cons
  * dk/dv [B,Hkv,N,D] (F32 or BF16). Q/K/V, O and dO may each be F32 (F32 inputs are rounded to
  * BF16 first; an F32 O enters the row term rowsum(dO * O) unrounded). dK/dV sum over the query heads of each group in a
  * fixed order (no atomics), the deterministic analogue of repeat_kv_heads_backward
- * (runtime/heads.rs:29-51). dS is scaled then rounded to BF16, as the reference's
- * MatmulBf16Fp32Backward chain does (examples/grouped_attention_tensor.rs:30-40). */
+ * (runtime/heads.rs:29-51). dS enters its two GEMMs rounded to BF16, as in the reference's
+ * MatmulBf16Fp32Backward chain (examples/grouped_attention_tensor.rs:30-40), which rounds scale*dS;
+ * here dS is rounded before the scale, which multiplies dQ and dK once (equal within BF16
+ * rounding). The context's workspace grows to B*Hq*ceil(N/32)*ceil(M/64)*4 KiB for the stored dS
+ * (4 GiB at B4, Hq32, S4096) unless that exceeds the environment's HK_ATTN_DS_BUDGET bytes (default
+ * 8 GiB), in which case dQ recomputes S and dP instead. */
 hk_status hk_attention_backward(hk_context* ctx, const hk_tensor* q, const hk_tensor* k,
                                 const hk_tensor* v, const hk_tensor* o, const hk_tensor* lse,
                                 const hk_tensor* dout, float scale, int32_t causal,
