@@ -55,6 +55,8 @@ struct Ctx {
     void* workspace = nullptr;
     size_t ws_bytes = 0;
     void* scratch = nullptr;  // device address of `scratch` below on this context's device
+    int* flags = nullptr;     // device address of `check_flags` below
+    uint32_t flag_seq = 0;    // sequence number of the last embedding lookup
     std::vector<GroupEndsDev*> group_tables;  // live uploads, for the device programs' checks
     std::vector<ModuleDev*> modules;          // loaded device-program code objects
 };
@@ -66,6 +68,11 @@ struct Ctx {
 // hipGetSymbolAddress on the context's device, and every host-side use goes through Ctx::scratch.
 constexpr size_t kScratchBytes = size_t(8) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The embedding lookup's index check: a lookup that meets an index outside the table writes its
+// own sequence number into check_flags[0], so no launch has to clear the word first. Zeroed by
+// hk_init; only embedding lookups write it (one context per process).
+static __device__ __align__(256) int check_flags[64];
 
 std::mutex g_init_mu;
 Ctx* g_ctx = nullptr;
@@ -455,9 +462,15 @@ hk_status hk_init(int32_t device, hk_context** out) {
     e = hipGetSymbolAddress(&scratch_ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || scratch_ptr == nullptr)
         return fail(HK_LOAD_ERROR, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    void* flags_ptr = nullptr;
+    e = hipGetSymbolAddress(&flags_ptr, HIP_SYMBOL(check_flags));
+    if (e == hipSuccess && flags_ptr != nullptr) e = hipMemset(flags_ptr, 0, sizeof(check_flags));
+    if (e != hipSuccess || flags_ptr == nullptr)
+        return fail(HK_LOAD_ERROR, "check flags on device %d: %s", device, hipGetErrorString(e));
     Ctx* c = new Ctx();
     c->device = device;
     c->scratch = scratch_ptr;
+    c->flags = static_cast<int*>(flags_ptr);
     c->num_cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     c->stats.modules_loaded = 1;  // the fat binary linked into this library
     g_ctx = c;
@@ -1860,14 +1873,16 @@ static bool ids_prefix(const hk_tensor* ids, const hk_tensor* t) {  // t = ids.s
     return true;
 }
 // After a synchronous call: read the kernel's out-of-range flag (the workspace's first int).
-static hk_status ids_in_range(Ctx* c, hk_status st, int64_t vocab) {
+// The index check of a synchronous call: the flag word at `flag` equals `bad` when an index was
+// outside the table.
+static hk_status ids_in_range(Ctx* c, hk_status st, int64_t vocab, const void* flag, int bad) {
     if (st != HK_OK || c->async) return st;
-    int flag = 0;
-    if (hipMemcpy(&flag, c->workspace, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) {
+    int value = 0;
+    if (hipMemcpy(&value, flag, sizeof(value), hipMemcpyDeviceToHost) != hipSuccess) {
         c->poisoned = true;
         return fail(HK_COMPLETION_ERROR, "embedding: reading the index check failed");
     }
-    if (flag) return fail(HK_INVALID_ARGUMENT, "embedding index outside [0, %lld)", static_cast<long long>(vocab));
+    if (value == bad) return fail(HK_INVALID_ARGUMENT, "embedding index outside [0, %lld)", static_cast<long long>(vocab));
     return HK_OK;
 }
 }  // namespace
@@ -1956,11 +1971,11 @@ hk_status hk_embedding(hk_context* h, const hk_tensor* weight, const hk_tensor* 
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
     const int64_t vocab = weight->shape[0];
-    hk_status st = ensure_workspace(g.c, hk::embedding_workspace_bytes(tokens, vocab, false));
-    if (st != HK_OK) return st;
+    g.c->flag_seq = g.c->flag_seq + 1 == 0 ? 1 : g.c->flag_seq + 1;  // never 0, the word's initial value
+    const int seq = static_cast<int>(g.c->flag_seq);
     hipError_t e = hk::embedding(weight->data, static_cast<int>(dtype_size(ids->dtype)), ids->data, out->data, tokens,
-                                 vocab, weight->shape[1] * dtype_size(weight->dtype), g.c->workspace, g.c->stream);
-    return ids_in_range(g.c, complete(g.c, e, "embedding", 2), vocab);
+                                 vocab, weight->shape[1] * dtype_size(weight->dtype), g.c->flags, seq, g.c->stream);
+    return ids_in_range(g.c, complete(g.c, e, "embedding", 1), vocab, g.c->flags, seq);
 }
 
 hk_status hk_embedding_backward(hk_context* h, const hk_tensor* grad, const hk_tensor* ids, uint64_t num_weights,
@@ -1991,7 +2006,7 @@ hk_status hk_embedding_backward(hk_context* h, const hk_tensor* grad, const hk_t
     hipError_t e = hk::embedding_backward(grad->dtype, grad->data, static_cast<int>(dtype_size(ids->dtype)), ids->data,
                                           dweight->data, tokens, vocab, width, padding_idx, scale_grad_by_freq,
                                           g.c->workspace, g.c->stream);
-    return ids_in_range(g.c, complete(g.c, e, "embedding_backward", tokens ? 5 : 3), vocab);
+    return ids_in_range(g.c, complete(g.c, e, "embedding_backward", tokens ? 5 : 3), vocab, g.c->workspace, 1);
 }
 
 hk_status hk_softmax(hk_context* h, const hk_tensor* x, int32_t logarithmic, hk_tensor* y) {

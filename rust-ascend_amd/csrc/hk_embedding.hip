@@ -32,7 +32,7 @@ constexpr int kTokensPerBlock = kEmbThreads / kWave;
 template <typename Idx, typename U>
 __global__ void __launch_bounds__(kEmbThreads)
 embedding_gather_kernel(const U* __restrict__ table, const Idx* __restrict__ ids, U* __restrict__ out, int64_t tokens,
-                        int64_t vocab, int64_t units, int* __restrict__ flag) {
+                        int64_t vocab, int64_t units, int* __restrict__ flag, int seq) {
     const int lane = threadIdx.x % kWave;
     for (int64_t t = static_cast<int64_t>(blockIdx.x) * kTokensPerBlock + threadIdx.x / kWave; t < tokens;
          t += static_cast<int64_t>(gridDim.x) * kTokensPerBlock) {
@@ -44,7 +44,7 @@ embedding_gather_kernel(const U* __restrict__ table, const Idx* __restrict__ ids
             for (int64_t u = lane; u < units; u += kWave) dst[u] = src[u];
         } else {
             for (int64_t u = lane; u < units; u += kWave) dst[u] = U{};
-            if (lane == 0) *flag = 1;
+            if (lane == 0) *flag = seq;
         }
     }
 }
@@ -71,7 +71,6 @@ clear_counts_kernel(uint32_t* __restrict__ counts, int64_t n, int* __restrict__ 
     if (flat_begin(kEmbThreads) == 0) *flag = 0;
 }
 
-__global__ void clear_flag_kernel(int* __restrict__ flag) { *flag = 0; }
 
 // One workgroup per table row v: the positions of ID v are sorted[offsets[v] .. + counts[v]).
 template <typename T>
@@ -159,22 +158,22 @@ EmbWs carve(void* base, int64_t tokens, int64_t vocab) {
 
 template <typename Idx, typename U>
 void launch_gather(const void* table, const void* ids, void* out, int64_t tokens, int64_t vocab, int64_t row_bytes,
-                   int* flag, hipStream_t s) {
+                   int* flag, int seq, hipStream_t s) {
     const unsigned grid = flat_blocks(tokens, kTokensPerBlock);
     hipLaunchKernelGGL((embedding_gather_kernel<Idx, U>), dim3(grid), dim3(kEmbThreads), 0, s,
                        static_cast<const U*>(table), static_cast<const Idx*>(ids), static_cast<U*>(out), tokens,
-                       vocab, row_bytes / static_cast<int64_t>(sizeof(U)), flag);
+                       vocab, row_bytes / static_cast<int64_t>(sizeof(U)), flag, seq);
 }
 
 template <typename Idx>
 void gather_by_unit(const void* table, const void* ids, void* out, int64_t tokens, int64_t vocab, int64_t row_bytes,
-                    int* flag, hipStream_t s) {
+                    int* flag, int seq, hipStream_t s) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out) |
                         static_cast<uintptr_t>(row_bytes);
-    if (a % 16 == 0) launch_gather<Idx, u32x4_t>(table, ids, out, tokens, vocab, row_bytes, flag, s);
-    else if (a % 8 == 0) launch_gather<Idx, u32x2_t>(table, ids, out, tokens, vocab, row_bytes, flag, s);
-    else if (a % 4 == 0) launch_gather<Idx, uint32_t>(table, ids, out, tokens, vocab, row_bytes, flag, s);
-    else launch_gather<Idx, uint16_t>(table, ids, out, tokens, vocab, row_bytes, flag, s);
+    if (a % 16 == 0) launch_gather<Idx, u32x4_t>(table, ids, out, tokens, vocab, row_bytes, flag, seq, s);
+    else if (a % 8 == 0) launch_gather<Idx, u32x2_t>(table, ids, out, tokens, vocab, row_bytes, flag, seq, s);
+    else if (a % 4 == 0) launch_gather<Idx, uint32_t>(table, ids, out, tokens, vocab, row_bytes, flag, seq, s);
+    else launch_gather<Idx, uint16_t>(table, ids, out, tokens, vocab, row_bytes, flag, seq, s);
 }
 
 template <typename T>
@@ -195,12 +194,10 @@ size_t embedding_workspace_bytes(int64_t tokens, int64_t vocab, bool backward) {
 }
 
 hipError_t embedding(const void* table, int id_bytes, const void* ids, void* out, int64_t tokens, int64_t vocab,
-                     int64_t row_bytes, void* workspace, hipStream_t s) {
-    int* flag = static_cast<int*>(workspace);
-    hipLaunchKernelGGL(clear_flag_kernel, dim3(1), dim3(1), 0, s, flag);
+                     int64_t row_bytes, int* flag, int seq, hipStream_t s) {
     if (tokens > 0 && row_bytes > 0) {
-        if (id_bytes == 8) gather_by_unit<int64_t>(table, ids, out, tokens, vocab, row_bytes, flag, s);
-        else gather_by_unit<int32_t>(table, ids, out, tokens, vocab, row_bytes, flag, s);
+        if (id_bytes == 8) gather_by_unit<int64_t>(table, ids, out, tokens, vocab, row_bytes, flag, seq, s);
+        else gather_by_unit<int32_t>(table, ids, out, tokens, vocab, row_bytes, flag, seq, s);
     }
     return hipGetLastError();
 }

@@ -122,8 +122,10 @@ hipError_t column_sum(const float* dy, float* out, int64_t rows, int64_t width, 
 // Lookup of `tokens` rows of `row_bytes` bytes from a [vocab, .] table by INT32/INT64 IDs
 // (id_bytes 4 or 8); the workspace's first int becomes nonzero if an ID lies outside [0, vocab).
 size_t embedding_workspace_bytes(int64_t tokens, int64_t vocab, bool backward);
+// An index outside [0, vocab) writes `seq` to *flag (and zeros to its row); *flag is not cleared
+// first, so a caller gives every call its own seq and compares afterwards.
 hipError_t embedding(const void* table, int id_bytes, const void* ids, void* out, int64_t tokens, int64_t vocab,
-                     int64_t row_bytes, void* workspace, hipStream_t s);
+                     int64_t row_bytes, int* flag, int seq, hipStream_t s);
 // Dense gradient dw[vocab, width] from grad[tokens, width]; dtype is the hk_dtype code of grad/dw
 // (F32, F16 or BF16); padding == UINT64_MAX means no padding row.
 hipError_t embedding_backward(int dtype, const void* grad, int id_bytes, const void* ids, void* dw, int64_t tokens,
