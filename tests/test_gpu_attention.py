@@ -218,6 +218,26 @@ def test_backward_random_vs_oracle(d, causal, m, n, dq_form):
     rows_ok(host(dv), ref["dv"], 1e-2, "dv rows")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("m,n", [(1, 1), (1, 70), (5, 1), (33, 65), (65, 33), (129, 257)])
+def test_backward_tiny_and_ragged_shapes(m, n, causal, dq_form):
+    """Shapes that leave every tile partial (one query or one key, blocks of 32/64/128 cut short),
+    on both dQ forms: the stored form's dS blocks past N or M and unwritten blocks must not reach
+    dQ."""
+    d, h, hkv = 64, 2, 1
+    q_t, q = randn_bf16((1, h, m, d), seed=m + 3 * n + 71)
+    k_t, k = randn_bf16((1, hkv, n, d), seed=m + 3 * n + 72)
+    v_t, v = randn_bf16((1, hkv, n, d), seed=m + 3 * n + 73)
+    do_t, do = randn_bf16((1, h, m, d), seed=m + 3 * n + 74)
+    qs = max(n - m, 0) if causal else 0
+    _, _, dq, dk, dv = run_fwd_bwd(q_t, k_t, v_t, do_t, d ** -0.5, causal, qs)
+    ref = oracle.attention_f64(q, k, v, do, scale=d ** -0.5, causal=causal, query_start=qs, magnitudes=True)
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        g = host(got)
+        assert np.all(np.isfinite(g)), name
+        mag_ok(g, ref[name], ref[name + "_mag"], 1e-2, name)
+
+
 def test_backward_bf16_grads_and_determinism(dq_form):
     q_t, q = randn_bf16((1, 8, 192, 128), seed=51)
     k_t, k = randn_bf16((1, 2, 192, 128), seed=52)
