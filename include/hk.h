@@ -111,6 +111,15 @@ hk_status hk_set_async(hk_context* ctx, int32_t async_mode);
 /* Reference: CannSession::synchronize / ComputeClient::flush. */
 hk_status hk_sync(hk_context* ctx);
 hk_status hk_get_stats(hk_context* ctx, hk_stats* out);
+/* The context's workspace: device scratch that ops allocate on first need, grow when a
+ * larger call needs more, and keep for later calls (the stored-dS attention backward holds
+ * B*Hq*ceil(N/32)*ceil(M/64)*4 KiB, 4 GiB at B4 S4096 Hq32, within HK_ATTN_DS_BUDGET;
+ * a backward whose dS buffer cannot be allocated falls back to the recompute form). No
+ * reference counterpart: the reference allocates per call (runtime/matrix.rs:33-44).
+ * hk_workspace_size reports its size in bytes; hk_trim_workspace frees it, after the queued
+ * work, when it holds more than keep_bytes (0: always). */
+hk_status hk_workspace_size(hk_context* ctx, uint64_t* bytes);
+hk_status hk_trim_workspace(hk_context* ctx, uint64_t keep_bytes);
 /* Thread-local message of the last failure; reference: Display for CannError. */
 const char* hk_last_error(void);
 /* Number of the library's ABI (bumped on incompatible change). */

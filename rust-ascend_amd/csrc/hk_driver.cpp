@@ -18,6 +18,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -224,8 +225,23 @@ hk_status complete(Ctx* c, hipError_t launch, const char* op, int kernels) {
     return HK_OK;
 }
 
+// Upper bound on the workspace, in bytes: the environment variable HK_WORKSPACE_LIMIT (read on
+// every resize), else none. A larger request fails as an allocation failure does, so callers
+// that cap the library's device memory get the same fallbacks (the recompute form of the
+// attention backward) as when HBM is short.
+size_t workspace_limit() {
+    const char* env = std::getenv("HK_WORKSPACE_LIMIT");
+    if (env == nullptr || *env == '\0') return SIZE_MAX;
+    char* end = nullptr;
+    const unsigned long long v = std::strtoull(env, &end, 10);
+    return end != nullptr && *end == '\0' ? static_cast<size_t>(v) : SIZE_MAX;
+}
+
 hk_status ensure_workspace(Ctx* c, size_t bytes) {
     if (bytes <= c->ws_bytes) return HK_OK;
+    const size_t limit = workspace_limit();
+    if (bytes > limit)
+        return fail(HK_HIP_ERROR, "workspace of %zu bytes exceeds HK_WORKSPACE_LIMIT (%zu bytes)", bytes, limit);
     if (c->workspace) {
         // queued work may still read the old buffer
         hipError_t e = hipStreamSynchronize(c->stream);
@@ -237,13 +253,34 @@ hk_status ensure_workspace(Ctx* c, size_t bytes) {
         c->workspace = nullptr;
         c->ws_bytes = 0;
     }
-    size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    size_t want = bytes < (size_t(1) << 20) ? std::min(size_t(1) << 20, limit) : bytes;
     hipError_t e = hipMalloc(&c->workspace, want);
     if (e != hipSuccess) {
         c->workspace = nullptr;
+        // a failed allocation leaves HIP's last error set; every launch wrapper returns
+        // hipGetLastError(), so clear it here or the next op reports it and poisons the context
+        (void)hipGetLastError();
         return fail(HK_HIP_ERROR, "workspace allocation of %zu bytes failed: %s", want, hipGetErrorString(e));
     }
     c->ws_bytes = want;
+    return HK_OK;
+}
+
+// Frees the workspace when it holds more than keep bytes (after the queued work that may use it).
+hk_status trim_workspace(Ctx* c, size_t keep) {
+    if (!c->workspace || c->ws_bytes <= keep) return HK_OK;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "workspace trim: synchronization status %d", static_cast<int>(e));
+    }
+    e = hipFree(c->workspace);
+    c->workspace = nullptr;
+    c->ws_bytes = 0;
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(HK_HIP_ERROR, "workspace release failed: %s", hipGetErrorString(e));
+    }
     return HK_OK;
 }
 
@@ -546,6 +583,20 @@ hk_status hk_get_stats(hk_context* h, hk_stats* out) {
     if (!out) return fail(HK_INVALID_ARGUMENT, "null stats pointer");
     *out = g.c->stats;
     return HK_OK;
+}
+
+hk_status hk_workspace_size(hk_context* h, uint64_t* bytes) {
+    OpGuard g(h);
+    if (g.st != HK_OK && g.st != HK_POISONED) return g.st;
+    if (!bytes) return fail(HK_INVALID_ARGUMENT, "null output pointer");
+    *bytes = g.c->ws_bytes;
+    return HK_OK;
+}
+
+hk_status hk_trim_workspace(hk_context* h, uint64_t keep_bytes) {
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    return trim_workspace(g.c, static_cast<size_t>(keep_bytes));
 }
 
 hk_status hk_alloc(hk_context* h, size_t bytes, void** out) {
@@ -2109,6 +2160,36 @@ hk_status hk_repeat_kv_heads_backward(hk_context* h, const hk_tensor* dy, hk_ten
     return complete(g.c, e, "repeat_kv_heads_backward", numel(dx) ? 1 : 0);
 }
 
+// The RMSNorm row-split exchange's check word (check_flags[1]): a new sequence number per call,
+// the wait bound from HK_ROW_SPIN_LIMIT (polls per wait; default 2^24, ~1 s), and after a
+// synchronous call that launched a split kernel, a word equal to the call's number means a
+// wait ran out and the results are invalid. The device is left healthy (every wait is bounded),
+// so the context is not poisoned.
+static hk::RowCheck row_check(Ctx* c) {
+    c->flag_seq = c->flag_seq + 1 == 0 ? 1 : c->flag_seq + 1;
+    int limit = 1 << 24;
+    if (const char* env = std::getenv("HK_ROW_SPIN_LIMIT")) {
+        char* end = nullptr;
+        const long v = std::strtol(env, &end, 10);
+        if (end != nullptr && *end == '\0' && v > 0 && v <= INT32_MAX) limit = static_cast<int>(v);
+    }
+    return hk::RowCheck{c->flags + 1, static_cast<int>(c->flag_seq), limit, 0};
+}
+
+static hk_status row_check_result(Ctx* c, hk_status st, const hk::RowCheck& rc, const char* op) {
+    if (st != HK_OK || c->async || !rc.used) return st;
+    int value = 0;
+    if (hipMemcpy(&value, rc.flag, sizeof(value), hipMemcpyDeviceToHost) != hipSuccess) {
+        c->poisoned = true;
+        return fail(HK_COMPLETION_ERROR, "%s: reading the row exchange check failed", op);
+    }
+    if (value == rc.seq)
+        return fail(HK_COMPLETION_ERROR,
+                    "%s: a row-split exchange wait ran out after %d polls; the results of this call are invalid", op,
+                    rc.spin_limit);
+    return HK_OK;
+}
+
 hk_status hk_rms_norm(hk_context* h, const hk_tensor* x, const hk_tensor* w, double eps, hk_tensor* y,
                       hk_tensor* rstd) {
     // Reference: normalization.rs:153-166 (+ layout_for / epsilon_for, :12-48).
@@ -2128,9 +2209,10 @@ hk_status hk_rms_norm(hk_context* h, const hk_tensor* x, const hk_tensor* w, dou
     if (!disjoint({y, rstd}, {x, w})) return HK_INVALID_ARGUMENT;
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
+    hk::RowCheck rc = row_check(g.c);
     hipError_t e = hk::rms_norm_forward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), y->data,
-                                        static_cast<float*>(rstd->data), rows, width, e32, g.c->stream);
-    return complete(g.c, e, "rms_norm", rows ? 1 : 0);
+                                        static_cast<float*>(rstd->data), rows, width, e32, rc, g.c->stream);
+    return row_check_result(g.c, complete(g.c, e, "rms_norm", rows ? 1 : 0), rc, "rms_norm");
 }
 
 static hk_status rms_backward_args(const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy, const hk_tensor* rstd,
@@ -2161,11 +2243,14 @@ hk_status hk_rms_norm_backward(hk_context* h, const hk_tensor* x, const hk_tenso
     if (st != HK_OK) return st;
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
-    if ((st = ensure_workspace(g.c, hk::rms_backward_workspace_bytes(rows, width))) != HK_OK) return st;
+    if ((st = ensure_workspace(g.c, hk::rms_backward_workspace_bytes(rows, width, x->data, w->data, dy->data,
+                                                                     dx->data))) != HK_OK)
+        return st;
+    hk::RowCheck rc = row_check(g.c);
     hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
                                          static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
-                                         static_cast<float*>(g.c->workspace), rows, width, g.c->stream);
-    return complete(g.c, e, "rms_norm_backward", 2);
+                                         static_cast<float*>(g.c->workspace), rows, width, rc, g.c->stream);
+    return row_check_result(g.c, complete(g.c, e, "rms_norm_backward", 2), rc, "rms_norm_backward");
 }
 
 hk_status hk_rms_norm_backward_noalloc(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
@@ -2173,20 +2258,22 @@ hk_status hk_rms_norm_backward_noalloc(hk_context* h, const hk_tensor* x, const 
     int64_t rows, width;
     hk_status st = rms_backward_args(x, w, dy, rstd, dx, dw, &rows, &width);
     if (st != HK_OK) return st;
-    const size_t need = hk::rms_backward_workspace_bytes(rows, width);
+    const size_t need = hk::rms_backward_workspace_bytes(rows, width, x->data, w->data, dy->data, dx->data);
     if (need > kScratchBytes)
         return fail(HK_INVALID_ARGUMENT,
                     "rms_norm_backward_noalloc: %zu bytes of dgamma partials exceed its fixed %zu-byte device scratch "
-                    "(widths up to 4096 always fit; use hk_rms_norm_backward)",
+                    "(any row count fits up to width 4096 when the width is a multiple of 8 and the tensors are "
+                    "16-byte aligned, up to width 2048 otherwise; use hk_rms_norm_backward)",
                     need, kScratchBytes);
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
     // The same kernels as hk_rms_norm_backward; every partial is written before it is read, so the
     // scratch needs no clearing. Overlapping calls on one GPU share the array and race.
+    hk::RowCheck rc = row_check(g.c);
     hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
                                          static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
-                                         static_cast<float*>(g.c->scratch), rows, width, g.c->stream);
-    return complete(g.c, e, "rms_norm_backward_noalloc", 2);
+                                         static_cast<float*>(g.c->scratch), rows, width, rc, g.c->stream);
+    return row_check_result(g.c, complete(g.c, e, "rms_norm_backward_noalloc", 2), rc, "rms_norm_backward_noalloc");
 }
 
 // ------------------------------------------------------------------ RoPE
@@ -2373,10 +2460,19 @@ hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tens
     sh.o_f32 = o->dtype == HK_F32;
     hk::attention_bwd_plan(sh);
     Staged sq = staged(q), sk = staged(k), sv = staged(v), sd = staged(dout);
-    const size_t stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
+    const size_t staging = sq.bytes + sk.bytes + sv.bytes + sd.bytes;
+    size_t stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
-    if ((st = ensure_workspace(g.c, stat_bytes + sq.bytes + sk.bytes + sv.bytes + sd.bytes)) != HK_OK) return st;
+    st = ensure_workspace(g.c, stat_bytes + staging);
+    if (st == HK_HIP_ERROR && sh.store_ds) {
+        // the stored-dS buffer does not fit in free device memory: the recompute form of dQ
+        // needs only the row statistics
+        sh.store_ds = 0;
+        stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
+        st = ensure_workspace(g.c, stat_bytes + staging);
+    }
+    if (st != HK_OK) return st;
     char* cursor = static_cast<char*>(g.c->workspace) + stat_bytes;
     hipError_t e = stage(q, sq, cursor, g.c->stream);
     if (e == hipSuccess) e = stage(k, sk, cursor, g.c->stream);

@@ -9,13 +9,24 @@
 namespace hk {
 
 // ---- RMSNorm (hk_rmsnorm.hip)
-// Bytes of workspace the backward needs for its FP32 dw partial rows.
-size_t rms_backward_workspace_bytes(int64_t rows, int64_t width);
+// The row-split kernels' exchange check: a wave whose bounded wait (spin_limit polls) for a
+// partner's post runs out writes `seq` into *flag; the launchers set `used` when they launch a
+// kernel that may write it, so the caller knows to read the word back.
+struct RowCheck {
+    int* flag;
+    int seq;
+    int spin_limit;
+    int used;
+};
+// Bytes of workspace the backward needs for its FP64 dγ partial rows on the path these
+// operands take.
+size_t rms_backward_workspace_bytes(int64_t rows, int64_t width, const void* x, const void* w, const void* dy,
+                                    const void* dx);
 hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void* y, float* rstd,
-                            int64_t rows, int64_t width, float eps, hipStream_t s);
+                            int64_t rows, int64_t width, float eps, RowCheck& rc, hipStream_t s);
 hipError_t rms_norm_backward(int dtype_bf16, const void* x, const float* w, const void* dy,
                              const float* rstd, void* dx, float* dw, float* workspace, int64_t rows,
-                             int64_t width, hipStream_t s);
+                             int64_t width, RowCheck& rc, hipStream_t s);
 
 // ---- RoPE and casts (hk_rope.hip)
 // Table row of input row r: sum over leading axes a of coord_a(r) * tstride[a]

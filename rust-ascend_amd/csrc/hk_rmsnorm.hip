@@ -147,7 +147,6 @@ rms_fwd_fast(const T* __restrict__ x, const float* __restrict__ w, T* __restrict
 constexpr int kSplitThreads = 1024;
 constexpr int kSplitMaxWaves = 16;
 constexpr int kSplitMaxChunks = 2048;  // W <= 16384
-constexpr int kSpinLimit = 1 << 24;
 constexpr int kPostBytes = 2 * kSplitMaxWaves * 8;  // [G][2][QN] 64-bit posts, G * QN <= 16
 
 struct SplitShape {
@@ -171,9 +170,19 @@ SplitShape split_shape(int64_t width) {
     return sh;
 }
 
+// Failure report of the exchange: a wave whose wait for a partner's post runs out of spins goes
+// on with the stale post (wrong results, no hang) and writes the call's sequence number into the
+// check word, which the host reads after a synchronous call.
+struct SplitCheck {
+    int* flag;
+    int seq;
+    int spin_limit;
+};
+
 // Sum over the QN parts of row sequence k of group g (every wave of the group calls it with its
 // own part's value).
-__device__ __forceinline__ float split_row_sum(uint64_t* post, int g, int qn, int q, int64_t k, int lane, float part) {
+__device__ __forceinline__ float split_row_sum(uint64_t* post, int g, int qn, int q, int64_t k, int lane, float part,
+                                               const SplitCheck& chk) {
     const uint32_t tag = static_cast<uint32_t>(k) + 1;
     uint64_t* slots = post + (2 * g + static_cast<int>(k & 1)) * qn;
     // single 64-bit LDS accesses (tag and value together); the atomics keep the compiler from
@@ -182,15 +191,18 @@ __device__ __forceinline__ float split_row_sum(uint64_t* post, int g, int qn, in
         __hip_atomic_store(&slots[q], (static_cast<uint64_t>(tag) << 32) | __float_as_uint(part), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
     float total = 0.0f;
+    bool stale = false;
     for (int p = 0; p < qn; ++p) {
         uint64_t val;
         int spins = 0;
         do {
             val = __hip_atomic_load(&slots[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        } while (static_cast<uint32_t>(val >> 32) != tag && ++spins < kSpinLimit);
+        } while (static_cast<uint32_t>(val >> 32) != tag && ++spins < chk.spin_limit);
+        stale |= static_cast<uint32_t>(val >> 32) != tag;
         const float v = __uint_as_float(static_cast<uint32_t>(val));
         total = p == 0 ? v : total + v;
     }
+    if (stale && lane == 0) *chk.flag = chk.seq;
     return total;
 }
 
@@ -202,7 +214,7 @@ __host__ __device__ constexpr size_t split_lds_bytes(int chunks, int groups, boo
 template <typename T, int CPL, bool FULL>
 __global__ void __launch_bounds__(kSplitThreads)
 rms_fwd_split(const T* __restrict__ x, const float* __restrict__ w, T* __restrict__ y, float* __restrict__ rstd,
-              int64_t rows, int chunks, int qn, int groups, float eps) {
+              int64_t rows, int chunks, int qn, int groups, float eps, SplitCheck chk) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     uint64_t* post = reinterpret_cast<uint64_t*>(lds_raw);
     float* w_lds = reinterpret_cast<float*>(lds_raw + kPostBytes);
@@ -236,7 +248,7 @@ rms_fwd_split(const T* __restrict__ x, const float* __restrict__ w, T* __restric
             }
         }
         ss = wave_sum(ss);
-        const float total = split_row_sum(post, g, qn, q, k, lane, ss);
+        const float total = split_row_sum(post, g, qn, q, k, lane, ss, chk);
         const float r = 1.0f / sqrtf(total * inv_w + eps);
         T* yr = y + row * W;
 #pragma unroll
@@ -260,7 +272,7 @@ template <typename T, int CPL, bool FULL>
 __global__ void __launch_bounds__(kSplitThreads)
 rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
               const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial, int64_t rows,
-              int chunks, int qn, int groups) {
+              int chunks, int qn, int groups, SplitCheck chk) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     uint64_t* post = reinterpret_cast<uint64_t*>(lds_raw);
     float* w_lds = reinterpret_cast<float*>(lds_raw + kPostBytes);
@@ -321,7 +333,7 @@ rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __r
             }
         }
         dot = wave_sum(dot);
-        const float total = split_row_sum(post, g, qn, q, k, lane, dot);
+        const float total = split_row_sum(post, g, qn, q, k, lane, dot, chk);
         const float corr = (total * inv_w) * (r * r);
         T* dr = dx + row * W;
 #pragma unroll
@@ -555,30 +567,33 @@ int split_grid(int64_t rows, int groups) { return grid_for_rows(rows, groups, 25
 template <typename T, int CPL>
 void launch_split(bool bwd, const SplitShape& sh, int grid, const void* x, const float* w, const void* dy,
                   const float* rstd_in, void* out, float* rstd_out, double* partial, int64_t rows, float eps,
-                  hipStream_t s) {
+                  const SplitCheck& chk, hipStream_t s) {
     const dim3 block(64 * sh.qn * sh.groups);
     const size_t lds = split_lds_bytes(sh.chunks, sh.groups, bwd);
     if (bwd) {
         auto kernel = sh.full ? rms_bwd_split<T, CPL, true> : rms_bwd_split<T, CPL, false>;
         hipLaunchKernelGGL(kernel, dim3(grid), block, lds, s, static_cast<const T*>(x), w, static_cast<const T*>(dy),
-                           rstd_in, static_cast<T*>(out), partial, rows, sh.chunks, sh.qn, sh.groups);
+                           rstd_in, static_cast<T*>(out), partial, rows, sh.chunks, sh.qn, sh.groups, chk);
     } else {
         auto kernel = sh.full ? rms_fwd_split<T, CPL, true> : rms_fwd_split<T, CPL, false>;
         hipLaunchKernelGGL(kernel, dim3(grid), block, lds, s, static_cast<const T*>(x), w, static_cast<T*>(out),
-                           rstd_out, rows, sh.chunks, sh.qn, sh.groups, eps);
+                           rstd_out, rows, sh.chunks, sh.qn, sh.groups, eps, chk);
     }
 }
 
 template <typename T>
 void run_split(bool bwd, int64_t width, const void* x, const float* w, const void* dy, const float* rstd_in,
-               void* out, float* rstd_out, double* partial, int* parts, int64_t rows, float eps, hipStream_t s) {
+               void* out, float* rstd_out, double* partial, int* parts, int64_t rows, float eps, RowCheck& rc,
+               hipStream_t s) {
     const SplitShape sh = split_shape(width);
     const int grid = split_grid(rows, sh.groups);
     if (parts) *parts = grid;
+    const SplitCheck chk{rc.flag, rc.seq, rc.spin_limit > 0 ? rc.spin_limit : 1};
+    rc.used = 1;
     if (sh.cpl == 2)
-        launch_split<T, 2>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, s);
+        launch_split<T, 2>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, chk, s);
     else
-        launch_split<T, 1>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, s);
+        launch_split<T, 1>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, chk, s);
 }
 
 int parts_general(int64_t rows) {
@@ -589,7 +604,7 @@ int parts_general(int64_t rows) {
 
 template <typename T>
 hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, int64_t rows,
-                         int64_t width, float eps, hipStream_t s) {
+                         int64_t width, float eps, RowCheck& rc, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     if (fast_rows(width, {x, w, y})) {
         const int chunks_per_lane = static_cast<int>((width / 8 + 63) / 64);
@@ -598,7 +613,7 @@ hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, in
         else if (chunks_per_lane <= 4) launch_fwd_fast<T, 4>(x, w, y, rstd, rows, (int)width, eps, s);
         else launch_fwd_fast<T, 8>(x, w, y, rstd, rows, (int)width, eps, s);
     } else if (split_rows(width, {x, w, y})) {  // 4096 < W <= 16384
-        run_split<T>(false, width, x, w, nullptr, nullptr, y, rstd, nullptr, nullptr, rows, eps, s);
+        run_split<T>(false, width, x, w, nullptr, nullptr, y, rstd, nullptr, nullptr, rows, eps, rc, s);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_fwd_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
@@ -609,7 +624,7 @@ hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, in
 
 template <typename T>
 hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
-                          float* dw, void* ws, int64_t rows, int64_t width, hipStream_t s) {
+                          float* dw, void* ws, int64_t rows, int64_t width, RowCheck& rc, hipStream_t s) {
     double* workspace = static_cast<double*>(ws);  // the FP64 dγ partials
     if (rows == 0) {
         hipLaunchKernelGGL(fill_zero_f32, dim3(flat_blocks(width, 256)), dim3(256), 0, s, dw, width);
@@ -617,7 +632,7 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
     }
     if (split_rows(width, {x, w, dy, dx})) {
         int parts = 0;  // one FP64 partial row per workgroup, at most 256
-        run_split<T>(true, width, x, w, dy, rstd, dx, nullptr, workspace, &parts, rows, 0.0f, s);
+        run_split<T>(true, width, x, w, dy, rstd, dx, nullptr, workspace, &parts, rows, 0.0f, rc, s);
         hipLaunchKernelGGL(sum_partials8, dim3(static_cast<unsigned>(width / 8)), dim3(256), 0, s, workspace, parts,
                            (int)width, dw);
     } else {
@@ -637,22 +652,27 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
 
 }  // namespace
 
-size_t rms_backward_workspace_bytes(int64_t rows, int64_t width) {
-    const int parts = std::max(static_cast<int>(std::min<int64_t>(rows, 256)), parts_general(rows));
+// FP64 dγ partial rows of the backward's path for these operands: one per workgroup of the
+// row-split kernels (at most 256), else parts_general's column-chunk count (at most 512).
+size_t rms_backward_workspace_bytes(int64_t rows, int64_t width, const void* x, const void* w, const void* dy,
+                                    const void* dx) {
+    if (rows == 0) return 0;
+    const int parts = split_rows(width, {x, w, dy, dx}) ? split_grid(rows, split_shape(width).groups)
+                                                        : parts_general(rows);
     return static_cast<size_t>(parts) * static_cast<size_t>(width) * sizeof(double);
 }
 
 hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void* y, float* rstd,
-                            int64_t rows, int64_t width, float eps, hipStream_t s) {
-    return dtype_bf16 ? rms_forward_t<uint16_t>(x, w, y, rstd, rows, width, eps, s)
-                      : rms_forward_t<float>(x, w, y, rstd, rows, width, eps, s);
+                            int64_t rows, int64_t width, float eps, RowCheck& rc, hipStream_t s) {
+    return dtype_bf16 ? rms_forward_t<uint16_t>(x, w, y, rstd, rows, width, eps, rc, s)
+                      : rms_forward_t<float>(x, w, y, rstd, rows, width, eps, rc, s);
 }
 
 hipError_t rms_norm_backward(int dtype_bf16, const void* x, const float* w, const void* dy,
                              const float* rstd, void* dx, float* dw, float* workspace, int64_t rows,
-                             int64_t width, hipStream_t s) {
-    return dtype_bf16 ? rms_backward_t<uint16_t>(x, w, dy, rstd, dx, dw, workspace, rows, width, s)
-                      : rms_backward_t<float>(x, w, dy, rstd, dx, dw, workspace, rows, width, s);
+                             int64_t width, RowCheck& rc, hipStream_t s) {
+    return dtype_bf16 ? rms_backward_t<uint16_t>(x, w, dy, rstd, dx, dw, workspace, rows, width, rc, s)
+                      : rms_backward_t<float>(x, w, dy, rstd, dx, dw, workspace, rows, width, rc, s);
 }
 
 }  // namespace hk

@@ -81,6 +81,8 @@ SIGNATURES = {
     "hk_set_async": [_CTX, _i32],
     "hk_sync": [_CTX],
     "hk_get_stats": [_CTX, ctypes.POINTER(HkStats)],
+    "hk_workspace_size": [_CTX, ctypes.POINTER(_u64)],
+    "hk_trim_workspace": [_CTX, _u64],
     "hk_last_error": [],
     "hk_abi_version": [],
     "hk_alloc": [_CTX, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)],

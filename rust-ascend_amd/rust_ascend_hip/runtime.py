@@ -202,6 +202,21 @@ class HipRuntime:
         check(lib.hk_get_stats(_context(), ctypes.byref(s)))
         return {"modules_loaded": s.modules_loaded, "launches": s.launches, "synchronizations": s.synchronizations}
 
+    @staticmethod
+    def workspace_size() -> int:
+        """Bytes of device scratch the context holds for later calls."""
+        n = ctypes.c_uint64()
+        check(_lib.load().hk_workspace_size(_context(), ctypes.byref(n)))
+        return int(n.value)
+
+    @staticmethod
+    def trim_workspace(keep_bytes: int = 0) -> None:
+        """Frees the context's scratch when it holds more than keep_bytes (after queued work)."""
+        lib = _lib.load()
+        ctx = _context()
+        check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        check(lib.hk_trim_workspace(ctx, ctypes.c_uint64(keep_bytes)))
+
     # ---------------------------------------------------------------- GEMM
 
     @staticmethod

@@ -346,3 +346,24 @@ def test_masked_attention_contract():
     assert lib.hk_attention_masked_backward(None, q, k, k, fake(F32, (1, 2, 16, 64), 1 << 34),
                                             fake(F32, (1, 2, 16, 16), 1 << 26), 0.25, *grads,
                                             fake(F32, (1, 2, 16, 64), (1 << 20) + 1024)) == _lib.INVALID_ARGUMENT  # dMask overlaps Q
+
+
+def test_integration_extern_blocks_match_the_exports():
+    """Every function that INTEGRATION.md's Rust `extern "C"` blocks declare is exported by
+    libhk.so, and every exported hk_* function is declared in one of those blocks (nm -D on the
+    built library)."""
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "INTEGRATION.md")).read()
+    blocks = re.findall(r'extern "C" \{(.*?)\n\}', text, re.S)
+    assert blocks, "no extern block found"
+    declared = set()
+    for b in blocks:
+        declared |= set(re.findall(r"pub fn (hk_\w+)\(", b))
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = {ln.split()[-1] for ln in out.stdout.splitlines() if ln.split() and ln.split()[-1].startswith("hk_")
+                and ln.split()[-2] in ("T", "t")}
+    assert declared - exported == set(), declared - exported
+    assert exported - declared == set(), exported - declared
+    assert exported == set(declared_functions())

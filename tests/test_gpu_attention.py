@@ -195,6 +195,47 @@ def dq_form(request, monkeypatch):
     return request.param
 
 
+def test_backward_dq_form_follows_budget_and_workspace_limit(monkeypatch):
+    """The stored-dS form holds B*Hq*ceil(N/32)*ceil(M/64) blocks of 4 KiB in the context's
+    workspace. A budget one byte under that takes the recompute form (smaller workspace); a
+    workspace limit (HK_WORKSPACE_LIMIT) under it makes the stored-dS allocation fail, and the
+    backward falls back to the recompute form instead of returning the error; the next op
+    still runs (no stale HIP error left behind). hk_trim_workspace frees the scratch."""
+    B, H, HKV, M, N, D = 1, 8, 2, 1024, 1024, 64
+    ds_bytes = B * H * -(-N // 32) * -(-M // 64) * 4096
+    q_t, q = randn_bf16((B, H, M, D), seed=81)
+    k_t, k = randn_bf16((B, HKV, N, D), seed=82)
+    v_t, v = randn_bf16((B, HKV, N, D), seed=83)
+    do_t, do = randn_bf16((B, H, M, D), seed=84)
+    ref = oracle.attention_f64(q, k, v, do, scale=D ** -0.5, causal=True, magnitudes=True)
+
+    def run():
+        _, _, dq, dk, dv = run_fwd_bwd(q_t, k_t, v_t, do_t, D ** -0.5, True)
+        for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+            mag_ok(host(got), ref[name], ref[name + "_mag"], 1e-2, name)
+        return HipRuntime.workspace_size()
+
+    monkeypatch.delenv("HK_WORKSPACE_LIMIT", raising=False)
+    monkeypatch.setenv("HK_ATTN_DS_BUDGET", str(ds_bytes))
+    HipRuntime.trim_workspace(0)
+    assert HipRuntime.workspace_size() == 0
+    assert run() >= ds_bytes                       # stored dS
+    HipRuntime.trim_workspace(0)
+    monkeypatch.setenv("HK_ATTN_DS_BUDGET", str(ds_bytes - 1))
+    assert run() < ds_bytes                        # recompute form
+    HipRuntime.trim_workspace(0)
+    monkeypatch.setenv("HK_ATTN_DS_BUDGET", str(ds_bytes))
+    monkeypatch.setenv("HK_WORKSPACE_LIMIT", str(ds_bytes))  # under stats + dS: that allocation fails
+    assert run() <= ds_bytes                       # fell back to the recompute form
+    monkeypatch.delenv("HK_WORKSPACE_LIMIT")
+    o2, _ = HipRuntime.attention_forward(q_t, k_t, v_t, D ** -0.5, True)
+    assert torch.all(torch.isfinite(o2))
+    HipRuntime.trim_workspace(1 << 40)             # keeps anything under the bound
+    assert HipRuntime.workspace_size() > 0
+    HipRuntime.trim_workspace(0)
+    assert HipRuntime.workspace_size() == 0
+
+
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("m,n", [(256, 256), (200, 328), (64, 1000), (130, 130)])

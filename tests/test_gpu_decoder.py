@@ -4,16 +4,26 @@ parameters. The layer keeps BF16 activations (each rounding ~2^-9 relative), so 
 normwise, ||a - b|| / ||b|| for the output and every gradient, against plain float64, with a bound
 set per tensor by the drift that BF16 storage causes: a float32 CPU evaluation of the same layer
 that rounds to BF16 wherever the layer stores BF16 (activations and their gradients) is measured
-against float64 in the same test, and the GPU may drift at most 1.5 times as far (+1e-3), never
-beyond 2e-2. At C5 both drift ~1e-2 (measured: GPU y 9.74e-3 / table 1.12e-2, model 9.75e-3 /
+against float64 in the same test, and the GPU may drift at most 1.5 times as far (+1e-3), and
+never beyond max(1e-2, 1.05 times the model's drift). At C5 both drift ~1e-2 (measured: GPU y 9.74e-3 / table 1.12e-2, model 9.75e-3 /
 1.11e-2), at the small shape ~5e-3. A wiring mistake (a missing residual, a transposed
 projection, an unrotated head) exceeds these by far.
 
-C5 itself (hidden 4096, 32/8 heads, FFN 14336, 2 x 2048 tokens) runs at full size on the GPU with
-dY nonzero only on the first 128 positions of each sequence. Attention is causal, so those
-positions' outputs and every gradient depend on the first 128 positions only (a later query's dO
-is zero, so its dS row is zero and it adds nothing to dK, dV or any weight gradient): the float64
-reference over 2 x 128 tokens with the same weights pins the full-size kernels exactly."""
+C5 itself (hidden 4096, 32/8 heads, FFN 14336, 2 x 2048 tokens) is checked twice at full size:
+
+* against float64 on the CPU with dY nonzero only on the first 128 positions of each sequence.
+  Attention is causal, so those positions' outputs and every gradient depend on the first 128
+  positions only (a later query's dO is zero, so its dS row is zero and it adds nothing to dK, dV
+  or any weight gradient): the float64 reference over 2 x 128 tokens with the same weights pins
+  the full-size kernels. At this size BF16 storage alone (the model, rounding where the layer
+  rounds) drifts 0.95-1.1e-2 from float64 on every tensor (measured: y 9.64e-3, table 1.10e-2,
+  wqkv 1.08e-2, w1 1.09e-2), so no BF16-storage layer stays under 1e-2 there: the GPU may
+  drift at most 5 % more than the model, or 1e-2, whichever is larger (measured: 1-2 % more).
+* on all 2 x 2048 positions with dY nonzero everywhere, against the float32 BF16-storage model
+  evaluated on the GPU (torch float32 autograd, no TF32): that model rounds to BF16 at the same
+  points as the layer, so the two differ only by accumulation order, the fused attention's
+  internal roundings and the rounding flips these cause. Bound: per-row normwise 1e-2 on y and
+  normwise 1e-2 on every gradient."""
 import numpy as np
 import pytest
 import torch
@@ -25,7 +35,9 @@ pytestmark = pytest.mark.gpu
 
 SMALL = DecoderConfig(hidden=256, heads=4, kv_heads=2, ffn=512, vocab=1000, batch=2, seq=128)
 DRIFT_FACTOR = 1.5  # GPU's normwise distance from float64 <= 1.5 x the BF16-storage model's (+1e-3)
-PLAIN_TOL = 2e-2    # and never above 2e-2 (the model's drift is ~5e-3 here, ~1e-2 at C5)
+PLAIN_TOL = 1e-2    # and never above max(1e-2, 1.05 x the model's drift)
+MODEL_EXCESS = 1.05
+DIRECT_TOL = 1e-2   # GPU vs the float32 BF16-storage model at full C5 size
 
 
 class _Bf16Storage(torch.autograd.Function):
@@ -54,19 +66,20 @@ class _Bf16Grad(torch.autograd.Function):
         return g.to(torch.bfloat16).to(g.dtype)
 
 
-def reference(layer: DecoderLayer, ids, dy, emulate_bf16=False, dtype=torch.float64):
-    """Autograd of the layer in `dtype` (float64 by default) over ids [B, S'] (S' <= the layer's
-    seq: a prefix of each sequence) with upstream dy [B*S', H]. With emulate_bf16, every activation and activation
+def reference(layer: DecoderLayer, ids, dy, emulate_bf16=False, dtype=torch.float64, device="cpu"):
+    """Autograd of the layer in `dtype` (float64 by default) on `device` over ids [B, S'] (S' <= the
+    layer's seq: a prefix of each sequence) with upstream dy [B*S', H]. With emulate_bf16, every activation and activation
     gradient the GPU layer stores in BF16 is rounded to BF16 at the same point (the weight
     gradients stay unrounded, as the GPU keeps them in F32), so only accumulation order and the
     fused attention's internal roundings remain as differences."""
     c = layer.cfg
-    P = {k: getattr(layer, k).detach().cpu().to(dtype).requires_grad_(True)
+    P = {k: getattr(layer, k).detach().to(device=device, dtype=dtype).requires_grad_(True)
          for k in ("table", "wqkv", "wo", "wg", "wu", "wd", "w1", "w2")}
     seq = ids.shape[1]
+    ids = ids.to(device)
     T, H, D, hq, hkv = c.batch * seq, c.hidden, c.head_dim, c.heads, c.kv_heads
-    cos, sin = (torch.from_numpy(t).to(dtype) for t in rope_tables(seq, D, c.theta))
-    dy = dy.to(dtype)
+    cos, sin = (torch.from_numpy(t).to(device=device, dtype=dtype) for t in rope_tables(seq, D, c.theta))
+    dy = dy.to(device=device, dtype=dtype)
     R = _Bf16Storage.apply if emulate_bf16 else (lambda t: t)
     G = _Bf16Grad.apply if emulate_bf16 else (lambda t: t)
 
@@ -83,7 +96,7 @@ def reference(layer: DecoderLayer, ids, dy, emulate_bf16=False, dtype=torch.floa
     q, k, v = R(rope(qkv[:, :hq])), R(rope(qkv[:, hq:hq + hkv])), G(qkv[:, hq + hkv:])
     k, v = k.repeat_interleave(hq // hkv, 1), v.repeat_interleave(hq // hkv, 1)
     s = (q @ k.transpose(-1, -2)) * D ** -0.5
-    s = s.masked_fill(torch.triu(torch.ones(seq, seq, dtype=torch.bool), 1), float("-inf"))
+    s = s.masked_fill(torch.triu(torch.ones(seq, seq, dtype=torch.bool, device=device), 1), float("-inf"))
     o = R(torch.softmax(s, -1) @ v).permute(0, 2, 1, 3).reshape(T, H)
     h1 = R(x0 + R(o @ P["wo"].T))                              # dh1 = bf16(dh1_norm + dy)
     n2 = R(rms(G(h1), P["w2"]))                                # dn2 = bf16(dn2_g + dn2_u)
@@ -104,8 +117,9 @@ def check_layer(layer: DecoderLayer, ids, dy, prefix: int):
     layer. The layer stores BF16 activations, so it drifts from float64 by an amount its depth
     and widths set; the bound is that drift as a float32 CPU evaluation of the same layer with
     the same BF16 storage points shows it (the model), times DRIFT_FACTOR, per tensor, and never
-    more than PLAIN_TOL."""
+    more than max(PLAIN_TOL, MODEL_EXCESS times the model)."""
     c = layer.cfg
+    print(f"decoder layer {c.hidden}x{c.ffn}, {c.batch}x{c.seq} tokens, float64 on {prefix} positions", flush=True)
     y = layer.forward(ids)[:, :prefix].float().cpu().numpy().reshape(c.batch * prefix, c.hidden)
     grads = {k: v.float().cpu().numpy() for k, v in layer.backward(dy).items()}
     used = np.unique(ids[:, :prefix].cpu().numpy())
@@ -122,7 +136,8 @@ def check_layer(layer: DecoderLayer, ids, dy, prefix: int):
     print("GPU vs float64", {k: f"{v:.2e}" for k, v in gpu.items()}, flush=True)
     print("model vs float64", {k: f"{v:.2e}" for k, v in model.items()}, flush=True)
     for k in gpu:
-        assert gpu[k] <= min(DRIFT_FACTOR * model[k] + 1e-3, PLAIN_TOL), (k, gpu[k], model[k])
+        cap = max(PLAIN_TOL, MODEL_EXCESS * model[k])
+        assert gpu[k] <= min(DRIFT_FACTOR * model[k] + 1e-3, cap), (k, gpu[k], model[k])
     return grads
 
 
@@ -156,6 +171,43 @@ def test_decoder_layer_c5_full_size_prefix_gradient():
     dy[:, prefix:] = 0
     check_layer(layer, ids, dy, prefix)
     del layer
+    torch.cuda.empty_cache()
+
+
+def test_decoder_layer_c5_full_size_vs_bf16_storage_model():
+    """BASELINE config C5 at full size on every position: y and all gradients against the float32
+    BF16-storage model of the same layer, evaluated on the GPU with torch (no TF32)."""
+    c = DecoderConfig()
+    T, H = c.tokens, c.hidden
+    layer = DecoderLayer(c, seed=9)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    ids = torch.randint(0, c.vocab, (c.batch, c.seq), generator=g, device="cuda")
+    ids[1, 1000:1100] = ids[0, 7]  # a repeated ID
+    dy = torch.randn((c.batch, c.seq, H), generator=g, device="cuda").to(torch.bfloat16)
+    print("C5 full size: GPU layer", flush=True)
+    y = layer.forward(ids).reshape(T, H).float()
+    grads = {k: v.float().clone() for k, v in layer.backward(dy).items()}
+    torch.cuda.synchronize()
+    print("C5 full size: float32 BF16-storage model", flush=True)
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        y32, g32 = reference(layer, ids, dy.reshape(T, H), emulate_bf16=True, dtype=torch.float32, device="cuda")
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    row = (torch.linalg.vector_norm(y - y32, dim=1) / torch.linalg.vector_norm(y32, dim=1)).max().item()
+    errs = {"y rows": row}
+    used = torch.unique(ids)
+    for k, ref in g32.items():
+        got = grads[k]
+        if k == "table":
+            ref, got = ref[used], got[used]
+        errs[k] = (torch.linalg.vector_norm(got - ref) / torch.linalg.vector_norm(ref)).item()
+    print("GPU vs float32 BF16-storage model", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for k, e in errs.items():
+        assert e <= DIRECT_TOL, (k, e)
+    del layer, g32, grads
     torch.cuda.empty_cache()
 
 

@@ -136,6 +136,34 @@ def test_rms_norm_misaligned_view_uses_general_path():
     rel_ok(host(y), y_ref, 1e-2, "Y")
 
 
+def test_rms_norm_split_exchange_timeout_is_reported(monkeypatch):
+    """The row-split kernels' waits for their partners' posts are bounded; a wait that runs out
+    makes a synchronous call fail with HK_COMPLETION_ERROR (its results are invalid) instead of
+    returning stale sums silently. Forced from the host: HK_ROW_SPIN_LIMIT=1 lets every wait poll
+    once, so at width 16384 (16 waves per row) some wave reads a post its partner has not written
+    yet; every wait still ends. The context stays usable and the next call is exact again."""
+    rows, width = 4096, 16384
+    x_t, x = randn_bf16((rows, width), seed=91)
+    dy_t, dy = randn_bf16((rows, width), seed=92)
+    w = (1 + 0.1 * oracle.normal((width,), 91, 2)).astype(np.float32)
+    w_t = dev_f32(w)
+    y0, rstd0 = HipRuntime.rms_norm(x_t, w_t, 1e-6)
+    dx0, dw0 = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd0)
+    monkeypatch.setenv("HK_ROW_SPIN_LIMIT", "1")
+    print("rms_norm split exchange with a one-poll wait bound", flush=True)
+    with pytest.raises(HkError, match="exchange wait ran out"):
+        HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd0)
+    with pytest.raises(HkError, match="exchange wait ran out"):
+        HipRuntime.rms_norm(x_t, w_t, 1e-6)
+    monkeypatch.delenv("HK_ROW_SPIN_LIMIT")
+    y1, rstd1 = HipRuntime.rms_norm(x_t, w_t, 1e-6)
+    dx1, dw1 = HipRuntime.rms_norm_backward(x_t, w_t, dy_t, rstd1)
+    for a, b in ((y0, y1), (rstd0, rstd1), (dx0, dx1), (dw0, dw1)):
+        assert torch.equal(a, b)
+    y_ref, r_ref = oracle.rms_norm_f64(x[:64], w, 1e-6)
+    rel_ok(host(y1[:64]), y_ref, 1e-2, "Y")
+
+
 @pytest.mark.parametrize("case", ["0x6", "1x2", "3x6", "2x96"])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_rotary_f32_golden(golden, case, layout):

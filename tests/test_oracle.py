@@ -411,6 +411,54 @@ def test_row_err_definition(oracle):
     assert oracle.row_err(np.array([[np.nan, 0.0]]), np.array([[1.0, 0.0]])) == float("inf")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_rising_score_inputs_drive_the_lagging_rescale(oracle, causal):
+    """The GPU tests of the forward's lagging running max (test_gpu_attention_rescale.py) use
+    these inputs. Replaying the kernel's rule (64-key tiles in order, waves of 32 queries, a
+    rescale when some query's tile max passes its running max + 8 in base 2) shows that after the
+    first tile the "jump", "creep" and "extreme" rows are rescaled at least twice -- every such
+    row when nothing is masked, nearly every one that sees >= 512 keys when causal -- and that
+    the "descending" rows never are (their first tile holds the max)."""
+    from attn_cases import PATTERNS, base2_scores, rescale_counts, rising_inputs
+    m = n = 1024
+    for d in (16, 128):
+        q, k, _, _, names = rising_inputs(1, 4, 2, m, n, d, seed=d)
+        counts = rescale_counts(base2_scores(q, k, d ** -0.5, causal))[0]  # [H, M]
+        seen = np.arange(m) + 1 if causal else np.full(m, n)
+        for p in PATTERNS:
+            rows = np.array([i for i, nm in enumerate(names) if nm == p and seen[i] >= 512])
+            c = counts[:, rows]
+            if p == "descending":
+                assert np.all(c == 0), (d, p)
+            else:
+                frac = float(np.mean(c >= 2))
+                assert frac >= (1.0 if not causal else 0.9), (d, p, frac)
+
+
+@pytest.mark.parametrize("bug", ["keep_l", "keep_o", "alpha_inv"])
+def test_lagging_softmax_replay_matches_exact_and_catches_rescale_mistakes(oracle, bug):
+    """The kernel's tile-by-tile softmax with a lagging max, evaluated in float64, equals the
+    exact softmax on the rising-score inputs (so the rule itself changes nothing), and each
+    plausible mistake in the rescale (l or O left unscaled, the reciprocal factor) moves O by far
+    more than the per-row check's 1e-2 on those inputs: a kernel with such a mistake fails the
+    GPU tests, which apply that check."""
+    from attn_cases import LOG2E, base2_scores, lagging_softmax_f64, rising_inputs
+    m = n = 512
+    d = 64
+    q, k, v, _, _ = rising_inputs(1, 2, 1, m, n, d, seed=5)
+    for causal in (False, True):
+        s = base2_scores(q, k, d ** -0.5, causal)[0, 0]
+        vv = v[0, 0].astype(np.float64)
+        good, lse = lagging_softmax_f64(s, vv)
+        ex = np.exp((s - s.max(axis=1, keepdims=True)) / LOG2E)
+        exact = (ex @ vv) / ex.sum(axis=1, keepdims=True)
+        exact_lse = s.max(axis=1) / LOG2E + np.log(ex.sum(axis=1))
+        assert oracle.row_err(good, exact) < 1e-12
+        np.testing.assert_allclose(lse, exact_lse, rtol=1e-12, atol=1e-9)
+        bad, _ = lagging_softmax_f64(s, vv, bug=bug)
+        assert oracle.row_err(bad, exact) > 1e-1, (bug, causal)
+
+
 # ------------------------------------------------------------------ softmax rows
 
 def _reference_row_inputs(rows, width):

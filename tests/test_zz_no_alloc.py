@@ -53,10 +53,21 @@ def test_noalloc_backward_equals_the_allocating_one_on_two_calls():
         rel_ok(host(dw), dw_ref, 1e-4, "dW", atol_frac=1e-3)
 
 
-def test_noalloc_backward_rejects_partials_beyond_its_scratch():
-    # width 8192 (the general path) with 32768 rows needs 512 x 8192 FP64 partials = 32 MiB
-    x_t = torch.zeros((32768, 8192), dtype=torch.bfloat16, device=DEV)
-    w_t = torch.ones((8192,), dtype=torch.float32, device=DEV)
+def test_noalloc_backward_takes_any_row_count_at_width_4096():
+    # the row-split path keeps at most 256 partial rows (one per workgroup), so 32768 rows of
+    # width 4096 fit the 8 MiB scratch as C2's 16384 do
+    x_t, w_t, dy_t, rstd, _ = case(32768, 4096, torch.bfloat16, 87)
+    a = backward("hk_rms_norm_backward_noalloc", x_t, w_t, dy_t, rstd)
+    b = backward("hk_rms_norm_backward", x_t, w_t, dy_t, rstd)
+    assert torch.equal(bits(a[0]), bits(b[0])) and torch.equal(bits(a[1]), bits(b[1]))
+
+
+@pytest.mark.parametrize("width", [8192, 4100])
+def test_noalloc_backward_rejects_partials_beyond_its_scratch(width):
+    # width 8192 (the row-split path) with 32768 rows needs 256 x 8192 FP64 partials = 16 MiB;
+    # width 4100 (not a multiple of 8: the general path) 512 x 4100 = 16.4 MB
+    x_t = torch.zeros((32768, width), dtype=torch.bfloat16, device=DEV)
+    w_t = torch.ones((width,), dtype=torch.float32, device=DEV)
     rstd = torch.ones((32768,), dtype=torch.float32, device=DEV)
     with pytest.raises(HkError, match="scratch"):
         backward("hk_rms_norm_backward_noalloc", x_t, w_t, x_t, rstd)
