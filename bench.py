@@ -36,13 +36,13 @@ C2_BWD_BYTES = 3 * C2_ROWS * C2_WIDTH * 2 + 2 * C2_WIDTH * 4 + C2_ROWS * 4      
 
 # C1/C3 GEMM workloads: name -> (M, N, K, transpose A, transpose B, label)
 GEMMS = {
-    "gemm8192_nt": (8192, 8192, 8192, 0, 1, "C3 GEMM 8192^3 NT"),
-    "gemm8192_nn": (8192, 8192, 8192, 0, 0, "C3 GEMM 8192^3 NN"),
+    "gemm8192_nt": (8192, 8192, 8192, 0, 1, "C3 8192^3 NT"),
+    "gemm8192_nn": (8192, 8192, 8192, 0, 0, "C3 8192^3 NN"),
     "llama_up": (8192, 14336, 4096, 0, 1, "C3 Llama 8192x4096->14336 NT"),
     "llama_down": (8192, 4096, 14336, 0, 1, "C3 Llama 8192x14336->4096 NT"),
-    "gemm4096_nt": (4096, 4096, 4096, 0, 1, "C3 GEMM 4096^3 NT"),
-    "gemm1024_nt": (1024, 1024, 1024, 0, 1, "C3 GEMM 1024^3 NT"),
-    "c1": (512, 1024, 1024, 0, 1, "C1 Linear X[512,1024] W[1024,1024]^T"),
+    "gemm4096_nt": (4096, 4096, 4096, 0, 1, "C3 4096^3 NT"),
+    "gemm1024_nt": (1024, 1024, 1024, 0, 1, "C3 1024^3 NT"),
+    "c1": (512, 1024, 1024, 0, 1, "C1 Linear 512x1024 by 1024x1024^T"),
 }
 # CPU-baseline sample rows per GEMM workload (None: the whole product)
 CPU_ROWS = {"gemm8192_nt": 256, "gemm8192_nn": 16, "llama_up": 256, "llama_down": 256}
@@ -177,6 +177,23 @@ def roofline(bound, algo, ms, kernel, key=None):
     return out
 
 
+def short_roofline(rl, kernel=True):
+    """The roofline of a secondary line without what the line already states (value = achieved,
+    ms = the average launch, unit and peak implied by the line's unit): the fraction of peak, the
+    counter-measured HBM traffic per launch in MB, MFMA utilisation where measured."""
+    out = {"kernel": rl["kernel"]} if kernel else {}
+    out["frac"] = rl["frac"]
+    out["traffic_MB"] = None if rl.get("traffic") is None else round(rl["traffic"] / 1e6)
+    if "mfma_util" in rl:
+        out["mfma_util"] = rl["mfma_util"]
+    return out
+
+
+def short_cpu(cpu):
+    """A secondary line's CPU baseline without the unit it shares with the line."""
+    return {k: cpu[k] for k in ("value", "cores", "kind", "sample")}
+
+
 def bench_c2(steps, warmup):
     import ctypes
     import torch
@@ -251,8 +268,7 @@ def cpu_baseline_c2(threads):
     t = sorted(times)[1]
     return {"value": round((C2_FWD_BYTES + C2_BWD_BYTES) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "seconds_per_step": round(t, 3),
-            "sample": "full C2 step (fwd+bwd, 16384x4096), FP32 row-program order on BF16-valued inputs, "
-                      "median of 3"}
+            "sample": "whole C2 step, FP32 row-program order on BF16-valued inputs, median of 3"}
 
 
 def cpu_threads():
@@ -282,10 +298,7 @@ def cpu_baseline_gemm(m, n, k, ta, tb, rows=None):
         times.append(time.perf_counter() - t0)
     t = sorted(times)[len(times) // 2]
     return {"value": round(2 * mr * n * k / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "seconds": round(t * m / mr, 3),
-            "sample": (f"full {m}x{n}x{k} {'NT' if tb else 'NN'}" if mr == m else
-                       f"{mr} of {m} output rows of {m}x{n}x{k} {'NT' if tb else 'NN'} (seconds projected to all rows)") +
-                      f", f32 sequential-k host loop, {'median of 3' if reps == 3 else 'timed once'}"}
+            "sample": ("all rows" if mr == m else f"{mr}/{m} rows") + (", median of 3" if reps == 3 else "")}
 
 
 def cpu_baseline_attention():
@@ -307,10 +320,7 @@ def cpu_baseline_attention():
     t = time.perf_counter() - t0
     flops = 3.5 * 2 * 32 * S * S * D  # forward + backward, causal-useful (the GPU lines' count)
     return {"value": round(flops / t / 1e12, 6), "unit": "TFLOP/s", "cores": min(threads, 8), "kind": "port",
-            "seconds": round(t * 64, 1),
-            "sample": "C4 batch 0, 32/8 heads, first 1024 positions (1/64 of the causal work), forward + backward, "
-                      "f64 host loop with BF16 rounding points, timed once; parallel over the 8 (batch, KV head) "
-                      "pairs; seconds = projected to the whole config"}
+            "sample": "batch 0, positions < 1024 (1/64 of the work)"}
 
 
 def bench_gemm(m, n, k, ta, tb, iters=10, warmup=3, out=None):
@@ -473,20 +483,97 @@ def gemm_kernel_name(m, n, k, ta, tb):
     return "gemm_nt_dma_kernel"
 
 
-def bench_rope(iters=10):
+def c4_tables(S=4096, D=128, theta=5e5):
+    """C4's RoPE tables [1, 1, S, D/2] F32: angle = position * theta^(-2i/D), in float64."""
     import numpy as np
+    pos = np.arange(S, dtype=np.float64)[:, None]
+    ang = pos * (theta ** (-np.arange(0, D, 2) / D))[None, :]
+    return (np.cos(ang).astype(np.float32)[None, None], np.sin(ang).astype(np.float32)[None, None])
+
+
+def bench_rope(iters=10):
+    """C4's RoPE: split-half rotation of Q [4,32,4096,128] and K [4,8,4096,128] (two calls of the
+    C ABI per step, descriptors built once)."""
+    import ctypes
     import torch
-    from rust_ascend_hip import HipRuntime, RotaryLayout
-    pos = np.arange(4096, dtype=np.float64)[:, None]
-    ang = pos * (5e5 ** (-np.arange(0, 128, 2) / 128))[None, :]
-    c = torch.from_numpy(np.cos(ang).astype(np.float32)).cuda()[None, None]
-    s = torch.from_numpy(np.sin(ang).astype(np.float32)).cuda()[None, None]
+    from rust_ascend_hip import _lib, runtime
+    from rust_ascend_hip._lib import check
+    cos, sin = (torch.from_numpy(t).cuda() for t in c4_tables())
     q = torch.randn((4, 32, 4096, 128), device="cuda").to(torch.bfloat16)
-    # back-to-back calls between one pair of events (an event between every two calls costs the
+    k = torch.randn((4, 8, 4096, 128), device="cuda").to(torch.bfloat16)
+    yq, yk = torch.empty_like(q), torch.empty_like(k)
+    lib, ctx = _lib.load(), runtime._context()
+    check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    d = [runtime.desc(t) for t in (q, k, cos, sin, yq, yk)]
+
+    def step():
+        check(lib.hk_rotary_prefix(ctx, d[0], d[2], d[3], 128, 1, d[4]))
+        check(lib.hk_rotary_prefix(ctx, d[1], d[2], d[3], 128, 1, d[5]))
+    # back-to-back steps between one pair of events (an event between every two calls costs the
     # GPU time of its own)
-    ms = time_gpu(lambda: HipRuntime.rotary_prefix(q, c, s, 128, RotaryLayout.SplitHalf), iters)
-    algo = 2 * q.numel() * 2 + 2 * c.numel() * 4
+    ms = time_gpu(step, iters)
+    algo = 2 * (q.numel() + k.numel()) * 2 + 2 * 2 * cos.numel() * 4
     return ms, algo
+
+
+def cpu_baseline_rope():
+    """The oracle's restatement of the reference's rotary program (rotary_programs.rs:47-97,
+    101-156) on batch 0 of C4's Q and K (a quarter of the work), timed on the host."""
+    import numpy as np
+    import oracle
+    threads = cpu_threads()
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(6)
+    cos, sin = c4_tables()
+    q = oracle.bf16_round(rng.standard_normal((1, 32, 4096, 128), dtype=np.float32))
+    k = oracle.bf16_round(rng.standard_normal((1, 8, 4096, 128), dtype=np.float32))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.rotary_prefix(q, cos, sin, 128, 1)
+        oracle.rotary_prefix(k, cos, sin, 128, 1)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    algo = 2 * (q.size + k.size) * 2
+    return {"value": round(algo / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": "batch 0 (1/4), median of 3"}
+
+
+def bench_c4_step(iters=3):
+    """BASELINE C4 as one step: RoPE (split-half, theta 5e5) on Q and K, the causal GQA attention
+    forward and backward on the rotated Q/K, and the RoPE backward of dQ and dK (BF16 gradients),
+    eight C-ABI calls with descriptors built once. Returns (step ms, attention flops per step)."""
+    import ctypes
+    import torch
+    from rust_ascend_hip import _lib, runtime
+    from rust_ascend_hip._lib import check
+    B, H, HKV, S, D = 4, 32, 8, 4096, 128
+    g = torch.Generator(device="cuda")
+    g.manual_seed(44)
+    bf = torch.bfloat16
+    q = torch.randn((B, H, S, D), generator=g, device="cuda").to(bf)
+    k = torch.randn((B, HKV, S, D), generator=g, device="cuda").to(bf)
+    v = torch.randn((B, HKV, S, D), generator=g, device="cuda").to(bf)
+    do = torch.randn((B, H, S, D), generator=g, device="cuda").to(bf)
+    cos, sin = (torch.from_numpy(t).cuda() for t in c4_tables(S, D))
+    qr, kr, o, dq, dk, dv, dq0, dk0 = (torch.empty_like(t) for t in (q, k, q, q, k, v, q, k))
+    lse = torch.empty((B, H, S), device="cuda")
+    lib, ctx = _lib.load(), runtime._context()
+    check(lib.hk_set_stream(ctx, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    t = {n: runtime.desc(x) for n, x in dict(q=q, k=k, v=v, do=do, cos=cos, sin=sin, qr=qr, kr=kr, o=o, lse=lse,
+                                              dq=dq, dk=dk, dv=dv, dq0=dq0, dk0=dk0).items()}
+    sc, z = ctypes.c_float(D ** -0.5), ctypes.c_uint64(0)
+
+    def step():
+        check(lib.hk_rotary_prefix(ctx, t["q"], t["cos"], t["sin"], D, 1, t["qr"]))
+        check(lib.hk_rotary_prefix(ctx, t["k"], t["cos"], t["sin"], D, 1, t["kr"]))
+        check(lib.hk_attention_forward(ctx, t["qr"], t["kr"], t["v"], sc, 1, z, z, t["o"], t["lse"]))
+        check(lib.hk_attention_backward(ctx, t["qr"], t["kr"], t["v"], t["o"], t["lse"], t["do"], sc, 1, z, z,
+                                        t["dq"], t["dk"], t["dv"]))
+        check(lib.hk_rotary_prefix_backward(ctx, t["dq"], t["cos"], t["sin"], D, 1, t["dq0"]))
+        check(lib.hk_rotary_prefix_backward(ctx, t["dk"], t["cos"], t["sin"], D, 1, t["dk0"]))
+    ms = time_gpu(step, iters)
+    return ms, 3.5 * 2 * B * H * S * S * D
 
 
 def bench_attention(iters=5):
@@ -542,8 +629,8 @@ def bench_widened():
 
     def add(name, ms, bound, algo, kernel, unit, key):
         val = algo / ms / 1e9 if unit == "TFLOP/s" else algo / ms / 1e6
-        out.append({"workload": name, "value": round(val, 2), "unit": unit, "ms": round(ms, 5),
-                    "roofline": roofline(bound, algo, ms, kernel, key)})
+        out.append({"workload": name, "value": round(val, 1), "unit": unit, "ms": round(ms, 4),
+                    "roofline": short_roofline(roofline(bound, algo, ms, kernel, key), kernel=False)})
 
     def guarded(name, fn):
         try:
@@ -558,7 +645,7 @@ def bench_widened():
         ends = HipRuntime.upload_group_ends([rows * (i + 1) for i in range(E)])
         y = HipRuntime.grouped_nt(a, w, ends)
         ms = time_gpu(lambda: HipRuntime.grouped_nt_into(a, w, ends, y))
-        add(f"(f) M-grouped NT GEMM (MoE): {E} experts x {rows} rows, K {K}, N {N}, BF16 out", ms, "mfma",
+        add(f"(f) MoE grouped NT GEMM {E}x{rows} rows, K {K}, N {N}", ms, "mfma",
             2 * E * rows * N * K, "gemm_nt_m16_kernel", "TFLOP/s", "grouped")
     guarded("(f) M-grouped NT GEMM", grouped)
 
@@ -567,7 +654,7 @@ def bench_widened():
         a = torch.randn((M, K), generator=g, device="cuda")
         b = torch.randn((K, N), generator=g, device="cuda")
         ms = time_gpu(lambda: HipRuntime.gemm_padded_bf16_fp32(a, b))
-        add(f"(f) padded BF16-compute GEMM F32 [{M},{K}]x[{K},{N}] (pad + GEMM + crop)", ms, "mfma", 2 * M * N * K,
+        add(f"(f) padded GEMM F32 {M}^3 (pad+GEMM+crop)", ms, "mfma", 2 * M * N * K,
             "pad_bf16+gemm+crop_f32", "TFLOP/s", "padded")
     guarded("(f) padded GEMM", padded)
 
@@ -577,10 +664,10 @@ def bench_widened():
     def softmax():
         y = HipRuntime.softmax(x)
         ms = time_gpu(lambda: HipRuntime.softmax(x))
-        add(f"(f) softmax rows F32 [{R},{C}]", ms, "hbm", 2 * 4 * R * C, "softmax", "GB/s", "softmax")
+        add(f"(f) softmax F32 [{R},{C}]", ms, "hbm", 2 * 4 * R * C, "softmax", "GB/s", "softmax")
         dy = torch.randn((R, C), generator=g, device="cuda")
         ms = time_gpu(lambda: HipRuntime.softmax_backward(y, dy))
-        add(f"(f) softmax backward rows F32 [{R},{C}]", ms, "hbm", 3 * 4 * R * C, "softmax_backward", "GB/s",
+        add(f"(f) softmax bwd F32 [{R},{C}]", ms, "hbm", 3 * 4 * R * C, "softmax_backward", "GB/s",
             "softmax_bwd")
     guarded("(f) softmax rows", softmax)
 
@@ -592,7 +679,7 @@ def bench_widened():
             lp = HipRuntime.log_softmax(x)
             return HipRuntime.nll_loss(lp, labels, wt, LossReduction.Mean)
         ms = time_gpu(ce)
-        add(f"(f) cross entropy fwd F32 [{R},{C}] (log-softmax + NLLLoss mean, INT64 labels)", ms, "hbm",
+        add(f"(f) cross entropy F32 [{R},{C}]", ms, "hbm",
             2 * 4 * R * C + 8 * R + 4 * C, "softmax+nll_loss", "GB/s", "cross_entropy")
     guarded("(f) cross entropy", cross_entropy)
 
@@ -601,10 +688,10 @@ def bench_widened():
         gate = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
         up = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_gpu(lambda: HipRuntime.silu_mul(gate, up))
-        add(f"(f) SwiGLU silu_mul BF16 [{T},{F}]", ms, "hbm", 3 * 2 * T * F, "silu_mul_kernel", "GB/s", "silu_mul")
+        add(f"(f) silu_mul BF16 [{T},{F}]", ms, "hbm", 3 * 2 * T * F, "silu_mul_kernel", "GB/s", "silu_mul")
         gr = torch.randn((T, F), generator=g, device="cuda").to(torch.bfloat16)
         ms = time_gpu(lambda: HipRuntime.silu_mul_backward(gate, up, gr))
-        add(f"(f) SwiGLU silu_mul backward BF16 [{T},{F}]", ms, "hbm", 5 * 2 * T * F, "silu_mul_bwd_kernel", "GB/s",
+        add(f"(f) silu_mul bwd BF16 [{T},{F}]", ms, "hbm", 5 * 2 * T * F, "silu_mul_bwd_kernel", "GB/s",
             "silu_mul_bwd")
     guarded("(f) SwiGLU", swiglu)
 
@@ -614,7 +701,7 @@ def bench_widened():
         res = torch.randn((T, H), generator=g, device="cuda").to(torch.bfloat16)
         bb = torch.randn((H,), generator=g, device="cuda")
         ms = time_gpu(lambda: HipRuntime.bias_add(xb, bb, res))
-        add(f"(f) bias + residual add BF16 [{T},{H}], F32 bias", ms, "hbm", 3 * 2 * T * H + 4 * H, "bias_add_kernel",
+        add(f"(f) bias+residual add BF16 [{T},{H}]", ms, "hbm", 3 * 2 * T * H + 4 * H, "bias_add_kernel",
             "GB/s", "bias_add")
     guarded("(f) bias add", bias)
 
@@ -623,7 +710,7 @@ def bench_widened():
         table = torch.randn((V, H), generator=g, device="cuda").to(torch.bfloat16)
         ids = torch.randint(0, V, (T,), generator=g, device="cuda", dtype=torch.int64)
         ms = time_gpu(lambda: HipRuntime.embedding(table, ids))
-        add(f"(f) embedding gather BF16 table [{V},{H}], {T} INT64 IDs", ms, "hbm", 2 * 2 * T * H + 8 * T,
+        add(f"(f) embedding gather [{V},{H}] BF16, {T} IDs", ms, "hbm", 2 * 2 * T * H + 8 * T,
             "embedding_gather_kernel", "GB/s", "embedding")
     guarded("(f) embedding", embedding)
     return out
@@ -656,16 +743,86 @@ def bench_decoder(steps=5, warmup=2):
     return cfg, event_ms(fw), event_ms(bw)
 
 
-def c5_line(steps=5, warmup=2):
+def cpu_baseline_decoder(tokens=32):
+    """The C5 layer forward + backward composed from the oracle's restatements of the reference's
+    host loops (embedding, the FP32 row programs of RMSNorm, the f32 sequential-k GEMM, the
+    rotary program, the f64 attention with BF16 rounding points, SiLU-mul, the dense embedding
+    gradient) on one sequence of `tokens` positions with C5's widths and N(0, 0.02) weights,
+    timed on the host. The rate is tokens per second of that sample (the layer's cost is nearly
+    linear in tokens: 96 % of its flops are the projections)."""
+    import numpy as np
+    import oracle
+    from rust_ascend_hip import DecoderConfig
+    threads = cpu_threads()
+    oracle.set_threads(threads)
+    c = DecoderConfig()
+    T, Hd, F, D, hq, hkv = tokens, c.hidden, c.ffn, c.head_dim, c.heads, c.kv_heads
+    W = (hq + 2 * hkv) * D
+    rng = np.random.default_rng(5)
+
+    block = oracle.bf16_round(rng.standard_normal(1 << 20, dtype=np.float32) * np.float32(c.init_std))
+
+    def init(*shape):  # N(0, 0.02) BF16 values, a 1M-value block repeated (the timing does not depend on them)
+        return np.resize(block, shape)
+    table, wqkv, wo = init(c.vocab, Hd), init(W, Hd), init(Hd, Hd)
+    wg, wu, wd = init(F, Hd), init(F, Hd), init(Hd, F)
+    w1 = w2 = np.ones(Hd, np.float32)
+    ids = rng.integers(0, c.vocab, T)
+    dy = oracle.bf16_round(rng.standard_normal((T, Hd), dtype=np.float32))
+    cos, sin = oracle.rope_tables(np.arange(T), D, c.theta)
+    cos, sin = cos[None, None], sin[None, None]
+    heads = lambda x, n: np.ascontiguousarray(x.reshape(1, T, n, D).transpose(0, 2, 1, 3))
+    rows = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3).reshape(T, -1))
+    t0 = time.perf_counter()
+    x0 = oracle.embedding(table, ids)
+    n1, r1 = oracle.rms_norm_lanes_f32(x0, w1, c.eps)
+    qkv = oracle.gemm_f32(n1, wqkv, 0, 1)
+    q = oracle.rotary_prefix(heads(qkv[:, :hq * D], hq), cos, sin, D, 1)
+    k = oracle.rotary_prefix(heads(qkv[:, hq * D:(hq + hkv) * D], hkv), cos, sin, D, 1)
+    v = heads(qkv[:, (hq + hkv) * D:], hkv)
+    o = rows(oracle.attention_f64(q, k, v, scale=D ** -0.5, causal=True, want_grads=False)["out"]).astype(np.float32)
+    h1 = x0 + oracle.gemm_f32(o, wo, 0, 1)
+    n2, r2 = oracle.rms_norm_lanes_f32(h1, w2, c.eps)
+    gt, up = oracle.gemm_f32(n2, wg, 0, 1), oracle.gemm_f32(n2, wu, 0, 1)
+    m = oracle.silu_mul_f64(gt, up).astype(np.float32)
+    oracle.gemm_f32(m, wd, 0, 1)  # y = h1 + this
+    dm = oracle.gemm_f32(dy, wd, 0, 0)
+    oracle.gemm_f32(dy, m, 1, 0)                                   # dWd
+    dgt, dup = (x.astype(np.float32) for x in oracle.silu_mul_backward_f64(gt, up, dm))
+    dn2 = oracle.gemm_f32(dgt, wg, 0, 0) + oracle.gemm_f32(dup, wu, 0, 0)
+    oracle.gemm_f32(dgt, n2, 1, 0), oracle.gemm_f32(dup, n2, 1, 0)  # dWg, dWu
+    dh1 = oracle.rms_norm_backward_lanes_f32(h1, w2, dn2, r2)[0] + dy
+    do = oracle.gemm_f32(dh1, wo, 0, 0)
+    oracle.gemm_f32(dh1, o, 1, 0)                                   # dWo
+    g = oracle.attention_f64(q, k, v, heads(do, hq), scale=D ** -0.5, causal=True)
+    dq = oracle.rotary_prefix(g["dq"], cos, sin, D, 1, backward=True)
+    dk = oracle.rotary_prefix(g["dk"], cos, sin, D, 1, backward=True)
+    dqkv = np.concatenate([rows(dq), rows(dk), rows(g["dv"].astype(np.float32))], axis=1)
+    dn1 = oracle.gemm_f32(dqkv, wqkv, 0, 0)
+    oracle.gemm_f32(dqkv, n1, 1, 0)                                 # dWqkv
+    dx0 = oracle.rms_norm_backward_lanes_f32(x0, w1, dn1, r1)[0] + dh1
+    oracle.embedding_backward_f64(dx0, ids, c.vocab)                # dtable (dense)
+    t = time.perf_counter() - t0
+    return {"value": round(T / t, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 x {T} tokens"}
+
+
+def c5_line(steps=5, warmup=2, cpu=True):
     cfg, f_ms, b_ms = bench_decoder(steps, warmup)
     step_ms = f_ms + b_ms
     fl = cfg.flops_per_step()
-    return {"workload": "C5 Llama decoder layer fwd+bwd: hidden 4096, 32/8 heads, SwiGLU 14336, "
-                        "B2 x S2048, vocab 32000, BF16",
+    tflops = fl["total"] / (step_ms * 1e-3) / 1e12
+    line = {"workload": "C5 decoder layer fwd+bwd",
             "value": round(cfg.tokens / (step_ms * 1e-3), 1), "unit": "tokens/s",
             "ms": round(step_ms, 4), "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
-            "model_TFLOPs": round(fl["total"] / (step_ms * 1e-3) / 1e12, 1),
-            "frac_of_bf16_peak": round(fl["total"] / (step_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+            "model_TFLOPs": round(tflops, 1),
+            # the layer is GEMM-dominated (96 % of its model flops are the projections): its
+            # roofline is the model flops over the step against the BF16 MFMA peak
+            "roofline": {"kernel": "gemm_nt_m16_kernel (96 % of the flops)", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "traffic_MB": None}}
+    if cpu:
+        line["cpu_baseline"] = short_cpu(cpu_baseline_decoder())
+    return line
 
 
 def main():
@@ -716,7 +873,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) BF16 x and dy, F32 weight 1+N(0,0.1), resident in HBM)",
+        "data": "synthetic, seeded, resident in HBM (x, dy N(0,1) BF16; weight 1+N(0,0.1) F32)",
         "config": {"workload": "C2 RMSNorm fwd+bwd: x[16384,4096] BF16, weight F32, eps 1e-6, dX BF16, dW F32",
                    "rows": C2_ROWS, "width": C2_WIDTH, "bytes_per_step": step_bytes,
                    "fwd_ms": round(fwd_ms, 5), "bwd_ms": round(bwd_ms, 5),
@@ -725,35 +882,44 @@ def main():
         "roofline": roofline("hbm", C2_BWD_BYTES, bwd_ms, "rms_bwd_split"),
     }
     if not args.no_secondary:
-        sec = []
-        for key in ("gemm8192_nt", "gemm8192_nn", "llama_up", "llama_down", "gemm4096_nt", "gemm1024_nt", "c1"):
+        # Ordered so that the lines of the BASELINE configs come last in the printed line.
+        sec = bench_widened()
+        try:
+            sec.append(c5_line(cpu=not args.no_cpu))
+        except Exception as exc:  # reported, never silently replaced by another path
+            sec.append({"workload": "C5 decoder layer", "error": str(exc)[:200]})
+        ms, algo = bench_rope()
+        sec.append({"workload": "C4 RoPE Q and K",
+                    "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 4),
+                    "roofline": short_roofline(roofline("hbm", algo, ms, "rope_pairs", "rope"))})
+        if not args.no_cpu:
+            sec[-1]["cpu_baseline"] = short_cpu(cpu_baseline_rope())
+        try:
+            f_ms, b_ms, ff, bf = bench_attention()
+            sec.append({"workload": "C4 attention fwd", "value": round(ff / f_ms / 1e9, 1), "unit": "TFLOP/s",
+                        "ms": round(f_ms, 4),
+                        "roofline": short_roofline(roofline("mfma", ff, f_ms, "attn_fwd_pp", "attn_fwd"))})
+            sec.append({"workload": "C4 attention bwd", "value": round(bf / b_ms / 1e9, 1), "unit": "TFLOP/s",
+                        "ms": round(b_ms, 4),
+                        "roofline": short_roofline(roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq_ds",
+                                                            "attn_bwd"))})
+            st_ms, st_fl = bench_c4_step()
+            sec.append({"workload": "C4 step: RoPE Q,K + attention fwd+bwd + RoPE bwd", "value": round(st_fl / st_ms / 1e9, 1), "unit": "TFLOP/s",
+                        "ms": round(st_ms, 4), "frac": round(st_fl / st_ms / 1e9 / BF16_PEAK_TFLOPS, 4)})
+            if not args.no_cpu:
+                sec[-1]["cpu_baseline"] = short_cpu(cpu_baseline_attention())
+        except Exception as exc:  # reported, never silently replaced by another path
+            sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
+        for key in ("c1", "gemm1024_nt", "gemm4096_nt", "llama_down", "llama_up", "gemm8192_nn", "gemm8192_nt"):
             m, n, k, ta, tb, name = GEMMS[key]
             ms = bench_gemm(m, n, k, ta, tb)
             flops = 2 * m * n * k
-            sec.append({"workload": name, "value": round(flops / ms / 1e9, 2), "unit": "TFLOP/s",
-                        "ms": round(ms, 5),
-                        "roofline": roofline("mfma", flops, ms, gemm_kernel_name(m, n, k, ta, tb), key)})
+            sec.append({"workload": name, "value": round(flops / ms / 1e9, 1), "unit": "TFLOP/s",
+                        "ms": round(ms, 4),
+                        "roofline": short_roofline(roofline("mfma", flops, ms, gemm_kernel_name(m, n, k, ta, tb),
+                                                            key))})
             if not args.no_cpu:
-                sec[-1]["cpu_baseline"] = cpu_baseline_gemm(m, n, k, ta, tb, CPU_ROWS.get(key))
-        ms, algo = bench_rope()
-        sec.append({"workload": "C4 RoPE split-half Q[4,32,4096,128] BF16, tables [1,1,4096,64]",
-                    "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 5),
-                    "roofline": roofline("hbm", algo, ms, "rope_pairs", "rope")})
-        try:
-            f_ms, b_ms, ff, bf = bench_attention()
-            sec.append({"workload": "C4 causal GQA attention fwd B4 S4096 Hq32 Hkv8 D128", "value": round(ff / f_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(f_ms, 5), "roofline": roofline("mfma", ff, f_ms, "attn_fwd_pp", "attn_fwd")})
-            sec.append({"workload": "C4 causal GQA attention bwd B4 S4096 Hq32 Hkv8 D128", "value": round(bf / b_ms / 1e9, 2),
-                        "unit": "TFLOP/s", "ms": round(b_ms, 5), "roofline": roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq_ds", "attn_bwd")})
-            if not args.no_cpu:
-                sec[-1]["cpu_baseline"] = sec[-2]["cpu_baseline"] = cpu_baseline_attention()
-        except Exception as exc:  # reported, never silently replaced by another path
-            sec.append({"workload": "C4 causal GQA attention", "error": str(exc)[:200]})
-        try:
-            sec.append(c5_line())
-        except Exception as exc:
-            sec.append({"workload": "C5 decoder layer", "error": str(exc)[:200]})
-        sec.extend(bench_widened())
+                sec[-1]["cpu_baseline"] = short_cpu(cpu_baseline_gemm(m, n, k, ta, tb, CPU_ROWS.get(key)))
         line["secondary"] = sec
     if args.copy_calibration:
         copy_calibration()

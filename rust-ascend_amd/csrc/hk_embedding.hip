@@ -12,15 +12,23 @@
 // it to the host (which turns it into an invalid-argument error after the call completes).
 //
 // Layout: the lookup copies rows with 16-byte (or the widest aligned) units, one wavefront per
-// token. The gradient is deterministic: a stable radix sort of (ID, position) pairs groups the
-// positions of each ID in increasing order, and one workgroup per table row sums its gradient rows
-// in that order in F32 (no floating-point atomics), writing every row of dW (zeros where no ID
-// falls). Work: the lookup moves 2 * H * sizeof(T) bytes per token; the gradient reads
-// H * sizeof(T) per token and writes V * H * sizeof(T).
+// token. The gradient is deterministic: a stable least-significant-digit radix sort of
+// (ID, position) pairs, 8-bit digits, groups the positions of each ID in increasing order, and one
+// workgroup per table row sums its gradient rows in that order in F32 (no floating-point
+// atomics), writing every row of dW (zeros where no ID falls). Each sort pass is three launches:
+// per-tile digit histograms (4096 positions per workgroup, LDS counters), an exclusive scan of
+// the histograms in digit-major order (the output slot of each digit's first element in each
+// tile), and a scatter that places every element at its digit's slot plus its rank among the
+// tile's earlier elements with the same digit (ballots within a wavefront, LDS counts across
+// wavefronts and rounds), so equal digits keep their position order. The row offsets of dW come
+// from per-ID counts (integer atomics) and the same scan. Work: the lookup moves
+// 2 * H * sizeof(T) bytes per token; the gradient reads H * sizeof(T) per token and writes
+// V * H * sizeof(T); the sort moves 16 bytes per token and pass.
 #include "hk_common.hpp"
 #include "hk_kernels.hpp"
 
-#include <hipcub/hipcub.hpp>
+#include <algorithm>
+#include <utility>
 
 namespace hk {
 
@@ -72,6 +80,140 @@ clear_counts_kernel(uint32_t* __restrict__ counts, int64_t n, int* __restrict__ 
 }
 
 
+// ---- grouping by ID: exclusive scan and a stable radix sort, hand-written for wave64
+
+constexpr int kScanThreads = 1024;
+constexpr int kScanItems = 4;
+constexpr int kScanTile = kScanThreads * kScanItems;  // elements per workgroup
+
+// out[i] = sum of in[j] for j < i within each tile of kScanTile elements (in may equal out); the
+// tile's total goes to tile_sums[blockIdx.x] when tile_sums is not null.
+__global__ void __launch_bounds__(kScanThreads)
+scan_tiles_kernel(const uint32_t* in, uint32_t* out, int64_t n, uint32_t* __restrict__ tile_sums) {
+    __shared__ uint32_t wave_total[kScanThreads / kWave];
+    const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + static_cast<int64_t>(t) * kScanItems;
+    uint32_t v[kScanItems], ex[kScanItems];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j) {
+        v[j] = base + j < n ? in[base + j] : 0u;
+        ex[j] = sum;
+        sum += v[j];
+    }
+    uint32_t incl = sum;  // inclusive scan of the threads' sums within the wavefront
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += y;
+    }
+    if (lane == kWave - 1) wave_total[w] = incl;
+    __syncthreads();
+    uint32_t before = incl - sum;
+    for (int ww = 0; ww < w; ++ww) before += wave_total[ww];
+#pragma unroll
+    for (int j = 0; j < kScanItems; ++j)
+        if (base + j < n) out[base + j] = before + ex[j];
+    if (tile_sums != nullptr && t == kScanThreads - 1) tile_sums[blockIdx.x] = before + sum;
+}
+
+// Adds the scanned tile totals: out[i] += tile_base[i / kScanTile].
+__global__ void __launch_bounds__(kScanThreads)
+scan_add_kernel(uint32_t* __restrict__ out, int64_t n, const uint32_t* __restrict__ tile_base) {
+    const uint32_t add = tile_base[blockIdx.x];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+    for (int j = threadIdx.x; j < kScanTile; j += kScanThreads)
+        if (base + j < n) out[base + j] += add;
+}
+
+size_t scan_scratch_elems(int64_t n) {  // tile totals of every level, 64-entry aligned
+    size_t total = 0;
+    for (int64_t m = (n + kScanTile - 1) / kScanTile; m > 1; m = (m + kScanTile - 1) / kScanTile)
+        total += static_cast<size_t>((m + 63) / 64 * 64);
+    return total;
+}
+
+// Exclusive scan of n (< 2^31) counts whose total fits 32 bits.
+void scan_exclusive(const uint32_t* in, uint32_t* out, int64_t n, uint32_t* scratch, hipStream_t s) {
+    if (n <= 0) return;
+    const int64_t tiles = (n + kScanTile - 1) / kScanTile;
+    if (tiles == 1) {
+        hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanThreads), 0, s, in, out, n, nullptr);
+        return;
+    }
+    uint32_t* sums = scratch;
+    hipLaunchKernelGGL(scan_tiles_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kScanThreads), 0, s, in, out, n,
+                       sums);
+    scan_exclusive(sums, sums, tiles, scratch + (tiles + 63) / 64 * 64, s);
+    hipLaunchKernelGGL(scan_add_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kScanThreads), 0, s, out, n, sums);
+}
+
+constexpr int kSortThreads = 256;
+constexpr int kSortWaves = kSortThreads / kWave;
+constexpr int kSortRounds = 16;
+constexpr int kSortTile = kSortThreads * kSortRounds;  // positions per workgroup
+constexpr int kDigits = 256;
+
+// hist[d * tiles + b] = how many keys of tile b have digit d ((key >> shift) & 255).
+__global__ void __launch_bounds__(kSortThreads)
+digit_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift, uint32_t* __restrict__ hist, int tiles) {
+    __shared__ uint32_t h[kDigits];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+    for (int r = 0; r < kSortRounds; ++r) {
+        const int64_t i = base + r * kSortThreads + threadIdx.x;
+        if (i < n) atomicAdd(&h[(keys[i] >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    hist[static_cast<int64_t>(threadIdx.x) * tiles + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter of one pass: element i of tile b (positions in order, 256 per round) goes to
+// slot[d][b] + (elements of tile b before i with digit d). Within a round, a wavefront ranks its
+// lanes by eight ballots (the lanes sharing the digit, counted below the lane); the wavefronts
+// before it and the rounds before this one are added through LDS counts.
+__global__ void __launch_bounds__(kSortThreads)
+digit_scatter_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restrict__ vals, int64_t n, int shift,
+                     const uint32_t* __restrict__ slot, int tiles, uint32_t* __restrict__ keys_out,
+                     uint32_t* __restrict__ vals_out) {
+    __shared__ uint32_t next[kDigits];                 // this tile's next free slot of each digit
+    __shared__ uint32_t wave_count[kSortWaves][kDigits];
+    const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    next[t] = slot[static_cast<int64_t>(t) * tiles + blockIdx.x];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+    for (int r = 0; r < kSortRounds; ++r) {
+#pragma unroll
+        for (int ww = 0; ww < kSortWaves; ++ww) wave_count[ww][t] = 0;
+        __syncthreads();
+        const int64_t i = base + r * kSortThreads + t;
+        const bool active = i < n;
+        const uint32_t key = active ? keys[i] : 0u;
+        const uint32_t d = (key >> shift) & 255u;
+        uint64_t peers = __ballot(active);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const bool bit = (d >> b) & 1u;
+            const uint64_t set = __ballot(bit);
+            peers &= bit ? set : ~set;
+        }
+        const uint64_t below = peers & ((uint64_t{1} << lane) - 1);
+        if (active && below == 0) wave_count[w][d] = static_cast<uint32_t>(__popcll(peers));
+        __syncthreads();
+        if (active) {
+            uint32_t at = next[d] + static_cast<uint32_t>(__popcll(below));
+            for (int ww = 0; ww < w; ++ww) at += wave_count[ww][d];
+            keys_out[at] = key;
+            vals_out[at] = vals[i];
+        }
+        __syncthreads();
+        uint32_t add = 0;
+#pragma unroll
+        for (int ww = 0; ww < kSortWaves; ++ww) add += wave_count[ww][t];
+        next[t] += add;  // read by the next round after its first barrier
+    }
+}
+
 // One workgroup per table row v: the positions of ID v are sorted[offsets[v] .. + counts[v]).
 template <typename T>
 __global__ void __launch_bounds__(kEmbThreads)
@@ -115,9 +257,7 @@ embedding_dense_grad_kernel(const T* __restrict__ grad, const uint32_t* __restri
 // Workspace carve-up (256-byte aligned pieces).
 struct EmbWs {
     int* flag;
-    uint32_t *keys, *pos, *keys_sorted, *pos_sorted, *counts, *offsets;
-    void* cub;
-    size_t cub_bytes;
+    uint32_t *keys, *pos, *keys_alt, *pos_alt, *counts, *offsets, *hist, *scan;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
@@ -128,15 +268,11 @@ int key_bits(int64_t vocab) {  // bits holding keys 0..vocab (vocab itself marks
     return b;
 }
 
-size_t cub_bytes_for(int64_t tokens, int64_t vocab) {
-    size_t sort_bytes = 0, scan_bytes = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
-                                             static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
-                                             static_cast<uint32_t*>(nullptr), static_cast<int>(tokens), 0,
-                                             key_bits(vocab));
-    (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<const uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr), static_cast<int>(vocab + 1));
-    return sort_bytes > scan_bytes ? sort_bytes : scan_bytes;
+int64_t sort_tiles(int64_t tokens) { return (tokens + kSortTile - 1) / kSortTile; }
+
+size_t scan_bytes_for(int64_t tokens, int64_t vocab) {
+    const int64_t hist = kDigits * std::max<int64_t>(sort_tiles(tokens), 1);
+    return align256(4 * std::max(scan_scratch_elems(hist), scan_scratch_elems(vocab + 1)) + 256);
 }
 
 EmbWs carve(void* base, int64_t tokens, int64_t vocab) {
@@ -147,13 +283,31 @@ EmbWs carve(void* base, int64_t tokens, int64_t vocab) {
     const size_t tok = align256(static_cast<size_t>(tokens) * 4), voc = align256(static_cast<size_t>(vocab + 1) * 4);
     w.keys = reinterpret_cast<uint32_t*>(p); p += tok;
     w.pos = reinterpret_cast<uint32_t*>(p); p += tok;
-    w.keys_sorted = reinterpret_cast<uint32_t*>(p); p += tok;
-    w.pos_sorted = reinterpret_cast<uint32_t*>(p); p += tok;
+    w.keys_alt = reinterpret_cast<uint32_t*>(p); p += tok;
+    w.pos_alt = reinterpret_cast<uint32_t*>(p); p += tok;
     w.counts = reinterpret_cast<uint32_t*>(p); p += voc;
     w.offsets = reinterpret_cast<uint32_t*>(p); p += voc;
-    w.cub = p;
-    w.cub_bytes = cub_bytes_for(tokens, vocab);
+    w.hist = reinterpret_cast<uint32_t*>(p); p += align256(static_cast<size_t>(kDigits * sort_tiles(tokens)) * 4);
+    w.scan = reinterpret_cast<uint32_t*>(p);
     return w;
+}
+
+// Stable sort of (keys, pos) by the low `bits` bits of the keys, 8 bits per pass; returns the
+// buffers that hold the result (the input pair or the alternate pair).
+void sort_pairs(EmbWs& w, int64_t tokens, int bits, hipStream_t s, uint32_t** keys_out, uint32_t** pos_out) {
+    uint32_t *k0 = w.keys, *p0 = w.pos, *k1 = w.keys_alt, *p1 = w.pos_alt;
+    const int64_t tiles = sort_tiles(tokens);
+    for (int shift = 0; shift < bits; shift += 8) {
+        hipLaunchKernelGGL(digit_hist_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kSortThreads), 0, s, k0, tokens,
+                           shift, w.hist, static_cast<int>(tiles));
+        scan_exclusive(w.hist, w.hist, kDigits * tiles, w.scan, s);
+        hipLaunchKernelGGL(digit_scatter_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kSortThreads), 0, s, k0, p0,
+                           tokens, shift, w.hist, static_cast<int>(tiles), k1, p1);
+        std::swap(k0, k1);
+        std::swap(p0, p1);
+    }
+    *keys_out = k0;
+    *pos_out = p0;
 }
 
 template <typename Idx, typename U>
@@ -177,11 +331,11 @@ void gather_by_unit(const void* table, const void* ids, void* out, int64_t token
 }
 
 template <typename T>
-void launch_dense_grad(const void* grad, const EmbWs& w, void* dw, int64_t vocab, int64_t width, uint64_t padding,
-                       int scale, hipStream_t s) {
+void launch_dense_grad(const void* grad, const EmbWs& w, const uint32_t* pos_sorted, void* dw, int64_t vocab,
+                       int64_t width, uint64_t padding, int scale, hipStream_t s) {
     const bool vec = width % Chunk<T>::kPer == 0 && aligned16({grad, dw});
     hipLaunchKernelGGL(embedding_dense_grad_kernel<T>, dim3(static_cast<unsigned>(vocab)), dim3(kEmbThreads), 0, s,
-                       static_cast<const T*>(grad), w.pos_sorted, w.counts, w.offsets, static_cast<T*>(dw), width,
+                       static_cast<const T*>(grad), pos_sorted, w.counts, w.offsets, static_cast<T*>(dw), width,
                        padding, scale, vec);
 }
 
@@ -190,7 +344,7 @@ void launch_dense_grad(const void* grad, const EmbWs& w, void* dw, int64_t vocab
 size_t embedding_workspace_bytes(int64_t tokens, int64_t vocab, bool backward) {
     if (!backward) return 256;
     return 256 + 4 * align256(static_cast<size_t>(tokens) * 4) + 2 * align256(static_cast<size_t>(vocab + 1) * 4) +
-           align256(cub_bytes_for(tokens, vocab));
+           align256(static_cast<size_t>(kDigits * sort_tiles(tokens)) * 4) + scan_bytes_for(tokens, vocab);
 }
 
 hipError_t embedding(const void* table, int id_bytes, const void* ids, void* out, int64_t tokens, int64_t vocab,
@@ -216,18 +370,14 @@ hipError_t embedding_backward(int dtype, const void* grad, int id_bytes, const v
         else
             hipLaunchKernelGGL(embedding_keys_kernel<int32_t>, dim3(tgrid), dim3(kEmbThreads), 0, s,
                                static_cast<const int32_t*>(ids), tokens, vocab, w.keys, w.pos, w.counts, w.flag);
-        size_t cb = w.cub_bytes;
-        hipError_t e = hipcub::DeviceRadixSort::SortPairs(w.cub, cb, w.keys, w.keys_sorted, w.pos, w.pos_sorted,
-                                                          static_cast<int>(tokens), 0, key_bits(vocab), s);
-        if (e != hipSuccess) return e;
     }
-    size_t cb = w.cub_bytes;
-    hipError_t e = hipcub::DeviceScan::ExclusiveSum(w.cub, cb, w.counts, w.offsets, static_cast<int>(vocab + 1), s);
-    if (e != hipSuccess) return e;
+    uint32_t *keys_sorted = w.keys, *pos_sorted = w.pos;
+    if (tokens > 0) sort_pairs(w, tokens, key_bits(vocab), s, &keys_sorted, &pos_sorted);
+    scan_exclusive(w.counts, w.offsets, vocab + 1, w.scan, s);
     if (vocab > 0 && width > 0) {
-        if (dtype == 1) launch_dense_grad<_Float16>(grad, w, dw, vocab, width, padding, scale, s);
-        else if (dtype == 27) launch_dense_grad<uint16_t>(grad, w, dw, vocab, width, padding, scale, s);
-        else launch_dense_grad<float>(grad, w, dw, vocab, width, padding, scale, s);
+        if (dtype == 1) launch_dense_grad<_Float16>(grad, w, pos_sorted, dw, vocab, width, padding, scale, s);
+        else if (dtype == 27) launch_dense_grad<uint16_t>(grad, w, pos_sorted, dw, vocab, width, padding, scale, s);
+        else launch_dense_grad<float>(grad, w, pos_sorted, dw, vocab, width, padding, scale, s);
     }
     return hipGetLastError();
 }

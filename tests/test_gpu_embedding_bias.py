@@ -183,6 +183,47 @@ def test_embedding_backward_deterministic_and_repeated():
     close(host(a), want, 1e-5, 1e-4, "repeated IDs")
 
 
+def position_order_sums_f32(g, ids, vocab):
+    """dW in float32 with every row summed in increasing position order (what the kernel's
+    grouping promises), evaluated on the host one position at a time."""
+    ids = np.asarray(ids).reshape(-1)
+    g = np.asarray(g, np.float32).reshape(ids.size, -1)
+    dw = np.zeros((vocab, g.shape[1]), np.float32)
+    order = np.argsort(ids, kind="stable")  # positions of each ID, in increasing order
+    bounds = np.searchsorted(ids[order], np.arange(vocab + 1))
+    for v in np.unique(ids):
+        acc = np.zeros(g.shape[1], np.float32)
+        for p in order[bounds[v]:bounds[v + 1]]:
+            acc = acc + g[p]
+        dw[v] = acc
+    return dw
+
+
+@pytest.mark.parametrize("tokens,vocab", [(70000, 5000), (20000, (1 << 20) + 3), (4097, 40000), (1, 1)])
+def test_embedding_backward_groups_in_position_order(tokens, vocab):
+    """The grouping by ID is a stable radix sort (8-bit digits): 70000 positions span 18 sort
+    tiles and a two-level scan of the digit histograms; a 2^20 + 3 row table needs three digit
+    passes (the result lands in the other buffer pair); 40001 count entries take a multi-tile
+    scan. Gradient rows are F32 with magnitudes spread over 2^-20 .. 2^20, so the F32 sum of a row
+    depends on the order of its positions: the result must equal, bit for bit, the sums taken in
+    increasing position order."""
+    rng = np.random.default_rng(tokens + vocab)
+    hot = rng.integers(0, vocab, 16)
+    ids = np.where(rng.random(tokens) < 0.5, hot[rng.integers(0, 16, tokens)], rng.integers(0, vocab, tokens))
+    width = 64
+    g = (rng.standard_normal((tokens, width)) * np.exp2(rng.integers(-20, 21, (tokens, 1)))).astype(np.float32)
+    ids_t = torch.from_numpy(ids.astype(np.int64)).to(DEV)
+    print(f"embedding backward grouping: {tokens} positions, {vocab} rows", flush=True)
+    dw = HipRuntime.embedding_backward(dev_f32(g), ids_t, vocab)
+    used = np.unique(ids)
+    want = position_order_sums_f32(g, ids, vocab)
+    got = dw[torch.from_numpy(used).to(DEV)].cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.int32), want[used].view(np.int32))
+    assert int(torch.count_nonzero(dw).item()) == np.count_nonzero(want)
+    again = HipRuntime.embedding_backward(dev_f32(g), ids_t, vocab)
+    assert torch.equal(dw, again)
+
+
 def test_embedding_out_of_range_ids_error_and_recover():
     weights, _, _ = embedding_reference_inputs()
     w = dev_f32(weights)
