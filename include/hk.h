@@ -421,6 +421,37 @@ hk_status hk_qkv_rope_split(hk_context* ctx, const hk_tensor* qkv, const hk_tens
 /* The transpose: dQ, dK (rotated back) and dV -> dqkv [B, S, (Hq + 2 Hkv) D]. */
 hk_status hk_qkv_rope_merge(hk_context* ctx, const hk_tensor* dq, const hk_tensor* dk, const hk_tensor* dv,
                             const hk_tensor* cos, const hk_tensor* sin, int32_t layout, hk_tensor* dqkv);
+/* The fused QKV projection with RoPE in the GEMM's epilogue: x [B*S, H] (or [B, S, H]) times
+ * W [(Hq + 2 Hkv) D, H]^T (BF16, FP32 accumulation), each 128-wide head of the product written
+ * straight to its plane q [B, Hq, S, D] or k, v [B, Hkv, S, D], Q and K rotated on the way (tables
+ * cos/sin [S, D/2] F32 indexed by s, either layout). D = 128 and H % 8 == 0. Bit-identical to
+ * hk_gemm_into (NT, BF16 output) followed by hk_qkv_rope_split: each value is rounded to BF16 before
+ * its rotation, as the product's storage rounds it there. It composes the reference's linear NT
+ * (runtime/matrix.rs:47-74) and rotary_prefix (rotary_programs.rs:47-97, 101-156) on the rows of
+ * the fused projection, in one launch. */
+hk_status hk_qkv_projection_rope(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, const hk_tensor* cos,
+                                 const hk_tensor* sin, int32_t layout, hk_tensor* q, hk_tensor* k, hk_tensor* v);
+/* y [M, N] = residual + x [M, K] W [N, K]^T (BF16, FP32 accumulation): the product is rounded to BF16
+ * and the residual added in F32 and rounded, in the GEMM's epilogue. Bit-identical to hk_gemm_into
+ * (NT, BF16 output) followed by hk_bias_add(product, no bias, residual); the reference's linear
+ * (runtime/matrix.rs:47-74) and residual add (src/nn/affine.rs:14-25) in one launch. N % 16 == 0,
+ * K % 8 == 0. */
+hk_status hk_linear_residual(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, const hk_tensor* residual,
+                             hk_tensor* y);
+/* SwiGLU's two projections as one GEMM: x [T, H] times W_gu [2F, H]^T, whose rows interleave the gate
+ * and up weights in blocks of 16 (row 32 b + r is gate row 16 b + r for r < 16, up row 16 b + r - 16
+ * otherwise), writes gate and up [T, F] (BF16) and act = SiLU(gate) * up [T, F] from the BF16 values
+ * in the epilogue. Bit-identical to the two projections (hk_gemm_into, NT) and hk_silu_mul; the
+ * reference's swiglu_bf16_fp32 (src/nn/feed_forward.rs:24-42, MapProgram::SiluMul,
+ * rust-ascend-compiler/src/ascend/programs.rs:21-46) in one launch. F % 16 == 0, H % 8 == 0. */
+hk_status hk_swiglu_projection(hk_context* ctx, const hk_tensor* x, const hk_tensor* w_gu, hk_tensor* gate,
+                               hk_tensor* up, hk_tensor* act);
+/* The SwiGLU backward fused into the down projection's input gradient: dM = dY [T, H] Wd [H, F]
+ * (rounded to BF16 as hk_linear_nt_backward stores it) and hk_silu_mul_backward(gate, up, dM) in the
+ * epilogue, written as dgu [T, 2F] interleaved like W_gu's rows, so that dX = dgu W_gu and
+ * dW_gu = dgu^T X are single GEMMs (hk_linear_nt_backward(x, w_gu, dgu)). */
+hk_status hk_swiglu_projection_backward(hk_context* ctx, const hk_tensor* dy, const hk_tensor* wd,
+                                        const hk_tensor* gate, const hk_tensor* up, hk_tensor* dgu);
 /* x [B, H, S, D] -> y [B, S, H D] (attention output into token rows), and the reverse; D % 8 == 0. */
 hk_status hk_heads_to_rows(hk_context* ctx, const hk_tensor* x, hk_tensor* y);
 hk_status hk_rows_to_heads(hk_context* ctx, const hk_tensor* x, hk_tensor* y);
@@ -562,6 +593,18 @@ hk_status hk_attention_backward(hk_context* ctx, const hk_tensor* q, const hk_te
                                 const hk_tensor* dout, float scale, int32_t causal,
                                 uint64_t query_start, uint64_t key_start,
                                 hk_tensor* dq, hk_tensor* dk, hk_tensor* dv);
+/* hk_attention_backward for a decoder layer whose Q, K and V come from one fused projection with
+ * RoPE (hk_qkv_projection_rope): dQ, dK and dV are written straight into the projection's gradient
+ * rows dqkv [B, S, (Hq + 2 Hkv) D] (BF16), dQ and dK rotated back by RoPE's transpose (tables
+ * cos/sin [S, D/2] F32, either layout), instead of into planes. D = 64 or 128 and M = N = S.
+ * Bit-identical to hk_attention_backward with BF16 gradients followed by hk_qkv_rope_merge: each
+ * gradient is rounded to BF16 before its rotation, as the planes would store it. No reference
+ * counterpart as one call: it composes the attention backward (src/nn/attention.rs:69-80) with
+ * rotary_prefix_backward (rotary_programs.rs:47-97) on the fused projection's rows. */
+hk_status hk_attention_backward_qkv_rows(hk_context* ctx, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                         const hk_tensor* o, const hk_tensor* lse, const hk_tensor* dout, float scale,
+                                         int32_t causal, uint64_t query_start, uint64_t key_start, const hk_tensor* cos,
+                                         const hk_tensor* sin, int32_t layout, hk_tensor* dqkv);
 
 #ifdef __cplusplus
 }

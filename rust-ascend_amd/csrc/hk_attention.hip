@@ -230,7 +230,7 @@ __device__ __forceinline__ void tile_softmax(f32x16_t (&s)[2], int lane, float c
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mt = fmaxf(mt, s[tt][v]);
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64)) * c;
+    mt = pair32_max(mt) * c;
     if (__any(mt > m_run + kStaleMax)) {
         const float m_new = fmaxf(m_run, mt);
         const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
@@ -390,7 +390,7 @@ attn_fwd(FwdArgs a) {
     }
 
     // epilogue: O[q][d] = O^T / l ; lse = (m + log2 l) ln 2
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_tot = pair32_sum(l_run);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < a.m) {
         const int64_t obase = (bh * a.m + my_q) * D;
@@ -668,9 +668,8 @@ attn_fwd_pp(FwdArgs a) {
             for (int ks = 0; ks < 4; ++ks) pb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
         }
     };
-    // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j. Always the full phase: a P of zeros (no
-    // previous tile, or one this wave skips) adds nothing, and scores of a skipped or
-    // past-the-end tile are not used.
+    // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j (mfma_step below drops the halves that feed
+    // nothing).
     // Loads of half-step 2j: K_{j+1} and V_j (tiles that reach past n take the clamping path).
     auto tile_loads = [&](int j) {
         const bool k_next = j + 1 < ntiles, v_cur = j < ntiles;
@@ -708,12 +707,22 @@ attn_fwd_pp(FwdArgs a) {
             }
         }
     };
+    // MFMA phase j, left out when neither half feeds anything: P_{j-1} V_{j-1} is needed only when
+    // tile j-1 exists and this wave did not skip it (else P is zero), S_j only when tile j exists and
+    // this wave does not skip it (else its scores are not used). Causal waves skip the workgroup's
+    // tiles past their own diagonal (up to 3.5 of them for the first wave of a 256-query block);
+    // the results are unchanged. skip() is uniform per wave, so the branch is a scalar one. (Phase
+    // bodies with only one of the halves, as separate copies, pushed the kernel into spills.)
+    auto mfma_step = [&](int j) {
+        const bool pv = j >= 1 && !skip(j - 1), qk = j < ntiles && !skip(j);
+        if (pv || qk) mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
+    };
     // The barriers between half-steps wait for LDS accesses only (lds_barrier), so the tile
     // loads stay in flight from their half-step 2t to the end of 2t+1.
     if (group == 0) {
         for (int j = 0; j <= ntiles; ++j) {
             __builtin_amdgcn_s_setprio(1);  // half-step 2j
-            mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
+            mfma_step(j);
             __builtin_amdgcn_s_setprio(0);
             lds_barrier();
             if (j < ntiles) softmax(j);  // half-step 2j+1
@@ -724,7 +733,7 @@ attn_fwd_pp(FwdArgs a) {
         lds_barrier();  // half-step 0
         for (int j = 0; j <= ntiles; ++j) {
             __builtin_amdgcn_s_setprio(1);  // half-step 2j+1
-            mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
+            mfma_step(j);
             __builtin_amdgcn_s_setprio(0);
             landed();
             lds_barrier();
@@ -737,7 +746,7 @@ attn_fwd_pp(FwdArgs a) {
         landed();
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_tot = pair32_sum(l_run);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (my_q < a.m) {
         const int64_t obase = (bh * a.m + my_q) * D;
@@ -849,6 +858,16 @@ struct BwdArgs {
     // read by attn_bwd_dq_ds. Blocks whose pairs no query sees are left unwritten.
     uint16_t* ds;
     int64_t nkb, nsq;  // ceil(N / 32), ceil(M / 64)
+    // Rows output (a decoder layer's fused QKV gradient; M = N = S, D = 64 or 128): when rows is
+    // set, dQ, dK and dV go to BF16 token rows rows[(b S + s) row_w + col + d] instead of dq, dk
+    // and dv, col being the head's column in the fused projection (h D for Q, (Hq + kvh) D for K,
+    // (Hq + Hkv + kvh) D for V), with dQ and dK rotated back by RoPE's transpose (F32 tables
+    // rope_cos/rope_sin [S, D/2] indexed by s; layout 1 split-half, 0 interleaved).
+    uint16_t* rows;
+    int64_t row_w;
+    const float* rope_cos;
+    const float* rope_sin;
+    int rope_layout;
 };
 
 // Layout inside a dS block: four 1 KB chunks c = 2 qt + h, each holding 64 lanes x 16 bytes as
@@ -906,6 +925,60 @@ __device__ __forceinline__ void store_row4(void* base, bool bf16_out, int64_t ro
     } else {
         f32x4_t w = {v[0], v[1], v[2], v[3]};
         *reinterpret_cast<f32x4_t*>(static_cast<float*>(base) + row * D + d) = w;
+    }
+}
+
+// One lane's gradient row in the rows output: head dims 32 dt + 8 g4 + 4 lg + e of row s of batch b,
+// at column col of the token row. Each value is rounded to BF16 first (the planes' storage in the
+// unfused composition), then rotated back in F32 by rope_rotate and rounded again: the result is
+// bit-identical to writing the BF16 planes and running qkv_rope_merge on them. Split-half pairs
+// (d, d + D/2) sit in fragments dt and dt + DT/2 of the lane, interleaved ones next to each other.
+template <int D, int DT>
+__device__ __forceinline__ void store_grad_row(const BwdArgs& a, int64_t b, int64_t s, int64_t col, bool rotate,
+                                               int lg, const f32x16_t (&g)[DT]) {
+    static_assert(D == 32 * DT && DT % 2 == 0, "rows output for D = 64 or 128");
+    uint16_t* row = a.rows + (b * a.m + s) * a.row_w + col;
+    const float* ct = a.rope_cos + s * (D / 2);
+    const float* st = a.rope_sin + s * (D / 2);
+    if (!rotate) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * dt + 8 * g4 + 4 * lg;
+                *reinterpret_cast<u32x2_t*>(row + d) =
+                    u32x2_t{pack_bf16x2(g[dt][4 * g4], g[dt][4 * g4 + 1]), pack_bf16x2(g[dt][4 * g4 + 2], g[dt][4 * g4 + 3])};
+            }
+    } else if (a.rope_layout == 1) {
+#pragma unroll
+        for (int dt = 0; dt < DT / 2; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * dt + 8 * g4 + 4 * lg;
+                const f32x4_t c = *reinterpret_cast<const f32x4_t*>(ct + d);
+                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(st + d);
+                float ya[4], yb[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    rope_rotate<true>(round_bf16(g[dt][4 * g4 + e]), round_bf16(g[dt + DT / 2][4 * g4 + e]), c[e], sn[e],
+                                      ya[e], yb[e]);
+                *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(ya[0], ya[1]), pack_bf16x2(ya[2], ya[3])};
+                *reinterpret_cast<u32x2_t*>(row + d + D / 2) =
+                    u32x2_t{pack_bf16x2(yb[0], yb[1]), pack_bf16x2(yb[2], yb[3])};
+            }
+    } else {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * dt + 8 * g4 + 4 * lg;  // pairs (d, d + 1), (d + 2, d + 3)
+                const f32x2_t c = *reinterpret_cast<const f32x2_t*>(ct + d / 2);
+                const f32x2_t sn = *reinterpret_cast<const f32x2_t*>(st + d / 2);
+                float y[4];
+                rope_rotate<true>(round_bf16(g[dt][4 * g4]), round_bf16(g[dt][4 * g4 + 1]), c[0], sn[0], y[0], y[1]);
+                rope_rotate<true>(round_bf16(g[dt][4 * g4 + 2]), round_bf16(g[dt][4 * g4 + 3]), c[1], sn[1], y[2], y[3]);
+                *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+            }
     }
 }
 
@@ -1173,6 +1246,15 @@ attn_bwd_dkdv(BwdArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) dk[dt][v] *= a.scale;
+    if constexpr (D >= 64) {
+        if (a.rows != nullptr) {
+            if (my_key < a.n) {
+                store_grad_row<D, DT>(a, b, my_key, (a.heads + kvh) * D, true, lg, dk);
+                store_grad_row<D, DT>(a, b, my_key, (a.heads + a.kv_heads + kvh) * D, false, lg, dv);
+            }
+            return;
+        }
+    }
     if (my_key < a.n) {
         const int64_t row = static_cast<int64_t>(bkv) * a.n + my_key;
 #pragma unroll
@@ -1347,6 +1429,12 @@ attn_bwd_dq(BwdArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) dq[dt][v] *= a.scale;
+    if constexpr (D >= 64) {
+        if (a.rows != nullptr) {
+            if (my_q < a.m) store_grad_row<D, DT>(a, b, my_q, h * D, true, lg, dq);
+            return;
+        }
+    }
     if (my_q < a.m) {
         const int64_t row = static_cast<int64_t>(bh) * a.m + my_q;
 #pragma unroll
@@ -1513,6 +1601,12 @@ attn_bwd_dq_ds(BwdArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int v = 0; v < 16; ++v) dq[dt][v] *= a.scale;
+    if constexpr (D >= 64) {
+        if (a.rows != nullptr) {
+            if (my_q < a.m) store_grad_row<D, DT>(a, b, my_q, h * D, true, lg, dq);
+            return;
+        }
+    }
     if (my_q < a.m) {
         const int64_t row = static_cast<int64_t>(bh) * a.m + my_q;
 #pragma unroll
@@ -1552,7 +1646,7 @@ size_t stat_bytes(const AttnShape& sh) {  // row statistic and lse2, rounded to 
 template <int D>
 hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv, int dkv_bf16,
-                      float* stat, uint16_t* ds, hipStream_t s) {
+                      const AttnRowsOut* rows_out, float* stat, uint16_t* ds, hipStream_t s) {
     const int64_t rows = sh.batch * sh.heads * sh.m;
     constexpr int lanes = D / 8;
     const int64_t threads = rows * lanes;
@@ -1587,6 +1681,11 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
     a.ds = ds;
     a.nkb = (sh.n + 31) / 32;
     a.nsq = (sh.m + kQStep - 1) / kQStep;
+    a.rows = rows_out ? static_cast<uint16_t*>(rows_out->rows) : nullptr;
+    a.row_w = rows_out ? rows_out->row_w : 0;
+    a.rope_cos = rows_out ? rows_out->cos : nullptr;
+    a.rope_sin = rows_out ? rows_out->sin : nullptr;
+    a.rope_layout = rows_out ? rows_out->layout : 0;
     hipLaunchKernelGGL((attn_bwd_dkdv<D>), dim3(static_cast<unsigned>(sh.batch * sh.kv_heads * a.blocks)),
                        dim3(kThreads), 0, s, a);
     a.blocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
@@ -1629,14 +1728,15 @@ hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, 
 
 hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k, const void* v, const void* o,
                               const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv,
-                              int dkv_bf16, void* workspace, hipStream_t s) {
+                              int dkv_bf16, const AttnRowsOut* rows, void* workspace, hipStream_t s) {
     float* stat = static_cast<float*>(workspace);
     uint16_t* ds = sh.store_ds ? reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + stat_bytes(sh)) : nullptr;
+    if (rows && sh.d != 64 && sh.d != 128) return hipErrorInvalidValue;
     switch (sh.d) {
-        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
-        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
-        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
-        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, stat, ds, s);
+        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, nullptr, stat, ds, s);
+        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, nullptr, stat, ds, s);
+        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, rows, stat, ds, s);
+        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, rows, stat, ds, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -39,6 +39,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 __device__ __forceinline__ uint16_t f32_to_bf16(float a) {
     return static_cast<uint16_t>(pack_bf16x2(a, 0.0f) & 0xffffu);
 }
+// a rounded to BF16 (RNE) and widened back: the value a BF16 store and reload would give.
+__device__ __forceinline__ float round_bf16(float a) { return bf16lo(pack_bf16x2(a, 0.0f)); }
 
 // Element loaders/storers used by kernels templated on the storage type.
 template <typename T> struct Elem;
@@ -166,9 +168,12 @@ template <> struct Chunk<_Float16> {
 // expression order (rust-ascend-compiler/src/ascend/rotary_programs.rs:47-156): forward
 // y_a = a c - b s, y_b = b c + a s; backward (the transpose Jacobian) y_a = a c + b s,
 // y_b = b c - a s. Every kernel that rotates calls this, so fused and standalone RoPE agree bit
-// for bit.
+// for bit; the products are rounded before the sum (no contraction into fused multiply-adds,
+// which the compiler could otherwise choose differently in different kernels), as the
+// reference's separate vector multiply and add do.
 template <bool BWD>
 __device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, float& ya, float& yb) {
+#pragma clang fp contract(off)
     if constexpr (!BWD) {
         ya = a * c - b * s;
         yb = b * c + a * s;
@@ -176,6 +181,39 @@ __device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, 
         ya = a * c + b * s;
         yb = b * c - a * s;
     }
+}
+
+// SwiGLU gate in the reference's order of operations (rust-ascend-compiler/src/ascend/programs.rs:
+// 21-46): s = 1 / (1 + exp(-g)), y = (g s) u; backward ds = s (1 + g (1 - s)), dgate = (dy u) ds,
+// dup = dy (g s). Shared by the element-wise kernels and the GEMM epilogues that fuse them, with
+// no contraction into fused multiply-adds, so both give the same bits.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+#pragma clang fp contract(off)
+    const float s = 1.0f / (1.0f + expf(-g));
+    return (g * s) * u;
+}
+
+__device__ __forceinline__ void silu_mul_bwd1(float g, float u, float dy, float& dg, float& du) {
+#pragma clang fp contract(off)
+    const float s = 1.0f / (1.0f + expf(-g));
+    const float h = g * s;
+    const float ds = s * (1.0f + g * (1.0f - s));
+    dg = (dy * u) * ds;
+    du = dy * h;
+}
+
+// max / sum of x over lanes l and l ^ 32, on every lane: v_permlane32_swap exchanges the wave's two
+// 32-lane halves in the VALU (a few cycles) where __shfl_xor(x, 32) takes a ds_bpermute (~75 cycles
+// of LDS latency). The swap returns {lanes 0-31 of x twice, lanes 32-63 of x twice}, so lane l sees
+// x[l % 32] and x[l % 32 + 32]; both operations are symmetric, so every lane gets the same value
+// __shfl_xor would give it.
+__device__ __forceinline__ float pair32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // LDS vector types for the transposing reads (ds_read_b64_tr_b16).
@@ -202,16 +240,37 @@ __device__ __forceinline__ int64_t flat_begin(int threads) {
 }
 __device__ __forceinline__ int64_t flat_stride(int threads) { return static_cast<int64_t>(gridDim.x) * threads; }
 
-// Sum over the 64 lanes of a wavefront; every lane receives the total.
-// Butterfly order is fixed, so the result is deterministic.
+// x of lane l ^ 7 (ctrl 0x141, DPP row_half_mirror), l ^ 15 (0x140, row_mirror), l ^ 1 (0xB1,
+// quad_perm [1,0,3,2]) or l ^ 2 (0x4E, quad_perm [2,3,0,1]): VALU lane moves within 16-lane rows.
+template <int CTRL>
+__device__ __forceinline__ float lane_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum / max over the 64 lanes of a wavefront; every lane receives the same value. A butterfly over
+// the lane masks 32, 16 (the half swaps of v_permlane32_swap / v_permlane16_swap), 7, 15, 1, 2 (DPP
+// moves): six steps, each adding lane l's value and lane l ^ mask's in a commutative operation, so
+// partners compute the same value, and the masks span all 64 lanes, so every lane ends with the
+// total of one fixed association (deterministic). No LDS traffic: the ds_bpermute that __shfl_xor
+// compiles to costs ~75 cycles of latency per step, on the row's dependency chain in the row kernels.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    v = pair32_sum(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    v += lane_dpp<0x141>(v);
+    v += lane_dpp<0x140>(v);
+    v += lane_dpp<0xB1>(v);
+    v += lane_dpp<0x4E>(v);
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    v = pair32_max(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    v = fmaxf(v, lane_dpp<0x141>(v));
+    v = fmaxf(v, lane_dpp<0x140>(v));
+    v = fmaxf(v, lane_dpp<0xB1>(v));
+    v = fmaxf(v, lane_dpp<0x4E>(v));
     return v;
 }
 

@@ -1902,6 +1902,108 @@ hk_status hk_qkv_rope_merge(hk_context* h, const hk_tensor* dq, const hk_tensor*
                             const hk_tensor* cos, const hk_tensor* sin, int32_t layout, hk_tensor* dqkv) {
     return qkv_rope_common(h, true, dqkv, dq, dk, dv, cos, sin, layout);
 }
+hk_status hk_qkv_projection_rope(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* cos,
+                                 const hk_tensor* sin, int32_t layout, hk_tensor* q, hk_tensor* k, hk_tensor* v) {
+    const char* op = "qkv_projection_rope";
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "W") || !tensor_ok(q, "Q") || !tensor_ok(k, "K") || !tensor_ok(v, "V") ||
+        !tensor_ok(cos, "cos") || !tensor_ok(sin, "sin"))
+        return HK_INVALID_ARGUMENT;
+    if (layout != HK_ROTARY_INTERLEAVED && layout != HK_ROTARY_SPLIT_HALF)
+        return fail(HK_INVALID_ARGUMENT, "rotary layout must be 0 (Interleaved) or 1 (SplitHalf)");
+    if (!aligned_bf16({x, w, q, k, v}, op)) return HK_INVALID_ARGUMENT;
+    if (q->rank != 4 || k->rank != 4) return fail(HK_INVALID_ARGUMENT, "%s requires Q[B,Hq,S,D] and K/V[B,Hkv,S,D]", op);
+    const int64_t B = q->shape[0], Hq = q->shape[1], S = q->shape[2], D = q->shape[3], Hkv = k->shape[1];
+    if (B <= 0 || Hq <= 0 || Hkv <= 0 || S <= 0 || D != 128)
+        return fail(HK_INVALID_ARGUMENT, "%s requires positive dimensions and heads of width 128", op);
+    const int64_t W = (Hq + 2 * Hkv) * D;
+    const int64_t T = B * S;
+    const int64_t H = x->shape[x->rank - 1];
+    const bool x_ok = (x->rank == 2 && dims_are(x, {T, H})) || (x->rank == 3 && dims_are(x, {B, S, H}));
+    if (!dims_are(k, {B, Hkv, S, D}) || !dims_are(v, {B, Hkv, S, D}) || !x_ok || !dims_are(w, {W, H}))
+        return fail(HK_INVALID_ARGUMENT, "%s requires X [B*S,H] or [B,S,H], W [(Hq+2Hkv)*128,H], Q [B,Hq,S,128], "
+                                         "K/V [B,Hkv,S,128]", op);
+    if (cos->dtype != HK_F32 || sin->dtype != HK_F32 || !dims_are(cos, {S, D / 2}) || !dims_are(sin, {S, D / 2}) ||
+        reinterpret_cast<uintptr_t>(cos->data) % 16 != 0 || reinterpret_cast<uintptr_t>(sin->data) % 16 != 0)
+        return fail(HK_INVALID_ARGUMENT, "%s requires 16-byte aligned F32 cos/sin tables [S, D/2]", op);
+    if (!hk::qkv_rope_applies(T, H, W))
+        return fail(HK_INVALID_ARGUMENT, "%s requires H %% 8 == 0 and B*S*H, (Hq+2Hkv)*128*H below 2^30 elements", op);
+    if (!disjoint({q, k, v}, {x, w, cos, sin})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::gemm_qkv_rope(x->data, w->data, T, H, S, Hq, Hkv, static_cast<const float*>(cos->data),
+                                     static_cast<const float*>(sin->data), layout, q->data, k->data, v->data,
+                                     g.c->stream);
+    return complete(g.c, e, op, 1);
+}
+
+namespace {
+// Rank-2 BF16 [rows, cols] with cols % mult == 0 (rows any positive count).
+bool bf16_matrix(const hk_tensor* t, int64_t rows, int64_t cols) {
+    return t->dtype == HK_BF16 && t->rank == 2 && t->shape[0] == rows && t->shape[1] == cols;
+}
+}  // namespace
+
+hk_status hk_linear_residual(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* residual,
+                             hk_tensor* y) {
+    const char* op = "linear_residual";
+    if (!tensor_ok(x, "X") || !tensor_ok(w, "W") || !tensor_ok(residual, "residual") || !tensor_ok(y, "Y"))
+        return HK_INVALID_ARGUMENT;
+    if (x->rank != 2 || w->rank != 2) return fail(HK_INVALID_ARGUMENT, "%s requires X [M,K] and W [N,K]", op);
+    const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
+    if (!bf16_matrix(x, M, K) || !bf16_matrix(w, N, K) || !bf16_matrix(residual, M, N) || !bf16_matrix(y, M, N))
+        return fail(HK_INVALID_ARGUMENT, "%s requires BF16 X [M,K], W [N,K], residual and Y [M,N]", op);
+    if (!aligned_bf16({x, w, residual, y}, op)) return HK_INVALID_ARGUMENT;
+    if (M <= 0 || N % 16 != 0 || !hk::epi_applies(M, N, K))
+        return fail(HK_INVALID_ARGUMENT, "%s requires N %% 16 == 0, K %% 8 == 0 and M*K, N*K below 2^30 elements", op);
+    if (!disjoint({y}, {x, w, residual})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::gemm_residual(x->data, w->data, residual->data, y->data, M, N, K, g.c->stream);
+    return complete(g.c, e, op, 1);
+}
+
+hk_status hk_swiglu_projection(hk_context* h, const hk_tensor* x, const hk_tensor* w_gu, hk_tensor* gate,
+                               hk_tensor* up, hk_tensor* act) {
+    const char* op = "swiglu_projection";
+    if (!tensor_ok(x, "X") || !tensor_ok(w_gu, "W_gu") || !tensor_ok(gate, "gate") || !tensor_ok(up, "up") ||
+        !tensor_ok(act, "act"))
+        return HK_INVALID_ARGUMENT;
+    if (x->rank != 2 || w_gu->rank != 2) return fail(HK_INVALID_ARGUMENT, "%s requires X [T,H] and W_gu [2F,H]", op);
+    const int64_t T = x->shape[0], H = x->shape[1], F = w_gu->shape[0] / 2;
+    if (!bf16_matrix(x, T, H) || !bf16_matrix(w_gu, 2 * F, H) || !bf16_matrix(gate, T, F) || !bf16_matrix(up, T, F) ||
+        !bf16_matrix(act, T, F))
+        return fail(HK_INVALID_ARGUMENT, "%s requires BF16 X [T,H], W_gu [2F,H], gate/up/act [T,F]", op);
+    if (!aligned_bf16({x, w_gu, gate, up, act}, op)) return HK_INVALID_ARGUMENT;
+    if (T <= 0 || F <= 0 || F % 16 != 0 || !hk::epi_applies(T, 2 * F, H))
+        return fail(HK_INVALID_ARGUMENT, "%s requires F %% 16 == 0, H %% 8 == 0 and T*H, 2F*H below 2^30 elements", op);
+    if (!disjoint({gate, up, act}, {x, w_gu})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::gemm_swiglu(x->data, w_gu->data, gate->data, up->data, act->data, T, F, H, g.c->stream);
+    return complete(g.c, e, op, 1);
+}
+
+hk_status hk_swiglu_projection_backward(hk_context* h, const hk_tensor* dy, const hk_tensor* wd, const hk_tensor* gate,
+                                        const hk_tensor* up, hk_tensor* dgu) {
+    const char* op = "swiglu_projection_backward";
+    if (!tensor_ok(dy, "dY") || !tensor_ok(wd, "Wd") || !tensor_ok(gate, "gate") || !tensor_ok(up, "up") ||
+        !tensor_ok(dgu, "dgu"))
+        return HK_INVALID_ARGUMENT;
+    if (dy->rank != 2 || wd->rank != 2) return fail(HK_INVALID_ARGUMENT, "%s requires dY [T,H] and Wd [H,F]", op);
+    const int64_t T = dy->shape[0], H = dy->shape[1], F = wd->shape[1];
+    if (!bf16_matrix(dy, T, H) || !bf16_matrix(wd, H, F) || !bf16_matrix(gate, T, F) || !bf16_matrix(up, T, F) ||
+        !bf16_matrix(dgu, T, 2 * F))
+        return fail(HK_INVALID_ARGUMENT, "%s requires BF16 dY [T,H], Wd [H,F], gate/up [T,F], dgu [T,2F]", op);
+    if (!aligned_bf16({dy, wd, gate, up, dgu}, op)) return HK_INVALID_ARGUMENT;
+    if (T <= 0 || F <= 0 || F % 16 != 0 || !hk::epi_applies(T, F, H))
+        return fail(HK_INVALID_ARGUMENT, "%s requires F %% 16 == 0, H %% 8 == 0 and T*H, F*H below 2^30 elements", op);
+    if (!disjoint({dgu}, {dy, wd, gate, up})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    hipError_t e = hk::gemm_swiglu_backward(dy->data, wd->data, gate->data, up->data, dgu->data, T, F, H, g.c->stream);
+    return complete(g.c, e, op, 1);
+}
+
 hk_status hk_heads_to_rows(hk_context* h, const hk_tensor* x, hk_tensor* y) { return heads_rows_common(h, true, x, y); }
 hk_status hk_rows_to_heads(hk_context* h, const hk_tensor* x, hk_tensor* y) { return heads_rows_common(h, false, x, y); }
 
@@ -2435,28 +2537,51 @@ hk_status hk_attention_forward(hk_context* h, const hk_tensor* q, const hk_tenso
     return complete(g.c, e, "attention_forward", 1 + (sq.bytes ? 3 : 0));
 }
 
-hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
-                                const hk_tensor* o, const hk_tensor* lse, const hk_tensor* dout, float scale,
-                                int32_t causal, uint64_t qs, uint64_t ks, hk_tensor* dq, hk_tensor* dk,
-                                hk_tensor* dv) {
+namespace {
+// The checks and the call of hk_attention_backward and its rows form (`rows` set: dQ/dK/dV go
+// to the fused QKV gradient rows, and dq/dk/dv are null).
+hk_status attention_backward_common(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                    const hk_tensor* o, const hk_tensor* lse, const hk_tensor* dout, float scale,
+                                    int32_t causal, uint64_t qs, uint64_t ks, hk_tensor* dq, hk_tensor* dk,
+                                    hk_tensor* dv, const hk_tensor* cos, const hk_tensor* sin, int32_t layout,
+                                    hk_tensor* rows) {
     hk::AttnShape sh;
     hk_status st = attention_shape(q, k, v, scale, causal, qs, ks, &sh);
     if (st != HK_OK) return st;
-    if (!tensor_ok(o, "O") || !tensor_ok(lse, "lse") || !tensor_ok(dout, "dO") || !tensor_ok(dq, "dQ") ||
-        !tensor_ok(dk, "dK") || !tensor_ok(dv, "dV"))
-        return HK_INVALID_ARGUMENT;
+    if (!tensor_ok(o, "O") || !tensor_ok(lse, "lse") || !tensor_ok(dout, "dO")) return HK_INVALID_ARGUMENT;
     if ((o->dtype != HK_BF16 && o->dtype != HK_F32) || !same_shape(o, q) ||
         (dout->dtype != HK_BF16 && dout->dtype != HK_F32) || !same_shape(dout, q))
         return fail(HK_INVALID_ARGUMENT, "O and dO must be BF16 or F32 shaped like Q");
     if (lse->dtype != HK_F32 || lse->rank != 3 || lse->shape[0] != sh.batch || lse->shape[1] != sh.heads ||
         lse->shape[2] != sh.m)
         return fail(HK_INVALID_ARGUMENT, "lse must be F32 [B,Hq,M]");
-    if (!same_shape(dq, q) || !same_shape(dk, k) || !same_shape(dv, v))
-        return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must have the shapes of Q/K/V");
-    if ((dq->dtype != HK_F32 && dq->dtype != HK_BF16) || (dk->dtype != HK_F32 && dk->dtype != HK_BF16) ||
-        dv->dtype != dk->dtype)
-        return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must be F32 or BF16 (dK and dV alike)");
-    if (!disjoint({dq, dk, dv}, {q, k, v, o, lse, dout})) return HK_INVALID_ARGUMENT;
+    hk::AttnRowsOut rows_out{};
+    if (rows == nullptr) {
+        if (!tensor_ok(dq, "dQ") || !tensor_ok(dk, "dK") || !tensor_ok(dv, "dV")) return HK_INVALID_ARGUMENT;
+        if (!same_shape(dq, q) || !same_shape(dk, k) || !same_shape(dv, v))
+            return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must have the shapes of Q/K/V");
+        if ((dq->dtype != HK_F32 && dq->dtype != HK_BF16) || (dk->dtype != HK_F32 && dk->dtype != HK_BF16) ||
+            dv->dtype != dk->dtype)
+            return fail(HK_INVALID_ARGUMENT, "dQ/dK/dV must be F32 or BF16 (dK and dV alike)");
+        if (!disjoint({dq, dk, dv}, {q, k, v, o, lse, dout})) return HK_INVALID_ARGUMENT;
+    } else {
+        const char* op = "attention_backward_qkv_rows";
+        if (!tensor_ok(rows, "dQKV rows") || !tensor_ok(cos, "cos") || !tensor_ok(sin, "sin")) return HK_INVALID_ARGUMENT;
+        if (layout != HK_ROTARY_INTERLEAVED && layout != HK_ROTARY_SPLIT_HALF)
+            return fail(HK_INVALID_ARGUMENT, "rotary layout must be 0 (Interleaved) or 1 (SplitHalf)");
+        if ((sh.d != 64 && sh.d != 128) || sh.m != sh.n)
+            return fail(HK_INVALID_ARGUMENT, "%s requires heads of width 64 or 128 and as many keys as queries", op);
+        const int64_t S = sh.m, D = sh.d, W = (sh.heads + 2 * sh.kv_heads) * D;
+        if (!aligned_bf16({rows}, op)) return HK_INVALID_ARGUMENT;
+        if (!dims_are(rows, {sh.batch, S, W}))
+            return fail(HK_INVALID_ARGUMENT, "%s requires dQKV rows BF16 [B, S, (Hq+2Hkv)*D]", op);
+        if (cos->dtype != HK_F32 || sin->dtype != HK_F32 || !dims_are(cos, {S, D / 2}) || !dims_are(sin, {S, D / 2}) ||
+            reinterpret_cast<uintptr_t>(cos->data) % 16 != 0 || reinterpret_cast<uintptr_t>(sin->data) % 16 != 0)
+            return fail(HK_INVALID_ARGUMENT, "%s requires 16-byte aligned F32 cos/sin tables [S, D/2]", op);
+        if (!disjoint({rows}, {q, k, v, o, lse, dout, cos, sin})) return HK_INVALID_ARGUMENT;
+        rows_out = hk::AttnRowsOut{rows->data, W, static_cast<const float*>(cos->data),
+                                   static_cast<const float*>(sin->data), layout};
+    }
     sh.o_f32 = o->dtype == HK_F32;
     hk::attention_bwd_plan(sh);
     Staged sq = staged(q), sk = staged(k), sv = staged(v), sd = staged(dout);
@@ -2480,9 +2605,29 @@ hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tens
     if (e == hipSuccess) e = stage(dout, sd, cursor, g.c->stream);
     if (e == hipSuccess)
         e = hk::attention_backward(sh, sq.p, sk.p, sv.p, o->data, static_cast<const float*>(lse->data), sd.p,
-                                   dq->data, dq->dtype == HK_BF16, dk->data, dv->data, dk->dtype == HK_BF16,
-                                   g.c->workspace, g.c->stream);
-    return complete(g.c, e, "attention_backward", 3 + (sq.bytes ? 3 : 0) + (sd.bytes ? 1 : 0));
+                                   rows ? nullptr : dq->data, rows ? 1 : dq->dtype == HK_BF16,
+                                   rows ? nullptr : dk->data, rows ? nullptr : dv->data,
+                                   rows ? 1 : dk->dtype == HK_BF16, rows ? &rows_out : nullptr, g.c->workspace,
+                                   g.c->stream);
+    return complete(g.c, e, rows ? "attention_backward_qkv_rows" : "attention_backward",
+                    3 + (sq.bytes ? 3 : 0) + (sd.bytes ? 1 : 0));
+}
+}  // namespace
+
+hk_status hk_attention_backward(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                const hk_tensor* o, const hk_tensor* lse, const hk_tensor* dout, float scale,
+                                int32_t causal, uint64_t qs, uint64_t ks, hk_tensor* dq, hk_tensor* dk,
+                                hk_tensor* dv) {
+    return attention_backward_common(h, q, k, v, o, lse, dout, scale, causal, qs, ks, dq, dk, dv, nullptr, nullptr,
+                                     0, nullptr);
+}
+
+hk_status hk_attention_backward_qkv_rows(hk_context* h, const hk_tensor* q, const hk_tensor* k, const hk_tensor* v,
+                                         const hk_tensor* o, const hk_tensor* lse, const hk_tensor* dout, float scale,
+                                         int32_t causal, uint64_t qs, uint64_t ks, const hk_tensor* cos,
+                                         const hk_tensor* sin, int32_t layout, hk_tensor* dqkv) {
+    return attention_backward_common(h, q, k, v, o, lse, dout, scale, causal, qs, ks, nullptr, nullptr, nullptr, cos,
+                                     sin, layout, dqkv);
 }
 
 // ------------------------------------------------------------------ composed attention

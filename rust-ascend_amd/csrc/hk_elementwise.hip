@@ -26,21 +26,6 @@ namespace {
 
 constexpr int kEwThreads = 256;
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
-
-__device__ __forceinline__ float silu_mul1(float g, float u) {
-    const float s = sigmoid(g);
-    return (g * s) * u;
-}
-
-__device__ __forceinline__ void silu_mul_bwd1(float g, float u, float dy, float& dg, float& du) {
-    const float s = sigmoid(g);
-    const float h = g * s;
-    const float ds = s * (1.0f + g * (1.0f - s));
-    dg = (dy * u) * ds;
-    du = dy * h;
-}
-
 template <typename T>
 __global__ void __launch_bounds__(kEwThreads)
 silu_mul_kernel(const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ y, int64_t n, bool vec) {

@@ -603,6 +603,76 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
     return hipGetLastError();
 }
 
+bool epi_applies(int64_t m, int64_t n, int64_t k) {
+    const int64_t k64 = (k + kPK - 1) / kPK * kPK;
+    return m > 0 && n > 0 && k > 0 && k % 8 == 0 && m * k64 * 2 < (int64_t{1} << 31) &&
+           n * k64 * 2 < (int64_t{1} << 31);
+}
+
+bool qkv_rope_applies(int64_t tokens, int64_t hidden, int64_t width) {
+    return width % 128 == 0 && epi_applies(tokens, width, hidden);
+}
+
+namespace {
+// A fused-epilogue GEMM over p.m x p.n outputs (256x256 tiles, bands of 8 N-tiles per XCD unless
+// the tile grid is square, as launch_pp chooses).
+template <int EPI, bool B_MN>
+hipError_t launch_epi(GemmEpiArgs p, hipStream_t s) {
+    p.tiles_m = (p.m + kPPTile - 1) / kPPTile;
+    p.tiles_n = (p.n + kPPTile - 1) / kPPTile;
+    p.band_n = p.tiles_m == p.tiles_n ? 0 : 8;
+    const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+    if (p.k % kPK != 0) hipLaunchKernelGGL((gemm_epi_kernel<EPI, B_MN, true>), grid, dim3(kW4Threads), 0, s, p);
+    else hipLaunchKernelGGL((gemm_epi_kernel<EPI, B_MN, false>), grid, dim3(kW4Threads), 0, s, p);
+    return hipGetLastError();
+}
+
+GemmEpiArgs epi_args(const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k) {
+    GemmEpiArgs p{};
+    p.a = static_cast<const uint16_t*>(a);
+    p.b = static_cast<const uint16_t*>(b);
+    p.c = c;
+    p.m = static_cast<int>(m);
+    p.n = static_cast<int>(n);
+    p.k = static_cast<int>(k);
+    return p;
+}
+}  // namespace
+
+hipError_t gemm_qkv_rope(const void* x, const void* w, int64_t tokens, int64_t hidden, int64_t seq, int64_t hq,
+                         int64_t hkv, const float* cos_t, const float* sin_t, int layout, void* q, void* k, void* v,
+                         hipStream_t s) {
+    GemmEpiArgs p = epi_args(x, w, nullptr, tokens, (hq + 2 * hkv) * 128, hidden);
+    p.qkv = QkvRopeOut{static_cast<uint16_t*>(q), static_cast<uint16_t*>(k), static_cast<uint16_t*>(v), cos_t, sin_t,
+                       static_cast<int>(seq), static_cast<int>(hq), static_cast<int>(hkv), layout};
+    return launch_epi<kEpiQkvRope, false>(p, s);
+}
+
+hipError_t gemm_residual(const void* x, const void* w, const void* res, void* y, int64_t m, int64_t n, int64_t k,
+                         hipStream_t s) {
+    GemmEpiArgs p = epi_args(x, w, y, m, n, k);
+    p.res = static_cast<const uint16_t*>(res);
+    return launch_epi<kEpiResidual, false>(p, s);
+}
+
+hipError_t gemm_swiglu(const void* x, const void* w_gu, void* gate, void* up, void* act, int64_t m, int64_t f,
+                       int64_t k, hipStream_t s) {
+    GemmEpiArgs p = epi_args(x, w_gu, nullptr, m, 2 * f, k);
+    p.gate = static_cast<uint16_t*>(gate);
+    p.up = static_cast<uint16_t*>(up);
+    p.act = static_cast<uint16_t*>(act);
+    return launch_epi<kEpiSwiglu, false>(p, s);
+}
+
+hipError_t gemm_swiglu_backward(const void* dy, const void* wd, const void* gate, const void* up, void* dgu, int64_t m,
+                                int64_t f, int64_t k, hipStream_t s) {
+    GemmEpiArgs p = epi_args(dy, wd, nullptr, m, f, k);
+    p.gate = const_cast<uint16_t*>(static_cast<const uint16_t*>(gate));
+    p.up = const_cast<uint16_t*>(static_cast<const uint16_t*>(up));
+    p.dgu = static_cast<uint16_t*>(dgu);
+    return launch_epi<kEpiSwigluBwd, true>(p, s);
+}
+
 hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_bf16, int64_t m, int64_t n, int64_t k,
                                 const int32_t* block_group, int num_cus, hipStream_t s) {
     GemmArgs p{};

@@ -26,6 +26,37 @@ struct GemmArgs {
     int band_n;
 };
 
+// The decoder layer's fused QKV projection: the product's columns are Hq + 2 Hkv heads of 128
+// (Q heads, then K, then V) and its rows are tokens b * seq + s. Instead of the [T, W] rows, each
+// head's 128 columns go to its plane q [B, Hq, seq, 128] or k, v [B, Hkv, seq, 128], Q and K
+// rotated on the way (RoPE with F32 tables [seq, 64] indexed by s).
+struct QkvRopeOut {
+    uint16_t* q;
+    uint16_t* k;
+    uint16_t* v;
+    const float* cos;
+    const float* sin;
+    int seq, hq, hkv;
+    int layout;  // 1: split-half pairs (d, d + 64); 0: interleaved pairs (2p, 2p + 1)
+};
+// Epilogues of the tile kernel: the plain store, or one of the decoder layer's fusions.
+constexpr int kEpiPlain = 0;
+constexpr int kEpiQkvRope = 1;   // the QKV projection into rotated head planes (QkvRopeOut)
+constexpr int kEpiResidual = 2;  // C = bf16(bf16(acc) + res): a projection plus its residual
+constexpr int kEpiSwiglu = 3;    // gate and up in one product -> gate, up, SiLU(gate) * up
+constexpr int kEpiSwigluBwd = 4; // dM = dY Wd -> the SwiGLU gradients of gate and up
+// The gate/up product's B rows (and the columns of the SwiGLU gradient) interleave gate and up in
+// blocks of 16: row 32 b + r is gate row 16 b + r for r < 16 and up row 16 b + r - 16 otherwise,
+// so a wave's fragments 2q and 2q + 1 hold the gate and up values of the same 16 columns.
+struct GemmEpiArgs : GemmArgs {
+    QkvRopeOut qkv;
+    const uint16_t* res;  // kEpiResidual: [M, N] like C
+    uint16_t* gate;       // kEpiSwiglu: written, kEpiSwigluBwd: read; [M, F] with F = N / 2 (fwd), N (bwd)
+    uint16_t* up;
+    uint16_t* act;        // kEpiSwiglu: SiLU(gate) * up [M, F]
+    uint16_t* dgu;        // kEpiSwigluBwd: [M, 2F], the interleaved gradient of the gate/up product
+};
+
 // B operand of the tile whose first output row is row0 in batch g.
 // (The tile kernel below is a template over its argument type: other callers give it their own
 // argument struct and weight_slice overload.)
@@ -109,7 +140,130 @@ constexpr int kOutOfRange = static_cast<int>(0x80000000u);
 // workgroups (a 1.5-round grid of square tiles as 2 rounds of narrow ones). The B stage keeps its
 // 256 rows or columns; an MN-major B is staged 256 columns wide as for NJ = 8 (the columns past the
 // tile feed nothing).
-template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL, class Args, int NJ = 8>
+// Epilogue of the fused QKV projection (NJ = 8): a wave's 128 output columns are exactly one head
+// and a lane holds columns 16 j + 4 lg .. +3 of row 16 i + l16 in acc[i][j], so both members of
+// every rotation pair are in the lane (split-half: fragments j and j + 4; interleaved: neighbours
+// within a fragment). Each value is first rounded to BF16 -- the product's storage in the
+// unfused composition -- then rotated in F32 by rope_rotate and rounded again, so the planes are
+// bit-identical to the GEMM's BF16 rows followed by qkv_rope_split.
+template <class Args>
+__device__ __forceinline__ void store_qkv_rope(const Args& p, f32x4_t (&acc)[8][8], int tm, int tn, int wm, int wn,
+                                               int l16, int lg) {
+    const QkvRopeOut& o = p.qkv;
+    const int n0 = tn * kPPTile + 128 * wn;
+    if (n0 >= p.n) return;
+    const int head = n0 >> 7;
+    uint16_t* plane;
+    int hx, hh;
+    if (head < o.hq) {
+        plane = o.q, hx = o.hq, hh = head;
+    } else if (head < o.hq + o.hkv) {
+        plane = o.k, hx = o.hkv, hh = head - o.hq;
+    } else {
+        plane = o.v, hx = o.hkv, hh = head - o.hq - o.hkv;
+    }
+    const bool rotate = head < o.hq + o.hkv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
+        if (m >= p.m) continue;
+        const int b = m / o.seq, s = m - b * o.seq;
+        uint16_t* row = plane + (static_cast<int64_t>(b) * hx + hh) * o.seq * 128 + static_cast<int64_t>(s) * 128;
+        const float* ct = o.cos + static_cast<int64_t>(s) * 64;
+        const float* st = o.sin + static_cast<int64_t>(s) * 64;
+        if (!rotate) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const u32x2_t w = {pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+                *reinterpret_cast<u32x2_t*>(row + 16 * j + 4 * lg) = w;
+            }
+        } else if (o.layout == 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = 16 * j + 4 * lg;
+                const f32x4_t c = *reinterpret_cast<const f32x4_t*>(ct + d);
+                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(st + d);
+                float ya[4], yb[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    rope_rotate<false>(round_bf16(acc[i][j][e]), round_bf16(acc[i][j + 4][e]), c[e], sn[e], ya[e], yb[e]);
+                *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(ya[0], ya[1]), pack_bf16x2(ya[2], ya[3])};
+                *reinterpret_cast<u32x2_t*>(row + d + 64) = u32x2_t{pack_bf16x2(yb[0], yb[1]), pack_bf16x2(yb[2], yb[3])};
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 16 * j + 4 * lg;  // pairs (d, d + 1) and (d + 2, d + 3): angles d/2, d/2 + 1
+                const f32x2_t c = *reinterpret_cast<const f32x2_t*>(ct + d / 2);
+                const f32x2_t sn = *reinterpret_cast<const f32x2_t*>(st + d / 2);
+                float y[4];
+                rope_rotate<false>(round_bf16(acc[i][j][0]), round_bf16(acc[i][j][1]), c[0], sn[0], y[0], y[1]);
+                rope_rotate<false>(round_bf16(acc[i][j][2]), round_bf16(acc[i][j][3]), c[1], sn[1], y[2], y[3]);
+                *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+            }
+        }
+    }
+}
+
+// The element-wise fused epilogues (NJ fragments of 16 columns per wave): row m, the wave's first
+// column n0; each lane holds columns n0 + 16 j + 4 lg .. +3. Every value is rounded to BF16 where the
+// unfused composition stores it, so the results are bit-identical to the GEMM followed by the
+// element-wise kernel.
+template <int EPI, int NJ, class Args>
+__device__ __forceinline__ void store_fused_row(const Args& p, const f32x4_t (&acc)[NJ], int64_t g, int m, int n0,
+                                                int lg) {
+    if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int n = n0 + 16 * j + 4 * lg;
+            if (n >= p.n) continue;
+            const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
+            const u32x2_t r = *reinterpret_cast<const u32x2_t*>(p.res + off);
+            const float y0 = round_bf16(acc[j][0]) + bf16lo(r[0]), y1 = round_bf16(acc[j][1]) + bf16hi(r[0]);
+            const float y2 = round_bf16(acc[j][2]) + bf16lo(r[1]), y3 = round_bf16(acc[j][3]) + bf16hi(r[1]);
+            *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+        }
+    } else if constexpr (EPI == kEpiSwiglu) {
+        static_assert(NJ % 2 == 0, "gate/up fragment pairs");
+        const int f_cols = p.n / 2;
+#pragma unroll
+        for (int q = 0; q < NJ / 2; ++q) {
+            if (n0 + 32 * q >= p.n) continue;
+            const int f = n0 / 2 + 16 * q + 4 * lg;
+            float gv[4], uv[4], y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                gv[e] = round_bf16(acc[2 * q][e]);
+                uv[e] = round_bf16(acc[2 * q + 1][e]);
+                y[e] = silu_mul1(gv[e], uv[e]);
+            }
+            const int64_t off = static_cast<int64_t>(m) * f_cols + f;
+            *reinterpret_cast<u32x2_t*>(p.gate + off) = u32x2_t{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
+            *reinterpret_cast<u32x2_t*>(p.up + off) = u32x2_t{pack_bf16x2(uv[0], uv[1]), pack_bf16x2(uv[2], uv[3])};
+            *reinterpret_cast<u32x2_t*>(p.act + off) = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        }
+    } else {
+        static_assert(EPI == kEpiSwigluBwd, "fused epilogue");
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int f = n0 + 16 * j + 4 * lg;
+            if (f >= p.n) continue;
+            const int64_t off = static_cast<int64_t>(m) * p.n + f;
+            const u32x2_t gw = *reinterpret_cast<const u32x2_t*>(p.gate + off);
+            const u32x2_t uw = *reinterpret_cast<const u32x2_t*>(p.up + off);
+            const float gv[4] = {bf16lo(gw[0]), bf16hi(gw[0]), bf16lo(gw[1]), bf16hi(gw[1])};
+            const float uv[4] = {bf16lo(uw[0]), bf16hi(uw[0]), bf16lo(uw[1]), bf16hi(uw[1])};
+            float dg[4], du[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) silu_mul_bwd1(gv[e], uv[e], round_bf16(acc[j][e]), dg[e], du[e]);
+            uint16_t* row = p.dgu + static_cast<int64_t>(m) * (2 * p.n) + 32 * (f >> 4) + (f & 15);
+            *reinterpret_cast<u32x2_t*>(row) = u32x2_t{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+            *reinterpret_cast<u32x2_t*>(row + 16) = u32x2_t{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+        }
+    }
+}
+
+template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL, class Args, int NJ = 8, int EPI = kEpiPlain>
 __device__ __forceinline__ void gemm_m16_tile(Args p) {
     static_assert(NJ >= 1 && NJ <= 8, "B fragments per wave");
     constexpr int kTileN = 32 * NJ;  // output columns per tile
@@ -267,6 +421,18 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
     } while (s < nk);
     stage_barrier<0>();  // no load may still be writing LDS at exit
 
+    if constexpr (EPI == kEpiQkvRope) {
+        static_assert(NJ == 8 && OUT_BF16, "the fused QKV epilogue needs 128-column wave blocks");
+        store_qkv_rope(p, acc, tm, tn, wm, wn, l16, lg);
+        return;
+    } else if constexpr (EPI != kEpiPlain) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
+            if (m < p.m) store_fused_row<EPI, NJ>(p, acc[i], g, m, tn * kTileN + kWaveN * wn, lg);
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
@@ -290,6 +456,14 @@ template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL = false, int NJ = 8>
 __global__ void __launch_bounds__(kW4Threads, 1)
 gemm_nt_m16_kernel(GemmArgs p) {
     gemm_m16_tile<OUT_BF16, A_MN, B_MN, KTAIL, GemmArgs, NJ>(p);
+}
+
+// The fused-epilogue GEMMs (256x256 tiles, A K-major, B K-major or, for the SwiGLU backward's
+// dY Wd, MN-major).
+template <int EPI, bool B_MN, bool KTAIL>
+__global__ void __launch_bounds__(kW4Threads, 1)
+gemm_epi_kernel(GemmEpiArgs p) {
+    gemm_m16_tile<true, false, B_MN, KTAIL, GemmEpiArgs, 8, EPI>(p);
 }
 
 }  // namespace

@@ -93,6 +93,28 @@ hipError_t gemm_bf16(const void* a, const void* b, void* c, int out_bf16, int64_
 hipError_t gemm_bf16_grouped_nt(const void* a, const void* w, void* c, int out_bf16, int64_t m, int64_t n,
                                 int64_t k, const int32_t* block_group, int num_cus, hipStream_t s);
 
+// The decoder layer's fused QKV projection with RoPE: x [T, H] times W [(Hq + 2 Hkv) 128, H]^T into
+// q [B, Hq, seq, 128], k, v [B, Hkv, seq, 128] (T = B seq), Q and K rotated with tables
+// [seq, 64]; bit-identical to gemm_bf16 (NT, BF16 out) followed by qkv_rope (split).
+bool qkv_rope_applies(int64_t tokens, int64_t hidden, int64_t width);
+hipError_t gemm_qkv_rope(const void* x, const void* w, int64_t tokens, int64_t hidden, int64_t seq, int64_t hq,
+                         int64_t hkv, const float* cos_t, const float* sin_t, int layout, void* q, void* k, void* v,
+                         hipStream_t s);
+// The other fused-epilogue GEMMs of a decoder layer (BF16, 256x256 tiles at any M and N; they apply
+// when K % 8 == 0 and M K, N K stay below 2^30 elements, K rounded up to 64):
+bool epi_applies(int64_t m, int64_t n, int64_t k);
+// y [m, n] = res + x [m, k] W [n, k]^T (the product rounded to BF16 before the add)
+hipError_t gemm_residual(const void* x, const void* w, const void* res, void* y, int64_t m, int64_t n, int64_t k,
+                         hipStream_t s);
+// gate, up, act [m, f]: x [m, k] W_gu [2f, k]^T with W_gu's rows interleaving gate and up in blocks of
+// 16 (row 32 b + r: gate row 16 b + r for r < 16, else up row 16 b + r - 16); act = SiLU(gate) up
+hipError_t gemm_swiglu(const void* x, const void* w_gu, void* gate, void* up, void* act, int64_t m, int64_t f,
+                       int64_t k, hipStream_t s);
+// dgu [m, 2f] (interleaved as W_gu's rows) = the SwiGLU gradients of gate and up for
+// dM = dY [m, k] Wd [k, f] (Wd stored [k, f])
+hipError_t gemm_swiglu_backward(const void* dy, const void* wd, const void* gate, const void* up, void* dgu, int64_t m,
+                                int64_t f, int64_t k, hipStream_t s);
+
 // ---- NLLLoss (hk_loss.hip)
 // dtype 0 F32, 1 F16, 2 BF16 (input, weight, out, total, grad, dinput); id_bytes 4 or 8;
 // reduction 0 None, 1 Mean, 2 Sum. The forward writes *bad = 1 if a label outside [0, classes)
@@ -184,8 +206,19 @@ size_t attention_bwd_workspace_bytes(const AttnShape& sh);
 bool attention_shape_fits(const AttnShape& sh);
 hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o,
                              float* lse, hipStream_t s);
+// The backward's rows output (D = 64 or 128, M = N = S): dQ, dK, dV written as BF16 token rows
+// [B, S, row_w] of a fused QKV projection's gradient, dQ and dK rotated back by RoPE (tables
+// [S, D/2]); dq/dk/dv are then not written.
+struct AttnRowsOut {
+    void* rows;
+    int64_t row_w;
+    const float* cos;
+    const float* sin;
+    int layout;
+};
 hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k, const void* v,
                               const void* o, const float* lse, const void* dout, void* dq, int dq_bf16,
-                              void* dk, void* dv, int dkv_bf16, void* workspace, hipStream_t s);
+                              void* dk, void* dv, int dkv_bf16, const AttnRowsOut* rows, void* workspace,
+                              hipStream_t s);
 
 }  // namespace hk

@@ -128,6 +128,11 @@ SIGNATURES = {
     "hk_embedding": [_CTX, _T, _T, _T],
     "hk_embedding_backward": [_CTX, _T, _T, _u64, _u64, _i32, _T],
     "hk_qkv_rope_split": [_CTX, _T, _T, _T, _i32, _T, _T, _T],
+    "hk_qkv_projection_rope": [_CTX, _T, _T, _T, _T, _i32, _T, _T, _T],
+    "hk_linear_residual": [_CTX, _T, _T, _T, _T],
+    "hk_swiglu_projection": [_CTX, _T, _T, _T, _T, _T],
+    "hk_swiglu_projection_backward": [_CTX, _T, _T, _T, _T, _T],
+    "hk_attention_backward_qkv_rows": [_CTX, _T, _T, _T, _T, _T, _T, _f32, _i32, _u64, _u64, _T, _T, _i32, _T],
     "hk_qkv_rope_merge": [_CTX, _T, _T, _T, _T, _T, _i32, _T],
     "hk_heads_to_rows": [_CTX, _T, _T],
     "hk_rows_to_heads": [_CTX, _T, _T],

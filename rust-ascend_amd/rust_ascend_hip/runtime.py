@@ -480,6 +480,33 @@ class HipRuntime:
         return out
 
     @staticmethod
+    def qkv_projection_rope(x, w, cos, sin, batch: int, q_heads: int, kv_heads: int, layout=None):
+        """The fused QKV projection with RoPE: x [B*S, H] times w [(Hq+2Hkv)*128, H]^T straight into
+        (q [B,Hq,S,128], k, v [B,Hkv,S,128]), q and k rotated (tables [S, 64])."""
+        layout = RotaryLayout.SplitHalf if layout is None else layout
+        d = w.shape[0] // (q_heads + 2 * kv_heads)
+        s = x.shape[-2] if x.dim() == 3 else x.shape[0] // batch
+        q = _empty((batch, q_heads, s, d), x.dtype, x)
+        k = _empty((batch, kv_heads, s, d), x.dtype, x)
+        v = _empty((batch, kv_heads, s, d), x.dtype, x)
+        _call("hk_qkv_projection_rope", desc(x), desc(w), desc(cos), desc(sin), int(layout), desc(q), desc(k),
+              desc(v))
+        return q, k, v
+
+    @staticmethod
+    def attention_backward_qkv_rows(q, k, v, o, lse, grad, cos, sin, scale: float, causal: bool = True,
+                                    query_start: int = 0, key_start: int = 0, layout=None):
+        """The attention backward into the fused projection's gradient rows dqkv [B,S,(Hq+2Hkv)D]
+        (BF16), dQ and dK rotated back."""
+        layout = RotaryLayout.SplitHalf if layout is None else layout
+        b, hq, s, d = q.shape
+        out = _empty((b, s, (hq + 2 * k.shape[1]) * d), torch.bfloat16, q)
+        _call("hk_attention_backward_qkv_rows", desc(q), desc(k), desc(v), desc(o), desc(lse), desc(grad),
+              float(scale), int(bool(causal)), int(query_start), int(key_start), desc(cos), desc(sin), int(layout),
+              desc(out))
+        return out
+
+    @staticmethod
     def heads_to_rows(x):
         """[B,H,S,D] -> [B,S,H*D]."""
         b, h, s, d = x.shape

@@ -99,8 +99,12 @@ def reference(layer: DecoderLayer, ids, dy, emulate_bf16=False, dtype=torch.floa
     s = s.masked_fill(torch.triu(torch.ones(seq, seq, dtype=torch.bool, device=device), 1), float("-inf"))
     o = R(torch.softmax(s, -1) @ v).permute(0, 2, 1, 3).reshape(T, H)
     h1 = R(x0 + R(o @ P["wo"].T))                              # dh1 = bf16(dh1_norm + dy)
-    n2 = R(rms(G(h1), P["w2"]))                                # dn2 = bf16(dn2_g + dn2_u)
-    m = R(torch.nn.functional.silu(R(G(n2) @ P["wg"].T)) * R(G(n2) @ P["wu"].T))
+    n2 = R(rms(G(h1), P["w2"]))
+    if layer.fused_ffn:  # dn2 = bf16(dgate Wg + dup Wu), one product over the interleaved [dgate | dup]
+        n2g = G(n2)
+        m = R(torch.nn.functional.silu(R(n2g @ P["wg"].T)) * R(n2g @ P["wu"].T))
+    else:                # dn2 = bf16(bf16(dgate Wg) + bf16(dup Wu))
+        m = R(torch.nn.functional.silu(R(G(n2) @ P["wg"].T)) * R(G(n2) @ P["wu"].T))
     y = R(h1 + R(m @ P["wd"].T))
     (y * dy).sum().backward()
     return y.detach(), {k: t.grad for k, t in P.items()}
@@ -209,6 +213,59 @@ def test_decoder_layer_c5_full_size_vs_bf16_storage_model():
         assert e <= DIRECT_TOL, (k, e)
     del layer, g32, grads
     torch.cuda.empty_cache()
+
+
+def run_c5_layer(ids, dy, **flags):
+    layer = DecoderLayer(DecoderConfig(), seed=13, **flags)
+    for k, v in flags.items():
+        assert getattr(layer, k) == v
+    print(f"C5 layer {flags}", flush=True)
+    y = layer.forward(ids).clone()
+    grads = {k: v.clone() for k, v in layer.backward(dy).items()}
+    del layer
+    torch.cuda.empty_cache()
+    return y, grads
+
+
+def c5_inputs(seed):
+    c = DecoderConfig()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    ids = torch.randint(0, c.vocab, (c.batch, c.seq), generator=g, device="cuda")
+    dy = torch.randn((c.batch, c.seq, c.hidden), generator=g, device="cuda").to(torch.bfloat16)
+    return ids, dy
+
+
+def test_decoder_layer_c5_fused_rope_bit_exact_with_unfused():
+    """At C5 size the layer with RoPE in the QKV projection's and the attention backward's
+    epilogues (hk_qkv_projection_rope, hk_attention_backward_qkv_rows) gives the same output and
+    gradients, bit for bit, as the layer with the separate split/merge passes (hk_gemm_into +
+    hk_qkv_rope_split, hk_attention_backward + hk_qkv_rope_merge)."""
+    ids, dy = c5_inputs(13)
+    y1, g1 = run_c5_layer(ids, dy, fused_rope=True)
+    y0, g0 = run_c5_layer(ids, dy, fused_rope=False)
+    assert torch.equal(y1, y0)
+    for k in g1:
+        assert torch.equal(g1[k], g0[k]), k
+
+
+def test_decoder_layer_c5_fused_ffn_against_unfused():
+    """The fused feed-forward (residual adds in the O and down projections' epilogues, gate and up
+    as one GEMM with SiLU-mul in its epilogue, the SwiGLU backward in dY Wd's epilogue, dX and dW of
+    gate/up as one GEMM each) against the composition of separate kernels at C5 size: the forward
+    output and dWd (computed from the same values by the same kernel) bit for bit; the other
+    gradients differ only by dn2's rounding (one BF16 rounding of dgate Wg + dup Wu instead of
+    three) and must agree within 1e-2 normwise."""
+    ids, dy = c5_inputs(17)
+    y1, g1 = run_c5_layer(ids, dy, fused_ffn=True)
+    y0, g0 = run_c5_layer(ids, dy, fused_ffn=False)
+    assert torch.equal(y1, y0)
+    assert torch.equal(g1["wd"], g0["wd"])
+    errs = {k: (torch.linalg.vector_norm(g1[k].float() - g0[k].float()) /
+                torch.linalg.vector_norm(g0[k].float())).item() for k in g1}
+    print("fused vs unfused feed-forward", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for k, e in errs.items():
+        assert e <= 1e-2, (k, e)
 
 
 def test_decoder_layer_rejects_bad_config_and_ids():

@@ -91,3 +91,97 @@ def test_layout_rejects_bad_inputs():
         HipRuntime.qkv_rope_split(flat[1:].reshape(1, 8, 512), cos, cos, 4, 2)  # not 16-byte aligned
     with pytest.raises(HkError):
         HipRuntime.heads_to_rows(torch.zeros((1, 2, 3, 12), device=DEV, dtype=torch.bfloat16))  # D % 8
+
+
+# ------------------------------------------------------------------ fused QKV projection / backward rows
+
+def projection_inputs(b, s, hq, hkv, hidden, seed):
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    x = (torch.randn((b * s, hidden), generator=g, device=DEV) / hidden ** 0.25).to(torch.bfloat16)
+    w = (torch.randn(((hq + 2 * hkv) * 128, hidden), generator=g, device=DEV) / hidden ** 0.25).to(torch.bfloat16)
+    cos, sin = oracle.rope_tables(np.arange(s), 128, 5e5)
+    return x, w, dev_f32(cos), dev_f32(sin)
+
+
+# (B, S, Hq, Hkv, H): C5's projection (a grid of 384 256x256 tiles, so hk_gemm_into runs the same
+# tile kernel and the two paths must agree bit for bit), the same grid with K % 64 != 0 (the
+# partial-last-stage variant), then small and ragged shapes (fewer tiles: hk_gemm_into takes
+# another kernel there, so they are compared within the BF16 tolerance).
+PROJ_EXACT = [(2, 2048, 32, 8, 4096), (4, 1024, 32, 8, 1008)]
+PROJ_SMALL = [(2, 64, 4, 2, 256), (1, 48, 2, 1, 512), (3, 100, 1, 1, 200)]
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,hidden", PROJ_EXACT)
+@pytest.mark.parametrize("layout", [0, 1])
+def test_qkv_projection_rope_bit_exact_with_gemm_and_split(b, s, hq, hkv, hidden, layout):
+    x, w, cos, sin = projection_inputs(b, s, hq, hkv, hidden, seed=s + hidden + layout)
+    print(f"qkv projection rope {b}x{s} tokens, {hq}/{hkv} heads, H {hidden}, layout {layout}", flush=True)
+    q, k, v = HipRuntime.qkv_projection_rope(x, w, cos, sin, b, hq, hkv, RotaryLayout(layout))
+    rows = torch.empty((b, s, w.shape[0]), device=DEV, dtype=torch.bfloat16)
+    HipRuntime.gemm_into(x, w, 0, 1, rows.view(b * s, -1))
+    q2, k2, v2 = HipRuntime.qkv_rope_split(rows, cos, sin, hq, hkv, RotaryLayout(layout))
+    assert torch.equal(q, q2) and torch.equal(k, k2) and torch.equal(v, v2)
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,hidden", PROJ_SMALL)
+@pytest.mark.parametrize("layout", [0, 1])
+def test_qkv_projection_rope_small_shapes_vs_oracle(b, s, hq, hkv, hidden, layout):
+    x, w, cos, sin = projection_inputs(b, s, hq, hkv, hidden, seed=3 * s + hidden + layout)
+    q, k, v = HipRuntime.qkv_projection_rope(x, w, cos, sin, b, hq, hkv, RotaryLayout(layout))
+    y = oracle.gemm_f64(host(x), host(w), False, True).reshape(b, s, hq + 2 * hkv, 128).transpose(0, 2, 1, 3)
+    y = oracle.bf16_round(y)  # the product's storage, before the rotation
+    c4, s4 = host(cos)[None, None], host(sin)[None, None]
+    want_q = oracle.rotary_prefix(y[:, :hq], c4, s4, 128, layout)
+    want_k = oracle.rotary_prefix(y[:, hq:hq + hkv], c4, s4, 128, layout)
+    # per head row (128 values): the rotation keeps each pair's norm, but where a pair's two terms
+    # cancel an element can be ~0 while its rounding error stays ~2^-9 of the pair
+    for got, want, name in ((q, want_q, "q"), (k, want_k, "k"), (v, y[:, hq + hkv:], "v")):
+        e = oracle.row_err(host(got), want)
+        assert e <= 1e-2, (name, e)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("form", ["stored_ds", "recompute"])
+def test_attention_backward_qkv_rows_bit_exact_with_merge(d, layout, causal, form, monkeypatch):
+    """The rows form of the attention backward equals the plane form (BF16 gradients) followed by
+    qkv_rope_merge bit for bit, on both dQ forms, GQA with ragged tiles."""
+    if form == "recompute":
+        monkeypatch.setenv("HK_ATTN_DS_BUDGET", "0")
+    else:
+        monkeypatch.delenv("HK_ATTN_DS_BUDGET", raising=False)
+    b, hq, hkv, s = 2, 4, 2, 200
+    g = torch.Generator(device=DEV)
+    g.manual_seed(d + 10 * layout + causal)
+    q, k, v, do = (torch.randn(shape, generator=g, device=DEV).to(torch.bfloat16)
+                   for shape in ((b, hq, s, d), (b, hkv, s, d), (b, hkv, s, d), (b, hq, s, d)))
+    cos, sin = (dev_f32(t) for t in oracle.rope_tables(np.arange(s), d, 5e5))
+    scale = d ** -0.5
+    o, lse = HipRuntime.attention_forward(q, k, v, scale, causal)
+    rows = HipRuntime.attention_backward_qkv_rows(q, k, v, o, lse, do, cos, sin, scale, causal,
+                                                  layout=RotaryLayout(layout))
+    dq, dk, dv = HipRuntime.attention_backward(q, k, v, o, lse, do, scale, causal, grad_dtype=torch.bfloat16)
+    want = HipRuntime.qkv_rope_merge(dq, dk, dv, cos, sin, RotaryLayout(layout))
+    assert torch.equal(rows, want)
+
+
+def test_fused_projection_and_rows_reject_bad_inputs():
+    x, w, cos, sin = projection_inputs(1, 64, 2, 1, 256, seed=1)
+    q = torch.empty((1, 2, 64, 128), device=DEV, dtype=torch.bfloat16)
+    kv = torch.empty((1, 1, 64, 128), device=DEV, dtype=torch.bfloat16)
+    from rust_ascend_hip import runtime
+    with pytest.raises(HkError):  # tables must cover S
+        runtime._call("hk_qkv_projection_rope", runtime.desc(x), runtime.desc(w), runtime.desc(cos[:32]),
+                      runtime.desc(sin[:32]), 1, runtime.desc(q), runtime.desc(kv), runtime.desc(kv.clone()))
+    with pytest.raises(HkError):  # heads of width 64 are not taken by the fused projection
+        w64 = torch.empty((4 * 64, 256), device=DEV, dtype=torch.bfloat16)
+        q64, kv64 = q[..., :64].contiguous(), kv[..., :64].contiguous()
+        runtime._call("hk_qkv_projection_rope", runtime.desc(x), runtime.desc(w64), runtime.desc(cos[:, :32].contiguous()),
+                      runtime.desc(sin[:, :32].contiguous()), 1, runtime.desc(q64), runtime.desc(kv64),
+                      runtime.desc(kv64.clone()))
+    o, lse = HipRuntime.attention_forward(q, kv, kv, 0.1, True)
+    with pytest.raises(HkError):  # the rows form needs as many keys as queries
+        k2 = torch.zeros((1, 1, 80, 128), device=DEV, dtype=torch.bfloat16)
+        HipRuntime.attention_backward_qkv_rows(q, k2, k2, o, lse, q, cos, sin, 0.1, True)
