@@ -145,7 +145,14 @@ constexpr int kOutOfRange = static_cast<int>(0x80000000u);
 // every rotation pair are in the lane (split-half: fragments j and j + 4; interleaved: neighbours
 // within a fragment). Each value is first rounded to BF16 -- the product's storage in the
 // unfused composition -- then rotated in F32 by rope_rotate and rounded again, so the planes are
-// bit-identical to the GEMM's BF16 rows followed by qkv_rope_split.
+// bit-identical to the GEMM's BF16 rows followed by qkv_rope_split. The cos/sin values of a row
+// are fetched four rows ahead of its stores (a load issued after a store waits for it: vmcnt
+// counts both in order).
+struct RopeRowIn {  // the lane's 16 angles of one row: split-half c[j] = angles 16 j + 4 lg .. +3,
+    f32x4_t c[4];   // interleaved c[q] = angles 16 q + 2 lg, +1 (fragment 2q) and 16 q + 8 + 2 lg, +1
+    f32x4_t s[4];   // (fragment 2q + 1)
+};
+
 template <class Args>
 __device__ __forceinline__ void store_qkv_rope(const Args& p, f32x4_t (&acc)[8][8], int tm, int tn, int wm, int wn,
                                                int l16, int lg) {
@@ -163,45 +170,73 @@ __device__ __forceinline__ void store_qkv_rope(const Args& p, f32x4_t (&acc)[8][
         plane = o.v, hx = o.hkv, hh = head - o.hq - o.hkv;
     }
     const bool rotate = head < o.hq + o.hkv;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
-        if (m >= p.m) continue;
-        const int b = m / o.seq, s = m - b * o.seq;
-        uint16_t* row = plane + (static_cast<int64_t>(b) * hx + hh) * o.seq * 128 + static_cast<int64_t>(s) * 128;
+    const int m0 = tm * kPPTile + 128 * wm + l16;
+    constexpr int kAhead = 4;
+    RopeRowIn in[kAhead];
+    auto load_row = [&](RopeRowIn& r, int i) __attribute__((always_inline)) {
+        const int s = min(m0 + 16 * i, p.m - 1) % o.seq;  // issued for every row (no load under a branch)
         const float* ct = o.cos + static_cast<int64_t>(s) * 64;
         const float* st = o.sin + static_cast<int64_t>(s) * 64;
-        if (!rotate) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const u32x2_t w = {pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
-                *reinterpret_cast<u32x2_t*>(row + 16 * j + 4 * lg) = w;
-            }
-        } else if (o.layout == 1) {
+        if (o.layout == 1) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int d = 16 * j + 4 * lg;
-                const f32x4_t c = *reinterpret_cast<const f32x4_t*>(ct + d);
-                const f32x4_t sn = *reinterpret_cast<const f32x4_t*>(st + d);
-                float ya[4], yb[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    rope_rotate<false>(round_bf16(acc[i][j][e]), round_bf16(acc[i][j + 4][e]), c[e], sn[e], ya[e], yb[e]);
-                *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(ya[0], ya[1]), pack_bf16x2(ya[2], ya[3])};
-                *reinterpret_cast<u32x2_t*>(row + d + 64) = u32x2_t{pack_bf16x2(yb[0], yb[1]), pack_bf16x2(yb[2], yb[3])};
+                r.c[j] = *reinterpret_cast<const f32x4_t*>(ct + 16 * j + 4 * lg);
+                r.s[j] = *reinterpret_cast<const f32x4_t*>(st + 16 * j + 4 * lg);
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int d = 16 * j + 4 * lg;  // pairs (d, d + 1) and (d + 2, d + 3): angles d/2, d/2 + 1
-                const f32x2_t c = *reinterpret_cast<const f32x2_t*>(ct + d / 2);
-                const f32x2_t sn = *reinterpret_cast<const f32x2_t*>(st + d / 2);
-                float y[4];
-                rope_rotate<false>(round_bf16(acc[i][j][0]), round_bf16(acc[i][j][1]), c[0], sn[0], y[0], y[1]);
-                rope_rotate<false>(round_bf16(acc[i][j][2]), round_bf16(acc[i][j][3]), c[1], sn[1], y[2], y[3]);
-                *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+            for (int q = 0; q < 4; ++q) {
+                const f32x2_t c0 = *reinterpret_cast<const f32x2_t*>(ct + 16 * q + 2 * lg);
+                const f32x2_t c1 = *reinterpret_cast<const f32x2_t*>(ct + 16 * q + 8 + 2 * lg);
+                const f32x2_t s0 = *reinterpret_cast<const f32x2_t*>(st + 16 * q + 2 * lg);
+                const f32x2_t s1 = *reinterpret_cast<const f32x2_t*>(st + 16 * q + 8 + 2 * lg);
+                r.c[q] = f32x4_t{c0[0], c0[1], c1[0], c1[1]};
+                r.s[q] = f32x4_t{s0[0], s0[1], s1[0], s1[1]};
             }
         }
+    };
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) load_row(in[i], i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int m = m0 + 16 * i;
+        if (m < p.m) {
+            const int b = m / o.seq, s = m - b * o.seq;
+            uint16_t* row = plane + (static_cast<int64_t>(b) * hx + hh) * o.seq * 128 + static_cast<int64_t>(s) * 128;
+            const RopeRowIn& r = in[i % kAhead];
+            if (!rotate) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const u32x2_t w = {pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+                    *reinterpret_cast<u32x2_t*>(row + 16 * j + 4 * lg) = w;
+                }
+            } else if (o.layout == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int d = 16 * j + 4 * lg;
+                    float ya[4], yb[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        rope_rotate<false>(round_bf16(acc[i][j][e]), round_bf16(acc[i][j + 4][e]), r.c[j][e], r.s[j][e],
+                                           ya[e], yb[e]);
+                    *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(ya[0], ya[1]), pack_bf16x2(ya[2], ya[3])};
+                    *reinterpret_cast<u32x2_t*>(row + d + 64) = u32x2_t{pack_bf16x2(yb[0], yb[1]), pack_bf16x2(yb[2], yb[3])};
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int d = 16 * j + 4 * lg;  // pairs (d, d + 1) and (d + 2, d + 3): angles d/2, d/2 + 1
+                    const int h = 2 * (j & 1);
+                    const float c0 = r.c[j >> 1][h], c1 = r.c[j >> 1][h + 1];
+                    const float s0 = r.s[j >> 1][h], s1 = r.s[j >> 1][h + 1];
+                    float y[4];
+                    rope_rotate<false>(round_bf16(acc[i][j][0]), round_bf16(acc[i][j][1]), c0, s0, y[0], y[1]);
+                    rope_rotate<false>(round_bf16(acc[i][j][2]), round_bf16(acc[i][j][3]), c1, s1, y[2], y[3]);
+                    *reinterpret_cast<u32x2_t*>(row + d) = u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+                }
+            }
+        }
+        if (i + kAhead < 8) load_row(in[i % kAhead], i + kAhead);
     }
 }
 
@@ -209,16 +244,55 @@ __device__ __forceinline__ void store_qkv_rope(const Args& p, f32x4_t (&acc)[8][
 // column n0; each lane holds columns n0 + 16 j + 4 lg .. +3. Every value is rounded to BF16 where the
 // unfused composition stores it, so the results are bit-identical to the GEMM followed by the
 // element-wise kernel.
+// What an epilogue reads for one of a lane's rows: the residual (kEpiResidual) or the saved gate
+// and up values (kEpiSwigluBwd), 4 columns of each fragment. The tile loop fetches these rows
+// several ahead of its stores: vmcnt counts loads and stores together and in order, so a load
+// issued after a store is waited on only once that store has completed too, and fetching each row
+// just before storing it would serialize one store and one load round trip per fragment.
+template <int EPI, int NJ>
+struct EpiRowIn {
+    u32x2_t a[NJ];
+    u32x2_t b[EPI == kEpiSwigluBwd ? NJ : 1];
+};
+template <int EPI>
+constexpr bool epi_reads() {
+    return EPI == kEpiResidual || EPI == kEpiSwigluBwd;
+}
+template <int EPI>
+constexpr int epi_rows_ahead() {  // 16 VGPRs per residual row, 32 per gate/up row (8 residual rows spill)
+    return EPI == kEpiResidual ? 4 : 4;
+}
+
+// Issued for every row and fragment, also past the output's last row or column (clamped to the
+// last one: the value feeds no store), so no load sits under a branch.
 template <int EPI, int NJ, class Args>
-__device__ __forceinline__ void store_fused_row(const Args& p, const f32x4_t (&acc)[NJ], int64_t g, int m, int n0,
-                                                int lg) {
+__device__ __forceinline__ void load_fused_row(const Args& p, EpiRowIn<EPI, NJ>& in, int64_t g, int m, int n0,
+                                               int lg) {
+    const int mc = min(m, p.m - 1);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int n = min(n0 + 16 * j + 4 * lg, p.n - 4);
+        if constexpr (EPI == kEpiResidual) {
+            in.a[j] = *reinterpret_cast<const u32x2_t*>(p.res + (g * p.m + mc) * static_cast<int64_t>(p.n) + n);
+        } else {
+            static_assert(EPI == kEpiSwigluBwd, "epilogue inputs");
+            const int64_t off = static_cast<int64_t>(mc) * p.n + n;
+            in.a[j] = *reinterpret_cast<const u32x2_t*>(p.gate + off);
+            in.b[j] = *reinterpret_cast<const u32x2_t*>(p.up + off);
+        }
+    }
+}
+
+template <int EPI, int NJ, class Args>
+__device__ __forceinline__ void store_fused_row(const Args& p, const f32x4_t (&acc)[NJ], const EpiRowIn<EPI, NJ>& in,
+                                                int64_t g, int m, int n0, int lg) {
     if constexpr (EPI == kEpiResidual) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int n = n0 + 16 * j + 4 * lg;
             if (n >= p.n) continue;
             const int64_t off = (g * p.m + m) * static_cast<int64_t>(p.n) + n;
-            const u32x2_t r = *reinterpret_cast<const u32x2_t*>(p.res + off);
+            const u32x2_t r = in.a[j];
             const float y0 = round_bf16(acc[j][0]) + bf16lo(r[0]), y1 = round_bf16(acc[j][1]) + bf16hi(r[0]);
             const float y2 = round_bf16(acc[j][2]) + bf16lo(r[1]), y3 = round_bf16(acc[j][3]) + bf16hi(r[1]);
             *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.c) + off) = u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
@@ -248,9 +322,7 @@ __device__ __forceinline__ void store_fused_row(const Args& p, const f32x4_t (&a
         for (int j = 0; j < NJ; ++j) {
             const int f = n0 + 16 * j + 4 * lg;
             if (f >= p.n) continue;
-            const int64_t off = static_cast<int64_t>(m) * p.n + f;
-            const u32x2_t gw = *reinterpret_cast<const u32x2_t*>(p.gate + off);
-            const u32x2_t uw = *reinterpret_cast<const u32x2_t*>(p.up + off);
+            const u32x2_t gw = in.a[j], uw = in.b[j];
             const float gv[4] = {bf16lo(gw[0]), bf16hi(gw[0]), bf16lo(gw[1]), bf16hi(gw[1])};
             const float uv[4] = {bf16lo(uw[0]), bf16hi(uw[0]), bf16lo(uw[1]), bf16hi(uw[1])};
             float dg[4], du[4];
@@ -426,10 +498,19 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
         store_qkv_rope(p, acc, tm, tn, wm, wn, l16, lg);
         return;
     } else if constexpr (EPI != kEpiPlain) {
+        const int m0 = tm * kPPTile + 128 * wm + l16, n0 = tn * kTileN + kWaveN * wn;
+        constexpr int kAhead = epi_reads<EPI>() ? epi_rows_ahead<EPI>() : 1;
+        EpiRowIn<EPI, NJ> in[kAhead];
+        if constexpr (epi_reads<EPI>()) {
+#pragma unroll
+            for (int i = 0; i < kAhead; ++i) load_fused_row<EPI, NJ>(p, in[i], g, m0 + 16 * i, n0, lg);
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int m = tm * kPPTile + 128 * wm + 16 * i + l16;
-            if (m < p.m) store_fused_row<EPI, NJ>(p, acc[i], g, m, tn * kTileN + kWaveN * wn, lg);
+            if (m0 + 16 * i < p.m) store_fused_row<EPI, NJ>(p, acc[i], in[i % kAhead], g, m0 + 16 * i, n0, lg);
+            if constexpr (epi_reads<EPI>()) {
+                if (i + kAhead < 8) load_fused_row<EPI, NJ>(p, in[i % kAhead], g, m0 + 16 * (i + kAhead), n0, lg);
+            }
         }
         return;
     }
