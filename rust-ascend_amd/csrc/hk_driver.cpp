@@ -394,6 +394,7 @@ bool live_group_table(const Ctx* c, const void* h) {
 enum class ProgramKind { Dense, Batched, MGrouped };
 struct FunctionDev {
     hipFunction_t fn = nullptr;
+    hipFunction_t fn_wide = nullptr;  // NAME_wide: operand slices past 32-bit offsets (null if absent)
     std::string name;
     ProgramKind kind = ProgramKind::Dense;
     bool ta = false, tb = false, out_bf16 = true;
@@ -946,6 +947,12 @@ hk_status hk_module_get_function(hk_context* h, hk_module* module, const char* n
         (void)hipGetLastError();
         return fail(HK_LOAD_ERROR, "hipModuleGetFunction(%s): %s", f->name.c_str(), hipGetErrorString(e));
     }
+    // The companion for operand slices past 32-bit offsets; a code object without it serves only
+    // the shapes within them.
+    if (hipModuleGetFunction(&f->fn_wide, m->module, (f->name + "_wide").c_str()) != hipSuccess) {
+        (void)hipGetLastError();
+        f->fn_wide = nullptr;
+    }
     m->functions.push_back(std::move(f));
     *out = reinterpret_cast<hk_function*>(m->functions.back().get());
     return HK_OK;
@@ -1013,12 +1020,18 @@ hk_status hk_launch_kernel_with_args(hk_context* h, const hk_function* function,
                     (unsigned long long)want_a, (unsigned long long)(batched ? mk : 0), (unsigned long long)want_b,
                     (unsigned long long)(batched ? nk : 0), n, (unsigned long long)(batched ? mn : 0));
     // The 256x256 tile kernel addresses each operand slice with 32-bit byte offsets up to the end of
-    // the last 64-deep K stage.
-    const uint64_t k64 = (uint64_t(k) + 63) / 64 * 64;
-    if (uint64_t(m) * k64 * 2 >= (uint64_t(1) << 31) || uint64_t(n) * k64 * 2 >= (uint64_t(1) << 31))
-        return fail(HK_INVALID_ARGUMENT,
-                    "operand slice too large for the device programs' 32-bit offsets (M*K and N*K, K rounded up to "
-                    "64, must stay below 2^30 elements)");
+    // the last 64-deep K stage; past that, the program's _wide companion addresses from each tile
+    // (a K-major operand's 256 rows of K, an MN-major one's 64 k-rows of M or N columns per stage).
+    const uint64_t k64 = (uint64_t(k) + 63) / 64 * 64, lim = uint64_t(1) << 31;
+    hipFunction_t fn = f->fn;
+    if (uint64_t(m) * k64 * 2 >= lim || uint64_t(n) * k64 * 2 >= lim) {
+        auto reach = [&](bool mn_major, uint64_t cols) { return mn_major ? 64 * cols * 2 + 512 : 256 * k64 * 2; };
+        if (!f->fn_wide || reach(f->ta, m) >= lim || reach(!f->tb, n) >= lim)
+            return fail(HK_INVALID_ARGUMENT,
+                        "operand slice too large for the device programs' offsets (M*K or N*K of 2^30 elements or "
+                        "more needs K < 2^22 for a K-major operand and M or N < 2^24 for an MN-major one)");
+        fn = f->fn_wide;
+    }
     for (const hk_gm* x : {&a, &b, &d})
         if (x->addr == 0 || x->addr % 16 != 0)
             return fail(HK_INVALID_ARGUMENT, "operand addresses must be non-null and 16-byte aligned");
@@ -1031,7 +1044,7 @@ hk_status hk_launch_kernel_with_args(hk_context* h, const hk_function* function,
         !in_device_allocation(d.addr, d_bytes))
         return fail(HK_INVALID_ARGUMENT, "an operand range is not inside one device allocation of this process");
     const unsigned tiles = ((m + 255) / 256) * ((n + 255) / 256);
-    hipError_t e = hipModuleLaunchKernel(f->fn, tiles, 1, static_cast<unsigned>(batches), 256, 1, 1, 0, g.c->stream,
+    hipError_t e = hipModuleLaunchKernel(fn, tiles, 1, static_cast<unsigned>(batches), 256, 1, 1, 0, g.c->stream,
                                          args, nullptr);
     return complete(g.c, e, f->name.c_str(), 1);
 }

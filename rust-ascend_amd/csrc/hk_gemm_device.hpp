@@ -335,7 +335,14 @@ __device__ __forceinline__ void store_fused_row(const Args& p, const f32x4_t (&a
     }
 }
 
-template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL, class Args, int NJ = 8, int EPI = kEpiPlain>
+// WIDE: operands past 32-bit byte offsets (M*K or N*K >= 2^30 elements). Each buffer resource then
+// starts at the tile: a K-major operand at the tile's first row (its 256 rows span 256 K 2 < 2^31
+// bytes for K < 2^22), an MN-major one at the tile's first column of the stage's first k-row, rebuilt
+// per stage (64 k-rows of M or N columns: 128 M < 2^31 bytes for M < 2^24). Each resource's byte
+// count ends where the operand ends or, further from the end, past everything its loads can reach,
+// so rows past M or N and k-rows past K read as zero exactly as in the 32-bit form.
+template <bool OUT_BF16, bool A_MN, bool B_MN, bool KTAIL, class Args, int NJ = 8, int EPI = kEpiPlain,
+          bool WIDE = false>
 __device__ __forceinline__ void gemm_m16_tile(Args p) {
     static_assert(NJ >= 1 && NJ <= 8, "B fragments per wave");
     constexpr int kTileN = 32 * NJ;  // output columns per tile
@@ -378,7 +385,23 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
     const int r_in = lane >> 3;
     const int src_chunk = (lane & 7) ^ ((4 * (wave & 1) + (r_in >> 1)) & 7);
     const int voff = (r_in * p.k + src_chunk * 8) * 2;
-    const i32x4_t ra4 = buffer_resource(A, p.m * p.k * 2), rb4 = buffer_resource(B, p.n * p.k * 2);
+    // 32-bit form: one resource per operand slice, the tile's rows or columns in the offsets.
+    // WIDE: K-major resources start at the tile's first row (tile_a_row, tile_b_row); MN-major ones
+    // are built per stage by mn_resource below.
+    const int tile_a_row = WIDE && !A_MN ? tm * kPPTile : 0, tile_b_row = WIDE && !B_MN ? tn * kTileN : 0;
+    auto kmajor_bytes = [&](int rows, int row0) __attribute__((always_inline)) {
+        if constexpr (!WIDE) return rows * p.k * 2;
+        return min(rows - row0, kPPTile) * p.k * 2;
+    };
+    const i32x4_t ra4 = buffer_resource(A + static_cast<int64_t>(tile_a_row) * p.k, kmajor_bytes(p.m, tile_a_row));
+    const i32x4_t rb4 = buffer_resource(B + static_cast<int64_t>(tile_b_row) * p.k, kmajor_bytes(p.n, tile_b_row));
+    // WIDE MN-major operand X stored [K, cols]: the stage's 64 k-rows from column col0 on.
+    auto mn_resource = [&](const uint16_t* X, int cols, int col0, int kt) __attribute__((always_inline)) {
+        const int64_t first = static_cast<int64_t>(kt) * kPK * cols + col0;
+        const int64_t left = (static_cast<int64_t>(p.k) * cols - first) * 2;
+        const int64_t reach = static_cast<int64_t>(kPK) * cols * 2 + 2 * kPPTile;
+        return buffer_resource(X + first, static_cast<int>(left < reach ? left : reach));
+    };
     // MN-major operand (A stored [K,M] or B stored [K,N]): its half of a stage is 64 k-rows x 256
     // columns, 512-byte rows whose 64-byte blocks are XORed with k-row % 4. Load d of a wave fills
     // k-rows 2(wave + 4d) + {0, 1}; lane l takes position l % 32 of k-row l / 32, which holds the
@@ -387,8 +410,8 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
     // as zero, elsewhere they feed only outputs that are not stored.
     const int mn_row0 = 2 * wave + (lane >> 5), mn_pos = lane & 31;
     const int mn_c = (((mn_pos >> 2) ^ (mn_row0 & 3)) << 2) | (mn_pos & 3);
-    const int mn_voff_a = (mn_row0 * p.m + tm * kPPTile + mn_c * 8) * 2;
-    const int mn_voff_b = (mn_row0 * p.n + tn * kTileN + mn_c * 8) * 2;
+    const int mn_voff_a = (mn_row0 * p.m + (WIDE ? 0 : tm * kPPTile) + mn_c * 8) * 2;
+    const int mn_voff_b = (mn_row0 * p.n + (WIDE ? 0 : tn * kTileN) + mn_c * 8) * 2;
     const uint32_t lds0 = lds_address(slot0), lds1 = lds_address(slot1);
     // K-major load: the stage offset moves into the lane's offset, which the range check sees
     auto kmajor = [&](const i32x4_t& r, uint32_t dst, int row_off, int kt) __attribute__((always_inline)) {
@@ -401,11 +424,13 @@ __device__ __forceinline__ void gemm_m16_tile(Args p) {
         const int blk = wave + 4 * d;
         const uint32_t dst = lds_slot + (wave * 8 * kPK + d * 4 * 8 * kPK) * 2;
         if (d < 8) {
-            if constexpr (A_MN) load_lds16(ra4, dst, mn_voff_a + (kt * kPK + 8 * d) * p.m * 2, 0);
-            else kmajor(ra4, dst, voff + (tm * kPPTile + 8 * blk) * p.k * 2, kt);
+            if constexpr (A_MN && WIDE) load_lds16(mn_resource(A, p.m, tm * kPPTile, kt), dst, mn_voff_a + 8 * d * p.m * 2, 0);
+            else if constexpr (A_MN) load_lds16(ra4, dst, mn_voff_a + (kt * kPK + 8 * d) * p.m * 2, 0);
+            else kmajor(ra4, dst, voff + (tm * kPPTile - tile_a_row + 8 * blk) * p.k * 2, kt);
         } else {
-            if constexpr (B_MN) load_lds16(rb4, dst, mn_voff_b + (kt * kPK + 8 * (d - 8)) * p.n * 2, 0);
-            else kmajor(rb4, dst, voff + (tn * kTileN + 8 * (blk - 32)) * p.k * 2, kt);
+            if constexpr (B_MN && WIDE) load_lds16(mn_resource(B, p.n, tn * kTileN, kt), dst, mn_voff_b + 8 * (d - 8) * p.n * 2, 0);
+            else if constexpr (B_MN) load_lds16(rb4, dst, mn_voff_b + (kt * kPK + 8 * (d - 8)) * p.n * 2, 0);
+            else kmajor(rb4, dst, voff + (tn * kTileN - tile_b_row + 8 * (blk - 32)) * p.k * 2, kt);
         }
     };
 

@@ -13,7 +13,7 @@
 // programs and the group count of the M-grouped ones, whose grouped_layout holds the ascending,
 // 256-aligned group row ends (repeated ends are empty groups). The driver checks every argument
 // against the reference's contract before a launch (packed strides, alpha 1, M/N/K multiples of
-// 16, 32-bit operand offsets), so the programs trust them.
+// 16, operand offsets within the 32-bit or the wide form's reach), so the programs trust them.
 #include "hk_common.hpp"
 #include "hk_gemm_device.hpp"
 
@@ -60,7 +60,7 @@ __device__ __forceinline__ const uint16_t* weight_slice(const ProgramArgs& p, in
 // tile kernel; B stored [K,N] (not tb) is its MN-major B operand. The tile kernel's partial last
 // K stage handles K % 64 != 0 and reads whole stages exactly as the full-stage variant when
 // K % 64 == 0, so one variant serves every K.
-template <bool OUT_BF16, bool TA, bool TB>
+template <bool OUT_BF16, bool TA, bool TB, bool WIDE>
 __device__ __forceinline__ void run_program(const RudaGm& a, const RudaGm& b, const RudaGm& d, uint32_t m, uint32_t n,
                                             uint32_t k, const int32_t* grouped_layout, uint32_t num_groups) {
     ProgramArgs p{};
@@ -76,21 +76,27 @@ __device__ __forceinline__ void run_program(const RudaGm& a, const RudaGm& b, co
     p.band_n = p.tiles_m == p.tiles_n ? 0 : 8;  // libhk.so's tile order for the shape
     p.group_ends = grouped_layout;
     p.num_groups = static_cast<int>(num_groups);
-    gemm_m16_tile<OUT_BF16, TA, !TB, true>(p);
+    gemm_m16_tile<OUT_BF16, TA, !TB, true, ProgramArgs, 8, kEpiPlain, WIDE>(p);
 }
 
 }  // namespace
 
 }  // namespace hk
 
-#define HK_PROGRAM(NAME, OUT_BF16, TA, TB)                                                                       \
+// Each program NAME has a companion NAME_wide, the same program for operand slices past 32-bit
+// byte offsets (M*K or N*K >= 2^30 elements); the driver launches it in NAME's place for those
+// shapes. It is not one of the reference's names and callers never ask for it.
+#define HK_PROGRAM_ENTRY(SYMBOL, OUT_BF16, TA, TB, WIDE)                                                        \
     extern "C" __global__ void __launch_bounds__(hk::kW4Threads, 1)                                            \
-        NAME(hk::RudaGm gm_a, hk::RudaGm gm_b, hk::RudaGm gm_d, uint32_t shape_m, uint32_t shape_n,             \
-             uint32_t shape_k, int32_t* grouped_layout, uint32_t num_groups, hk::RudaEpilogue epilogue) {         \
+        SYMBOL(hk::RudaGm gm_a, hk::RudaGm gm_b, hk::RudaGm gm_d, uint32_t shape_m, uint32_t shape_n,           \
+               uint32_t shape_k, int32_t* grouped_layout, uint32_t num_groups, hk::RudaEpilogue epilogue) {       \
         (void)epilogue;                                                                                        \
-        hk::run_program<OUT_BF16, TA, TB>(gm_a, gm_b, gm_d, shape_m, shape_n, shape_k, grouped_layout,         \
-                                          num_groups);                                                         \
+        hk::run_program<OUT_BF16, TA, TB, WIDE>(gm_a, gm_b, gm_d, shape_m, shape_n, shape_k, grouped_layout,   \
+                                                num_groups);                                                   \
     }
+#define HK_PROGRAM(NAME, OUT_BF16, TA, TB)               \
+    HK_PROGRAM_ENTRY(NAME, OUT_BF16, TA, TB, false)      \
+    HK_PROGRAM_ENTRY(NAME##_wide, OUT_BF16, TA, TB, true)
 
 HK_PROGRAM(ruda_rust_bf16_dense_nn_bf16, true, false, false)
 HK_PROGRAM(ruda_rust_bf16_dense_nn_f32, false, false, false)

@@ -9,6 +9,8 @@ rust-ascend-kernels/src/ascend.rs:88-114):
   where both run the 256x256-tile kernel: the programs are that kernel behind the reference's
   argument structs, with the group-end table read in place of libhk.so's per-block table;
 * small and ragged shapes against the f64 oracle;
+* operand slices past 32-bit byte offsets (2^30 elements: each program's wide companion), exact on
+  integer-valued inputs;
 * the launch contract: every argument checked before the launch, the context healthy after.
 """
 import ctypes
@@ -210,6 +212,57 @@ def test_launch_contract_rejections_keep_the_context_healthy(dg):
     # the context still computes
     y = dg.gemm(a_t, b_t, Transpose.No, Transpose.Yes, torch.float32)
     f32_close(host(y), oracle.gemm_f64(a, b, 0, 1), "after rejections")
+
+
+# ------------------------------------------------------------------ operands past 32-bit offsets
+
+def _small_ints(shape, seed):
+    """BF16 integers in [-2, 2]: products and sums of up to 2^22 of them are exact in F32, so every
+    summation order gives the same F32 bits and any addressing mistake shows."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    return torch.randint(-2, 3, shape, generator=g, device=DEV, dtype=torch.int16).to(torch.bfloat16)
+
+
+# (ta, tb, m, n, k): an operand slice of 2^30 elements (2 GiB), past the 32-bit offsets of the
+# plain programs, so the driver runs each program's wide companion. The reference accepts these
+# (M/N/K <= INT32_MAX, plan.rs:72-77): e.g. a 131072-row vocabulary projection with K = 8192.
+WIDE_SHAPES = [
+    (0, 1, 256, 131072, 8192),  # NT: B [N, K], K-major
+    (0, 0, 256, 131072, 8192),  # NN: B stored [K, N], MN-major
+    (1, 0, 131072, 256, 8192),  # TN: A stored [K, M], MN-major
+    (0, 1, 131072, 272, 8192),  # NT: A [M, K], K-major, ragged N
+]
+
+
+@pytest.mark.parametrize("ta,tb,m,n,k", WIDE_SHAPES)
+def test_programs_past_32bit_offsets_are_exact(dg, ta, tb, m, n, k):
+    print(f"wide program ta={ta} tb={tb} m={m} n={n} k={k}", flush=True)
+    a_t = _small_ints((k, m) if ta else (m, k), seed=m + ta)
+    b_t = _small_ints((n, k) if tb else (k, n), seed=n + tb + 1)
+    af, bf = a_t.float(), b_t.float()
+    want = (af.t() if ta else af) @ (bf.t() if tb else bf)  # exact: |sum| <= 4 K = 2^15
+    del af, bf
+    got = dg.gemm(a_t, b_t, Transpose(ta), Transpose(tb), torch.float32)
+    assert torch.equal(got, want), float((got - want).abs().max())
+    del got
+    got16 = dg.gemm(a_t, b_t, Transpose(ta), Transpose(tb), torch.bfloat16)
+    assert torch.equal(got16, want.to(torch.bfloat16))
+
+
+def test_programs_reject_shapes_past_the_wide_reach(dg):
+    """M*K >= 2^30 with K >= 2^22 (a K-major tile's 256 rows pass 2^31 bytes) is refused before any
+    address is looked at; the context still computes."""
+    fn = dg.prepare("bf16_dense_nt_bf16")
+    m, n, k = 256, 256, 1 << 22
+    t = torch.zeros((16, 16), dtype=torch.bfloat16, device=DEV)
+    argv, _keep = _argv(HkGm(t.data_ptr(), k, 0), HkGm(t.data_ptr(), k, 0), HkGm(t.data_ptr(), n, 0), m, n, k)
+    with pytest.raises(HkError, match="too large for the device programs"):
+        _launch(fn, argv)
+    a_t, a = randn_bf16((64, 32), seed=5)
+    b_t, b = randn_bf16((48, 32), seed=6)
+    f32_close(host(dg.gemm(a_t, b_t, Transpose.No, Transpose.Yes, torch.float32)), oracle.gemm_f64(a, b, 0, 1),
+              "after the rejection")
 
 
 def test_module_lifecycle_and_stats():
