@@ -46,7 +46,7 @@ GEMMS = {
 }
 # CPU-baseline sample rows per GEMM workload (None: the whole product)
 CPU_ROWS = {"gemm8192_nt": 256, "gemm8192_nn": 16, "llama_up": 256, "llama_down": 256}
-KERNELS = sorted(list(GEMMS) + ["c2", "attn_fwd", "attn_bwd", "rope"])
+KERNELS = sorted(list(GEMMS) + ["c2", "attn_fwd", "attn_bwd", "rope", "c5"])
 
 
 def parse():
@@ -402,6 +402,13 @@ def run_kernel(name, steps, warmup):
                                                             dqkv[4]))]
         else:
             calls = [lambda: check(lib.hk_attention_backward(ctx, *dqkv, sc, 1, z, z, dq, dk, dv))]
+    elif name == "c5":  # one decoder-layer step (forward + backward), as bench_decoder builds it
+        from rust_ascend_hip import DecoderConfig, DecoderLayer
+        cfg = DecoderConfig()
+        layer = DecoderLayer(cfg, seed=5)
+        layer.ids.copy_(torch.randint(0, cfg.vocab, (cfg.batch, cfg.seq), generator=g, device="cuda"))
+        layer.dy.copy_(torch.randn(layer.dy.shape, generator=g, device="cuda").to(torch.bfloat16))
+        calls = [layer.step]
     else:  # rope
         import numpy as np
         pos = np.arange(4096, dtype=np.float64)[:, None]
@@ -817,9 +824,14 @@ def c5_line(steps=5, warmup=2, cpu=True):
             "ms": round(step_ms, 4), "fwd_ms": round(f_ms, 4), "bwd_ms": round(b_ms, 4),
             "model_TFLOPs": round(tflops, 1),
             # the layer is GEMM-dominated (96 % of its model flops are the projections): its
-            # roofline is the model flops over the step against the BF16 MFMA peak
+            # roofline is the model flops over the step against the BF16 MFMA peak; traffic and
+            # MFMA utilisation are the step's counters (all its kernels) when measured
             "roofline": {"kernel": "gemm_nt_m16_kernel (96 % of the flops)", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                          "traffic_MB": None}}
+    counters = read_counters("c5")
+    if counters:
+        line["roofline"]["traffic_MB"] = round(counters["traffic"] / 1e6)
+        line["roofline"]["mfma_util"] = counters["mfma_util"]
     if cpu:
         line["cpu_baseline"] = short_cpu(cpu_baseline_decoder())
     return line
