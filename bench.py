@@ -891,7 +891,9 @@ def main():
                    "fwd_ms": round(fwd_ms, 5), "bwd_ms": round(bwd_ms, 5),
                    "fwd_GBps": round(C2_FWD_BYTES / fwd_ms / 1e6, 1),
                    "bwd_GBps": round(C2_BWD_BYTES / bwd_ms / 1e6, 1)},
-        "roofline": roofline("hbm", C2_BWD_BYTES, bwd_ms, "rms_bwd_split"),
+        # the backward call is two kernels (the row kernel and the dγ partial sum); the events
+        # time the call, so the roofline is the call's
+        "roofline": roofline("hbm", C2_BWD_BYTES, bwd_ms, "rms_bwd_split+sum_partials8"),
     }
     if not args.no_secondary:
         # Ordered so that the lines of the BASELINE configs come last in the printed line.
