@@ -868,6 +868,12 @@ struct BwdArgs {
     const float* rope_cos;
     const float* rope_sin;
     int rope_layout;
+    // dK/dV split (splits > 1): each head's query steps of a key block are divided into `splits`
+    // contiguous ranges, one workgroup each, which write their F32 dK (scaled) and dV sums to
+    // partial[((split * 2 + kv) * B Hkv + bkv) * n + key][d] (kv 0: dK, 1: dV); attn_bwd_dkdv_reduce
+    // adds them in split order and stores the result as the unsplit kernel would.
+    int splits;
+    float* partial;
 };
 
 // Layout inside a dS block: four 1 KB chunks c = 2 qt + h, each holding 64 lanes x 16 bytes as
@@ -1032,6 +1038,40 @@ __device__ __forceinline__ uint32_t lds_address_f(const float* p) {
 constexpr int kQStep = 64;    // queries per step of the dK/dV kernel
 constexpr int kKBlock = 128;  // keys per dK/dV workgroup (4 waves x 32)
 
+// dK (scaled here: the kernel leaves the softmax scale out of dS) and dV of key my_key of (b, kvh)
+// from a lane's accumulators (head dims 32 dt + 8 g4 + 4 lg + e in acc[dt][4 g4 + e]): BF16/F32
+// planes, or the rows output with RoPE's transpose on dK.
+template <int D, int DT>
+__device__ __forceinline__ void dkdv_store(const BwdArgs& a, int64_t b, int64_t kvh, int bkv, int64_t my_key, int lg,
+                                           f32x16_t (&dk)[DT], f32x16_t (&dv)[DT]) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) dk[dt][v] *= a.scale;
+    if constexpr (D >= 64) {
+        if (a.rows != nullptr) {
+            if (my_key < a.n) {
+                store_grad_row<D, DT>(a, b, my_key, (a.heads + kvh) * D, true, lg, dk);
+                store_grad_row<D, DT>(a, b, my_key, (a.heads + a.kv_heads + kvh) * D, false, lg, dv);
+            }
+            return;
+        }
+    }
+    if (my_key < a.n) {
+        const int64_t row = static_cast<int64_t>(bkv) * a.n + my_key;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int d = 32 * dt + 8 * g4 + 4 * lg;
+                const float kv4[4] = {dk[dt][4 * g4], dk[dt][4 * g4 + 1], dk[dt][4 * g4 + 2], dk[dt][4 * g4 + 3]};
+                const float vv4[4] = {dv[dt][4 * g4], dv[dt][4 * g4 + 1], dv[dt][4 * g4 + 2], dv[dt][4 * g4 + 3]};
+                store_row4<D>(a.dk, a.dkv_bf16, row, d, kv4);
+                store_row4<D>(a.dv, a.dkv_bf16, row, d, vv4);
+            }
+    }
+}
+
 // dK and dV of 128 keys of one (batch, KV head): loop over the group's query heads (in head
 // order) and over 64-query steps, accumulating in registers; no atomics.
 //   S = Q K^T and dP = dO V^T are computed with the queries as rows and this wave's 32 keys
@@ -1041,7 +1081,11 @@ constexpr int kKBlock = 128;  // keys per dK/dV workgroup (4 waves x 32)
 //   The Q/dO tiles and the rows' statistics of step it+1 are fetched straight into LDS (no
 //   staging registers) while step it is computed, and waited for before the barrier that ends
 //   step it.
-template <int D>
+//   Split (a.splits > 1, for grids too small or too uneven to keep every CU busy: causal key
+//   blocks near the start see every query, those near the end few of them): each head's query
+//   steps of the key block are divided among a.splits workgroups (contiguous ranges), whose F32
+//   partial sums attn_bwd_dkdv_reduce adds.
+template <int D, bool SPLIT>
 __global__ void __launch_bounds__(kThreads, 1)
 attn_bwd_dkdv(BwdArgs a) {
     constexpr int DP = D < 32 ? 32 : D;
@@ -1057,8 +1101,10 @@ attn_bwd_dkdv(BwdArgs a) {
     // logical order: (batch, KV head), key block heaviest first -- the workgroups resident on
     // one XCD read the same Q / dO heads
     const int logical = xcd_logical();
-    const int bkv = logical / a.blocks;  // b * kv_heads + kvh
-    const int nb = logical % a.blocks;
+    const int splits = SPLIT ? a.splits : 1;
+    const int bkv = logical / (a.blocks * splits);  // b * kv_heads + kvh
+    const int nb = logical % (a.blocks * splits) / splits;
+    const int split = SPLIT ? logical % splits : 0;
     const int64_t b = bkv / a.kv_heads;
     const int64_t group = a.heads / a.kv_heads;
     const int64_t kvh = bkv % a.kv_heads;
@@ -1094,8 +1140,14 @@ attn_bwd_dkdv(BwdArgs a) {
         qfirst = n0 - a.diag;
         qfirst = qfirst < 0 ? 0 : qfirst;
     }
-    const int step0 = static_cast<int>(qfirst / kQStep);
-    const int nsteps_head = qfirst < a.m ? static_cast<int>((a.m + kQStep - 1) / kQStep) - step0 : 0;
+    int step0 = static_cast<int>(qfirst / kQStep);
+    int nsteps_head = qfirst < a.m ? static_cast<int>((a.m + kQStep - 1) / kQStep) - step0 : 0;
+    if constexpr (SPLIT) {  // this split's share of each head's query steps
+        const int chunk = (nsteps_head + splits - 1) / splits;
+        const int s0 = min(split * chunk, nsteps_head), s1 = min(s0 + chunk, nsteps_head);
+        step0 += s0;
+        nsteps_head = s1 - s0;
+    }
     const int total = nsteps_head * static_cast<int>(group);
 
     const int tile_voff = TDma::lane_offset(wave, lane);
@@ -1242,32 +1294,63 @@ attn_bwd_dkdv(BwdArgs a) {
         lds_barrier();
     }
 
+    if constexpr (SPLIT) {
+        // this split's sums (dK scaled) as F32 planes: the store path of the unsplit kernel, with
+        // the partial planes as its dK and dV
+        BwdArgs pa = a;
+        const int64_t nkv = a.n * (static_cast<int64_t>(gridDim.x) / (a.blocks * splits));
+        pa.dk = a.partial + static_cast<int64_t>(split) * 2 * nkv * D;
+        pa.dv = a.partial + (static_cast<int64_t>(split) * 2 + 1) * nkv * D;
+        pa.dkv_bf16 = 0;
+        pa.rows = nullptr;
+        dkdv_store<D, DT>(pa, b, kvh, bkv, my_key, lg, dk, dv);
+    } else {
+        dkdv_store<D, DT>(a, b, kvh, bkv, my_key, lg, dk, dv);
+    }
+}
+
+// The splits' F32 partial dK (scaled) and dV of 128 keys of one (batch, KV head), added in split
+// order and stored by dkdv_store (BF16/F32 planes or rows output; scale 1, the partials carry it)
+// in the dK/dV kernel's lane layout: the result is what that kernel stores unsplit, up to the
+// order of the F32 additions.
+template <int D>
+__global__ void __launch_bounds__(kThreads)
+attn_bwd_dkdv_reduce(BwdArgs a) {
+    constexpr int DP = D < 32 ? 32 : D;
+    constexpr int DT = DP / 32;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lq = lane & 31, lg = lane >> 5;
+    const int bkv = blockIdx.x / a.blocks, nb = blockIdx.x % a.blocks;
+    const int64_t b = bkv / a.kv_heads, kvh = bkv % a.kv_heads;
+    const int64_t my_key = static_cast<int64_t>(nb) * kKBlock + wave * 32 + lq;
+    if (my_key >= a.n) return;
+    const int64_t nkv = a.n * static_cast<int64_t>(gridDim.x / a.blocks);
+    f32x16_t dk[DT], dv[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) dk[dt][v] *= a.scale;
-    if constexpr (D >= 64) {
-        if (a.rows != nullptr) {
-            if (my_key < a.n) {
-                store_grad_row<D, DT>(a, b, my_key, (a.heads + kvh) * D, true, lg, dk);
-                store_grad_row<D, DT>(a, b, my_key, (a.heads + a.kv_heads + kvh) * D, false, lg, dv);
-            }
-            return;
-        }
-    }
-    if (my_key < a.n) {
-        const int64_t row = static_cast<int64_t>(bkv) * a.n + my_key;
+        for (int v = 0; v < 16; ++v) dk[dt][v] = dv[dt][v] = 0.0f;
+    for (int sp = 0; sp < a.splits; ++sp) {
+        const float* pk = a.partial + ((static_cast<int64_t>(sp) * 2) * nkv + static_cast<int64_t>(bkv) * a.n + my_key) * D;
+        const float* pv = pk + nkv * D;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
                 const int d = 32 * dt + 8 * g4 + 4 * lg;
-                const float kv4[4] = {dk[dt][4 * g4], dk[dt][4 * g4 + 1], dk[dt][4 * g4 + 2], dk[dt][4 * g4 + 3]};
-                const float vv4[4] = {dv[dt][4 * g4], dv[dt][4 * g4 + 1], dv[dt][4 * g4 + 2], dv[dt][4 * g4 + 3]};
-                store_row4<D>(a.dk, a.dkv_bf16, row, d, kv4);
-                store_row4<D>(a.dv, a.dkv_bf16, row, d, vv4);
+                if (d >= D) continue;
+                const f32x4_t k4 = *reinterpret_cast<const f32x4_t*>(pk + d);
+                const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(pv + d);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dk[dt][4 * g4 + e] += k4[e];
+                    dv[dt][4 * g4 + e] += v4[e];
+                }
             }
     }
+    BwdArgs ra = a;
+    ra.scale = 1.0f;
+    dkdv_store<D, DT>(ra, b, kvh, bkv, my_key, lg, dk, dv);
 }
 
 // dQ of 128 queries of one (batch, head), looping over 64-key tiles up to the diagonal:
@@ -1643,10 +1726,40 @@ size_t stat_bytes(const AttnShape& sh) {  // row statistic and lse2, rounded to 
     return (2 * static_cast<size_t>(sh.batch * sh.heads * sh.m) * sizeof(float) + 255) & ~size_t(255);
 }
 
+// Workgroups per dK/dV key block: causal key blocks near the start of the sequence see every
+// query and those near its end few of them, so a grid of one round of workgroups (C5: 256 key
+// blocks on 256 CUs) takes as long as its heaviest block, ~1.9x the average at C5. Splitting
+// every block's steps s ways (s = 2 or 4) lets the dispatcher fill the CUs evenly: s is the
+// smallest whose heaviest share is at most the average work per CU, i.e. ratio = heaviest block x
+// CUs / all blocks' work <= s (1 when the ratio is at most 1: C4's four rounds already balance).
+// The environment variable HK_ATTN_DKV_SPLITS (1, 2 or 4) overrides the choice.
+int dkv_splits_for(const AttnShape& sh, int num_cus) {
+    if (const char* env = std::getenv("HK_ATTN_DKV_SPLITS")) {
+        const int v = std::atoi(env);
+        if (v == 1 || v == 2 || v == 4) return v;
+    }
+    const int64_t blocks = (sh.n + kKBlock - 1) / kKBlock, qsteps = (sh.m + kQStep - 1) / kQStep;
+    const int64_t group = sh.heads / sh.kv_heads, diag = clamp_diag(sh);
+    int64_t heaviest = 0, work = 0;
+    for (int64_t nb = 0; nb < blocks; ++nb) {
+        const int64_t qfirst = sh.causal ? std::max<int64_t>(nb * kKBlock - diag, 0) : 0;
+        const int64_t steps = qfirst < sh.m ? (qsteps - qfirst / kQStep) * group : 0;
+        heaviest = std::max(heaviest, steps);
+        work += steps;
+    }
+    work *= sh.batch * sh.kv_heads;
+    if (work == 0) return 1;
+    const double ratio = static_cast<double>(heaviest) * num_cus / static_cast<double>(work);
+    return ratio <= 1.0 ? 1 : (ratio <= 2.0 ? 2 : 4);
+}
+size_t partial_bytes(const AttnShape& sh) {  // the split's F32 dK and dV partial sums
+    return sh.dkv_splits > 1 ? static_cast<size_t>(sh.dkv_splits) * 2 * sh.batch * sh.kv_heads * sh.n * sh.d * 4 : 0;
+}
+
 template <int D>
 hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv, int dkv_bf16,
-                      const AttnRowsOut* rows_out, float* stat, uint16_t* ds, hipStream_t s) {
+                      const AttnRowsOut* rows_out, float* stat, uint16_t* ds, float* partial, hipStream_t s) {
     const int64_t rows = sh.batch * sh.heads * sh.m;
     constexpr int lanes = D / 8;
     const int64_t threads = rows * lanes;
@@ -1686,8 +1799,16 @@ hipError_t launch_bwd(const AttnShape& sh, const void* q, const void* k, const v
     a.rope_cos = rows_out ? rows_out->cos : nullptr;
     a.rope_sin = rows_out ? rows_out->sin : nullptr;
     a.rope_layout = rows_out ? rows_out->layout : 0;
-    hipLaunchKernelGGL((attn_bwd_dkdv<D>), dim3(static_cast<unsigned>(sh.batch * sh.kv_heads * a.blocks)),
-                       dim3(kThreads), 0, s, a);
+    a.splits = sh.dkv_splits;
+    a.partial = partial;
+    const dim3 dkdv_grid(static_cast<unsigned>(sh.batch * sh.kv_heads * a.blocks * a.splits));
+    if (a.splits > 1) {
+        hipLaunchKernelGGL((attn_bwd_dkdv<D, true>), dkdv_grid, dim3(kThreads), 0, s, a);
+        hipLaunchKernelGGL((attn_bwd_dkdv_reduce<D>), dim3(static_cast<unsigned>(sh.batch * sh.kv_heads * a.blocks)),
+                           dim3(kThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((attn_bwd_dkdv<D, false>), dkdv_grid, dim3(kThreads), 0, s, a);
+    }
     a.blocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
     if (ds)
         hipLaunchKernelGGL((attn_bwd_dq_ds<D>), dim3(static_cast<unsigned>(sh.batch * sh.heads * a.blocks)),
@@ -1711,9 +1832,14 @@ bool attention_shape_fits(const AttnShape& sh) {
     return fwd < kItemLimit && dkdv < kItemLimit && dq < kItemLimit;
 }
 
-void attention_bwd_plan(AttnShape& sh) { sh.store_ds = bwd_stores_ds(sh) ? 1 : 0; }
+void attention_bwd_plan(AttnShape& sh, int num_cus) {
+    sh.store_ds = bwd_stores_ds(sh) ? 1 : 0;
+    sh.dkv_splits = dkv_splits_for(sh, num_cus);
+}
 
-size_t attention_bwd_workspace_bytes(const AttnShape& sh) { return stat_bytes(sh) + ds_bytes(sh); }
+size_t attention_bwd_workspace_bytes(const AttnShape& sh) {
+    return stat_bytes(sh) + ((ds_bytes(sh) + 255) & ~size_t(255)) + partial_bytes(sh);
+}
 
 hipError_t attention_forward(const AttnShape& sh, const void* q, const void* k, const void* v, void* o, float* lse,
                              hipStream_t s) {
@@ -1730,13 +1856,16 @@ hipError_t attention_backward(const AttnShape& sh, const void* q, const void* k,
                               const float* lse, const void* dout, void* dq, int dq_bf16, void* dk, void* dv,
                               int dkv_bf16, const AttnRowsOut* rows, void* workspace, hipStream_t s) {
     float* stat = static_cast<float*>(workspace);
-    uint16_t* ds = sh.store_ds ? reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + stat_bytes(sh)) : nullptr;
+    char* after_stat = static_cast<char*>(workspace) + stat_bytes(sh);
+    uint16_t* ds = sh.store_ds ? reinterpret_cast<uint16_t*>(after_stat) : nullptr;
+    float* partial = sh.dkv_splits > 1 ? reinterpret_cast<float*>(after_stat + ((ds_bytes(sh) + 255) & ~size_t(255)))
+                                       : nullptr;
     if (rows && sh.d != 64 && sh.d != 128) return hipErrorInvalidValue;
     switch (sh.d) {
-        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, nullptr, stat, ds, s);
-        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, nullptr, stat, ds, s);
-        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, rows, stat, ds, s);
-        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, rows, stat, ds, s);
+        case 16: return launch_bwd<16>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, nullptr, stat, ds, partial, s);
+        case 32: return launch_bwd<32>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, nullptr, stat, ds, partial, s);
+        case 64: return launch_bwd<64>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, rows, stat, ds, partial, s);
+        case 128: return launch_bwd<128>(sh, q, k, v, o, lse, dout, dq, dq_bf16, dk, dv, dkv_bf16, rows, stat, ds, partial, s);
         default: return hipErrorInvalidValue;
     }
 }

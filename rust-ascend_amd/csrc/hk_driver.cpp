@@ -2596,17 +2596,18 @@ hk_status attention_backward_common(hk_context* h, const hk_tensor* q, const hk_
                                    static_cast<const float*>(sin->data), layout};
     }
     sh.o_f32 = o->dtype == HK_F32;
-    hk::attention_bwd_plan(sh);
     Staged sq = staged(q), sk = staged(k), sv = staged(v), sd = staged(dout);
     const size_t staging = sq.bytes + sk.bytes + sv.bytes + sd.bytes;
-    size_t stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
     OpGuard g(h);
     if (g.st != HK_OK) return g.st;
+    hk::attention_bwd_plan(sh, g.c->num_cus);
+    size_t stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
     st = ensure_workspace(g.c, stat_bytes + staging);
-    if (st == HK_HIP_ERROR && sh.store_ds) {
-        // the stored-dS buffer does not fit in free device memory: the recompute form of dQ
-        // needs only the row statistics
+    if (st == HK_HIP_ERROR && (sh.store_ds || sh.dkv_splits > 1)) {
+        // the stored-dS buffer or the split's partial sums do not fit in free device memory (or
+        // the workspace limit): the recompute form of dQ, unsplit, needs only the row statistics
         sh.store_ds = 0;
+        sh.dkv_splits = 1;
         stat_bytes = ws_round(hk::attention_bwd_workspace_bytes(sh));
         st = ensure_workspace(g.c, stat_bytes + staging);
     }

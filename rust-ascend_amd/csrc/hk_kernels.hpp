@@ -196,10 +196,11 @@ struct AttnShape {
     uint64_t query_start, key_start;
     int32_t o_f32 = 0;  // O (forward output, backward input) is F32 instead of BF16
     int32_t store_ds = 0;  // backward: dS stored for the dQ kernel (set by attention_bwd_plan)
+    int32_t dkv_splits = 1;  // backward: workgroups per dK/dV key block (set by attention_bwd_plan)
 };
-// Chooses the backward's dQ form for the shape (sets store_ds); the workspace size and the
-// backward call then follow that choice.
-void attention_bwd_plan(AttnShape& sh);
+// Chooses the backward's dQ form (store_ds) and dK/dV split (dkv_splits) for the shape on num_cus
+// CUs; the workspace size and the backward call then follow that choice.
+void attention_bwd_plan(AttnShape& sh, int num_cus);
 size_t attention_bwd_workspace_bytes(const AttnShape& sh);
 // Whether the fused kernels can take the shape: one head of Q/K/V (M*D and N*D BF16 elements)
 // within 32-bit buffer offsets, and every launch's work items within a dispatch's 32-bit count.

@@ -236,6 +236,50 @@ def test_backward_dq_form_follows_budget_and_workspace_limit(monkeypatch):
     assert HipRuntime.workspace_size() == 0
 
 
+# dK/dV split: each head's query steps of a key block over 1, 2 or 4 workgroups whose F32 partial
+# sums a reduce kernel adds (chosen by the CU fill of the grid; HK_ATTN_DKV_SPLITS forces it).
+# Shapes: causal and not, GQA and MHA, ragged M/N, a split whose share is empty (few steps), key
+# positions after the queries' (leading rows see no key).
+SPLIT_SHAPES = [  # (batch, heads, kv_heads, m, n, d, causal, query_start, key_start)
+    (1, 8, 2, 1024, 1024, 128, True, 0, 0),
+    (2, 4, 4, 300, 520, 64, True, 220, 0),
+    (1, 4, 1, 640, 640, 32, False, 0, 0),
+    (1, 2, 2, 96, 130, 16, True, 34, 0),
+    (1, 4, 2, 200, 260, 64, True, 1000, 1100),
+]
+
+
+@pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_backward_dkdv_splits_vs_oracle_and_unsplit(shape, dq_form, monkeypatch):
+    B, H, HKV, M, N, D, causal, qs, ks = shape
+    q_t, q = randn_bf16((B, H, M, D), seed=M + D + 1)
+    k_t, k = randn_bf16((B, HKV, N, D), seed=N + D + 2)
+    v_t, v = randn_bf16((B, HKV, N, D), seed=N + D + 3)
+    do_t, do = randn_bf16((B, H, M, D), seed=M + D + 4)
+    o, lse = HipRuntime.attention_forward(q_t, k_t, v_t, D ** -0.5, causal, qs, ks)
+    ref = oracle.attention_f64(q, k, v, do, scale=D ** -0.5, causal=causal, query_start=qs, key_start=ks,
+                               magnitudes=True)
+    got = {}
+    for splits in ("1", "2", "4"):
+        monkeypatch.setenv("HK_ATTN_DKV_SPLITS", splits)
+        print(f"dkdv splits {splits} shape {shape} form {dq_form}", flush=True)
+        dq, dk, dv = HipRuntime.attention_backward(q_t, k_t, v_t, o, lse, do_t, D ** -0.5, causal, qs, ks,
+                                                   grad_dtype=torch.float32)
+        for name, t in (("dk", dk), ("dv", dv)):
+            assert torch.all(torch.isfinite(t)), (splits, name)
+            mag_ok(host(t), ref[name], ref[name + "_mag"], 1e-2, f"{name} splits {splits}")
+        got[splits] = (host(dq), host(dk), host(dv))
+    # the splits change only the order of the F32 additions of dK and dV: per key row within
+    # 1e-5 of the unsplit result; dQ does not depend on them
+    for splits in ("2", "4"):
+        np.testing.assert_array_equal(got[splits][0], got["1"][0])
+        for i, name in ((1, "dk"), (2, "dv")):
+            a, b = got[splits][i], got["1"][i]
+            num = np.linalg.norm((a - b).reshape(-1, D), axis=1)
+            den = np.maximum(np.linalg.norm(b.reshape(-1, D), axis=1), 1e-30)
+            assert float(np.max(num / den)) <= 1e-5, (splits, name, float(np.max(num / den)))
+
+
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("m,n", [(256, 256), (200, 328), (64, 1000), (130, 130)])
