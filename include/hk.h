@@ -353,6 +353,15 @@ hk_status hk_rms_norm(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, d
 hk_status hk_rms_norm_backward(hk_context* ctx, const hk_tensor* x, const hk_tensor* w,
                                const hk_tensor* dy, const hk_tensor* rstd,
                                hk_tensor* dx, hk_tensor* dw);
+/* hk_rms_norm_backward with the residual branch's gradient added: dx = residual + the backward's dx,
+ * the dx as stored (BF16: rounded) plus the residual in F32, stored again; dw as
+ * hk_rms_norm_backward. Bit-identical to hk_rms_norm_backward followed by hk_bias_add(dx, no bias,
+ * residual): the reference's rms_norm backward (row_programs.rs:200-217, normalization.rs:168-186)
+ * and residual add (src/nn/affine.rs:14-25) of a pre-norm block's input, in one pass. residual:
+ * dX's dtype and shape, not overlapping dX. */
+hk_status hk_rms_norm_backward_residual(hk_context* ctx, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                                        const hk_tensor* rstd, const hk_tensor* residual, hk_tensor* dx,
+                                        hk_tensor* dw);
 /* hk_rms_norm_backward without any allocation: no counterpart in the reference. For callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). Same arguments, checks and results as hk_rms_norm_backward (the same

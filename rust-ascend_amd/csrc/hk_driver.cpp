@@ -2363,9 +2363,33 @@ hk_status hk_rms_norm_backward(hk_context* h, const hk_tensor* x, const hk_tenso
         return st;
     hk::RowCheck rc = row_check(g.c);
     hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
-                                         static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
-                                         static_cast<float*>(g.c->workspace), rows, width, rc, g.c->stream);
+                                         static_cast<const float*>(rstd->data), nullptr, dx->data,
+                                         static_cast<float*>(dw->data), static_cast<float*>(g.c->workspace), rows,
+                                         width, rc, g.c->stream);
     return row_check_result(g.c, complete(g.c, e, "rms_norm_backward", 2), rc, "rms_norm_backward");
+}
+
+hk_status hk_rms_norm_backward_residual(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
+                                        const hk_tensor* rstd, const hk_tensor* residual, hk_tensor* dx, hk_tensor* dw) {
+    const char* op = "rms_norm_backward_residual";
+    int64_t rows, width;
+    hk_status st = rms_backward_args(x, w, dy, rstd, dx, dw, &rows, &width);
+    if (st != HK_OK) return st;
+    if (!tensor_ok(residual, "residual")) return HK_INVALID_ARGUMENT;
+    if (residual->dtype != dx->dtype || !same_shape(residual, dx))
+        return fail(HK_INVALID_ARGUMENT, "%s requires a residual gradient of dX's dtype and shape", op);
+    if (!disjoint({dx}, {residual})) return HK_INVALID_ARGUMENT;
+    OpGuard g(h);
+    if (g.st != HK_OK) return g.st;
+    if ((st = ensure_workspace(g.c, hk::rms_backward_workspace_bytes(rows, width, x->data, w->data, dy->data,
+                                                                     dx->data))) != HK_OK)
+        return st;
+    hk::RowCheck rc = row_check(g.c);
+    hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
+                                         static_cast<const float*>(rstd->data), residual->data, dx->data,
+                                         static_cast<float*>(dw->data), static_cast<float*>(g.c->workspace), rows,
+                                         width, rc, g.c->stream);
+    return row_check_result(g.c, complete(g.c, e, op, 2), rc, op);
 }
 
 hk_status hk_rms_norm_backward_noalloc(hk_context* h, const hk_tensor* x, const hk_tensor* w, const hk_tensor* dy,
@@ -2386,8 +2410,9 @@ hk_status hk_rms_norm_backward_noalloc(hk_context* h, const hk_tensor* x, const 
     // scratch needs no clearing. Overlapping calls on one GPU share the array and race.
     hk::RowCheck rc = row_check(g.c);
     hipError_t e = hk::rms_norm_backward(x->dtype == HK_BF16, x->data, static_cast<const float*>(w->data), dy->data,
-                                         static_cast<const float*>(rstd->data), dx->data, static_cast<float*>(dw->data),
-                                         static_cast<float*>(g.c->scratch), rows, width, rc, g.c->stream);
+                                         static_cast<const float*>(rstd->data), nullptr, dx->data,
+                                         static_cast<float*>(dw->data), static_cast<float*>(g.c->scratch), rows, width,
+                                         rc, g.c->stream);
     return row_check_result(g.c, complete(g.c, e, "rms_norm_backward_noalloc", 2), rc, "rms_norm_backward_noalloc");
 }
 

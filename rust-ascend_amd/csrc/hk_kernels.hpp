@@ -24,8 +24,9 @@ size_t rms_backward_workspace_bytes(int64_t rows, int64_t width, const void* x, 
                                     const void* dx);
 hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void* y, float* rstd,
                             int64_t rows, int64_t width, float eps, RowCheck& rc, hipStream_t s);
+// res (nullable, like dx): dx = res + the backward's dx as stored, added in F32 and stored again.
 hipError_t rms_norm_backward(int dtype_bf16, const void* x, const float* w, const void* dy,
-                             const float* rstd, void* dx, float* dw, float* workspace, int64_t rows,
+                             const float* rstd, const void* res, void* dx, float* dw, float* workspace, int64_t rows,
                              int64_t width, RowCheck& rc, hipStream_t s);
 
 // ---- RoPE and casts (hk_rope.hip)

@@ -268,11 +268,25 @@ rms_fwd_split(const T* __restrict__ x, const float* __restrict__ w, T* __restric
     }
 }
 
-template <typename T, int CPL, bool FULL>
+// v as a store of type T keeps it (BF16: rounded to nearest even; F32: v itself) plus r: the
+// empty asm makes v a finished value, so the product that formed it is not contracted into the
+// add (the unfused composition stores v, then adds).
+template <typename T>
+__device__ __forceinline__ float add_stored(float v, float r) {
+    float s;
+    if constexpr (sizeof(T) == 2) s = round_bf16(v);
+    else s = v;
+    asm volatile("" : "+v"(s));
+    return s + r;
+}
+
+// RES: dx = res + (the row's dx as stored), added in F32 and stored again -- the backward followed
+// by a residual add of the stored dx, in one pass (a decoder layer's residual branch gradient).
+template <typename T, int CPL, bool FULL, bool RES>
 __global__ void __launch_bounds__(kSplitThreads)
 rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
-              const float* __restrict__ rstd, T* __restrict__ dx, double* __restrict__ partial, int64_t rows,
-              int chunks, int qn, int groups, SplitCheck chk) {
+              const float* __restrict__ rstd, const T* __restrict__ res, T* __restrict__ dx,
+              double* __restrict__ partial, int64_t rows, int chunks, int qn, int groups, SplitCheck chk) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     uint64_t* post = reinterpret_cast<uint64_t*>(lds_raw);
     float* w_lds = reinterpret_cast<float*>(lds_raw + kPostBytes);
@@ -333,6 +347,12 @@ rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __r
             }
         }
         dot = wave_sum(dot);
+        Raw8<T> rs[RES ? CPL : 1];
+        if constexpr (RES) {  // issued before the exchange wait, used at the stores
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (FULL || cbase + 64 * j < chunks) rs[j].load(res + row * W + 8 * (cbase + 64 * j));
+        }
         const float total = split_row_sum(post, g, qn, q, k, lane, dot, chk);
         const float corr = (total * inv_w) * (r * r);
         T* dr = dx + row * W;
@@ -348,6 +368,12 @@ rms_bwd_split(const T* __restrict__ x, const float* __restrict__ w, const T* __r
                 load8(w_lds + 8 * c, wv);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) o[e] = (gv[e] * wv[e] - xv[e] * corr) * r;
+                if constexpr (RES) {
+                    float rv[8];
+                    rs[j].get(rv);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = add_stored<T>(o[e], rv[e]);
+                }
                 store8_stream(dr + 8 * c, o);
             }
         }
@@ -481,7 +507,8 @@ rms_fwd_general(const T* __restrict__ x, const float* __restrict__ w, T* __restr
 template <typename T>
 __global__ void __launch_bounds__(kRowsThreads)
 rms_bwd_dx_general(const T* __restrict__ x, const float* __restrict__ w, const T* __restrict__ dy,
-                   const float* __restrict__ rstd, T* __restrict__ dx, int64_t rows, int64_t width) {
+                   const float* __restrict__ rstd, const T* __restrict__ res, T* __restrict__ dx, int64_t rows,
+                   int64_t width) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int waves_per_block = blockDim.x >> 6;
@@ -496,8 +523,10 @@ rms_bwd_dx_general(const T* __restrict__ x, const float* __restrict__ w, const T
         dot = wave_sum(dot);
         const float corr = (dot / static_cast<float>(width)) * (r * r);
         T* dr = dx + row * width;
-        for (int64_t c = lane; c < width; c += 64)
-            Elem<T>::store(dr, c, (Elem<T>::load(gr, c) * w[c] - Elem<T>::load(xr, c) * corr) * r);
+        for (int64_t c = lane; c < width; c += 64) {
+            const float v = (Elem<T>::load(gr, c) * w[c] - Elem<T>::load(xr, c) * corr) * r;
+            Elem<T>::store(dr, c, res ? add_stored<T>(v, Elem<T>::load(res + row * width, c)) : v);
+        }
     }
 }
 
@@ -566,14 +595,16 @@ int split_grid(int64_t rows, int groups) { return grid_for_rows(rows, groups, 25
 
 template <typename T, int CPL>
 void launch_split(bool bwd, const SplitShape& sh, int grid, const void* x, const float* w, const void* dy,
-                  const float* rstd_in, void* out, float* rstd_out, double* partial, int64_t rows, float eps,
-                  const SplitCheck& chk, hipStream_t s) {
+                  const float* rstd_in, const void* res, void* out, float* rstd_out, double* partial, int64_t rows,
+                  float eps, const SplitCheck& chk, hipStream_t s) {
     const dim3 block(64 * sh.qn * sh.groups);
     const size_t lds = split_lds_bytes(sh.chunks, sh.groups, bwd);
     if (bwd) {
-        auto kernel = sh.full ? rms_bwd_split<T, CPL, true> : rms_bwd_split<T, CPL, false>;
+        auto kernel = res ? (sh.full ? rms_bwd_split<T, CPL, true, true> : rms_bwd_split<T, CPL, false, true>)
+                          : (sh.full ? rms_bwd_split<T, CPL, true, false> : rms_bwd_split<T, CPL, false, false>);
         hipLaunchKernelGGL(kernel, dim3(grid), block, lds, s, static_cast<const T*>(x), w, static_cast<const T*>(dy),
-                           rstd_in, static_cast<T*>(out), partial, rows, sh.chunks, sh.qn, sh.groups, chk);
+                           rstd_in, static_cast<const T*>(res), static_cast<T*>(out), partial, rows, sh.chunks, sh.qn,
+                           sh.groups, chk);
     } else {
         auto kernel = sh.full ? rms_fwd_split<T, CPL, true> : rms_fwd_split<T, CPL, false>;
         hipLaunchKernelGGL(kernel, dim3(grid), block, lds, s, static_cast<const T*>(x), w, static_cast<T*>(out),
@@ -583,17 +614,17 @@ void launch_split(bool bwd, const SplitShape& sh, int grid, const void* x, const
 
 template <typename T>
 void run_split(bool bwd, int64_t width, const void* x, const float* w, const void* dy, const float* rstd_in,
-               void* out, float* rstd_out, double* partial, int* parts, int64_t rows, float eps, RowCheck& rc,
-               hipStream_t s) {
+               const void* res, void* out, float* rstd_out, double* partial, int* parts, int64_t rows, float eps,
+               RowCheck& rc, hipStream_t s) {
     const SplitShape sh = split_shape(width);
     const int grid = split_grid(rows, sh.groups);
     if (parts) *parts = grid;
     const SplitCheck chk{rc.flag, rc.seq, rc.spin_limit > 0 ? rc.spin_limit : 1};
     rc.used = 1;
     if (sh.cpl == 2)
-        launch_split<T, 2>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, chk, s);
+        launch_split<T, 2>(bwd, sh, grid, x, w, dy, rstd_in, res, out, rstd_out, partial, rows, eps, chk, s);
     else
-        launch_split<T, 1>(bwd, sh, grid, x, w, dy, rstd_in, out, rstd_out, partial, rows, eps, chk, s);
+        launch_split<T, 1>(bwd, sh, grid, x, w, dy, rstd_in, res, out, rstd_out, partial, rows, eps, chk, s);
 }
 
 int parts_general(int64_t rows) {
@@ -613,7 +644,7 @@ hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, in
         else if (chunks_per_lane <= 4) launch_fwd_fast<T, 4>(x, w, y, rstd, rows, (int)width, eps, s);
         else launch_fwd_fast<T, 8>(x, w, y, rstd, rows, (int)width, eps, s);
     } else if (split_rows(width, {x, w, y})) {  // 4096 < W <= 16384
-        run_split<T>(false, width, x, w, nullptr, nullptr, y, rstd, nullptr, nullptr, rows, eps, rc, s);
+        run_split<T>(false, width, x, w, nullptr, nullptr, nullptr, y, rstd, nullptr, nullptr, rows, eps, rc, s);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_fwd_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
@@ -623,7 +654,7 @@ hipError_t rms_forward_t(const void* x, const float* w, void* y, float* rstd, in
 }
 
 template <typename T>
-hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const float* rstd, void* dx,
+hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const float* rstd, const void* res, void* dx,
                           float* dw, void* ws, int64_t rows, int64_t width, RowCheck& rc, hipStream_t s) {
     double* workspace = static_cast<double*>(ws);  // the FP64 dγ partials
     if (rows == 0) {
@@ -632,14 +663,14 @@ hipError_t rms_backward_t(const void* x, const float* w, const void* dy, const f
     }
     if (split_rows(width, {x, w, dy, dx})) {
         int parts = 0;  // one FP64 partial row per workgroup, at most 256
-        run_split<T>(true, width, x, w, dy, rstd, dx, nullptr, workspace, &parts, rows, 0.0f, rc, s);
+        run_split<T>(true, width, x, w, dy, rstd, res, dx, nullptr, workspace, &parts, rows, 0.0f, rc, s);
         hipLaunchKernelGGL(sum_partials8, dim3(static_cast<unsigned>(width / 8)), dim3(256), 0, s, workspace, parts,
                            (int)width, dw);
     } else {
         const int grid = grid_for_rows(rows, kRowsThreads / 64, 4096);
         hipLaunchKernelGGL((rms_bwd_dx_general<T>), dim3(grid), dim3(kRowsThreads), 0, s,
-                           static_cast<const T*>(x), w, static_cast<const T*>(dy), rstd, static_cast<T*>(dx),
-                           rows, width);
+                           static_cast<const T*>(x), w, static_cast<const T*>(dy), rstd, static_cast<const T*>(res),
+                           static_cast<T*>(dx), rows, width);
         const int parts = parts_general(rows);
         const int64_t per = (rows + parts - 1) / parts;
         hipLaunchKernelGGL((rms_bwd_dw_general<T>), dim3((width + 255) / 256, parts), dim3(256), 0, s,
@@ -669,10 +700,10 @@ hipError_t rms_norm_forward(int dtype_bf16, const void* x, const float* w, void*
 }
 
 hipError_t rms_norm_backward(int dtype_bf16, const void* x, const float* w, const void* dy,
-                             const float* rstd, void* dx, float* dw, float* workspace, int64_t rows,
+                             const float* rstd, const void* res, void* dx, float* dw, float* workspace, int64_t rows,
                              int64_t width, RowCheck& rc, hipStream_t s) {
-    return dtype_bf16 ? rms_backward_t<uint16_t>(x, w, dy, rstd, dx, dw, workspace, rows, width, rc, s)
-                      : rms_backward_t<float>(x, w, dy, rstd, dx, dw, workspace, rows, width, rc, s);
+    return dtype_bf16 ? rms_backward_t<uint16_t>(x, w, dy, rstd, res, dx, dw, workspace, rows, width, rc, s)
+                      : rms_backward_t<float>(x, w, dy, rstd, res, dx, dw, workspace, rows, width, rc, s);
 }
 
 }  // namespace hk

@@ -144,6 +144,7 @@ SIGNATURES = {
     "hk_rms_norm": [_CTX, _T, _T, ctypes.c_double, _T, _T],
     "hk_rms_norm_backward": [_CTX, _T, _T, _T, _T, _T, _T],
     "hk_rms_norm_backward_noalloc": [_CTX, _T, _T, _T, _T, _T, _T],
+    "hk_rms_norm_backward_residual": [_CTX, _T, _T, _T, _T, _T, _T, _T],
     "hk_rotary": [_CTX, _T, _T, _T, _i32, _T],
     "hk_rotary_backward": [_CTX, _T, _T, _T, _i32, _T],
     "hk_rotary_prefix": [_CTX, _T, _T, _T, _i32, _i32, _T],

@@ -91,7 +91,8 @@ class DecoderLayer:
         self.fused_rope = fused_rope and c.head_dim == 128 and c.hidden % 8 == 0
         # the O and down projections add their residual in the GEMM epilogue; gate and up are one GEMM
         # (weights interleaved in blocks of 16 rows) with SiLU-mul in its epilogue, and the SwiGLU
-        # backward runs in the epilogue of dY Wd, so dX and dW of gate/up are one GEMM each
+        # backward runs in the epilogue of dY Wd, so dX and dW of gate/up are one GEMM each; the two
+        # norms' backward add the residual branch's gradient as they store dX
         self.fused_ffn = fused_ffn and c.ffn % 16 == 0 and c.hidden % 16 == 0
         dev = torch.device(device)
         g = torch.Generator(device=dev)
@@ -204,9 +205,12 @@ class DecoderLayer:
                (lib.hk_linear_nt_backward, (d(self.n2), d(self._wg), d(self.dgate), d(self.dn2_g), d(gr["wg"]))),
                (lib.hk_linear_nt_backward, (d(self.n2), d(self._wu), d(self.dup), d(self.dn2_u), d(gr["wu"]))),
                (lib.hk_bias_add, (d(self.dn2_g), None, d(self.dn2_u), d(self.dn2)))]),
-            (lib.hk_rms_norm_backward, (d(self.h1), d(self.w2), d(self.dn2), d(self.rstd2), d(self.dh1_norm),
-                                        d(gr["w2"]))),
-            (lib.hk_bias_add, (d(self.dh1_norm), None, d(self.dy), d(self.dh1))),
+            # dh1 = dY (the residual branch) + the norm's backward: one pass in the fused composition
+            *([(lib.hk_rms_norm_backward_residual, (d(self.h1), d(self.w2), d(self.dn2), d(self.rstd2), d(self.dy),
+                                                    d(self.dh1), d(gr["w2"])))] if self.fused_ffn else
+              [(lib.hk_rms_norm_backward, (d(self.h1), d(self.w2), d(self.dn2), d(self.rstd2), d(self.dh1_norm),
+                                           d(gr["w2"]))),
+               (lib.hk_bias_add, (d(self.dh1_norm), None, d(self.dy), d(self.dh1)))]),
             # h1 = x0 + rows(o) Wo^T
             (lib.hk_linear_nt_backward, (rows(self.o_rows, H), d(self.wo), d(self.dh1), rows(self.do_rows, H),
                                          d(gr["wo"]))),
@@ -219,9 +223,11 @@ class DecoderLayer:
                (lib.hk_qkv_rope_merge, (d(self.dq), d(self.dk), d(self.dv), d(self.cos), d(self.sin), sh,
                                         d(self.dqkv)))]),
             (lib.hk_linear_nt_backward, (d(self.n1), d(self.wqkv), rows(self.dqkv, W), d(self.dn1), d(gr["wqkv"]))),
-            (lib.hk_rms_norm_backward, (d(self.x0), d(self.w1), d(self.dn1), d(self.rstd1), d(self.dx0_norm),
-                                        d(gr["w1"]))),
-            (lib.hk_bias_add, (d(self.dx0_norm), None, d(self.dh1), d(self.dx0))),
+            *([(lib.hk_rms_norm_backward_residual, (d(self.x0), d(self.w1), d(self.dn1), d(self.rstd1), d(self.dh1),
+                                                    d(self.dx0), d(gr["w1"])))] if self.fused_ffn else
+              [(lib.hk_rms_norm_backward, (d(self.x0), d(self.w1), d(self.dn1), d(self.rstd1), d(self.dx0_norm),
+                                           d(gr["w1"]))),
+               (lib.hk_bias_add, (d(self.dx0_norm), None, d(self.dh1), d(self.dx0)))]),
             (lib.hk_embedding_backward, (d(self.dx0.view(c.batch, c.seq, H)), d(self.ids), ctypes.c_uint64(c.vocab),
                                          ctypes.c_uint64(_lib.NO_PADDING), 0, d(gr["table"]))),
         ]

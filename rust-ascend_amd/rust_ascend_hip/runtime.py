@@ -658,6 +658,16 @@ class HipRuntime:
         _call("hk_rms_norm_backward", desc(x), desc(weight), desc(grad), desc(rstd), desc(dx), desc(dw))
         return dx, dw
 
+    @staticmethod
+    def rms_norm_backward_residual(x, weight, grad, rstd, residual):
+        """[dX + residual, F32 dW] in one pass: the norm's backward with a residual branch's
+        gradient added as dX is stored (hk_rms_norm_backward_residual)."""
+        dx = _empty(x.shape, x.dtype, x)
+        dw = _empty((x.shape[-1],), torch.float32, x)
+        _call("hk_rms_norm_backward_residual", desc(x), desc(weight), desc(grad), desc(rstd), desc(residual),
+              desc(dx), desc(dw))
+        return dx, dw
+
     # ---------------------------------------------------------------- RoPE
 
     @staticmethod

@@ -112,6 +112,47 @@ def test_rms_norm_c2_full_size_and_determinism():
     assert strict <= 1e-4, f"dW strict relative error {strict:.3e}"
 
 
+@pytest.mark.parametrize("dtype,rows,width,offset", [
+    (torch.bfloat16, 16384, 4096, 0),   # C2: the row-split kernel, two chunks per lane
+    (torch.bfloat16, 37, 1000, 0),      # split kernel, partial lanes
+    (torch.float32, 300, 4096, 0),      # F32 storage (the add is exact: no rounding in between)
+    (torch.bfloat16, 64, 4100, 0),      # width not a multiple of 8: the general kernels
+    (torch.bfloat16, 64, 512, 1),       # misaligned views: the general kernels
+])
+def test_rms_norm_backward_residual_bit_exact_with_backward_and_add(dtype, rows, width, offset):
+    """hk_rms_norm_backward_residual = hk_rms_norm_backward then hk_bias_add(dx, no bias, residual),
+    bit for bit, and the same dW."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(rows + width)
+
+    def rand(shape, std=1.0):
+        t = (torch.randn((shape[0] * shape[1] + offset,), generator=g, device=DEV) * std).to(dtype)
+        return t[offset:].view(shape)
+
+    x, dy, res = rand((rows, width)), rand((rows, width)), rand((rows, width), 0.5)
+    w = (1 + 0.1 * torch.randn((width,), generator=g, device=DEV)).float()
+    _, rstd = HipRuntime.rms_norm(x, w, 1e-6)
+    print(f"rms backward residual {dtype} {rows}x{width} offset {offset}", flush=True)
+    dx, dw = HipRuntime.rms_norm_backward_residual(x, w, dy, rstd, res)
+    dx0, dw0 = HipRuntime.rms_norm_backward(x, w, dy, rstd)
+    want = HipRuntime.bias_add(dx0, None, res)
+    assert torch.equal(dx, want)
+    assert torch.equal(dw, dw0)
+
+
+def test_rms_norm_backward_residual_rejects_bad_residual():
+    x, _ = randn_bf16((8, 64), seed=1)
+    dy, _ = randn_bf16((8, 64), seed=2)
+    w = torch.ones(64, device=DEV)
+    _, rstd = HipRuntime.rms_norm(x, w, 1e-6)
+    with pytest.raises(HkError, match="residual"):
+        HipRuntime.rms_norm_backward_residual(x, w, dy, rstd, torch.zeros((8, 64), device=DEV))  # F32
+    with pytest.raises(HkError, match="residual"):
+        HipRuntime.rms_norm_backward_residual(x, w, dy, rstd, torch.zeros((8, 32), device=DEV, dtype=torch.bfloat16))
+    dx, _ = HipRuntime.rms_norm_backward_residual(x, w, dy, rstd, torch.zeros_like(x))  # still healthy
+    assert torch.equal(dx, HipRuntime.rms_norm_backward(x, w, dy, rstd)[0])
+
+
 def test_rms_norm_empty_batch_and_known_answer(golden):
     w = dev_f32(np.ones(32, np.float32))
     x = torch.empty((0, 32), device=DEV)
