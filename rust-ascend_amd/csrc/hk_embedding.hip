@@ -214,6 +214,94 @@ digit_scatter_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restri
     }
 }
 
+// The whole sort in one workgroup for up to kSmallSort positions (C5: 4096): keys and positions
+// stay in LDS through every 8-bit pass, so a pass is a histogram, a 256-entry scan and a stable
+// scatter separated by barriers instead of three launches with global round trips. The scatter
+// takes the positions in rounds of 1024 in order, each wavefront ranking its lanes by ballots as
+// digit_scatter_kernel does, so the order is that of the multi-workgroup sort.
+constexpr int kSmallSortThreads = 1024;
+constexpr int kSmallSortWaves = kSmallSortThreads / kWave;
+constexpr int kSmallSort = 8192;
+__global__ void __launch_bounds__(kSmallSortThreads)
+small_sort_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ pos_in, int n, int bits,
+                  uint32_t* __restrict__ keys_out, uint32_t* __restrict__ pos_out) {
+    __shared__ uint32_t kb[2][kSmallSort];
+    __shared__ uint32_t pb[2][kSmallSort];
+    __shared__ uint32_t base[kDigits];
+    __shared__ uint32_t wave_count[kSmallSortWaves][kDigits];
+    const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        kb[0][i] = keys_in[i];
+        pb[0][i] = pos_in[i];
+    }
+    for (int i = t; i < kSmallSortWaves * kDigits; i += kSmallSortThreads) (&wave_count[0][0])[i] = 0;
+    int src = 0;
+    for (int shift = 0; shift < bits; shift += 8, src ^= 1) {
+        if (t < kDigits) base[t] = 0;
+        __syncthreads();
+        for (int i = t; i < n; i += kSmallSortThreads) atomicAdd(&base[(kb[src][i] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (t < kWave) {  // exclusive scan of the 256 digit counts by the first wavefront
+            uint32_t c[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                c[j] = base[4 * t + j];
+                sum += c[j];
+            }
+            uint32_t incl = sum;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const uint32_t y = __shfl_up(incl, off, kWave);
+                if (lane >= off) incl += y;
+            }
+            uint32_t run = incl - sum;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                base[4 * t + j] = run;
+                run += c[j];
+            }
+        }
+        __syncthreads();
+        for (int r0 = 0; r0 < n; r0 += kSmallSortThreads) {
+            const int i = r0 + t;
+            const bool active = i < n;
+            const uint32_t key = active ? kb[src][i] : 0u;
+            const uint32_t d = (key >> shift) & 255u;
+            uint64_t peers = __ballot(active);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const bool bit = (d >> b) & 1u;
+                const uint64_t set = __ballot(bit);
+                peers &= bit ? set : ~set;
+            }
+            const uint64_t below = peers & ((uint64_t{1} << lane) - 1);
+            if (active && below == 0) wave_count[w][d] = static_cast<uint32_t>(__popcll(peers));
+            __syncthreads();
+            if (active) {
+                uint32_t at = base[d] + static_cast<uint32_t>(__popcll(below));
+                for (int ww = 0; ww < w; ++ww) at += wave_count[ww][d];
+                kb[src ^ 1][at] = key;
+                pb[src ^ 1][at] = pb[src][i];
+            }
+            __syncthreads();
+            if (t < kDigits) {
+                uint32_t add = 0;
+#pragma unroll
+                for (int ww = 0; ww < kSmallSortWaves; ++ww) {
+                    add += wave_count[ww][t];
+                    wave_count[ww][t] = 0;
+                }
+                base[t] += add;
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        keys_out[i] = kb[src][i];
+        pos_out[i] = pb[src][i];
+    }
+}
+
 // One workgroup per table row v: the positions of ID v are sorted[offsets[v] .. + counts[v]).
 template <typename T>
 __global__ void __launch_bounds__(kEmbThreads)
@@ -292,10 +380,18 @@ EmbWs carve(void* base, int64_t tokens, int64_t vocab) {
     return w;
 }
 
-// Stable sort of (keys, pos) by the low `bits` bits of the keys, 8 bits per pass; returns the
-// buffers that hold the result (the input pair or the alternate pair).
+// Stable sort of (keys, pos) by the low `bits` bits of the keys, 8 bits per pass (in one workgroup
+// up to kSmallSort positions); returns the buffers that hold the result (the input pair or the
+// alternate pair).
 void sort_pairs(EmbWs& w, int64_t tokens, int bits, hipStream_t s, uint32_t** keys_out, uint32_t** pos_out) {
     uint32_t *k0 = w.keys, *p0 = w.pos, *k1 = w.keys_alt, *p1 = w.pos_alt;
+    if (tokens <= kSmallSort) {
+        hipLaunchKernelGGL(small_sort_kernel, dim3(1), dim3(kSmallSortThreads), 0, s, k0, p0, static_cast<int>(tokens),
+                           bits, k1, p1);
+        *keys_out = k1;
+        *pos_out = p1;
+        return;
+    }
     const int64_t tiles = sort_tiles(tokens);
     for (int shift = 0; shift < bits; shift += 8) {
         hipLaunchKernelGGL(digit_hist_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kSortThreads), 0, s, k0, tokens,

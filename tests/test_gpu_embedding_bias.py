@@ -199,12 +199,14 @@ def position_order_sums_f32(g, ids, vocab):
     return dw
 
 
-@pytest.mark.parametrize("tokens,vocab", [(70000, 5000), (20000, (1 << 20) + 3), (4097, 40000), (1, 1)])
+@pytest.mark.parametrize("tokens,vocab", [(70000, 5000), (20000, (1 << 20) + 3), (4097, 40000), (1, 1),
+                                          (8192, 32000), (8193, 32000), (3000, (1 << 20) + 3)])
 def test_embedding_backward_groups_in_position_order(tokens, vocab):
     """The grouping by ID is a stable radix sort (8-bit digits): 70000 positions span 18 sort
     tiles and a two-level scan of the digit histograms; a 2^20 + 3 row table needs three digit
     passes (the result lands in the other buffer pair); 40001 count entries take a multi-tile
-    scan. Gradient rows are F32 with magnitudes spread over 2^-20 .. 2^20, so the F32 sum of a row
+    scan; up to 8192 positions the sort runs in one workgroup's LDS (8192 and 3000 positions,
+    the latter over three passes), 8193 takes the multi-workgroup kernels. Gradient rows are F32 with magnitudes spread over 2^-20 .. 2^20, so the F32 sum of a row
     depends on the order of its positions: the result must equal, bit for bit, the sums taken in
     increasing position order."""
     rng = np.random.default_rng(tokens + vocab)
