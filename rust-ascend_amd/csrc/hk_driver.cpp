@@ -2172,7 +2172,8 @@ hk_status hk_embedding_backward(hk_context* h, const hk_tensor* grad, const hk_t
     hipError_t e = hk::embedding_backward(grad->dtype, grad->data, static_cast<int>(dtype_size(ids->dtype)), ids->data,
                                           dweight->data, tokens, vocab, width, padding_idx, scale_grad_by_freq,
                                           g.c->workspace, g.c->stream);
-    return ids_in_range(g.c, complete(g.c, e, "embedding_backward", tokens ? 5 : 3), vocab, g.c->workspace, 1);
+    st = complete(g.c, e, "embedding_backward", hk::embedding_backward_launches(tokens, vocab, width));
+    return ids_in_range(g.c, st, vocab, g.c->workspace, 1);
 }
 
 hk_status hk_softmax(hk_context* h, const hk_tensor* x, int32_t logarithmic, hk_tensor* y) {

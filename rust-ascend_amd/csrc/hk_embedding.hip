@@ -21,7 +21,10 @@
 // tile), and a scatter that places every element at its digit's slot plus its rank among the
 // tile's earlier elements with the same digit (ballots within a wavefront, LDS counts across
 // wavefronts and rounds), so equal digits keep their position order. The row offsets of dW come
-// from per-ID counts (integer atomics) and the same scan. Work: the lookup moves
+// from per-ID counts (integer atomics) and the same scan. Up to 8192 positions and 65535 table rows
+// (the decoder layer's 4096 x 32000) the whole grouping runs in one 1024-thread workgroup instead:
+// the same digit passes and ballot ranks over keys held in LDS, each ID's range then read off the
+// sorted keys. Work: the lookup moves
 // 2 * H * sizeof(T) bytes per token; the gradient reads H * sizeof(T) per token and writes
 // V * H * sizeof(T); the sort moves 16 bytes per token and pass.
 #include "hk_common.hpp"
@@ -222,30 +225,29 @@ digit_scatter_kernel(const uint32_t* __restrict__ keys, const uint32_t* __restri
 constexpr int kSmallSortThreads = 1024;
 constexpr int kSmallSortWaves = kSmallSortThreads / kWave;
 constexpr int kSmallSort = 8192;
-__global__ void __launch_bounds__(kSmallSortThreads)
-small_sort_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ pos_in, int n, int bits,
-                  uint32_t* __restrict__ keys_out, uint32_t* __restrict__ pos_out) {
-    __shared__ uint32_t kb[2][kSmallSort];
-    __shared__ uint32_t pb[2][kSmallSort];
-    __shared__ uint32_t base[kDigits];
-    __shared__ uint32_t wave_count[kSmallSortWaves][kDigits];
+struct SmallSortLds {
+    uint32_t kb[2][kSmallSort];
+    uint32_t pb[2][kSmallSort];
+    uint32_t base[kDigits];
+    uint32_t wave_count[kSmallSortWaves][kDigits];
+};
+
+// Sorts the n pairs in L.kb[0] / L.pb[0] (filled by the caller before a barrier); returns the
+// buffer index holding the result. Every thread of the workgroup calls it.
+__device__ int lds_radix_sort(SmallSortLds& L, int n, int bits) {
     const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
-    for (int i = t; i < n; i += kSmallSortThreads) {
-        kb[0][i] = keys_in[i];
-        pb[0][i] = pos_in[i];
-    }
-    for (int i = t; i < kSmallSortWaves * kDigits; i += kSmallSortThreads) (&wave_count[0][0])[i] = 0;
+    for (int i = t; i < kSmallSortWaves * kDigits; i += kSmallSortThreads) (&L.wave_count[0][0])[i] = 0;
     int src = 0;
     for (int shift = 0; shift < bits; shift += 8, src ^= 1) {
-        if (t < kDigits) base[t] = 0;
+        if (t < kDigits) L.base[t] = 0;
         __syncthreads();
-        for (int i = t; i < n; i += kSmallSortThreads) atomicAdd(&base[(kb[src][i] >> shift) & 255u], 1u);
+        for (int i = t; i < n; i += kSmallSortThreads) atomicAdd(&L.base[(L.kb[src][i] >> shift) & 255u], 1u);
         __syncthreads();
         if (t < kWave) {  // exclusive scan of the 256 digit counts by the first wavefront
             uint32_t c[4], sum = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                c[j] = base[4 * t + j];
+                c[j] = L.base[4 * t + j];
                 sum += c[j];
             }
             uint32_t incl = sum;
@@ -257,7 +259,7 @@ small_sort_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restri
             uint32_t run = incl - sum;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                base[4 * t + j] = run;
+                L.base[4 * t + j] = run;
                 run += c[j];
             }
         }
@@ -265,7 +267,7 @@ small_sort_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restri
         for (int r0 = 0; r0 < n; r0 += kSmallSortThreads) {
             const int i = r0 + t;
             const bool active = i < n;
-            const uint32_t key = active ? kb[src][i] : 0u;
+            const uint32_t key = active ? L.kb[src][i] : 0u;
             const uint32_t d = (key >> shift) & 255u;
             uint64_t peers = __ballot(active);
 #pragma unroll
@@ -275,34 +277,92 @@ small_sort_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restri
                 peers &= bit ? set : ~set;
             }
             const uint64_t below = peers & ((uint64_t{1} << lane) - 1);
-            if (active && below == 0) wave_count[w][d] = static_cast<uint32_t>(__popcll(peers));
+            if (active && below == 0) L.wave_count[w][d] = static_cast<uint32_t>(__popcll(peers));
             __syncthreads();
             if (active) {
-                uint32_t at = base[d] + static_cast<uint32_t>(__popcll(below));
-                for (int ww = 0; ww < w; ++ww) at += wave_count[ww][d];
-                kb[src ^ 1][at] = key;
-                pb[src ^ 1][at] = pb[src][i];
+                uint32_t at = L.base[d] + static_cast<uint32_t>(__popcll(below));
+                for (int ww = 0; ww < w; ++ww) at += L.wave_count[ww][d];
+                L.kb[src ^ 1][at] = key;
+                L.pb[src ^ 1][at] = L.pb[src][i];
             }
             __syncthreads();
             if (t < kDigits) {
                 uint32_t add = 0;
 #pragma unroll
                 for (int ww = 0; ww < kSmallSortWaves; ++ww) {
-                    add += wave_count[ww][t];
-                    wave_count[ww][t] = 0;
+                    add += L.wave_count[ww][t];
+                    L.wave_count[ww][t] = 0;
                 }
-                base[t] += add;
+                L.base[t] += add;
             }
             __syncthreads();
         }
     }
+    return src;
+}
+
+__global__ void __launch_bounds__(kSmallSortThreads)
+small_sort_kernel(const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ pos_in, int n, int bits,
+                  uint32_t* __restrict__ keys_out, uint32_t* __restrict__ pos_out) {
+    __shared__ SmallSortLds L;
+    const int t = threadIdx.x;
     for (int i = t; i < n; i += kSmallSortThreads) {
-        keys_out[i] = kb[src][i];
-        pos_out[i] = pb[src][i];
+        L.kb[0][i] = keys_in[i];
+        L.pb[0][i] = pos_in[i];
+    }
+    const int src = lds_radix_sort(L, n, bits);
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        keys_out[i] = L.kb[src][i];
+        pos_out[i] = L.pb[src][i];
     }
 }
 
-// One workgroup per table row v: the positions of ID v are sorted[offsets[v] .. + counts[v]).
+// The whole grouping for up to kSmallSort positions and tables of up to kSmallVocab rows in one
+// workgroup (C5: 4096 positions, 32000 rows): the check word and the V + 1 counts cleared, the
+// keys (ID, or V for an invalid ID) and positions built in LDS, sorted there, and each ID's
+// range read off the sorted keys (offsets[k] = its first slot, counts[k] = its run length; the
+// counts of IDs that do not occur stay 0) -- one launch for what the general path does in six
+// (clear, keys, sort passes, a multi-tile scan of the counts).
+constexpr int64_t kSmallVocab = 1 << 16;
+template <typename Idx>
+__global__ void __launch_bounds__(kSmallSortThreads)
+small_grouping_kernel(const Idx* __restrict__ ids, int n, int64_t vocab, int bits, uint32_t* __restrict__ counts,
+                      uint32_t* __restrict__ offsets, uint32_t* __restrict__ pos_out, int* __restrict__ flag) {
+    __shared__ SmallSortLds L;
+    const int t = threadIdx.x;
+    for (int64_t i = t; i <= vocab; i += kSmallSortThreads) counts[i] = 0;
+    if (t == 0) *flag = 0;
+    __syncthreads();  // the clears come before any count or check-word write below
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        const int64_t id = static_cast<int64_t>(ids[i]);
+        const bool valid = id >= 0 && id < vocab;
+        L.kb[0][i] = static_cast<uint32_t>(valid ? id : vocab);
+        L.pb[0][i] = static_cast<uint32_t>(i);
+        if (!valid) *flag = 1;
+    }
+    const int src = lds_radix_sort(L, n, bits);
+    // runs of equal keys: the last position of a run finds the run's first by a binary search of the
+    // sorted keys (in LDS) and writes both
+    const uint32_t* keys = L.kb[src];
+    for (int i = t; i < n; i += kSmallSortThreads) {
+        const uint32_t k = keys[i];
+        pos_out[i] = L.pb[src][i];
+        if (i == n - 1 || keys[i + 1] != k) {
+            int lo = 0, hi = i;  // first index in [0, i] holding k
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (keys[mid] < k) lo = mid + 1;
+                else hi = mid;
+            }
+            offsets[k] = static_cast<uint32_t>(lo);
+            counts[k] = static_cast<uint32_t>(i + 1 - lo);
+        }
+    }
+}
+
+// One workgroup per table row v: the positions of ID v are sorted[offsets[v] .. + counts[v]),
+// summed in that order (offsets[v] is read only where counts[v] > 0: the one-workgroup grouping
+// leaves the offsets of absent IDs unwritten).
 template <typename T>
 __global__ void __launch_bounds__(kEmbThreads)
 embedding_dense_grad_kernel(const T* __restrict__ grad, const uint32_t* __restrict__ sorted_pos,
@@ -311,7 +371,7 @@ embedding_dense_grad_kernel(const T* __restrict__ grad, const uint32_t* __restri
     constexpr int P = Chunk<T>::kPer;
     const int64_t v = blockIdx.x;
     const uint32_t cnt = (static_cast<uint64_t>(v) == padding) ? 0u : counts[v];
-    const uint32_t off = offsets[v];
+    const uint32_t off = cnt ? offsets[v] : 0u;
     const float divisor = static_cast<float>(counts[v]);
     T* row = dw + v * width;
     if (vec) {
@@ -452,10 +512,52 @@ hipError_t embedding(const void* table, int id_bytes, const void* ids, void* out
     return hipGetLastError();
 }
 
+namespace {
+
+bool small_grouping(int64_t tokens, int64_t vocab) {
+    return tokens > 0 && tokens <= kSmallSort && vocab < kSmallVocab;
+}
+
+int scan_launches(int64_t n) {
+    if (n <= 0) return 0;
+    const int64_t tiles = (n + kScanTile - 1) / kScanTile;
+    return tiles == 1 ? 1 : 2 + scan_launches(tiles);
+}
+
+}  // namespace
+
+int embedding_backward_launches(int64_t tokens, int64_t vocab, int64_t width) {
+    const int dense = vocab > 0 && width > 0 ? 1 : 0;
+    if (small_grouping(tokens, vocab)) return 1 + dense;
+    int n = 1 + scan_launches(vocab + 1) + dense;  // clear, count scan, dense rows
+    if (tokens > 0) {
+        n += 1;  // keys
+        if (tokens <= kSmallSort) n += 1;
+        else n += (key_bits(vocab) + 7) / 8 * (2 + scan_launches(kDigits * sort_tiles(tokens)));
+    }
+    return n;
+}
+
 hipError_t embedding_backward(int dtype, const void* grad, int id_bytes, const void* ids, void* dw, int64_t tokens,
                               int64_t vocab, int64_t width, uint64_t padding, int scale, void* workspace,
                               hipStream_t s) {
     EmbWs w = carve(workspace, tokens, vocab);
+    if (small_grouping(tokens, vocab)) {
+        if (id_bytes == 8)
+            hipLaunchKernelGGL(small_grouping_kernel<int64_t>, dim3(1), dim3(kSmallSortThreads), 0, s,
+                               static_cast<const int64_t*>(ids), static_cast<int>(tokens), vocab, key_bits(vocab),
+                               w.counts, w.offsets, w.pos_alt, w.flag);
+        else
+            hipLaunchKernelGGL(small_grouping_kernel<int32_t>, dim3(1), dim3(kSmallSortThreads), 0, s,
+                               static_cast<const int32_t*>(ids), static_cast<int>(tokens), vocab, key_bits(vocab),
+                               w.counts, w.offsets, w.pos_alt, w.flag);
+        if (vocab > 0 && width > 0) {
+            if (dtype == 1) launch_dense_grad<_Float16>(grad, w, w.pos_alt, dw, vocab, width, padding, scale, s);
+            else if (dtype == 27) launch_dense_grad<uint16_t>(grad, w, w.pos_alt, dw, vocab, width, padding, scale, s);
+            else launch_dense_grad<float>(grad, w, w.pos_alt, dw, vocab, width, padding, scale, s);
+        }
+        return hipGetLastError();
+    }
     const unsigned cgrid = flat_blocks(vocab + 1, kEmbThreads);
     hipLaunchKernelGGL(clear_counts_kernel, dim3(cgrid), dim3(kEmbThreads), 0, s, w.counts, vocab + 1, w.flag);
     if (tokens > 0) {

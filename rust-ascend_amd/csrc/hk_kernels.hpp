@@ -165,6 +165,8 @@ hipError_t embedding(const void* table, int id_bytes, const void* ids, void* out
 hipError_t embedding_backward(int dtype, const void* grad, int id_bytes, const void* ids, void* dw, int64_t tokens,
                               int64_t vocab, int64_t width, uint64_t padding, int scale, void* workspace,
                               hipStream_t s);
+// Kernel launches one embedding_backward call enqueues (for the context's launch counter).
+int embedding_backward_launches(int64_t tokens, int64_t vocab, int64_t width);
 
 // Row softmax / log-softmax over the last axis of contiguous F32 [rows, width] (hk_softmax.hip).
 hipError_t softmax_forward(const float* x, float* y, int64_t rows, int64_t width, int logarithmic, hipStream_t s);
