@@ -912,7 +912,7 @@ def main():
             f_ms, b_ms, ff, bf = bench_attention()
             sec.append({"workload": "C4 attention fwd", "value": round(ff / f_ms / 1e9, 1), "unit": "TFLOP/s",
                         "ms": round(f_ms, 4),
-                        "roofline": short_roofline(roofline("mfma", ff, f_ms, "attn_fwd_pp", "attn_fwd"))})
+                        "roofline": short_roofline(roofline("mfma", ff, f_ms, "attn_fwd_pp16", "attn_fwd"))})
             sec.append({"workload": "C4 attention bwd", "value": round(bf / b_ms / 1e9, 1), "unit": "TFLOP/s",
                         "ms": round(b_ms, 4),
                         "roofline": short_roofline(roofline("mfma", bf, b_ms, "attn_bwd_dkdv+attn_bwd_dq_ds",

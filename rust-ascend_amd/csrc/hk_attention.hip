@@ -18,9 +18,9 @@
 //   * one workgroup = 4 wavefronts = 128 query rows of one (batch, head); K/V tiles of 64 keys
 //     are double-buffered in LDS (rows XOR-swizzled in 16-byte chunks) and prefetched from HBM
 //     into registers one tile ahead;
-//   * each wave computes S^T = K Q^T (v_mfma_f32_32x32x16_bf16, Q held in registers as the B
-//     operand), so every lane owns ONE query column: the row max/sum need a single exchange
-//     with lane^32 instead of a 32-lane reduction;
+//   * each wave computes S^T = K Q^T (Q held in registers as the B operand; v_mfma_f32_32x32x16_bf16
+//     for D <= 32, 16x16x32 in the ping-pong kernel for D = 64 / 128), so every lane owns query
+//     columns: the row max/sum need one or two lane exchanges instead of a 32-lane reduction;
 //   * the FP32 accumulators of S^T, converted to BF16, are directly the B operand of
 //     O^T = V^T P^T (the key order inside each MFMA k-group is matched on the V side);
 //     V^T comes straight from the row-major V tile through ds_read_b64_tr_b16 (the gfx950
@@ -410,7 +410,7 @@ attn_fwd(FwdArgs a) {
 
 // Ping-pong forward kernel for D = 64 / 128: 8 wavefronts = 256 query rows per workgroup,
 // two waves per SIMD (waves w and w+4). Each wave alternates an MFMA phase (P.V of the previous
-// tile and S = K Q^T of the current one, 32 MFMAs) with a softmax phase (VALU and v_exp_f32),
+// tile and S = K Q^T of the current one, 64 16x16x32 MFMAs at D = 128) with a softmax phase (VALU and v_exp_f32),
 // and the second group of four waves runs one phase behind the first: at every barrier the two
 // waves on a SIMD swap roles, so the matrix core is fed by one while the other computes the
 // exponentials, instead of both waiting on their own softmax. The MFMA phase raises the wave's
@@ -428,82 +428,12 @@ attn_fwd(FwdArgs a) {
 // those spill). The pads are chosen for gfx950's 64 banks (256-byte bank line):
 //   K rows of D+8 elements: the 16 rows of an operand read (16 lanes, 16 bytes each) start
 //     16 bytes apart modulo 256 -> 16 distinct bank groups;
-//   V rows of D+32 elements: the 4 rows x 64 bytes of a transposing read (32 lanes, 8 bytes
-//     each) start 64 bytes apart modulo 256 -> 4 distinct bank groups.
+//   V rows of D+16 elements (kV16Stride below).
 template <int D> constexpr int kKStride = D + 8;
-template <int D> constexpr int kVStride = D + 32;
 
 template <int STRIDE>
 __device__ __forceinline__ bf16x8_t pad_read16(const uint16_t* t, int row, int chunk) {
     return *reinterpret_cast<const bf16x8_t*>(t + row * STRIDE + chunk * 8);
-}
-
-// Same operand as tile_read_tr, from a padded [64][STRIDE] tile.
-template <int STRIDE>
-__device__ __forceinline__ bf16x8_t pad_read_tr(const uint16_t* t, int lane, int kbase0, int kbase1, int ibase) {
-    const int g = (lane >> 4) & 1;
-    const int i = lane & 15;
-    const int col = ibase + 16 * g + 4 * (i & 3);
-    const int r = i >> 2;
-    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + (kbase0 + r) * STRIDE + col));
-    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + (kbase1 + r) * STRIDE + col));
-    typedef short v8i16_t __attribute__((ext_vector_type(8)));
-    v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8_t, v);
-}
-
-// MFMA phase of the ping-pong kernel: up to 16 MFMAs of O^T += V^T P^T (tile j-1) followed by
-// 16 (D=128) or 8 (D=64) MFMAs of S^T = K Q^T (tile j), as one software pipeline: the LDS
-// operand of MFMA i + kAhead is read while MFMA i runs, through a ring of kAhead + 1 registers.
-// The fences keep the compiler from regrouping the reads in front of their MFMAs (which
-// serializes every MFMA behind a full LDS round trip); the empty asm makes the wait for each
-// operand land right before its MFMA.
-constexpr int kAhead = 6;
-
-// NL global->LDS loads (load(d), d < NL) are spread one per few MFMAs, so they trickle into the
-// memory pipeline while the matrix core is busy instead of stalling the wave as a burst.
-template <int D, bool PV, bool QK, int NL = 0, class Load = void (*)(int)>
-__device__ __forceinline__ void mfma_phase(const uint16_t* Vt, const uint16_t* Kt, const bf16x8_t (&pb)[4],
-                                           const bf16x8_t (&qf)[D / 16], int lane, int lq, int lg,
-                                           f32x16_t (&o)[D / 32], f32x16_t (&s)[2], Load&& load = nullptr) {
-    constexpr int DT = D / 32, KS = D / 16;
-    constexpr int NPV = PV ? 4 * DT : 0;  // P.V MFMAs: ks-major, dt-minor
-    constexpr int NQK = QK ? 2 * KS : 0;  // score MFMAs: ks-major, tt-minor
-    constexpr int N = NPV + NQK;
-    constexpr int R = kAhead + 1;
-    auto fetch = [&](int i) -> bf16x8_t {
-        if (i < NPV) {
-            const int ks = i / DT, dt = i % DT;
-            const int kb0 = 16 * ks + 4 * lg;
-            return pad_read_tr<kVStride<D>>(Vt, lane, kb0, kb0 + 8, 32 * dt);
-        }
-        const int q = i - NPV, ks = q >> 1, tt = q & 1;
-        return pad_read16<kKStride<D>>(Kt, 32 * tt + lq, 2 * ks + lg);
-    };
-    bf16x8_t ring[R];
-#pragma unroll
-    for (int i = 0; i < kAhead && i < N; ++i) ring[i % R] = fetch(i);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        if (i + kAhead < N) ring[(i + kAhead) % R] = fetch(i + kAhead);
-        __builtin_amdgcn_sched_barrier(0);
-        bf16x8_t x = ring[i % R];
-        asm volatile("" : "+v"(x));
-        if (i < NPV) {
-            const int ks = i / DT, dt = i % DT;
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, pb[ks], o[dt], 0, 0, 0);
-        } else {
-            const int q = i - NPV, ks = q >> 1, tt = q & 1;
-            const f32x16_t zero = {};
-            s[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, qf[ks], ks == 0 ? zero : s[tt], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (NL > 0) {
-#pragma unroll
-            for (int d = i * NL / N; d < (i + 1) * NL / N; ++d) load(d);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
 }
 
 constexpr int kPPWaves = 8;
@@ -550,22 +480,185 @@ struct PadTileDma {
     }
 };
 
+// The ping-pong kernel's tiles are v_mfma_f32_16x16x32_bf16 ones. Each wave's 32 queries are two
+// 16-query blocks qb and a 64-key tile four 16-key blocks kb:
+//   S^T = K Q^T: s[qb][kb] (lane l: query 16 qb + l % 16, keys 16 kb + 4 (l / 16) + 0..3), the A
+//     operand K rows 16 kb + l % 16 at head dims 32 ks + 8 (l / 16) from LDS, the B operand Q from
+//     registers; every K operand read feeds the MFMAs of both query blocks;
+//   O^T += V^T P^T: o[db][qb] (lane l: query 16 qb + l % 16, head dims 16 db + 4 (l / 16) + 0..3)
+//     over two 32-key steps ps. The lane's P values of step ps are keys 32 ps + 4 g + 0..3 and
+//     32 ps + 16 + 4 g + 0..3 (g = l / 16), used as its 8 k values in that order; the V^T operand
+//     follows the same key order: two transposing reads of 4 key rows each (v16_read_tr). Every V
+//     operand read also feeds both query blocks.
+// Against the same kernel with 32x32x16 tiles (one 32-query block per wave, the lane's query
+// l % 32) this moves a quarter of the accumulator registers per MFMA and half the register bytes
+// per multiply-accumulate; measured on one box at C4 0.636-0.640 ms against 0.649-0.650 ms. A
+// query's row max and sum span the four lanes l % 16 + 16 g (two lane swaps).
+
+// V tile rows of D + 16 elements (288 bytes for D = 128): the 8 rows x 32 bytes a transposing
+// read touches per 32 lanes (rows 32 ps + 4 g + r, g < 2, r < 4, at 16 db .. 16 db + 15) start
+// 32 bytes apart modulo 256, so they fall on 8 distinct 32-byte bank groups.
+template <int D> constexpr int kV16Stride = D + 16;
+
+// 16x16x32 A operand V^T of head dims 16 db .. 16 db + 15 and key step ps (see above).
+template <int STRIDE>
+__device__ __forceinline__ bf16x8_t v16_read_tr(const uint16_t* t, int lane, int ps, int db) {
+    const int i = lane & 15, g = lane >> 4;
+    const int col = 16 * db + 4 * (i & 3);
+    const int r = i >> 2;
+    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + (32 * ps + 4 * g + r) * STRIDE + col));
+    const v4i16_t hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(t + (32 * ps + 16 + 4 * g + r) * STRIDE + col));
+    typedef short v8i16_t __attribute__((ext_vector_type(8)));
+    v8i16_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// Max / sum over the four lanes l % 16 + 16 g that share a query (two swap steps; partners compute
+// the same value in the same order).
+__device__ __forceinline__ float quad_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return pair32_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return pair32_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+}
+
+// Online-softmax update of one tile for the 16x16 layout (tile_softmax's rules: base 2, the
+// running max lagging by at most kStaleMax, masked keys -inf), leaving P as the B operands
+// pb[ps][qb] of the two 32-key steps.
+template <int DB>
+__device__ __forceinline__ void tile_softmax16(f32x4_t (&s)[2][4], int lane, float c, bool mask, int64_t kv0,
+                                               const int64_t (&key_limit)[2], float (&m_run)[2], float (&l_run)[2],
+                                               f32x4_t (&o)[DB][2], bf16x8_t (&pb)[2][2]) {
+    const int g = lane >> 4;
+    if (mask) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            // key kv0 + 16 kb + 4 g + e is visible iff 16 kb + e <= rel
+            int64_t rel64 = key_limit[qb] - kv0 - 4 * g;
+            rel64 = rel64 < -1 ? -1 : (rel64 > kBlockN ? kBlockN : rel64);
+            int rel = static_cast<int>(rel64);
+            asm volatile("" : "+v"(rel));
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[qb][kb][e] = 16 * kb + e <= rel ? s[qb][kb][e] : -INFINITY;
+        }
+    }
+    float mt[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        float x = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x = fmaxf(x, s[qb][kb][e]);
+        mt[qb] = quad_max(x) * c;
+    }
+    if (__any(mt[0] > m_run[0] + kStaleMax || mt[1] > m_run[1] + kStaleMax)) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const float m_new = fmaxf(m_run[qb], mt[qb]);
+            const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run[qb] - m_new);
+            m_run[qb] = m_new;
+            l_run[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[db][qb][e] *= alpha;
+        }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const float neg_m = m_run[qb] == -INFINITY ? 0.0f : -m_run[qb];
+        float ls = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float p = fast_exp2(__builtin_fmaf(s[qb][kb][e], c, neg_m));
+                s[qb][kb][e] = p;
+                ls += p;
+            }
+        l_run[qb] += ls;
+    }
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const f32x4_t& a = s[qb][2 * ps];
+            const f32x4_t& b = s[qb][2 * ps + 1];
+            const u32x4_t w = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                               pack_bf16x2(b[2], b[3])};
+            pb[ps][qb] = __builtin_bit_cast(bf16x8_t, w);
+        }
+}
+
+// MFMA phase of the ping-pong kernel: O^T += V^T P^T of tile j-1 (2 DB operand reads, 4 DB MFMAs),
+// then S^T = K Q^T of tile j (4 KS reads, 8 KS MFMAs), as one software pipeline: the LDS operand of
+// read i + kAhead is fetched while the MFMAs of read i run, through a ring of kAhead + 1 registers.
+// The fences keep the compiler from regrouping the reads in front of their MFMAs (which serializes
+// every MFMA behind a full LDS round trip); the empty asm makes the wait for each operand land
+// right before its MFMAs.
+constexpr int kAhead = 6;
+
+template <int D>
+__device__ __forceinline__ void mfma_phase16(const uint16_t* Vt, const uint16_t* Kt, const bf16x8_t (&pb)[2][2],
+                                             const bf16x8_t (&qf)[2][D / 32], int lane, f32x4_t (&o)[D / 16][2],
+                                             f32x4_t (&s)[2][4]) {
+    constexpr int DB = D / 16, KS = D / 32;
+    constexpr int NPV = 2 * DB;  // (ps, db), ps-major
+    constexpr int NQK = 4 * KS;  // (ks, kb), ks-major
+    constexpr int N = NPV + NQK;
+    constexpr int R = kAhead + 1;
+    const int l16 = lane & 15, g = lane >> 4;
+    auto fetch = [&](int i) -> bf16x8_t {
+        if (i < NPV) return v16_read_tr<kV16Stride<D>>(Vt, lane, i / DB, i % DB);
+        const int q = i - NPV, ks = q >> 2, kb = q & 3;
+        return pad_read16<kKStride<D>>(Kt, 16 * kb + l16, 4 * ks + g);
+    };
+    bf16x8_t ring[R];
+#pragma unroll
+    for (int i = 0; i < kAhead && i < N; ++i) ring[i % R] = fetch(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if (i + kAhead < N) ring[(i + kAhead) % R] = fetch(i + kAhead);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8_t x = ring[i % R];
+        asm volatile("" : "+v"(x));
+        if (i < NPV) {
+            const int ps = i / DB, db = i % DB;
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+                o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, pb[ps][qb], o[db][qb], 0, 0, 0);
+        } else {
+            const int q = i - NPV, ks = q >> 2, kb = q & 3;
+            const f32x4_t zero = {};
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+                s[qb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, qf[qb][ks], ks == 0 ? zero : s[qb][kb], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 template <int D>
 __global__ void __launch_bounds__(kPPThreads, 1)
-attn_fwd_pp(FwdArgs a) {
+attn_fwd_pp16(FwdArgs a) {
     static_assert(D == 64 || D == 128, "ping-pong kernel is for D = 64 or 128");
-    constexpr int KS = D / 16;
-    constexpr int DT = D / 32;
+    constexpr int KS = D / 32;  // 32-wide head-dim steps of S^T
+    constexpr int DB = D / 16;  // 16-wide head-dim blocks of O^T
     __shared__ __attribute__((aligned(16))) uint16_t kbuf[2][kBlockN * kKStride<D>];
-    __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kBlockN * kVStride<D>];
+    __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kBlockN * kV16Stride<D>];
     using KDma = PadTileDma<D, kKStride<D>>;
-    using VDma = PadTileDma<D, kVStride<D>>;
+    using VDma = PadTileDma<D, kV16Stride<D>>;
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int lq = lane & 31, lg = lane >> 5;
+    const int l16 = lane & 15, g = lane >> 4;
     const int group = wave >> 2;  // 0: leads, 1: one half-step behind
-    // logical order: KV head group, query block heaviest first, query head in the group
     const int logical = xcd_logical();
     const int group_heads = static_cast<int>(a.heads / a.kv_heads);
     const int per_group = a.mblocks * group_heads;
@@ -579,9 +672,8 @@ attn_fwd_pp(FwdArgs a) {
     const uint16_t* V = a.v + ((b * a.kv_heads + kvh) * a.n) * D;
     const int64_t q0 = static_cast<int64_t>(mb) * kPPBlockM;
     const int64_t q0w = q0 + wave * 32;
-    const int64_t my_q = q0w + lq;
+    const int64_t my_q[2] = {q0w + l16, q0w + 16 + l16};
 
-    // keys this workgroup needs: [0, kv_end); tiles [0, nfull) are visible to all its rows
     int64_t kv_end = a.n, full_end = a.n;
     if (a.causal) {
         const int64_t last = q0 + kPPBlockM - 1 + a.diag;
@@ -592,65 +684,61 @@ attn_fwd_pp(FwdArgs a) {
     const int ntiles = kv_end > 0 ? static_cast<int>((kv_end + kBlockN - 1) / kBlockN) : 0;
     int nfull = full_end > 0 ? static_cast<int>(full_end / kBlockN) : 0;
     nfull = nfull < ntiles ? nfull : ntiles;
-    int64_t key_limit = a.n - 1;
-    if (a.causal) key_limit = my_q + a.diag < key_limit ? my_q + a.diag : key_limit;
-    // this wave's 32 rows see no key of tile j (it still takes part in every barrier)
+    int64_t key_limit[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        key_limit[qb] = a.n - 1;
+        if (a.causal) key_limit[qb] = my_q[qb] + a.diag < key_limit[qb] ? my_q[qb] + a.diag : key_limit[qb];
+    }
     auto skip = [&](int j) { return a.causal && static_cast<int64_t>(j) * kBlockN > q0w + 31 + a.diag; };
 
-    bf16x8_t qf[KS];
-    {
-        const int64_t qr = my_q < a.m ? my_q : a.m - 1;
+    bf16x8_t qf[2][KS];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const bf16x8_t*>(Q + qr * D + 16 * s + 8 * lg);
+    for (int qb = 0; qb < 2; ++qb) {
+        const int64_t qr = my_q[qb] < a.m ? my_q[qb] : a.m - 1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qf[qb][ks] = *reinterpret_cast<const bf16x8_t*>(Q + qr * D + 32 * ks + 8 * g);
     }
     float c = a.scale_log2;
     if (c < 0.0f) {
         c = -c;
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-            qf[s] = __builtin_bit_cast(bf16x8_t, __builtin_bit_cast(u32x4_t, qf[s]) ^ 0x80008000u);
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                qf[qb][ks] = __builtin_bit_cast(bf16x8_t, __builtin_bit_cast(u32x4_t, qf[qb][ks]) ^ 0x80008000u);
     }
-    settle(qf);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) settle(qf[qb]);
 
-    f32x16_t o[DT];
+    f32x4_t o[DB][2];
 #pragma unroll
-    for (int i = 0; i < DT; ++i)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-    f32x16_t s[2];
-    bf16x8_t pb[4];
+        for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.0f, 0.0f};
+    f32x4_t s[2][4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) s[tt][v] = 0.0f;
+        for (int kb = 0; kb < 4; ++kb) s[qb][kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8_t pb[2][2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) pb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
+    for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) pb[ps][qb] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
 
-    // byte offsets into one K/V head stay below 2^31 (checked by the launcher)
     const i32x4_t rk = buffer_resource(K, static_cast<int>(a.n * D * 2));
     const i32x4_t rv = buffer_resource(V, static_cast<int>(a.n * D * 2));
     const int n32 = static_cast<int>(a.n);
     if (ntiles > 0) KDma::issue(rk, kbuf[0], 0, n32, wave, lane);
-    // the first MFMA phase multiplies a zero P with V buffer 1: it must hold finite values
-    for (int i = t; i < kBlockN * kVStride<D> / 8; i += kPPThreads)
+    for (int i = t; i < kBlockN * kV16Stride<D> / 8; i += kPPThreads)
         *reinterpret_cast<u32x4_t*>(vbuf[1] + 8 * i) = u32x4_t{0, 0, 0, 0};
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    // Half-step hs (0 .. 2*ntiles+1) ends with a barrier; K_{hs/2} and V_{hs/2-1} are in LDS
-    // during it. The leading group runs MFMA phase t at half-step 2t and softmax t at 2t+1; the
-    // lagging group runs them one half-step later. Each group's schedule is straight-line code
-    // (two copies of the loop), so the values that live across phases stay in their registers.
-    // The loads of K_{t+1} and V_t (into the buffers read two half-steps earlier) go out in
-    // half-step 2t from the lagging group, which is then in its softmax phase: the wave that
-    // feeds the matrix core issues nothing but MFMAs and LDS reads (vector memory instructions
-    // in its stream would hold back the MFMAs behind them). The lagging group's four waves
-    // share the tile's load instructions and wait for them before the barrier that ends
-    // half-step 2t+1.
     constexpr int kKInstr = KDma::kInstr, kVInstr = VDma::kInstr;
     constexpr int kLoadsPerWave = (kKInstr + kVInstr + 3) / 4;
-    // lane offsets of this wave's load instructions, for whole tiles
     int loff[kLoadsPerWave];
 #pragma unroll
     for (int d = 0; d < kLoadsPerWave; ++d) {
@@ -661,24 +749,20 @@ attn_fwd_pp(FwdArgs a) {
     auto landed = [&]() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
     auto softmax = [&](int j) {
         if (!skip(j)) {
-            tile_softmax<DT>(s, lane, c, j >= nfull, static_cast<int64_t>(j) * kBlockN, key_limit, m_run, l_run, o,
-                             pb);
+            tile_softmax16<DB>(s, lane, c, j >= nfull, static_cast<int64_t>(j) * kBlockN, key_limit, m_run, l_run, o,
+                               pb);
         } else {
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) pb[ks] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
+            for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) pb[ps][qb] = __builtin_bit_cast(bf16x8_t, u32x4_t{0, 0, 0, 0});
         }
     };
-    // MFMA phase of tile j: P_{j-1} V_{j-1}, then S_j (mfma_step below drops the halves that feed
-    // nothing).
-    // Loads of half-step 2j: K_{j+1} and V_j (tiles that reach past n take the clamping path).
     auto tile_loads = [&](int j) {
         const bool k_next = j + 1 < ntiles, v_cur = j < ntiles;
         uint16_t* kdst = kbuf[(j + 1) & 1];
         uint16_t* vdst = vbuf[j & 1];
         const bool k_whole = (j + 2) * kBlockN <= n32, v_whole = (j + 1) * kBlockN <= n32;
-        // Both tiles due and whole (every step but the last ones): one uniform branch, then the
-        // loads alone. Deciding per load, as below, leaves a scalar branch around every load in the
-        // softmax phase that issues them (C4 forward ~3% slower).
         if (k_next && k_whole && v_cur && v_whole) {
 #pragma unroll
             for (int d = 0; d < kLoadsPerWave; ++d) {
@@ -692,7 +776,7 @@ attn_fwd_pp(FwdArgs a) {
         }
 #pragma unroll
         for (int d = 0; d < kLoadsPerWave; ++d) {
-            const int q = (wave & 3) + 4 * d;  // this wave's share of the tile's instructions
+            const int q = (wave & 3) + 4 * d;
             if (q < kKInstr) {
                 if (k_next && k_whole)
                     load_lds16(rk, lds_address(kdst + 8 * 64 * q), loff[d], (j + 1) * kBlockN * D * 2);
@@ -707,37 +791,29 @@ attn_fwd_pp(FwdArgs a) {
             }
         }
     };
-    // MFMA phase j, left out when neither half feeds anything: P_{j-1} V_{j-1} is needed only when
-    // tile j-1 exists and this wave did not skip it (else P is zero), S_j only when tile j exists and
-    // this wave does not skip it (else its scores are not used). Causal waves skip the workgroup's
-    // tiles past their own diagonal (up to 3.5 of them for the first wave of a 256-query block);
-    // the results are unchanged. skip() is uniform per wave, so the branch is a scalar one. (Phase
-    // bodies with only one of the halves, as separate copies, pushed the kernel into spills.)
     auto mfma_step = [&](int j) {
         const bool pv = j >= 1 && !skip(j - 1), qk = j < ntiles && !skip(j);
-        if (pv || qk) mfma_phase<D, true, true>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, lq, lg, o, s);
+        if (pv || qk) mfma_phase16<D>(vbuf[(j - 1) & 1], kbuf[j & 1], pb, qf, lane, o, s);
     };
-    // The barriers between half-steps wait for LDS accesses only (lds_barrier), so the tile
-    // loads stay in flight from their half-step 2t to the end of 2t+1.
     if (group == 0) {
         for (int j = 0; j <= ntiles; ++j) {
-            __builtin_amdgcn_s_setprio(1);  // half-step 2j
+            __builtin_amdgcn_s_setprio(1);
             mfma_step(j);
             __builtin_amdgcn_s_setprio(0);
             lds_barrier();
-            if (j < ntiles) softmax(j);  // half-step 2j+1
+            if (j < ntiles) softmax(j);
             lds_barrier();
         }
     } else {
         tile_loads(0);
-        lds_barrier();  // half-step 0
+        lds_barrier();
         for (int j = 0; j <= ntiles; ++j) {
-            __builtin_amdgcn_s_setprio(1);  // half-step 2j+1
+            __builtin_amdgcn_s_setprio(1);
             mfma_step(j);
             __builtin_amdgcn_s_setprio(0);
             landed();
             lds_barrier();
-            if (j < ntiles) {  // half-step 2j+2
+            if (j < ntiles) {
                 tile_loads(j + 1);
                 softmax(j);
                 lds_barrier();
@@ -746,20 +822,19 @@ attn_fwd_pp(FwdArgs a) {
         landed();
     }
 
-    const float l_tot = pair32_sum(l_run);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (my_q < a.m) {
-        const int64_t obase = (bh * a.m + my_q) * D;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+    for (int qb = 0; qb < 2; ++qb) {
+        const float l_tot = quad_sum(l_run[qb]);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        if (my_q[qb] < a.m) {
+            const int64_t obase = (bh * a.m + my_q[qb]) * D;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = 32 * dt + 8 * g + 4 * lg;
-                store_o4(a, obase + d, o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                         o[dt][4 * g + 3] * inv);
-            }
-        if (lg == 0)
-            a.lse[bh * a.m + my_q] = l_tot > 0.0f ? (m_run + log2f(l_tot)) * kLn2 : -INFINITY;
+            for (int db = 0; db < DB; ++db)
+                store_o4(a, obase + 16 * db + 4 * g, o[db][qb][0] * inv, o[db][qb][1] * inv, o[db][qb][2] * inv,
+                         o[db][qb][3] * inv);
+            if (g == 0)
+                a.lse[bh * a.m + my_q[qb]] = l_tot > 0.0f ? (m_run[qb] + log2f(l_tot)) * kLn2 : -INFINITY;
+        }
     }
 }
 
@@ -796,7 +871,7 @@ hipError_t launch_fwd(const AttnShape& sh, const void* q, const void* k, const v
     if constexpr (D >= 64) {
         a.mblocks = static_cast<int>((sh.m + kPPBlockM - 1) / kPPBlockM);
         const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
-        hipLaunchKernelGGL((attn_fwd_pp<D>), grid, dim3(kPPThreads), 0, s, a);
+        hipLaunchKernelGGL((attn_fwd_pp16<D>), grid, dim3(kPPThreads), 0, s, a);
     } else {
         a.mblocks = static_cast<int>((sh.m + kBlockM - 1) / kBlockM);
         const dim3 grid(static_cast<unsigned>(sh.batch * sh.heads * a.mblocks));
@@ -992,7 +1067,7 @@ __device__ __forceinline__ void store_grad_row(const BwdArgs& a, int64_t b, int6
 // MFMA i runs, through a ring of kAhead + 1 registers, so no MFMA waits on an LDS round trip
 // (left to itself, with the registers of these kernels in use, the compiler reads each
 // operand into one register right before its MFMA). The fences and the empty asm are those of
-// mfma_phase.
+// mfma_phase16.
 template <int N, class Fetch, class Mma>
 __device__ __forceinline__ void mfma_ring(Fetch&& fetch, Mma&& mma) {
     constexpr int R = kAhead + 1;
