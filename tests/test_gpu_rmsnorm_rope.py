@@ -247,6 +247,33 @@ def test_rotary_c4_shape_bf16(layout):
         close(host(back), want_back, 1e-6, 1e-6, "rope backward f32")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("shape,p", [((3, 5, 100, 128), 128), ((2, 3, 64), 48), ((1, 7, 9, 80), 64), ((4, 1, 33, 16), 16)])
+def test_rotary_prefix_broadcast_tables_match_per_row_tables(dtype, layout, shape, p):
+    """Tables [1, ..., 1, S, P/2] broadcast over the leading axes give exactly the bits of the same
+    tables expanded to the input's leading shape (every row its own table row), forward and
+    backward, tail columns included; and agree with the oracle."""
+    S, half = shape[-2], p // 2
+    g = torch.Generator(device=DEV)
+    g.manual_seed(sum(shape) + p)
+    x = torch.randn(shape, generator=g, device=DEV).to(dtype)
+    ang = torch.rand((S, half), generator=g, device=DEV) * 6.0
+    lead = (1,) * (len(shape) - 2)
+    c, s = torch.cos(ang).reshape(lead + (S, half)), torch.sin(ang).reshape(lead + (S, half))
+    full = shape[:-1] + (half,)
+    c_full, s_full = c.expand(full).contiguous(), s.expand(full).contiguous()
+    print(f"rope broadcast tables {shape} p {p} layout {layout} {dtype}", flush=True)
+    for fn in (HipRuntime.rotary_prefix, HipRuntime.rotary_prefix_backward):
+        got = fn(x, c, s, p, RotaryLayout(layout))
+        want = fn(x, c_full, s_full, p, RotaryLayout(layout))
+        assert torch.equal(got.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                           want.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+    want64 = oracle.rotary_prefix(host(x).astype(np.float64), host(c), host(s), p, layout)
+    close(host(HipRuntime.rotary_prefix(x, c, s, p, RotaryLayout(layout))), want64,
+          1e-2 if dtype == torch.bfloat16 else 1e-5, 1e-2 if dtype == torch.bfloat16 else 1e-5, "rope broadcast")
+
+
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("width", [2, 6, 64, 96, 128])
 def test_rotary_random_widths_vs_oracle(layout, width):
