@@ -160,12 +160,15 @@ _lib = None
 _lock = threading.Lock()
 
 
-def load(path: str = LIB_PATH):
-    """Load libhk.so and bind every entry point; raises HkError(LOAD_ERROR) if absent."""
+def load(path: str = None):
+    """Load libhk.so (the module's LIB_PATH as it stands at the first call, or `path`) and bind
+    every entry point; raises HkError(LOAD_ERROR) if absent."""
     global _lib
     with _lock:
         if _lib is not None:
             return _lib
+        if path is None:
+            path = LIB_PATH
         if not os.path.exists(path):
             raise HkError(LOAD_ERROR, f"{path} is missing: build it with __graft_entry__.build() "
                                       "(no CPU fallback exists)")
