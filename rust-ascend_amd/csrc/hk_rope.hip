@@ -48,23 +48,17 @@ __device__ __forceinline__ int64_t table_row(int64_t row, const RopeMap& map) {
     return t;
 }
 
+// One thread's V pairs p0 .. p0+V-1 of one row: xr, yr at the row's first element, t the offset
+// of the pairs' first angle in the tables.
 template <typename T, int V, int LAYOUT, bool BWD>
-__global__ void __launch_bounds__(256)
-rope_pairs(const T* __restrict__ x, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-           T* __restrict__ y, int64_t rows, int64_t width, int64_t half, RopeMap map) {
-    const int64_t per_row = half / V;
-    for (int64_t idx = flat_begin(256); idx < rows * per_row; idx += flat_stride(256)) {
-        const int64_t row = idx / per_row;
-        const int64_t p0 = (idx - row * per_row) * V;
-        const int64_t t = table_row(row, map) * half + p0;
+__device__ __forceinline__ void rope_chunk(const T* __restrict__ xr, T* __restrict__ yr, const float* __restrict__ cos_t,
+                                           const float* __restrict__ sin_t, int64_t t, int64_t p0, int64_t half) {
         float c[V], s[V], a[V], b[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) {
             c[i] = cos_t[t + i];
             s[i] = sin_t[t + i];
         }
-        const T* xr = x + row * width;
-        T* yr = y + row * width;
         if constexpr (LAYOUT == 1) {
             load_v<T, V>(xr + p0, a);
             load_v<T, V>(xr + half + p0, b);
@@ -115,7 +109,59 @@ rope_pairs(const T* __restrict__ x, const float* __restrict__ cos_t, const float
                 }
             }
         }
+}
+
+// Any table map: work item idx is pair chunk idx % (half / V) of row idx / (half / V).
+template <typename T, int V, int LAYOUT, bool BWD>
+__global__ void __launch_bounds__(256)
+rope_pairs(const T* __restrict__ x, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+           T* __restrict__ y, int64_t rows, int64_t width, int64_t half, RopeMap map) {
+    const int64_t per_row = half / V;
+    for (int64_t idx = flat_begin(256); idx < rows * per_row; idx += flat_stride(256)) {
+        const int64_t row = idx / per_row;
+        const int64_t p0 = (idx - row * per_row) * V;
+        rope_chunk<T, V, LAYOUT, BWD>(x + row * width, y + row * width, cos_t, sin_t, table_row(row, map) * half + p0,
+                                      p0, half);
     }
+}
+
+// The common table maps without a division per work item: the table row is the input row
+// (period 0) or the input row modulo `period` (tables broadcast over the leading axes outside a
+// contiguous innermost run, e.g. [1, 1, S, P/2] for [B, H, S, P] inputs). 2^tpr_shift threads per
+// row (half / 8, a power of two dividing 256), each the same 8 pairs of every row it visits; the
+// table row advances with the row by a step taken modulo the period once. Same arithmetic per
+// pair as rope_pairs, so the results are bit-identical.
+template <typename T, int LAYOUT, bool BWD>
+__global__ void __launch_bounds__(256)
+rope_rows(const T* __restrict__ x, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+          T* __restrict__ y, int rows, int width, int half, int tpr_shift, int period) {
+    const int rb = 256 >> tpr_shift;  // rows per workgroup pass
+    const int p0 = (static_cast<int>(threadIdx.x) & ((1 << tpr_shift) - 1)) * 8;
+    const int step = static_cast<int>(gridDim.x) * rb;
+    int row = static_cast<int>(blockIdx.x) * rb + (static_cast<int>(threadIdx.x) >> tpr_shift);
+    int t = period ? row % period : row;
+    const int tstep = period ? step % period : step;
+    for (; row < rows; row += step) {
+        const int64_t off = static_cast<int64_t>(row) * width;
+        rope_chunk<T, 8, LAYOUT, BWD>(x + off, y + off, cos_t, sin_t, static_cast<int64_t>(t) * half + p0, p0, half);
+        t += tstep;
+        if (period && t >= period) t -= period;
+    }
+}
+
+// 0: the table row is the input row; P > 0: the input row modulo P; -1: a general map.
+int64_t table_period(const RopeMap& map) {
+    if (map.same_row) return 0;
+    int64_t acc = 1;
+    int a = map.nlead - 1;
+    for (; a >= 0; --a) {  // the innermost axes whose table strides are their row-major strides
+        if (map.shape[a] == 1) continue;
+        if (map.tstride[a] != acc) break;
+        acc *= map.shape[a];
+    }
+    for (; a >= 0; --a)  // every other axis broadcast
+        if (map.shape[a] != 1 && map.tstride[a] != 0) return -1;
+    return acc;
 }
 
 // Columns [p, width) of every row, copied as raw bits.
@@ -135,6 +181,19 @@ void launch_pairs(bool bwd, const void* x, const float* c, const float* s, void*
                   int64_t width, int64_t half, const RopeMap& map, hipStream_t st) {
     const int64_t n = rows * (half / V);
     const dim3 grid(flat_blocks(n, 256));
+    if constexpr (V == 8) {
+        const int64_t tpr = half / 8, period = table_period(map);
+        if (period >= 0 && tpr <= 256 && (tpr & (tpr - 1)) == 0 && rows * width < (int64_t{1} << 31)) {
+            const int shift = __builtin_ctzll(static_cast<unsigned long long>(tpr));
+            if (bwd)
+                hipLaunchKernelGGL((rope_rows<T, LAYOUT, true>), grid, dim3(256), 0, st, static_cast<const T*>(x), c, s,
+                                   static_cast<T*>(y), (int)rows, (int)width, (int)half, shift, (int)period);
+            else
+                hipLaunchKernelGGL((rope_rows<T, LAYOUT, false>), grid, dim3(256), 0, st, static_cast<const T*>(x), c,
+                                   s, static_cast<T*>(y), (int)rows, (int)width, (int)half, shift, (int)period);
+            return;
+        }
+    }
     if (bwd)
         hipLaunchKernelGGL((rope_pairs<T, V, LAYOUT, true>), grid, dim3(256), 0, st, static_cast<const T*>(x), c,
                            s, static_cast<T*>(y), rows, width, half, map);

@@ -274,6 +274,34 @@ def test_rotary_prefix_broadcast_tables_match_per_row_tables(dtype, layout, shap
           1e-2 if dtype == torch.bfloat16 else 1e-5, 1e-2 if dtype == torch.bfloat16 else 1e-5, "rope broadcast")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("shape,tshape", [((3, 4, 10, 64), (3, 1, 10, 32)), ((2, 6, 5, 7, 32), (1, 6, 1, 7, 16)),
+                                          ((5, 3, 128), (5, 1, 64)), ((6, 16, 256), (1, 16, 128))])
+def test_rotary_general_table_maps_match_per_row_tables(dtype, layout, shape, tshape):
+    """Tables broadcast over axes that do not leave a contiguous innermost run (here a middle or
+    inner axis: the table row is not the input row modulo a period, so the kernel walks the
+    leading axes per row) give exactly the bits of the same tables expanded per row, forward and
+    backward; the last shape is a period pattern at 16 threads per row."""
+    half = tshape[-1]
+    g = torch.Generator(device=DEV)
+    g.manual_seed(sum(shape) + half)
+    x = torch.randn(shape, generator=g, device=DEV).to(dtype)
+    c = torch.cos(torch.rand(tshape, generator=g, device=DEV) * 6.0)
+    s = torch.sin(torch.rand(tshape, generator=g, device=DEV) * 6.0)
+    full = shape[:-1] + (half,)
+    c_full, s_full = c.expand(full).contiguous(), s.expand(full).contiguous()
+    print(f"rope general table map {shape} tables {tshape} layout {layout} {dtype}", flush=True)
+    bits = torch.int16 if dtype == torch.bfloat16 else torch.int32
+    for fn in (HipRuntime.rotary_prefix, HipRuntime.rotary_prefix_backward):
+        got = fn(x, c, s, 2 * half, RotaryLayout(layout))
+        want = fn(x, c_full, s_full, 2 * half, RotaryLayout(layout))
+        assert torch.equal(got.view(bits), want.view(bits))
+    want64 = oracle.rotary_prefix(host(x).astype(np.float64), host(c_full), host(s_full), 2 * half, layout)
+    close(host(HipRuntime.rotary_prefix(x, c, s, 2 * half, RotaryLayout(layout))), want64,
+          1e-2 if dtype == torch.bfloat16 else 1e-5, 1e-2 if dtype == torch.bfloat16 else 1e-5, "rope general map")
+
+
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("width", [2, 6, 64, 96, 128])
 def test_rotary_random_widths_vs_oracle(layout, width):
