@@ -108,6 +108,53 @@ def test_padded_large_tails_vs_oracle(m, n, k, ta, tb):
     f32_close(host(w.grad), d_opb.T if tb else d_opb, "dB")
 
 
+def _bits16(t):
+    """uint16 bit patterns of a BF16 device tensor."""
+    return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _specials(shape, seed):
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal(shape).astype(np.float32)
+    flat = a.reshape(-1)
+    specials = np.array([np.inf, -np.inf, 1 + 2.0**-8, 1 + 3 * 2.0**-8, 1e-40, -1e-42, 3.4e38, 0.0], np.float32)
+    flat[rng.choice(flat.size, 64, replace=False)] = np.resize(specials, 64)
+    return a
+
+
+def _assert_padded_bits(got, bits):
+    want = np.zeros(tuple(got.shape), np.uint16)
+    want[..., : bits.shape[-2], : bits.shape[-1]] = bits
+    assert np.array_equal(_bits16(got), want)
+
+
+@pytest.mark.parametrize("shape", [(1000, 777), (1001, 1024), (3, 600, 530), (640, 1024), (2, 520, 1536)])
+def test_padded_snapshots_hold_exact_bits(shape):
+    """The padded BF16 operand snapshots hold exactly the RNE BF16 bits of the F32 inputs inside and
+    zero bits in the padding, rows and columns rounded up to multiples of 16: the row-wise pad kernel
+    (padded rows of 512 columns or more) at 16-byte aligned and unaligned widths, with row padding
+    and batches, and the element kernel for the narrow B; the inputs carry rounding ties,
+    subnormals, the largest finite value and infinities."""
+    a = _specials(shape, sum(shape))
+    b = np.random.default_rng(len(shape)).standard_normal(shape[:-2] + (shape[-1], 20)).astype(np.float32)
+    print(f"padded snapshots {shape}", flush=True)
+    _, ap, bp = HipRuntime.gemm_padded_bf16_fp32(dev_f32(a), dev_f32(b))
+    _assert_padded_bits(ap, oracle.bf16_bits(a))
+    _assert_padded_bits(bp, oracle.bf16_bits(b))
+
+
+@pytest.mark.parametrize("shape", [(1000, 777), (1001, 1024), (600, 530), (40, 2050)])
+def test_frozen_padded_weight_copy_holds_exact_bits(shape):
+    """A frozen BF16 weight whose axes are not multiples of 16 is copied bit for bit into its
+    zero-padded snapshot (infinities and subnormals included): the row-wise pad kernel's BF16 path
+    at 16-byte aligned and unaligned widths, and its element path at the row edges."""
+    w = dev_f32(_specials(shape, 7 + sum(shape))).to(torch.bfloat16)
+    x = dev_f32(np.random.default_rng(3).standard_normal((16, shape[1])).astype(np.float32))
+    print(f"frozen padded weight {shape}", flush=True)
+    _, wp = HipRuntime.linear_frozen_padded_bf16_fp32(x, w)
+    _assert_padded_bits(wp, _bits16(w))
+
+
 def test_padded_rejections_leave_the_context_healthy():
     a = dev_f32(np.ones((3, 7), np.float32))
     with pytest.raises(HkError):
