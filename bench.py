@@ -905,7 +905,7 @@ def main():
         ms, algo = bench_rope()
         sec.append({"workload": "C4 RoPE Q and K",
                     "value": round(algo / ms / 1e6, 1), "unit": "GB/s", "ms": round(ms, 4),
-                    "roofline": short_roofline(roofline("hbm", algo, ms, "rope_pairs", "rope"))})
+                    "roofline": short_roofline(roofline("hbm", algo, ms, "rope_rows", "rope"))})
         if not args.no_cpu:
             sec[-1]["cpu_baseline"] = short_cpu(cpu_baseline_rope())
         try:
