@@ -183,7 +183,7 @@ void launch_pairs(bool bwd, const void* x, const float* c, const float* s, void*
     const dim3 grid(flat_blocks(n, 256));
     if constexpr (V == 8) {
         const int64_t tpr = half / 8, period = table_period(map);
-        if (period >= 0 && tpr <= 256 && (tpr & (tpr - 1)) == 0 && rows * width < (int64_t{1} << 31)) {
+        if (period >= 0 && tpr >= 1 && tpr <= 256 && (tpr & (tpr - 1)) == 0 && rows * width < (int64_t{1} << 31)) {
             const int shift = __builtin_ctzll(static_cast<unsigned long long>(tpr));
             if (bwd)
                 hipLaunchKernelGGL((rope_rows<T, LAYOUT, true>), grid, dim3(256), 0, st, static_cast<const T*>(x), c, s,
