@@ -277,12 +277,16 @@ def test_rotary_prefix_broadcast_tables_match_per_row_tables(dtype, layout, shap
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("shape,tshape", [((3, 4, 10, 64), (3, 1, 10, 32)), ((2, 6, 5, 7, 32), (1, 6, 1, 7, 16)),
-                                          ((5, 3, 128), (5, 1, 64)), ((6, 16, 256), (1, 16, 128))])
+                                          ((5, 3, 128), (5, 1, 64)), ((6, 16, 256), (1, 16, 128)),
+                                          ((3, 4, 10, 64), (1, 4, 10, 32)), ((2, 1, 5, 1, 9, 64), (1, 1, 5, 1, 9, 32)),
+                                          ((4, 3, 1, 48), (4, 3, 1, 24))])
 def test_rotary_general_table_maps_match_per_row_tables(dtype, layout, shape, tshape):
-    """Tables broadcast over axes that do not leave a contiguous innermost run (here a middle or
-    inner axis: the table row is not the input row modulo a period, so the kernel walks the
-    leading axes per row) give exactly the bits of the same tables expanded per row, forward and
-    backward; the last shape is a period pattern at 16 threads per row."""
+    """Tables broadcast over axes that do not leave a contiguous innermost run (the first three
+    shapes: a middle or inner axis, so the table row is not the input row modulo a period and the
+    kernel walks the leading axes per row) give exactly the bits of the same tables expanded per
+    row, forward and backward. The other shapes are period patterns (the table row is the input row modulo the
+    table's row count): at 16 threads per row, over two leading axes (period 40), with singleton
+    axes inside the pattern, and a same-shape table at 3 threads per row (the general kernel)."""
     half = tshape[-1]
     g = torch.Generator(device=DEV)
     g.manual_seed(sum(shape) + half)
