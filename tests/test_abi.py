@@ -349,9 +349,9 @@ def test_masked_attention_contract():
 
 
 def test_integration_extern_blocks_match_the_exports():
-    """Every function that INTEGRATION.md's Rust `extern "C"` blocks declare is exported by
-    libhk.so, and every exported hk_* function is declared in one of those blocks (nm -D on the
-    built library)."""
+    """Every function that the Rust `extern "C"` blocks of the repository's integration guide
+    declare is exported by libhk.so, and every exported hk_* function is declared in one of those
+    blocks (nm -D on the built library)."""
     import os
     import subprocess
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
